@@ -1,0 +1,247 @@
+#!/usr/bin/env python3
+"""Benchmark of the YOLO frame path on one MI355X -> one JSON line on stdout.
+
+Workloads (BASELINE.json metric "e2e ms/frame & FPS @640 fp16 (yolo11n b1, yolo11x b16);
+conv MFMA util %"):
+  * primary (value): yolo11n detect, batch 1, 810x1080 synthetic BGR frame already in HBM;
+    one step = one launch of the whole-frame graph (letterbox + net + DFL decode + NMS +
+    D2H of the results into pinned memory) + wait + host fetch of the detections, the
+    loop of the reference's `pipeline` mode (engine/engine.cu:2020-2031) minus the PCIe
+    upload (the PCIe-inclusive figure is reported separately).
+  * yolo11x detect, batch 16, sixteen 640x640 frames in HBM: whole-frame graph
+    throughput, and conv MFMA utilisation = sum(conv FLOPs) / (sum(conv time) * peak)
+    from per-op hipEvent timing.
+  * roofline: the implicit-GEMM conv kernel on the isolated-conv-sweep shape
+    3x3 s1 256->256 @80x80, batch 32, timed with hipEvents on the
+    engine stream.
+  * cpu_baseline: the numpy fp32 per-op oracle (letterbox + every op + decode + NMS) for
+    yolo11n batch 1 on this host's cores, bounded to ~15 s.
+
+Weights are seeded random-init (no checkpoints offline); data are synthetic frames.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "yolo11.cu_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK_FP16 = 2.5e15        # MI355X dense fp16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12         # MI355X HBM3E, B/s
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def conv_flops(eng, k):
+    info = eng.op_info(k)
+    H, W, _ = eng.tensor_shape(info["out"])
+    return 2.0 * H * W * info["Cout"] * info["k"] * info["k"] * info["Cin"] / max(info["g"], 1)
+
+
+def bench_n(workdir, steps, warmup):
+    import modelgen
+    import yolort
+    d = os.path.join(workdir, "yolo11n")
+    modelgen.write_model(d, "yolo11", "n", cls_bias=-8.0)
+    img = modelgen.synth_frame(810, 1080, 20, 1)
+    eng = yolort.Engine(d, 1)
+    dev = yolort.DeviceBuffer(img.nbytes)
+    eng.upload(dev, img)
+    eng.frame_graph([dev.ptr], [810], [1080])
+    for _ in range(warmup):
+        eng.frame_run()
+        eng.get(0)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.frame_run()
+        dets = eng.get(0)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    graph_ms = eng.time_graph(1, 1, max(steps, 50))
+    kept, raw = len(dets), eng.raw_count(0)
+    # PCIe-inclusive variant: the raw frame is uploaded from pinned memory inside the graph
+    pin = yolort.PinnedBuffer(img.shape)
+    pin.array[...] = img
+    eng.frame_graph([dev.ptr], [810], [1080], [pin.ptr])
+    for _ in range(warmup):
+        eng.frame_run()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.frame_run()
+        eng.get(0)
+    ms_pcie = (time.perf_counter() - t0) * 1e3 / steps
+    per_op = eng.profile_ops(1, 20)
+    pin.free()
+    dev.free()
+    eng.close()
+    return dict(ms=ms, graph_ms=graph_ms, ms_pcie=ms_pcie, kept=kept, raw=raw,
+                stream_ops_ms=float(per_op.sum()))
+
+
+def bench_x(workdir, iters):
+    import modelgen
+    import yolort
+    d = os.path.join(workdir, "yolo11x")
+    t0 = time.perf_counter()
+    modelgen.write_model(d, "yolo11", "x", cls_bias=-8.0)
+    log(f"yolo11x generated in {time.perf_counter() - t0:.1f}s")
+    B = 16
+    t0 = time.perf_counter()
+    eng = yolort.Engine(d, B, yolort.YOLO_NOGRAPH)
+    log(f"yolo11x engine (autotune) ready in {time.perf_counter() - t0:.1f}s")
+    frames = [modelgen.synth_frame(640, 640, 50, 100 + i) for i in range(B)]
+    devs = [yolort.DeviceBuffer(f.nbytes) for f in frames]
+    for b, f in zip(devs, frames):
+        eng.upload(b, f)
+    eng.frame_graph([b.ptr for b in devs], [640] * B, [640] * B)
+    for _ in range(3):
+        eng.frame_run()
+    ms = eng.time_graph(1, B, iters)
+    per_op = eng.profile_ops(B, max(3, iters // 4))
+    conv_f, conv_t, attn_t = 0.0, 0.0, 0.0
+    for k in range(eng.num_ops):
+        info = eng.op_info(k)
+        if info["kind"] == "CONV":
+            conv_f += B * conv_flops(eng, k)
+            conv_t += per_op[k] * 1e-3
+        elif info["kind"] == "ATTN":
+            attn_t += per_op[k] * 1e-3
+    kept = [len(eng.get(s)) for s in range(B)]
+    for b in devs:
+        b.free()
+    eng.close()
+    return dict(ms_per_batch=ms, img_per_s=B * 1e3 / ms, conv_tflops=conv_f / conv_t / 1e12,
+                conv_mfma_util=conv_f / conv_t / PEAK_FP16, conv_ms=conv_t * 1e3,
+                attn_ms=attn_t * 1e3, stream_ops_ms=float(per_op.sum()), kept_min=min(kept),
+                kept_max=max(kept))
+
+
+def bench_conv(workdir, iters):
+    import numpy as np
+    import modelgen
+    import yolort
+    d = os.path.join(workdir, "conv_c1")
+    H, W, cin, cout, k, s, B = 80, 80, 256, 256, 3, 1, 32
+    modelgen.write_single_conv(d, H, W, cin, cout, k, s, seed=7)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOGRAPH)
+    x = np.random.default_rng(11).standard_normal((B, H, W, cin), dtype=np.float32).astype(np.float16)
+    eng.write(0, x)
+    ms = float(eng.profile_ops(B, iters)[0])
+    flops = 2.0 * B * H * W * cout * k * k * cin
+    cfg = eng.op_config(0)
+    eng.close()
+    return dict(ms=ms, flops=flops, tflops=flops / ms / 1e9, cfg=cfg,
+                shape=f"3x3 s1 {cin}->{cout} @{H}x{W} b{B}")
+
+
+def cpu_baseline(budget_s=15.0):
+    import numpy as np
+    import modelgen
+    from oracle import graphfile, interp, post
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        cores = os.cpu_count()
+    with tempfile.TemporaryDirectory() as d:
+        modelgen.write_model(d, "yolo11", "n", cls_bias=-8.0)
+        g = graphfile.load(d)
+        img = modelgen.synth_frame(810, 1080, 20, 1)
+
+        def frame():
+            x = post.letterbox(img, 640, 640)[None]
+            I = interp.Interp(g, 1)
+            I.set_input(x)
+            I.run()
+            heads = [(b[0], c[0], None, s) for b, c, _, s in I.heads_in]
+            return post.detect(heads, 80)
+
+        frame()
+        times = []
+        t_start = time.perf_counter()
+        while time.perf_counter() - t_start < budget_s and len(times) < 50:
+            t0 = time.perf_counter()
+            frame()
+            times.append(time.perf_counter() - t0)
+    ms = float(np.median(times)) * 1e3
+    return dict(value=round(1e3 / ms, 3), unit="frames/s", cores=int(cores), kind="port",
+                sample=f"yolo11n b1 810x1080 frame, letterbox+109 ops+decode+NMS, numpy fp32; "
+                       f"median of {len(times)} frames = {ms:.1f} ms/frame")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only", choices=["all", "n", "x", "conv"], default="all")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (frames are independent; see DESIGN.md for how "
+              f"the path shards); --gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+    workdir = tempfile.mkdtemp(prefix="yolo_bench_")
+    out = {}
+    if args.only in ("all", "conv"):
+        log("conv sweep roofline shape ...")
+        out["conv"] = bench_conv(workdir, 20)
+        log(out["conv"])
+    if args.only in ("all", "n"):
+        log("yolo11n b1 e2e ...")
+        out["n"] = bench_n(workdir, args.steps, args.warmup)
+        log(out["n"])
+    if args.only in ("all", "x"):
+        log("yolo11x b16 ...")
+        out["x"] = bench_x(workdir, 20)
+        log(out["x"])
+    cpu = None
+    if args.only == "all" and not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline()
+        log(cpu)
+    n = out.get("n")
+    x = out.get("x")
+    conv = out.get("conv")
+    line = {
+        "metric": "e2e ms/frame & FPS @640 fp16 (yolo11n b1, yolo11x b16); conv MFMA util %",
+        "value": round(1e3 / n["ms"], 2) if n else None,
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(n["ms"], 4) if n else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic frames, seeded random-init weights",
+        "config": {"workload": "yolo11n detect b1 e2e (letterbox+net+decode+NMS, frame in HBM)",
+                   "imgsz": 640, "frame": "810x1080 u8 BGR", "batch": 1},
+    }
+    if n:
+        line["yolo11n_b1"] = {"ms_per_frame": round(n["ms"], 4), "graph_ms": round(n["graph_ms"], 4),
+                              "ms_per_frame_pcie": round(n["ms_pcie"], 4), "kept": n["kept"],
+                              "raw_candidates": n["raw"], "stream_ops_ms": round(n["stream_ops_ms"], 4)}
+    if x:
+        line["yolo11x_b16"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in x.items()}
+    if conv:
+        achieved = conv["flops"] / (conv["ms"] * 1e-3)
+        line["roofline"] = {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": 2500.0,
+                            "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16, 4), "traffic": None,
+                            "kernel": f"k_conv_gemm cfg {conv['cfg']}", "shape": conv["shape"],
+                            "ms": round(conv["ms"], 4)}
+    if cpu:
+        line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,147 @@
+/* C ABI of the MI355X (gfx950) YOLOv8 / YOLO11 inference engine.
+ *
+ * Part 1 re-exports the reference's embedding API with the same names, argument meaning
+ * and error behaviour; every declaration cites the reference declaration it replaces
+ * (engine/yolo.h in Soju06/yolo11.cu).  The only type change: the stream is a hipStream_t
+ * (engine/yolo.h:19 returns cudaStream_t).
+ *
+ * Part 2 adds extensions the reference has only as CLI modes or not at all: explicit
+ * destroy, error-returning create, runtime thresholds, the per-op parity harness (the
+ * reference's `dump` mode), the whole-frame graph (its `pipeline` mode), per-op timing
+ * (its `profile` mode) and small device/pinned allocation helpers for callers without a
+ * GPU allocator of their own.
+ *
+ * Threading: one stream per handle; a handle is not thread-safe (engine/engine.cu:1656).
+ */
+#ifndef YOLO_MI355X_H
+#define YOLO_MI355X_H
+
+#include <stddef.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ----------------------------------------------------------------------------------
+ * Part 1: the reference's embedding API
+ * ---------------------------------------------------------------------------------- */
+
+/* engine/yolo.h:7 */
+typedef struct { float x1, y1, x2, y2, score; int cls; } YoloDet;
+/* engine/yolo.h:8 */
+typedef struct { float x, y, w, h, angle, score; int cls; } YoloObbDet;
+
+/* engine/yolo.h:10-11 -- load model dir, fuse, autotune, build and calibrate one hipGraph
+ * per B = 1..max_batch.  Like the reference, any load or HIP failure prints a message and
+ * calls exit(1); use yolo_create_ex for an error-returning variant. */
+void* yolo_create(const char* model_dir, int max_batch);
+/* engine/yolo.h:12-16 -- 0 detect, 1 obb, 2 classify, 3 segment. */
+int yolo_task(void* h);
+/* engine/yolo.h:17-18 -- calibrated latency (ms) of the batch-B graph. */
+float yolo_exec_ms(void* h, int B);
+/* engine/yolo.h:19 */
+hipStream_t yolo_stream(void* h);
+/* engine/yolo.h:20-23 -- letterbox a device BGR u8 HWC frame into batch slot `slot`
+ * (async on the engine stream; the frame must stay alive until the stream passes it). */
+void yolo_preprocess(void* h, const unsigned char* dev_bgr, int height, int width, int slot);
+/* engine/yolo.h:24-25 -- launch the batch-B graph and wait. */
+void yolo_run(void* h, int B);
+/* engine/yolo.h:26-28 */
+void yolo_run_async(void* h, int B);
+void yolo_sync(void* h);
+/* engine/yolo.h:29-30 -- detections of a slot in original-image coordinates; returns
+ * min(count, cap). */
+int yolo_get(void* h, int slot, YoloDet* out, int cap);
+/* engine/yolo.h:31-35 -- classify models are not supported by this engine: the graph loader
+ * rejects task "classify", so these are never reached with a classify handle;
+ * yolo_preprocess_cls is a no-op and yolo_get_cls returns 0 (the reference's value for a
+ * non-classify handle, engine/engine.cu:1772). */
+void yolo_preprocess_cls(void* h, const unsigned char* dev_bgr, int height, int width, int slot);
+int yolo_get_cls(void* h, int slot, int* ids, float* probs, int k);
+/* engine/yolo.h:36-38 */
+void yolo_slot_geom(void* h, int slot, float* scale, int* top, int* left);
+/* engine/yolo.h:39-41 -- OBB models are rejected at load (no OBB kernels yet); returns 0. */
+int yolo_get_obb(void* h, int slot, YoloObbDet* out, int cap);
+/* engine/yolo.h:42-43 */
+void yolo_mask_dim(void* h, int* ph, int* pw);
+/* engine/yolo.h:44-49 -- binary mask of detection `det` of `slot` (ph*pw bytes); 0 or -1. */
+int yolo_get_mask(void* h, int slot, int det, unsigned char* out);
+
+/* ----------------------------------------------------------------------------------
+ * Part 2: extensions (no counterpart in engine/yolo.h unless cited)
+ * ---------------------------------------------------------------------------------- */
+
+#define YOLO_NOFUSE 1      /* keep CONV+ADD pairs separate (the reference's NOFUSE / dump)  */
+#define YOLO_NOTUNE 2      /* skip the startup tile autotuner (the reference's NOTUNE)       */
+#define YOLO_NOGRAPH 4     /* do not capture per-B graphs at create (yolo_run then streams)  */
+
+/* Error-returning create: NULL on failure with a message in err (if non-NULL). */
+void* yolo_create_ex(const char* model_dir, int max_batch, int flags, char* err, int errlen);
+/* The reference has no destroy (the handle lives until exit); this frees everything. */
+void yolo_destroy(void* h);
+/* Parse and validate a model dir on the host only (no GPU needed).  Returns the op count
+ * after loading, or -1 with a message in err.  Same grammar and invariants as
+ * loadGraph (engine/engine.cu:88-191). */
+int yolo_graph_check(const char* model_dir, char* err, int errlen);
+/* Runtime post-processing parameters.  The reference hard-codes conf 0.25, IoU 0.45 and
+ * 300 outputs (engine/engine.cu:1411,1466,28); these live in device memory so captured
+ * graphs pick them up without re-capture.  max_det <= 300.  Returns 0 or -1. */
+int yolo_set_thresholds(void* h, float conf, float iou, int max_det);
+/* Candidates that passed conf before NMS for a slot in the last run (the reference's
+ * h_rawcnt truncation tripwire, engine/engine.cu:1538-1546). */
+int yolo_raw_count(void* h, int slot);
+
+/* Per-op parity harness -- the reference's `dump` mode (engine/engine.cu:1843-1888). */
+int yolo_num_ops(void* h);
+/* info[0..8] = kind, a, b, out, k, s, g, Cin, Cout.  Kinds: 0 CONV, 1 ADD, 2 MAXPOOL5,
+ * 3 UPSAMPLE2, 4 COPYC, 5 ATTN, 6 DECODE, 7 GAP, 8 SOFTMAX, 9 DECODEOBB, 10 PS2,
+ * 11 DECODESEG, 12 MASKS (the reference's OpKind order, engine/engine.cu:33-34). */
+int yolo_op_info(void* h, int k, int* info);
+int yolo_num_tensors(void* h);
+/* hwc[0..2] = H, W, C of tensor t. */
+int yolo_tensor_shape(void* h, int t, int* hwc);
+/* Copy tensor t of the first B images to/from contiguous host fp16 [B][H][W][C]. */
+int yolo_read_tensor(void* h, int t, int B, void* host_f16);
+int yolo_write_tensor(void* h, int t, int B, const void* host_f16);
+/* Run op k alone for B images on the engine stream and wait.  Returns 0 or -1. */
+int yolo_run_op(void* h, int k, int B);
+/* Run NMS (+ masks) and the result copies for B images after the DECODE ops ran. */
+int yolo_run_post(void* h, int B);
+/* Tile configuration the dispatcher uses for a CONV op (autotuned or heuristic), and an
+ * override (cfg < 0 restores the heuristic).  Returns -1 for non-GEMM ops. */
+int yolo_op_config(void* h, int k);
+int yolo_set_op_config(void* h, int k, int cfg);
+/* Number of GEMM tile configurations compiled in, and the shape of one:
+ * out[0..3] = BM (pixels), BN (channels), waves along M, waves along N. */
+int yolo_num_tile_configs(void);
+int yolo_tile_config(int cfg, int* out);
+
+/* Whole-frame graph -- the reference's `pipeline` mode (engine/engine.cu:1974-2032):
+ * one graph holding [H2D of each raw frame] + letterbox of each slot + network + decode +
+ * NMS + result copies.  host_bgr may be NULL (frames already in device memory) or an
+ * array of B pinned host pointers.  Replaces any previous frame graph. */
+int yolo_frame_graph(void* h, int B, const unsigned char* const* dev_bgr,
+                     const unsigned char* const* host_bgr, const int* heights, const int* widths);
+int yolo_frame_run(void* h);       /* launch + wait */
+int yolo_frame_launch(void* h);    /* launch only    */
+
+/* Timing on the engine stream with hipEvents (the reference's `bench`/`profile` modes,
+ * engine/engine.cu:2033-2090). */
+/* Average ms of `iters` launches of the batch-B graph (which = 0) or frame graph (1). */
+float yolo_time_graph(void* h, int which, int B, int iters);
+/* Per-op average ms over `iters` stream-ordered passes (ms[k] for every op k). */
+int yolo_profile_ops(void* h, int B, int iters, float* ms);
+
+/* Allocation helpers (device / pinned host) and copies on the engine stream. */
+void* yolo_dev_alloc(size_t bytes);
+void yolo_dev_free(void* p);
+void* yolo_host_alloc(size_t bytes);
+void yolo_host_free(void* p);
+int yolo_copy_h2d(void* h, void* dst, const void* src, size_t bytes);
+int yolo_copy_d2h(void* h, void* dst, const void* src, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* YOLO_MI355X_H */

@@ -1,0 +1,218 @@
+"""Pre/post-processing oracle (numpy fp32) -- TEST INFRASTRUCTURE, see oracle/__init__.py.
+
+Functions, the reference lines they restate, and what pins them (tests/test_oracle_post.py):
+
+letterbox_geom  host geometry, engine/engine.cu:1704-1710.  Pinned by the C0 numbers
+                (810x1080 -> scale 0.5926, nh 480, top 80) and identity at equal size.
+letterbox       k_preprocess, engine/engine.cu:966-998 (fp32 bilinear, half-pixel map,
+                replicate clamp, pad 114, BGR->RGB, /255, fp16 out).  Pinned by: the
+                scale-1 identity (output == src/255 exactly), constant images, and a
+                float64 bilinear written from the textbook half-pixel formula.
+decode          k_decode<NM>, engine/engine.cu:844-906 (first-max argmax over the real
+                classes, sigmoid, keep score >= conf, DFL expectation, xyxy * stride).
+                Pinned by one-hot bins -> integer distances, uniform bins -> 7.5, and a
+                scipy.special.softmax / expit restatement.
+nms             k_nms, engine/engine.cu:1048-1123: greedy, same-class only, suppress when
+                inter/union > thr with a union > 0 guard.  Deliberate differences, shared
+                with the HIP engine: candidates are ranked by the total order (score desc,
+                anchor asc) instead of an unstable bitonic sort over atomic-order slots,
+                and the cap keeps the top `cap` by that order instead of the first 1,024 in
+                arrival order.  Pinned by the greedy-NMS characterisation (survivors are
+                pairwise below thr per class; every suppressed box overlaps a higher-ranked
+                survivor above thr) and brute force on tiny sets.
+masks           k_mask_assemble, engine/engine.cu:1125-1158 (coef . proto, half-open box
+                crop at proto scale, logit > 0).  Pinned by a hand-built case with a known
+                answer and by the crop/threshold invariants.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+F32 = np.float32
+
+
+# ----------------------------------------------------------------------------- letterbox
+def letterbox_geom(S_h: int, S_w: int, sh: int, sw: int):
+    """(scale, top, left, nh, nw) exactly as the engine host computes them in fp32."""
+    scale = min(F32(S_h) / F32(sh), F32(S_w) / F32(sw))
+    nh = int(math.floor(float(F32(sh) * scale) + 0.5))   # roundf on a positive value
+    nw = int(math.floor(float(F32(sw) * scale) + 0.5))
+    top, left = (S_h - nh) // 2, (S_w - nw) // 2
+    return F32(scale), top, left, nh, nw
+
+
+def letterbox(src: np.ndarray, S_h: int, S_w: int) -> np.ndarray:
+    """src: u8 BGR [sh, sw, 3] -> fp16 RGB [S_h, S_w, 3] in [0, 1] (pad 114)."""
+    sh, sw, _ = src.shape
+    scale, top, left, nh, nw = letterbox_geom(S_h, S_w, sh, sw)
+    y, x = np.mgrid[0:S_h, 0:S_w]
+    inside = (y >= top) & (y < top + nh) & (x >= left) & (x < left + nw)
+    fy = (F32(0.5) + (y - top).astype(F32)) / scale - F32(0.5)
+    fx = (F32(0.5) + (x - left).astype(F32)) / scale - F32(0.5)
+    y0 = np.floor(fy).astype(np.int64)
+    x0 = np.floor(fx).astype(np.int64)
+    wy = (fy - y0.astype(F32)).astype(F32)
+    wx = (fx - x0.astype(F32)).astype(F32)
+    y1 = np.minimum(y0 + 1, sh - 1)
+    x1 = np.minimum(x0 + 1, sw - 1)
+    y0 = np.clip(y0, 0, sh - 1)
+    x0 = np.clip(x0, 0, sw - 1)
+    y1 = np.clip(y1, 0, sh - 1)
+    x1 = np.clip(x1, 0, sw - 1)
+    one = F32(1.0)
+    w00 = (one - wy) * (one - wx)
+    w01 = (one - wy) * wx
+    w10 = wy * (one - wx)
+    w11 = wy * wx
+    s = src.astype(F32)
+    out = np.empty((S_h, S_w, 3), F32)
+    for c_dst, c_src in ((0, 2), (1, 1), (2, 0)):   # RGB out from BGR in
+        p00 = s[y0, x0, c_src]
+        p01 = s[y0, x1, c_src]
+        p10 = s[y1, x0, c_src]
+        p11 = s[y1, x1, c_src]
+        v = ((p00 * w00 + p01 * w01) + p10 * w10) + p11 * w11
+        v = np.where(inside, v, F32(114.0)).astype(F32)
+        out[..., c_dst] = v / F32(255.0)
+    return out.astype(np.float16)
+
+
+# ----------------------------------------------------------------------------- decode
+def dfl(bins: np.ndarray) -> np.ndarray:
+    """bins [..., 4, 16] -> expected distance [..., 4] (softmax over 16 bins, sum p*i)."""
+    mx = bins.max(axis=-1, keepdims=True)
+    p = np.exp((bins - mx).astype(F32)).astype(F32)
+    ssum = np.zeros(bins.shape[:-1], F32)
+    esum = np.zeros(bins.shape[:-1], F32)
+    for i in range(16):
+        ssum = ssum + p[..., i]
+        esum = esum + p[..., i] * F32(i)
+    return (esum / ssum).astype(F32)
+
+
+def decode(box: np.ndarray, cls: np.ndarray, nc: int, stride: int, conf: float,
+           coef: np.ndarray | None = None, anchor_base: int = 0):
+    """One image, one level.  box [H,W,64], cls [H,W,ncpad], coef [H,W,nm] or None.
+    Returns a dict of per-candidate arrays in anchor order (anchor index = base + y*W + x)."""
+    H, W, _ = box.shape
+    logits = cls[..., :nc].astype(F32).reshape(H * W, nc)
+    best = logits.max(axis=1)
+    bcls = logits.argmax(axis=1)          # first maximum, like the strict '>' scan
+    score = (F32(1.0) / (F32(1.0) + np.exp(-best))).astype(F32)
+    keep = score >= F32(conf)
+    idx = np.nonzero(keep)[0]
+    d = dfl(box.astype(F32).reshape(H * W, 4, 16)[idx])
+    yy, xx = idx // W, idx % W
+    cx = xx.astype(F32) + F32(0.5)
+    cy = yy.astype(F32) + F32(0.5)
+    st = F32(stride)
+    xyxy = np.stack([(cx - d[:, 0]) * st, (cy - d[:, 1]) * st,
+                     (cx + d[:, 2]) * st, (cy + d[:, 3]) * st], 1).astype(F32)
+    out = {"anchor": (idx + anchor_base).astype(np.int64), "box": xyxy,
+           "score": score[idx], "cls": bcls[idx].astype(np.int64)}
+    if coef is not None:
+        out["coef"] = coef.astype(F32).reshape(H * W, -1)[idx]
+    return out
+
+
+def decode_all(heads, nc: int, conf: float):
+    """heads: list of (box, cls, coef|None, stride) for ONE image, levels in op order."""
+    parts, base = [], 0
+    for box, cls, coef, st in heads:
+        parts.append(decode(box, cls, nc, st, conf, coef, base))
+        base += box.shape[0] * box.shape[1]
+    return {k: np.concatenate([p[k] for p in parts]) for k in parts[0]}
+
+
+# ----------------------------------------------------------------------------- nms
+def iou_row(a: np.ndarray, b: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """inter and union of box a [4] against boxes b [n,4], fp32, reference order of ops."""
+    xx1 = np.maximum(a[0], b[:, 0])
+    yy1 = np.maximum(a[1], b[:, 1])
+    xx2 = np.minimum(a[2], b[:, 2])
+    yy2 = np.minimum(a[3], b[:, 3])
+    w = np.maximum(F32(0.0), xx2 - xx1)
+    h = np.maximum(F32(0.0), yy2 - yy1)
+    inter = (w * h).astype(F32)
+    aarea = (a[2] - a[0]) * (a[3] - a[1])
+    ua = ((aarea + (b[:, 2] - b[:, 0]) * (b[:, 3] - b[:, 1])) - inter).astype(F32)
+    return inter, ua
+
+
+def rank_order(score: np.ndarray, anchor: np.ndarray) -> np.ndarray:
+    """Indices sorted by (score desc, anchor asc)."""
+    return np.lexsort((anchor, -score.astype(np.float64)))
+
+
+def nms(c: dict, iou_thr: float, max_det: int = 300, cap: int = 2048):
+    """Greedy same-class NMS over decoded candidates c (dict from decode_all).
+    Returns (indices into c of the survivors in output order, n_raw)."""
+    n_raw = len(c["score"])
+    order = rank_order(c["score"], c["anchor"])[:cap]
+    boxes = c["box"][order]
+    cls = c["cls"][order]
+    m = len(order)
+    dead = np.zeros(m, bool)
+    keep = []
+    thr = F32(iou_thr)
+    for i in range(m):
+        if dead[i]:
+            continue
+        keep.append(order[i])
+        if len(keep) == max_det:
+            break
+        j = np.arange(i + 1, m)
+        j = j[(~dead[j]) & (cls[j] == cls[i])]
+        if len(j) == 0:
+            continue
+        inter, ua = iou_row(boxes[i], boxes[j])
+        with np.errstate(divide="ignore", invalid="ignore"):
+            sup = (ua > 0) & ((inter / np.where(ua > 0, ua, F32(1.0))).astype(F32) > thr)
+        dead[j[sup]] = True
+    return np.asarray(keep, np.int64), n_raw
+
+
+def detect(heads, nc: int, conf: float = 0.25, iou: float = 0.45, max_det: int = 300,
+           cap: int = 2048):
+    """decode + NMS for one image -> dict with arrays in survivor order."""
+    c = decode_all(heads, nc, conf)
+    keep, n_raw = nms(c, iou, max_det, cap)
+    out = {k: v[keep] for k, v in c.items()}
+    out["n_raw"] = n_raw
+    return out
+
+
+# ----------------------------------------------------------------------------- masks
+def masks(proto: np.ndarray, coef: np.ndarray, boxes: np.ndarray, net_h: int, net_w: int) -> np.ndarray:
+    """proto [Ph,Pw,nm], coef [n,nm], boxes [n,4] in net pixels -> u8 [n,Ph,Pw]."""
+    Ph, Pw, nm = proto.shape
+    rx, ry = F32(Pw) / F32(net_w), F32(Ph) / F32(net_h)
+    logit = np.einsum("hwc,nc->nhw", proto.astype(F32), coef.astype(F32)).astype(F32)
+    ys = np.arange(Ph, dtype=F32)[None, :, None]
+    xs = np.arange(Pw, dtype=F32)[None, None, :]
+    bx1 = (boxes[:, 0] * rx)[:, None, None]
+    by1 = (boxes[:, 1] * ry)[:, None, None]
+    bx2 = (boxes[:, 2] * rx)[:, None, None]
+    by2 = (boxes[:, 3] * ry)[:, None, None]
+    inside = (xs >= bx1) & (xs < bx2) & (ys >= by1) & (ys < by2)
+    return (inside & (logit > 0)).astype(np.uint8)
+
+
+# ----------------------------------------------------------------------------- matching
+def box_iou(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Plain IoU between matched rows of a and b ([n,4] each), float64."""
+    a = a.astype(np.float64)
+    b = b.astype(np.float64)
+    iw = np.clip(np.minimum(a[:, 2], b[:, 2]) - np.maximum(a[:, 0], b[:, 0]), 0, None)
+    ih = np.clip(np.minimum(a[:, 3], b[:, 3]) - np.maximum(a[:, 1], b[:, 1]), 0, None)
+    inter = iw * ih
+    ua = (a[:, 2] - a[:, 0]) * (a[:, 3] - a[:, 1]) + (b[:, 2] - b[:, 0]) * (b[:, 3] - b[:, 1]) - inter
+    return np.where(ua > 0, inter / np.where(ua > 0, ua, 1), 1.0)
+
+
+def rel_err(gpu: np.ndarray, ref: np.ndarray) -> float:
+    """max|gpu - ref| / (max|ref| + 1e-6), the reference's per-op metric (test/compare.py:21-25)."""
+    ref = ref.astype(np.float64)
+    return float(np.abs(gpu.astype(np.float64) - ref).max() / (np.abs(ref).max() + 1e-6))

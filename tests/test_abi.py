@@ -1,0 +1,63 @@
+"""C-ABI library checks that need no GPU: it loads, exports every symbol include/yolo.h
+declares, and its host-only loader (yolo_graph_check) accepts the generated model dirs and
+rejects malformed ones with the reference loader's rules (engine/engine.cu:88-191)."""
+import os
+import shutil
+
+import pytest
+
+import modelgen
+import yolort
+
+
+def test_exports_every_header_symbol():
+    lib = yolort.load()
+    syms = yolort.header_symbols()
+    assert len(syms) >= 40
+    missing = [s for s in syms if not hasattr(lib, s)]
+    assert not missing, missing
+    # the ctypes signature table covers the whole header, nothing more
+    assert sorted(yolort._SIGS) == syms
+
+
+def test_tile_table():
+    tiles = yolort.tile_configs()
+    assert len(tiles) >= 8
+    for BM, BN, WM, WN in tiles:
+        assert (BM // WM) % 16 == 0 and (BN // WN) % 16 == 0
+        assert 64 * WM * WN <= 1024
+
+
+@pytest.mark.parametrize("arch,scale,task,nops", [("yolo11", "n", "detect", 112), ("yolo11", "m", "detect", 144),
+                                                  ("yolo11", "n", "segment", 127), ("yolov8", "n", "detect", 77)])
+def test_graph_check_accepts(models, arch, scale, task, nops):
+    d = models(arch, scale, task)
+    n, err = yolort.graph_check(d)
+    assert n == nops, err
+
+
+def _mutate(src, dst, fn):
+    shutil.copytree(src, dst)
+    p = os.path.join(dst, "model.graph")
+    lines = open(p).read().splitlines()
+    open(p, "w").write("\n".join(fn(lines)) + "\n")
+    return dst
+
+
+@pytest.mark.parametrize("name,fn,msg", [
+    ("badtask", lambda L: [L[0], "TASK classify 1000 640"] + L[2:], "classify"),
+    ("badop", lambda L: L[:-1] + ["FOO 1 2"], "bad op"),
+    ("short", lambda L: L[:-1] + [" ".join(L[-1].split()[:2])], "short op line"),
+    ("imgsz", lambda L: [L[0], "TASK detect 80 320"] + L[2:], "imgsz"),
+    ("ncpad", lambda L: [L[0], "TASK detect 81 640"] + L[2:], "8-aligned cls view"),
+    ("tensor", lambda L: [l if not l.startswith("T 0 ") else "T 999 0 3" for l in L], "missing buffer"),
+])
+def test_graph_check_rejects(models, tmp_path, name, fn, msg):
+    d = _mutate(models("yolo11", "n"), str(tmp_path / name), fn)
+    n, err = yolort.graph_check(d)
+    assert n == -1 and msg in err, err
+
+
+def test_graph_check_missing_dir(tmp_path):
+    n, err = yolort.graph_check(str(tmp_path / "nope"))
+    assert n == -1 and "model.graph" in err

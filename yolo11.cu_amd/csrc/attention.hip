@@ -1,0 +1,162 @@
+// C2PSA attention for gfx950: one fused kernel per ATTN op.
+//
+// Semantics (export/export.py:492-500; the reference runs it as 2*heads+2 launches per
+// image through its GEMM kernel plus a softmax and a V-transpose kernel,
+// engine/engine.cu:1363-1397):
+//   qkv view [B][N][heads * (2kd + hd)], per head [q (kd) | k (kd) | v (hd)]
+//   out[b][n][h*hd + c] = sum_j softmax_j(q_n . k_j * kd^-1/2) * v_j[c]
+//
+// Design: grid (ceil(N/64), heads, B); a block of 4 waves owns 64 queries of one
+// (image, head) and streams the keys in chunks of 64 through LDS, flash-style, so the
+// N x N score matrix never exists in memory.
+//  * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16 (kd = 32 is
+//    one MFMA K step): each lane then holds 16 scores of ONE query, so the online-softmax
+//    max needs only a 4-lane-group exchange and the running sum stays lane-local.
+//  * O^T = V^T P^T, again one MFMA per 32 keys per 16 channels.  The probabilities never
+//    leave registers: the k-index assignment of the P operand is simply the one the score
+//    tiles already have, and V^T is read from LDS with the same assignment (the MFMA sum
+//    over k does not depend on how k is distributed, only that A and B agree).
+//  * exp is exp2 with log2(e) folded into the score scale; fp32 statistics, fp16 P and V,
+//    fp32 accumulation.
+#include "engine.hpp"
+
+namespace yolo {
+
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int AQ = 64;      // queries per block
+constexpr int AK = 64;      // keys per chunk
+constexpr int VT_PITCH = 72;  // halves per V^T row in LDS (64 keys + 8 pad, breaks bank aliasing)
+
+__device__ __forceinline__ int kswz(int row, int c) { return row * 4 + (c ^ ((row >> 1) & 3)); }
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int heads, float scale_log2) {
+  constexpr int KD = 32;
+  constexpr int CT = HD / 16;  // channel tiles of the output
+  __shared__ f16x8 sK[AK * 4];
+  __shared__ f16 sVt[HD * VT_PITCH];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int h = blockIdx.y, img = blockIdx.z;
+  const int per = 2 * KD + HD;
+  const int qoff = qkv.o + h * per;
+  const size_t imgbase = (size_t)img * N;  // token index base of this image
+
+  // Q fragment: query lr of this wave, dims 8*lg .. 8*lg+7 (MFMA B operand)
+  const int q = blockIdx.x * AQ + wave * 16 + lr;
+  f16x8 fq = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (q < N) fq = *(const f16x8*)(qkv.p + (imgbase + q) * qkv.s + qoff + 8 * lg);
+
+  float mrun = -INFINITY, lrun = 0.f;
+  f32x4 oacc[CT];
+#pragma unroll
+  for (int i = 0; i < CT; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nchunk = (N + AK - 1) / AK;
+  for (int ch = 0; ch < nchunk; ch++) {
+    const int k0 = ch * AK;
+    // ---- stage K [64][32] and V^T [HD][64] of this chunk
+    {
+      const int key = t >> 2, c = t & 3;
+      f16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (k0 + key < N) kv = *(const f16x8*)(qkv.p + (imgbase + k0 + key) * qkv.s + qoff + KD + 8 * c);
+      sK[kswz(key, c)] = kv;
+    }
+    for (int i = t; i < AK * (HD / 8); i += 256) {
+      const int key = i / (HD / 8), g = i - key * (HD / 8);
+      f16x8 vv = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (k0 + key < N) vv = *(const f16x8*)(qkv.p + (imgbase + k0 + key) * qkv.s + qoff + 2 * KD + 8 * g);
+#pragma unroll
+      for (int j = 0; j < 8; j++) sVt[(8 * g + j) * VT_PITCH + key] = vv[j];
+    }
+    __syncthreads();
+
+    // ---- S^T tiles: lane holds scores of query lr for keys kt*16 + 4*lg + r
+    float s[4][4];
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+      f16x8 fk = sK[kswz(kt * 16 + lr, lg)];
+      f32x4 z = __builtin_amdgcn_mfma_f32_16x16x32_f16(fk, fq, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int key = k0 + kt * 16 + 4 * lg + r;
+        s[kt][r] = key < N ? z[r] * scale_log2 : -INFINITY;
+        cmax = fmaxf(cmax, s[kt][r]);
+      }
+    }
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+    const float mnew = fmaxf(mrun, cmax);
+    const float alpha = exp2f(mrun - mnew);
+    mrun = mnew;
+    float psum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        s[kt][r] = exp2f(s[kt][r] - mnew);
+        psum += s[kt][r];
+      }
+    lrun = lrun * alpha + psum;
+#pragma unroll
+    for (int i = 0; i < CT; i++) oacc[i] *= alpha;
+
+    // ---- O^T += V^T P^T, 32 keys per MFMA: element e<4 -> key 4lg+e, e>=4 -> 16+4lg+e-4
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      f16x8 fp;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        fp[e] = (f16)s[2 * hh][e];
+        fp[4 + e] = (f16)s[2 * hh + 1][e];
+      }
+#pragma unroll
+      for (int i = 0; i < CT; i++) {
+        const f16* vrow = sVt + (i * 16 + lr) * VT_PITCH + hh * 32 + 4 * lg;
+        const f16x4 v0 = *(const f16x4*)(vrow);
+        const f16x4 v1 = *(const f16x4*)(vrow + 16);
+        f16x8 fv = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        oacc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fv, fp, oacc[i], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+
+  lrun += __shfl_xor(lrun, 16);
+  lrun += __shfl_xor(lrun, 32);
+  if (q >= N) return;
+  const float inv = 1.f / lrun;
+  f16* out = y.p + (imgbase + q) * y.s + y.o + h * HD;
+#pragma unroll
+  for (int i = 0; i < CT; i++) {
+    f16x4 o = {(f16)(oacc[i][0] * inv), (f16)(oacc[i][1] * inv), (f16)(oacc[i][2] * inv),
+               (f16)(oacc[i][3] * inv)};
+    *(f16x4*)(out + i * 16 + 4 * lg) = o;
+  }
+}
+
+void launchAttention(const View& qkv, const View& y, int heads, int kd, int hd, int Bn,
+                     hipStream_t st) {
+  (void)kd;  // the loader accepts kd == 32 only
+  const int N = qkv.H * qkv.W;
+  const float scale_log2 = (1.0f / sqrtf(32.0f)) * 1.4426950408889634f;
+  dim3 grid((N + AQ - 1) / AQ, heads, Bn);
+  switch (hd) {
+    case 16: k_attention<16><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
+    case 32: k_attention<32><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
+    case 48: k_attention<48><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
+    case 64: k_attention<64><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
+    case 80: k_attention<80><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
+    case 96: k_attention<96><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
+    case 112: k_attention<112><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
+    case 128: k_attention<128><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
+    default: break;
+  }
+}
+
+}  // namespace yolo

@@ -1,0 +1,813 @@
+// Host runtime of the MI355X YOLO engine and its C ABI (include/yolo.h).
+//
+// Mirrors the reference's host side (engine/engine.cu): loadGraph (:88-248), runOp
+// (:1261-1453), forward (:1455-1481), fuseAdds (:1484-1501), autotune (:1503-1533),
+// per-B graph capture and calibration (:1665-1695) and the embedding API (:1653-1794),
+// plus the CLI's dump / pipeline / profile / bench modes (:1843-2090) as C entry points.
+//
+// Memory layout in HBM: every activation buffer of the graph is an NHWC fp16 region of
+// B_max images carved from one arena (256-byte aligned); a tensor is a channel slice of a
+// buffer, so split/concat cost nothing.  Candidates use one fixed slot per anchor
+// ([B][A][6 + nm] fp32) plus a key array ([B][A] fp32), so decode needs no counter reset
+// and no atomics, and every graph replay starts from a clean state.
+#include "engine.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "../../include/yolo.h"
+
+namespace yolo {
+
+struct Failure : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+static std::string fmt(const char* f, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, f);
+  vsnprintf(buf, sizeof buf, f, ap);
+  va_end(ap);
+  return buf;
+}
+
+#define HCK(x)                                                                                    \
+  do {                                                                                            \
+    hipError_t e_ = (x);                                                                          \
+    if (e_ != hipSuccess)                                                                         \
+      throw yolo::Failure(yolo::fmt("HIP error %s at %s:%d", hipGetErrorString(e_), __FILE__, __LINE__)); \
+  } while (0)
+
+struct SlotGeom {
+  float scale = 1.f;
+  int top = 0, left = 0;
+};
+
+struct Engine {
+  GraphDesc g;
+  std::vector<OpDesc> ops;
+  int B = 1;
+  hipStream_t st = nullptr;
+  // device memory
+  void* arena = nullptr;
+  std::vector<f16*> bufp;
+  f16* weights = nullptr;
+  float* bias = nullptr;
+  size_t nweights = 0, nbias = 0;
+  float* cand = nullptr;
+  float* keys = nullptr;
+  unsigned long long* nmsScratch = nullptr;
+  float* outdets = nullptr;
+  int* outidx = nullptr;
+  int* outcnt = nullptr;
+  int* rawcnt = nullptr;
+  uint8_t* masks = nullptr;
+  PostParams* params = nullptr;
+  PostParams hparams{0.25f, 0.45f, MAX_OUT, 0};
+  // pinned mirrors (filled inside the graph)
+  float* h_out = nullptr;
+  int* h_cnt = nullptr;
+  int* h_rawcnt = nullptr;
+  int cstride = 6;
+  int lastDecode = -1;
+  DecodeArgs dec{};
+  // graphs
+  std::vector<hipGraphExec_t> graphs;
+  std::vector<float> execMs;
+  hipGraphExec_t frameGraph = nullptr;
+  int frameB = 0;
+  std::vector<SlotGeom> slots;
+  std::vector<SlotGeom> frameSlots;
+
+  ~Engine() { release(); }
+
+  View view(int t) const {
+    const TenDesc& T = g.tens[t];
+    const BufDesc& Bd = g.bufs[T.buf];
+    return View{bufp[T.buf], Bd.H, Bd.W, Bd.C, T.coff, T.C};
+  }
+
+  void release() {
+    for (auto& ge : graphs)
+      if (ge) (void)hipGraphExecDestroy(ge);
+    graphs.clear();
+    if (frameGraph) (void)hipGraphExecDestroy(frameGraph);
+    frameGraph = nullptr;
+    void* dptrs[] = {arena, weights, bias, cand, keys, nmsScratch, outdets, outidx, outcnt, rawcnt, masks, params};
+    for (void* p : dptrs)
+      if (p) (void)hipFree(p);
+    arena = nullptr; weights = nullptr; bias = nullptr; cand = nullptr; keys = nullptr;
+    nmsScratch = nullptr; outdets = nullptr; outidx = nullptr; outcnt = nullptr; rawcnt = nullptr;
+    masks = nullptr; params = nullptr;
+    void* hptrs[] = {h_out, h_cnt, h_rawcnt};
+    for (void* p : hptrs)
+      if (p) (void)hipHostFree(p);
+    h_out = nullptr; h_cnt = nullptr; h_rawcnt = nullptr;
+    if (st) (void)hipStreamDestroy(st);
+    st = nullptr;
+  }
+
+  // ---------------------------------------------------------------- load
+  void load(const std::string& dir, int maxB, bool fuse) {
+    std::string err;
+    if (maxB < 1) throw Failure("max_batch must be >= 1");
+    if (!parseGraph(dir, g, err) || !validateGraph(g, err)) throw Failure(err);
+    B = maxB;
+    ops = g.ops;
+    if (fuse) fuseAdds(ops);
+    for (size_t i = 0; i < ops.size(); i++) {
+      const OpDesc& op = ops[i];
+      if (op.kind == CONV && op.g == 1 && op.Cin == 3 && op.b >= 0)
+        throw Failure(fmt("op %zu: first conv with a residual is not supported", i));
+      if (op.kind == CONV && op.b >= 0) {
+        const TenDesc& r = g.tens[op.b];
+        const TenDesc& y = g.tens[op.out];
+        if (g.bufs[r.buf].H != g.bufs[y.buf].H || g.bufs[r.buf].W != g.bufs[y.buf].W || r.C != y.C ||
+            r.coff % 8 || g.bufs[r.buf].C % 8)
+          throw Failure(fmt("op %zu: residual view does not match the output", i));
+      }
+      if (op.kind == DECODE || op.kind == DECODESEG) lastDecode = (int)i;
+    }
+    // weights: read, check ranges, repack depthwise [C][k*k] -> [k*k][C]
+    std::vector<char> wf, bf;
+    if (!readFile(dir + "/weights.f16", wf, err) || !readFile(dir + "/bias.f32", bf, err)) throw Failure(err);
+    nweights = wf.size() / 2;
+    nbias = bf.size() / 4;
+    f16* w = (f16*)wf.data();
+    for (size_t i = 0; i < g.ops.size(); i++) {
+      const OpDesc& op = g.ops[i];
+      if (op.kind != CONV) continue;
+      size_t cnt = (size_t)op.Cout * op.k * op.k * (op.Cin / op.g);
+      if (op.woff + cnt > nweights || op.boff + (size_t)op.Cout > nbias)
+        throw Failure(fmt("op %zu: weight/bias offsets exceed weights.f16 / bias.f32", i));
+      if (op.g > 1) {
+        int C = op.Cin, KK = op.k * op.k;
+        std::vector<f16> t((size_t)C * KK);
+        for (int c = 0; c < C; c++)
+          for (int r = 0; r < KK; r++) t[(size_t)r * C + c] = w[op.woff + (size_t)c * KK + r];
+        memcpy(w + op.woff, t.data(), t.size() * sizeof(f16));
+      }
+    }
+    HCK(hipStreamCreate(&st));
+    HCK(hipMalloc(&weights, std::max<size_t>(wf.size(), 16)));
+    HCK(hipMalloc(&bias, std::max<size_t>(bf.size(), 16)));
+    HCK(hipMemcpy(weights, wf.data(), wf.size(), hipMemcpyHostToDevice));
+    HCK(hipMemcpy(bias, bf.data(), bf.size(), hipMemcpyHostToDevice));
+    // activation arena
+    size_t total = 0;
+    std::vector<size_t> offs;
+    for (const BufDesc& b : g.bufs) {
+      offs.push_back(total);
+      total += ((size_t)B * b.H * b.W * b.C * sizeof(f16) + 255) & ~(size_t)255;
+    }
+    HCK(hipMalloc(&arena, total));
+    HCK(hipMemset(arena, 0, total));
+    for (size_t i = 0; i < g.bufs.size(); i++) bufp.push_back((f16*)((char*)arena + offs[i]));
+    // post-processing state
+    const int A = std::max(g.numAnchors, 1);   // graphs without DECODE keep 1-slot buffers
+    cstride = g.detStride;
+    HCK(hipMalloc(&cand, (size_t)B * A * cstride * sizeof(float)));
+    HCK(hipMalloc(&keys, (size_t)B * A * sizeof(float)));
+    HCK(hipMalloc(&nmsScratch, (size_t)B * nmsScratchBytes(A)));
+    HCK(hipMalloc(&outdets, (size_t)B * MAX_OUT * 6 * sizeof(float)));
+    HCK(hipMalloc(&outidx, (size_t)B * MAX_OUT * sizeof(int)));
+    HCK(hipMalloc(&outcnt, (size_t)B * sizeof(int)));
+    HCK(hipMalloc(&rawcnt, (size_t)B * sizeof(int)));
+    HCK(hipMemset(cand, 0, (size_t)B * A * cstride * sizeof(float)));
+    HCK(hipMemset(outdets, 0, (size_t)B * MAX_OUT * 6 * sizeof(float)));
+    HCK(hipMemset(outidx, 0, (size_t)B * MAX_OUT * sizeof(int)));
+    HCK(hipMemset(outcnt, 0, (size_t)B * sizeof(int)));
+    HCK(hipMemset(rawcnt, 0, (size_t)B * sizeof(int)));
+    if (g.protoTen >= 0) {
+      const BufDesc& pb = g.bufs[g.tens[g.protoTen].buf];
+      HCK(hipMalloc(&masks, (size_t)B * MAX_OUT * pb.H * pb.W));
+      HCK(hipMemset(masks, 0, (size_t)B * MAX_OUT * pb.H * pb.W));
+    }
+    HCK(hipMalloc(&params, sizeof(PostParams)));
+    HCK(hipMemcpy(params, &hparams, sizeof(PostParams), hipMemcpyHostToDevice));
+    HCK(hipHostMalloc(&h_out, (size_t)B * MAX_OUT * 6 * sizeof(float), hipHostMallocDefault));
+    HCK(hipHostMalloc(&h_cnt, (size_t)B * sizeof(int), hipHostMallocDefault));
+    HCK(hipHostMalloc(&h_rawcnt, (size_t)B * sizeof(int), hipHostMallocDefault));
+    memset(h_out, 0, (size_t)B * MAX_OUT * 6 * sizeof(float));
+    memset(h_cnt, 0, (size_t)B * sizeof(int));
+    memset(h_rawcnt, 0, (size_t)B * sizeof(int));
+    // decode levels in op order
+    dec = DecodeArgs{};
+    int base = 0;
+    for (const OpDesc& op : ops) {
+      if (op.kind != DECODE && op.kind != DECODESEG) continue;
+      DecodeLevel& L = dec.lv[dec.nlev++];
+      L.box = view(op.a);
+      L.cls = view(op.b);
+      L.coef = op.kind == DECODESEG ? view(op.out) : View{nullptr, 0, 0, 0, 0, 0};
+      L.H = L.box.H;
+      L.W = L.box.W;
+      L.stride = op.stride;
+      L.base = base;
+      base += L.H * L.W;
+    }
+    dec.A = A;
+    dec.nc = g.nc;
+    dec.nm = g.seg ? g.nm : 0;
+    slots.assign(B, SlotGeom{});
+    HCK(hipDeviceSynchronize());
+  }
+
+  // ---------------------------------------------------------------- dispatch
+  void runOp(int k, int Bn) {
+    const OpDesc& op = ops[k];
+    switch (op.kind) {
+      case CONV: {
+        View x = view(op.a), y = view(op.out);
+        View r{};
+        const View* rp = nullptr;
+        if (op.b >= 0) { r = view(op.b); rp = &r; }
+        const f16* w = weights + op.woff;
+        const float* b = bias + op.boff;
+        if (op.g == 1 && op.Cin == 3)
+          launchConvFirst(x, y, w, b, op.s, op.p, op.act, Bn, st);
+        else if (op.g == 1)
+          launchConvGemm(op.cfg, x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, st);
+        else
+          launchDwConv(x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, st);
+        break;
+      }
+      case ADD: launchAdd(view(op.a), view(op.b), view(op.out), Bn, st); break;
+      case MAXPOOL5: launchMaxPool5(view(op.a), view(op.out), Bn, st); break;
+      case UPSAMPLE2: launchUpsample2(view(op.a), view(op.out), Bn, st); break;
+      case COPYC: launchCopyC(view(op.a), view(op.out), Bn, st); break;
+      case PS2: launchPS2(view(op.a), view(op.out), Bn, st); break;
+      case ATTN: launchAttention(view(op.a), view(op.out), op.heads, op.kd, op.hd, Bn, st); break;
+      case DECODE:
+      case DECODESEG:
+        // all levels decode in one launch, issued at the last DECODE op (every head
+        // tensor is final by then)
+        if (k == lastDecode) launchDecode(dec, cand, keys, params, Bn, st);
+        break;
+      default: break;   // MASKS is declarative; assembly runs after NMS
+    }
+  }
+
+  void post(int Bn) {
+    if (g.numAnchors == 0) return;   // no detection head (single-op graphs)
+    launchNms(cand, keys, g.numAnchors, cstride, outdets, outidx, outcnt, rawcnt, nmsScratch, params, Bn, st);
+    if (g.protoTen >= 0) {
+      View pr = view(g.protoTen);
+      launchMasks(pr, cand, cstride, g.numAnchors, g.nm, outidx, outcnt, outdets, masks,
+                  (float)pr.W / g.bufs[g.tens[0].buf].W, (float)pr.H / g.bufs[g.tens[0].buf].H, Bn, st);
+    }
+    HCK(hipMemcpyAsync(h_rawcnt, rawcnt, Bn * sizeof(int), hipMemcpyDeviceToHost, st));
+    HCK(hipMemcpyAsync(h_cnt, outcnt, Bn * sizeof(int), hipMemcpyDeviceToHost, st));
+    HCK(hipMemcpyAsync(h_out, outdets, (size_t)Bn * MAX_OUT * 6 * sizeof(float), hipMemcpyDeviceToHost, st));
+  }
+
+  void forward(int Bn) {
+    for (size_t k = 0; k < ops.size(); k++) runOp((int)k, Bn);
+    post(Bn);
+  }
+
+  // ---------------------------------------------------------------- autotune
+  // Time every eligible tile shape of every GEMM conv at the max batch (1 warm-up + 5
+  // timed launches each) and keep the fastest; identical shapes share one measurement.
+  void autotune() {
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    std::map<std::tuple<int, int, int, int, int, int, int, int>, int> cache;
+    for (size_t k = 0; k < ops.size(); k++) {
+      OpDesc& op = ops[k];
+      if (op.kind != CONV || op.g != 1 || op.Cin == 3) continue;
+      View y = view(op.out);
+      const int M = B * y.H * y.W, N = op.Cout, K = op.k * op.k * op.Cin;
+      auto key = std::make_tuple(y.H, y.W, op.Cin, op.Cout, op.k, op.s, op.b >= 0 ? 1 : 0, op.act);
+      auto it = cache.find(key);
+      if (it != cache.end()) { op.cfg = it->second; continue; }
+      int best = heuristicTile(M, N, K);
+      float bestMs = 1e30f;
+      for (int cfg = 0; cfg < numTileConfigs(); cfg++) {
+        if (!tileOk(cfg, M, N, K)) continue;
+        op.cfg = cfg;
+        runOp((int)k, B);
+        HCK(hipEventRecord(e0, st));
+        for (int r = 0; r < 5; r++) runOp((int)k, B);
+        HCK(hipEventRecord(e1, st));
+        HCK(hipEventSynchronize(e1));
+        float ms = 0.f;
+        HCK(hipEventElapsedTime(&ms, e0, e1));
+        if (ms < bestMs) { bestMs = ms; best = cfg; }
+      }
+      op.cfg = best;
+      cache[key] = best;
+    }
+    HCK(hipGetLastError());
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  }
+
+  // ---------------------------------------------------------------- graphs
+  hipGraphExec_t capture(int Bn, const std::vector<std::pair<const uint8_t*, SlotGeom>>* frames,
+                         const unsigned char* const* host, const int* hs, const int* ws) {
+    hipGraph_t gr;
+    HCK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+    try {
+      if (frames) {
+        const BufDesc& ib = g.bufs[g.tens[0].buf];
+        for (int s = 0; s < Bn; s++) {
+          const uint8_t* src = (*frames)[s].first;
+          if (host && host[s])
+            HCK(hipMemcpyAsync((void*)src, host[s], (size_t)hs[s] * ws[s] * 3, hipMemcpyHostToDevice, st));
+          const SlotGeom& sg = (*frames)[s].second;
+          int nh = (int)roundf(hs[s] * sg.scale), nw = (int)roundf(ws[s] * sg.scale);
+          launchPreprocess(src, hs[s], ws[s], bufp[g.tens[0].buf] + (size_t)s * ib.H * ib.W * 3, ib.H, ib.W,
+                           sg.scale, sg.top, sg.left, nh, nw, st);
+        }
+      }
+      forward(Bn);
+    } catch (...) {
+      hipGraph_t dummy;
+      (void)hipStreamEndCapture(st, &dummy);
+      if (dummy) (void)hipGraphDestroy(dummy);
+      throw;
+    }
+    HCK(hipStreamEndCapture(st, &gr));
+    hipGraphExec_t ex;
+    HCK(hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0));
+    HCK(hipGraphDestroy(gr));
+    return ex;
+  }
+
+  void buildGraphs() {
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    graphs.assign(B, nullptr);
+    execMs.assign(B, 0.f);
+    for (int Bn = 1; Bn <= B; Bn++) {
+      graphs[Bn - 1] = capture(Bn, nullptr, nullptr, nullptr, nullptr);
+      for (int i = 0; i < 3; i++) HCK(hipGraphLaunch(graphs[Bn - 1], st));
+      HCK(hipStreamSynchronize(st));
+      HCK(hipEventRecord(e0, st));
+      for (int i = 0; i < 10; i++) HCK(hipGraphLaunch(graphs[Bn - 1], st));
+      HCK(hipEventRecord(e1, st));
+      HCK(hipEventSynchronize(e1));
+      float ms = 0.f;
+      HCK(hipEventElapsedTime(&ms, e0, e1));
+      execMs[Bn - 1] = ms / 10.f;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  }
+
+  SlotGeom geom(int sh, int sw) const {
+    const BufDesc& ib = g.bufs[g.tens[0].buf];
+    SlotGeom sg;
+    sg.scale = std::min((float)ib.H / sh, (float)ib.W / sw);
+    int nh = (int)roundf(sh * sg.scale), nw = (int)roundf(sw * sg.scale);
+    sg.top = (ib.H - nh) / 2;
+    sg.left = (ib.W - nw) / 2;
+    return sg;
+  }
+
+  void run(int Bn) {
+    if (Bn < 1 || Bn > B) throw Failure(fmt("batch %d outside 1..%d", Bn, B));
+    if (!graphs.empty() && graphs[Bn - 1])
+      HCK(hipGraphLaunch(graphs[Bn - 1], st));
+    else
+      forward(Bn);
+  }
+};
+
+}  // namespace yolo
+
+using yolo::Engine;
+using yolo::Failure;
+
+namespace {
+
+void setErr(char* err, int errlen, const char* msg) {
+  if (err && errlen > 0) {
+    strncpy(err, msg, errlen - 1);
+    err[errlen - 1] = 0;
+  }
+}
+
+Engine* create(const char* dir, int maxB, int flags) {
+  auto* e = new Engine();
+  try {
+    e->load(dir, maxB, !(flags & YOLO_NOFUSE));
+    if (!(flags & YOLO_NOTUNE)) e->autotune();
+    if (!(flags & YOLO_NOGRAPH)) e->buildGraphs();
+  } catch (...) {
+    delete e;
+    throw;
+  }
+  return e;
+}
+
+Engine* E(void* h) { return static_cast<Engine*>(h); }
+
+template <typename F>
+int guarded(F f) {
+  try {
+    return f();
+  } catch (const std::exception& ex) {
+    fprintf(stderr, "yolo: %s\n", ex.what());
+    return -1;
+  }
+}
+
+void fatal(const std::exception& ex) {
+  fprintf(stderr, "yolo: %s\n", ex.what());
+  exit(1);
+}
+
+}  // namespace
+
+extern "C" {
+
+void* yolo_create(const char* model_dir, int max_batch) {
+  try {
+    Engine* e = create(model_dir, max_batch, 0);
+    printf("engine ready: B=1..%d, exec %.3f..%.3f ms\n", max_batch, e->execMs[0], e->execMs[max_batch - 1]);
+    return e;
+  } catch (const std::exception& ex) {
+    fatal(ex);
+  }
+  return nullptr;
+}
+
+void* yolo_create_ex(const char* model_dir, int max_batch, int flags, char* err, int errlen) {
+  try {
+    return create(model_dir, max_batch, flags);
+  } catch (const std::exception& ex) {
+    setErr(err, errlen, ex.what());
+    return nullptr;
+  }
+}
+
+void yolo_destroy(void* h) {
+  if (!h) return;
+  (void)hipStreamSynchronize(E(h)->st);
+  delete E(h);
+}
+
+int yolo_graph_check(const char* model_dir, char* err, int errlen) {
+  yolo::GraphDesc g;
+  std::string msg;
+  if (!yolo::parseGraph(model_dir, g, msg) || !yolo::validateGraph(g, msg)) {
+    setErr(err, errlen, msg.c_str());
+    return -1;
+  }
+  return (int)g.ops.size();
+}
+
+int yolo_task(void* h) { return E(h)->g.seg ? 3 : 0; }
+
+float yolo_exec_ms(void* h, int B) {
+  Engine* e = E(h);
+  return (B >= 1 && B <= (int)e->execMs.size()) ? e->execMs[B - 1] : -1.f;
+}
+
+hipStream_t yolo_stream(void* h) { return E(h)->st; }
+
+void yolo_preprocess(void* h, const unsigned char* dev_bgr, int height, int width, int slot) {
+  Engine* e = E(h);
+  try {
+    if (slot < 0 || slot >= e->B) throw Failure("slot out of range");
+    if (e->g.bufs[e->g.tens[0].buf].C != 3) throw Failure("letterbox needs a 3-channel input tensor");
+    yolo::SlotGeom sg = e->geom(height, width);
+    e->slots[slot] = sg;
+    const yolo::BufDesc& ib = e->g.bufs[e->g.tens[0].buf];
+    int nh = (int)roundf(height * sg.scale), nw = (int)roundf(width * sg.scale);
+    yolo::launchPreprocess(dev_bgr, height, width, e->bufp[e->g.tens[0].buf] + (size_t)slot * ib.H * ib.W * 3,
+                           ib.H, ib.W, sg.scale, sg.top, sg.left, nh, nw, e->st);
+    HCK(hipGetLastError());
+  } catch (const std::exception& ex) {
+    fatal(ex);
+  }
+}
+
+void yolo_run(void* h, int B) {
+  try {
+    E(h)->run(B);
+    HCK(hipStreamSynchronize(E(h)->st));
+  } catch (const std::exception& ex) {
+    fatal(ex);
+  }
+}
+
+void yolo_run_async(void* h, int B) {
+  try {
+    E(h)->run(B);
+  } catch (const std::exception& ex) {
+    fatal(ex);
+  }
+}
+
+void yolo_sync(void* h) {
+  try {
+    HCK(hipStreamSynchronize(E(h)->st));
+  } catch (const std::exception& ex) {
+    fatal(ex);
+  }
+}
+
+int yolo_get(void* h, int slot, YoloDet* out, int cap) {
+  Engine* e = E(h);
+  if (slot < 0 || slot >= e->B) return 0;
+  const yolo::SlotGeom& sm = e->slots[slot];
+  int cnt = std::min(e->h_cnt[slot], cap);
+  for (int i = 0; i < cnt; i++) {
+    const float* d = e->h_out + ((size_t)slot * yolo::MAX_OUT + i) * 6;
+    out[i] = YoloDet{(d[0] - sm.left) / sm.scale, (d[1] - sm.top) / sm.scale, (d[2] - sm.left) / sm.scale,
+                     (d[3] - sm.top) / sm.scale, d[4], (int)d[5]};
+  }
+  return cnt;
+}
+
+void yolo_preprocess_cls(void* h, const unsigned char* dev_bgr, int height, int width, int slot) {
+  (void)h; (void)dev_bgr; (void)height; (void)width; (void)slot;
+}
+
+int yolo_get_cls(void* h, int slot, int* ids, float* probs, int k) {
+  (void)h; (void)slot; (void)ids; (void)probs; (void)k;
+  return 0;
+}
+
+void yolo_slot_geom(void* h, int slot, float* scale, int* top, int* left) {
+  Engine* e = E(h);
+  if (slot < 0 || slot >= e->B) return;
+  *scale = e->slots[slot].scale;
+  *top = e->slots[slot].top;
+  *left = e->slots[slot].left;
+}
+
+int yolo_get_obb(void* h, int slot, YoloObbDet* out, int cap) {
+  (void)h; (void)slot; (void)out; (void)cap;
+  return 0;
+}
+
+void yolo_mask_dim(void* h, int* ph, int* pw) {
+  Engine* e = E(h);
+  if (e->g.protoTen < 0) { *ph = *pw = 0; return; }
+  const yolo::BufDesc& b = e->g.bufs[e->g.tens[e->g.protoTen].buf];
+  *ph = b.H;
+  *pw = b.W;
+}
+
+int yolo_get_mask(void* h, int slot, int det, unsigned char* out) {
+  Engine* e = E(h);
+  if (e->g.protoTen < 0 || slot < 0 || slot >= e->B || det < 0 || det >= e->h_cnt[slot]) return -1;
+  const yolo::BufDesc& b = e->g.bufs[e->g.tens[e->g.protoTen].buf];
+  size_t sz = (size_t)b.H * b.W;
+  return hipMemcpy(out, e->masks + ((size_t)slot * yolo::MAX_OUT + det) * sz, sz, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+
+int yolo_set_thresholds(void* h, float conf, float iou, int max_det) {
+  Engine* e = E(h);
+  if (max_det < 0 || max_det > yolo::MAX_OUT || !(iou >= 0.f) || !(conf >= 0.f)) return -1;
+  e->hparams = yolo::PostParams{conf, iou, max_det, 0};
+  return hipMemcpy(e->params, &e->hparams, sizeof(yolo::PostParams), hipMemcpyHostToDevice) == hipSuccess ? 0 : -1;
+}
+
+int yolo_raw_count(void* h, int slot) {
+  Engine* e = E(h);
+  return (slot >= 0 && slot < e->B) ? e->h_rawcnt[slot] : -1;
+}
+
+int yolo_num_ops(void* h) { return (int)E(h)->ops.size(); }
+
+int yolo_op_info(void* h, int k, int* info) {
+  Engine* e = E(h);
+  if (k < 0 || k >= (int)e->ops.size()) return -1;
+  const yolo::OpDesc& op = e->ops[k];
+  int v[9] = {op.kind, op.a, op.b, op.out, op.k, op.s, op.g, op.Cin, op.Cout};
+  memcpy(info, v, sizeof v);
+  return 0;
+}
+
+int yolo_num_tensors(void* h) { return (int)E(h)->g.tens.size(); }
+
+int yolo_tensor_shape(void* h, int t, int* hwc) {
+  Engine* e = E(h);
+  if (t < 0 || t >= (int)e->g.tens.size()) return -1;
+  yolo::View v = e->view(t);
+  hwc[0] = v.H;
+  hwc[1] = v.W;
+  hwc[2] = v.C;
+  return 0;
+}
+
+int yolo_read_tensor(void* h, int t, int B, void* host_f16) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (t < 0 || t >= (int)e->g.tens.size() || B < 1 || B > e->B) return -1;
+    yolo::View v = e->view(t);
+    HCK(hipStreamSynchronize(e->st));
+    HCK(hipMemcpy2D(host_f16, v.C * 2, v.p + v.o, (size_t)v.s * 2, v.C * 2, (size_t)B * v.H * v.W,
+                    hipMemcpyDeviceToHost));
+    return 0;
+  });
+}
+
+int yolo_write_tensor(void* h, int t, int B, const void* host_f16) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (t < 0 || t >= (int)e->g.tens.size() || B < 1 || B > e->B) return -1;
+    yolo::View v = e->view(t);
+    HCK(hipStreamSynchronize(e->st));
+    HCK(hipMemcpy2D(v.p + v.o, (size_t)v.s * 2, host_f16, v.C * 2, v.C * 2, (size_t)B * v.H * v.W,
+                    hipMemcpyHostToDevice));
+    return 0;
+  });
+}
+
+int yolo_run_op(void* h, int k, int B) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (k < 0 || k >= (int)e->ops.size() || B < 1 || B > e->B) return -1;
+    e->runOp(k, B);
+    HCK(hipGetLastError());
+    HCK(hipStreamSynchronize(e->st));
+    return 0;
+  });
+}
+
+int yolo_run_post(void* h, int B) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (B < 1 || B > e->B) return -1;
+    e->post(B);
+    HCK(hipGetLastError());
+    HCK(hipStreamSynchronize(e->st));
+    return 0;
+  });
+}
+
+int yolo_op_config(void* h, int k) {
+  Engine* e = E(h);
+  if (k < 0 || k >= (int)e->ops.size()) return -1;
+  const yolo::OpDesc& op = e->ops[k];
+  if (op.kind != yolo::CONV || op.g != 1 || op.Cin == 3) return -1;
+  if (op.cfg >= 0) return op.cfg;
+  yolo::View y = e->view(op.out);
+  return yolo::heuristicTile(e->B * y.H * y.W, op.Cout, op.k * op.k * op.Cin);
+}
+
+int yolo_set_op_config(void* h, int k, int cfg) {
+  Engine* e = E(h);
+  if (k < 0 || k >= (int)e->ops.size()) return -1;
+  yolo::OpDesc& op = e->ops[k];
+  if (op.kind != yolo::CONV || op.g != 1 || op.Cin == 3 || cfg >= yolo::numTileConfigs()) return -1;
+  op.cfg = cfg < 0 ? -1 : cfg;
+  return 0;
+}
+
+int yolo_num_tile_configs(void) { return yolo::numTileConfigs(); }
+
+int yolo_tile_config(int cfg, int* out) {
+  if (cfg < 0 || cfg >= yolo::numTileConfigs()) return -1;
+  const yolo::TileCfg& t = yolo::tileConfig(cfg);
+  out[0] = t.BM;
+  out[1] = t.BN;
+  out[2] = t.WM;
+  out[3] = t.WN;
+  return 0;
+}
+
+int yolo_frame_graph(void* h, int B, const unsigned char* const* dev_bgr, const unsigned char* const* host_bgr,
+                     const int* heights, const int* widths) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (B < 1 || B > e->B) return -1;
+    if (e->g.bufs[e->g.tens[0].buf].C != 3) throw Failure("letterbox needs a 3-channel input tensor");
+    std::vector<std::pair<const uint8_t*, yolo::SlotGeom>> frames;
+    for (int s = 0; s < B; s++) {
+      if (!dev_bgr[s] || heights[s] <= 0 || widths[s] <= 0) return -1;
+      frames.push_back({dev_bgr[s], e->geom(heights[s], widths[s])});
+    }
+    if (e->frameGraph) HCK(hipGraphExecDestroy(e->frameGraph));
+    e->frameGraph = nullptr;
+    e->frameGraph = e->capture(B, &frames, host_bgr, heights, widths);
+    e->frameB = B;
+    for (int s = 0; s < B; s++) e->slots[s] = frames[s].second;
+    return 0;
+  });
+}
+
+int yolo_frame_run(void* h) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (!e->frameGraph) return -1;
+    HCK(hipGraphLaunch(e->frameGraph, e->st));
+    HCK(hipStreamSynchronize(e->st));
+    return 0;
+  });
+}
+
+int yolo_frame_launch(void* h) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (!e->frameGraph) return -1;
+    HCK(hipGraphLaunch(e->frameGraph, e->st));
+    return 0;
+  });
+}
+
+float yolo_time_graph(void* h, int which, int B, int iters) {
+  float result = -1.f;
+  guarded([&] {
+    Engine* e = E(h);
+    hipGraphExec_t ge = nullptr;
+    if (which == 1) ge = e->frameGraph;
+    else if (B >= 1 && B <= (int)e->graphs.size()) ge = e->graphs[B - 1];
+    if (!ge || iters < 1) return -1;
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    HCK(hipEventRecord(e0, e->st));
+    for (int i = 0; i < iters; i++) HCK(hipGraphLaunch(ge, e->st));
+    HCK(hipEventRecord(e1, e->st));
+    HCK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HCK(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    result = ms / iters;
+    return 0;
+  });
+  return result;
+}
+
+int yolo_profile_ops(void* h, int B, int iters, float* ms) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (B < 1 || B > e->B || iters < 1) return -1;
+    const int n = (int)e->ops.size();
+    std::vector<hipEvent_t> ev(n + 1);
+    for (auto& x : ev) HCK(hipEventCreate(&x));
+    std::vector<double> acc(n, 0.0);
+    for (int it = 0; it < iters; it++) {
+      HCK(hipEventRecord(ev[0], e->st));
+      for (int k = 0; k < n; k++) {
+        e->runOp(k, B);
+        HCK(hipEventRecord(ev[k + 1], e->st));
+      }
+      HCK(hipEventSynchronize(ev[n]));
+      for (int k = 0; k < n; k++) {
+        float t = 0.f;
+        HCK(hipEventElapsedTime(&t, ev[k], ev[k + 1]));
+        acc[k] += t;
+      }
+    }
+    for (auto& x : ev) hipEventDestroy(x);
+    for (int k = 0; k < n; k++) ms[k] = (float)(acc[k] / iters);
+    return 0;
+  });
+}
+
+void* yolo_dev_alloc(size_t bytes) {
+  void* p = nullptr;
+  return hipMalloc(&p, bytes) == hipSuccess ? p : nullptr;
+}
+
+void yolo_dev_free(void* p) {
+  if (p) (void)hipFree(p);
+}
+
+void* yolo_host_alloc(size_t bytes) {
+  void* p = nullptr;
+  return hipHostMalloc(&p, bytes, hipHostMallocDefault) == hipSuccess ? p : nullptr;
+}
+
+void yolo_host_free(void* p) {
+  if (p) (void)hipHostFree(p);
+}
+
+int yolo_copy_h2d(void* h, void* dst, const void* src, size_t bytes) {
+  return guarded([&] {
+    HCK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, E(h)->st));
+    HCK(hipStreamSynchronize(E(h)->st));
+    return 0;
+  });
+}
+
+int yolo_copy_d2h(void* h, void* dst, const void* src, size_t bytes) {
+  return guarded([&] {
+    HCK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, E(h)->st));
+    HCK(hipStreamSynchronize(E(h)->st));
+    return 0;
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,120 @@
+// Internal declarations of the MI355X YOLO engine: graph description (host), device views
+// and the kernel launchers every .hip file exports to the host runtime.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+namespace yolo {
+
+typedef _Float16 f16;
+
+// ------------------------------------------------------------------ graph (host side)
+// Op kinds keep the reference's numbering (engine/engine.cu:33-34).
+enum OpKind { CONV = 0, ADD, MAXPOOL5, UPSAMPLE2, COPYC, ATTN, DECODE, GAP, SOFTMAX, DECODEOBB,
+              PS2, DECODESEG, MASKS };
+
+struct BufDesc { int H, W, C; };
+struct TenDesc { int buf, coff, C; };
+struct OpDesc {
+  int kind = 0;
+  int a = -1, b = -1, out = -1;       // CONV: a = input, b = fused residual (-1 none)
+  int k = 0, s = 0, p = 0, g = 0, act = 0, Cin = 0, Cout = 0;
+  long woff = 0, boff = 0;
+  int heads = 0, kd = 0, hd = 0;      // ATTN
+  int stride = 0;                     // DECODE*
+  int cfg = -1;                       // GEMM tile config (-1 = heuristic)
+};
+
+struct GraphDesc {
+  int version = 0;
+  std::string task = "detect";
+  int nc = 80, imgsz = 0;
+  std::vector<BufDesc> bufs;
+  std::vector<TenDesc> tens;
+  std::vector<OpDesc> ops;
+  // derived by validate()
+  bool seg = false;
+  int nm = 0, protoTen = -1;
+  int detStride = 6;                  // floats per candidate record
+  int numAnchors = 0;                 // sum of H*W over the DECODE levels
+};
+
+// Parses model.graph (engine/engine.cu:88-141) and checks the invariants the kernels rely
+// on (engine/engine.cu:143-191 plus this engine's own: every view %8-aligned).  Returns
+// false with a message.
+bool parseGraph(const std::string& dir, GraphDesc& g, std::string& err);
+bool validateGraph(GraphDesc& g, std::string& err);
+// CONV followed by an ADD consuming its output -> CONV with residual (engine/engine.cu:1484).
+int fuseAdds(std::vector<OpDesc>& ops);
+bool readFile(const std::string& path, std::vector<char>& out, std::string& err);
+
+// ------------------------------------------------------------------ device views
+// A tensor view: channel slice [o, o+C) of an NHWC buffer with row stride s (= buffer C).
+// Image b, pixel (y, x) of the view starts at p + ((b*H + y)*W + x)*s + o.
+struct View {
+  f16* p;
+  int H, W, s, o, C;
+};
+
+// Post-processing parameters, read by kernels from device memory so graphs need no
+// re-capture when they change.
+struct PostParams {
+  float conf;
+  float iou;
+  int max_det;
+  int pad;
+};
+
+constexpr int MAX_OUT = 300;          // output records per image (engine/engine.cu:28)
+constexpr int NMS_CAP = 2048;         // top-ranked candidates that enter NMS
+
+// Detection levels handled by one decode launch.
+struct DecodeLevel {
+  View box, cls, coef;                // coef.p == nullptr for detect
+  int H, W, stride, base;             // base = first anchor index of the level
+};
+struct DecodeArgs {
+  DecodeLevel lv[3];
+  int nlev, A, nc, nm;
+};
+
+// ------------------------------------------------------------------ GEMM tile configs
+struct TileCfg { int BM, BN, WM, WN; };
+int numTileConfigs();
+const TileCfg& tileConfig(int cfg);
+
+// ------------------------------------------------------------------ launchers
+// conv.hip
+void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
+                    const float* bias, int k, int s, int p, int act, int Bn, hipStream_t st);
+void launchConvFirst(const View& x, const View& y, const f16* w, const float* bias, int s, int p,
+                     int act, int Bn, hipStream_t st);
+void launchDwConv(const View& x, const View& y, const View* res, const f16* wt_kkc,
+                  const float* bias, int k, int s, int p, int act, int Bn, hipStream_t st);
+int heuristicTile(int M, int N, int K);
+bool tileOk(int cfg, int M, int N, int K);
+// elementwise.hip
+void launchAdd(const View& a, const View& b, const View& y, int Bn, hipStream_t st);
+void launchMaxPool5(const View& x, const View& y, int Bn, hipStream_t st);
+void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st);
+void launchCopyC(const View& x, const View& y, int Bn, hipStream_t st);
+void launchPS2(const View& x, const View& y, int Bn, hipStream_t st);
+// attention.hip
+void launchAttention(const View& qkv, const View& y, int heads, int kd, int hd, int Bn,
+                     hipStream_t st);
+// frame.hip
+void launchPreprocess(const uint8_t* src, int sh, int sw, f16* dst, int dh, int dw, float scale,
+                      int top, int left, int nh, int nw, hipStream_t st);
+void launchDecode(const DecodeArgs& a, float* cand, float* keys, const PostParams* prm, int Bn,
+                  hipStream_t st);
+void launchNms(const float* cand, const float* keys, int A, int cstride, float* out, int* outidx,
+               int* outcnt, int* rawcnt, unsigned long long* scratch, const PostParams* prm,
+               int Bn, hipStream_t st);
+void launchMasks(const View& proto, const float* cand, int cstride, int A, int nm,
+                 const int* outidx, const int* outcnt, const float* outdets, uint8_t* masks,
+                 float rx, float ry, int Bn, hipStream_t st);
+size_t nmsScratchBytes(int A);
+
+}  // namespace yolo

@@ -1,0 +1,307 @@
+"""ctypes binding of libyolo11_amd.so (the C ABI in include/yolo.h).
+
+This is the Python face of the engine for tests and benchmarks; it talks to the library
+only through the C ABI, uses numpy for host arrays and the library's own allocation
+helpers for device memory (no torch in the process, so exactly one HIP runtime is
+loaded).  There is no CPU fallback: if the library is missing, `load()` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libyolo11_amd.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "yolo.h")
+
+YOLO_NOFUSE, YOLO_NOTUNE, YOLO_NOGRAPH = 1, 2, 4
+OP_KINDS = ["CONV", "ADD", "MAXPOOL5", "UPSAMPLE2", "COPYC", "ATTN", "DECODE", "GAP", "SOFTMAX",
+            "DECODEOBB", "PS2", "DECODESEG", "MASKS"]
+MAX_OUT = 300
+
+
+class YoloDet(C.Structure):
+    _fields_ = [("x1", C.c_float), ("y1", C.c_float), ("x2", C.c_float), ("y2", C.c_float),
+                ("score", C.c_float), ("cls", C.c_int)]
+
+
+class YoloObbDet(C.Structure):
+    _fields_ = [("x", C.c_float), ("y", C.c_float), ("w", C.c_float), ("h", C.c_float),
+                ("angle", C.c_float), ("score", C.c_float), ("cls", C.c_int)]
+
+
+_SIGS = {
+    "yolo_create": (C.c_void_p, [C.c_char_p, C.c_int]),
+    "yolo_task": (C.c_int, [C.c_void_p]),
+    "yolo_exec_ms": (C.c_float, [C.c_void_p, C.c_int]),
+    "yolo_stream": (C.c_void_p, [C.c_void_p]),
+    "yolo_preprocess": (None, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "yolo_run": (None, [C.c_void_p, C.c_int]),
+    "yolo_run_async": (None, [C.c_void_p, C.c_int]),
+    "yolo_sync": (None, [C.c_void_p]),
+    "yolo_get": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(YoloDet), C.c_int]),
+    "yolo_preprocess_cls": (None, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "yolo_get_cls": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_float), C.c_int]),
+    "yolo_slot_geom": (None, [C.c_void_p, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "yolo_get_obb": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(YoloObbDet), C.c_int]),
+    "yolo_mask_dim": (None, [C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "yolo_get_mask": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    "yolo_create_ex": (C.c_void_p, [C.c_char_p, C.c_int, C.c_int, C.c_char_p, C.c_int]),
+    "yolo_destroy": (None, [C.c_void_p]),
+    "yolo_graph_check": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int]),
+    "yolo_set_thresholds": (C.c_int, [C.c_void_p, C.c_float, C.c_float, C.c_int]),
+    "yolo_raw_count": (C.c_int, [C.c_void_p, C.c_int]),
+    "yolo_num_ops": (C.c_int, [C.c_void_p]),
+    "yolo_op_info": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int)]),
+    "yolo_num_tensors": (C.c_int, [C.c_void_p]),
+    "yolo_tensor_shape": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int)]),
+    "yolo_read_tensor": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    "yolo_write_tensor": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    "yolo_run_op": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    "yolo_run_post": (C.c_int, [C.c_void_p, C.c_int]),
+    "yolo_op_config": (C.c_int, [C.c_void_p, C.c_int]),
+    "yolo_set_op_config": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    "yolo_num_tile_configs": (C.c_int, []),
+    "yolo_tile_config": (C.c_int, [C.c_int, C.POINTER(C.c_int)]),
+    "yolo_frame_graph": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
+                                   C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "yolo_frame_run": (C.c_int, [C.c_void_p]),
+    "yolo_frame_launch": (C.c_int, [C.c_void_p]),
+    "yolo_time_graph": (C.c_float, [C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "yolo_profile_ops": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_float)]),
+    "yolo_dev_alloc": (C.c_void_p, [C.c_size_t]),
+    "yolo_dev_free": (None, [C.c_void_p]),
+    "yolo_host_alloc": (C.c_void_p, [C.c_size_t]),
+    "yolo_host_free": (None, [C.c_void_p]),
+    "yolo_copy_h2d": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+    "yolo_copy_d2h": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+}
+
+_lib = None
+
+
+def header_symbols() -> list[str]:
+    """Function names declared in include/yolo.h."""
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(yolo_[a-z0-9_]+)\s*\(", txt)))
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        lib = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def tile_configs() -> list[tuple[int, int, int, int]]:
+    lib = load()
+    out = []
+    for i in range(lib.yolo_num_tile_configs()):
+        v = (C.c_int * 4)()
+        lib.yolo_tile_config(i, v)
+        out.append(tuple(v))
+    return out
+
+
+class DeviceBuffer:
+    """Device memory from the engine's allocator."""
+
+    def __init__(self, nbytes: int):
+        self.lib = load()
+        self.nbytes = nbytes
+        self.ptr = self.lib.yolo_dev_alloc(max(nbytes, 16))
+        if not self.ptr:
+            raise MemoryError(f"yolo_dev_alloc({nbytes}) failed")
+
+    def free(self):
+        if self.ptr:
+            self.lib.yolo_dev_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class PinnedBuffer:
+    """Pinned host memory viewed as a numpy array."""
+
+    def __init__(self, shape, dtype=np.uint8):
+        self.lib = load()
+        dt = np.dtype(dtype)
+        n = int(np.prod(shape)) * dt.itemsize
+        self.ptr = self.lib.yolo_host_alloc(max(n, 16))
+        if not self.ptr:
+            raise MemoryError("yolo_host_alloc failed")
+        self.array = np.ctypeslib.as_array((C.c_uint8 * n).from_address(self.ptr)).view(dt).reshape(shape)
+
+    def free(self):
+        if self.ptr:
+            self.array = None
+            self.lib.yolo_host_free(self.ptr)
+            self.ptr = None
+
+
+class Engine:
+    def __init__(self, model_dir: str, max_batch: int = 1, flags: int = 0):
+        self.lib = load()
+        err = C.create_string_buffer(1024)
+        self.h = self.lib.yolo_create_ex(model_dir.encode(), max_batch, flags, err, 1024)
+        if not self.h:
+            raise RuntimeError(f"yolo_create_ex failed: {err.value.decode()}")
+        self.max_batch = max_batch
+
+    def close(self):
+        if self.h:
+            self.lib.yolo_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    # -- graph introspection
+    @property
+    def num_ops(self) -> int:
+        return self.lib.yolo_num_ops(self.h)
+
+    def op_info(self, k: int) -> dict:
+        v = (C.c_int * 9)()
+        if self.lib.yolo_op_info(self.h, k, v) != 0:
+            raise IndexError(k)
+        kind, a, b, out, kk, s, g, cin, cout = v
+        return dict(kind=OP_KINDS[kind], a=a, b=b, out=out, k=kk, s=s, g=g, Cin=cin, Cout=cout)
+
+    def tensor_shape(self, t: int) -> tuple[int, int, int]:
+        v = (C.c_int * 3)()
+        if self.lib.yolo_tensor_shape(self.h, t, v) != 0:
+            raise IndexError(t)
+        return tuple(v)
+
+    def read(self, t: int, B: int = 1) -> np.ndarray:
+        H, W, Cc = self.tensor_shape(t)
+        out = np.empty((B, H, W, Cc), np.float16)
+        if self.lib.yolo_read_tensor(self.h, t, B, out.ctypes.data) != 0:
+            raise RuntimeError("yolo_read_tensor failed")
+        return out
+
+    def write(self, t: int, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr, dtype=np.float16)
+        H, W, Cc = self.tensor_shape(t)
+        assert arr.shape[1:] == (H, W, Cc), (arr.shape, (H, W, Cc))
+        if self.lib.yolo_write_tensor(self.h, t, arr.shape[0], arr.ctypes.data) != 0:
+            raise RuntimeError("yolo_write_tensor failed")
+
+    def run_op(self, k: int, B: int = 1):
+        if self.lib.yolo_run_op(self.h, k, B) != 0:
+            raise RuntimeError(f"yolo_run_op({k}) failed")
+
+    def run_post(self, B: int = 1):
+        if self.lib.yolo_run_post(self.h, B) != 0:
+            raise RuntimeError("yolo_run_post failed")
+
+    def op_config(self, k: int) -> int:
+        return self.lib.yolo_op_config(self.h, k)
+
+    def set_op_config(self, k: int, cfg: int):
+        if self.lib.yolo_set_op_config(self.h, k, cfg) != 0:
+            raise ValueError((k, cfg))
+
+    # -- frame API
+    def set_thresholds(self, conf=0.25, iou=0.45, max_det=300):
+        if self.lib.yolo_set_thresholds(self.h, conf, iou, max_det) != 0:
+            raise ValueError((conf, iou, max_det))
+
+    def preprocess(self, dev_ptr: int, h: int, w: int, slot: int = 0):
+        self.lib.yolo_preprocess(self.h, dev_ptr, h, w, slot)
+
+    def run(self, B: int = 1):
+        self.lib.yolo_run(self.h, B)
+
+    def sync(self):
+        self.lib.yolo_sync(self.h)
+
+    def get(self, slot: int = 0, cap: int = MAX_OUT) -> np.ndarray:
+        arr = (YoloDet * cap)()
+        n = self.lib.yolo_get(self.h, slot, arr, cap)
+        return np.array([(d.x1, d.y1, d.x2, d.y2, d.score, d.cls) for d in arr[:n]], np.float64).reshape(n, 6)
+
+    def raw_count(self, slot: int = 0) -> int:
+        return self.lib.yolo_raw_count(self.h, slot)
+
+    def slot_geom(self, slot: int = 0):
+        s, t, l = C.c_float(), C.c_int(), C.c_int()
+        self.lib.yolo_slot_geom(self.h, slot, C.byref(s), C.byref(t), C.byref(l))
+        return s.value, t.value, l.value
+
+    def mask_dim(self):
+        ph, pw = C.c_int(), C.c_int()
+        self.lib.yolo_mask_dim(self.h, C.byref(ph), C.byref(pw))
+        return ph.value, pw.value
+
+    def get_mask(self, slot: int, det: int) -> np.ndarray | None:
+        ph, pw = self.mask_dim()
+        out = np.empty((ph, pw), np.uint8)
+        if self.lib.yolo_get_mask(self.h, slot, det, out.ctypes.data) != 0:
+            return None
+        return out
+
+    def exec_ms(self, B: int = 1) -> float:
+        return self.lib.yolo_exec_ms(self.h, B)
+
+    def task(self) -> int:
+        return self.lib.yolo_task(self.h)
+
+    def frame_graph(self, dev_ptrs, heights, widths, host_ptrs=None):
+        B = len(dev_ptrs)
+        dv = (C.c_void_p * B)(*dev_ptrs)
+        hv = (C.c_void_p * B)(*host_ptrs) if host_ptrs is not None else None
+        hs = (C.c_int * B)(*heights)
+        ws = (C.c_int * B)(*widths)
+        if self.lib.yolo_frame_graph(self.h, B, dv, hv, hs, ws) != 0:
+            raise RuntimeError("yolo_frame_graph failed")
+
+    def frame_run(self):
+        if self.lib.yolo_frame_run(self.h) != 0:
+            raise RuntimeError("yolo_frame_run failed")
+
+    def time_graph(self, which: int, B: int, iters: int) -> float:
+        ms = self.lib.yolo_time_graph(self.h, which, B, iters)
+        if ms < 0:
+            raise RuntimeError("yolo_time_graph failed")
+        return ms
+
+    def profile_ops(self, B: int, iters: int) -> np.ndarray:
+        n = self.num_ops
+        out = (C.c_float * n)()
+        if self.lib.yolo_profile_ops(self.h, B, iters, out) != 0:
+            raise RuntimeError("yolo_profile_ops failed")
+        return np.array(out, np.float64)
+
+    def upload(self, buf: DeviceBuffer, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= buf.nbytes
+        if self.lib.yolo_copy_h2d(self.h, buf.ptr, arr.ctypes.data, arr.nbytes) != 0:
+            raise RuntimeError("yolo_copy_h2d failed")
+
+
+def graph_check(model_dir: str) -> tuple[int, str]:
+    lib = load()
+    err = C.create_string_buffer(1024)
+    n = lib.yolo_graph_check(model_dir.encode(), err, 1024)
+    return n, err.value.decode()
