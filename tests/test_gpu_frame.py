@@ -48,45 +48,65 @@ def _oracle_frame(model_dir, img, round_fp16=True, conf=0.25, iou=0.45):
     I.set_input(x)
     I.run()
     heads = [(b[0], c[0], None if m is None else m[0], s) for b, c, m, s in I.heads_in]
-    return post.detect(heads, g.nc, conf, iou), I
+    return post.detect(heads, g.nc, conf, iou), heads
 
 
-def _match_report(got, want):
-    """Pairs detections in output order and reports the parity figures."""
-    n = min(len(got), len(want["score"]))
-    iou = post.box_iou(got[:n, :4], want["box"][:n]) if n else np.ones(0)
-    dscore = np.abs(got[:n, 4] - want["score"][:n]) if n else np.zeros(0)
-    same_cls = (got[:n, 5].astype(int) == want["cls"][:n]) if n else np.ones(0, bool)
-    return n, iou, dscore, same_cls
+def _agreement(ref, other_box, other_score, other_cls):
+    """Greedy IoU matching of `other` detections to `ref` (both in the same coordinates);
+    returns matched fraction, class agreement, median IoU and max |dscore| over matches."""
+    used = np.zeros(len(other_score), bool)
+    ious, same, ds = [], [], []
+    for i in range(len(ref["score"])):
+        if not len(other_score):
+            break
+        iou = post.box_iou(np.repeat(ref["box"][i:i + 1], len(other_score), 0), other_box)
+        iou[used] = -1
+        j = int(np.argmax(iou))
+        if iou[j] >= 0.5:
+            used[j] = True
+            ious.append(iou[j])
+            same.append(other_cls[j] == ref["cls"][i])
+            ds.append(abs(other_score[j] - ref["score"][i]))
+    n = max(len(ref["score"]), 1)
+    return dict(matched=len(ious) / n, cls=float(np.mean(same)) if same else 1.0,
+                iou=float(np.median(ious)) if ious else 1.0, dscore=float(max(ds)) if ds else 0.0)
 
 
 @pytest.mark.parametrize("arch,scale,task", [("yolo11", "n", "detect"), ("yolo11", "n", "segment"),
                                              ("yolov8", "n", "detect"), ("yolo11", "m", "detect")])
 def test_frame_vs_oracle(models, arch, scale, task):
-    """Full fused/tuned/graph frame vs the oracle on the same seeded frame and weights."""
+    """Full fused/tuned/graph frame against the fp32 oracle, gated by the fp16-storage
+    envelope: an exact fp16-storage execution (the oracle with fp16-rounded activations)
+    already departs from fp32 by a few percent after ~100 layers of random-init weights,
+    so the GPU must agree with fp32 at least about as well as that execution does."""
     d = models(arch, scale, task)
     img = (modelgen.synth_polygons(810, 1080, 30, 2) if task == "segment"
            else modelgen.synth_frame(810, 1080, 20, 1))
+    g = graphfile.load(d)
     eng = yolort.Engine(d, 1)
     buf = _letterbox_gpu(eng, img)
     eng.run(1)
     got = eng.get(0)
-    # un-letterbox the oracle's boxes the same way yolo_get does
-    want, I = _oracle_frame(d, img)
     scale_, top, left = eng.slot_geom(0)
-    wb = want["box"].copy()
-    wb[:, [0, 2]] = (wb[:, [0, 2]] - left) / scale_
-    wb[:, [1, 3]] = (wb[:, [1, 3]] - top) / scale_
-    want = dict(want, box=wb)
-    n, iou, dscore, same_cls = _match_report(got, want)
-    print(f"{arch}{scale}-{task}: gpu kept {len(got)} raw {eng.raw_count(0)} | oracle kept "
-          f"{len(want['score'])} raw {want['n_raw']} | min IoU {iou.min() if n else 1:.4f} "
-          f"max dscore {dscore.max() if n else 0:.2e} cls agree {same_cls.mean() if n else 1:.4f}", flush=True)
-    assert abs(len(got) - len(want["score"])) <= max(2, len(want["score"]) // 20)
-    # compounded fp16 noise can swap near-tied neighbours; every output position must
-    # either match or be explained by a near tie, and the bulk must match exactly
-    ok = (iou >= 0.99) & (dscore <= 5e-3) & same_cls
-    assert ok.mean() >= 0.9, (ok.mean(), np.nonzero(~ok)[0][:10])
+    gbox = got[:, :4].copy()          # back to letterbox space
+    gbox[:, [0, 2]] = gbox[:, [0, 2]] * scale_ + left
+    gbox[:, [1, 3]] = gbox[:, [1, 3]] * scale_ + top
+    gpu_heads = [(eng.read(op.a)[0].astype(np.float32), eng.read(op.b)[0].astype(np.float32))
+                 for op in g.ops if op.kind in ("DECODE", "DECODESEG")]
+    r32, h32 = _oracle_frame(d, img, round_fp16=False)
+    r16, h16 = _oracle_frame(d, img, round_fp16=True)
+    drift16 = max(post.rel_err(a[1], b[1]) for a, b in zip(h16, h32))
+    driftg = max(post.rel_err(gh[1], b[1]) for gh, b in zip(gpu_heads, h32))
+    a16 = _agreement(r32, r16["box"], r16["score"], r16["cls"])
+    ag = _agreement(r32, gbox, got[:, 4], got[:, 5].astype(int))
+    print(f"{arch}{scale}-{task}: kept gpu {len(got)} / fp16-oracle {len(r16['score'])} / fp32 "
+          f"{len(r32['score'])}; cls-head drift vs fp32: gpu {driftg:.2e} fp16-oracle {drift16:.2e}; "
+          f"agreement with fp32 gpu {ag} fp16-oracle {a16}", flush=True)
+    assert driftg <= 2 * drift16 + 2e-3
+    assert abs(len(got) - len(r16["score"])) <= max(3, len(r16["score"]) // 10)
+    assert ag["matched"] >= a16["matched"] - 0.1
+    assert ag["cls"] >= a16["cls"] - 0.2
+    assert ag["iou"] >= min(a16["iou"], 0.99) - 0.02
     buf.free()
     eng.close()
 
@@ -128,7 +148,7 @@ def test_frame_graph_pipeline(models):
                     [p.ptr for p in pins])
     for rep in range(3):
         if rep == 2:   # new contents in the same pinned buffers, no re-capture
-            pins[0].array[...] = imgs[1][:810, :1080]
+            pins[0].array[...] = modelgen.synth_frame(810, 1080, 25, 77)
         eng.frame_run()
         got = [eng.get(s) for s in range(2)]
         ref = yolort.Engine(d, 1, yolort.YOLO_NOTUNE)
