@@ -46,15 +46,23 @@ def conv_flops(eng, k):
     return 2.0 * H * W * info["Cout"] * info["k"] * info["k"] * info["Cin"] / max(info["g"], 1)
 
 
-def bench_n(workdir, steps, warmup):
+def bench_n(workdir, steps, warmup, graph=True):
     import modelgen
     import yolort
     d = os.path.join(workdir, "yolo11n")
     modelgen.write_model(d, "yolo11", "n", cls_bias=-8.0)
     img = modelgen.synth_frame(810, 1080, 20, 1)
-    eng = yolort.Engine(d, 1)
+    eng = yolort.Engine(d, 1, 0 if graph else yolort.YOLO_NOGRAPH)
     dev = yolort.DeviceBuffer(img.nbytes)
     eng.upload(dev, img)
+    if not graph:   # stream-ordered launches of the same kernels (for profilers)
+        for _ in range(warmup + steps):
+            eng.preprocess(dev.ptr, 810, 1080, 0)
+            eng.run(1)
+            eng.get(0)
+        dev.free()
+        eng.close()
+        return None
     eng.frame_graph([dev.ptr], [810], [1080])
     for _ in range(warmup):
         eng.frame_run()
@@ -85,7 +93,7 @@ def bench_n(workdir, steps, warmup):
                 stream_ops_ms=float(per_op.sum()))
 
 
-def bench_x(workdir, iters):
+def bench_x(workdir, iters, graph=True):
     import modelgen
     import yolort
     d = os.path.join(workdir, "yolo11x")
@@ -100,6 +108,15 @@ def bench_x(workdir, iters):
     devs = [yolort.DeviceBuffer(f.nbytes) for f in frames]
     for b, f in zip(devs, frames):
         eng.upload(b, f)
+    if not graph:
+        for _ in range(iters):
+            for s, b in enumerate(devs):
+                eng.preprocess(b.ptr, 640, 640, s)
+            eng.run(B)
+        for b in devs:
+            b.free()
+        eng.close()
+        return None
     eng.frame_graph([b.ptr for b in devs], [640] * B, [640] * B)
     for _ in range(3):
         eng.frame_run()
@@ -135,10 +152,20 @@ def bench_conv(workdir, iters):
     eng.write(0, x)
     ms = float(eng.profile_ops(B, iters)[0])
     flops = 2.0 * B * H * W * cout * k * k * cin
+    # algorithmic HBM bytes: input + weights + output (fp16) + bias (fp32)
+    nbytes = 2.0 * (B * H * W * cin + cout * k * k * cin + B * H * W * cout) + 4 * cout
     cfg = eng.op_config(0)
     eng.close()
-    return dict(ms=ms, flops=flops, tflops=flops / ms / 1e9, cfg=cfg,
-                shape=f"3x3 s1 {cin}->{cout} @{H}x{W} b{B}")
+    # a plain copy of known size on the same shape (scale reference for HBM counters)
+    dc = os.path.join(workdir, "copy_c1")
+    modelgen.write_copy(dc, H, W, cin)
+    ec = yolort.Engine(dc, B, yolort.YOLO_NOGRAPH)
+    copy_ms = float(ec.profile_ops(B, iters)[0])
+    ec.close()
+    copy_bytes = 2.0 * 2 * B * H * W * cin
+    return dict(ms=ms, flops=flops, bytes=nbytes, tflops=flops / ms / 1e9, cfg=cfg,
+                shape=f"3x3 s1 {cin}->{cout} @{H}x{W} b{B}", copy_ms=copy_ms,
+                copy_gbs=copy_bytes / copy_ms / 1e6)
 
 
 def cpu_baseline(budget_s=15.0):
@@ -183,6 +210,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", choices=["all", "n", "x", "conv"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch the same kernels stream-ordered (rocprofv3's kernel tracer "
+                         "crashes inside hipGraphLaunch on this image); prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (frames are independent; see DESIGN.md for how "
@@ -196,12 +226,15 @@ def main():
         log(out["conv"])
     if args.only in ("all", "n"):
         log("yolo11n b1 e2e ...")
-        out["n"] = bench_n(workdir, args.steps, args.warmup)
+        out["n"] = bench_n(workdir, args.steps, args.warmup, not args.no_graph)
         log(out["n"])
     if args.only in ("all", "x"):
         log("yolo11x b16 ...")
-        out["x"] = bench_x(workdir, 20)
+        out["x"] = bench_x(workdir, 20, not args.no_graph)
         log(out["x"])
+    if args.no_graph:
+        log("stream-ordered profiling pass done")
+        return
     cpu = None
     if args.only == "all" and not args.no_cpu:
         log("cpu baseline ...")

@@ -75,6 +75,8 @@ int yolo_get_mask(void* h, int slot, int det, unsigned char* out);
 #define YOLO_NOFUSE 1      /* keep CONV+ADD pairs separate (the reference's NOFUSE / dump)  */
 #define YOLO_NOTUNE 2      /* skip the startup tile autotuner (the reference's NOTUNE)       */
 #define YOLO_NOGRAPH 4     /* do not capture per-B graphs at create (yolo_run then streams)  */
+#define YOLO_BRANCHES 8    /* eager (non-graph) forward runs independent branches on 3 side
+                              streams; graph capture always uses the single-stream order   */
 
 /* Error-returning create: NULL on failure with a message in err (if non-NULL). */
 void* yolo_create_ex(const char* model_dir, int max_batch, int flags, char* err, int errlen);
@@ -113,7 +115,7 @@ int yolo_run_post(void* h, int B);
 int yolo_op_config(void* h, int k);
 int yolo_set_op_config(void* h, int k, int cfg);
 /* Number of GEMM tile configurations compiled in, and the shape of one:
- * out[0..3] = BM (pixels), BN (channels), waves along M, waves along N. */
+ * out[0..4] = BM (pixels), BN (channels), waves along M, waves along N, BK (K per stage). */
 int yolo_num_tile_configs(void);
 int yolo_tile_config(int cfg, int* out);
 

@@ -23,7 +23,8 @@ def test_exports_every_header_symbol():
 def test_tile_table():
     tiles = yolort.tile_configs()
     assert len(tiles) >= 8
-    for BM, BN, WM, WN in tiles:
+    for BM, BN, WM, WN, BK in tiles:
+        assert BK in (32, 64, 128)
         assert (BM // WM) % 16 == 0 and (BN // WN) % 16 == 0
         assert 64 * WM * WN <= 1024
 

@@ -172,7 +172,8 @@ def test_thresholds_runtime(models):
     img = modelgen.synth_frame(810, 1080, 20, 1)
     eng = yolort.Engine(d, 1)
     buf = _letterbox_gpu(eng, img)
-    for conf, iou, md in [(0.25, 0.45, 300), (0.25, 0.7, 300), (0.5, 0.45, 300), (0.25, 0.45, 7)]:
+    for conf, iou, md in [(0.25, 0.45, 300), (0.25, 0.7, 300), (0.5, 0.45, 300), (0.25, 0.45, 7),
+                          (0.0, 0.45, 300), (0.0, 0.7, 100), (0.001, 0.5, 300)]:
         eng.set_thresholds(conf, iou, md)
         eng.run(1)
         got = eng.get(0)
@@ -189,3 +190,11 @@ def test_thresholds_runtime(models):
         np.testing.assert_array_equal(got[:, 5].astype(int), want["cls"])
     buf.free()
     eng.close()
+
+
+@pytest.mark.skip(reason="branch-concurrent graph capture is switched off: capturing the "
+                  "fork/join plan crashed inside hipStreamEndCapture and the cause is not isolated")
+def test_concurrent_branches_equal_serial(models):
+    """The multi-stream plan (independent branches on side streams) must give bit-identical
+    tensors and detections to the single-stream order, on every graph replay."""
+    pytest.skip("disabled")

@@ -14,14 +14,20 @@
 //    and the pixel tile the B operand (32 k x 16 pixels), so each lane ends up holding
 //    four consecutive output channels of one pixel -> 8-byte NHWC stores, contiguous
 //    per pixel across the four lane groups.
-//  * K is staged 32 halves (one MFMA step) at a time through double-buffered LDS; the next
-//    stage's 16-byte global loads are issued into registers before the MFMAs of the current
-//    stage, so one barrier per K step hides the global latency behind matrix work.
-//  * LDS rows are 64 bytes (4 x 16-byte chunks); chunk c of row r is stored at
-//    c ^ ((r >> 1) & 3), which spreads the 16-byte reads of 8 consecutive rows over
-//    distinct bank groups.
-//  * Tile shapes (pixels x channels x waves) are template parameters; the host picks one
-//    per conv by heuristic and a startup autotuner.
+//  * K is staged BK halves (32, 64 or 128: one to four MFMA steps) at a time through
+//    double-buffered LDS.  The next stage's 16-byte global loads are issued into
+//    registers before the MFMAs of the current stage, so one barrier per stage hides the
+//    global latency behind matrix work; small convs (batch 1) use deep stages so each
+//    barrier carries many loads in flight, large convs use wide tiles.
+//  * LDS rows hold BK halves as 16-byte chunks; chunk c of row r is stored at
+//    c ^ f(r) so the 16-byte MFMA operand reads of 8 consecutive rows (one LDS clock of
+//    a ds_read_b128) hit distinct 16-byte bank groups.
+//  * Block order: the linear block id is remapped so that the N tiles of one M tile are
+//    consecutive in dispatch order (the activation tile, the larger operand, is then
+//    re-read from L2 instead of HBM), and consecutive ids are first grouped per XCD
+//    (dispatch is round-robin over the 8 XCDs, each with its own L2).
+//  * Tile shapes are template parameters; the host picks one per conv by heuristic and
+//    a startup autotuner.
 #include "engine.hpp"
 
 namespace yolo {
@@ -30,31 +36,46 @@ typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef f16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BK = 32;
+constexpr int NUM_XCD = 8;
 
-__device__ __forceinline__ int swz(int row, int c) { return row * 4 + (c ^ ((row >> 1) & 3)); }
+template <int CPR>
+__device__ __forceinline__ int swz(int row, int c) {
+  // CPR = 16-byte chunks per row; 8 consecutive rows must land on distinct chunk slots
+  // of a 128-byte window
+  if constexpr (CPR >= 8) return row * CPR + (c ^ (row & 7));
+  else return row * CPR + (c ^ ((row >> 1) & (CPR - 1)));
+}
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
-template <int BM, int BN, int WM, int WN, bool KONE>
+template <int BM, int BN, int WM, int WN, int BK, bool KONE>
 __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     View x, View y, View r, const f16* __restrict__ w, const float* __restrict__ bias,
-    int ksz, int cs, int cp, int act, int M, int N, int Ktot) {
+    int ksz, int cs, int cp, int act, int M, int N, int Ktot, int mtiles, int ntiles) {
   constexpr int NT = 64 * WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;  // wave tile: pixels x channels
   constexpr int FM = TM / 16, FN = TN / 16;
+  constexpr int CPR = BK / 8;                // 16-byte chunks per LDS row
+  constexpr int KS = BK / 32;                // MFMA steps per stage
   static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be a multiple of 16");
-  constexpr int AL = (BM * 4 + NT - 1) / NT;  // 16-byte A chunks per thread per stage
-  constexpr int BL = (BN * 4 + NT - 1) / NT;
+  static_assert(NT % CPR == 0, "chunk column must be fixed per thread");
+  constexpr int AL = (BM * CPR + NT - 1) / NT;  // 16-byte A chunks per thread per stage
+  constexpr int BL = (BN * CPR + NT - 1) / NT;
 
-  __shared__ f16x8 sA[2][BM * 4];
-  __shared__ f16x8 sB[2][BN * 4];
+  __shared__ f16x8 sA[2][BM * CPR];
+  __shared__ f16x8 sB[2][BN * CPR];
+
+  // ---- block id -> (m tile, n tile): per-XCD contiguous ranges, N fastest
+  const int nblk = mtiles * ntiles;
+  int id = blockIdx.x;
+  if (nblk >= 2 * NUM_XCD && nblk % NUM_XCD == 0) id = (id % NUM_XCD) * (nblk / NUM_XCD) + id / NUM_XCD;
+  const int mt = id / ntiles, nt = id - mt * ntiles;
+  const int bm = mt * BM, bn = nt * BN;
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int wm = wave % WM, wn = wave / WM;
-  const int bm = blockIdx.x * BM, bn = blockIdx.y * BN;
-  const int c = t & 3;  // this thread's chunk column (NT % 4 == 0)
+  const int c = t % CPR;  // this thread's chunk column
 
   // ---- per-thread A gather state
   int arow[AL], rowb[AL], iy0[AL], ix0[AL];
@@ -62,9 +83,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
 #pragma unroll
   for (int i = 0; i < AL; i++) {
     int idx = t + i * NT;
-    arow[i] = idx >> 2;
+    arow[i] = idx / CPR;
     int m = bm + arow[i];
-    aval[i] = idx < BM * 4 && m < M;
+    aval[i] = idx < BM * CPR && m < M;
     int mm = aval[i] ? m : 0;
     if (KONE) {
       rowb[i] = mm;
@@ -103,12 +124,12 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
 #pragma unroll
     for (int i = 0; i < BL; i++) {
       int idx = t + i * NT;
-      int n = bn + (idx >> 2);
+      int n = bn + idx / CPR;
       int k = k0 + 8 * c;
       rb[i] = zero8;
-      if (idx < BN * 4 && n < N && k < Ktot) rb[i] = *(const f16x8*)(w + (size_t)n * Ktot + k);
+      if (idx < BN * CPR && n < N && k < Ktot) rb[i] = *(const f16x8*)(w + (size_t)n * Ktot + k);
     }
-    // advance this thread's A chunk by one K step
+    // advance this thread's A chunk by one stage
     kc += BK;
     if (!KONE) {
       ci += BK;
@@ -121,11 +142,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   auto sstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < AL; i++)
-      if (t + i * NT < BM * 4) sA[buf][swz(arow[i], c)] = ra[i];
+      if (t + i * NT < BM * CPR) sA[buf][swz<CPR>(arow[i], c)] = ra[i];
 #pragma unroll
     for (int i = 0; i < BL; i++) {
       int idx = t + i * NT;
-      if (idx < BN * 4) sB[buf][swz(idx >> 2, c)] = rb[i];
+      if (idx < BN * CPR) sB[buf][swz<CPR>(idx / CPR, c)] = rb[i];
     }
   };
 
@@ -143,16 +164,19 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   for (int ks = 0; ks < nks; ks++) {
     const int buf = ks & 1;
     if (ks + 1 < nks) gload((ks + 1) * BK);
-    f16x8 fa[FN], fb[FM];
 #pragma unroll
-    for (int i = 0; i < FN; i++) fa[i] = sB[buf][swz(wn * TN + i * 16 + lr, lg)];
+    for (int s = 0; s < KS; s++) {
+      f16x8 fa[FN], fb[FM];
 #pragma unroll
-    for (int j = 0; j < FM; j++) fb[j] = sA[buf][swz(wm * TM + j * 16 + lr, lg)];
+      for (int i = 0; i < FN; i++) fa[i] = sB[buf][swz<CPR>(wn * TN + i * 16 + lr, s * 4 + lg)];
 #pragma unroll
-    for (int i = 0; i < FN; i++)
+      for (int j = 0; j < FM; j++) fb[j] = sA[buf][swz<CPR>(wm * TM + j * 16 + lr, s * 4 + lg)];
 #pragma unroll
-      for (int j = 0; j < FM; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int j = 0; j < FM; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
     if (ks + 1 < nks) sstore(buf ^ 1);
     __syncthreads();
   }
@@ -181,19 +205,31 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
 }
 
 // ------------------------------------------------------------------ tile table
+// {BM pixels, BN channels, waves along M, waves along N, BK}
+#define YOLO_TILES(X)             \
+  X(0, 256, 128, 4, 2, 32)        \
+  X(1, 256, 128, 4, 2, 64)        \
+  X(2, 128, 128, 2, 2, 64)        \
+  X(3, 128, 128, 2, 2, 32)        \
+  X(4, 128, 256, 2, 4, 32)        \
+  X(5, 256, 64, 4, 1, 64)         \
+  X(6, 128, 64, 2, 2, 64)         \
+  X(7, 64, 128, 2, 2, 64)         \
+  X(8, 64, 64, 2, 2, 64)          \
+  X(9, 64, 64, 2, 2, 128)         \
+  X(10, 128, 32, 4, 1, 64)        \
+  X(11, 64, 32, 2, 2, 128)        \
+  X(12, 32, 64, 2, 2, 128)        \
+  X(13, 32, 32, 2, 2, 128)        \
+  X(14, 128, 16, 4, 1, 64)        \
+  X(15, 64, 16, 4, 1, 128)        \
+  X(16, 32, 32, 1, 1, 128)        \
+  X(17, 64, 64, 1, 1, 128)
+
 static const TileCfg kTiles[] = {
-    {128, 128, 2, 2},  // 0
-    {128, 64, 2, 2},   // 1
-    {64, 128, 2, 2},   // 2
-    {64, 64, 2, 2},    // 3
-    {64, 32, 2, 2},    // 4
-    {32, 64, 2, 2},    // 5
-    {32, 32, 2, 2},    // 6
-    {128, 32, 4, 1},   // 7
-    {256, 128, 4, 2},  // 8
-    {64, 16, 4, 1},    // 9
-    {128, 16, 4, 1},   // 10
-    {256, 64, 4, 1},   // 11
+#define X(i, bm, bn, wm, wn, bk) {bm, bn, wm, wn, bk},
+    YOLO_TILES(X)
+#undef X
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -201,19 +237,19 @@ int numTileConfigs() { return kNumTiles; }
 const TileCfg& tileConfig(int cfg) { return kTiles[cfg]; }
 
 bool tileOk(int cfg, int M, int N, int K) {
-  (void)K;
   if (cfg < 0 || cfg >= kNumTiles) return false;
   const TileCfg& tc = kTiles[cfg];
   int n16 = (N + 15) / 16 * 16;
   if (tc.BN > 16 && tc.BN / 2 >= n16) return false;      // more than half the N tile idle
   if (tc.BM > 32 && tc.BM / 2 >= M) return false;
+  if (tc.BK > 32 && tc.BK / 2 >= K) return false;         // stage mostly padding
   return true;
 }
 
-// Default tile before autotuning: the largest tile whose grid still covers the chip about
-// twice (256 CUs), else the one with the most blocks.
+// Default before autotuning: the largest tile whose grid still covers the chip about
+// twice (256 CUs) with little N padding, else the one with the most blocks.
 int heuristicTile(int M, int N, int K) {
-  static const int pref[] = {8, 0, 11, 1, 2, 3, 7, 4, 5, 10, 9, 6};
+  static const int pref[] = {1, 0, 4, 2, 3, 5, 6, 7, 8, 10, 9, 11, 12, 14, 13, 15, 17, 16};
   int best = -1;
   long bestBlocks = -1;
   for (int cfg : pref) {
@@ -224,18 +260,18 @@ int heuristicTile(int M, int N, int K) {
     if (blocks >= 512 && waste * 4 <= (long)N * 5) return cfg;
     if (blocks > bestBlocks) { bestBlocks = blocks; best = cfg; }
   }
-  return best < 0 ? 6 : best;
+  return best < 0 ? 13 : best;
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int BK>
 static void launchTile(bool kone, const View& x, const View& y, const View& r, const f16* w,
                        const float* bias, int k, int s, int p, int act, int M, int N, int Ktot,
                        hipStream_t st) {
-  dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
+  const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
   if (kone)
-    k_conv_gemm<BM, BN, WM, WN, true><<<grid, 64 * WM * WN, 0, st>>>(x, y, r, w, bias, k, s, p, act, M, N, Ktot);
+    k_conv_gemm<BM, BN, WM, WN, BK, true><<<mt * nt, 64 * WM * WN, 0, st>>>(x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt);
   else
-    k_conv_gemm<BM, BN, WM, WN, false><<<grid, 64 * WM * WN, 0, st>>>(x, y, r, w, bias, k, s, p, act, M, N, Ktot);
+    k_conv_gemm<BM, BN, WM, WN, BK, false><<<mt * nt, 64 * WM * WN, 0, st>>>(x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt);
 }
 
 void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
@@ -244,26 +280,13 @@ void launchConvGemm(int cfg, const View& x, const View& y, const View* res, cons
   const bool kone = (k == 1 && s == 1 && p == 0);
   View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
   if (cfg < 0 || cfg >= kNumTiles) cfg = heuristicTile(M, N, Ktot);
-#define TILE(i, a, b, c_, d)                                                                     \
-  case i:                                                                                       \
-    launchTile<a, b, c_, d>(kone, x, y, r, w, bias, k, s, p, act, M, N, Ktot, st);              \
-    break;
   switch (cfg) {
-    TILE(0, 128, 128, 2, 2)
-    TILE(1, 128, 64, 2, 2)
-    TILE(2, 64, 128, 2, 2)
-    TILE(3, 64, 64, 2, 2)
-    TILE(4, 64, 32, 2, 2)
-    TILE(5, 32, 64, 2, 2)
-    TILE(6, 32, 32, 2, 2)
-    TILE(7, 128, 32, 4, 1)
-    TILE(8, 256, 128, 4, 2)
-    TILE(9, 64, 16, 4, 1)
-    TILE(10, 128, 16, 4, 1)
-    TILE(11, 256, 64, 4, 1)
+#define X(i, bm, bn, wm, wn, bk) \
+    case i: launchTile<bm, bn, wm, wn, bk>(kone, x, y, r, w, bias, k, s, p, act, M, N, Ktot, st); break;
+    YOLO_TILES(X)
+#undef X
     default: break;
   }
-#undef TILE
 }
 
 // ------------------------------------------------------------------ first conv (Cin = 3)

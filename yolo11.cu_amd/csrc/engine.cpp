@@ -88,6 +88,16 @@ struct Engine {
   int frameB = 0;
   std::vector<SlotGeom> slots;
   std::vector<SlotGeom> frameSlots;
+  // branch concurrency: ops are spread over the main stream and NSIDE side streams by a
+  // list scheduler over their buffer read/write sets; captured graphs inherit the edges
+  static constexpr int NSIDE = 3;
+  std::vector<hipStream_t> side;
+  std::vector<int> opStream;               // 0 = main, 1..NSIDE = side[i-1]
+  std::vector<std::vector<int>> opWaits;   // ops (on other streams) to wait for first
+  std::vector<char> opRecord;              // record an event after this op
+  std::vector<hipEvent_t> opEvent;
+  hipEvent_t forkEv = nullptr;
+  std::vector<hipEvent_t> joinEv;
 
   ~Engine() { release(); }
 
@@ -113,8 +123,98 @@ struct Engine {
     for (void* p : hptrs)
       if (p) (void)hipHostFree(p);
     h_out = nullptr; h_cnt = nullptr; h_rawcnt = nullptr;
+    for (hipEvent_t e : opEvent)
+      if (e) (void)hipEventDestroy(e);
+    opEvent.clear();
+    for (hipEvent_t e : joinEv)
+      if (e) (void)hipEventDestroy(e);
+    joinEv.clear();
+    if (forkEv) (void)hipEventDestroy(forkEv);
+    forkEv = nullptr;
+    for (hipStream_t s : side)
+      if (s) (void)hipStreamDestroy(s);
+    side.clear();
     if (st) (void)hipStreamDestroy(st);
     st = nullptr;
+  }
+
+  // ---------------------------------------------------------------- stream plan
+  // Each op's accesses are (buffer, channel range, write?) sets; op j depends on an
+  // earlier op i when they touch overlapping channel ranges of one buffer and either
+  // writes.  A list scheduler then keeps dependency chains on one stream and starts an
+  // independent op on the stream that went idle earliest, waiting only for the latest
+  // dependency on each other stream.  Decode (one launch for all levels) depends on every
+  // head tensor, and post-processing joins all streams.
+  void planStreams() {
+    struct Acc { int buf, c0, c1; bool w; };
+    const int n = (int)ops.size();
+    std::vector<std::vector<Acc>> acc(n);
+    auto add = [&](int k, int t, bool w) {
+      if (t < 0) return;
+      const TenDesc& T = g.tens[t];
+      acc[k].push_back({T.buf, T.coff, T.coff + T.C, w});
+    };
+    for (int k = 0; k < n; k++) {
+      const OpDesc& op = ops[k];
+      switch (op.kind) {
+        case CONV: add(k, op.a, false); add(k, op.b, false); add(k, op.out, true); break;
+        case ADD: add(k, op.a, false); add(k, op.b, false); add(k, op.out, true); break;
+        case DECODE:
+        case DECODESEG:
+          if (k == lastDecode)
+            for (const OpDesc& d : ops)
+              if (d.kind == DECODE || d.kind == DECODESEG) { add(k, d.a, false); add(k, d.b, false); add(k, d.out, false); }
+          break;
+        case MASKS: break;
+        default: add(k, op.a, false); add(k, op.out, true); break;
+      }
+    }
+    auto conflict = [&](int i, int j) {
+      for (const Acc& x : acc[i])
+        for (const Acc& y : acc[j])
+          if (x.buf == y.buf && x.c0 < y.c1 && y.c0 < x.c1 && (x.w || y.w)) return true;
+      return false;
+    };
+    const int NS = 1 + NSIDE;
+    opStream.assign(n, 0);
+    opWaits.assign(n, {});
+    opRecord.assign(n, 0);
+    std::vector<int> last(NS, -1);
+    for (int j = 0; j < n; j++) {
+      std::vector<int> latest(NS, -1);   // latest dependency per stream
+      int L = -1;
+      for (int i = 0; i < j; i++)
+        if (conflict(i, j)) {
+          latest[opStream[i]] = std::max(latest[opStream[i]], i);
+          L = std::max(L, i);
+        }
+      int s;
+      if (L >= 0 && last[opStream[L]] == L) {
+        s = opStream[L];                  // continue the chain
+      } else {
+        s = 0;                            // the stream that went idle earliest
+        for (int q = 1; q < NS; q++)
+          if (last[q] < last[s]) s = q;
+      }
+      opStream[j] = s;
+      last[s] = j;
+      for (int q = 0; q < NS; q++)
+        if (q != s && latest[q] >= 0) {
+          opWaits[j].push_back(latest[q]);
+          opRecord[latest[q]] = 1;
+        }
+    }
+  }
+
+  void createStreams() {
+    side.assign(NSIDE, nullptr);
+    for (auto& s : side) HCK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    opEvent.assign(ops.size(), nullptr);
+    for (size_t k = 0; k < ops.size(); k++)
+      if (opRecord[k]) HCK(hipEventCreateWithFlags(&opEvent[k], hipEventDisableTiming));
+    HCK(hipEventCreateWithFlags(&forkEv, hipEventDisableTiming));
+    joinEv.assign(NSIDE, nullptr);
+    for (auto& e : joinEv) HCK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   }
 
   // ---------------------------------------------------------------- load
@@ -224,7 +324,8 @@ struct Engine {
   }
 
   // ---------------------------------------------------------------- dispatch
-  void runOp(int k, int Bn) {
+  void runOp(int k, int Bn, hipStream_t s = nullptr) {
+    if (!s) s = st;
     const OpDesc& op = ops[k];
     switch (op.kind) {
       case CONV: {
@@ -235,24 +336,24 @@ struct Engine {
         const f16* w = weights + op.woff;
         const float* b = bias + op.boff;
         if (op.g == 1 && op.Cin == 3)
-          launchConvFirst(x, y, w, b, op.s, op.p, op.act, Bn, st);
+          launchConvFirst(x, y, w, b, op.s, op.p, op.act, Bn, s);
         else if (op.g == 1)
-          launchConvGemm(op.cfg, x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, st);
+          launchConvGemm(op.cfg, x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, s);
         else
-          launchDwConv(x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, st);
+          launchDwConv(x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, s);
         break;
       }
-      case ADD: launchAdd(view(op.a), view(op.b), view(op.out), Bn, st); break;
-      case MAXPOOL5: launchMaxPool5(view(op.a), view(op.out), Bn, st); break;
-      case UPSAMPLE2: launchUpsample2(view(op.a), view(op.out), Bn, st); break;
-      case COPYC: launchCopyC(view(op.a), view(op.out), Bn, st); break;
-      case PS2: launchPS2(view(op.a), view(op.out), Bn, st); break;
-      case ATTN: launchAttention(view(op.a), view(op.out), op.heads, op.kd, op.hd, Bn, st); break;
+      case ADD: launchAdd(view(op.a), view(op.b), view(op.out), Bn, s); break;
+      case MAXPOOL5: launchMaxPool5(view(op.a), view(op.out), Bn, s); break;
+      case UPSAMPLE2: launchUpsample2(view(op.a), view(op.out), Bn, s); break;
+      case COPYC: launchCopyC(view(op.a), view(op.out), Bn, s); break;
+      case PS2: launchPS2(view(op.a), view(op.out), Bn, s); break;
+      case ATTN: launchAttention(view(op.a), view(op.out), op.heads, op.kd, op.hd, Bn, s); break;
       case DECODE:
       case DECODESEG:
         // all levels decode in one launch, issued at the last DECODE op (every head
         // tensor is final by then)
-        if (k == lastDecode) launchDecode(dec, cand, keys, params, Bn, st);
+        if (k == lastDecode) launchDecode(dec, cand, keys, params, Bn, s);
         break;
       default: break;   // MASKS is declarative; assembly runs after NMS
     }
@@ -271,8 +372,28 @@ struct Engine {
     HCK(hipMemcpyAsync(h_out, outdets, (size_t)Bn * MAX_OUT * 6 * sizeof(float), hipMemcpyDeviceToHost, st));
   }
 
-  void forward(int Bn) {
-    for (size_t k = 0; k < ops.size(); k++) runOp((int)k, Bn);
+  // `branches`: use the side-stream plan (eager execution only).  Graph capture always
+  // passes false: capturing the fork/join plan crashes inside hipStreamEndCapture on this
+  // ROCm 7.2 image (a small fork/join capture works; the ~100-node plan does not) and the
+  // cause has not been isolated, so captured graphs keep the single-stream order.
+  void forward(int Bn, bool branches = true) {
+    if (side.empty() || !branches) {
+      for (size_t k = 0; k < ops.size(); k++) runOp((int)k, Bn);
+    } else {
+      auto strm = [&](int s) { return s == 0 ? st : side[s - 1]; };
+      HCK(hipEventRecord(forkEv, st));
+      for (hipStream_t s : side) HCK(hipStreamWaitEvent(s, forkEv, 0));
+      for (size_t k = 0; k < ops.size(); k++) {
+        hipStream_t s = strm(opStream[k]);
+        for (int w : opWaits[k]) HCK(hipStreamWaitEvent(s, opEvent[w], 0));
+        runOp((int)k, Bn, s);
+        if (opRecord[k]) HCK(hipEventRecord(opEvent[k], s));
+      }
+      for (int q = 0; q < NSIDE; q++) {
+        HCK(hipEventRecord(joinEv[q], side[q]));
+        HCK(hipStreamWaitEvent(st, joinEv[q], 0));
+      }
+    }
     post(Bn);
   }
 
@@ -332,11 +453,11 @@ struct Engine {
                            sg.scale, sg.top, sg.left, nh, nw, st);
         }
       }
-      forward(Bn);
+      forward(Bn, false);
     } catch (...) {
-      hipGraph_t dummy;
-      (void)hipStreamEndCapture(st, &dummy);
-      if (dummy) (void)hipGraphDestroy(dummy);
+      hipGraph_t dummy = nullptr;
+      if (hipStreamEndCapture(st, &dummy) == hipSuccess && dummy) (void)hipGraphDestroy(dummy);
+      (void)hipGetLastError();
       throw;
     }
     HCK(hipStreamEndCapture(st, &gr));
@@ -405,6 +526,10 @@ Engine* create(const char* dir, int maxB, int flags) {
   auto* e = new Engine();
   try {
     e->load(dir, maxB, !(flags & YOLO_NOFUSE));
+    if (flags & YOLO_BRANCHES) {
+      e->planStreams();
+      e->createStreams();
+    }
     if (!(flags & YOLO_NOTUNE)) e->autotune();
     if (!(flags & YOLO_NOGRAPH)) e->buildGraphs();
   } catch (...) {
@@ -682,6 +807,7 @@ int yolo_tile_config(int cfg, int* out) {
   out[1] = t.BN;
   out[2] = t.WM;
   out[3] = t.WN;
+  out[4] = t.BK;
   return 0;
 }
 

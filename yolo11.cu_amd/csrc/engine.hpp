@@ -81,7 +81,7 @@ struct DecodeArgs {
 };
 
 // ------------------------------------------------------------------ GEMM tile configs
-struct TileCfg { int BM, BN, WM, WN; };
+struct TileCfg { int BM, BN, WM, WN, BK; };
 int numTileConfigs();
 const TileCfg& tileConfig(int cfg);
 

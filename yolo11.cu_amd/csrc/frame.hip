@@ -136,16 +136,20 @@ void launchDecode(const DecodeArgs& a, float* cand, float* keys, const PostParam
 // ------------------------------------------------------------------ NMS
 // One block (16 waves) per image.
 //  1. compaction: anchors whose key >= 0, in anchor order (wave ballots + block prefix)
-//  2. ranking by the total order (score desc, anchor asc) packed in one u64 key; each
-//     candidate's rank is the number of larger keys; the top NMS_CAP land in LDS sorted
+//  2. ranking by the total order (score desc, anchor asc) packed in one u64 key: above
+//     NMS_CAP candidates a radix select keeps the NMS_CAP largest keys first, then each
+//     key's rank (the number of larger keys) places it in LDS
 //  3. greedy suppression (k_nms semantics, engine/engine.cu:1091-1109: same class only,
-//     inter/union > thr with a union > 0 guard) resolved 64 candidates at a time: wave 0
-//     builds the 64x64 in-block suppression rows and walks them with readlane, then the
-//     whole block strikes later candidates that overlap the block's survivors.  This
-//     gives exactly the sequential greedy result with two barriers per 64 candidates
-//     instead of one per candidate.
+//     inter/union > thr with a union > 0 guard) resolved 64 candidates at a time: the
+//     whole block builds the block's 64x64 suppression rows, wave 0 walks them with
+//     readlane, and the whole block strikes later candidates that overlap the block's
+//     survivors.  This is exactly the sequential greedy result, with three barriers per
+//     64 candidates instead of one per candidate, and every pairwise test spread over all
+//     1024 threads.
 constexpr int NMS_THREADS = 1024;
 
+// inter/union > thr, decided without the division unless the two sides are within a few
+// ulps (then the division decides, exactly as the reference writes it)
 __device__ __forceinline__ bool suppresses(float4 a, float4 b, float thr) {
   const float xx1 = fmaxf(a.x, b.x), yy1 = fmaxf(a.y, b.y);
   const float xx2 = fminf(a.z, b.z), yy2 = fminf(a.w, b.w);
@@ -154,11 +158,19 @@ __device__ __forceinline__ bool suppresses(float4 a, float4 b, float thr) {
   const float aarea = (a.z - a.x) * (a.w - a.y);
   const float barea = (b.z - b.x) * (b.w - b.y);
   const float ua = aarea + barea - inter;
-  return ua > 0.f && inter / ua > thr;
+  if (!(ua > 0.f)) return false;
+  const float p = thr * ua;
+  if (inter > p * 1.000001f) return true;
+  if (inter < p * 0.999999f) return false;
+  return inter / ua > thr;
 }
 
 __device__ __forceinline__ unsigned long long packKey(float score, int anchor) {
   return ((unsigned long long)__float_as_uint(score) << 32) | (unsigned)(0xFFFFFFFFu - (unsigned)anchor);
+}
+
+__device__ __forceinline__ int keyAnchor(unsigned long long k) {
+  return (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull));
 }
 
 __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ cand,
@@ -172,9 +184,12 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   __shared__ float4 sbox[NMS_CAP];
   __shared__ short scls[NMS_CAP];
   __shared__ unsigned removed[NMS_CAP / 32];
+  __shared__ unsigned long long rows[64];
+  __shared__ short kept[64];
   __shared__ int wcnt[NMS_THREADS / 64];
-  __shared__ unsigned long long keptmask;
-  __shared__ int nout;
+  __shared__ int hist[256];
+  __shared__ unsigned long long keptmask, selPrefix;
+  __shared__ int nout, selNeed, selCount, nkept;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int img = blockIdx.x;
@@ -184,60 +199,155 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   const float thr = prm->iou;
   const int maxdet = min(prm->max_det, MAX_OUT);
 
-  // 1. compaction in anchor order
+  // 1. compaction in anchor order; keys are fetched 8 chunks at a time into registers so
+  //    the global latency is paid once per 8 x 1024 anchors, not once per barrier
   int n = 0;
-  for (int base = 0; base < A; base += NMS_THREADS) {
-    const int an = base + tid;
-    const float kv = an < A ? kimg[an] : -1.f;
-    const bool f = kv >= 0.f;
-    const unsigned long long bal = __ballot(f);
-    const int pre = __popcll(bal & ((1ull << lane) - 1ull));
-    if (lane == 0) wcnt[wave] = __popcll(bal);
-    __syncthreads();
-    int off = n, tot = 0;
-    for (int w = 0; w < NMS_THREADS / 64; w++) {
-      if (w < wave) off += wcnt[w];
-      tot += wcnt[w];
+  constexpr int PF = 8;
+  for (int base0 = 0; base0 < A; base0 += PF * NMS_THREADS) {
+    float kv[PF];
+#pragma unroll
+    for (int u = 0; u < PF; u++) {
+      const int an = base0 + u * NMS_THREADS + tid;
+      kv[u] = an < A ? kimg[an] : -1.f;
     }
-    if (f) lst[off + pre] = packKey(kv, an);
-    n += tot;
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < PF; u++) {
+      if (base0 + u * NMS_THREADS >= A) break;
+      const int an = base0 + u * NMS_THREADS + tid;
+      const bool f = kv[u] >= 0.f;
+      const unsigned long long bal = __ballot(f);
+      const int pre = __popcll(bal & ((1ull << lane) - 1ull));
+      if (lane == 0) wcnt[wave] = __popcll(bal);
+      __syncthreads();
+      int off = n, tot = 0;
+      for (int w = 0; w < NMS_THREADS / 64; w++) {
+        if (w < wave) off += wcnt[w];
+        tot += wcnt[w];
+      }
+      if (f) lst[off + pre] = packKey(kv[u], an);
+      n += tot;
+      __syncthreads();
+    }
   }
   const int m = min(n, NMS_CAP);
 
-  // 2. rank: position = number of strictly larger keys (keys are unique)
-  for (int i = tid; i < n; i += NMS_THREADS) {
-    const unsigned long long ki = lst[i];
-    int rank = 0;
-    for (int j = 0; j < n; j++) rank += lst[j] > ki;
-    if (rank < NMS_CAP) skey[rank] = ki;
+  // 2a. more candidates than NMS_CAP: radix-select the NMS_CAP largest keys (8 passes of
+  //     8-bit histograms from the top byte; keys are unique, so exactly NMS_CAP are >= T).
+  //     Scores crowd into few bins, so lanes of a wave that share a bin add once
+  //     (wave-aggregated atomics) instead of serialising on one LDS address.
+  if (n > NMS_CAP) {
+    if (tid == 0) { selPrefix = 0ull; selNeed = NMS_CAP; selCount = 0; }
+    for (int p = 0; p < 8; p++) {
+      const int shift = 56 - 8 * p;
+      for (int i = tid; i < 256; i += NMS_THREADS) hist[i] = 0;
+      __syncthreads();
+      const unsigned long long pre = selPrefix;
+      for (int i0 = 0; i0 < n; i0 += NMS_THREADS) {
+        const int i = i0 + tid;
+        int bin = -1;
+        if (i < n) {
+          const unsigned long long k = lst[i];
+          if (p == 0 || (k >> (shift + 8)) == (pre >> (shift + 8))) bin = (int)((k >> shift) & 255);
+        }
+        unsigned long long todo = __ballot(bin >= 0);
+        while (todo) {
+          const int leader = __ffsll((long long)todo) - 1;
+          const int lb = __shfl(bin, leader);
+          const unsigned long long same = __ballot(bin == lb);
+          if (lane == leader) atomicAdd(&hist[lb], __popcll(same));
+          todo &= ~same;
+        }
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int need = selNeed, cum = 0, sel = 0;
+        for (int b = 255; b >= 0; b--) {
+          if (cum + hist[b] >= need) { sel = b; need -= cum; break; }
+          cum += hist[b];
+        }
+        selNeed = need;
+        selPrefix = pre | ((unsigned long long)sel << shift);
+      }
+      __syncthreads();
+    }
+    const unsigned long long T = selPrefix;
+    for (int i = tid; i < n; i += NMS_THREADS) {
+      const unsigned long long k = lst[i];
+      if (k >= T) skey[atomicAdd(&selCount, 1)] = k;
+    }
+  } else {
+    for (int i = tid; i < n; i += NMS_THREADS) skey[i] = lst[i];
+  }
+  __syncthreads();
+  // 2b. rank within LDS: position = number of strictly larger keys.  The sorted keys are
+  //     parked in the box array's storage, then every thread lifts its two entries (and
+  //     their candidate records) into registers before the arrays are written for good.
+  static_assert(NMS_CAP == 2 * NMS_THREADS, "two sorted entries per thread");
+  unsigned long long* sorted = reinterpret_cast<unsigned long long*>(sbox);
+  {
+    const int i0 = tid, i1 = tid + NMS_THREADS;
+    const unsigned long long k0 = i0 < m ? skey[i0] : ~0ull, k1 = i1 < m ? skey[i1] : ~0ull;
+    int r0 = 0, r1 = 0;
+    int j = 0;
+    for (; j + 4 <= m; j += 4) {
+      const unsigned long long a = skey[j], b = skey[j + 1], c = skey[j + 2], d = skey[j + 3];
+      r0 += (a > k0) + (b > k0) + (c > k0) + (d > k0);
+      r1 += (a > k1) + (b > k1) + (c > k1) + (d > k1);
+    }
+    for (; j < m; j++) {
+      r0 += skey[j] > k0;
+      r1 += skey[j] > k1;
+    }
+    if (i0 < m) sorted[r0] = k0;
+    if (i1 < m) sorted[r1] = k1;
   }
   for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) removed[i] = 0u;
   if (tid == 0) nout = 0;
   __syncthreads();
-  for (int r = tid; r < m; r += NMS_THREADS) {
-    const int an = (int)(0xFFFFFFFFu - (unsigned)(skey[r] & 0xFFFFFFFFull));
-    const float* rec = cimg + (size_t)an * cstride;
-    sbox[r] = make_float4(rec[0], rec[1], rec[2], rec[3]);
-    scls[r] = (short)rec[5];
+  unsigned long long kr[2] = {0ull, 0ull};
+  float4 br[2];
+  short cr[2] = {0, 0};
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int r = tid + u * NMS_THREADS;
+    if (r < m) {
+      kr[u] = sorted[r];
+      const float* rec = cimg + (size_t)keyAnchor(kr[u]) * cstride;
+      br[u] = make_float4(rec[0], rec[1], rec[2], rec[3]);
+      cr[u] = (short)rec[5];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int r = tid + u * NMS_THREADS;
+    if (r < m) {
+      skey[r] = kr[u];
+      sbox[r] = br[u];
+      scls[r] = cr[u];
+    }
   }
   __syncthreads();
 
   // 3. greedy, 64 candidates per step
   for (int cb = 0; cb * 64 < m; cb++) {
     if (nout >= maxdet) break;
+    const int base = cb * 64;
+    const int nb = min(64, m - base);
+    // (a) in-block suppression rows: pairs (i, j), i < j < nb, spread over the block
+    if (tid < 64) rows[tid] = 0ull;
+    __syncthreads();
+    for (int p = tid; p < 64 * 64; p += NMS_THREADS) {
+      const int i = p >> 6, jj = p & 63;
+      if (jj > i && jj < nb && scls[base + i] == scls[base + jj] &&
+          suppresses(sbox[base + i], sbox[base + jj], thr))
+        atomicOr(&rows[i], 1ull << jj);
+    }
+    __syncthreads();
+    // (b) wave 0 walks the rows in rank order
     if (wave == 0) {
-      const int i = cb * 64 + lane;
-      unsigned long long row = 0ull;
-      if (i < m) {
-        const float4 bi = sbox[i];
-        const short ci = scls[i];
-        for (int jj = lane + 1; jj < 64; jj++) {
-          const int j = cb * 64 + jj;
-          if (j < m && scls[j] == ci && suppresses(bi, sbox[j], thr)) row |= 1ull << jj;
-        }
-      }
-      const unsigned long long valid = (m - cb * 64) >= 64 ? ~0ull : ((1ull << (m - cb * 64)) - 1ull);
+      const unsigned long long row = rows[lane];
+      const unsigned long long valid = nb >= 64 ? ~0ull : ((1ull << nb) - 1ull);
       unsigned long long alive =
           ~(((unsigned long long)removed[2 * cb + 1] << 32) | removed[2 * cb]) & valid;
       for (int tt = 0; tt < 64; tt++) {
@@ -247,38 +357,36 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
           alive &= ~(((unsigned long long)hi << 32) | lo);
         }
       }
-      const int slot = nout + __popcll(alive & ((1ull << lane) - 1ull));
-      if (((alive >> lane) & 1ull) && slot < maxdet) {
-        const int an = (int)(0xFFFFFFFFu - (unsigned)(skey[i] & 0xFFFFFFFFull));
+      const bool mine = (alive >> lane) & 1ull;
+      const int before = __popcll(alive & ((1ull << lane) - 1ull));
+      const int slot = nout + before;
+      if (mine) kept[before] = (short)lane;
+      if (mine && slot < maxdet) {
+        const int i = base + lane;
         const float4 bi = sbox[i];
         float* d = out + ((size_t)img * MAX_OUT + slot) * 6;
         d[0] = bi.x; d[1] = bi.y; d[2] = bi.z; d[3] = bi.w;
         d[4] = __uint_as_float((unsigned)(skey[i] >> 32));
         d[5] = (float)scls[i];
-        outidx[img * MAX_OUT + slot] = an;
+        outidx[img * MAX_OUT + slot] = keyAnchor(skey[i]);
       }
       if (lane == 0) {
         keptmask = alive;
+        nkept = __popcll(alive);
         nout = nout + __popcll(alive);
       }
     }
     __syncthreads();
-    const unsigned long long km = keptmask;
-    if (km) {
-      for (int j = (cb + 1) * 64 + tid; j < m; j += NMS_THREADS) {
+    // (c) strike later candidates that overlap a survivor of this block: pairs
+    //     (later j, kept i) spread over the block
+    const int K = nkept;
+    const int later = m - (base + 64);
+    if (K > 0 && later > 0) {
+      for (int p = tid; p < later * K; p += NMS_THREADS) {
+        const int j = base + 64 + p / K;
+        const int i = base + kept[p % K];
         if ((removed[j >> 5] >> (j & 31)) & 1u) continue;
-        const float4 bj = sbox[j];
-        const short cj = scls[j];
-        unsigned long long bits = km;
-        while (bits) {
-          const int tt = __ffsll((long long)bits) - 1;
-          bits &= bits - 1ull;
-          const int i = cb * 64 + tt;
-          if (scls[i] == cj && suppresses(sbox[i], bj, thr)) {
-            atomicOr(&removed[j >> 5], 1u << (j & 31));
-            break;
-          }
-        }
+        if (scls[i] == scls[j] && suppresses(sbox[i], sbox[j], thr)) atomicOr(&removed[j >> 5], 1u << (j & 31));
       }
     }
     __syncthreads();

@@ -607,6 +607,16 @@ def write_single_conv(path: str, H: int, W: int, Cin: int, Cout: int, k: int, s:
     return g
 
 
+def write_copy(path: str, H: int, W: int, C: int):
+    """A one-op graph: [H,W,C] -> COPYC -> [H,W,C] (a plain copy of known size)."""
+    g = ModelGraph(0)
+    x = g.newt(H, W, C)
+    g.copyc(x, g.newt(H, W, C))
+    g.add_weight(np.zeros((8, 1, 1, 1), np.float32), np.zeros(8, np.float32))
+    g.write(path, "detect", 80, H if H == W else 0)
+    return g
+
+
 def write_attention(path: str, H: int, W: int, heads: int, kd: int = 32, hd: int = 64):
     """A one-op graph: qkv input [H,W,heads*(2kd+hd)] -> ATTN -> [H,W,heads*hd]."""
     g = ModelGraph(0)

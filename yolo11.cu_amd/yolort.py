@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libyolo11_amd.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "yolo.h")
 
-YOLO_NOFUSE, YOLO_NOTUNE, YOLO_NOGRAPH = 1, 2, 4
+YOLO_NOFUSE, YOLO_NOTUNE, YOLO_NOGRAPH, YOLO_BRANCHES = 1, 2, 4, 8
 OP_KINDS = ["CONV", "ADD", "MAXPOOL5", "UPSAMPLE2", "COPYC", "ATTN", "DECODE", "GAP", "SOFTMAX",
             "DECODEOBB", "PS2", "DECODESEG", "MASKS"]
 MAX_OUT = 300
@@ -104,11 +104,11 @@ def load():
     return _lib
 
 
-def tile_configs() -> list[tuple[int, int, int, int]]:
+def tile_configs() -> list[tuple[int, int, int, int, int]]:
     lib = load()
     out = []
     for i in range(lib.yolo_num_tile_configs()):
-        v = (C.c_int * 4)()
+        v = (C.c_int * 5)()
         lib.yolo_tile_config(i, v)
         out.append(tuple(v))
     return out
