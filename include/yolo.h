@@ -115,7 +115,8 @@ int yolo_run_post(void* h, int B);
 int yolo_op_config(void* h, int k);
 int yolo_set_op_config(void* h, int k, int cfg);
 /* Number of GEMM tile configurations compiled in, and the shape of one:
- * out[0..4] = BM (pixels), BN (channels), waves along M, waves along N, BK (K per stage). */
+ * out[0..5] = BM (pixels), BN (channels), waves along M, waves along N, BK (K per stage),
+ * LDS ring stages. */
 int yolo_num_tile_configs(void);
 int yolo_tile_config(int cfg, int* out);
 

@@ -23,10 +23,15 @@ def test_exports_every_header_symbol():
 def test_tile_table():
     tiles = yolort.tile_configs()
     assert len(tiles) >= 8
-    for BM, BN, WM, WN, BK in tiles:
+    for BM, BN, WM, WN, BK, NS in tiles:
         assert BK in (32, 64, 128)
         assert (BM // WM) % 16 == 0 and (BN // WN) % 16 == 0
-        assert 64 * WM * WN <= 1024
+        assert 64 * WM * WN <= 1024 and (WM * WN) % 4 == 0
+        assert 2 <= NS <= 4
+        # the LDS ring fits the 160 KiB of a CU
+        assert NS * (BM + BN) * BK * 2 <= 160 * 1024
+        # every wave issues the same number of 64-chunk DMA groups for both operands
+        assert (BM * BK // 8 // 64) % (WM * WN) == 0 and (BN * BK // 8 // 64) % (WM * WN) == 0
 
 
 @pytest.mark.parametrize("arch,scale,task,nops", [("yolo11", "n", "detect", 112), ("yolo11", "m", "detect", 144),

@@ -7,25 +7,36 @@
 //   ("dense K": no per-tap padding), W = OHWI weights, A = the im2col row of pixel m,
 //   gathered on the fly from the NHWC input (no im2col buffer).
 // Epilogue: + bias, SiLU (act 1), + residual (act first, then +res), fp16 store into a
-// strided channel slice, so concat is zero-copy.  Accumulation is always fp32.
+//   strided channel slice, so concat is zero-copy.  Accumulation is always fp32.
 //
 // MI355X design:
 //  * v_mfma_f32_16x16x32_f16: the weight tile is the MFMA A operand (16 channels x 32 k)
 //    and the pixel tile the B operand (32 k x 16 pixels), so each lane ends up holding
-//    four consecutive output channels of one pixel -> 8-byte NHWC stores, contiguous
-//    per pixel across the four lane groups.
-//  * K is staged BK halves (32, 64 or 128: one to four MFMA steps) at a time through
-//    double-buffered LDS.  The next stage's 16-byte global loads are issued into
-//    registers before the MFMAs of the current stage, so one barrier per stage hides the
-//    global latency behind matrix work; small convs (batch 1) use deep stages so each
-//    barrier carries many loads in flight, large convs use wide tiles.
-//  * LDS rows hold BK halves as 16-byte chunks; chunk c of row r is stored at
-//    c ^ f(r) so the 16-byte MFMA operand reads of 8 consecutive rows (one LDS clock of
-//    a ds_read_b128) hit distinct 16-byte bank groups.
+//    four output channels of one pixel.
+//  * Global -> LDS without registers: every 16-byte chunk of a K stage (BK halves of BM
+//    pixel rows and BN weight rows) is fetched by buffer_load_dwordx4 ... lds, which
+//    writes lane L's 16 bytes to LDS at M0 + 16*L.  The buffer descriptor's range check
+//    returns zeros for offsets past the tensor, so the halo of the 3x3 window, the pixel
+//    tail (m >= M), the channel tail (n >= N) and the K tail are all a single "offset =
+//    OOB" select, with no branches and no zero stores.
+//  * An NS-stage LDS ring (NS = 2..4, one __shared__ array per stage so the compiler's
+//    LDS-DMA alias tracking sees distinct objects): while the MFMAs consume stage k, the
+//    DMA of stages k+1 .. k+NS-1 is in flight.  One s_barrier per stage; each wave waits
+//    only for its own loads of stage k (s_waitcnt vmcnt with the count of loads issued
+//    after it), and the barrier makes every wave's stage-k chunks visible.
+//  * LDS rows hold BK halves as 16-byte chunks; chunk c of row r is stored at c ^ f(r),
+//    with f chosen so that the 16-byte operand reads of 16 consecutive rows at one logical
+//    chunk land in distinct 16-byte slots modulo 256 bytes (and 8 aligned rows modulo 128
+//    bytes).  Since the DMA fixes the slot per lane, the swizzle is realised by the choice
+//    of which global chunk each lane fetches.
+//  * Weight rows of each 32-channel group are loaded in the order 8*(j/4) + 4*h + j%4
+//    (fragment h, row j), so after the MFMAs a lane holds 8 consecutive output channels
+//    across a fragment pair: 16-byte bias/residual loads and 16-byte NHWC stores, 64
+//    contiguous bytes per pixel per wave store.
 //  * Block order: the linear block id is remapped so that the N tiles of one M tile are
-//    consecutive in dispatch order (the activation tile, the larger operand, is then
-//    re-read from L2 instead of HBM), and consecutive ids are first grouped per XCD
-//    (dispatch is round-robin over the 8 XCDs, each with its own L2).
+//    consecutive in dispatch order (the activation tile is then re-read from L2), and
+//    consecutive ids are first grouped per XCD (dispatch is round-robin over the 8 XCDs,
+//    each with its own L2).
 //  * Tile shapes are template parameters; the host picks one per conv by heuristic and
 //    a startup autotuner.
 #include "engine.hpp"
@@ -35,35 +46,92 @@ namespace yolo {
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef f16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
 constexpr int NUM_XCD = 8;
+constexpr unsigned OOB_OFF = 0x80000000u;  // past every descriptor's num_records (< 2^31)
 
+template <int N>
+using ic = std::integral_constant<int, N>;
+
+// Slot permutation of the chunks of LDS row `row` (CPR chunks of 16 bytes per row).  It reads
+// only bits 0..3 of the row: fragment reads start at multiples of 16 rows, and a thread's DMA
+// rows differ by multiples of 16, so both sides can evaluate it on (row & 15).
 template <int CPR>
-__device__ __forceinline__ int swz(int row, int c) {
-  // CPR = 16-byte chunks per row; 8 consecutive rows must land on distinct chunk slots
-  // of a 128-byte window
-  if constexpr (CPR >= 8) return row * CPR + (c ^ (row & 7));
-  else return row * CPR + (c ^ ((row >> 1) & (CPR - 1)));
+__device__ __forceinline__ int swzf(int row) {
+  if constexpr (CPR == 4) return ((row >> 1) ^ ((row >> 3) & 1)) & 3;
+  else if constexpr (CPR == 8) return (row ^ ((row >> 3) & 1)) & 7;
+  else return row & 15;
+}
+template <int CPR>
+__device__ __forceinline__ int swz(int row, int c) { return row * CPR + (c ^ swzf<CPR>(row)); }
+
+// Output channel held by LDS weight row r when fragment pairs are interleaved.
+__device__ __forceinline__ int chperm(int r) {
+  return (r & ~31) | (((r >> 2) & 3) << 3) | (((r >> 4) & 1) << 2) | (r & 3);
+}
+
+// s_waitcnt vmcnt(n) only (expcnt and lgkmcnt at their maxima: no wait).
+template <int N>
+__device__ __forceinline__ void vmwait() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// LDS fragment reads are issued as inline asm so that the compiler's LDS-DMA alias tracking,
+// which cannot follow the ring and would insert vmcnt waits for in-flight stages, stays out
+// of the main loop; lgkm_wait_all makes the fragments available (the "+v" ties keep every
+// use of a fragment after the wait).
+typedef __attribute__((address_space(3))) f16x8* lds_f16x8;
+template <int OFF>
+__device__ __forceinline__ f16x8 ds_read16(unsigned addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds_read offset field is 16 bits");
+  f16x8 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+template <int FN, int FM>
+__device__ __forceinline__ void lgkm_wait_all(f16x8 (&fa)[FN], f16x8 (&fb)[FM]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < FN; i++) asm volatile("" : "+v"(fa[i]));
+#pragma unroll
+  for (int j = 0; j < FM; j++) asm volatile("" : "+v"(fb[j]));
+}
+template <int N, typename F, int I = 0>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(ic<I>{});
+    static_for<N, F, I + 1>(static_cast<F&&>(f));
+  }
 }
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
-template <int BM, int BN, int WM, int WN, int BK, bool KONE>
+template <int BM, int BN, int WM, int WN, int BK, int NS, bool KONE>
 __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     View x, View y, View r, const f16* __restrict__ w, const float* __restrict__ bias,
-    int ksz, int cs, int cp, int act, int M, int N, int Ktot, int mtiles, int ntiles) {
-  constexpr int NT = 64 * WM * WN;
+    int ksz, int cs, int cp, int act, int M, int N, int Ktot, int mtiles, int ntiles,
+    int xbytes) {
+  constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;  // wave tile: pixels x channels
   constexpr int FM = TM / 16, FN = TN / 16;
   constexpr int CPR = BK / 8;                // 16-byte chunks per LDS row
   constexpr int KS = BK / 32;                // MFMA steps per stage
+  constexpr int QA = BM * CPR / 64, QB = BN * CPR / 64;  // 64-chunk groups per stage
+  constexpr int IA = QA / NW, IB = QB / NW;  // DMA instructions per thread per stage
+  constexpr int NI = IA + IB;
+  constexpr int SZ = (BM + BN) * CPR;        // chunks per stage: pixel rows, then weight rows
+  constexpr bool PAIR = FN % 2 == 0;
   static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be a multiple of 16");
-  static_assert(NT % CPR == 0, "chunk column must be fixed per thread");
-  constexpr int AL = (BM * CPR + NT - 1) / NT;  // 16-byte A chunks per thread per stage
-  constexpr int BL = (BN * CPR + NT - 1) / NT;
+  static_assert(NW % 4 == 0, "the per-thread chunk column is shared only for 4k waves");
+  static_assert(QA % NW == 0 && QB % NW == 0, "every wave issues the same DMA count");
+  static_assert(NS >= 2 && NS <= 4 && (NS - 2) * NI < 64, "ring depth");
 
-  __shared__ f16x8 sA[2][BM * CPR];
-  __shared__ f16x8 sB[2][BN * CPR];
+  __shared__ f16x8 S0[SZ];
+  __shared__ f16x8 S1[SZ];
+  __shared__ f16x8 S2[NS > 2 ? SZ : 1];
+  __shared__ f16x8 S3[NS > 3 ? SZ : 1];
 
   // ---- block id -> (m tile, n tile): per-XCD contiguous ranges, N fastest
   const int nblk = mtiles * ntiles;
@@ -73,80 +141,94 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   const int bm = mt * BM, bn = nt * BN;
 
   const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave % WM, wn = wave / WM;
-  const int c = t % CPR;  // this thread's chunk column
 
-  // ---- per-thread A gather state
-  int arow[AL], rowb[AL], iy0[AL], ix0[AL];
-  bool aval[AL];
+  // ---- DMA assignment: instruction i of this wave fills chunk group q = i*NW + wave, lane
+  // L the slot 64q + L; with NW % 4 == 0 every instruction's row has the same low 4 bits
+  // pattern, so one chunk column c serves all of this thread's loads.
+  const int rsub = lane / CPR;
+  const int c = (lane % CPR) ^ swzf<CPR>(wave * (64 / CPR) + rsub);
+
+  __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(x.p, (short)0, xbytes, 0x00020000);
+  __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(w), (short)0, N * Ktot * 2, 0x00020000);
+
+  int apb[IA], aiy[IA], aix[IA];
+  bool aok[IA];
 #pragma unroll
-  for (int i = 0; i < AL; i++) {
-    int idx = t + i * NT;
-    arow[i] = idx / CPR;
-    int m = bm + arow[i];
-    aval[i] = idx < BM * CPR && m < M;
-    int mm = aval[i] ? m : 0;
+  for (int i = 0; i < IA; i++) {
+    const int row = (i * NW + wave) * (64 / CPR) + rsub;
+    const int m = bm + row;
+    aok[i] = m < M;
+    const int mm = aok[i] ? m : 0;
     if (KONE) {
-      rowb[i] = mm;
-      iy0[i] = ix0[i] = 0;
+      apb[i] = mm * x.s + x.o;
+      aiy[i] = aix[i] = 0;
     } else {
-      int HWo = y.H * y.W;
-      int img = mm / HWo, rem = mm - img * HWo;
-      int oy = rem / y.W, ox = rem - oy * y.W;
-      rowb[i] = img * x.H;
-      iy0[i] = oy * cs - cp;
-      ix0[i] = ox * cs - cp;
+      const int HWo = y.H * y.W;
+      const int img = mm / HWo, rem = mm - img * HWo;
+      const int oy = rem / y.W, ox = rem - oy * y.W;
+      aiy[i] = oy * cs - cp;
+      aix[i] = ox * cs - cp;
+      apb[i] = ((img * x.H + aiy[i]) * x.W + aix[i]) * x.s + x.o;
     }
   }
+  int bw[IB];
+  bool bok[IB];
+#pragma unroll
+  for (int i = 0; i < IB; i++) {
+    const int row = (i * NW + wave) * (64 / CPR) + rsub;
+    const int n = bn + (PAIR ? chperm(row) : row);
+    bok[i] = n < N;
+    bw[i] = bok[i] ? n * Ktot : 0;
+  }
+
+  // k position of this thread's chunk in the next stage to issue
   const int Cin = x.C;
-  int kc = 8 * c;               // flat k of this thread's chunk
-  int ci = kc % Cin, tap = kc / Cin;
-  int ky = tap / ksz, kx = tap - ky * ksz;
+  int kc = 8 * c;
+  int ci = 0, kx = 0, ky = 0, toff = 0;
+  if (!KONE) {
+    ci = kc % Cin;
+    const int tap = kc / Cin;
+    ky = tap / ksz;
+    kx = tap - ky * ksz;
+    toff = (ky * x.W + kx) * x.s + ci;
+  }
 
-  f16x8 ra[AL], rb[BL];
-  const f16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-
-  auto gload = [&](int k0) {
+  auto issue = [&](f16x8* buf) {
+    const bool kin = kc < Ktot;
 #pragma unroll
-    for (int i = 0; i < AL; i++) {
-      ra[i] = zero8;
-      if (aval[i] && kc < Ktot) {
-        if (KONE) {
-          ra[i] = *(const f16x8*)(x.p + (size_t)rowb[i] * x.s + x.o + kc);
-        } else {
-          int iy = iy0[i] + ky, ix = ix0[i] + kx;
-          if (iy >= 0 && iy < x.H && ix >= 0 && ix < x.W)
-            ra[i] = *(const f16x8*)(x.p + ((size_t)(rowb[i] + iy) * x.W + ix) * x.s + x.o + ci);
-        }
+    for (int i = 0; i < IA; i++) {
+      unsigned off;
+      if (KONE) {
+        off = (aok[i] && kin) ? 2u * (unsigned)(apb[i] + kc) : OOB_OFF;
+      } else {
+        const int iy = aiy[i] + ky, ix = aix[i] + kx;
+        const bool ok = aok[i] && kin && (unsigned)iy < (unsigned)x.H && (unsigned)ix < (unsigned)x.W;
+        off = ok ? 2u * (unsigned)(apb[i] + toff) : OOB_OFF;
       }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(buf + (i * NW + wave) * 64), 16, off, 0, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < BL; i++) {
-      int idx = t + i * NT;
-      int n = bn + idx / CPR;
-      int k = k0 + 8 * c;
-      rb[i] = zero8;
-      if (idx < BN * CPR && n < N && k < Ktot) rb[i] = *(const f16x8*)(w + (size_t)n * Ktot + k);
+    for (int i = 0; i < IB; i++) {
+      const unsigned off = (bok[i] && kin) ? 2u * (unsigned)(bw[i] + kc) : OOB_OFF;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(buf + (QA + i * NW + wave) * 64), 16, off, 0, 0, 0);
     }
-    // advance this thread's A chunk by one stage
     kc += BK;
     if (!KONE) {
       ci += BK;
+      toff += BK;
       while (ci >= Cin) {
         ci -= Cin;
-        if (++kx == ksz) { kx = 0; ky++; }
+        toff += x.s - Cin;
+        if (++kx == ksz) {
+          kx = 0;
+          ky++;
+          toff += (x.W - ksz) * x.s;
+        }
       }
-    }
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < AL; i++)
-      if (t + i * NT < BM * CPR) sA[buf][swz<CPR>(arow[i], c)] = ra[i];
-#pragma unroll
-    for (int i = 0; i < BL; i++) {
-      int idx = t + i * NT;
-      if (idx < BN * CPR) sB[buf][swz<CPR>(idx / CPR, c)] = rb[i];
     }
   };
 
@@ -156,78 +238,158 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
 #pragma unroll
     for (int j = 0; j < FM; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nks = (Ktot + BK - 1) / BK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
+  // Fragment reads: lane (lr, lg) of a 16-row fragment reads row base + lr at logical chunk
+  // 4s + lg; the row bases are multiples of 16, so the physical chunk depends on lr only.
   const int lr = lane & 15, lg = lane >> 4;
-  for (int ks = 0; ks < nks; ks++) {
-    const int buf = ks & 1;
-    if (ks + 1 < nks) gload((ks + 1) * BK);
+  unsigned offA[KS], offB[KS];
+#pragma unroll
+  for (int s = 0; s < KS; s++) {
+    const unsigned ch = 16u * (unsigned)(lr * CPR + ((4 * s + lg) ^ swzf<CPR>(lr)));
+    offA[s] = 16u * (unsigned)(wm * TM * CPR) + ch;
+    offB[s] = 16u * (unsigned)((BM + wn * TN) * CPR) + ch;
+  }
+  auto compute = [&](const f16x8* buf) {
+    const unsigned base = (unsigned)(size_t)(lds_f16x8)buf;
 #pragma unroll
     for (int s = 0; s < KS; s++) {
       f16x8 fa[FN], fb[FM];
-#pragma unroll
-      for (int i = 0; i < FN; i++) fa[i] = sB[buf][swz<CPR>(wn * TN + i * 16 + lr, s * 4 + lg)];
-#pragma unroll
-      for (int j = 0; j < FM; j++) fb[j] = sA[buf][swz<CPR>(wm * TM + j * 16 + lr, s * 4 + lg)];
+      const unsigned aA = base + offA[s], aB = base + offB[s];
+      static_for<FN>([&](auto I) { fa[I] = ds_read16<I * 16 * CPR * 16>(aB); });
+      static_for<FM>([&](auto J) { fb[J] = ds_read16<J * 16 * CPR * 16>(aA); });
+      lgkm_wait_all(fa, fb);
 #pragma unroll
       for (int i = 0; i < FN; i++)
 #pragma unroll
         for (int j = 0; j < FM; j++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
-    if (ks + 1 < nks) sstore(buf ^ 1);
-    __syncthreads();
+  };
+
+  auto stage = [&](auto J) -> f16x8* {
+    if constexpr (decltype(J)::value == 0) return S0;
+    else if constexpr (decltype(J)::value == 1) return S1;
+    else if constexpr (decltype(J)::value == 2) return S2;
+    else return S3;
+  };
+
+  const int nks = (Ktot + BK - 1) / BK;
+  // step k: wait for this wave's stage-k loads, barrier (all waves' stage-k chunks are in
+  // LDS and every wave is done reading stage k-1's buffer), refill that buffer with stage
+  // k+NS-1, then the MFMAs of stage k.
+  auto step = [&](auto J, int k) {
+    constexpr int j = decltype(J)::value;
+    const int ahead = min(NS - 2, nks - 1 - k);  // stages after k that may stay in flight
+    if constexpr (NS == 4) {
+      if (ahead >= 2) vmwait<2 * NI>();
+      else if (ahead == 1) vmwait<NI>();
+      else vmwait<0>();
+    } else if constexpr (NS == 3) {
+      if (ahead >= 1) vmwait<NI>();
+      else vmwait<0>();
+    } else {
+      vmwait<0>();
+    }
+    asm volatile("s_barrier" ::: "memory");
+    if (k + NS - 1 < nks) issue(stage(ic<(j + NS - 1) % NS>{}));
+    compute(stage(J));
+  };
+
+  issue(S0);
+  if constexpr (NS > 2) { if (1 < nks) issue(S1); }
+  if constexpr (NS > 3) { if (2 < nks) issue(S2); }
+  for (int k = 0; k < nks; k += NS) {
+    step(ic<0>{}, k);
+    if (k + 1 < nks) step(ic<1>{}, k + 1);
+    if constexpr (NS > 2) { if (k + 2 < nks) step(ic<2>{}, k + 2); }
+    if constexpr (NS > 3) { if (k + 3 < nks) step(ic<3>{}, k + 3); }
   }
 
-  // ---- epilogue: lane holds channels n0..n0+3 of pixel m for every (i, j) fragment
+  // ---- epilogue
+  if constexpr (PAIR) {
+    // fragments (2p, 2p+1): lane holds channels n0 .. n0+7 of pixel m
 #pragma unroll
-  for (int i = 0; i < FN; i++) {
-    const int n0 = bn + wn * TN + i * 16 + 4 * lg;
-    if (n0 >= N) continue;
-    const float b0 = bias[n0], b1 = bias[n0 + 1], b2 = bias[n0 + 2], b3 = bias[n0 + 3];
+    for (int p = 0; p < FN / 2; p++) {
+      const int n0 = bn + wn * TN + 32 * p + 8 * lg;
+      if (n0 >= N) continue;  // N % 8 == 0: all 8 channels valid or none
+      float b[8];
 #pragma unroll
-    for (int j = 0; j < FM; j++) {
-      const int m = bm + wm * TM + j * 16 + lr;
-      if (m >= M) continue;
-      float v0 = acc[i][j][0] + b0, v1 = acc[i][j][1] + b1;
-      float v2 = acc[i][j][2] + b2, v3 = acc[i][j][3] + b3;
-      if (act == 1) { v0 = silu(v0); v1 = silu(v1); v2 = silu(v2); v3 = silu(v3); }
-      if (r.p) {
-        f16x4 rv = *(const f16x4*)(r.p + (size_t)m * r.s + r.o + n0);
-        v0 += (float)rv[0]; v1 += (float)rv[1]; v2 += (float)rv[2]; v3 += (float)rv[3];
+      for (int e = 0; e < 8; e++) b[e] = bias[n0 + e];
+#pragma unroll
+      for (int jj = 0; jj < FM; jj++) {
+        const int m = bm + wm * TM + jj * 16 + lr;
+        if (m >= M) continue;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          v[e] = acc[2 * p][jj][e] + b[e];
+          v[4 + e] = acc[2 * p + 1][jj][e] + b[4 + e];
+        }
+        if (act == 1) {
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] = silu(v[e]);
+        }
+        if (r.p) {
+          const f16x8 rv = *(const f16x8*)(r.p + (size_t)m * r.s + r.o + n0);
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] += (float)rv[e];
+        }
+        f16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = (f16)v[e];
+        *(f16x8*)(y.p + (size_t)m * y.s + y.o + n0) = o;
       }
-      f16x4 o = {(f16)v0, (f16)v1, (f16)v2, (f16)v3};
-      *(f16x4*)(y.p + (size_t)m * y.s + y.o + n0) = o;
+    }
+  } else {
+    // single fragment: lane holds channels n0 .. n0+3 of pixel m
+#pragma unroll
+    for (int i = 0; i < FN; i++) {
+      const int n0 = bn + wn * TN + i * 16 + 4 * lg;
+      if (n0 >= N) continue;
+      const float b0 = bias[n0], b1 = bias[n0 + 1], b2 = bias[n0 + 2], b3 = bias[n0 + 3];
+#pragma unroll
+      for (int jj = 0; jj < FM; jj++) {
+        const int m = bm + wm * TM + jj * 16 + lr;
+        if (m >= M) continue;
+        float v0 = acc[i][jj][0] + b0, v1 = acc[i][jj][1] + b1;
+        float v2 = acc[i][jj][2] + b2, v3 = acc[i][jj][3] + b3;
+        if (act == 1) { v0 = silu(v0); v1 = silu(v1); v2 = silu(v2); v3 = silu(v3); }
+        if (r.p) {
+          const f16x4 rv = *(const f16x4*)(r.p + (size_t)m * r.s + r.o + n0);
+          v0 += (float)rv[0]; v1 += (float)rv[1]; v2 += (float)rv[2]; v3 += (float)rv[3];
+        }
+        const f16x4 o = {(f16)v0, (f16)v1, (f16)v2, (f16)v3};
+        *(f16x4*)(y.p + (size_t)m * y.s + y.o + n0) = o;
+      }
     }
   }
 }
 
 // ------------------------------------------------------------------ tile table
-// {BM pixels, BN channels, waves along M, waves along N, BK}
-#define YOLO_TILES(X)             \
-  X(0, 256, 128, 4, 2, 32)        \
-  X(1, 256, 128, 4, 2, 64)        \
-  X(2, 128, 128, 2, 2, 64)        \
-  X(3, 128, 128, 2, 2, 32)        \
-  X(4, 128, 256, 2, 4, 32)        \
-  X(5, 256, 64, 4, 1, 64)         \
-  X(6, 128, 64, 2, 2, 64)         \
-  X(7, 64, 128, 2, 2, 64)         \
-  X(8, 64, 64, 2, 2, 64)          \
-  X(9, 64, 64, 2, 2, 128)         \
-  X(10, 128, 32, 4, 1, 64)        \
-  X(11, 64, 32, 2, 2, 128)        \
-  X(12, 32, 64, 2, 2, 128)        \
-  X(13, 32, 32, 2, 2, 128)        \
-  X(14, 128, 16, 4, 1, 64)        \
-  X(15, 64, 16, 4, 1, 128)        \
-  X(16, 32, 32, 1, 1, 128)        \
-  X(17, 64, 64, 1, 1, 128)
+// {BM pixels, BN channels, waves along M, waves along N, BK, LDS stages}
+#define YOLO_TILES(X)                 \
+  X(0, 256, 256, 4, 2, 32, 3)         \
+  X(1, 256, 128, 4, 2, 32, 4)         \
+  X(2, 256, 128, 4, 2, 32, 3)         \
+  X(3, 256, 128, 2, 2, 32, 3)         \
+  X(4, 128, 256, 2, 2, 32, 3)         \
+  X(5, 128, 256, 2, 4, 32, 3)         \
+  X(6, 128, 128, 2, 2, 64, 3)         \
+  X(7, 128, 128, 2, 2, 32, 4)         \
+  X(8, 256, 64, 4, 2, 64, 3)          \
+  X(9, 256, 64, 4, 1, 32, 4)          \
+  X(10, 128, 64, 2, 2, 64, 3)         \
+  X(11, 64, 128, 2, 2, 64, 3)         \
+  X(12, 64, 64, 2, 2, 64, 3)          \
+  X(13, 64, 64, 2, 2, 128, 3)         \
+  X(14, 128, 32, 4, 1, 64, 3)         \
+  X(15, 64, 32, 2, 2, 128, 3)         \
+  X(16, 32, 64, 2, 2, 128, 3)         \
+  X(17, 32, 32, 2, 2, 128, 3)         \
+  X(18, 128, 16, 4, 1, 128, 2)        \
+  X(19, 64, 16, 4, 1, 128, 3)
 
 static const TileCfg kTiles[] = {
-#define X(i, bm, bn, wm, wn, bk) {bm, bn, wm, wn, bk},
+#define X(i, bm, bn, wm, wn, bk, ns) {bm, bn, wm, wn, bk, ns},
     YOLO_TILES(X)
 #undef X
 };
@@ -246,43 +408,51 @@ bool tileOk(int cfg, int M, int N, int K) {
   return true;
 }
 
-// Default before autotuning: the largest tile whose grid still covers the chip about
-// twice (256 CUs) with little N padding, else the one with the most blocks.
+// Default before autotuning: the first tile in preference order whose grid covers the
+// chip at least twice (256 CUs) with at most 25% N padding, else the one with the most
+// blocks.
 int heuristicTile(int M, int N, int K) {
-  static const int pref[] = {1, 0, 4, 2, 3, 5, 6, 7, 8, 10, 9, 11, 12, 14, 13, 15, 17, 16};
+  static const int pref[] = {2, 1, 0, 5, 7, 3, 4, 6, 9, 8, 10, 11, 12, 14, 13, 15, 16, 17, 19, 18};
   int best = -1;
   long bestBlocks = -1;
   for (int cfg : pref) {
     if (!tileOk(cfg, M, N, K)) continue;
     const TileCfg& tc = kTiles[cfg];
     long blocks = (long)((M + tc.BM - 1) / tc.BM) * ((N + tc.BN - 1) / tc.BN);
-    long waste = (long)((N + tc.BN - 1) / tc.BN) * tc.BN;
-    if (blocks >= 512 && waste * 4 <= (long)N * 5) return cfg;
+    long padded = (long)((N + tc.BN - 1) / tc.BN) * tc.BN;
+    if (blocks >= 512 && padded * 4 <= (long)N * 5) return cfg;
     if (blocks > bestBlocks) { bestBlocks = blocks; best = cfg; }
   }
-  return best < 0 ? 13 : best;
+  return best < 0 ? 17 : best;
 }
 
-template <int BM, int BN, int WM, int WN, int BK>
+template <int BM, int BN, int WM, int WN, int BK, int NS>
 static void launchTile(bool kone, const View& x, const View& y, const View& r, const f16* w,
                        const float* bias, int k, int s, int p, int act, int M, int N, int Ktot,
-                       hipStream_t st) {
+                       int xbytes, hipStream_t st) {
   const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
   if (kone)
-    k_conv_gemm<BM, BN, WM, WN, BK, true><<<mt * nt, 64 * WM * WN, 0, st>>>(x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt);
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, true><<<mt * nt, 64 * WM * WN, 0, st>>>(
+        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes);
   else
-    k_conv_gemm<BM, BN, WM, WN, BK, false><<<mt * nt, 64 * WM * WN, 0, st>>>(x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt);
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, false><<<mt * nt, 64 * WM * WN, 0, st>>>(
+        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes);
 }
+
+// Byte offsets into the input and weight tensors are 32-bit buffer offsets; the loader
+// rejects graphs whose conv inputs or weights reach 2 GiB (convGemmFits).
+bool convGemmFits(long inBytes, long wBytes) { return inBytes < (1L << 31) && wBytes < (1L << 31); }
 
 void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
                     const float* bias, int k, int s, int p, int act, int Bn, hipStream_t st) {
   const int M = Bn * y.H * y.W, N = y.C, Ktot = k * k * x.C;
   const bool kone = (k == 1 && s == 1 && p == 0);
+  const int xbytes = (int)((long)Bn * x.H * x.W * x.s * 2);
   View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
   if (cfg < 0 || cfg >= kNumTiles) cfg = heuristicTile(M, N, Ktot);
   switch (cfg) {
-#define X(i, bm, bn, wm, wn, bk) \
-    case i: launchTile<bm, bn, wm, wn, bk>(kone, x, y, r, w, bias, k, s, p, act, M, N, Ktot, st); break;
+#define X(i, bm, bn, wm, wn, bk, ns) \
+    case i: launchTile<bm, bn, wm, wn, bk, ns>(kone, x, y, r, w, bias, k, s, p, act, M, N, Ktot, xbytes, st); break;
     YOLO_TILES(X)
 #undef X
     default: break;

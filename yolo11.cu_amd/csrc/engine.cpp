@@ -236,6 +236,11 @@ struct Engine {
             r.coff % 8 || g.bufs[r.buf].C % 8)
           throw Failure(fmt("op %zu: residual view does not match the output", i));
       }
+      if (op.kind == CONV && op.g == 1 && op.Cin != 3) {
+        const BufDesc& xb = g.bufs[g.tens[op.a].buf];
+        if (!convGemmFits((long)B * xb.H * xb.W * xb.C * 2, (long)op.Cout * op.k * op.k * op.Cin * 2))
+          throw Failure(fmt("op %zu: conv input or weights reach 2 GiB at batch %d", i, B));
+      }
       if (op.kind == DECODE || op.kind == DECODESEG) lastDecode = (int)i;
     }
     // weights: read, check ranges, repack depthwise [C][k*k] -> [k*k][C]
@@ -808,6 +813,7 @@ int yolo_tile_config(int cfg, int* out) {
   out[2] = t.WM;
   out[3] = t.WN;
   out[4] = t.BK;
+  out[5] = t.NS;
   return 0;
 }
 

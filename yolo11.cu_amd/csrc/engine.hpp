@@ -81,7 +81,7 @@ struct DecodeArgs {
 };
 
 // ------------------------------------------------------------------ GEMM tile configs
-struct TileCfg { int BM, BN, WM, WN, BK; };
+struct TileCfg { int BM, BN, WM, WN, BK, NS; };
 int numTileConfigs();
 const TileCfg& tileConfig(int cfg);
 
@@ -95,6 +95,7 @@ void launchDwConv(const View& x, const View& y, const View* res, const f16* wt_k
                   const float* bias, int k, int s, int p, int act, int Bn, hipStream_t st);
 int heuristicTile(int M, int N, int K);
 bool tileOk(int cfg, int M, int N, int K);
+bool convGemmFits(long inBytes, long wBytes);
 // elementwise.hip
 void launchAdd(const View& a, const View& b, const View& y, int Bn, hipStream_t st);
 void launchMaxPool5(const View& x, const View& y, int Bn, hipStream_t st);

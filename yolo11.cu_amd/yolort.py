@@ -104,11 +104,12 @@ def load():
     return _lib
 
 
-def tile_configs() -> list[tuple[int, int, int, int, int]]:
+def tile_configs() -> list[tuple[int, int, int, int, int, int]]:
+    """(BM, BN, WM, WN, BK, stages) of every compiled GEMM tile configuration."""
     lib = load()
     out = []
     for i in range(lib.yolo_num_tile_configs()):
-        v = (C.c_int * 5)()
+        v = (C.c_int * 6)()
         lib.yolo_tile_config(i, v)
         out.append(tuple(v))
     return out
