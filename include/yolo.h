@@ -133,7 +133,9 @@ int yolo_frame_launch(void* h);    /* launch only    */
  * engine/engine.cu:2033-2090). */
 /* Average ms of `iters` launches of the batch-B graph (which = 0) or frame graph (1). */
 float yolo_time_graph(void* h, int which, int B, int iters);
-/* Per-op average ms over `iters` stream-ordered passes (ms[k] for every op k). */
+/* Per-op average ms over `iters` stream-ordered passes (ms[k] for every op k).  An op executed
+ * inside a preceding op's launch (the second and third MAXPOOL5 of a fused SPPF chain)
+ * reports only its event overhead. */
 int yolo_profile_ops(void* h, int B, int iters, float* ms);
 
 /* Allocation helpers (device / pinned host) and copies on the engine stream. */

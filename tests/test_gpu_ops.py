@@ -182,3 +182,29 @@ def test_attention_op(tmp_path, H, W, heads):
     print(f"attention {H}x{W} heads={heads}: rel {rel:.2e}", flush=True)
     assert rel <= TOL
     eng.close()
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_sppf_pool_chain(models, B):
+    """The fused SPPF pool chain (one launch for three MAXPOOL5) is bit-exact against the
+    oracle's mp5, mp5(mp5), mp5(mp5(mp5)) on random activations, and the standalone
+    MAXPOOL5 of a chain follower (what the per-op harness runs) is exact too."""
+    d = models("yolo11", "n", "detect")
+    eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    kinds = [eng.op_info(k) for k in range(eng.num_ops)]
+    head = next(k for k in range(len(kinds) - 2)
+                if all(kinds[k + i]["kind"] == "MAXPOOL5" for i in range(3)))
+    x = (np.random.default_rng(B).standard_normal((B,) + eng.tensor_shape(kinds[head]["a"]),
+                                                  dtype=np.float32) * 3).astype(np.float16)
+    eng.write(kinds[head]["a"], x)
+    eng.run_op(head, B)
+    want = x.astype(np.float32)
+    for i in range(3):
+        want = interp.maxpool5(want)
+        got = eng.read(kinds[head + i]["out"], B).astype(np.float32)
+        assert np.array_equal(got, want), (i, np.abs(got - want).max())
+    # follower alone: mp5 of the chain head's output
+    eng.run_op(head + 1, B)
+    got = eng.read(kinds[head + 1]["out"], B).astype(np.float32)
+    assert np.array_equal(got, interp.maxpool5(eng.read(kinds[head]["out"], B).astype(np.float32)))
+    eng.close()

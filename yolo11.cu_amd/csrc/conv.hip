@@ -25,10 +25,12 @@
 //    only for its own loads of stage k (s_waitcnt vmcnt with the count of loads issued
 //    after it), and the barrier makes every wave's stage-k chunks visible.
 //  * LDS rows hold BK halves as 16-byte chunks; chunk c of row r is stored at c ^ f(r),
-//    with f chosen so that the 16-byte operand reads of 16 consecutive rows at one logical
-//    chunk land in distinct 16-byte slots modulo 256 bytes (and 8 aligned rows modulo 128
-//    bytes).  Since the DMA fixes the slot per lane, the swizzle is realised by the choice
-//    of which global chunk each lane fetches.
+//    with f chosen so that a half-wave's 16-byte operand reads (16 consecutive rows at two
+//    adjacent logical chunks) cover every 16-byte slot of a 256-byte bank window exactly
+//    twice: zero SQ_LDS_BANK_CONFLICT on gfx950.  Since the DMA fixes the slot per lane,
+//    the swizzle is realised by the choice of which global chunk each lane fetches.
+//  * 3x3 convs walk K channel-block-major (all taps of BK channels, then the next BK), so
+//    a block's live input window stays small enough for the 9 tap re-reads to hit L2.
 //  * Weight rows of each 32-channel group are loaded in the order 8*(j/4) + 4*h + j%4
 //    (fragment h, row j), so after the MFMAs a lane holds 8 consecutive output channels
 //    across a fragment pair: 16-byte bias/residual loads and 16-byte NHWC stores, 64
@@ -59,8 +61,8 @@ using ic = std::integral_constant<int, N>;
 // rows differ by multiples of 16, so both sides can evaluate it on (row & 15).
 template <int CPR>
 __device__ __forceinline__ int swzf(int row) {
-  if constexpr (CPR == 4) return ((row >> 1) ^ ((row >> 3) & 1)) & 3;
-  else if constexpr (CPR == 8) return (row ^ ((row >> 3) & 1)) & 7;
+  if constexpr (CPR == 4) return (row >> 1) & 3;
+  else if constexpr (CPR == 8) return row & 7;
   else return row & 15;
 }
 template <int CPR>
@@ -80,8 +82,8 @@ __device__ __forceinline__ void vmwait() {
 
 // LDS fragment reads are issued as inline asm so that the compiler's LDS-DMA alias tracking,
 // which cannot follow the ring and would insert vmcnt waits for in-flight stages, stays out
-// of the main loop; lgkm_wait_all makes the fragments available (the "+v" ties keep every
-// use of a fragment after the wait).
+// of the main loop; after lgkm_wait<N>() all but the last N reads have landed, and an empty
+// asm with a "+v" tie on a fragment keeps every use of it after that wait.
 typedef __attribute__((address_space(3))) f16x8* lds_f16x8;
 template <int OFF>
 __device__ __forceinline__ f16x8 ds_read16(unsigned addr) {
@@ -90,13 +92,10 @@ __device__ __forceinline__ f16x8 ds_read16(unsigned addr) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
   return v;
 }
-template <int FN, int FM>
-__device__ __forceinline__ void lgkm_wait_all(f16x8 (&fa)[FN], f16x8 (&fb)[FM]) {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-  for (int i = 0; i < FN; i++) asm volatile("" : "+v"(fa[i]));
-#pragma unroll
-  for (int j = 0; j < FM; j++) asm volatile("" : "+v"(fb[j]));
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
 }
 template <int N, typename F, int I = 0>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -185,25 +184,41 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     bw[i] = bok[i] ? n * Ktot : 0;
   }
 
-  // k position of this thread's chunk in the next stage to issue
+  // K order.  Tap-major (the weights' memory order, k = (ky*ksz + kx)*Cin + ci) for 1x1
+  // convs and when Cin is not a multiple of BK; otherwise channel-block-major: stage
+  // (cb, tap) covers channels [cb*BK, cb*BK + BK) of tap `tap`, all taps of one channel
+  // block before the next.  The reduction is order-free; channel-block-major keeps a block's
+  // live input window at BK channels (about 20 KB for a 128-pixel tile at BK = 32) instead
+  // of all Cin channels, so the 9 taps re-read it from L2 rather than HBM.
+  // State of this thread's chunk for the next stage to issue: kw = flat k in the weight row,
+  // (ky, kx, ci) its tap and channel, toff = its element offset from the pixel's (0, 0) tap.
   const int Cin = x.C;
-  int kc = 8 * c;
+  const bool cbmajor = !KONE && ksz > 1 && Cin % BK == 0;
+  int kw = 8 * c;
   int ci = 0, kx = 0, ky = 0, toff = 0;
   if (!KONE) {
-    ci = kc % Cin;
-    const int tap = kc / Cin;
-    ky = tap / ksz;
-    kx = tap - ky * ksz;
+    if (cbmajor) {
+      ci = kw;
+    } else {
+      ci = kw % Cin;
+      const int tap = kw / Cin;
+      ky = tap / ksz;
+      kx = tap - ky * ksz;
+    }
+    kw = (ky * ksz + kx) * Cin + ci;
     toff = (ky * x.W + kx) * x.s + ci;
   }
+  const int rowstep = (x.W - ksz) * x.s;              // last tap of a row -> first of the next
+  const int cbstep = BK - ksz * x.W * x.s;            // last tap -> (0, 0) of the next channel block
+  const int kwstep = BK - ksz * ksz * Cin;
 
   auto issue = [&](f16x8* buf) {
-    const bool kin = kc < Ktot;
+    const bool kin = kw < Ktot;
 #pragma unroll
     for (int i = 0; i < IA; i++) {
       unsigned off;
       if (KONE) {
-        off = (aok[i] && kin) ? 2u * (unsigned)(apb[i] + kc) : OOB_OFF;
+        off = (aok[i] && kin) ? 2u * (unsigned)(apb[i] + kw) : OOB_OFF;
       } else {
         const int iy = aiy[i] + ky, ix = aix[i] + kx;
         const bool ok = aok[i] && kin && (unsigned)iy < (unsigned)x.H && (unsigned)ix < (unsigned)x.W;
@@ -213,11 +228,26 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     }
 #pragma unroll
     for (int i = 0; i < IB; i++) {
-      const unsigned off = (bok[i] && kin) ? 2u * (unsigned)(bw[i] + kc) : OOB_OFF;
+      const unsigned off = (bok[i] && kin) ? 2u * (unsigned)(bw[i] + kw) : OOB_OFF;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(buf + (QA + i * NW + wave) * 64), 16, off, 0, 0, 0);
     }
-    kc += BK;
-    if (!KONE) {
+    if (KONE) {
+      kw += BK;
+    } else if (cbmajor) {
+      kw += Cin;
+      toff += x.s;
+      if (++kx == ksz) {
+        kx = 0;
+        toff += rowstep;
+        if (++ky == ksz) {
+          ky = 0;
+          ci += BK;
+          toff += cbstep;
+          kw += kwstep;
+        }
+      }
+    } else {
+      kw += BK;
       ci += BK;
       toff += BK;
       while (ci >= Cin) {
@@ -226,7 +256,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
         if (++kx == ksz) {
           kx = 0;
           ky++;
-          toff += (x.W - ksz) * x.s;
+          toff += rowstep;
         }
       }
     }
@@ -248,21 +278,26 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     offA[s] = 16u * (unsigned)(wm * TM * CPR) + ch;
     offB[s] = 16u * (unsigned)((BM + wn * TN) * CPR) + ch;
   }
-  auto compute = [&](const f16x8* buf) {
+  auto reads = [&](const f16x8* buf, int s, f16x8 (&fa)[FN], f16x8 (&fb)[FM]) {
     const unsigned base = (unsigned)(size_t)(lds_f16x8)buf;
+    const unsigned aA = base + offA[s], aB = base + offB[s];
+    static_for<FN>([&](auto I) { fa[I] = ds_read16<I * 16 * CPR * 16>(aB); });
+    static_for<FM>([&](auto J) { fb[J] = ds_read16<J * 16 * CPR * 16>(aA); });
+  };
+  // LDS returns in order: column j of MFMAs starts as soon as fb[j] has landed
+  auto mfmas = [&](f16x8 (&fa)[FN], f16x8 (&fb)[FM]) {
+    static_for<FM>([&](auto J) {
+      lgkm_wait<FM - 1 - J>();
+      if constexpr (J == 0) {
 #pragma unroll
-    for (int s = 0; s < KS; s++) {
-      f16x8 fa[FN], fb[FM];
-      const unsigned aA = base + offA[s], aB = base + offB[s];
-      static_for<FN>([&](auto I) { fa[I] = ds_read16<I * 16 * CPR * 16>(aB); });
-      static_for<FM>([&](auto J) { fb[J] = ds_read16<J * 16 * CPR * 16>(aA); });
-      lgkm_wait_all(fa, fb);
+        for (int i = 0; i < FN; i++) asm volatile("" : "+v"(fa[i]));
+      }
+      asm volatile("" : "+v"(fb[J]));
 #pragma unroll
       for (int i = 0; i < FN; i++)
-#pragma unroll
-        for (int j = 0; j < FM; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    }
+        acc[i][J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[J], acc[i][J], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);  // keep this column ahead of the next wait
+    });
   };
 
   auto stage = [&](auto J) -> f16x8* {
@@ -275,7 +310,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   const int nks = (Ktot + BK - 1) / BK;
   // step k: wait for this wave's stage-k loads, barrier (all waves' stage-k chunks are in
   // LDS and every wave is done reading stage k-1's buffer), refill that buffer with stage
-  // k+NS-1, then the MFMAs of stage k.
+  // k+NS-1, then the fragment reads and MFMAs of stage k.
   auto step = [&](auto J, int k) {
     constexpr int j = decltype(J)::value;
     const int ahead = min(NS - 2, nks - 1 - k);  // stages after k that may stay in flight
@@ -290,8 +325,19 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
       vmwait<0>();
     }
     asm volatile("s_barrier" ::: "memory");
+    // first fragment reads go out before the DMA address arithmetic, which then hides
+    // their latency
+    f16x8 fa[FN], fb[FM];
+    reads(stage(J), 0, fa, fb);
+    __builtin_amdgcn_sched_barrier(0);
     if (k + NS - 1 < nks) issue(stage(ic<(j + NS - 1) % NS>{}));
-    compute(stage(J));
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(fa, fb);
+#pragma unroll
+    for (int s = 1; s < KS; s++) {
+      reads(stage(J), s, fa, fb);
+      mfmas(fa, fb);
+    }
   };
 
   issue(S0);
@@ -533,16 +579,35 @@ __global__ __launch_bounds__(256) void k_dwconv(View x, View y, View r, const f1
   float a[8];
 #pragma unroll
   for (int j = 0; j < 8; j++) a[j] = bias[c + j];
-  for (int ky = 0; ky < ksz; ky++) {
-    const int iy = oy * cs - cp + ky;
-    if (iy < 0 || iy >= x.H) continue;
-    for (int kx = 0; kx < ksz; kx++) {
-      const int ix = ox * cs - cp + kx;
-      if (ix < 0 || ix >= x.W) continue;
-      const f16x8 xv = *(const f16x8*)(x.p + ((size_t)(img * x.H + iy) * x.W + ix) * x.s + x.o + c);
-      const f16x8 wv = *(const f16x8*)(w + (size_t)(ky * ksz + kx) * y.C + c);
+  if (ksz == 3) {
+    // the common case: all 9 taps are loaded unconditionally from clamped addresses (so
+    // they are in flight together) and out-of-image taps are zeroed by a select
+    f16x8 xv[9], wv[9];
+    bool ok[9];
 #pragma unroll
-      for (int j = 0; j < 8; j++) a[j] += (float)xv[j] * (float)wv[j];
+    for (int t = 0; t < 9; t++) {
+      const int iy = oy * cs - cp + t / 3, ix = ox * cs - cp + t % 3;
+      ok[t] = iy >= 0 && iy < x.H && ix >= 0 && ix < x.W;
+      const int cy = min(max(iy, 0), x.H - 1), cx = min(max(ix, 0), x.W - 1);
+      xv[t] = *(const f16x8*)(x.p + ((size_t)(img * x.H + cy) * x.W + cx) * x.s + x.o + c);
+      wv[t] = *(const f16x8*)(w + (size_t)t * y.C + c);
+    }
+#pragma unroll
+    for (int t = 0; t < 9; t++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) a[j] += ok[t] ? (float)xv[t][j] * (float)wv[t][j] : 0.f;
+  } else {
+    for (int ky = 0; ky < ksz; ky++) {
+      const int iy = oy * cs - cp + ky;
+      if (iy < 0 || iy >= x.H) continue;
+      for (int kx = 0; kx < ksz; kx++) {
+        const int ix = ox * cs - cp + kx;
+        if (ix < 0 || ix >= x.W) continue;
+        const f16x8 xv = *(const f16x8*)(x.p + ((size_t)(img * x.H + iy) * x.W + ix) * x.s + x.o + c);
+        const f16x8 wv = *(const f16x8*)(w + (size_t)(ky * ksz + kx) * y.C + c);
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[j] += (float)xv[j] * (float)wv[j];
+      }
     }
   }
   f16x8 rv = {0, 0, 0, 0, 0, 0, 0, 0};

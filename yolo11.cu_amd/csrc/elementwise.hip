@@ -1,4 +1,4 @@
-// Bandwidth-bound NHWC view kernels: ADD, MAXPOOL5, UPSAMPLE2, COPYC, PS2.
+// Bandwidth-bound NHWC view kernels: ADD, MAXPOOL5 (and the fused SPPF pool chain),\n// UPSAMPLE2, COPYC, PS2.
 // Each thread moves one 8-channel group (16 bytes) of one pixel; the loader guarantees
 // every view offset, width and row stride is a multiple of 8 halves, so all accesses
 // are aligned 128-bit loads/stores.  Semantics follow the reference ops
@@ -28,27 +28,77 @@ __global__ __launch_bounds__(256) void k_add(View a, View b, View y, int total) 
 }
 
 // 5x5 stride-1 max pool with implicit -inf padding of 2 (F.max_pool2d(x, 5, 1, 2)).
+// Window taps are clamped to the image instead of skipped: a clamped tap lands on a border
+// pixel that is inside the window anyway, so the max is unchanged, and the 25 loads carry
+// no branches and can all be in flight together.
 __global__ __launch_bounds__(256) void k_maxpool5(View x, View y, int total) {
   int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   int cg = y.C >> 3, g = idx % cg, m = idx / cg;
   int HW = y.H * y.W, img = m / HW, rem = m - img * HW;
   int oy = rem / y.W, ox = rem - oy * y.W;
-  f16x8 mx;
+  f16x8 v[25];
 #pragma unroll
-  for (int j = 0; j < 8; j++) mx[j] = (f16)(-65504.0f);
-  for (int dy = -2; dy <= 2; dy++) {
-    int iy = oy + dy;
-    if (iy < 0 || iy >= x.H) continue;
-    for (int dx = -2; dx <= 2; dx++) {
-      int ix = ox + dx;
-      if (ix < 0 || ix >= x.W) continue;
-      f16x8 v = ld8(x, (size_t)(img * x.H + iy) * x.W + ix, g * 8);
+  for (int dy = 0; dy < 5; dy++) {
+    const int iy = min(max(oy + dy - 2, 0), x.H - 1);
 #pragma unroll
-      for (int j = 0; j < 8; j++) mx[j] = v[j] > mx[j] ? v[j] : mx[j];
+    for (int dx = 0; dx < 5; dx++) {
+      const int ix = min(max(ox + dx - 2, 0), x.W - 1);
+      v[dy * 5 + dx] = ld8(x, (size_t)(img * x.H + iy) * x.W + ix, g * 8);
     }
   }
+  f16x8 mx = v[0];
+#pragma unroll
+  for (int t = 1; t < 25; t++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) mx[j] = v[t][j] > mx[j] ? v[t][j] : mx[j];
   st8(y, m, g * 8, mx);
+}
+
+// SPPF pool chain: y1 = mp5(x), y2 = mp5(y1), y3 = mp5(y2) in one launch (the reference
+// runs three MAXPOOL5 ops, export/export.py:475-491).  One block per (image, 8-channel
+// group) keeps the whole H x W plane in LDS; each mp5 is a separable pair of clipped
+// 5-wide max passes (row pass into `t`, column pass back into `a`, which is also stored).
+__device__ __forceinline__ f16x8 max8(f16x8 a, f16x8 b) {
+  f16x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; j++) o[j] = a[j] > b[j] ? a[j] : b[j];
+  return o;
+}
+__global__ __launch_bounds__(256) void k_sppf_pool(View x, View y1, View y2, View y3) {
+  extern __shared__ f16x8 sp[];
+  const int H = x.H, W = x.W, HW = H * W;
+  f16x8* a = sp;
+  f16x8* t = sp + HW;
+  const int g = blockIdx.x, img = blockIdx.y;
+  const size_t pix0 = (size_t)img * HW;
+  for (int p = threadIdx.x; p < HW; p += blockDim.x) a[p] = ld8(x, pix0 + p, g * 8);
+  __syncthreads();
+  for (int it = 0; it < 3; it++) {
+    for (int p = threadIdx.x; p < HW; p += blockDim.x) {
+      const int py = p / W, px = p - py * W;
+      const f16x8* row = a + py * W;
+      f16x8 m = row[px];
+      if (px >= 1) m = max8(m, row[px - 1]);
+      if (px >= 2) m = max8(m, row[px - 2]);
+      if (px + 1 < W) m = max8(m, row[px + 1]);
+      if (px + 2 < W) m = max8(m, row[px + 2]);
+      t[p] = m;
+    }
+    __syncthreads();
+    const View& yo = it == 0 ? y1 : it == 1 ? y2 : y3;
+    for (int p = threadIdx.x; p < HW; p += blockDim.x) {
+      const int py = p / W;
+      f16x8 m = t[p];
+      if (py >= 1) m = max8(m, t[p - W]);
+      if (py >= 2) m = max8(m, t[p - 2 * W]);
+      if (py + 1 < H) m = max8(m, t[p + W]);
+      if (py + 2 < H) m = max8(m, t[p + 2 * W]);
+      a[p] = m;
+      st8(yo, pix0 + p, g * 8, m);
+    }
+    __syncthreads();
+  }
 }
 
 // nearest x2: out(oy, ox) = in(oy/2, ox/2)
@@ -90,6 +140,11 @@ void launchAdd(const View& a, const View& b, const View& y, int Bn, hipStream_t 
 void launchMaxPool5(const View& x, const View& y, int Bn, hipStream_t st) {
   int total = Bn * y.H * y.W * (y.C / 8);
   k_maxpool5<<<grid(total), 256, 0, st>>>(x, y, total);
+}
+size_t sppfPoolLds(int H, int W) { return (size_t)2 * H * W * sizeof(f16x8); }
+void launchSppfPool(const View& x, const View& y1, const View& y2, const View& y3, int Bn,
+                    hipStream_t st) {
+  k_sppf_pool<<<dim3(x.C / 8, Bn), 256, sppfPoolLds(x.H, x.W), st>>>(x, y1, y2, y3);
 }
 void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st) {
   int total = Bn * y.H * y.W * (y.C / 8);

@@ -224,7 +224,24 @@ struct Engine {
     if (!parseGraph(dir, g, err) || !validateGraph(g, err)) throw Failure(err);
     B = maxB;
     ops = g.ops;
-    if (fuse) fuseAdds(ops);
+    if (fuse) {
+      fuseAdds(ops);
+      // SPPF: three chained MAXPOOL5 ops -> one launch (the plane must fit the LDS budget)
+      for (size_t i = 0; i + 2 < ops.size(); i++) {
+        OpDesc &p0 = ops[i], &p1 = ops[i + 1], &p2 = ops[i + 2];
+        if (p0.kind != MAXPOOL5 || p1.kind != MAXPOOL5 || p2.kind != MAXPOOL5) continue;
+        // exporters register a fresh tensor id per use, so match the views themselves
+        auto same = [&](int t0, int t1) {
+          const TenDesc &u = g.tens[t0], &v = g.tens[t1];
+          return u.buf == v.buf && u.coff == v.coff && u.C == v.C;
+        };
+        if (!same(p1.a, p0.out) || !same(p2.a, p1.out) || p0.chain || p1.chain || p2.chain) continue;
+        const BufDesc& xb = g.bufs[g.tens[p0.a].buf];
+        if (sppfPoolLds(xb.H, xb.W) > 64 * 1024) continue;
+        p0.chain = 3;
+        p1.chain = p2.chain = -1;
+      }
+    }
     for (size_t i = 0; i < ops.size(); i++) {
       const OpDesc& op = ops[i];
       if (op.kind == CONV && op.g == 1 && op.Cin == 3 && op.b >= 0)
@@ -349,7 +366,12 @@ struct Engine {
         break;
       }
       case ADD: launchAdd(view(op.a), view(op.b), view(op.out), Bn, s); break;
-      case MAXPOOL5: launchMaxPool5(view(op.a), view(op.out), Bn, s); break;
+      case MAXPOOL5:
+        if (op.chain == 3)
+          launchSppfPool(view(op.a), view(op.out), view(ops[k + 1].out), view(ops[k + 2].out), Bn, s);
+        else
+          launchMaxPool5(view(op.a), view(op.out), Bn, s);
+        break;
       case UPSAMPLE2: launchUpsample2(view(op.a), view(op.out), Bn, s); break;
       case COPYC: launchCopyC(view(op.a), view(op.out), Bn, s); break;
       case PS2: launchPS2(view(op.a), view(op.out), Bn, s); break;
@@ -383,7 +405,8 @@ struct Engine {
   // cause has not been isolated, so captured graphs keep the single-stream order.
   void forward(int Bn, bool branches = true) {
     if (side.empty() || !branches) {
-      for (size_t k = 0; k < ops.size(); k++) runOp((int)k, Bn);
+      for (size_t k = 0; k < ops.size(); k++)
+        if (ops[k].chain >= 0) runOp((int)k, Bn);
     } else {
       auto strm = [&](int s) { return s == 0 ? st : side[s - 1]; };
       HCK(hipEventRecord(forkEv, st));
@@ -391,7 +414,7 @@ struct Engine {
       for (size_t k = 0; k < ops.size(); k++) {
         hipStream_t s = strm(opStream[k]);
         for (int w : opWaits[k]) HCK(hipStreamWaitEvent(s, opEvent[w], 0));
-        runOp((int)k, Bn, s);
+        if (ops[k].chain >= 0) runOp((int)k, Bn, s);
         if (opRecord[k]) HCK(hipEventRecord(opEvent[k], s));
       }
       for (int q = 0; q < NSIDE; q++) {
@@ -892,7 +915,7 @@ int yolo_profile_ops(void* h, int B, int iters, float* ms) {
     for (int it = 0; it < iters; it++) {
       HCK(hipEventRecord(ev[0], e->st));
       for (int k = 0; k < n; k++) {
-        e->runOp(k, B);
+        if (e->ops[k].chain >= 0) e->runOp(k, B);   // chain followers run inside the head
         HCK(hipEventRecord(ev[k + 1], e->st));
       }
       HCK(hipEventSynchronize(ev[n]));

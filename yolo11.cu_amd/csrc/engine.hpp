@@ -25,6 +25,8 @@ struct OpDesc {
   int heads = 0, kd = 0, hd = 0;      // ATTN
   int stride = 0;                     // DECODE*
   int cfg = -1;                       // GEMM tile config (-1 = heuristic)
+  int chain = 0;                      // MAXPOOL5: 3 = head of a fused SPPF chain,
+                                      // -1 = pooled by the chain head in forward()
 };
 
 struct GraphDesc {
@@ -99,6 +101,11 @@ bool convGemmFits(long inBytes, long wBytes);
 // elementwise.hip
 void launchAdd(const View& a, const View& b, const View& y, int Bn, hipStream_t st);
 void launchMaxPool5(const View& x, const View& y, int Bn, hipStream_t st);
+// Three chained MAXPOOL5 (y1 = mp5(x), y2 = mp5(y1), y3 = mp5(y2)) in one launch; the plane
+// is held in LDS (sppfPoolLds bytes), so the loader only fuses planes that fit.
+size_t sppfPoolLds(int H, int W);
+void launchSppfPool(const View& x, const View& y1, const View& y2, const View& y3, int Bn,
+                    hipStream_t st);
 void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st);
 void launchCopyC(const View& x, const View& y, int Bn, hipStream_t st);
 void launchPS2(const View& x, const View& y, int Bn, hipStream_t st);

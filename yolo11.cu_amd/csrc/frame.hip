@@ -76,12 +76,21 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict_
   const f16* cp = L.cls.p + pix * L.cls.s + L.cls.o;
   float best = -INFINITY;
   int bcls = 0;
-  for (int c0 = 0; c0 < L.cls.C; c0 += 8) {
-    const f16x8 v = *(const f16x8*)(cp + c0);
+  // 8 chunks (64 classes) are fetched before any is consumed, so their latencies overlap
+  for (int c0 = 0; c0 < L.cls.C; c0 += 64) {
+    f16x8 v[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const float f = (float)v[j];
-      if (c0 + j < a.nc && f > best) { best = f; bcls = c0 + j; }
+    for (int u = 0; u < 8; u++)
+      if (c0 + 8 * u < L.cls.C) v[u] = *(const f16x8*)(cp + c0 + 8 * u);
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      if (c0 + 8 * u >= L.cls.C) break;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int cl = c0 + 8 * u + j;
+        const float f = (float)v[u][j];
+        if (cl < a.nc && f > best) { best = f; bcls = cl; }
+      }
     }
   }
   const float score = 1.f / (1.f + expf(-best));
@@ -334,28 +343,30 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     if (nout >= maxdet) break;
     const int base = cb * 64;
     const int nb = min(64, m - base);
-    // (a) in-block suppression rows: pairs (i, j), i < j < nb, spread over the block
-    if (tid < 64) rows[tid] = 0ull;
-    __syncthreads();
-    for (int p = tid; p < 64 * 64; p += NMS_THREADS) {
-      const int i = p >> 6, jj = p & 63;
-      if (jj > i && jj < nb && scls[base + i] == scls[base + jj] &&
-          suppresses(sbox[base + i], sbox[base + jj], thr))
-        atomicOr(&rows[i], 1ull << jj);
+    // (a) in-block suppression rows: wave w builds rows w, w+16, ...; lane j of the wave
+    //     tests pair (i, j) and the row is the wave's ballot (no atomics, no clearing)
+    for (int i = wave; i < 64; i += NMS_THREADS / 64) {
+      const bool hit = lane > i && lane < nb && i < nb && scls[base + i] == scls[base + lane] &&
+                       suppresses(sbox[base + i], sbox[base + lane], thr);
+      const unsigned long long row = __ballot(hit);
+      if (lane == 0) rows[i] = row;
     }
     __syncthreads();
-    // (b) wave 0 walks the rows in rank order
+    // (b) wave 0 walks the survivors in rank order: the lowest alive bit is kept and clears
+    //     its row; one iteration per survivor (scalar bit scan + two readlanes)
     if (wave == 0) {
       const unsigned long long row = rows[lane];
       const unsigned long long valid = nb >= 64 ? ~0ull : ((1ull << nb) - 1ull);
-      unsigned long long alive =
-          ~(((unsigned long long)removed[2 * cb + 1] << 32) | removed[2 * cb]) & valid;
-      for (int tt = 0; tt < 64; tt++) {
-        if ((alive >> tt) & 1ull) {
-          const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, tt);
-          const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), tt);
-          alive &= ~(((unsigned long long)hi << 32) | lo);
-        }
+      const unsigned rlo = __builtin_amdgcn_readfirstlane(removed[2 * cb]);
+      const unsigned rhi = __builtin_amdgcn_readfirstlane(removed[2 * cb + 1]);
+      unsigned long long todo = ~(((unsigned long long)rhi << 32) | rlo) & valid;
+      unsigned long long alive = 0ull;
+      while (todo) {
+        const int tt = __builtin_ctzll(todo);
+        alive |= 1ull << tt;
+        const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, tt);
+        const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), tt);
+        todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << tt));
       }
       const bool mine = (alive >> lane) & 1ull;
       const int before = __popcll(alive & ((1ull << lane) - 1ull));
