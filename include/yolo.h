@@ -76,7 +76,10 @@ int yolo_get_mask(void* h, int slot, int det, unsigned char* out);
 #define YOLO_NOTUNE 2      /* skip the startup tile autotuner (the reference's NOTUNE)       */
 #define YOLO_NOGRAPH 4     /* do not capture per-B graphs at create (yolo_run then streams)  */
 #define YOLO_BRANCHES 8    /* eager (non-graph) forward runs independent branches on 3 side
-                              streams; graph capture always uses the single-stream order   */
+                              streams                                                      */
+#define YOLO_DAGGRAPH 16   /* graphs are a dependency DAG of per-op kernel nodes (independent
+                              branches may run concurrently) instead of one single-stream
+                              capture; slower for batch 1 on ROCm 7.2                      */
 
 /* Error-returning create: NULL on failure with a message in err (if non-NULL). */
 void* yolo_create_ex(const char* model_dir, int max_batch, int flags, char* err, int errlen);
@@ -113,7 +116,13 @@ int yolo_run_post(void* h, int B);
 /* Tile configuration the dispatcher uses for a CONV op (autotuned or heuristic), and an
  * override (cfg < 0 restores the heuristic).  Returns -1 for non-GEMM ops. */
 int yolo_op_config(void* h, int k);
-int yolo_set_op_config(void* h, int k, int cfg);
+int yolo_set_op_config(void* h, int k, int cfg);   /* also resets the op's split-K to 1 */
+/* Split-K factor of a GEMM CONV op (autotuned at create, 1 = none) and an override: the K
+ * stages are divided over `splits` blocks per output tile whose fp32 partials are summed in
+ * split order (deterministic).  The override is refused (-1) once graphs are captured
+ * (YOLO_NOGRAPH handles only), for non-GEMM ops and for splits that leave a block empty. */
+int yolo_op_split(void* h, int k);
+int yolo_set_op_split(void* h, int k, int splits);
 /* Number of GEMM tile configurations compiled in, and the shape of one:
  * out[0..5] = BM (pixels), BN (channels), waves along M, waves along N, BK (K per stage),
  * LDS ring stages. */

@@ -27,7 +27,7 @@ def test_tile_table():
         assert BK in (32, 64, 128)
         assert (BM // WM) % 16 == 0 and (BN // WN) % 16 == 0
         assert 64 * WM * WN <= 1024 and (WM * WN) % 4 == 0
-        assert 2 <= NS <= 4
+        assert 2 <= NS <= 8
         # the LDS ring fits the 160 KiB of a CU
         assert NS * (BM + BN) * BK * 2 <= 160 * 1024
         # every wave issues the same number of 64-chunk DMA groups for both operands

@@ -198,3 +198,36 @@ def test_concurrent_branches_equal_serial(models):
     """The multi-stream plan (independent branches on side streams) must give bit-identical
     tensors and detections to the single-stream order, on every graph replay."""
     pytest.skip("disabled")
+
+
+@pytest.mark.parametrize("task", ["detect", "segment"])
+def test_dag_graph_equals_serial_graph(models, task):
+    """Graphs built as a dependency DAG of per-op nodes (independent branches run
+    concurrently) give bit-identical detections and masks to the single-stream graph, over
+    replays; the frame graph too."""
+    d = models("yolo11", "n", task)
+    img = modelgen.synth_frame(810, 1080, 20, 3)
+    res = {}
+    for name, flags in (("dag", yolort.YOLO_NOTUNE | yolort.YOLO_DAGGRAPH), ("serial", yolort.YOLO_NOTUNE)):
+        eng = yolort.Engine(d, 2, flags)
+        bufs = [_letterbox_gpu(eng, img, s) for s in range(2)]
+        outs = []
+        for _ in range(3):
+            eng.run(2)
+            outs.append([eng.get(s) for s in range(2)])
+        if task == "segment":
+            outs.append([eng.get_mask(0, i) for i in range(min(3, len(outs[0][0])))])
+        dev = yolort.DeviceBuffer(img.nbytes)
+        eng.upload(dev, img)
+        eng.frame_graph([dev.ptr], [img.shape[0]], [img.shape[1]])
+        eng.frame_run()
+        outs.append([eng.get(0)])
+        res[name] = outs
+        dev.free()
+        for b in bufs:
+            b.free()
+        eng.close()
+    for a, b in zip(res["dag"], res["serial"]):
+        for x, y in zip(a, b):
+            np.testing.assert_array_equal(x, y)
+    assert len(res["dag"][0][0]) > 0

@@ -208,3 +208,48 @@ def test_sppf_pool_chain(models, B):
     got = eng.read(kinds[head + 1]["out"], B).astype(np.float32)
     assert np.array_equal(got, interp.maxpool5(eng.read(kinds[head]["out"], B).astype(np.float32)))
     eng.close()
+
+
+@pytest.mark.parametrize("shape", [(20, 20, 512, 256, 3, 1), (40, 40, 128, 64, 3, 2),
+                                   (20, 20, 1024, 512, 1, 1), (13, 17, 96, 40, 3, 1)])
+def test_conv_split_k(tmp_path, shape):
+    """Split-K: every split count a tile admits gives the oracle's result within the per-op
+    bar, is bit-identical across launches (fixed reduction order, counters re-armed by the
+    kernel) and across the tile's first and second use of the workspace."""
+    H, W, cin, cout, k, s = shape
+    d = str(tmp_path / "splitk")
+    modelgen.write_single_conv(d, H, W, cin, cout, k, s, seed=5)
+    g = graphfile.load(d)
+    B = 1
+    x = np.random.default_rng(7).standard_normal((B, H, W, cin), dtype=np.float32).astype(np.float16)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    eng.write(0, x)
+    ref = interp.Interp(g, B)
+    ref.set_input(x.astype(np.float32))
+    ref.run_op(g.ops[0])
+    want = ref.view(g.ops[0].out)
+    tried = 0
+    for cfg in (13, 16, 17, 12, 7):
+        eng.set_op_config(0, cfg)
+        eng.run_op(0, B)
+        base = eng.read(g.ops[0].out, B)
+        for S in (2, 3, 4, 8, 16):
+            try:
+                eng.set_op_split(0, S)
+            except ValueError:
+                continue            # tile/K combination leaves a split empty
+            assert eng.op_split(0) == S
+            eng.run_op(0, B)
+            got1 = eng.read(g.ops[0].out, B)
+            eng.run_op(0, B)
+            got2 = eng.read(g.ops[0].out, B)
+            assert np.array_equal(got1, got2), (cfg, S)
+            rel = post.rel_err(got1.astype(np.float32), want)
+            print(f"shape {shape} cfg {cfg} S {S}: rel {rel:.2e}", flush=True)
+            assert rel <= TOL, (cfg, S, rel)
+            # against the unsplit launch: only fp32 summation order differs
+            assert post.rel_err(got1.astype(np.float32), base.astype(np.float32)) <= 2e-3
+            tried += 1
+        eng.set_op_config(0, cfg)   # back to split 1 for the next tile
+    assert tried >= 4
+    eng.close()

@@ -19,9 +19,9 @@
 //    returns zeros for offsets past the tensor, so the halo of the 3x3 window, the pixel
 //    tail (m >= M), the channel tail (n >= N) and the K tail are all a single "offset =
 //    OOB" select, with no branches and no zero stores.
-//  * An NS-stage LDS ring (NS = 2..4, one __shared__ array per stage so the compiler's
-//    LDS-DMA alias tracking sees distinct objects): while the MFMAs consume stage k, the
-//    DMA of stages k+1 .. k+NS-1 is in flight.  One s_barrier per stage; each wave waits
+//  * An NS-stage LDS ring (NS = 2..8): while the MFMAs consume stage k, the DMA of stages
+//    k+1 .. k+NS-1 is in flight; small convs use deep rings so most of their K extent is
+//    requested at once.  One s_barrier per stage; each wave waits
 //    only for its own loads of stage k (s_waitcnt vmcnt with the count of loads issued
 //    after it), and the barrier makes every wave's stage-k chunks visible.
 //  * LDS rows hold BK halves as 16-byte chunks; chunk c of row r is stored at c ^ f(r),
@@ -111,8 +111,8 @@ template <int BM, int BN, int WM, int WN, int BK, int NS, bool KONE>
 __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     View x, View y, View r, const f16* __restrict__ w, const float* __restrict__ bias,
     int ksz, int cs, int cp, int act, int M, int N, int Ktot, int mtiles, int ntiles,
-    int xbytes) {
-  constexpr int NW = WM * WN;
+    int xbytes, int splits, int spl, float* __restrict__ ws, int* __restrict__ cnt) {
+  constexpr int NW = WM * WN, NT = 64 * NW;
   constexpr int TM = BM / WM, TN = BN / WN;  // wave tile: pixels x channels
   constexpr int FM = TM / 16, FN = TN / 16;
   constexpr int CPR = BK / 8;                // 16-byte chunks per LDS row
@@ -125,16 +125,15 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be a multiple of 16");
   static_assert(NW % 4 == 0, "the per-thread chunk column is shared only for 4k waves");
   static_assert(QA % NW == 0 && QB % NW == 0, "every wave issues the same DMA count");
-  static_assert(NS >= 2 && NS <= 4 && (NS - 2) * NI < 64, "ring depth");
+  static_assert(NS >= 2 && NS <= 8 && (NS - 2) * NI < 64, "ring depth");
 
-  __shared__ f16x8 S0[SZ];
-  __shared__ f16x8 S1[SZ];
-  __shared__ f16x8 S2[NS > 2 ? SZ : 1];
-  __shared__ f16x8 S3[NS > 3 ? SZ : 1];
+  __shared__ f16x8 ring[NS * SZ];   // NS stages of SZ chunks
 
   // ---- block id -> (m tile, n tile): per-XCD contiguous ranges, N fastest
+  // split-K: blocks [s*nblk, (s+1)*nblk) take K stages [s*spl, s*spl + spl)
   const int nblk = mtiles * ntiles;
-  int id = blockIdx.x;
+  const int split = blockIdx.x / nblk;
+  int id = blockIdx.x - split * nblk;
   if (nblk >= 2 * NUM_XCD && nblk % NUM_XCD == 0) id = (id % NUM_XCD) * (nblk / NUM_XCD) + id / NUM_XCD;
   const int mt = id / ntiles, nt = id - mt * ntiles;
   const int bm = mt * BM, bn = nt * BN;
@@ -194,17 +193,21 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   // (ky, kx, ci) its tap and channel, toff = its element offset from the pixel's (0, 0) tap.
   const int Cin = x.C;
   const bool cbmajor = !KONE && ksz > 1 && Cin % BK == 0;
-  int kw = 8 * c;
+  const int st0 = split * spl;   // first K stage of this block
+  int kw = st0 * BK + 8 * c;
   int ci = 0, kx = 0, ky = 0, toff = 0;
   if (!KONE) {
+    int tap;
     if (cbmajor) {
-      ci = kw;
+      const int taps = ksz * ksz, cb = st0 / taps;
+      tap = st0 - cb * taps;
+      ci = cb * BK + 8 * c;
     } else {
       ci = kw % Cin;
-      const int tap = kw / Cin;
-      ky = tap / ksz;
-      kx = tap - ky * ksz;
+      tap = kw / Cin;
     }
+    ky = tap / ksz;
+    kx = tap - ky * ksz;
     kw = (ky * ksz + kx) * Cin + ci;
     toff = (ky * x.W + kx) * x.s + ci;
   }
@@ -300,54 +303,75 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     });
   };
 
-  auto stage = [&](auto J) -> f16x8* {
-    if constexpr (decltype(J)::value == 0) return S0;
-    else if constexpr (decltype(J)::value == 1) return S1;
-    else if constexpr (decltype(J)::value == 2) return S2;
-    else return S3;
-  };
-
-  const int nks = (Ktot + BK - 1) / BK;
+  const int nks = min((Ktot + BK - 1) / BK - st0, spl);   // this block's stages (>= 1)
   // step k: wait for this wave's stage-k loads, barrier (all waves' stage-k chunks are in
   // LDS and every wave is done reading stage k-1's buffer), refill that buffer with stage
   // k+NS-1, then the fragment reads and MFMAs of stage k.
-  auto step = [&](auto J, int k) {
-    constexpr int j = decltype(J)::value;
-    const int ahead = min(NS - 2, nks - 1 - k);  // stages after k that may stay in flight
-    if constexpr (NS == 4) {
-      if (ahead >= 2) vmwait<2 * NI>();
-      else if (ahead == 1) vmwait<NI>();
-      else vmwait<0>();
-    } else if constexpr (NS == 3) {
-      if (ahead >= 1) vmwait<NI>();
-      else vmwait<0>();
-    } else {
-      vmwait<0>();
-    }
+  auto waitStage = [&](int ahead) {   // stages issued after k that may stay in flight
+    static_for<NS - 1>([&](auto A) {
+      if (ahead == A) vmwait<A * NI>();
+    });
+  };
+  for (int k = 0; k < min(NS - 1, nks); k++) issue(ring + k * SZ);
+  int cur = 0;   // ring slot of stage k
+  for (int k = 0; k < nks; k++) {
+    waitStage(min(NS - 2, nks - 1 - k));
     asm volatile("s_barrier" ::: "memory");
+    const f16x8* buf = ring + cur * SZ;
     // first fragment reads go out before the DMA address arithmetic, which then hides
     // their latency
     f16x8 fa[FN], fb[FM];
-    reads(stage(J), 0, fa, fb);
+    reads(buf, 0, fa, fb);
     __builtin_amdgcn_sched_barrier(0);
-    if (k + NS - 1 < nks) issue(stage(ic<(j + NS - 1) % NS>{}));
+    if (k + NS - 1 < nks) issue(ring + (cur == 0 ? NS - 1 : cur - 1) * SZ);
     __builtin_amdgcn_sched_barrier(0);
     mfmas(fa, fb);
 #pragma unroll
     for (int s = 1; s < KS; s++) {
-      reads(stage(J), s, fa, fb);
+      reads(buf, s, fa, fb);
       mfmas(fa, fb);
     }
-  };
+    cur = cur + 1 == NS ? 0 : cur + 1;
+  }
 
-  issue(S0);
-  if constexpr (NS > 2) { if (1 < nks) issue(S1); }
-  if constexpr (NS > 3) { if (2 < nks) issue(S2); }
-  for (int k = 0; k < nks; k += NS) {
-    step(ic<0>{}, k);
-    if (k + 1 < nks) step(ic<1>{}, k + 1);
-    if constexpr (NS > 2) { if (k + 2 < nks) step(ic<2>{}, k + 2); }
-    if constexpr (NS > 3) { if (k + 3 < nks) step(ic<3>{}, k + 3); }
+  // ---- split-K reduction: every split stores its fp32 partial tile (thread-private
+  // layout, 16-byte stores), then the last block to arrive for the tile (device-scope
+  // counter) sums all partials in split order -- deterministic whatever the arrival order --
+  // resets the counter for the next launch and runs the epilogue.
+  if (splits > 1) {
+    __shared__ int lastBlock;
+    const int tile = mt * ntiles + nt;
+    constexpr int TILE = BM * BN;
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+        *(f32x4*)(ws + ((size_t)split * nblk + tile) * TILE + ((i * FM + j) * NT + t) * 4) = acc[i][j];
+    __threadfence();
+    __syncthreads();
+    if (t == 0) lastBlock = atomicAdd(&cnt[tile], 1) == splits - 1;
+    __syncthreads();
+    if (!lastBlock) return;
+    __threadfence();
+    f32x4 sum[FN][FM];
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++) sum[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < splits; sp++) {
+#pragma unroll
+      for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int j = 0; j < FM; j++)
+          sum[i][j] += sp == split ? acc[i][j]
+                                   : *(const f32x4*)(ws + ((size_t)sp * nblk + tile) * TILE +
+                                                     ((i * FM + j) * NT + t) * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++) acc[i][j] = sum[i][j];
+    if (t == 0) cnt[tile] = 0;
   }
 
   // ---- epilogue
@@ -432,7 +456,17 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   X(16, 32, 64, 2, 2, 128, 3)         \
   X(17, 32, 32, 2, 2, 128, 3)         \
   X(18, 128, 16, 4, 1, 128, 2)        \
-  X(19, 64, 16, 4, 1, 128, 3)
+  X(19, 64, 16, 4, 1, 128, 3)         \
+  X(20, 256, 256, 2, 4, 64, 2)        \
+  X(21, 256, 256, 2, 4, 32, 3)        \
+  X(22, 256, 128, 2, 4, 64, 2)        \
+  X(23, 128, 256, 2, 4, 64, 2)        \
+  X(24, 32, 32, 2, 2, 64, 8)          \
+  X(25, 32, 64, 2, 2, 64, 8)          \
+  X(26, 64, 32, 2, 2, 64, 8)          \
+  X(27, 64, 64, 2, 2, 64, 6)          \
+  X(28, 32, 32, 2, 2, 128, 4)         \
+  X(29, 64, 16, 4, 1, 128, 5)
 
 static const TileCfg kTiles[] = {
 #define X(i, bm, bn, wm, wn, bk, ns) {bm, bn, wm, wn, bk, ns},
@@ -475,30 +509,55 @@ int heuristicTile(int M, int N, int K) {
 template <int BM, int BN, int WM, int WN, int BK, int NS>
 static void launchTile(bool kone, const View& x, const View& y, const View& r, const f16* w,
                        const float* bias, int k, int s, int p, int act, int M, int N, int Ktot,
-                       int xbytes, hipStream_t st) {
+                       int xbytes, int splits, float* ws, int* cnt, hipStream_t st) {
   const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
+  const int spl = splitStages(Ktot, BK, splits);
   if (kone)
-    k_conv_gemm<BM, BN, WM, WN, BK, NS, true><<<mt * nt, 64 * WM * WN, 0, st>>>(
-        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes);
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, true><<<mt * nt * splits, 64 * WM * WN, 0, st>>>(
+        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, splits, spl, ws, cnt);
   else
-    k_conv_gemm<BM, BN, WM, WN, BK, NS, false><<<mt * nt, 64 * WM * WN, 0, st>>>(
-        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes);
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, false><<<mt * nt * splits, 64 * WM * WN, 0, st>>>(
+        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, splits, spl, ws, cnt);
 }
 
 // Byte offsets into the input and weight tensors are 32-bit buffer offsets; the loader
 // rejects graphs whose conv inputs or weights reach 2 GiB (convGemmFits).
 bool convGemmFits(long inBytes, long wBytes) { return inBytes < (1L << 31) && wBytes < (1L << 31); }
 
+int splitStages(int Ktot, int BK, int splits) {
+  const int nks = (Ktot + BK - 1) / BK;
+  return (nks + splits - 1) / splits;
+}
+bool splitOk(int cfg, int Ktot, int splits) {
+  if (splits == 1) return true;
+  if (cfg < 0 || cfg >= kNumTiles || splits < 1 || splits > MAX_SPLITS) return false;
+  const int nks = (Ktot + kTiles[cfg].BK - 1) / kTiles[cfg].BK;
+  const int spl = splitStages(Ktot, kTiles[cfg].BK, splits);
+  return spl >= 1 && (splits - 1) * spl < nks;   // every split gets at least one stage
+}
+size_t splitWorkspaceBytes(int cfg, int M, int N, int splits) {
+  if (splits <= 1 || cfg < 0 || cfg >= kNumTiles) return 0;
+  const TileCfg& tc = kTiles[cfg];
+  const size_t tiles = (size_t)((M + tc.BM - 1) / tc.BM) * ((N + tc.BN - 1) / tc.BN);
+  return tiles * splits * tc.BM * tc.BN * sizeof(float);
+}
+int splitTiles(int cfg, int M, int N) {
+  const TileCfg& tc = kTiles[cfg];
+  return ((M + tc.BM - 1) / tc.BM) * ((N + tc.BN - 1) / tc.BN);
+}
+
 void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
-                    const float* bias, int k, int s, int p, int act, int Bn, hipStream_t st) {
+                    const float* bias, int k, int s, int p, int act, int Bn, int splits,
+                    float* ws, int* cnt, hipStream_t st) {
   const int M = Bn * y.H * y.W, N = y.C, Ktot = k * k * x.C;
   const bool kone = (k == 1 && s == 1 && p == 0);
   const int xbytes = (int)((long)Bn * x.H * x.W * x.s * 2);
   View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
   if (cfg < 0 || cfg >= kNumTiles) cfg = heuristicTile(M, N, Ktot);
+  if (splits < 1 || !ws || !cnt || !splitOk(cfg, Ktot, splits)) splits = 1;
   switch (cfg) {
 #define X(i, bm, bn, wm, wn, bk, ns) \
-    case i: launchTile<bm, bn, wm, wn, bk, ns>(kone, x, y, r, w, bias, k, s, p, act, M, N, Ktot, xbytes, st); break;
+    case i: launchTile<bm, bn, wm, wn, bk, ns>(kone, x, y, r, w, bias, k, s, p, act, M, N, Ktot, xbytes, splits, ws, cnt, st); break;
     YOLO_TILES(X)
 #undef X
     default: break;

@@ -65,16 +65,25 @@ struct Engine {
   float* bias = nullptr;
   size_t nweights = 0, nbias = 0;
   float* cand = nullptr;
-  float* keys = nullptr;
+  int* nmsCount = nullptr;            // per-image decode list length (NMS re-arms it)
   unsigned long long* nmsScratch = nullptr;
+  // results: [outcnt B][rawcnt B] then (256-aligned) outdets B*MAX_OUT*6 in one block, so
+  // one copy brings everything the host reads back
+  void* results = nullptr;
+  size_t detOff = 0;
   float* outdets = nullptr;
   int* outidx = nullptr;
   int* outcnt = nullptr;
   int* rawcnt = nullptr;
   uint8_t* masks = nullptr;
   PostParams* params = nullptr;
+  // split-K partial tiles and tile counters: per-op regions (wsOff / cntOff) after tuning
+  float* splitWs = nullptr;
+  int* splitCnt = nullptr;
+  size_t splitWsBytes = 0, splitCntN = 0;
   PostParams hparams{0.25f, 0.45f, MAX_OUT, 0};
-  // pinned mirrors (filled inside the graph)
+  // pinned mirror of `results` (filled inside the graph)
+  void* h_results = nullptr;
   float* h_out = nullptr;
   int* h_cnt = nullptr;
   int* h_rawcnt = nullptr;
@@ -113,16 +122,17 @@ struct Engine {
     graphs.clear();
     if (frameGraph) (void)hipGraphExecDestroy(frameGraph);
     frameGraph = nullptr;
-    void* dptrs[] = {arena, weights, bias, cand, keys, nmsScratch, outdets, outidx, outcnt, rawcnt, masks, params};
+    void* dptrs[] = {arena, weights, bias, cand, nmsCount, nmsScratch, results, outidx, masks, params,
+                     splitWs, splitCnt};
     for (void* p : dptrs)
       if (p) (void)hipFree(p);
-    arena = nullptr; weights = nullptr; bias = nullptr; cand = nullptr; keys = nullptr;
-    nmsScratch = nullptr; outdets = nullptr; outidx = nullptr; outcnt = nullptr; rawcnt = nullptr;
-    masks = nullptr; params = nullptr;
-    void* hptrs[] = {h_out, h_cnt, h_rawcnt};
-    for (void* p : hptrs)
-      if (p) (void)hipHostFree(p);
-    h_out = nullptr; h_cnt = nullptr; h_rawcnt = nullptr;
+    arena = nullptr; weights = nullptr; bias = nullptr; cand = nullptr; nmsCount = nullptr;
+    nmsScratch = nullptr; results = nullptr; outdets = nullptr; outidx = nullptr; outcnt = nullptr;
+    rawcnt = nullptr;
+    masks = nullptr; params = nullptr; splitWs = nullptr; splitCnt = nullptr;
+    splitWsBytes = splitCntN = 0;
+    if (h_results) (void)hipHostFree(h_results);
+    h_results = nullptr; h_out = nullptr; h_cnt = nullptr; h_rawcnt = nullptr;
     for (hipEvent_t e : opEvent)
       if (e) (void)hipEventDestroy(e);
     opEvent.clear();
@@ -145,10 +155,14 @@ struct Engine {
   // independent op on the stream that went idle earliest, waiting only for the latest
   // dependency on each other stream.  Decode (one launch for all levels) depends on every
   // head tensor, and post-processing joins all streams.
-  void planStreams() {
-    struct Acc { int buf, c0, c1; bool w; };
+  // Buffer-region access sets of every op (what it reads and writes), the basis of both
+  // the eager multi-stream plan and the graph DAG.  A fused pool chain's head carries the
+  // accesses of its followers.
+  struct Acc { int buf, c0, c1; bool w; };
+  std::vector<std::vector<Acc>> acc;
+  void computeAccesses() {
     const int n = (int)ops.size();
-    std::vector<std::vector<Acc>> acc(n);
+    acc.assign(n, {});
     auto add = [&](int k, int t, bool w) {
       if (t < 0) return;
       const TenDesc& T = g.tens[t];
@@ -156,9 +170,10 @@ struct Engine {
     };
     for (int k = 0; k < n; k++) {
       const OpDesc& op = ops[k];
+      const int at = op.chain < 0 ? k - 1 - (k >= 2 && ops[k - 1].chain < 0 ? 1 : 0) : k;
       switch (op.kind) {
-        case CONV: add(k, op.a, false); add(k, op.b, false); add(k, op.out, true); break;
-        case ADD: add(k, op.a, false); add(k, op.b, false); add(k, op.out, true); break;
+        case CONV: add(at, op.a, false); add(at, op.b, false); add(at, op.out, true); break;
+        case ADD: add(at, op.a, false); add(at, op.b, false); add(at, op.out, true); break;
         case DECODE:
         case DECODESEG:
           if (k == lastDecode)
@@ -166,15 +181,46 @@ struct Engine {
               if (d.kind == DECODE || d.kind == DECODESEG) { add(k, d.a, false); add(k, d.b, false); add(k, d.out, false); }
           break;
         case MASKS: break;
-        default: add(k, op.a, false); add(k, op.out, true); break;
+        default: add(at, op.a, false); add(at, op.out, true); break;
       }
     }
-    auto conflict = [&](int i, int j) {
-      for (const Acc& x : acc[i])
-        for (const Acc& y : acc[j])
-          if (x.buf == y.buf && x.c0 < y.c1 && y.c0 < x.c1 && (x.w || y.w)) return true;
-      return false;
-    };
+  }
+  bool conflict(int i, int j) const {
+    for (const Acc& x : acc[i])
+      for (const Acc& y : acc[j])
+        if (x.buf == y.buf && x.c0 < y.c1 && y.c0 < x.c1 && (x.w || y.w)) return true;
+    return false;
+  }
+
+  // Graph DAG: deps[j] = earlier ops whose accesses conflict with op j's, transitively
+  // reduced (an edge implied by a path through another dependency is dropped).
+  std::vector<std::vector<int>> dagDeps;
+  void planDag() {
+    computeAccesses();
+    const int n = (int)ops.size();
+    const int words = (n + 63) / 64;
+    std::vector<std::vector<uint64_t>> anc(n, std::vector<uint64_t>(words, 0));
+    dagDeps.assign(n, {});
+    for (int j = 0; j < n; j++) {
+      if (acc[j].empty()) continue;
+      std::vector<int> d;
+      for (int i = j - 1; i >= 0; i--)
+        if (!acc[i].empty() && conflict(i, j)) d.push_back(i);
+      // latest first: a dependency already reachable from a kept one is implied
+      std::vector<uint64_t> reach(words, 0);
+      for (int i : d) {
+        if ((reach[i >> 6] >> (i & 63)) & 1) continue;
+        dagDeps[j].push_back(i);
+        reach[i >> 6] |= 1ull << (i & 63);
+        for (int w = 0; w < words; w++) reach[w] |= anc[i][w];
+      }
+      anc[j] = reach;
+    }
+  }
+
+  void planStreams() {
+    computeAccesses();
+    const int n = (int)ops.size();
     const int NS = 1 + NSIDE;
     opStream.assign(n, 0);
     opWaits.assign(n, {});
@@ -299,17 +345,19 @@ struct Engine {
     const int A = std::max(g.numAnchors, 1);   // graphs without DECODE keep 1-slot buffers
     cstride = g.detStride;
     HCK(hipMalloc(&cand, (size_t)B * A * cstride * sizeof(float)));
-    HCK(hipMalloc(&keys, (size_t)B * A * sizeof(float)));
+    HCK(hipMalloc(&nmsCount, (size_t)B * sizeof(int)));
+    HCK(hipMemset(nmsCount, 0, (size_t)B * sizeof(int)));
     HCK(hipMalloc(&nmsScratch, (size_t)B * nmsScratchBytes(A)));
-    HCK(hipMalloc(&outdets, (size_t)B * MAX_OUT * 6 * sizeof(float)));
+    detOff = ((size_t)2 * B * sizeof(int) + 255) & ~(size_t)255;
+    const size_t resBytes = detOff + (size_t)B * MAX_OUT * 6 * sizeof(float);
+    HCK(hipMalloc(&results, resBytes));
+    HCK(hipMemset(results, 0, resBytes));
+    outcnt = (int*)results;
+    rawcnt = outcnt + B;
+    outdets = (float*)((char*)results + detOff);
     HCK(hipMalloc(&outidx, (size_t)B * MAX_OUT * sizeof(int)));
-    HCK(hipMalloc(&outcnt, (size_t)B * sizeof(int)));
-    HCK(hipMalloc(&rawcnt, (size_t)B * sizeof(int)));
     HCK(hipMemset(cand, 0, (size_t)B * A * cstride * sizeof(float)));
-    HCK(hipMemset(outdets, 0, (size_t)B * MAX_OUT * 6 * sizeof(float)));
     HCK(hipMemset(outidx, 0, (size_t)B * MAX_OUT * sizeof(int)));
-    HCK(hipMemset(outcnt, 0, (size_t)B * sizeof(int)));
-    HCK(hipMemset(rawcnt, 0, (size_t)B * sizeof(int)));
     if (g.protoTen >= 0) {
       const BufDesc& pb = g.bufs[g.tens[g.protoTen].buf];
       HCK(hipMalloc(&masks, (size_t)B * MAX_OUT * pb.H * pb.W));
@@ -317,12 +365,11 @@ struct Engine {
     }
     HCK(hipMalloc(&params, sizeof(PostParams)));
     HCK(hipMemcpy(params, &hparams, sizeof(PostParams), hipMemcpyHostToDevice));
-    HCK(hipHostMalloc(&h_out, (size_t)B * MAX_OUT * 6 * sizeof(float), hipHostMallocDefault));
-    HCK(hipHostMalloc(&h_cnt, (size_t)B * sizeof(int), hipHostMallocDefault));
-    HCK(hipHostMalloc(&h_rawcnt, (size_t)B * sizeof(int), hipHostMallocDefault));
-    memset(h_out, 0, (size_t)B * MAX_OUT * 6 * sizeof(float));
-    memset(h_cnt, 0, (size_t)B * sizeof(int));
-    memset(h_rawcnt, 0, (size_t)B * sizeof(int));
+    HCK(hipHostMalloc(&h_results, resBytes, hipHostMallocDefault));
+    memset(h_results, 0, resBytes);
+    h_cnt = (int*)h_results;
+    h_rawcnt = h_cnt + B;
+    h_out = (float*)((char*)h_results + detOff);
     // decode levels in op order
     dec = DecodeArgs{};
     int base = 0;
@@ -360,7 +407,9 @@ struct Engine {
         if (op.g == 1 && op.Cin == 3)
           launchConvFirst(x, y, w, b, op.s, op.p, op.act, Bn, s);
         else if (op.g == 1)
-          launchConvGemm(op.cfg, x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, s);
+          launchConvGemm(op.cfg, x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, op.split,
+                         op.wsOff >= 0 ? splitWs + op.wsOff : nullptr,
+                         op.cntOff >= 0 ? splitCnt + op.cntOff : nullptr, s);
         else
           launchDwConv(x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, s);
         break;
@@ -380,7 +429,7 @@ struct Engine {
       case DECODESEG:
         // all levels decode in one launch, issued at the last DECODE op (every head
         // tensor is final by then)
-        if (k == lastDecode) launchDecode(dec, cand, keys, params, Bn, s);
+        if (k == lastDecode) launchDecode(dec, cand, nmsScratch, nmsCount, params, Bn, s);
         break;
       default: break;   // MASKS is declarative; assembly runs after NMS
     }
@@ -388,21 +437,20 @@ struct Engine {
 
   void post(int Bn) {
     if (g.numAnchors == 0) return;   // no detection head (single-op graphs)
-    launchNms(cand, keys, g.numAnchors, cstride, outdets, outidx, outcnt, rawcnt, nmsScratch, params, Bn, st);
+    launchNms(cand, nmsScratch, nmsCount, g.numAnchors, cstride, outdets, outidx, outcnt, rawcnt, params, Bn, st);
     if (g.protoTen >= 0) {
       View pr = view(g.protoTen);
       launchMasks(pr, cand, cstride, g.numAnchors, g.nm, outidx, outcnt, outdets, masks,
                   (float)pr.W / g.bufs[g.tens[0].buf].W, (float)pr.H / g.bufs[g.tens[0].buf].H, Bn, st);
     }
-    HCK(hipMemcpyAsync(h_rawcnt, rawcnt, Bn * sizeof(int), hipMemcpyDeviceToHost, st));
-    HCK(hipMemcpyAsync(h_cnt, outcnt, Bn * sizeof(int), hipMemcpyDeviceToHost, st));
-    HCK(hipMemcpyAsync(h_out, outdets, (size_t)Bn * MAX_OUT * 6 * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipMemcpyAsync(h_results, results, detOff + (size_t)Bn * MAX_OUT * 6 * sizeof(float),
+                       hipMemcpyDeviceToHost, st));
   }
 
-  // `branches`: use the side-stream plan (eager execution only).  Graph capture always
-  // passes false: capturing the fork/join plan crashes inside hipStreamEndCapture on this
-  // ROCm 7.2 image (a small fork/join capture works; the ~100-node plan does not) and the
-  // cause has not been isolated, so captured graphs keep the single-stream order.
+  // `branches`: use the side-stream plan (eager execution only).  Graphs never capture the
+  // fork/join plan (capturing it crashed inside hipStreamEndCapture on this ROCm 7.2 image;
+  // the cause was not isolated): they get branch concurrency from the explicit DAG of
+  // per-op child graphs built in capture() instead.
   void forward(int Bn, bool branches = true) {
     if (side.empty() || !branches) {
       for (size_t k = 0; k < ops.size(); k++)
@@ -425,14 +473,52 @@ struct Engine {
     post(Bn);
   }
 
+  // ---------------------------------------------------------------- split-K scratch
+  // Grow the shared split-K buffers to at least `bytes` / `ncnt` (counters zeroed).  Only
+  // called before any graph is captured: graphs hold raw pointers into these buffers.
+  void ensureSplitScratch(size_t bytes, size_t ncnt) {
+    if (bytes > splitWsBytes) {
+      if (splitWs) HCK(hipFree(splitWs));
+      splitWs = nullptr;
+      HCK(hipMalloc(&splitWs, bytes));
+      splitWsBytes = bytes;
+    }
+    if (ncnt > splitCntN) {
+      if (splitCnt) HCK(hipFree(splitCnt));
+      splitCnt = nullptr;
+      HCK(hipMalloc(&splitCnt, ncnt * sizeof(int)));
+      HCK(hipMemset(splitCnt, 0, ncnt * sizeof(int)));
+      splitCntN = ncnt;
+    }
+  }
+  // Give every split op its own workspace and counter range (sized at the max batch), so
+  // ops on concurrent streams never share partials.
+  void assignSplits() {
+    size_t wsTot = 0, cntTot = 0;
+    for (OpDesc& op : ops) {
+      op.wsOff = op.cntOff = -1;
+      if (op.kind != CONV || op.g != 1 || op.Cin == 3 || op.split <= 1) continue;
+      View y = view(op.out);
+      const int M = B * y.H * y.W, cfg = op.cfg >= 0 ? op.cfg : heuristicTile(M, op.Cout, op.k * op.k * op.Cin);
+      op.cfg = cfg;
+      op.wsOff = (long)(wsTot / sizeof(float));
+      op.cntOff = (long)cntTot;
+      wsTot += (splitWorkspaceBytes(cfg, M, op.Cout, op.split) + 255) & ~(size_t)255;
+      cntTot += splitTiles(cfg, M, op.Cout);
+    }
+    ensureSplitScratch(wsTot, cntTot);
+  }
+
   // ---------------------------------------------------------------- autotune
-  // Time every eligible tile shape of every GEMM conv at the max batch (1 warm-up + 5
-  // timed launches each) and keep the fastest; identical shapes share one measurement.
+  // Time every eligible (tile shape, split-K factor) of every GEMM conv at the max batch
+  // (1 warm-up + 5 timed launches each) and keep the fastest; identical shapes share one
+  // measurement.  Splits are tried only while the tile grid leaves CUs idle.
   void autotune() {
     hipEvent_t e0, e1;
     HCK(hipEventCreate(&e0));
     HCK(hipEventCreate(&e1));
-    std::map<std::tuple<int, int, int, int, int, int, int, int>, int> cache;
+    std::map<std::tuple<int, int, int, int, int, int, int, int>, std::pair<int, int>> cache;
+    static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
     for (size_t k = 0; k < ops.size(); k++) {
       OpDesc& op = ops[k];
       if (op.kind != CONV || op.g != 1 || op.Cin == 3) continue;
@@ -440,23 +526,32 @@ struct Engine {
       const int M = B * y.H * y.W, N = op.Cout, K = op.k * op.k * op.Cin;
       auto key = std::make_tuple(y.H, y.W, op.Cin, op.Cout, op.k, op.s, op.b >= 0 ? 1 : 0, op.act);
       auto it = cache.find(key);
-      if (it != cache.end()) { op.cfg = it->second; continue; }
-      int best = heuristicTile(M, N, K);
+      if (it != cache.end()) { op.cfg = it->second.first; op.split = it->second.second; continue; }
+      int best = heuristicTile(M, N, K), bestSplit = 1;
       float bestMs = 1e30f;
       for (int cfg = 0; cfg < numTileConfigs(); cfg++) {
         if (!tileOk(cfg, M, N, K)) continue;
-        op.cfg = cfg;
-        runOp((int)k, B);
-        HCK(hipEventRecord(e0, st));
-        for (int r = 0; r < 5; r++) runOp((int)k, B);
-        HCK(hipEventRecord(e1, st));
-        HCK(hipEventSynchronize(e1));
-        float ms = 0.f;
-        HCK(hipEventElapsedTime(&ms, e0, e1));
-        if (ms < bestMs) { bestMs = ms; best = cfg; }
+        const int tiles = splitTiles(cfg, M, N);
+        for (int S : kSplits) {
+          if (S > 1 && (tiles * S > 1024 || tiles >= 256 || !splitOk(cfg, K, S))) continue;
+          op.cfg = cfg;
+          op.split = S;
+          op.wsOff = op.cntOff = S > 1 ? 0 : -1;
+          if (S > 1) ensureSplitScratch(splitWorkspaceBytes(cfg, M, N, S), (size_t)tiles);
+          runOp((int)k, B);
+          HCK(hipEventRecord(e0, st));
+          for (int r = 0; r < 5; r++) runOp((int)k, B);
+          HCK(hipEventRecord(e1, st));
+          HCK(hipEventSynchronize(e1));
+          float ms = 0.f;
+          HCK(hipEventElapsedTime(&ms, e0, e1));
+          if (ms < bestMs) { bestMs = ms; best = cfg; bestSplit = S; }
+        }
       }
       op.cfg = best;
-      cache[key] = best;
+      op.split = bestSplit;
+      op.wsOff = op.cntOff = -1;
+      cache[key] = {best, bestSplit};
     }
     HCK(hipGetLastError());
     (void)hipEventDestroy(e0);
@@ -464,24 +559,13 @@ struct Engine {
   }
 
   // ---------------------------------------------------------------- graphs
-  hipGraphExec_t capture(int Bn, const std::vector<std::pair<const uint8_t*, SlotGeom>>* frames,
-                         const unsigned char* const* host, const int* hs, const int* ws) {
-    hipGraph_t gr;
+  // Single-stream capture of whatever `f` enqueues on the engine stream.
+  template <class F>
+  hipGraph_t captureOne(F&& f) {
+    hipGraph_t gr = nullptr;
     HCK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
     try {
-      if (frames) {
-        const BufDesc& ib = g.bufs[g.tens[0].buf];
-        for (int s = 0; s < Bn; s++) {
-          const uint8_t* src = (*frames)[s].first;
-          if (host && host[s])
-            HCK(hipMemcpyAsync((void*)src, host[s], (size_t)hs[s] * ws[s] * 3, hipMemcpyHostToDevice, st));
-          const SlotGeom& sg = (*frames)[s].second;
-          int nh = (int)roundf(hs[s] * sg.scale), nw = (int)roundf(ws[s] * sg.scale);
-          launchPreprocess(src, hs[s], ws[s], bufp[g.tens[0].buf] + (size_t)s * ib.H * ib.W * 3, ib.H, ib.W,
-                           sg.scale, sg.top, sg.left, nh, nw, st);
-        }
-      }
-      forward(Bn, false);
+      f();
     } catch (...) {
       hipGraph_t dummy = nullptr;
       if (hipStreamEndCapture(st, &dummy) == hipSuccess && dummy) (void)hipGraphDestroy(dummy);
@@ -489,6 +573,97 @@ struct Engine {
       throw;
     }
     HCK(hipStreamEndCapture(st, &gr));
+    return gr;
+  }
+
+  void preprocessFrames(int Bn, const std::vector<std::pair<const uint8_t*, SlotGeom>>& frames,
+                        const unsigned char* const* host, const int* hs, const int* ws) {
+    const BufDesc& ib = g.bufs[g.tens[0].buf];
+    for (int s = 0; s < Bn; s++) {
+      const uint8_t* src = frames[s].first;
+      if (host && host[s])
+        HCK(hipMemcpyAsync((void*)src, host[s], (size_t)hs[s] * ws[s] * 3, hipMemcpyHostToDevice, st));
+      const SlotGeom& sg = frames[s].second;
+      int nh = (int)roundf(hs[s] * sg.scale), nw = (int)roundf(ws[s] * sg.scale);
+      launchPreprocess(src, hs[s], ws[s], bufp[g.tens[0].buf] + (size_t)s * ib.H * ib.W * 3, ib.H, ib.W,
+                       sg.scale, sg.top, sg.left, nh, nw, st);
+    }
+  }
+
+  // Batch-Bn graph: [frame prologue] + network + post, by default one single-stream
+  // capture.  With a DAG plan (YOLO_DAGGRAPH) every op is captured alone and re-added as
+  // kernel nodes whose edges are its buffer conflicts, so the runtime may run independent
+  // branches (the head's box/cls chains, neck levels) concurrently.  On ROCm 7.2 the
+  // runtime's cross-stream node synchronisation costs more than the overlap gains for
+  // these few-microsecond kernels (yolo11n b1: 0.56 ms DAG vs 0.46 ms serial).
+  hipGraphExec_t capture(int Bn, const std::vector<std::pair<const uint8_t*, SlotGeom>>* frames,
+                         const unsigned char* const* host, const int* hs, const int* ws) {
+    hipGraph_t gr = nullptr;
+    if (dagDeps.empty()) {
+      gr = captureOne([&] {
+        if (frames) preprocessFrames(Bn, *frames, host, hs, ws);
+        forward(Bn, false);
+      });
+    } else {
+      HCK(hipGraphCreate(&gr, 0));
+      try {
+        // a captured op is a chain of kernel nodes: re-add them as kernel nodes of the
+        // parent (chained, the first one on `deps`); anything else becomes a child graph
+        auto addChild = [&](hipGraph_t sub, const std::vector<hipGraphNode_t>& deps) {
+          size_t nn = 0;
+          HCK(hipGraphGetNodes(sub, nullptr, &nn));
+          hipGraphNode_t node = nullptr;
+          if (nn > 0) {
+            std::vector<hipGraphNode_t> sn(nn);
+            HCK(hipGraphGetNodes(sub, sn.data(), &nn));
+            bool allKernels = true;
+            for (auto x : sn) {
+              hipGraphNodeType ty;
+              HCK(hipGraphNodeGetType(x, &ty));
+              allKernels = allKernels && ty == hipGraphNodeTypeKernel;
+            }
+            if (allKernels) {
+              // captured nodes come back in capture (= dependency) order for a single stream
+              std::vector<hipGraphNode_t> d = deps;
+              for (auto x : sn) {
+                hipKernelNodeParams kp{};
+                HCK(hipGraphKernelNodeGetParams(x, &kp));
+                HCK(hipGraphAddKernelNode(&node, gr, d.data(), d.size(), &kp));
+                d.assign(1, node);
+              }
+            } else {
+              HCK(hipGraphAddChildGraphNode(&node, gr, deps.data(), deps.size(), sub));
+            }
+          }
+          HCK(hipGraphDestroy(sub));
+          return node;
+        };
+        hipGraphNode_t pre = nullptr;
+        if (frames) pre = addChild(captureOne([&] { preprocessFrames(Bn, *frames, host, hs, ws); }), {});
+        const int n = (int)ops.size();
+        const int inBuf = g.tens[0].buf;
+        std::vector<hipGraphNode_t> node(n, nullptr);
+        std::vector<char> hasSucc(n, 0);
+        for (int k = 0; k < n; k++) {
+          if (ops[k].chain < 0 || acc[k].empty()) continue;
+          std::vector<hipGraphNode_t> deps;
+          for (int d : dagDeps[k])
+            if (node[d]) { deps.push_back(node[d]); hasSucc[d] = 1; }
+          bool readsInput = false;
+          for (const Acc& x : acc[k]) readsInput = readsInput || x.buf == inBuf;
+          if (pre && (readsInput || deps.empty())) deps.push_back(pre);
+          node[k] = addChild(captureOne([&] { runOp(k, Bn); }), deps);
+        }
+        std::vector<hipGraphNode_t> sinks;
+        for (int k = 0; k < n; k++)
+          if (node[k] && !hasSucc[k]) sinks.push_back(node[k]);
+        if (sinks.empty() && pre) sinks.push_back(pre);
+        addChild(captureOne([&] { post(Bn); }), sinks);
+      } catch (...) {
+        (void)hipGraphDestroy(gr);
+        throw;
+      }
+    }
     hipGraphExec_t ex;
     HCK(hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0));
     HCK(hipGraphDestroy(gr));
@@ -559,6 +734,8 @@ Engine* create(const char* dir, int maxB, int flags) {
       e->createStreams();
     }
     if (!(flags & YOLO_NOTUNE)) e->autotune();
+    e->assignSplits();
+    if (flags & YOLO_DAGGRAPH) e->planDag();
     if (!(flags & YOLO_NOGRAPH)) e->buildGraphs();
   } catch (...) {
     delete e;
@@ -789,6 +966,9 @@ int yolo_run_op(void* h, int k, int B) {
   return guarded([&] {
     Engine* e = E(h);
     if (k < 0 || k >= (int)e->ops.size() || B < 1 || B > e->B) return -1;
+    // ops run one at a time may repeat a decode without NMS in between: start its
+    // candidate lists empty
+    if (k == e->lastDecode) HCK(hipMemsetAsync(e->nmsCount, 0, (size_t)e->B * sizeof(int), e->st));
     e->runOp(k, B);
     HCK(hipGetLastError());
     HCK(hipStreamSynchronize(e->st));
@@ -823,7 +1003,37 @@ int yolo_set_op_config(void* h, int k, int cfg) {
   yolo::OpDesc& op = e->ops[k];
   if (op.kind != yolo::CONV || op.g != 1 || op.Cin == 3 || cfg >= yolo::numTileConfigs()) return -1;
   op.cfg = cfg < 0 ? -1 : cfg;
+  op.split = 1;                 // a different tile needs a different split workspace
+  op.wsOff = op.cntOff = -1;
   return 0;
+}
+
+int yolo_op_split(void* h, int k) {
+  Engine* e = E(h);
+  if (k < 0 || k >= (int)e->ops.size()) return -1;
+  const yolo::OpDesc& op = e->ops[k];
+  if (op.kind != yolo::CONV || op.g != 1 || op.Cin == 3) return -1;
+  return op.split;
+}
+
+int yolo_set_op_split(void* h, int k, int splits) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (k < 0 || k >= (int)e->ops.size()) return -1;
+    yolo::OpDesc& op = e->ops[k];
+    if (op.kind != yolo::CONV || op.g != 1 || op.Cin == 3) return -1;
+    bool captured = e->frameGraph != nullptr;
+    for (auto ge : e->graphs) captured = captured || ge != nullptr;
+    if (captured) return -1;    // captured graphs hold the current workspace pointers
+    const yolo::View y = e->view(op.out);
+    const int M = e->B * y.H * y.W, K = op.k * op.k * op.Cin;
+    const int cfg = op.cfg >= 0 ? op.cfg : yolo::heuristicTile(M, op.Cout, K);
+    if (splits < 1 || splits > yolo::MAX_SPLITS || !yolo::splitOk(cfg, K, splits)) return -1;
+    op.cfg = cfg;
+    op.split = splits;
+    e->assignSplits();
+    return 0;
+  });
 }
 
 int yolo_num_tile_configs(void) { return yolo::numTileConfigs(); }
@@ -913,6 +1123,7 @@ int yolo_profile_ops(void* h, int B, int iters, float* ms) {
     for (auto& x : ev) HCK(hipEventCreate(&x));
     std::vector<double> acc(n, 0.0);
     for (int it = 0; it < iters; it++) {
+      HCK(hipMemsetAsync(e->nmsCount, 0, (size_t)e->B * sizeof(int), e->st));   // no NMS here
       HCK(hipEventRecord(ev[0], e->st));
       for (int k = 0; k < n; k++) {
         if (e->ops[k].chain >= 0) e->runOp(k, B);   // chain followers run inside the head
@@ -925,6 +1136,7 @@ int yolo_profile_ops(void* h, int B, int iters, float* ms) {
         acc[k] += t;
       }
     }
+    HCK(hipMemsetAsync(e->nmsCount, 0, (size_t)e->B * sizeof(int), e->st));
     for (auto& x : ev) hipEventDestroy(x);
     for (int k = 0; k < n; k++) ms[k] = (float)(acc[k] / iters);
     return 0;

@@ -25,6 +25,8 @@ struct OpDesc {
   int heads = 0, kd = 0, hd = 0;      // ATTN
   int stride = 0;                     // DECODE*
   int cfg = -1;                       // GEMM tile config (-1 = heuristic)
+  int split = 1;                      // GEMM split-K factor
+  long wsOff = -1, cntOff = -1;       // split-K workspace / counter offsets (engine-owned)
   int chain = 0;                      // MAXPOOL5: 3 = head of a fused SPPF chain,
                                       // -1 = pooled by the chain head in forward()
 };
@@ -89,8 +91,17 @@ const TileCfg& tileConfig(int cfg);
 
 // ------------------------------------------------------------------ launchers
 // conv.hip
+// Split-K: `splits` > 1 partitions the K stages over that many blocks per output tile; `ws`
+// holds splits x tiles x BM x BN fp32 partials (splitWorkspaceBytes) and `cnt` one zeroed
+// counter per tile (splitTiles), which the kernel leaves zeroed again.
+constexpr int MAX_SPLITS = 16;
+int splitStages(int Ktot, int BK, int splits);
+bool splitOk(int cfg, int Ktot, int splits);
+size_t splitWorkspaceBytes(int cfg, int M, int N, int splits);
+int splitTiles(int cfg, int M, int N);
 void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
-                    const float* bias, int k, int s, int p, int act, int Bn, hipStream_t st);
+                    const float* bias, int k, int s, int p, int act, int Bn, int splits,
+                    float* ws, int* cnt, hipStream_t st);
 void launchConvFirst(const View& x, const View& y, const f16* w, const float* bias, int s, int p,
                      int act, int Bn, hipStream_t st);
 void launchDwConv(const View& x, const View& y, const View* res, const f16* wt_kkc,
@@ -115,11 +126,13 @@ void launchAttention(const View& qkv, const View& y, int heads, int kd, int hd, 
 // frame.hip
 void launchPreprocess(const uint8_t* src, int sh, int sw, f16* dst, int dh, int dw, float scale,
                       int top, int left, int nh, int nw, hipStream_t st);
-void launchDecode(const DecodeArgs& a, float* cand, float* keys, const PostParams* prm, int Bn,
-                  hipStream_t st);
-void launchNms(const float* cand, const float* keys, int A, int cstride, float* out, int* outidx,
-               int* outcnt, int* rawcnt, unsigned long long* scratch, const PostParams* prm,
-               int Bn, hipStream_t st);
+// Decode appends each image's survivors as packed (score, anchor) keys to lists[img*A ..]
+// and counts[img] (zero on entry; NMS re-arms it).
+void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lists, int* counts,
+                  const PostParams* prm, int Bn, hipStream_t st);
+void launchNms(const float* cand, unsigned long long* lists, int* counts, int A, int cstride,
+               float* out, int* outidx, int* outcnt, int* rawcnt, const PostParams* prm, int Bn,
+               hipStream_t st);
 void launchMasks(const View& proto, const float* cand, int cstride, int A, int nm,
                  const int* outidx, const int* outcnt, const float* outdets, uint8_t* masks,
                  float rx, float ry, int Bn, hipStream_t st);

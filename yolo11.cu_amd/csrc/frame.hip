@@ -58,14 +58,27 @@ void launchPreprocess(const uint8_t* src, int sh, int sw, f16* dst, int dh, int 
 // counter, every anchor owns slot `anchor` of the candidate array and writes its score
 // (or -1) to keys[anchor]; NMS compacts in anchor order, so results do not depend on
 // thread scheduling.
+__device__ __forceinline__ unsigned long long packKey(float score, int anchor) {
+  return ((unsigned long long)__float_as_uint(score) << 32) | (unsigned)(0xFFFFFFFFu - (unsigned)anchor);
+}
+
+__device__ __forceinline__ int keyAnchor(unsigned long long k) {
+  return (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull));
+}
+
+// grid (anchor blocks, images): a wave never spans two images, so the survivors of a wave
+// are appended to the image's candidate list with one atomic (wave-aggregated).  The list
+// order depends on arrival; NMS sorts by key, so results do not.
 __global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict__ cand,
-                                                float* __restrict__ keys,
-                                                const PostParams* __restrict__ prm, int total,
-                                                int cstride) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  const int img = idx / a.A, an = idx - img * a.A;
-  int lv = 0;
+                                                unsigned long long* __restrict__ lst,
+                                                int* __restrict__ count,
+                                                const PostParams* __restrict__ prm, int cstride) {
+  const int img = blockIdx.y;
+  const int an = blockIdx.x * blockDim.x + threadIdx.x;
+  const bool inside = an < a.A;
+  const int idx = img * a.A + (inside ? an : 0);
+  float best = -INFINITY;
+  int bcls = 0, lv = 0;
   if (a.nlev > 1 && an >= a.lv[1].base) lv = 1;
   if (a.nlev > 2 && an >= a.lv[2].base) lv = 2;
   const DecodeLevel& L = a.lv[lv];
@@ -74,10 +87,8 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict_
   const size_t pix = (size_t)img * L.H * L.W + local;
 
   const f16* cp = L.cls.p + pix * L.cls.s + L.cls.o;
-  float best = -INFINITY;
-  int bcls = 0;
   // 8 chunks (64 classes) are fetched before any is consumed, so their latencies overlap
-  for (int c0 = 0; c0 < L.cls.C; c0 += 64) {
+  for (int c0 = 0; inside && c0 < L.cls.C; c0 += 64) {
     f16x8 v[8];
 #pragma unroll
     for (int u = 0; u < 8; u++)
@@ -94,8 +105,17 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict_
     }
   }
   const float score = 1.f / (1.f + expf(-best));
-  const bool keep = score >= prm->conf;
-  keys[idx] = keep ? score : -1.f;
+  const bool keep = inside && score >= prm->conf;
+  const unsigned long long bal = __ballot(keep);
+  if (bal) {
+    const int leader = __ffsll((long long)bal) - 1;
+    const int lane = threadIdx.x & 63;
+    int base = 0;
+    if (lane == leader) base = atomicAdd(&count[img], __popcll(bal));
+    base = __shfl(base, leader);
+    const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
+    if (keep && pos < a.A) lst[(size_t)img * a.A + pos] = packKey(score, an);
+  }
   if (!keep) return;
 
   const f16* bp = L.box.p + pix * L.box.s + L.box.o;
@@ -136,26 +156,30 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict_
   }
 }
 
-void launchDecode(const DecodeArgs& a, float* cand, float* keys, const PostParams* prm, int Bn,
-                  hipStream_t st) {
-  const int total = Bn * a.A;
-  k_decode<<<(total + 255) / 256, 256, 0, st>>>(a, cand, keys, prm, total, 6 + a.nm);
+void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lst, int* count,
+                  const PostParams* prm, int Bn, hipStream_t st) {
+  k_decode<<<dim3((a.A + 255) / 256, Bn), 256, 0, st>>>(a, cand, lst, count, prm, 6 + a.nm);
 }
 
 // ------------------------------------------------------------------ NMS
-// One block (16 waves) per image.
-//  1. compaction: anchors whose key >= 0, in anchor order (wave ballots + block prefix)
-//  2. ranking by the total order (score desc, anchor asc) packed in one u64 key: above
-//     NMS_CAP candidates a radix select keeps the NMS_CAP largest keys first, then each
-//     key's rank (the number of larger keys) places it in LDS
-//  3. greedy suppression (k_nms semantics, engine/engine.cu:1091-1109: same class only,
-//     inter/union > thr with a union > 0 guard) resolved 64 candidates at a time: the
-//     whole block builds the block's 64x64 suppression rows, wave 0 walks them with
-//     readlane, and the whole block strikes later candidates that overlap the block's
-//     survivors.  This is exactly the sequential greedy result, with three barriers per
-//     64 candidates instead of one per candidate, and every pairwise test spread over all
-//     1024 threads.
+// One block (16 waves) per image, on the candidate list the decode kernel appended.
+//  1. selection + ranking by the total order (score desc, anchor asc) packed in one u64
+//     key: above NMS_CAP candidates a radix select keeps the NMS_CAP largest keys, then
+//     each key's rank (the number of larger keys, counted by several threads per key)
+//     places it in LDS; the list's arrival order therefore never matters
+//  2. greedy suppression (k_nms semantics, engine/engine.cu:1091-1109: same class only,
+//     inter/union > thr with a union > 0 guard).  Suppression never crosses classes, so
+//     the greedy result is the union of independent per-class greedy passes: when every
+//     class has at most 64 candidates, each wave takes a share of the classes present,
+//     gathers a class's members in rank order with ballots (one lane per member), builds
+//     their suppression rows with ballots and resolves them by a bit scan; survivors are
+//     flagged by rank and a block prefix sum over the flags gives their output slots.
+//     Otherwise (a class with more than 64 candidates): 64 candidates per step, the block
+//     building that step's 64x64 rows, wave 0 walking them, the block striking later
+//     candidates.  Both give exactly the sequential greedy result.
+//  3. the list counter is re-armed (zeroed) for the next frame.
 constexpr int NMS_THREADS = 1024;
+constexpr int NMS_CLASSES = 1024;            // class histogram size of the per-class path
 
 // inter/union > thr, decided without the division unless the two sides are within a few
 // ulps (then the division decides, exactly as the reference writes it)
@@ -174,73 +198,36 @@ __device__ __forceinline__ bool suppresses(float4 a, float4 b, float thr) {
   return inter / ua > thr;
 }
 
-__device__ __forceinline__ unsigned long long packKey(float score, int anchor) {
-  return ((unsigned long long)__float_as_uint(score) << 32) | (unsigned)(0xFFFFFFFFu - (unsigned)anchor);
-}
-
-__device__ __forceinline__ int keyAnchor(unsigned long long k) {
-  return (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull));
-}
-
 __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ cand,
-                                                     const float* __restrict__ keys, int A,
-                                                     int cstride, float* __restrict__ out,
+                                                     unsigned long long* __restrict__ lists,
+                                                     int* __restrict__ counts, int A, int cstride,
+                                                     float* __restrict__ out,
                                                      int* __restrict__ outidx, int* __restrict__ outcnt,
                                                      int* __restrict__ rawcnt,
-                                                     unsigned long long* __restrict__ scratch,
                                                      const PostParams* __restrict__ prm) {
   __shared__ unsigned long long skey[NMS_CAP];
   __shared__ float4 sbox[NMS_CAP];
   __shared__ short scls[NMS_CAP];
+  __shared__ int chist[NMS_CLASSES];
+  __shared__ short present[NMS_CLASSES];
+  __shared__ int npresent, maxClass, wsum[NMS_THREADS / 64];
   __shared__ unsigned removed[NMS_CAP / 32];
   __shared__ unsigned long long rows[64];
   __shared__ short kept[64];
-  __shared__ int wcnt[NMS_THREADS / 64];
   __shared__ int hist[256];
   __shared__ unsigned long long keptmask, selPrefix;
   __shared__ int nout, selNeed, selCount, nkept;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int img = blockIdx.x;
-  const float* kimg = keys + (size_t)img * A;
   const float* cimg = cand + (size_t)img * A * cstride;
-  unsigned long long* lst = scratch + (size_t)img * A;
+  const unsigned long long* lst = lists + (size_t)img * A;
   const float thr = prm->iou;
   const int maxdet = min(prm->max_det, MAX_OUT);
-
-  // 1. compaction in anchor order; keys are fetched 8 chunks at a time into registers so
-  //    the global latency is paid once per 8 x 1024 anchors, not once per barrier
-  int n = 0;
-  constexpr int PF = 8;
-  for (int base0 = 0; base0 < A; base0 += PF * NMS_THREADS) {
-    float kv[PF];
-#pragma unroll
-    for (int u = 0; u < PF; u++) {
-      const int an = base0 + u * NMS_THREADS + tid;
-      kv[u] = an < A ? kimg[an] : -1.f;
-    }
-#pragma unroll
-    for (int u = 0; u < PF; u++) {
-      if (base0 + u * NMS_THREADS >= A) break;
-      const int an = base0 + u * NMS_THREADS + tid;
-      const bool f = kv[u] >= 0.f;
-      const unsigned long long bal = __ballot(f);
-      const int pre = __popcll(bal & ((1ull << lane) - 1ull));
-      if (lane == 0) wcnt[wave] = __popcll(bal);
-      __syncthreads();
-      int off = n, tot = 0;
-      for (int w = 0; w < NMS_THREADS / 64; w++) {
-        if (w < wave) off += wcnt[w];
-        tot += wcnt[w];
-      }
-      if (f) lst[off + pre] = packKey(kv[u], an);
-      n += tot;
-      __syncthreads();
-    }
-  }
+  const int n = min(counts[img], A);
   const int m = min(n, NMS_CAP);
 
-  // 2a. more candidates than NMS_CAP: radix-select the NMS_CAP largest keys (8 passes of
+  // 1a. more candidates than NMS_CAP: radix-select the NMS_CAP largest keys (8 passes of
   //     8-bit histograms from the top byte; keys are unique, so exactly NMS_CAP are >= T).
   //     Scores crowd into few bins, so lanes of a wave that share a bin add once
   //     (wave-aggregated atomics) instead of serialising on one LDS address.
@@ -287,31 +274,49 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   } else {
     for (int i = tid; i < n; i += NMS_THREADS) skey[i] = lst[i];
   }
+  if (tid == 0) nout = 0;
   __syncthreads();
-  // 2b. rank within LDS: position = number of strictly larger keys.  The sorted keys are
-  //     parked in the box array's storage, then every thread lifts its two entries (and
-  //     their candidate records) into registers before the arrays are written for good.
+
+  // 1b. rank = number of strictly larger keys.  Up to 1024 keys, TPK threads (adjacent
+  //     lanes) share a key's scan and add their counts with shuffles; above that every
+  //     thread ranks two keys.  Sorted keys are parked in the box array's storage, then
+  //     every thread lifts its entries (and their candidate records) into registers before
+  //     the arrays are written for good.
   static_assert(NMS_CAP == 2 * NMS_THREADS, "two sorted entries per thread");
   unsigned long long* sorted = reinterpret_cast<unsigned long long*>(sbox);
-  {
+  if (m <= NMS_THREADS) {
+    int tpk = 1;
+    while (tpk < 64 && m * tpk * 2 <= NMS_THREADS) tpk *= 2;
+    const int i = tid / tpk, part = tid - i * tpk;
+    unsigned long long k = ~0ull;
+    int r = 0;
+    if (i < m) {
+      k = skey[i];
+      int j = part;
+      for (; j + 7 * tpk < m; j += 8 * tpk) {   // 8 independent loads per trip
+        unsigned long long v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = skey[j + u * tpk];
+#pragma unroll
+        for (int u = 0; u < 8; u++) r += v[u] > k;
+      }
+      for (; j < m; j += tpk) r += skey[j] > k;
+    }
+    for (int o = 1; o < tpk; o <<= 1) r += __shfl_xor(r, o);
+    if (i < m && part == 0) sorted[r] = k;
+  } else {
     const int i0 = tid, i1 = tid + NMS_THREADS;
-    const unsigned long long k0 = i0 < m ? skey[i0] : ~0ull, k1 = i1 < m ? skey[i1] : ~0ull;
+    const unsigned long long k0 = skey[i0], k1 = i1 < m ? skey[i1] : ~0ull;
     int r0 = 0, r1 = 0;
-    int j = 0;
-    for (; j + 4 <= m; j += 4) {
-      const unsigned long long a = skey[j], b = skey[j + 1], c = skey[j + 2], d = skey[j + 3];
-      r0 += (a > k0) + (b > k0) + (c > k0) + (d > k0);
-      r1 += (a > k1) + (b > k1) + (c > k1) + (d > k1);
+    for (int j = 0; j < m; j++) {
+      const unsigned long long v = skey[j];
+      r0 += v > k0;
+      r1 += v > k1;
     }
-    for (; j < m; j++) {
-      r0 += skey[j] > k0;
-      r1 += skey[j] > k1;
-    }
-    if (i0 < m) sorted[r0] = k0;
+    sorted[r0] = k0;
     if (i1 < m) sorted[r1] = k1;
   }
   for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) removed[i] = 0u;
-  if (tid == 0) nout = 0;
   __syncthreads();
   unsigned long long kr[2] = {0ull, 0ull};
   float4 br[2];
@@ -338,82 +343,169 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   }
   __syncthreads();
 
-  // 3. greedy, 64 candidates per step
-  for (int cb = 0; cb * 64 < m; cb++) {
-    if (nout >= maxdet) break;
-    const int base = cb * 64;
-    const int nb = min(64, m - base);
-    // (a) in-block suppression rows: wave w builds rows w, w+16, ...; lane j of the wave
-    //     tests pair (i, j) and the row is the wave's ballot (no atomics, no clearing)
-    for (int i = wave; i < 64; i += NMS_THREADS / 64) {
-      const bool hit = lane > i && lane < nb && i < nb && scls[base + i] == scls[base + lane] &&
-                       suppresses(sbox[base + i], sbox[base + lane], thr);
-      const unsigned long long row = __ballot(hit);
-      if (lane == 0) rows[i] = row;
+  // writes survivor `i` (rank order) to output slot `slot`
+  auto emit = [&](int i, int slot) {
+    const float4 bi = sbox[i];
+    float* d = out + ((size_t)img * MAX_OUT + slot) * 6;
+    d[0] = bi.x; d[1] = bi.y; d[2] = bi.z; d[3] = bi.w;
+    d[4] = __uint_as_float((unsigned)(skey[i] >> 32));
+    d[5] = (float)scls[i];
+    outidx[img * MAX_OUT + slot] = keyAnchor(skey[i]);
+  };
+
+  // class histogram (classes present, largest class) for the per-class path
+  for (int c = tid; c < NMS_CLASSES; c += NMS_THREADS) chist[c] = 0;
+  if (tid == 0) { npresent = 0; maxClass = 0; }
+  __syncthreads();
+  bool perClass = true;
+  for (int i = tid; i < m; i += NMS_THREADS) {
+    const int c = scls[i];
+    if (c < 0 || c >= NMS_CLASSES) perClass = false;   // never for a valid model
+    else atomicAdd(&chist[c], 1);
+  }
+  perClass = __syncthreads_and(perClass);
+  for (int c = tid; c < NMS_CLASSES; c += NMS_THREADS) {
+    const int h = chist[c];
+    if (h > 0) {
+      present[atomicAdd(&npresent, 1)] = (short)c;
+      atomicMax(&maxClass, h);
     }
-    __syncthreads();
-    // (b) wave 0 walks the survivors in rank order: the lowest alive bit is kept and clears
-    //     its row; one iteration per survivor (scalar bit scan + two readlanes)
-    if (wave == 0) {
-      const unsigned long long row = rows[lane];
-      const unsigned long long valid = nb >= 64 ? ~0ull : ((1ull << nb) - 1ull);
-      const unsigned rlo = __builtin_amdgcn_readfirstlane(removed[2 * cb]);
-      const unsigned rhi = __builtin_amdgcn_readfirstlane(removed[2 * cb + 1]);
-      unsigned long long todo = ~(((unsigned long long)rhi << 32) | rlo) & valid;
-      unsigned long long alive = 0ull;
+  }
+  __syncthreads();
+  perClass = perClass && maxClass <= 64;
+
+  if (perClass) {
+    // 2a. per-class greedy: wave w takes present[w], present[w + 16], ...; `removed` holds
+    //     the kept flag of every candidate by rank (reused as a bit array)
+    for (int pc = wave; pc < npresent; pc += NMS_THREADS / 64) {
+      const int c = present[pc];
+      // members in rank order: lane t gets the t-th member's rank
+      int mine = -1, g = 0;
+      for (int i0 = 0; i0 < m; i0 += 64) {
+        const int i = i0 + lane;
+        const bool in = i < m && scls[i] == c;
+        const unsigned long long bal = __ballot(in);
+        const int before = __popcll(bal & ((1ull << lane) - 1ull));
+        // lane (g + before) of the wave receives member i: invert with a ds_bpermute-free
+        // scan -- each lane checks whether its slot falls in this chunk
+        const int slot = lane - g;
+        if (slot >= 0 && slot < __popcll(bal)) {
+          // the slot-th set bit of bal
+          unsigned long long b = bal;
+          for (int q = 0; q < slot; q++) b &= b - 1ull;
+          mine = i0 + __builtin_ctzll(b);
+        }
+        g += __popcll(bal);
+      }
+      const float4 bx = mine >= 0 ? sbox[mine] : make_float4(0.f, 0.f, 0.f, 0.f);
+      // row of member t: later members it suppresses
+      unsigned long long row = 0ull;
+      for (int t = 0; t < g; t++) {
+        const float4 bt = make_float4(__shfl(bx.x, t), __shfl(bx.y, t), __shfl(bx.z, t), __shfl(bx.w, t));
+        const unsigned long long r = __ballot(lane > t && lane < g && suppresses(bt, bx, thr));
+        if (lane == t) row = r;
+      }
+      unsigned long long todo = g >= 64 ? ~0ull : ((1ull << g) - 1ull), keep = 0ull;
       while (todo) {
-        const int tt = __builtin_ctzll(todo);
-        alive |= 1ull << tt;
-        const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, tt);
-        const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), tt);
-        todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << tt));
+        const int t = __builtin_ctzll(todo);
+        keep |= 1ull << t;
+        const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, t);
+        const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), t);
+        todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << t));
       }
-      const bool mine = (alive >> lane) & 1ull;
-      const int before = __popcll(alive & ((1ull << lane) - 1ull));
-      const int slot = nout + before;
-      if (mine) kept[before] = (short)lane;
-      if (mine && slot < maxdet) {
-        const int i = base + lane;
-        const float4 bi = sbox[i];
-        float* d = out + ((size_t)img * MAX_OUT + slot) * 6;
-        d[0] = bi.x; d[1] = bi.y; d[2] = bi.z; d[3] = bi.w;
-        d[4] = __uint_as_float((unsigned)(skey[i] >> 32));
-        d[5] = (float)scls[i];
-        outidx[img * MAX_OUT + slot] = keyAnchor(skey[i]);
-      }
-      if (lane == 0) {
-        keptmask = alive;
-        nkept = __popcll(alive);
-        nout = nout + __popcll(alive);
-      }
+      if ((keep >> lane) & 1ull) atomicOr(&removed[mine >> 5], 1u << (mine & 31));
     }
     __syncthreads();
-    // (c) strike later candidates that overlap a survivor of this block: pairs
-    //     (later j, kept i) spread over the block
-    const int K = nkept;
-    const int later = m - (base + 64);
-    if (K > 0 && later > 0) {
-      for (int p = tid; p < later * K; p += NMS_THREADS) {
-        const int j = base + 64 + p / K;
-        const int i = base + kept[p % K];
-        if ((removed[j >> 5] >> (j & 31)) & 1u) continue;
-        if (scls[i] == scls[j] && suppresses(sbox[i], sbox[j], thr)) atomicOr(&removed[j >> 5], 1u << (j & 31));
-      }
+    // 2b. output slots: exclusive prefix count of kept flags in rank order (thread t owns
+    //     ranks 2t, 2t+1)
+    const int r0 = 2 * tid, r1 = 2 * tid + 1;
+    const int f0 = r0 < m ? (removed[r0 >> 5] >> (r0 & 31)) & 1 : 0;
+    const int f1 = r1 < m ? (removed[r1 >> 5] >> (r1 & 31)) & 1 : 0;
+    int v = f0 + f1, incl = v;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
     }
+    if (lane == 63) wsum[wave] = incl;
     __syncthreads();
+    int off = 0;
+    for (int w = 0; w < wave; w++) off += wsum[w];
+    const int ex = off + incl - v;
+    if (f0 && ex < maxdet) emit(r0, ex);
+    if (f1 && ex + f0 < maxdet) emit(r1, ex + f0);
+    if (tid == NMS_THREADS - 1) nout = off + incl;
+    __syncthreads();
+  } else {
+    // 2'. 64 candidates per step
+    for (int cb = 0; cb * 64 < m; cb++) {
+      if (nout >= maxdet) break;
+      const int base = cb * 64;
+      const int nb = min(64, m - base);
+      // (a) in-block suppression rows: wave w builds rows w, w+16, ...; lane j of the wave
+      //     tests pair (i, j) and the row is the wave's ballot (no atomics, no clearing)
+      for (int i = wave; i < 64; i += NMS_THREADS / 64) {
+        const bool hit = lane > i && lane < nb && i < nb && scls[base + i] == scls[base + lane] &&
+                         suppresses(sbox[base + i], sbox[base + lane], thr);
+        const unsigned long long row = __ballot(hit);
+        if (lane == 0) rows[i] = row;
+      }
+      __syncthreads();
+      // (b) wave 0 walks the survivors in rank order: the lowest alive bit is kept and
+      //     clears its row; one iteration per survivor (scalar bit scan + two readlanes)
+      if (wave == 0) {
+        const unsigned long long row = rows[lane];
+        const unsigned long long valid = nb >= 64 ? ~0ull : ((1ull << nb) - 1ull);
+        const unsigned rlo = __builtin_amdgcn_readfirstlane(removed[2 * cb]);
+        const unsigned rhi = __builtin_amdgcn_readfirstlane(removed[2 * cb + 1]);
+        unsigned long long todo = ~(((unsigned long long)rhi << 32) | rlo) & valid;
+        unsigned long long alive = 0ull;
+        while (todo) {
+          const int tt = __builtin_ctzll(todo);
+          alive |= 1ull << tt;
+          const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, tt);
+          const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), tt);
+          todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << tt));
+        }
+        const bool mine = (alive >> lane) & 1ull;
+        const int before = __popcll(alive & ((1ull << lane) - 1ull));
+        const int slot = nout + before;
+        if (mine) kept[before] = (short)lane;
+        if (mine && slot < maxdet) emit(base + lane, slot);
+        if (lane == 0) {
+          keptmask = alive;
+          nkept = __popcll(alive);
+          nout = nout + __popcll(alive);
+        }
+      }
+      __syncthreads();
+      // (c) strike later candidates that overlap a survivor of this block: pairs
+      //     (later j, kept i) spread over the block
+      const int K = nkept;
+      const int later = m - (base + 64);
+      if (K > 0 && later > 0) {
+        for (int p = tid; p < later * K; p += NMS_THREADS) {
+          const int j = base + 64 + p / K;
+          const int i = base + kept[p % K];
+          if ((removed[j >> 5] >> (j & 31)) & 1u) continue;
+          if (scls[i] == scls[j] && suppresses(sbox[i], sbox[j], thr)) atomicOr(&removed[j >> 5], 1u << (j & 31));
+        }
+      }
+      __syncthreads();
+    }
   }
   if (tid == 0) {
     outcnt[img] = min(nout, maxdet);
     rawcnt[img] = n;
+    counts[img] = 0;   // re-arm the decode list for the next frame
   }
 }
 
 size_t nmsScratchBytes(int A) { return (size_t)A * sizeof(unsigned long long); }
 
-void launchNms(const float* cand, const float* keys, int A, int cstride, float* out, int* outidx,
-               int* outcnt, int* rawcnt, unsigned long long* scratch, const PostParams* prm,
-               int Bn, hipStream_t st) {
-  k_nms<<<Bn, NMS_THREADS, 0, st>>>(cand, keys, A, cstride, out, outidx, outcnt, rawcnt, scratch, prm);
+void launchNms(const float* cand, unsigned long long* lists, int* counts, int A, int cstride,
+               float* out, int* outidx, int* outcnt, int* rawcnt, const PostParams* prm, int Bn,
+               hipStream_t st) {
+  k_nms<<<Bn, NMS_THREADS, 0, st>>>(cand, lists, counts, A, cstride, out, outidx, outcnt, rawcnt, prm);
 }
 
 // ------------------------------------------------------------------ masks

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libyolo11_amd.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "yolo.h")
 
-YOLO_NOFUSE, YOLO_NOTUNE, YOLO_NOGRAPH, YOLO_BRANCHES = 1, 2, 4, 8
+YOLO_NOFUSE, YOLO_NOTUNE, YOLO_NOGRAPH, YOLO_BRANCHES, YOLO_DAGGRAPH = 1, 2, 4, 8, 16
 OP_KINDS = ["CONV", "ADD", "MAXPOOL5", "UPSAMPLE2", "COPYC", "ATTN", "DECODE", "GAP", "SOFTMAX",
             "DECODEOBB", "PS2", "DECODESEG", "MASKS"]
 MAX_OUT = 300
@@ -64,6 +64,8 @@ _SIGS = {
     "yolo_run_post": (C.c_int, [C.c_void_p, C.c_int]),
     "yolo_op_config": (C.c_int, [C.c_void_p, C.c_int]),
     "yolo_set_op_config": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    "yolo_op_split": (C.c_int, [C.c_void_p, C.c_int]),
+    "yolo_set_op_split": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
     "yolo_num_tile_configs": (C.c_int, []),
     "yolo_tile_config": (C.c_int, [C.c_int, C.POINTER(C.c_int)]),
     "yolo_frame_graph": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
@@ -222,6 +224,13 @@ class Engine:
     def set_op_config(self, k: int, cfg: int):
         if self.lib.yolo_set_op_config(self.h, k, cfg) != 0:
             raise ValueError((k, cfg))
+
+    def op_split(self, k: int) -> int:
+        return self.lib.yolo_op_split(self.h, k)
+
+    def set_op_split(self, k: int, splits: int):
+        if self.lib.yolo_set_op_split(self.h, k, splits) != 0:
+            raise ValueError((k, splits))
 
     # -- frame API
     def set_thresholds(self, conf=0.25, iou=0.45, max_det=300):
