@@ -253,3 +253,26 @@ def test_conv_split_k(tmp_path, shape):
         eng.set_op_config(0, cfg)   # back to split 1 for the next tile
     assert tried >= 4
     eng.close()
+
+
+@pytest.mark.parametrize("cout", [16, 32, 48, 96, 160, 256, 24])
+def test_conv_first(tmp_path, cout):
+    """The stem conv (Cin 3, 3x3 s2): the MFMA kernel (Cout % 16 == 0, paired 16-byte stores
+    when Cout % 32 == 0) and the direct kernel (Cout 24) against the oracle, with ragged
+    image edges and a batch."""
+    H, W, B = 37, 45, 2
+    d = str(tmp_path / "stem")
+    modelgen.write_single_conv(d, H, W, 3, cout, 3, 2, seed=cout)
+    g = graphfile.load(d)
+    x = np.random.default_rng(cout).uniform(0, 1, (B, H, W, 3)).astype(np.float16)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    eng.write(0, x)
+    eng.run_op(0, B)
+    got = eng.read(g.ops[0].out, B).astype(np.float32)
+    ref = interp.Interp(g, B)
+    ref.set_input(x.astype(np.float32))
+    ref.run_op(g.ops[0])
+    rel = post.rel_err(got, ref.view(g.ops[0].out))
+    print(f"stem Cout {cout}: rel {rel:.2e}", flush=True)
+    assert rel <= TOL
+    eng.close()

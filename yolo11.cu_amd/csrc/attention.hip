@@ -7,8 +7,8 @@
 //   out[b][n][h*hd + c] = sum_j softmax_j(q_n . k_j * kd^-1/2) * v_j[c]
 //
 // Design: grid (ceil(N/64), heads, B); a block of 4 waves owns 64 queries of one
-// (image, head) and streams the keys in chunks of 64 through LDS, flash-style, so the
-// N x N score matrix never exists in memory.
+// (image, head) and walks the keys in chunks of 64, flash-style, so the N x N score matrix
+// never exists in memory.  Small N (every key fits LDS) stages all keys at once.
 //  * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16 (kd = 32 is
 //    one MFMA K step): each lane then holds 16 scores of ONE query, so the online-softmax
 //    max needs only a 4-lane-group exchange and the running sum stays lane-local.
@@ -32,12 +32,20 @@ constexpr int VT_PITCH = 72;  // halves per V^T row in LDS (64 keys + 8 pad, bre
 
 __device__ __forceinline__ int kswz(int row, int c) { return row * 4 + (c ^ ((row >> 1) & 3)); }
 
-template <int HD>
+// WHOLE: every key of the (image, head) is staged in LDS once (dynamic LDS, N <= ATT_WHOLE_MAX)
+// with all global loads in flight together, and the chunk loop then runs without barriers;
+// otherwise keys stream through a 64-key buffer, one barrier pair per chunk.
+constexpr int ATT_WHOLE_MAX = 512;
+constexpr size_t ATT_WHOLE_LDS = 128 * 1024;   // dynamic LDS opt-in set by attentionInit()
+static bool attWholeOk = false;                 // the opt-in succeeded
+
+template <int HD, bool WHOLE>
 __global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int heads, float scale_log2) {
   constexpr int KD = 32;
   constexpr int CT = HD / 16;  // channel tiles of the output
-  __shared__ f16x8 sK[AK * 4];
-  __shared__ f16 sVt[HD * VT_PITCH];
+  extern __shared__ f16x8 dyn[];
+  __shared__ f16x8 sKs[WHOLE ? 1 : AK * 4];
+  __shared__ f16 sVts[WHOLE ? 1 : HD * VT_PITCH];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int lr = lane & 15, lg = lane >> 4;
@@ -45,6 +53,28 @@ __global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int 
   const int per = 2 * KD + HD;
   const int qoff = qkv.o + h * per;
   const size_t imgbase = (size_t)img * N;  // token index base of this image
+  const int nchunk = (N + AK - 1) / AK;
+  const int NP = nchunk * AK;
+  const int vpitch = WHOLE ? NP + 8 : VT_PITCH;
+  f16x8* sK = WHOLE ? dyn : sKs;
+  f16* sVt = WHOLE ? (f16*)(dyn + NP * 4) : sVts;
+
+  // stage keys [k0, k0 + cnt) into LDS rows kbase.. (K as 4 swizzled 16-byte chunks, V^T)
+  auto stage = [&](int k0, int cnt, int kbase) {
+    for (int i = t; i < cnt * 4; i += 256) {
+      const int key = i >> 2, c = i & 3;
+      f16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (k0 + key < N) kv = *(const f16x8*)(qkv.p + (imgbase + k0 + key) * qkv.s + qoff + KD + 8 * c);
+      sK[kswz(kbase + key, c)] = kv;
+    }
+    for (int i = t; i < cnt * (HD / 8); i += 256) {
+      const int key = i / (HD / 8), g = i - key * (HD / 8);
+      f16x8 vv = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (k0 + key < N) vv = *(const f16x8*)(qkv.p + (imgbase + k0 + key) * qkv.s + qoff + 2 * KD + 8 * g);
+#pragma unroll
+      for (int j = 0; j < 8; j++) sVt[(8 * g + j) * vpitch + kbase + key] = vv[j];
+    }
+  };
 
   // Q fragment: query lr of this wave, dims 8*lg .. 8*lg+7 (MFMA B operand)
   const int q = blockIdx.x * AQ + wave * 16 + lr;
@@ -56,31 +86,24 @@ __global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int 
 #pragma unroll
   for (int i = 0; i < CT; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nchunk = (N + AK - 1) / AK;
+  if (WHOLE) {
+    stage(0, NP, 0);
+    __syncthreads();
+  }
   for (int ch = 0; ch < nchunk; ch++) {
     const int k0 = ch * AK;
-    // ---- stage K [64][32] and V^T [HD][64] of this chunk
-    {
-      const int key = t >> 2, c = t & 3;
-      f16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (k0 + key < N) kv = *(const f16x8*)(qkv.p + (imgbase + k0 + key) * qkv.s + qoff + KD + 8 * c);
-      sK[kswz(key, c)] = kv;
+    const int kb = WHOLE ? k0 : 0;   // LDS row of this chunk's first key
+    if (!WHOLE) {
+      stage(k0, AK, 0);
+      __syncthreads();
     }
-    for (int i = t; i < AK * (HD / 8); i += 256) {
-      const int key = i / (HD / 8), g = i - key * (HD / 8);
-      f16x8 vv = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (k0 + key < N) vv = *(const f16x8*)(qkv.p + (imgbase + k0 + key) * qkv.s + qoff + 2 * KD + 8 * g);
-#pragma unroll
-      for (int j = 0; j < 8; j++) sVt[(8 * g + j) * VT_PITCH + key] = vv[j];
-    }
-    __syncthreads();
 
     // ---- S^T tiles: lane holds scores of query lr for keys kt*16 + 4*lg + r
     float s[4][4];
     float cmax = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 4; kt++) {
-      f16x8 fk = sK[kswz(kt * 16 + lr, lg)];
+      f16x8 fk = sK[kswz(kb + kt * 16 + lr, lg)];
       f32x4 z = __builtin_amdgcn_mfma_f32_16x16x32_f16(fk, fq, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
       for (int r = 0; r < 4; r++) {
@@ -117,14 +140,14 @@ __global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int 
       }
 #pragma unroll
       for (int i = 0; i < CT; i++) {
-        const f16* vrow = sVt + (i * 16 + lr) * VT_PITCH + hh * 32 + 4 * lg;
+        const f16* vrow = sVt + (i * 16 + lr) * vpitch + kb + hh * 32 + 4 * lg;
         const f16x4 v0 = *(const f16x4*)(vrow);
         const f16x4 v1 = *(const f16x4*)(vrow + 16);
         f16x8 fv = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
         oacc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fv, fp, oacc[i], 0, 0, 0);
       }
     }
-    __syncthreads();
+    if (!WHOLE) __syncthreads();
   }
 
   lrun += __shfl_xor(lrun, 16);
@@ -140,21 +163,44 @@ __global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int 
   }
 }
 
+template <int HD>
+static void launchAttn(const View& qkv, const View& y, int N, int heads, float sl2, int Bn, hipStream_t st) {
+  dim3 grid((N + AQ - 1) / AQ, heads, Bn);
+  const int NP = (N + AK - 1) / AK * AK;
+  const size_t lds = (size_t)NP * 4 * sizeof(f16x8) + (size_t)HD * (NP + 8) * sizeof(f16);
+  if (attWholeOk && N <= ATT_WHOLE_MAX && lds <= ATT_WHOLE_LDS)
+    k_attention<HD, true><<<grid, 256, lds, st>>>(qkv, y, N, heads, sl2);
+  else
+    k_attention<HD, false><<<grid, 256, 0, st>>>(qkv, y, N, heads, sl2);
+}
+
+// Whole-key kernels use more than the default 64 KiB of dynamic LDS; opt them in once per
+// process (a function attribute, not a stream operation).
+void attentionInit() {
+  bool ok = true;
+#define ATT_ALLOW(HD)                                                                          \
+  ok = ok && hipFuncSetAttribute((const void*)k_attention<HD, true>,                           \
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)ATT_WHOLE_LDS) == hipSuccess;
+  ATT_ALLOW(16) ATT_ALLOW(32) ATT_ALLOW(48) ATT_ALLOW(64) ATT_ALLOW(80) ATT_ALLOW(96) ATT_ALLOW(112) ATT_ALLOW(128)
+#undef ATT_ALLOW
+  (void)hipGetLastError();
+  attWholeOk = ok;
+}
+
 void launchAttention(const View& qkv, const View& y, int heads, int kd, int hd, int Bn,
                      hipStream_t st) {
   (void)kd;  // the loader accepts kd == 32 only
   const int N = qkv.H * qkv.W;
   const float scale_log2 = (1.0f / sqrtf(32.0f)) * 1.4426950408889634f;
-  dim3 grid((N + AQ - 1) / AQ, heads, Bn);
   switch (hd) {
-    case 16: k_attention<16><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
-    case 32: k_attention<32><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
-    case 48: k_attention<48><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
-    case 64: k_attention<64><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
-    case 80: k_attention<80><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
-    case 96: k_attention<96><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
-    case 112: k_attention<112><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
-    case 128: k_attention<128><<<grid, 256, 0, st>>>(qkv, y, N, heads, scale_log2); break;
+    case 16: launchAttn<16>(qkv, y, N, heads, scale_log2, Bn, st); break;
+    case 32: launchAttn<32>(qkv, y, N, heads, scale_log2, Bn, st); break;
+    case 48: launchAttn<48>(qkv, y, N, heads, scale_log2, Bn, st); break;
+    case 64: launchAttn<64>(qkv, y, N, heads, scale_log2, Bn, st); break;
+    case 80: launchAttn<80>(qkv, y, N, heads, scale_log2, Bn, st); break;
+    case 96: launchAttn<96>(qkv, y, N, heads, scale_log2, Bn, st); break;
+    case 112: launchAttn<112>(qkv, y, N, heads, scale_log2, Bn, st); break;
+    case 128: launchAttn<128>(qkv, y, N, heads, scale_log2, Bn, st); break;
     default: break;
   }
 }

@@ -304,6 +304,19 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   };
 
   const int nks = min((Ktot + BK - 1) / BK - st0, spl);   // this block's stages (>= 1)
+  // Narrow wave tiles fetch their epilogue bias now, so its latency hides behind the K loop
+  // (for short-K convs it would otherwise be a full extra global round trip at the end).
+  // Lane channels: fragment i of a pair p holds n0(p) + 4h .. +3; unpaired: n0(i) .. +3.
+  constexpr bool BPRE = FN <= 4;
+  float bpre[BPRE ? FN : 1][4];
+  if constexpr (BPRE) {
+#pragma unroll
+    for (int i = 0; i < FN; i++) {
+      const int n0 = PAIR ? bn + wn * TN + 32 * (i / 2) + 8 * lg + 4 * (i % 2) : bn + wn * TN + i * 16 + 4 * lg;
+#pragma unroll
+      for (int e = 0; e < 4; e++) bpre[i][e] = n0 < N ? bias[n0 + e] : 0.f;
+    }
+  }
   // step k: wait for this wave's stage-k loads, barrier (all waves' stage-k chunks are in
   // LDS and every wave is done reading stage k-1's buffer), refill that buffer with stage
   // k+NS-1, then the fragment reads and MFMAs of stage k.
@@ -383,7 +396,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
       if (n0 >= N) continue;  // N % 8 == 0: all 8 channels valid or none
       float b[8];
 #pragma unroll
-      for (int e = 0; e < 8; e++) b[e] = bias[n0 + e];
+      for (int e = 0; e < 4; e++) {
+        b[e] = BPRE ? bpre[BPRE ? 2 * p : 0][e] : bias[n0 + e];
+        b[4 + e] = BPRE ? bpre[BPRE ? 2 * p + 1 : 0][e] : bias[n0 + 4 + e];
+      }
 #pragma unroll
       for (int jj = 0; jj < FM; jj++) {
         const int m = bm + wm * TM + jj * 16 + lr;
@@ -415,7 +431,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     for (int i = 0; i < FN; i++) {
       const int n0 = bn + wn * TN + i * 16 + 4 * lg;
       if (n0 >= N) continue;
-      const float b0 = bias[n0], b1 = bias[n0 + 1], b2 = bias[n0 + 2], b3 = bias[n0 + 3];
+      const float b0 = BPRE ? bpre[BPRE ? i : 0][0] : bias[n0], b1 = BPRE ? bpre[BPRE ? i : 0][1] : bias[n0 + 1];
+      const float b2 = BPRE ? bpre[BPRE ? i : 0][2] : bias[n0 + 2], b3 = BPRE ? bpre[BPRE ? i : 0][3] : bias[n0 + 3];
 #pragma unroll
       for (int jj = 0; jj < FM; jj++) {
         const int m = bm + wm * TM + jj * 16 + lr;
@@ -614,10 +631,137 @@ __global__ __launch_bounds__(256) void k_conv_first(View x, View y, const f16* _
   }
 }
 
+// MFMA form of the stem (used when Cout % 16 == 0 and stride <= 2): K = 27 taps padded to
+// one 32-wide v_mfma_f32_16x16x32_f16 step.  A block owns FIRST_RB output rows x 128 output
+// columns x up to 128 output channels (grid (column segments, row groups, images x channel
+// blocks)).  Everything it reads is staged in LDS with coalesced loads: the input window
+// ((FIRST_RB-1)*s + 3 rows x (127*s + 3) columns x 3 channels, zeros outside the image), the
+// weights and the biases.  Lane (p, g) then builds its B fragment (k = 8g .. 8g+7 of pixel p)
+// from LDS at a per-lane constant offset, and its A fragments (weight rows permuted as in the
+// GEMM so fragment pairs give 8 consecutive channels per lane) once per block.  Each
+// 16-pixel group's outputs pass through a per-wave LDS buffer so global stores are
+// contiguous 16-byte-per-lane runs.
+constexpr int FIRST_TP = 128;                        // output columns per block
+constexpr int FIRST_RB = 4;                          // output rows per block
+constexpr int FIRST_COLS = (FIRST_TP - 1) * 2 + 3;   // input columns (stride <= 2)
+constexpr int FIRST_ROWS = (FIRST_RB - 1) * 2 + 3;   // input rows (stride <= 2)
+
+template <bool PAIR>
+__global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f16* __restrict__ w,
+                                                         const float* __restrict__ bias, int cs,
+                                                         int cp, int act, int ncb) {
+  constexpr int NF = 8;   // 16-channel fragments per block (128 channels)
+  constexpr int OPITCH = 16 * NF + 8;
+  __shared__ f16 tile[FIRST_ROWS][FIRST_COLS * 3];
+  __shared__ f16 sw[16 * NF * 27];
+  __shared__ float sb[16 * NF];
+  __shared__ __attribute__((aligned(16))) f16 ostage[4][16 * OPITCH];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int ox0 = blockIdx.x * FIRST_TP, oy0 = blockIdx.y * FIRST_RB;
+  const int img = blockIdx.z / ncb, cb = (blockIdx.z - img * ncb) * 16 * NF;
+  const int nf = min(NF, (y.C - cb) / 16);
+  const int cols = (FIRST_TP - 1) * cs + 3, rows = (FIRST_RB - 1) * cs + 3;
+  const int ix0 = ox0 * cs - cp, iy0 = oy0 * cs - cp;
+
+  // ---- stage input window, weights, biases
+  const f16* xb = x.p + (size_t)img * x.H * x.W * x.s + x.o;
+  for (int r = 0; r < rows; r++) {
+    const int iy = iy0 + r;
+    const bool rowin = iy >= 0 && iy < x.H;
+    const f16* xrow = xb + (size_t)(rowin ? iy : 0) * x.W * x.s;
+    for (int q = threadIdx.x; q < cols * 3; q += 256) {
+      const int c = q / 3, ci = q - 3 * c;   // constant divisor: a multiply-high
+      const int ix = ix0 + c;
+      tile[r][q] = (rowin && ix >= 0 && ix < x.W) ? xrow[ix * x.s + ci] : (f16)0.f;
+    }
+  }
+  for (int e = threadIdx.x; e < nf * 16 * 27; e += 256) sw[e] = w[(size_t)cb * 27 + e];
+  for (int e = threadIdx.x; e < nf * 16; e += 256) sb[e] = bias[cb + e];
+  __syncthreads();
+
+  int toff[8];
+  bool tok[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int k = 8 * lg + j, t = k / 3, ci = k - 3 * t;
+    tok[j] = k < 27;
+    toff[j] = tok[j] ? (t / 3) * (FIRST_COLS * 3) + (t % 3) * 3 + ci : 0;
+  }
+  f16x8 fw[NF];
+  float bb[NF][4];
+#pragma unroll
+  for (int f = 0; f < NF; f++) {
+    fw[f] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    const int row = 16 * f + lr;
+    const int co = PAIR ? chperm(row) : row;   // channel within the block
+    const int n0 = PAIR ? 32 * (f / 2) + 8 * lg + 4 * (f % 2) : 16 * f + 4 * lg;
+    if (f < nf) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) fw[f][j] = tok[j] ? sw[co * 27 + 8 * lg + j] : (f16)0.f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) bb[f][e] = sb[n0 + e];
+    }
+  }
+
+  const f16* tflat = &tile[0][0];
+  f16* obuf = &ostage[wave][0];
+  const int chunks = 2 * nf;                 // 16-byte chunks per pixel (16*nf channels)
+  // lane's first (pixel, chunk) of the output exchange and the per-step advance of 64 items
+  const int pxl = lane / chunks, ckl = lane - pxl * chunks;
+  const int pxs = 64 / chunks, cks = 64 - pxs * chunks;
+  for (int rr = 0; rr < FIRST_RB; rr++) {
+    const int oy = oy0 + rr;
+    if (oy >= y.H) break;                    // block-uniform
+#pragma unroll
+    for (int gi = 0; gi < FIRST_TP / 64; gi++) {
+      const int pbase = wave * (FIRST_TP / 4) + gi * 16;
+      if (ox0 + pbase >= y.W) break;         // wave-uniform
+      const int p = pbase + lr;
+      f16x8 fb;
+#pragma unroll
+      for (int j = 0; j < 8; j++) fb[j] = tok[j] ? tflat[rr * cs * (FIRST_COLS * 3) + toff[j] + 3 * cs * p] : (f16)0.f;
+#pragma unroll
+      for (int f = 0; f < NF; f++) {
+        if (f >= nf) break;
+        const f32x4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fw[f], fb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        const int c0 = PAIR ? 32 * (f / 2) + 8 * lg + 4 * (f % 2) : 16 * f + 4 * lg;
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float v = acc[e] + bb[f][e];
+          o[e] = (f16)(act == 1 ? silu(v) : v);
+        }
+        *(f16x4*)(obuf + lr * OPITCH + c0) = o;
+      }
+      // wave-local exchange: every lane's LDS writes land before any lane reads
+      __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+      __builtin_amdgcn_wave_barrier();
+      const int npix = min(16, y.W - (ox0 + pbase));
+      f16* orow = y.p + ((size_t)(img * y.H + oy) * y.W + ox0 + pbase) * y.s + y.o + cb;
+      for (int px = pxl, ck = ckl; px < npix; px += pxs, ck += cks) {   // (px, ck) = lane + 64*it
+        if (ck >= chunks) { ck -= chunks; px++; if (px >= npix) break; }
+        *(f16x8*)(orow + (size_t)px * y.s + 8 * ck) = *(const f16x8*)(obuf + px * OPITCH + 8 * ck);
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+}
+
 void launchConvFirst(const View& x, const View& y, const f16* w, const float* bias, int s, int p,
                      int act, int Bn, hipStream_t st) {
   const int M = Bn * y.H * y.W;
-  k_conv_first<<<(M + 255) / 256, 256, 0, st>>>(x, y, w, bias, s, p, act, M);
+  if (y.C % 16 == 0 && s >= 1 && s <= 2) {
+    const int ncb = (y.C + 127) / 128;
+    dim3 grid((y.W + FIRST_TP - 1) / FIRST_TP, (y.H + FIRST_RB - 1) / FIRST_RB, Bn * ncb);
+    if (y.C % 32 == 0)
+      k_conv_first_mfma<true><<<grid, 256, 0, st>>>(x, y, w, bias, s, p, act, ncb);
+    else
+      k_conv_first_mfma<false><<<grid, 256, 0, st>>>(x, y, w, bias, s, p, act, ncb);
+  } else {
+    k_conv_first<<<(M + 255) / 256, 256, 0, st>>>(x, y, w, bias, s, p, act, M);
+  }
 }
 
 // ------------------------------------------------------------------ depthwise conv

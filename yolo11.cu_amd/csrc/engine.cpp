@@ -327,6 +327,7 @@ struct Engine {
       }
     }
     HCK(hipStreamCreate(&st));
+    attentionInit();
     HCK(hipMalloc(&weights, std::max<size_t>(wf.size(), 16)));
     HCK(hipMalloc(&bias, std::max<size_t>(bf.size(), 16)));
     HCK(hipMemcpy(weights, wf.data(), wf.size(), hipMemcpyHostToDevice));
@@ -511,14 +512,26 @@ struct Engine {
 
   // ---------------------------------------------------------------- autotune
   // Time every eligible (tile shape, split-K factor) of every GEMM conv at the max batch
-  // (1 warm-up + 5 timed launches each) and keep the fastest; identical shapes share one
-  // measurement.  Splits are tried only while the tile grid leaves CUs idle.
+  // (2 warm-up launches, then the median of 7 individually timed ones) and keep the
+  // fastest; identical shapes share one measurement.  Splits are tried only while the tile grid leaves CUs idle.
   void autotune() {
     hipEvent_t e0, e1;
     HCK(hipEventCreate(&e0));
     HCK(hipEventCreate(&e1));
     std::map<std::tuple<int, int, int, int, int, int, int, int>, std::pair<int, int>> cache;
     static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    // YOLO_TUNE_TILES="a,b,..." restricts the candidate tile configs (for A/B studies)
+    std::vector<char> allowed(numTileConfigs(), 1);
+    if (const char* lim = getenv("YOLO_TUNE_TILES")) {
+      std::fill(allowed.begin(), allowed.end(), 0);
+      for (const char* q = lim; *q;) {
+        char* end = nullptr;
+        const long v = strtol(q, &end, 10);
+        if (end == q) break;
+        if (v >= 0 && v < numTileConfigs()) allowed[v] = 1;
+        q = *end ? end + 1 : end;
+      }
+    }
     for (size_t k = 0; k < ops.size(); k++) {
       OpDesc& op = ops[k];
       if (op.kind != CONV || op.g != 1 || op.Cin == 3) continue;
@@ -530,7 +543,7 @@ struct Engine {
       int best = heuristicTile(M, N, K), bestSplit = 1;
       float bestMs = 1e30f;
       for (int cfg = 0; cfg < numTileConfigs(); cfg++) {
-        if (!tileOk(cfg, M, N, K)) continue;
+        if (!allowed[cfg] || !tileOk(cfg, M, N, K)) continue;
         const int tiles = splitTiles(cfg, M, N);
         for (int S : kSplits) {
           if (S > 1 && (tiles * S > 1024 || tiles >= 256 || !splitOk(cfg, K, S))) continue;
@@ -538,13 +551,17 @@ struct Engine {
           op.split = S;
           op.wsOff = op.cntOff = S > 1 ? 0 : -1;
           if (S > 1) ensureSplitScratch(splitWorkspaceBytes(cfg, M, N, S), (size_t)tiles);
-          runOp((int)k, B);
-          HCK(hipEventRecord(e0, st));
-          for (int r = 0; r < 5; r++) runOp((int)k, B);
-          HCK(hipEventRecord(e1, st));
-          HCK(hipEventSynchronize(e1));
-          float ms = 0.f;
-          HCK(hipEventElapsedTime(&ms, e0, e1));
+          for (int r = 0; r < 2; r++) runOp((int)k, B);
+          float t[7];
+          for (int r = 0; r < 7; r++) {
+            HCK(hipEventRecord(e0, st));
+            runOp((int)k, B);
+            HCK(hipEventRecord(e1, st));
+            HCK(hipEventSynchronize(e1));
+            HCK(hipEventElapsedTime(&t[r], e0, e1));
+          }
+          std::sort(t, t + 7);
+          const float ms = t[3];   // median: robust to clock ramps and one-off stalls
           if (ms < bestMs) { bestMs = ms; best = cfg; bestSplit = S; }
         }
       }

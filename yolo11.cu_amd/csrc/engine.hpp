@@ -121,6 +121,7 @@ void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st);
 void launchCopyC(const View& x, const View& y, int Bn, hipStream_t st);
 void launchPS2(const View& x, const View& y, int Bn, hipStream_t st);
 // attention.hip
+void attentionInit();
 void launchAttention(const View& qkv, const View& y, int heads, int kd, int hd, int Bn,
                      hipStream_t st);
 // frame.hip
