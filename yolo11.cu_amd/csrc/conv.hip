@@ -304,10 +304,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   };
 
   const int nks = min((Ktot + BK - 1) / BK - st0, spl);   // this block's stages (>= 1)
-  // Narrow wave tiles fetch their epilogue bias now, so its latency hides behind the K loop
+  // Small wave tiles fetch their epilogue bias now, so its latency hides behind the K loop
   // (for short-K convs it would otherwise be a full extra global round trip at the end).
   // Lane channels: fragment i of a pair p holds n0(p) + 4h .. +3; unpaired: n0(i) .. +3.
-  constexpr bool BPRE = FN <= 4;
+  constexpr bool BPRE = FN * FM <= 8;   // small tiles only: keep big tiles under the VGPR cliff
   float bpre[BPRE ? FN : 1][4];
   if constexpr (BPRE) {
 #pragma unroll
@@ -325,26 +325,33 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
       if (ahead == A) vmwait<A * NI>();
     });
   };
-  for (int k = 0; k < min(NS - 1, nks); k++) issue(ring + k * SZ);
-  int cur = 0;   // ring slot of stage k
-  for (int k = 0; k < nks; k++) {
-    waitStage(min(NS - 2, nks - 1 - k));
-    asm volatile("s_barrier" ::: "memory");
-    const f16x8* buf = ring + cur * SZ;
-    // first fragment reads go out before the DMA address arithmetic, which then hides
-    // their latency
-    f16x8 fa[FN], fb[FM];
-    reads(buf, 0, fa, fb);
-    __builtin_amdgcn_sched_barrier(0);
-    if (k + NS - 1 < nks) issue(ring + (cur == 0 ? NS - 1 : cur - 1) * SZ);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(fa, fb);
+  static_for<NS - 1>([&](auto J) {
+    if (J < nks) issue(ring + J * SZ);
+  });
+  // the k loop is unrolled NS-fold so every ring slot address is a compile-time offset
+  for (int k0 = 0; k0 < nks; k0 += NS) {
+    static_for<NS>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const int k = k0 + j;
+      if (k < nks) {
+        waitStage(min(NS - 2, nks - 1 - k));
+        asm volatile("s_barrier" ::: "memory");
+        const f16x8* buf = ring + j * SZ;
+        // first fragment reads go out before the DMA address arithmetic, which then hides
+        // their latency
+        f16x8 fa[FN], fb[FM];
+        reads(buf, 0, fa, fb);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + NS - 1 < nks) issue(ring + ((j + NS - 1) % NS) * SZ);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fa, fb);
 #pragma unroll
-    for (int s = 1; s < KS; s++) {
-      reads(buf, s, fa, fb);
-      mfmas(fa, fb);
-    }
-    cur = cur + 1 == NS ? 0 : cur + 1;
+        for (int s = 1; s < KS; s++) {
+          reads(buf, s, fa, fb);
+          mfmas(fa, fb);
+        }
+      }
+    });
   }
 
   // ---- split-K reduction: every split stores its fp32 partial tile (thread-private
@@ -366,24 +373,16 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     __syncthreads();
     if (!lastBlock) return;
     __threadfence();
-    f32x4 sum[FN][FM];
+    // re-read every partial, this block's own included, so the sum is formed in place (no
+    // second accumulator set competing for registers) and always in split order
 #pragma unroll
     for (int i = 0; i < FN; i++)
 #pragma unroll
-      for (int j = 0; j < FM; j++) sum[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < splits; sp++) {
-#pragma unroll
-      for (int i = 0; i < FN; i++)
-#pragma unroll
-        for (int j = 0; j < FM; j++)
-          sum[i][j] += sp == split ? acc[i][j]
-                                   : *(const f32x4*)(ws + ((size_t)sp * nblk + tile) * TILE +
-                                                     ((i * FM + j) * NT + t) * 4);
-    }
-#pragma unroll
-    for (int i = 0; i < FN; i++)
-#pragma unroll
-      for (int j = 0; j < FM; j++) acc[i][j] = sum[i][j];
+      for (int j = 0; j < FM; j++) {
+        const float* src = ws + (size_t)tile * TILE + ((i * FM + j) * NT + t) * 4;
+        acc[i][j] = *(const f32x4*)src;
+        for (int sp = 1; sp < splits; sp++) acc[i][j] += *(const f32x4*)(src + (size_t)sp * nblk * TILE);
+      }
     if (t == 0) cnt[tile] = 0;
   }
 
