@@ -13,7 +13,8 @@ conv MFMA util %"):
     from per-op hipEvent timing.
   * roofline: the implicit-GEMM conv kernel on the isolated-conv-sweep shape
     3x3 s1 256->256 @80x80, batch 32, timed with hipEvents on the
-    engine stream.
+    engine stream; `traffic` = HBM bytes per launch from the committed PMC pass
+    (profiles/conv_gemm_c1_traffic.json) when the autotuner picks the tile it measured.
   * cpu_baseline: the numpy fp32 per-op oracle (letterbox + every op + decode + NMS) for
     yolo11n batch 1 on this host's cores, bounded to ~15 s.
 
@@ -38,6 +39,18 @@ PEAK_HBM = 8.0e12         # MI355X HBM3E, B/s
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def measured_traffic(cfg):
+    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 PMC pass
+    (FETCH_SIZE and WRITE_SIZE scaled by a plain copy of known size), when this run's
+    autotuner picked the tile that pass measured; otherwise None."""
+    path = os.path.join(ROOT, "profiles", "conv_gemm_c1_traffic.json")
+    try:
+        rec = json.load(open(path))
+    except (OSError, ValueError):
+        return None
+    return int(rec["traffic_bytes"]) if rec.get("cfg") == cfg else None
 
 
 def conv_flops(eng, k):
@@ -268,7 +281,8 @@ def main():
     if conv:
         achieved = conv["flops"] / (conv["ms"] * 1e-3)
         line["roofline"] = {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": 2500.0,
-                            "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16, 4), "traffic": None,
+                            "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16, 4),
+                            "traffic": measured_traffic(conv["cfg"]),
                             "kernel": f"k_conv_gemm cfg {conv['cfg']}", "shape": conv["shape"],
                             "ms": round(conv["ms"], 4)}
     if cpu:
