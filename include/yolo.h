@@ -61,7 +61,10 @@ void yolo_preprocess_cls(void* h, const unsigned char* dev_bgr, int height, int 
 int yolo_get_cls(void* h, int slot, int* ids, float* probs, int k);
 /* engine/yolo.h:36-38 */
 void yolo_slot_geom(void* h, int slot, float* scale, int* top, int* left);
-/* engine/yolo.h:39-41 -- OBB models are rejected at load (no OBB kernels yet); returns 0. */
+/* engine/yolo.h:39-41 -- rotated boxes of an OBB handle in original-image coordinates
+ * (centre x, y and w, h divided by the letterbox scale, angle in radians unchanged, no
+ * clipping); returns the count written.  Returns 0 on detect/segment handles, and
+ * yolo_get returns 0 on OBB handles (the reference reads the wrong record stride there). */
 int yolo_get_obb(void* h, int slot, YoloObbDet* out, int cap);
 /* engine/yolo.h:42-43 */
 void yolo_mask_dim(void* h, int* ph, int* pw);

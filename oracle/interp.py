@@ -116,7 +116,7 @@ class Interp:
     def __init__(self, g: Graph, B: int = 1, round_fp16: bool = False):
         self.g, self.B, self.round_fp16 = g, B, round_fp16
         self.bufs = [np.zeros((B, H, W, C), F32) for (H, W, C) in g.bufs]
-        self.heads_in: list = []   # DECODE / DECODESEG inputs, in op order
+        self.heads_in: list = []   # DECODE / DECODESEG / DECODEOBB inputs, in op order
 
     def view(self, t: int) -> np.ndarray:
         b, coff, C = self.g.tens[t]
@@ -161,8 +161,9 @@ class Interp:
         if op.kind == "ATTN":
             self.write(op.out, attention(self.view(op.a), op.heads, op.kd, op.hd))
             return op.out
-        if op.kind in ("DECODE", "DECODESEG"):
-            coef = self.view(op.out).copy() if op.kind == "DECODESEG" else None
+        if op.kind in ("DECODE", "DECODESEG", "DECODEOBB"):
+            # DECODESEG: coef = mask coefficients; DECODEOBB: coef = angle view
+            coef = self.view(op.out).copy() if op.kind != "DECODE" else None
             self.heads_in.append((self.view(op.a).copy(), self.view(op.b).copy(), coef, op.stride))
             return None
         if op.kind == "MASKS":

@@ -23,6 +23,21 @@ nms             k_nms, engine/engine.cu:1048-1123: greedy, same-class only, supp
 masks           k_mask_assemble, engine/engine.cu:1125-1158 (coef . proto, half-open box
                 crop at proto scale, logit > 0).  Pinned by a hand-built case with a known
                 answer and by the crop/threshold invariants.
+decode_obb      k_decode_obb, engine/engine.cu:908-964 (theta = (sigmoid(t) - 0.25) * pi,
+                dist2rbox, record cx, cy, w, h, score, cls, theta).  Pinned by a float64
+                restatement of ultralytics dist2rbox as a rotation matrix
+                (docs/specs/obb.md:116-128), theta = pi/4 at logit 0, and the axis-aligned
+                case reducing to the detect decode.
+covariance,     probiou (engine/engine.cu:1160-1176, ultralytics batch_probiou with its eps
+probiou         placement).  Pinned by the Bhattacharyya distance between two Gaussians
+                computed in float64 with numpy.linalg (det, inv) from R diag(w^2/12, h^2/12)
+                R^T, rotation invariance, theta ~ theta + pi, (w, h, theta) ~ (h, w,
+                theta + pi/2), identical boxes (bd clamped at eps) and far boxes (clamped
+                at 100).
+nms_obb         k_nms_obb, engine/engine.cu:1178-1252: ultralytics fast-NMS (a suppressed
+                box still suppresses; iou >= thr; same class only).  Ranked and capped by
+                the same total order as nms.  Pinned by brute force on tiny sets, a chain
+                case where fast-NMS and greedy NMS differ, and the >= tie.
 """
 from __future__ import annotations
 
@@ -179,6 +194,111 @@ def detect(heads, nc: int, conf: float = 0.25, iou: float = 0.45, max_det: int =
     """decode + NMS for one image -> dict with arrays in survivor order."""
     c = decode_all(heads, nc, conf)
     keep, n_raw = nms(c, iou, max_det, cap)
+    out = {k: v[keep] for k, v in c.items()}
+    out["n_raw"] = n_raw
+    return out
+
+
+# ----------------------------------------------------------------------------- OBB
+PI32 = F32(3.14159265358979)
+EPS = F32(1e-7)
+
+
+def decode_obb(box: np.ndarray, cls: np.ndarray, ang: np.ndarray, nc: int, stride: int,
+               conf: float, anchor_base: int = 0):
+    """One image, one level.  box [H,W,64], cls [H,W,ncpad], ang [H,W,>=1] (channel 0 real).
+    Returns per-candidate arrays in anchor order; rbox = (cx, cy, w, h) in net pixels."""
+    H, W, _ = box.shape
+    logits = cls[..., :nc].astype(F32).reshape(H * W, nc)
+    best = logits.max(axis=1)
+    bcls = logits.argmax(axis=1)
+    score = (F32(1.0) / (F32(1.0) + np.exp(-best))).astype(F32)
+    idx = np.nonzero(score >= F32(conf))[0]
+    d = dfl(box.astype(F32).reshape(H * W, 4, 16)[idx])
+    t0 = ang[..., 0].astype(F32).reshape(H * W)[idx]
+    th = ((F32(1.0) / (F32(1.0) + np.exp(-t0))).astype(F32) - F32(0.25)) * PI32
+    th = th.astype(F32)
+    xf = (d[:, 2] - d[:, 0]) * F32(0.5)
+    yf = (d[:, 3] - d[:, 1]) * F32(0.5)
+    cs, sn = np.cos(th), np.sin(th)
+    yy, xx = idx // W, idx % W
+    ax = xx.astype(F32) + F32(0.5)
+    ay = yy.astype(F32) + F32(0.5)
+    st = F32(stride)
+    cx = ((ax + xf * cs) - yf * sn) * st
+    cy = ((ay + xf * sn) + yf * cs) * st
+    rbox = np.stack([cx, cy, (d[:, 0] + d[:, 2]) * st, (d[:, 1] + d[:, 3]) * st], 1).astype(F32)
+    return {"anchor": (idx + anchor_base).astype(np.int64), "rbox": rbox, "theta": th,
+            "score": score[idx], "cls": bcls[idx].astype(np.int64)}
+
+
+def decode_obb_all(heads, nc: int, conf: float):
+    """heads: list of (box, cls, ang, stride) for ONE image, levels in op order."""
+    parts, base = [], 0
+    for box, cls, ang, st in heads:
+        parts.append(decode_obb(box, cls, ang, nc, st, conf, base))
+        base += box.shape[0] * box.shape[1]
+    return {k: np.concatenate([p[k] for p in parts]) for k in parts[0]}
+
+
+def covariance(w: np.ndarray, h: np.ndarray, th: np.ndarray):
+    """(A, B, C) of the Gaussian of a w x h box rotated by th; covariance [[A, C], [C, B]]."""
+    w, h, th = (np.asarray(v, F32) for v in (w, h, th))
+    a = (w * w) * F32(1.0 / 12.0)
+    b = (h * h) * F32(1.0 / 12.0)
+    cs, sn = np.cos(th), np.sin(th)
+    A = ((a * cs) * cs + (b * sn) * sn).astype(F32)
+    B = ((a * sn) * sn + (b * cs) * cs).astype(F32)
+    C = (((a - b) * cs) * sn).astype(F32)
+    return A, B, C
+
+
+def probiou(x1, y1, A1, B1, C1, x2, y2, A2, B2, C2) -> np.ndarray:
+    """probiou of box 1 vs box 2 (broadcasting fp32 arrays), the reference's operation order."""
+    dx = (x1 - x2).astype(F32)
+    dy = (y1 - y2).astype(F32)
+    sA = (A1 + A2).astype(F32)
+    sB = (B1 + B2).astype(F32)
+    sC = (C1 + C2).astype(F32)
+    disc = (sA * sB - sC * sC).astype(F32)
+    den = disc + EPS
+    t1 = (F32(0.25) * ((sA * dy) * dy + (sB * dx) * dx)) / den
+    t2 = (F32(0.5) * ((sC * (-dx)) * dy)) / den
+    det1 = np.maximum(A1 * B1 - C1 * C1, F32(0.0)).astype(F32)
+    det2 = np.maximum(A2 * B2 - C2 * C2, F32(0.0)).astype(F32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        t3 = F32(0.5) * np.log(disc / (F32(4.0) * np.sqrt(det1 * det2) + EPS) + EPS)
+    bd = np.minimum(np.maximum((t1 + t2) + t3, EPS), F32(100.0)).astype(F32)
+    return (F32(1.0) - np.sqrt((F32(1.0) - np.exp(-bd)) + EPS)).astype(F32)
+
+
+def nms_obb(c: dict, iou_thr: float, max_det: int = 300, cap: int = 2048):
+    """Fast-NMS over decoded OBB candidates c (dict from decode_obb_all): rank j is dropped
+    iff a higher rank of its class has probiou >= thr with it.  Returns (indices into c of
+    the survivors in output order, n_raw)."""
+    n_raw = len(c["score"])
+    order = rank_order(c["score"], c["anchor"])[:cap]
+    rb, th, cl = c["rbox"][order], c["theta"][order], c["cls"][order]
+    A, B, C = covariance(rb[:, 2], rb[:, 3], th)
+    thr = F32(iou_thr)
+    dead = np.zeros(len(order), bool)
+    for k in np.unique(cl):
+        mem = np.nonzero(cl == k)[0]               # rank order within the class
+        if len(mem) < 2:
+            continue
+        i, j = mem[:, None], mem[None, :]
+        iou = probiou(rb[i, 0], rb[i, 1], A[i], B[i], C[i], rb[j, 0], rb[j, 1], A[j], B[j], C[j])
+        hit = np.triu(iou >= thr, 1)               # [earlier, later]
+        dead[mem] = hit.any(axis=0)
+    keep = order[~dead][:max_det]
+    return np.asarray(keep, np.int64), n_raw
+
+
+def detect_obb(heads, nc: int, conf: float = 0.25, iou: float = 0.45, max_det: int = 300,
+               cap: int = 2048):
+    """decode_obb + fast-NMS for one image -> dict with arrays in survivor order."""
+    c = decode_obb_all(heads, nc, conf)
+    keep, n_raw = nms_obb(c, iou, max_det, cap)
     out = {k: v[keep] for k, v in c.items()}
     out["n_raw"] = n_raw
     return out

@@ -22,11 +22,11 @@ def models(tmp_path_factory):
     base = tmp_path_factory.mktemp("models")
     cache = {}
 
-    def get(arch="yolo11", scale="n", task="detect", cls_bias=-8.0, imgsz=640, seed=0):
-        key = (arch, scale, task, cls_bias, imgsz, seed)
+    def get(arch="yolo11", scale="n", task="detect", cls_bias=-8.0, imgsz=640, seed=0, nc=80):
+        key = (arch, scale, task, cls_bias, imgsz, seed, nc)
         if key not in cache:
             d = str(base / "_".join(str(k) for k in key))
-            modelgen.write_model(d, arch, scale, task, 80, imgsz, seed, cls_bias)
+            modelgen.write_model(d, arch, scale, task, nc, imgsz, seed, cls_bias)
             cache[key] = d
         return cache[key]
 

@@ -64,6 +64,21 @@ def test_graph_check_rejects(models, tmp_path, name, fn, msg):
     assert n == -1 and msg in err, err
 
 
+def test_graph_check_obb(models, tmp_path):
+    """yolo11n-obb at 1024: 118 ops + 3 DECODEOBB; DECODEOBB outside an obb graph and a
+    DECODE inside one are rejected."""
+    d = models("yolo11", "n", "obb", -6.25, 1024, 0, 15)
+    n, err = yolort.graph_check(d)
+    assert n == 121, err
+    bad = _mutate(d, str(tmp_path / "obbtask"), lambda L: [L[0], "TASK detect 15 1024"] + L[2:])
+    n, err = yolort.graph_check(bad)
+    assert n == -1 and "DECODEOBB needs task=obb" in err, err
+    bad = _mutate(d, str(tmp_path / "obbdec"), lambda L: [
+        " ".join(["DECODE"] + l.split()[1:3] + l.split()[4:]) if l.startswith("DECODEOBB") else l for l in L])
+    n, err = yolort.graph_check(bad)
+    assert n == -1 and "obb graphs decode with DECODEOBB" in err, err
+
+
 def test_graph_check_missing_dir(tmp_path):
     n, err = yolort.graph_check(str(tmp_path / "nope"))
     assert n == -1 and "model.graph" in err

@@ -72,6 +72,31 @@ def test_head_widths(scale, npr, c4, c2, c3):
     assert cls_conv[8] == c3 and cls_conv[9] == 80
 
 
+@pytest.mark.parametrize("scale,c3,c4", [("n", 64, 16), ("s", 128, 32), ("m", 256, 64)])
+def test_obb_head(scale, c3, c4):
+    """docs/specs/obb.md:13-61: layers 0..22 as detect, 11 head convs per level (cv2 3, cv3
+    5, cv4 3), c2 = 64, c3 = max(ch0, min(nc, 100)), c4 = max(ch0 // 4, ne); cls padded to
+    16 and angle to 8 channels; 16384 + 4096 + 1024 = 21504 anchors at 1024."""
+    g = modelgen.build_model("yolo11", scale, task="obb", nc=15, imgsz=1024, calibrate=False).graph
+    det = modelgen.build_model("yolo11", scale, calibrate=False).graph
+    dec = [op for op in g.ops if op[0] == "DECODEOBB"]
+    assert len(dec) == 3 and not [op for op in g.ops if op[0] == "DECODE"]
+    n_conv = sum(op[0] == "CONV" for op in g.ops)
+    assert n_conv == sum(op[0] == "CONV" for op in det.ops) + 9     # + cv4: 3 per level
+    shapes = [g.shape(op[1]) for op in dec]
+    assert [(h, w) for h, w, _ in shapes] == [(128, 128), (64, 64), (32, 32)]
+    assert sum(h * w for h, w, _ in shapes) == 21504
+    convs = [op for op in g.ops if op[0] == "CONV"]
+    for _, box, cls, ang, st in dec:
+        assert g.shape(box)[2] == 64 and g.shape(cls)[2] == 16 and g.shape(ang)[2] == 8
+        cls_conv = [o for o in convs if o[2] == cls][0]
+        ang_conv = [o for o in convs if o[2] == ang][0]
+        assert cls_conv[8] == c3 and ang_conv[8] == c4 and ang_conv[3] == 1
+    # the body (everything before the head's 3 x (8 convs + decode)) is the detect graph's
+    body = len(det.ops) - 27
+    assert [op[:1] + op[3:10] for op in g.ops[:body]] == [op[:1] + op[3:10] for op in det.ops[:body]]
+
+
 def test_files_roundtrip(tmp_path):
     d = str(tmp_path / "n")
     info = modelgen.write_model(d, "yolo11", "n", calibrate=False) if False else \

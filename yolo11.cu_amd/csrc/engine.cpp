@@ -67,7 +67,7 @@ struct Engine {
   float* cand = nullptr;
   int* nmsCount = nullptr;            // per-image decode list length (NMS re-arms it)
   unsigned long long* nmsScratch = nullptr;
-  // results: [outcnt B][rawcnt B] then (256-aligned) outdets B*MAX_OUT*6 in one block, so
+  // results: [outcnt B][rawcnt B] then (256-aligned) outdets B*MAX_OUT*outK in one block, so
   // one copy brings everything the host reads back
   void* results = nullptr;
   size_t detOff = 0;
@@ -176,9 +176,10 @@ struct Engine {
         case ADD: add(at, op.a, false); add(at, op.b, false); add(at, op.out, true); break;
         case DECODE:
         case DECODESEG:
+        case DECODEOBB:
           if (k == lastDecode)
             for (const OpDesc& d : ops)
-              if (d.kind == DECODE || d.kind == DECODESEG) { add(k, d.a, false); add(k, d.b, false); add(k, d.out, false); }
+              if (isDecode(d.kind)) { add(k, d.a, false); add(k, d.b, false); add(k, d.out, false); }
           break;
         case MASKS: break;
         default: add(at, op.a, false); add(at, op.out, true); break;
@@ -304,7 +305,7 @@ struct Engine {
         if (!convGemmFits((long)B * xb.H * xb.W * xb.C * 2, (long)op.Cout * op.k * op.k * op.Cin * 2))
           throw Failure(fmt("op %zu: conv input or weights reach 2 GiB at batch %d", i, B));
       }
-      if (op.kind == DECODE || op.kind == DECODESEG) lastDecode = (int)i;
+      if (isDecode(op.kind)) lastDecode = (int)i;
     }
     // weights: read, check ranges, repack depthwise [C][k*k] -> [k*k][C]
     std::vector<char> wf, bf;
@@ -350,7 +351,7 @@ struct Engine {
     HCK(hipMemset(nmsCount, 0, (size_t)B * sizeof(int)));
     HCK(hipMalloc(&nmsScratch, (size_t)B * nmsScratchBytes(A)));
     detOff = ((size_t)2 * B * sizeof(int) + 255) & ~(size_t)255;
-    const size_t resBytes = detOff + (size_t)B * MAX_OUT * 6 * sizeof(float);
+    const size_t resBytes = detOff + (size_t)B * MAX_OUT * g.outK * sizeof(float);
     HCK(hipMalloc(&results, resBytes));
     HCK(hipMemset(results, 0, resBytes));
     outcnt = (int*)results;
@@ -375,11 +376,11 @@ struct Engine {
     dec = DecodeArgs{};
     int base = 0;
     for (const OpDesc& op : ops) {
-      if (op.kind != DECODE && op.kind != DECODESEG) continue;
+      if (!isDecode(op.kind)) continue;
       DecodeLevel& L = dec.lv[dec.nlev++];
       L.box = view(op.a);
       L.cls = view(op.b);
-      L.coef = op.kind == DECODESEG ? view(op.out) : View{nullptr, 0, 0, 0, 0, 0};
+      L.coef = op.kind != DECODE ? view(op.out) : View{nullptr, 0, 0, 0, 0, 0};
       L.H = L.box.H;
       L.W = L.box.W;
       L.stride = op.stride;
@@ -389,6 +390,7 @@ struct Engine {
     dec.A = A;
     dec.nc = g.nc;
     dec.nm = g.seg ? g.nm : 0;
+    dec.obb = g.obb ? 1 : 0;
     slots.assign(B, SlotGeom{});
     HCK(hipDeviceSynchronize());
   }
@@ -428,6 +430,7 @@ struct Engine {
       case ATTN: launchAttention(view(op.a), view(op.out), op.heads, op.kd, op.hd, Bn, s); break;
       case DECODE:
       case DECODESEG:
+      case DECODEOBB:
         // all levels decode in one launch, issued at the last DECODE op (every head
         // tensor is final by then)
         if (k == lastDecode) launchDecode(dec, cand, nmsScratch, nmsCount, params, Bn, s);
@@ -438,13 +441,16 @@ struct Engine {
 
   void post(int Bn) {
     if (g.numAnchors == 0) return;   // no detection head (single-op graphs)
-    launchNms(cand, nmsScratch, nmsCount, g.numAnchors, cstride, outdets, outidx, outcnt, rawcnt, params, Bn, st);
+    if (g.obb)
+      launchNmsObb(cand, nmsScratch, nmsCount, g.numAnchors, outdets, outidx, outcnt, rawcnt, params, Bn, st);
+    else
+      launchNms(cand, nmsScratch, nmsCount, g.numAnchors, cstride, outdets, outidx, outcnt, rawcnt, params, Bn, st);
     if (g.protoTen >= 0) {
       View pr = view(g.protoTen);
       launchMasks(pr, cand, cstride, g.numAnchors, g.nm, outidx, outcnt, outdets, masks,
                   (float)pr.W / g.bufs[g.tens[0].buf].W, (float)pr.H / g.bufs[g.tens[0].buf].H, Bn, st);
     }
-    HCK(hipMemcpyAsync(h_results, results, detOff + (size_t)Bn * MAX_OUT * 6 * sizeof(float),
+    HCK(hipMemcpyAsync(h_results, results, detOff + (size_t)Bn * MAX_OUT * g.outK * sizeof(float),
                        hipMemcpyDeviceToHost, st));
   }
 
@@ -818,7 +824,7 @@ int yolo_graph_check(const char* model_dir, char* err, int errlen) {
   return (int)g.ops.size();
 }
 
-int yolo_task(void* h) { return E(h)->g.seg ? 3 : 0; }
+int yolo_task(void* h) { return E(h)->g.seg ? 3 : (E(h)->g.obb ? 1 : 0); }
 
 float yolo_exec_ms(void* h, int B) {
   Engine* e = E(h);
@@ -871,7 +877,7 @@ void yolo_sync(void* h) {
 
 int yolo_get(void* h, int slot, YoloDet* out, int cap) {
   Engine* e = E(h);
-  if (slot < 0 || slot >= e->B) return 0;
+  if (slot < 0 || slot >= e->B || e->g.obb) return 0;   // OBB records: yolo_get_obb
   const yolo::SlotGeom& sm = e->slots[slot];
   int cnt = std::min(e->h_cnt[slot], cap);
   for (int i = 0; i < cnt; i++) {
@@ -899,9 +905,19 @@ void yolo_slot_geom(void* h, int slot, float* scale, int* top, int* left) {
   *left = e->slots[slot].left;
 }
 
+// Rotated boxes in original-image coordinates: centre un-padded, centre and size divided by
+// the letterbox scale, angle unchanged, no clipping (engine/engine.cu:1783-1794).
 int yolo_get_obb(void* h, int slot, YoloObbDet* out, int cap) {
-  (void)h; (void)slot; (void)out; (void)cap;
-  return 0;
+  Engine* e = E(h);
+  if (slot < 0 || slot >= e->B || !e->g.obb) return 0;
+  const yolo::SlotGeom& sm = e->slots[slot];
+  int cnt = std::min(e->h_cnt[slot], cap);
+  for (int i = 0; i < cnt; i++) {
+    const float* d = e->h_out + ((size_t)slot * yolo::MAX_OUT + i) * 7;
+    out[i] = YoloObbDet{(d[0] - sm.left) / sm.scale, (d[1] - sm.top) / sm.scale, d[2] / sm.scale,
+                        d[3] / sm.scale, d[6], d[4], (int)d[5]};
+  }
+  return cnt;
 }
 
 void yolo_mask_dim(void* h, int* ph, int* pw) {

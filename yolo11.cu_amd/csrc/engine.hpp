@@ -15,6 +15,8 @@ typedef _Float16 f16;
 enum OpKind { CONV = 0, ADD, MAXPOOL5, UPSAMPLE2, COPYC, ATTN, DECODE, GAP, SOFTMAX, DECODEOBB,
               PS2, DECODESEG, MASKS };
 
+inline bool isDecode(int kind) { return kind == DECODE || kind == DECODESEG || kind == DECODEOBB; }
+
 struct BufDesc { int H, W, C; };
 struct TenDesc { int buf, coff, C; };
 struct OpDesc {
@@ -39,9 +41,10 @@ struct GraphDesc {
   std::vector<TenDesc> tens;
   std::vector<OpDesc> ops;
   // derived by validate()
-  bool seg = false;
+  bool seg = false, obb = false;
   int nm = 0, protoTen = -1;
   int detStride = 6;                  // floats per candidate record
+  int outK = 6;                       // floats per output record (OBB 7)
   int numAnchors = 0;                 // sum of H*W over the DECODE levels
 };
 
@@ -80,8 +83,8 @@ struct DecodeLevel {
   int H, W, stride, base;             // base = first anchor index of the level
 };
 struct DecodeArgs {
-  DecodeLevel lv[3];
-  int nlev, A, nc, nm;
+  DecodeLevel lv[3];                  // OBB: coef is the angle view (channel 0 real)
+  int nlev, A, nc, nm, obb;
 };
 
 // ------------------------------------------------------------------ GEMM tile configs
@@ -134,6 +137,11 @@ void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lists, i
 void launchNms(const float* cand, unsigned long long* lists, int* counts, int A, int cstride,
                float* out, int* outidx, int* outcnt, int* rawcnt, const PostParams* prm, int Bn,
                hipStream_t st);
+// Rotated NMS over 7-float OBB records (cx, cy, w, h, score, cls, theta); output records
+// have the same layout.
+void launchNmsObb(const float* cand, unsigned long long* lists, int* counts, int A, float* out,
+                  int* outidx, int* outcnt, int* rawcnt, const PostParams* prm, int Bn,
+                  hipStream_t st);
 void launchMasks(const View& proto, const float* cand, int cstride, int A, int nm,
                  const int* outidx, const int* outcnt, const float* outdets, uint8_t* masks,
                  float rx, float ry, int Bn, hipStream_t st);

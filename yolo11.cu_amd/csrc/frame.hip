@@ -54,10 +54,9 @@ void launchPreprocess(const uint8_t* src, int sh, int sw, f16* dst, int dh, int 
 // One thread per anchor over all levels of all images (one launch instead of one per
 // level).  Per anchor (k_decode, engine/engine.cu:844-906): first-max argmax over the nc
 // real classes (pad logits excluded), score = sigmoid(best), keep if score >= conf, DFL
-// expectation per side, xyxy = (x + 0.5 -+ d) * stride.  Instead of an atomic slot
-// counter, every anchor owns slot `anchor` of the candidate array and writes its score
-// (or -1) to keys[anchor]; NMS compacts in anchor order, so results do not depend on
-// thread scheduling.
+// expectation per side, xyxy = (x + 0.5 -+ d) * stride.  Every anchor owns record
+// `anchor` of the candidate array; survivors append a packed (score, anchor) key to the
+// image's list, which NMS ranks, so results do not depend on thread scheduling.
 __device__ __forceinline__ unsigned long long packKey(float score, int anchor) {
   return ((unsigned long long)__float_as_uint(score) << 32) | (unsigned)(0xFFFFFFFFu - (unsigned)anchor);
 }
@@ -69,6 +68,10 @@ __device__ __forceinline__ int keyAnchor(unsigned long long k) {
 // grid (anchor blocks, images): a wave never spans two images, so the survivors of a wave
 // are appended to the image's candidate list with one atomic (wave-aggregated).  The list
 // order depends on arrival; NMS sorts by key, so results do not.
+// OBB (k_decode_obb, engine/engine.cu:908-964): the angle view (channel 0 real) gives
+// theta = (sigmoid(t) - 0.25) * pi, the DFL distances are rotated by theta about the anchor
+// (dist2rbox), w = l + r, h = t + b, and the record is cx, cy, w, h, score, cls, theta.
+template <bool OBB>
 __global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict__ cand,
                                                 unsigned long long* __restrict__ lst,
                                                 int* __restrict__ count,
@@ -140,6 +143,20 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict_
   }
   const float cx = (float)xx + 0.5f, cy = (float)yy + 0.5f, st = (float)L.stride;
   float* o = cand + (size_t)idx * cstride;
+  if (OBB) {
+    const float t0 = (float)L.coef.p[pix * L.coef.s + L.coef.o];
+    const float th = (1.f / (1.f + expf(-t0)) - 0.25f) * 3.14159265358979f;
+    const float xf = (d[2] - d[0]) * 0.5f, yf = (d[3] - d[1]) * 0.5f;
+    const float cs = cosf(th), sn = sinf(th);
+    o[0] = (cx + xf * cs - yf * sn) * st;
+    o[1] = (cy + xf * sn + yf * cs) * st;
+    o[2] = (d[0] + d[2]) * st;
+    o[3] = (d[1] + d[3]) * st;
+    o[4] = score;
+    o[5] = (float)bcls;
+    o[6] = th;
+    return;
+  }
   o[0] = (cx - d[0]) * st;
   o[1] = (cy - d[1]) * st;
   o[2] = (cx + d[2]) * st;
@@ -158,7 +175,11 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict_
 
 void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lst, int* count,
                   const PostParams* prm, int Bn, hipStream_t st) {
-  k_decode<<<dim3((a.A + 255) / 256, Bn), 256, 0, st>>>(a, cand, lst, count, prm, 6 + a.nm);
+  const dim3 grid((a.A + 255) / 256, Bn);
+  if (a.obb)
+    k_decode<true><<<grid, 256, 0, st>>>(a, cand, lst, count, prm, 7);
+  else
+    k_decode<false><<<grid, 256, 0, st>>>(a, cand, lst, count, prm, 6 + a.nm);
 }
 
 // ------------------------------------------------------------------ NMS
@@ -198,46 +219,34 @@ __device__ __forceinline__ bool suppresses(float4 a, float4 b, float thr) {
   return inter / ua > thr;
 }
 
-__global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ cand,
-                                                     unsigned long long* __restrict__ lists,
-                                                     int* __restrict__ counts, int A, int cstride,
-                                                     float* __restrict__ out,
-                                                     int* __restrict__ outidx, int* __restrict__ outcnt,
-                                                     int* __restrict__ rawcnt,
-                                                     const PostParams* __restrict__ prm) {
-  __shared__ unsigned long long skey[NMS_CAP];
-  __shared__ float4 sbox[NMS_CAP];
-  __shared__ short scls[NMS_CAP];
-  __shared__ int chist[NMS_CLASSES];
-  __shared__ short present[NMS_CLASSES];
-  __shared__ int npresent, maxClass, wsum[NMS_THREADS / 64];
-  __shared__ unsigned removed[NMS_CAP / 32];
-  __shared__ unsigned long long rows[64];
-  __shared__ short kept[64];
-  __shared__ int hist[256];
-  __shared__ unsigned long long keptmask, selPrefix;
-  __shared__ int nout, selNeed, selCount, nkept;
+// Selection + ranking shared by both NMS kernels.  Leaves the m = min(n, NMS_CAP) largest
+// keys of lst[0..n) in descending order in sorted[0..m):
+//  - above NMS_CAP candidates a radix select keeps the NMS_CAP largest keys (8 passes of
+//    8-bit histograms from the top byte; keys are unique, so exactly NMS_CAP are >= T).
+//    Scores crowd into few bins, so lanes of a wave that share a bin add once
+//    (wave-aggregated atomics) instead of serialising on one LDS address;
+//  - rank = number of strictly larger keys.  Up to 1024 keys, TPK threads (adjacent lanes)
+//    share a key's scan and add their counts with shuffles; above that every thread ranks
+//    two keys.
+// `skey` (NMS_CAP keys) stages the selected keys and must not alias `sorted`.  Every thread
+// of the block calls it; it ends with a barrier.
+struct RankShared {
+  int hist[256];
+  unsigned long long prefix;
+  int need, count;
+};
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int img = blockIdx.x;
-  const float* cimg = cand + (size_t)img * A * cstride;
-  const unsigned long long* lst = lists + (size_t)img * A;
-  const float thr = prm->iou;
-  const int maxdet = min(prm->max_det, MAX_OUT);
-  const int n = min(counts[img], A);
+__device__ void selectAndRank(const unsigned long long* __restrict__ lst, int n,
+                              unsigned long long* skey, unsigned long long* sorted, RankShared& rs) {
+  const int tid = threadIdx.x, lane = tid & 63;
   const int m = min(n, NMS_CAP);
-
-  // 1a. more candidates than NMS_CAP: radix-select the NMS_CAP largest keys (8 passes of
-  //     8-bit histograms from the top byte; keys are unique, so exactly NMS_CAP are >= T).
-  //     Scores crowd into few bins, so lanes of a wave that share a bin add once
-  //     (wave-aggregated atomics) instead of serialising on one LDS address.
   if (n > NMS_CAP) {
-    if (tid == 0) { selPrefix = 0ull; selNeed = NMS_CAP; selCount = 0; }
+    if (tid == 0) { rs.prefix = 0ull; rs.need = NMS_CAP; rs.count = 0; }
     for (int p = 0; p < 8; p++) {
       const int shift = 56 - 8 * p;
-      for (int i = tid; i < 256; i += NMS_THREADS) hist[i] = 0;
+      for (int i = tid; i < 256; i += NMS_THREADS) rs.hist[i] = 0;
       __syncthreads();
-      const unsigned long long pre = selPrefix;
+      const unsigned long long pre = rs.prefix;
       for (int i0 = 0; i0 < n; i0 += NMS_THREADS) {
         const int i = i0 + tid;
         int bin = -1;
@@ -250,40 +259,32 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
           const int leader = __ffsll((long long)todo) - 1;
           const int lb = __shfl(bin, leader);
           const unsigned long long same = __ballot(bin == lb);
-          if (lane == leader) atomicAdd(&hist[lb], __popcll(same));
+          if (lane == leader) atomicAdd(&rs.hist[lb], __popcll(same));
           todo &= ~same;
         }
       }
       __syncthreads();
       if (tid == 0) {
-        int need = selNeed, cum = 0, sel = 0;
+        int need = rs.need, cum = 0, sel = 0;
         for (int b = 255; b >= 0; b--) {
-          if (cum + hist[b] >= need) { sel = b; need -= cum; break; }
-          cum += hist[b];
+          if (cum + rs.hist[b] >= need) { sel = b; need -= cum; break; }
+          cum += rs.hist[b];
         }
-        selNeed = need;
-        selPrefix = pre | ((unsigned long long)sel << shift);
+        rs.need = need;
+        rs.prefix = pre | ((unsigned long long)sel << shift);
       }
       __syncthreads();
     }
-    const unsigned long long T = selPrefix;
+    const unsigned long long T = rs.prefix;
     for (int i = tid; i < n; i += NMS_THREADS) {
       const unsigned long long k = lst[i];
-      if (k >= T) skey[atomicAdd(&selCount, 1)] = k;
+      if (k >= T) skey[atomicAdd(&rs.count, 1)] = k;
     }
   } else {
     for (int i = tid; i < n; i += NMS_THREADS) skey[i] = lst[i];
   }
-  if (tid == 0) nout = 0;
   __syncthreads();
-
-  // 1b. rank = number of strictly larger keys.  Up to 1024 keys, TPK threads (adjacent
-  //     lanes) share a key's scan and add their counts with shuffles; above that every
-  //     thread ranks two keys.  Sorted keys are parked in the box array's storage, then
-  //     every thread lifts its entries (and their candidate records) into registers before
-  //     the arrays are written for good.
-  static_assert(NMS_CAP == 2 * NMS_THREADS, "two sorted entries per thread");
-  unsigned long long* sorted = reinterpret_cast<unsigned long long*>(sbox);
+  static_assert(NMS_CAP == 2 * NMS_THREADS, "two ranked keys per thread");
   if (m <= NMS_THREADS) {
     int tpk = 1;
     while (tpk < 64 && m * tpk * 2 <= NMS_THREADS) tpk *= 2;
@@ -316,8 +317,44 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     sorted[r0] = k0;
     if (i1 < m) sorted[r1] = k1;
   }
-  for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) removed[i] = 0u;
   __syncthreads();
+}
+
+__global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ cand,
+                                                     unsigned long long* __restrict__ lists,
+                                                     int* __restrict__ counts, int A, int cstride,
+                                                     float* __restrict__ out,
+                                                     int* __restrict__ outidx, int* __restrict__ outcnt,
+                                                     int* __restrict__ rawcnt,
+                                                     const PostParams* __restrict__ prm) {
+  __shared__ unsigned long long skey[NMS_CAP];
+  __shared__ float4 sbox[NMS_CAP];
+  __shared__ short scls[NMS_CAP];
+  __shared__ int chist[NMS_CLASSES];
+  __shared__ short present[NMS_CLASSES];
+  __shared__ int npresent, maxClass, wsum[NMS_THREADS / 64];
+  __shared__ unsigned removed[NMS_CAP / 32];
+  __shared__ unsigned long long rows[64];
+  __shared__ short kept[64];
+  __shared__ RankShared rs;
+  __shared__ unsigned long long keptmask;
+  __shared__ int nout, nkept;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int img = blockIdx.x;
+  const float* cimg = cand + (size_t)img * A * cstride;
+  const float thr = prm->iou;
+  const int maxdet = min(prm->max_det, MAX_OUT);
+  const int n = min(counts[img], A);
+  const int m = min(n, NMS_CAP);
+  if (tid == 0) nout = 0;
+
+  // 1. the m best keys in rank order, parked in the box array's storage; every thread then
+  //    lifts its entries (and their candidate records) into registers before the arrays
+  //    are written for good
+  unsigned long long* sorted = reinterpret_cast<unsigned long long*>(sbox);
+  selectAndRank(lists + (size_t)img * A, n, skey, sorted, rs);
+  for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) removed[i] = 0u;
   unsigned long long kr[2] = {0ull, 0ull};
   float4 br[2];
   short cr[2] = {0, 0};
@@ -498,6 +535,158 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     rawcnt[img] = n;
     counts[img] = 0;   // re-arm the decode list for the next frame
   }
+}
+
+// ------------------------------------------------------------------ rotated NMS (OBB)
+// probiou of two rotated boxes as Gaussians (centre x, y; covariance [[A, C], [C, B]];
+// det = max(A*B - C*C, 0)): the ultralytics batch_probiou expression that k_nms_obb
+// evaluates (engine/engine.cu:1160-1176), eps 1e-7 in the t1/t2 denominator, in the t3
+// sqrt denominator and added to the log argument, bd clamped to [eps, 100].
+__device__ __forceinline__ float probiou(float2 p1, float4 g1, float det1, float2 p2, float4 g2,
+                                         float det2) {
+  const float eps = 1e-7f;
+  const float dx = p1.x - p2.x, dy = p1.y - p2.y;
+  const float sA = g1.x + g2.x, sB = g1.y + g2.y, sC = g1.z + g2.z;
+  const float disc = sA * sB - sC * sC;
+  const float den = disc + eps;
+  const float t1 = 0.25f * (sA * dy * dy + sB * dx * dx) / den;
+  const float t2 = 0.5f * (sC * (-dx) * dy) / den;
+  const float t3 = 0.5f * logf(disc / (4.f * sqrtf(det1 * det2) + eps) + eps);
+  const float bd = fminf(fmaxf(t1 + t2 + t3, eps), 100.f);
+  return 1.f - sqrtf(1.f - expf(-bd) + eps);
+}
+
+// One block (16 waves) per image.  ultralytics fast-NMS semantics, as k_nms_obb
+// (engine/engine.cu:1178-1252): candidate j is dropped iff some higher-ranked candidate
+// of its class, suppressed or not, has probiou >= thr with it.  There is no sequential
+// dependence, so every candidate is decided independently:
+//  1. selection + ranking by (score desc, anchor asc), as for detect;
+//  2. each thread owns ranks 2t, 2t+1: it loads their records and turns (w, h, theta) into
+//     the covariance terms once (a = w^2/12, b = h^2/12, A = a cos^2 + b sin^2,
+//     B = a sin^2 + b cos^2, C = (a - b) cos sin, engine/engine.cu:1199-1204);
+//  3. thread t decides ranks t and m-1-t (equal total scan length per thread), scanning
+//     the higher ranks of the same class and stopping at the first suppressor;
+//  4. survivors take output slots by a block prefix count in rank order (max_det cap).
+__global__ __launch_bounds__(NMS_THREADS) void k_nms_obb(const float* __restrict__ cand,
+                                                         unsigned long long* __restrict__ lists,
+                                                         int* __restrict__ counts, int A,
+                                                         float* __restrict__ out,
+                                                         int* __restrict__ outidx,
+                                                         int* __restrict__ outcnt,
+                                                         int* __restrict__ rawcnt,
+                                                         const PostParams* __restrict__ prm) {
+  // regionA: ranked keys during selection, then (A, B, C, class) per rank
+  // regionB: staged keys during selection, then (x, y) per rank
+  __shared__ float4 regionA[NMS_CAP];
+  __shared__ unsigned long long regionB[NMS_CAP];
+  __shared__ float sdet[NMS_CAP];
+  __shared__ unsigned dead[NMS_CAP / 32];
+  __shared__ RankShared rs;
+  __shared__ int wsum[NMS_THREADS / 64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int img = blockIdx.x;
+  const float* cimg = cand + (size_t)img * A * 7;
+  const float thr = prm->iou;
+  const int maxdet = min(prm->max_det, MAX_OUT);
+  const int n = min(counts[img], A);
+  const int m = min(n, NMS_CAP);
+
+  unsigned long long* sorted = reinterpret_cast<unsigned long long*>(regionA);
+  selectAndRank(lists + (size_t)img * A, n, regionB, sorted, rs);
+  for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) dead[i] = 0u;
+  unsigned long long kr[2] = {0ull, 0ull};
+  float4 gr[2];
+  float2 pr[2];
+  float dr[2];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int r = 2 * tid + u;
+    if (r < m) {
+      kr[u] = sorted[r];
+      const float* rec = cimg + (size_t)keyAnchor(kr[u]) * 7;
+      const float w = rec[2], h = rec[3], th = rec[6];
+      const float a = w * w * (1.f / 12.f), b = h * h * (1.f / 12.f);
+      const float cs = cosf(th), sn = sinf(th);
+      const float Aa = a * cs * cs + b * sn * sn;
+      const float Bb = a * sn * sn + b * cs * cs;
+      const float Cc = (a - b) * cs * sn;
+      gr[u] = make_float4(Aa, Bb, Cc, rec[5]);
+      pr[u] = make_float2(rec[0], rec[1]);
+      dr[u] = fmaxf(Aa * Bb - Cc * Cc, 0.f);
+    }
+  }
+  __syncthreads();
+  float2* sxy = reinterpret_cast<float2*>(regionB);
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int r = 2 * tid + u;
+    if (r < m) {
+      regionA[r] = gr[u];
+      sxy[r] = pr[u];
+      sdet[r] = dr[u];
+    }
+  }
+  __syncthreads();
+
+  // 3. fast-NMS decisions
+  if (2 * tid < m) {
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int j = u == 0 ? tid : m - 1 - tid;
+      if (u == 1 && j == tid) break;
+      const float4 gj = regionA[j];
+      const float2 pj = sxy[j];
+      const float dj = sdet[j];
+      for (int i = 0; i < j; i++) {
+        const float4 gi = regionA[i];
+        if (gi.w != gj.w) continue;
+        if (probiou(sxy[i], gi, sdet[i], pj, gj, dj) >= thr) {
+          atomicOr(&dead[j >> 5], 1u << (j & 31));
+          break;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // 4. output slots: exclusive prefix count of survivors in rank order (thread t owns
+  //    ranks 2t, 2t+1, whose keys it still holds)
+  const int r0 = 2 * tid, r1 = 2 * tid + 1;
+  const int f0 = r0 < m ? !((dead[r0 >> 5] >> (r0 & 31)) & 1u) : 0;
+  const int f1 = r1 < m ? !((dead[r1 >> 5] >> (r1 & 31)) & 1u) : 0;
+  const int v = f0 + f1;
+  int incl = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int off = 0;
+  for (int w = 0; w < wave; w++) off += wsum[w];
+  const int ex = off + incl - v;
+  auto emit = [&](unsigned long long key, int slot) {
+    const int an = keyAnchor(key);
+    const float* rec = cimg + (size_t)an * 7;
+    float* d = out + ((size_t)img * MAX_OUT + slot) * 7;
+#pragma unroll
+    for (int q = 0; q < 7; q++) d[q] = rec[q];
+    outidx[img * MAX_OUT + slot] = an;
+  };
+  if (f0 && ex < maxdet) emit(kr[0], ex);
+  if (f1 && ex + f0 < maxdet) emit(kr[1], ex + f0);
+  if (tid == NMS_THREADS - 1) {
+    outcnt[img] = min(off + incl, maxdet);
+    rawcnt[img] = n;
+    counts[img] = 0;   // re-arm the decode list for the next frame
+  }
+}
+
+void launchNmsObb(const float* cand, unsigned long long* lists, int* counts, int A, float* out,
+                  int* outidx, int* outcnt, int* rawcnt, const PostParams* prm, int Bn,
+                  hipStream_t st) {
+  k_nms_obb<<<Bn, NMS_THREADS, 0, st>>>(cand, lists, counts, A, out, outidx, outcnt, rawcnt, prm);
 }
 
 size_t nmsScratchBytes(int A) { return (size_t)A * sizeof(unsigned long long); }

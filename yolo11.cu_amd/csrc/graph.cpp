@@ -128,9 +128,9 @@ bool validateGraph(GraphDesc& g, std::string& err) {
   if (g.imgsz && (in.H != g.imgsz || in.W != g.imgsz)) return bad("imgsz header mismatch");
   if (g.tens[0].coff != 0) return bad("input tensor must start at channel 0 of its buffer");
   if (g.task == "classify") return bad("task classify is not supported by this engine");
-  if (g.task == "obb") return bad("task obb is not supported by this engine");
-  if (g.task != "detect" && g.task != "segment") return bad("unknown task " + g.task);
+  if (g.task != "detect" && g.task != "segment" && g.task != "obb") return bad("unknown task " + g.task);
   g.seg = g.task == "segment";
+  g.obb = g.task == "obb";
 
   int nlev = 0;
   g.numAnchors = 0;
@@ -197,7 +197,8 @@ bool validateGraph(GraphDesc& g, std::string& err) {
         break;
       }
       case DECODE:
-      case DECODESEG: {
+      case DECODESEG:
+      case DECODEOBB: {
         if (!tenOk(op.a) || !tenOk(op.b)) return bad(at + "tensor id out of range");
         Shape bx = shp(op.a), c = shp(op.b);
         if (bx.C != 64) return bad(at + "DECODE box view must have 64 channels (4 x reg_max 16)");
@@ -213,8 +214,14 @@ bool validateGraph(GraphDesc& g, std::string& err) {
           if (!tenOk(op.out)) return bad(at + "tensor id out of range");
           Shape m = shp(op.out);
           if (m.H != bx.H || m.W != bx.W || !al8(op.out)) return bad(at + "DECODESEG coef view");
-        } else if (g.seg) {
-          return bad(at + "segment graphs decode with DECODESEG");
+        } else if (op.kind == DECODEOBB) {
+          // engine/engine.cu:161-167: the angle view is %8-padded, channel 0 real
+          if (!g.obb) return bad(at + "DECODEOBB needs task=obb");
+          if (!tenOk(op.out)) return bad(at + "tensor id out of range");
+          Shape an = shp(op.out);
+          if (an.H != bx.H || an.W != bx.W || !al8(op.out)) return bad(at + "DECODEOBB angle view");
+        } else if (g.seg || g.obb) {
+          return bad(at + (g.seg ? "segment graphs decode with DECODESEG" : "obb graphs decode with DECODEOBB"));
         }
         if (op.stride <= 0) return bad(at + "bad stride");
         if (nlev == 3) return bad(at + "at most 3 detection levels");
@@ -230,7 +237,7 @@ bool validateGraph(GraphDesc& g, std::string& err) {
         break;
       }
       default:
-        return bad(at + "op kind not supported by this engine (GAP/SOFTMAX/DECODEOBB)");
+        return bad(at + "op kind not supported by this engine (GAP/SOFTMAX)");
     }
   }
   if (g.seg) {
@@ -239,7 +246,9 @@ bool validateGraph(GraphDesc& g, std::string& err) {
     for (const OpDesc& op : g.ops)
       if (op.kind == DECODESEG && shp(op.out).C != g.nm) return bad("DECODESEG coef count != proto channels");
   }
-  g.detStride = 6 + (g.seg ? g.nm : 0);
+  if (g.obb && g.protoTen >= 0) return bad("obb graphs carry no MASKS op");
+  g.detStride = g.obb ? 7 : 6 + (g.seg ? g.nm : 0);
+  g.outK = g.obb ? 7 : 6;
   return true;
 }
 

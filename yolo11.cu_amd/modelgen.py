@@ -454,7 +454,7 @@ def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc
                 calibrate: bool = True) -> ModelInfo:
     """Builds the flat op graph of a seeded random-init YOLO model (export/export.py:317-441)."""
     assert arch in SCALES and scale in SCALES[arch], (arch, scale)
-    assert task in ("detect", "segment"), task
+    assert task in ("detect", "segment", "obb"), task
     assert imgsz % 32 == 0
     depth, width, max_ch = SCALES[arch][scale]
     v11 = arch == "yolo11"
@@ -530,7 +530,7 @@ def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc
             y = g.ten(catbuf[i], 0, ch[i])
         outs[i] = y
 
-    # Detect / Segment head
+    # Detect / Segment / OBB head (export/export.py:400-438)
     feats_idx = HEAD_FROM[arch]
     feats = [outs[j] for j in feats_idx]
     chs = [ch[j] for j in feats_idx]
@@ -540,6 +540,8 @@ def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc
     c3h = max(chs[0], min(nc, 100))
     ncpad = ceil8(nc)
     seg = task == "segment"
+    obb = task == "obb"
+    c4o = max(chs[0] // 4, 1)            # OBB angle branch width, ne = 1 (docs/specs/obb.md:60-61)
     if seg:
         npr = ceil8(min(256, max_ch) * width)
         t = g.conv(feats[0], ConvSpec(chs[0], npr, 3))
@@ -565,6 +567,11 @@ def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc
             mc = g.conv(mc, ConvSpec(c4, c4, 3))
             mc = g.conv(mc, ConvSpec(c4, nm, 1, act=ACT_NONE, bn=False))
             g.ops.append(("DECODESEG", b, c, mc, st))
+        elif obb:
+            a = g.conv(f, ConvSpec(cx, c4o, 3))
+            a = g.conv(a, ConvSpec(c4o, c4o, 3))
+            a = g.conv_pad(a, ConvSpec(c4o, 1, 1, act=ACT_NONE, bn=False), 8)
+            g.ops.append(("DECODEOBB", b, c, a, st))
         else:
             g.ops.append(("DECODE", b, c, st))
     if seg:

@@ -251,6 +251,13 @@ class Engine:
         n = self.lib.yolo_get(self.h, slot, arr, cap)
         return np.array([(d.x1, d.y1, d.x2, d.y2, d.score, d.cls) for d in arr[:n]], np.float64).reshape(n, 6)
 
+    def get_obb(self, slot: int = 0, cap: int = MAX_OUT) -> np.ndarray:
+        """OBB survivors as rows (cx, cy, w, h, theta, score, cls) in original-image coords."""
+        arr = (YoloObbDet * cap)()
+        n = self.lib.yolo_get_obb(self.h, slot, arr, cap)
+        return np.array([(d.x, d.y, d.w, d.h, d.angle, d.score, d.cls) for d in arr[:n]],
+                        np.float64).reshape(n, 7)
+
     def raw_count(self, slot: int = 0) -> int:
         return self.lib.yolo_raw_count(self.h, slot)
 
