@@ -15,6 +15,9 @@ conv MFMA util %"):
     3x3 s1 256->256 @80x80, batch 32, timed with hipEvents on the
     engine stream; `traffic` = HBM bytes per launch from the committed PMC pass
     (profiles/conv_gemm_c1_traffic.json) when the autotuner picks the tile it measured.
+  * yolo11n-obb at 1024 (15 classes, 1024x1024 frame) and yolo11n-seg at 640, batch 1:
+    whole-frame graph, frame in HBM (side figures; the reference quotes 1.6 ms and 1.21 ms
+    on an RTX 3060 Ti, README.md:80-81).
   * cpu_baseline: the numpy fp32 per-op oracle (letterbox + every op + decode + NMS) for
     yolo11n batch 1 on this host's cores, bounded to ~15 s.
 
@@ -104,6 +107,42 @@ def bench_n(workdir, steps, warmup, graph=True):
     eng.close()
     return dict(ms=ms, graph_ms=graph_ms, ms_pcie=ms_pcie, kept=kept, raw=raw,
                 stream_ops_ms=float(per_op.sum()))
+
+
+def bench_task(workdir, task, imgsz, nc, cls_bias, frame, steps, warmup, graph=True):
+    """yolo11n of another task head at batch 1: the whole-frame graph (letterbox + net +
+    decode + NMS [+ masks] + result copy) with the raw frame in HBM, like bench_n."""
+    import modelgen
+    import yolort
+    d = os.path.join(workdir, f"yolo11n-{task}")
+    modelgen.write_model(d, "yolo11", "n", task, nc, imgsz, 0, cls_bias)
+    eng = yolort.Engine(d, 1, 0 if graph else yolort.YOLO_NOGRAPH)
+    dev = yolort.DeviceBuffer(frame.nbytes)
+    eng.upload(dev, frame)
+    h, w = frame.shape[:2]
+    get = eng.get_obb if task == "obb" else eng.get
+    if not graph:
+        for _ in range(warmup + steps):
+            eng.preprocess(dev.ptr, h, w, 0)
+            eng.run(1)
+            get(0)
+        dev.free()
+        eng.close()
+        return None
+    eng.frame_graph([dev.ptr], [h], [w])
+    for _ in range(warmup):
+        eng.frame_run()
+        get(0)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.frame_run()
+        dets = get(0)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    graph_ms = eng.time_graph(1, 1, max(steps, 50))
+    kept, raw = len(dets), eng.raw_count(0)
+    dev.free()
+    eng.close()
+    return dict(ms=ms, graph_ms=graph_ms, kept=kept, raw=raw)
 
 
 def bench_x(workdir, iters, graph=True):
@@ -221,7 +260,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "n", "x", "conv"], default="all")
+    ap.add_argument("--only", choices=["all", "n", "x", "conv", "obb", "seg"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the same kernels stream-ordered (rocprofv3's kernel tracer "
@@ -245,6 +284,18 @@ def main():
         log("yolo11x b16 ...")
         out["x"] = bench_x(workdir, 20, not args.no_graph)
         log(out["x"])
+    if args.only in ("all", "obb", "seg"):
+        import modelgen
+        if args.only in ("all", "obb"):
+            log("yolo11n-obb b1 @1024 e2e ...")
+            out["obb"] = bench_task(workdir, "obb", 1024, 15, -6.25, modelgen.synth_frame(1024, 1024, 50, 7),
+                                    args.steps, args.warmup, not args.no_graph)
+            log(out["obb"])
+        if args.only in ("all", "seg"):
+            log("yolo11n-seg b1 e2e ...")
+            out["seg"] = bench_task(workdir, "segment", 640, 80, -8.0, modelgen.synth_polygons(640, 640, 30, 4),
+                                    args.steps, args.warmup, not args.no_graph)
+            log(out["seg"])
     if args.no_graph:
         log("stream-ordered profiling pass done")
         return
@@ -278,6 +329,11 @@ def main():
                               "raw_candidates": n["raw"], "stream_ops_ms": round(n["stream_ops_ms"], 4)}
     if x:
         line["yolo11x_b16"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in x.items()}
+    for key, name in (("obb", "yolo11n_obb_b1_1024"), ("seg", "yolo11n_seg_b1")):
+        r = out.get(key)
+        if r:
+            line[name] = {"ms_per_frame": round(r["ms"], 4), "graph_ms": round(r["graph_ms"], 4),
+                          "kept": r["kept"], "raw_candidates": r["raw"]}
     if conv:
         achieved = conv["flops"] / (conv["ms"] * 1e-3)
         line["roofline"] = {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": 2500.0,

@@ -239,3 +239,42 @@ def test_decode_obb_special_cases():
     ctr = [(xyxy[0] + xyxy[2]) / 2, (xyxy[1] + xyxy[3]) / 2, xyxy[2] - xyxy[0], xyxy[3] - xyxy[1]]
     assert abs(float(r["theta"][0])) < 1e-3
     np.testing.assert_allclose(r["rbox"][0], ctr, rtol=0, atol=0.05)
+
+
+def test_far_pair_skip_bound():
+    """The device NMS skips a same-class pair without evaluating probiou when both boxes are
+    "bounded" (covariance determinant >= 1 and >= 1e-4 trace^2, i.e. condition number below
+    ~1e4) and |d|^2 > 8 B*(thr) (A1 + B1 + A2 + B2), with B*(thr) = -ln(1 + eps - (1 - thr)^2)
+    (for 0.05 <= thr <= 0.95).  Every pair so skipped must have fp32 probiou < thr: checked
+    just beyond the skip distance on random pairs and on sticks aligned with their offset
+    (where bd / |d|^2 is smallest and the fp32 cross term cancels most)."""
+    rng = np.random.default_rng(5)
+    checked = 0
+    for thr in (0.05, 0.3, 0.45, 0.7, 0.95):
+        t = F32(thr)
+        K = F32(8) * -np.log(F32(1) + F32(1e-7) - (F32(1) - t) * (F32(1) - t))
+        for trial in range(3000):
+            stick = trial % 2 == 0
+            if stick:
+                phi = rng.uniform(-math.pi, math.pi)
+                b = []
+                for _ in range(2):
+                    w = rng.uniform(20, 400)
+                    b.append((w, w / rng.uniform(10, 100), phi + rng.normal(0, 0.02)))
+                ang = phi
+            else:
+                b = [(rng.uniform(1, 200), rng.uniform(1, 200), rng.uniform(-1, 3)) for _ in range(2)]
+                ang = rng.uniform(-math.pi, math.pi)
+            cov = [post.covariance(F32(w), F32(h), F32(th)) for w, h, th in b]
+            dets = [max(A * B - C * C, 0) for A, B, C in cov]
+            if any(dt < 1 or dt < F32(1e-4) * (A + B) * (A + B) for dt, (A, B, C) in zip(dets, cov)):
+                continue
+            checked += 1
+            tr = (cov[0][0] + cov[1][0]) + (cov[0][1] + cov[1][1])
+            r = math.sqrt(float(K * tr) * (1 + rng.uniform(1e-6, 0.02)))
+            dx, dy = F32(r * math.cos(ang)), F32(r * math.sin(ang))
+            if not dx * dx + dy * dy > K * tr:
+                continue
+            v = post.probiou(dx, dy, *cov[0], F32(0), F32(0), *cov[1])
+            assert v < t, (thr, b, float(v))
+    assert checked > 10000

@@ -225,9 +225,10 @@ __device__ __forceinline__ bool suppresses(float4 a, float4 b, float thr) {
 //    8-bit histograms from the top byte; keys are unique, so exactly NMS_CAP are >= T).
 //    Scores crowd into few bins, so lanes of a wave that share a bin add once
 //    (wave-aggregated atomics) instead of serialising on one LDS address;
-//  - rank = number of strictly larger keys.  Up to 1024 keys, TPK threads (adjacent lanes)
-//    share a key's scan and add their counts with shuffles; above that every thread ranks
-//    two keys.
+//  - up to 512 keys: rank = number of strictly larger keys, TPK threads (adjacent lanes)
+//    sharing a key's scan and adding their counts with shuffles; above that a bitonic sort
+//    (descending) of the keys padded with zeros to 1024 or 2048 (log2(P)(log2(P)+1)/2
+//    compare-exchange steps instead of P^2 compares).
 // `skey` (NMS_CAP keys) stages the selected keys and must not alias `sorted`.  Every thread
 // of the block calls it; it ends with a barrier.
 struct RankShared {
@@ -284,8 +285,8 @@ __device__ void selectAndRank(const unsigned long long* __restrict__ lst, int n,
     for (int i = tid; i < n; i += NMS_THREADS) skey[i] = lst[i];
   }
   __syncthreads();
-  static_assert(NMS_CAP == 2 * NMS_THREADS, "two ranked keys per thread");
-  if (m <= NMS_THREADS) {
+  static_assert(NMS_CAP == 2 * NMS_THREADS, "one compare-exchange per thread and step");
+  if (m <= 512) {
     int tpk = 1;
     while (tpk < 64 && m * tpk * 2 <= NMS_THREADS) tpk *= 2;
     const int i = tid / tpk, part = tid - i * tpk;
@@ -306,16 +307,23 @@ __device__ void selectAndRank(const unsigned long long* __restrict__ lst, int n,
     for (int o = 1; o < tpk; o <<= 1) r += __shfl_xor(r, o);
     if (i < m && part == 0) sorted[r] = k;
   } else {
-    const int i0 = tid, i1 = tid + NMS_THREADS;
-    const unsigned long long k0 = skey[i0], k1 = i1 < m ? skey[i1] : ~0ull;
-    int r0 = 0, r1 = 0;
-    for (int j = 0; j < m; j++) {
-      const unsigned long long v = skey[j];
-      r0 += v > k0;
-      r1 += v > k1;
+    const int P = m > 1024 ? 2048 : 1024;
+    for (int i = m + tid; i < P; i += NMS_THREADS) skey[i] = 0ull;   // below every real key
+    __syncthreads();
+    for (int k = 2; k <= P; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        if (tid < P / 2) {
+          const int i = ((tid & ~(j - 1)) << 1) | (tid & (j - 1)), l = i + j;
+          const unsigned long long a = skey[i], b = skey[l];
+          if ((a < b) == ((i & k) == 0)) {   // descending where (i & k) == 0
+            skey[i] = b;
+            skey[l] = a;
+          }
+        }
+        __syncthreads();
+      }
     }
-    sorted[r0] = k0;
-    if (i1 < m) sorted[r1] = k1;
+    for (int r = tid; r < m; r += NMS_THREADS) sorted[r] = skey[r];
   }
   __syncthreads();
 }
@@ -564,9 +572,23 @@ __device__ __forceinline__ float probiou(float2 p1, float4 g1, float det1, float
 //  2. each thread owns ranks 2t, 2t+1: it loads their records and turns (w, h, theta) into
 //     the covariance terms once (a = w^2/12, b = h^2/12, A = a cos^2 + b sin^2,
 //     B = a sin^2 + b cos^2, C = (a - b) cos sin, engine/engine.cu:1199-1204);
-//  3. thread t decides ranks t and m-1-t (equal total scan length per thread), scanning
-//     the higher ranks of the same class and stopping at the first suppressor;
-//  4. survivors take output slots by a block prefix count in rank order (max_det cap).
+//  3. the ranks are grouped by class (a class histogram, its prefix sum, then one wave per
+//     class gathering the class's ranks in order with ballots), so the lanes of a wave
+//     decide candidates of one class and scan the same higher-ranked members together;
+//  4. lane p of a wave decides class-major position p; the wave walks the higher-ranked
+//     positions of its lanes' classes together and first applies a cheap exact bound: for
+//     covariances with determinant >= 1, bd >= |d|^2 / (4 trace(S1 + S2)), and iou >= thr
+//     needs bd <= B* = -ln(1 + eps - (1 - thr)^2), so |d|^2 > 8 B* trace (a factor-2
+//     margin) rules a pair out.  The bound is used for 0.05 <= thr <= 0.95 and for boxes
+//     whose covariance condition number is below ~1e4, where fp32 rounding of the full
+//     expression stays far inside that margin.  Pairs it cannot rule out go to a per-wave
+//     LDS queue; each 64 queued pairs are evaluated exactly, one pair per lane, so the
+//     transcendental path runs on full waves;
+//  5. survivors take output slots by a block prefix count in rank order (max_det cap).
+constexpr float OBB_DET_MIN = 1.f;
+constexpr float OBB_COND = 1e-4f;            // det >= OBB_COND * trace^2: condition < ~1e4
+constexpr int OBB_QUEUE = 128;               // per-wave queue of pairs for exact evaluation
+
 __global__ __launch_bounds__(NMS_THREADS) void k_nms_obb(const float* __restrict__ cand,
                                                          unsigned long long* __restrict__ lists,
                                                          int* __restrict__ counts, int A,
@@ -579,10 +601,16 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms_obb(const float* __restrict
   // regionB: staged keys during selection, then (x, y) per rank
   __shared__ float4 regionA[NMS_CAP];
   __shared__ unsigned long long regionB[NMS_CAP];
-  __shared__ float sdet[NMS_CAP];
+  __shared__ short perm[NMS_CAP];             // class-major position -> rank
+  __shared__ int cstart[NMS_CLASSES];         // class histogram, then its exclusive prefix
+  __shared__ short present[NMS_CLASSES];
   __shared__ unsigned dead[NMS_CAP / 32];
   __shared__ RankShared rs;
   __shared__ int wsum[NMS_THREADS / 64];
+  __shared__ int npresent;
+  __shared__ float4 ppos[NMS_CAP];            // class-major: x, y, trace (-1: no bound)
+  __shared__ unsigned queue[NMS_THREADS / 64][OBB_QUEUE];
+  static_assert(NMS_CLASSES == NMS_THREADS, "one class bin per thread");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int img = blockIdx.x;
@@ -591,14 +619,17 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms_obb(const float* __restrict
   const int maxdet = min(prm->max_det, MAX_OUT);
   const int n = min(counts[img], A);
   const int m = min(n, NMS_CAP);
+  const float bstar = (thr >= 0.05f && thr <= 0.95f) ? -logf(1.f + 1e-7f - (1.f - thr) * (1.f - thr)) : 0.f;
+  const float skipK = bstar > 0.f ? 8.f * bstar : INFINITY;
 
   unsigned long long* sorted = reinterpret_cast<unsigned long long*>(regionA);
   selectAndRank(lists + (size_t)img * A, n, regionB, sorted, rs);
   for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) dead[i] = 0u;
+  cstart[tid] = 0;
+  if (tid == 0) npresent = 0;
   unsigned long long kr[2] = {0ull, 0ull};
   float4 gr[2];
   float2 pr[2];
-  float dr[2];
 #pragma unroll
   for (int u = 0; u < 2; u++) {
     const int r = 2 * tid + u;
@@ -611,9 +642,9 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms_obb(const float* __restrict
       const float Aa = a * cs * cs + b * sn * sn;
       const float Bb = a * sn * sn + b * cs * cs;
       const float Cc = (a - b) * cs * sn;
-      gr[u] = make_float4(Aa, Bb, Cc, rec[5]);
+      const float cl = fminf(fmaxf(rec[5], 0.f), (float)(NMS_CLASSES - 1));
+      gr[u] = make_float4(Aa, Bb, Cc, cl);
       pr[u] = make_float2(rec[0], rec[1]);
-      dr[u] = fmaxf(Aa * Bb - Cc * Cc, 0.f);
     }
   }
   __syncthreads();
@@ -624,33 +655,103 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms_obb(const float* __restrict
     if (r < m) {
       regionA[r] = gr[u];
       sxy[r] = pr[u];
-      sdet[r] = dr[u];
+      atomicAdd(&cstart[(int)gr[u].w], 1);
+    }
+  }
+  __syncthreads();
+  // 3a. classes present and the exclusive prefix of the histogram (thread t owns class t)
+  {
+    const int h = cstart[tid];
+    if (h > 0) present[atomicAdd(&npresent, 1)] = (short)tid;
+    int incl = h;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int off = 0;
+    for (int w = 0; w < wave; w++) off += wsum[w];
+    cstart[tid] = off + incl - h;
+  }
+  __syncthreads();
+  // 3b. one wave per class: its ranks in order, appended with ballots (no atomics)
+  for (int pc = wave; pc < npresent; pc += NMS_THREADS / 64) {
+    const int c = present[pc];
+    const float cf = (float)c;
+    int g = cstart[c];
+    for (int i0 = 0; i0 < m; i0 += 64) {
+      const int r = i0 + lane;
+      const bool in = r < m && regionA[r].w == cf;
+      const unsigned long long bal = __ballot(in);
+      if (in) perm[g + __popcll(bal & ((1ull << lane) - 1ull))] = (short)r;
+      g += __popcll(bal);
     }
   }
   __syncthreads();
 
-  // 3. fast-NMS decisions
-  if (2 * tid < m) {
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const int j = u == 0 ? tid : m - 1 - tid;
-      if (u == 1 && j == tid) break;
-      const float4 gj = regionA[j];
-      const float2 pj = sxy[j];
-      const float dj = sdet[j];
-      for (int i = 0; i < j; i++) {
-        const float4 gi = regionA[i];
-        if (gi.w != gj.w) continue;
-        if (probiou(sxy[i], gi, sdet[i], pj, gj, dj) >= thr) {
-          atomicOr(&dead[j >> 5], 1u << (j & 31));
-          break;
+  // class-major copies of what the cheap bound reads
+  for (int p = tid; p < m; p += NMS_THREADS) {
+    const int r = perm[p];
+    const float4 g = regionA[r];
+    const float2 xy = sxy[r];
+    const float tr = g.x + g.y;
+    const float det = fmaxf(g.x * g.y - g.z * g.z, 0.f);
+    const bool bounded = det >= OBB_DET_MIN && det >= OBB_COND * tr * tr;
+    ppos[p] = make_float4(xy.x, xy.y, bounded ? tr : -1.f, 0.f);
+  }
+  __syncthreads();
+
+  // 4. fast-NMS decisions
+  unsigned* wq = queue[wave];
+  int qhead = 0, qtail = 0;                   // wave-uniform queue cursors
+  auto flush = [&](int cnt) {                 // exact probiou of the cnt (<= 64) oldest pairs
+    if (lane < cnt) {
+      const unsigned e = wq[(qhead + lane) & (OBB_QUEUE - 1)];
+      const int i = perm[e >> 16], j = perm[e & 0xFFFFu];
+      const float4 gi = regionA[i], gj = regionA[j];
+      const float di = fmaxf(gi.x * gi.y - gi.z * gi.z, 0.f);
+      const float dj = fmaxf(gj.x * gj.y - gj.z * gj.z, 0.f);
+      if (probiou(sxy[i], gi, di, sxy[j], gj, dj) >= thr) atomicOr(&dead[j >> 5], 1u << (j & 31));
+    }
+    qhead += cnt;
+  };
+  for (int base = wave * 64; base < m; base += NMS_THREADS) {
+    const int p = base + lane;
+    const bool valid = p < m;
+    const int j = valid ? perm[p] : 0;
+    const float4 me = valid ? ppos[p] : make_float4(0.f, 0.f, -1.f, 0.f);
+    const int s = valid ? cstart[(int)regionA[j].w] : 0x7fffffff;
+    bool alive = valid && s < p;              // has a higher-ranked member of its class
+    int lo = s, hi = valid ? p : 0;
+    for (int o = 32; o > 0; o >>= 1) {
+      lo = min(lo, __shfl_xor(lo, o));
+      hi = max(hi, __shfl_xor(hi, o));
+    }
+    float4 nxt = lo < hi ? ppos[lo] : make_float4(0.f, 0.f, -1.f, 0.f);
+    for (int q = lo; q < hi; q++) {
+      if (!__ballot(alive)) break;
+      const float4 oi = nxt;
+      if (q + 1 < hi) nxt = ppos[q + 1];      // next position's load overlaps this one's work
+      const float dx = oi.x - me.x, dy = oi.y - me.y;
+      const bool far = me.z > 0.f && oi.z > 0.f && dx * dx + dy * dy > skipK * (oi.z + me.z);
+      const bool need = alive && q >= s && !far;
+      const unsigned long long bal = __ballot(need);
+      if (bal) {
+        if (need) wq[(qtail + __popcll(bal & ((1ull << lane) - 1ull))) & (OBB_QUEUE - 1)] = ((unsigned)q << 16) | (unsigned)p;
+        qtail += __popcll(bal);
+        if (qtail - qhead >= 64) {
+          flush(64);
+          if (alive) alive = !((dead[j >> 5] >> (j & 31)) & 1u);
         }
       }
+      alive = alive && q + 1 < p;
     }
   }
+  flush(qtail - qhead);
   __syncthreads();
 
-  // 4. output slots: exclusive prefix count of survivors in rank order (thread t owns
+  // 5. output slots: exclusive prefix count of survivors in rank order (thread t owns
   //    ranks 2t, 2t+1, whose keys it still holds)
   const int r0 = 2 * tid, r1 = 2 * tid + 1;
   const int f0 = r0 < m ? !((dead[r0 >> 5] >> (r0 & 31)) & 1u) : 0;
