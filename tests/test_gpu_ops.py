@@ -276,3 +276,43 @@ def test_conv_first(tmp_path, cout):
     print(f"stem Cout {cout}: rel {rel:.2e}", flush=True)
     assert rel <= TOL
     eng.close()
+
+
+@pytest.mark.parametrize("ncls", [1, 12, 20, 80])
+def test_nms_paths_crafted_heads(models, ncls):
+    """Decode + NMS on crafted head tensors that drive each NMS path: one class (over 2048
+    candidates: radix select, then the 64-per-step blockwise path), 12 classes (~170 per
+    class: blockwise), 20 classes (50-120 per class: the per-class path with two chunks) and
+    80 classes (one chunk per class).  Exact: same raw count, survivors, order and classes
+    as the oracle."""
+    d = models("yolo11", "n")
+    g = graphfile.load(d)
+    eng = yolort.Engine(d, 1, yolort.YOLO_NOFUSE | yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    rng = np.random.default_rng(ncls)
+    dec = [(k, op) for k, op in enumerate(g.ops) if op.kind == "DECODE"]
+    heads = []
+    for _, op in dec:
+        H, W, C = eng.tensor_shape(op.b)
+        cls = np.full((1, H, W, C), -20.0, np.float32)
+        pick = rng.integers(0, ncls, (H, W))
+        cls[0, np.arange(H)[:, None], np.arange(W)[None, :], pick] = rng.uniform(-2.5, 4.0, (H, W))
+        box = rng.normal(0.0, 1.5, (1, H, W, 64)).astype(np.float32)
+        box[..., 2::16] += 2.0                 # mass near bin 2: boxes a few strides wide
+        eng.write(op.b, cls)
+        eng.write(op.a, box)
+        heads.append((box[0].astype(np.float16).astype(np.float32),
+                      cls[0].astype(np.float16).astype(np.float32), None, op.stride))
+    for conf, iou in ((0.25, 0.45), (0.95, 0.3)):
+        eng.set_thresholds(conf, iou, 300)
+        eng.run_op(dec[-1][0], 1)
+        eng.run_post(1)
+        want = post.detect(heads, 80, conf, iou)
+        got = eng.get(0)
+        print(f"{ncls} classes conf {conf}: raw {eng.raw_count(0)} / {want['n_raw']}, kept {len(got)} / "
+              f"{len(want['score'])}", flush=True)
+        assert eng.raw_count(0) == want["n_raw"]
+        assert len(got) == len(want["score"])
+        np.testing.assert_array_equal(got[:, 5].astype(int), want["cls"])
+        np.testing.assert_allclose(got[:, 4], want["score"], rtol=0, atol=2e-6)
+        np.testing.assert_allclose(got[:, :4], want["box"], rtol=0, atol=2e-3)
+    eng.close()

@@ -87,9 +87,37 @@ __global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int 
   for (int i = 0; i < CT; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (WHOLE) {
-    stage(0, NP, 0);
+    // every key at once: all global loads are issued before the first LDS store
+    constexpr int KIT = ATT_WHOLE_MAX * 4 / 256, VIT = ATT_WHOLE_MAX * (HD / 8) / 256;
+    f16x8 kv[KIT], vv[VIT];
+#pragma unroll
+    for (int u = 0; u < KIT; u++) {
+      const int i = t + 256 * u, key = i >> 2;
+      kv[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      if (key < N) kv[u] = *(const f16x8*)(qkv.p + (imgbase + key) * qkv.s + qoff + KD + 8 * (i & 3));
+    }
+#pragma unroll
+    for (int u = 0; u < VIT; u++) {
+      const int i = t + 256 * u, key = i / (HD / 8);
+      vv[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      if (key < N) vv[u] = *(const f16x8*)(qkv.p + (imgbase + key) * qkv.s + qoff + 2 * KD + 8 * (i % (HD / 8)));
+    }
+#pragma unroll
+    for (int u = 0; u < KIT; u++) {
+      const int i = t + 256 * u, key = i >> 2;
+      if (key < NP) sK[kswz(key, i & 3)] = kv[u];
+    }
+#pragma unroll
+    for (int u = 0; u < VIT; u++) {
+      const int i = t + 256 * u, key = i / (HD / 8), g = i % (HD / 8);
+      if (key < NP) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) sVt[(8 * g + j) * vpitch + key] = vv[u][j];
+      }
+    }
     __syncthreads();
   }
+#pragma unroll 2
   for (int ch = 0; ch < nchunk; ch++) {
     const int k0 = ch * AK;
     const int kb = WHOLE ? k0 : 0;   // LDS row of this chunk's first key

@@ -56,48 +56,69 @@ __global__ __launch_bounds__(256) void k_maxpool5(View x, View y, int total) {
 }
 
 // SPPF pool chain: y1 = mp5(x), y2 = mp5(y1), y3 = mp5(y2) in one launch (the reference
-// runs three MAXPOOL5 ops, export/export.py:475-491).  One block per (image, 8-channel
-// group) keeps the whole H x W plane in LDS; each mp5 is a separable pair of clipped
-// 5-wide max passes (row pass into `t`, column pass back into `a`, which is also stored).
-__device__ __forceinline__ f16x8 max8(f16x8 a, f16x8 b) {
-  f16x8 o;
-#pragma unroll
-  for (int j = 0; j < 8; j++) o[j] = a[j] > b[j] ? a[j] : b[j];
-  return o;
-}
+// runs three MAXPOOL5 ops, export/export.py:475-491).  With windows clipped at the border,
+// mp5(mp5(x)) is the clipped 9-wide max of x and mp5 applied three times the clipped 13-wide
+// max, so the three outputs are separable 5-, 9- and 13-wide maxima of x: one row pass
+// (planes r5, r9, r13 from one growing window) and one column pass, with the x plane of one
+// (image, 8-channel group) per block in LDS.  Max is exact, so this equals the chained pools.
+__device__ __forceinline__ f16x8 max8(f16x8 a, f16x8 b) { return __builtin_elementwise_max(a, b); }
+
 __global__ __launch_bounds__(256) void k_sppf_pool(View x, View y1, View y2, View y3) {
   extern __shared__ f16x8 sp[];
   const int H = x.H, W = x.W, HW = H * W;
   f16x8* a = sp;
-  f16x8* t = sp + HW;
+  f16x8* r5 = sp + HW;
+  f16x8* r9 = r5 + HW;
+  f16x8* r13 = r9 + HW;
   const int g = blockIdx.x, img = blockIdx.y;
   const size_t pix0 = (size_t)img * HW;
-  for (int p = threadIdx.x; p < HW; p += blockDim.x) a[p] = ld8(x, pix0 + p, g * 8);
+  for (int p0 = 0; p0 < HW; p0 += 4 * 256) {   // 4 loads in flight per thread
+    f16x8 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int p = p0 + u * 256 + threadIdx.x;
+      if (p < HW) v[u] = ld8(x, pix0 + p, g * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int p = p0 + u * 256 + threadIdx.x;
+      if (p < HW) a[p] = v[u];
+    }
+  }
   __syncthreads();
-  for (int it = 0; it < 3; it++) {
-    for (int p = threadIdx.x; p < HW; p += blockDim.x) {
-      const int py = p / W, px = p - py * W;
-      const f16x8* row = a + py * W;
-      f16x8 m = row[px];
-      if (px >= 1) m = max8(m, row[px - 1]);
-      if (px >= 2) m = max8(m, row[px - 2]);
-      if (px + 1 < W) m = max8(m, row[px + 1]);
-      if (px + 2 < W) m = max8(m, row[px + 2]);
-      t[p] = m;
+  for (int p = threadIdx.x; p < HW; p += blockDim.x) {
+    const int py = p / W, px = p - py * W;
+    const f16x8* row = a + py * W;
+    f16x8 m = row[px];
+#pragma unroll
+    for (int d = 1; d <= 6; d++) {
+      if (px >= d) m = max8(m, row[px - d]);
+      if (px + d < W) m = max8(m, row[px + d]);
+      if (d == 2) r5[p] = m;
+      if (d == 4) r9[p] = m;
     }
-    __syncthreads();
-    const View& yo = it == 0 ? y1 : it == 1 ? y2 : y3;
-    for (int p = threadIdx.x; p < HW; p += blockDim.x) {
-      const int py = p / W;
-      f16x8 m = t[p];
-      if (py >= 1) m = max8(m, t[p - W]);
-      if (py >= 2) m = max8(m, t[p - 2 * W]);
-      if (py + 1 < H) m = max8(m, t[p + W]);
-      if (py + 2 < H) m = max8(m, t[p + 2 * W]);
-      a[p] = m;
-      st8(yo, pix0 + p, g * 8, m);
+    r13[p] = m;
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < HW; p += blockDim.x) {
+    const int py = p / W;
+    f16x8 m5 = r5[p], m9 = r9[p], m13 = r13[p];
+#pragma unroll
+    for (int d = 1; d <= 6; d++) {
+      if (py >= d) {
+        if (d <= 2) m5 = max8(m5, r5[p - d * W]);
+        if (d <= 4) m9 = max8(m9, r9[p - d * W]);
+        m13 = max8(m13, r13[p - d * W]);
+      }
+      if (py + d < H) {
+        if (d <= 2) m5 = max8(m5, r5[p + d * W]);
+        if (d <= 4) m9 = max8(m9, r9[p + d * W]);
+        m13 = max8(m13, r13[p + d * W]);
+      }
     }
-    __syncthreads();
+    st8(y1, pix0 + p, g * 8, m5);
+    st8(y2, pix0 + p, g * 8, m9);
+    st8(y3, pix0 + p, g * 8, m13);
   }
 }
 
@@ -141,7 +162,7 @@ void launchMaxPool5(const View& x, const View& y, int Bn, hipStream_t st) {
   int total = Bn * y.H * y.W * (y.C / 8);
   k_maxpool5<<<grid(total), 256, 0, st>>>(x, y, total);
 }
-size_t sppfPoolLds(int H, int W) { return (size_t)2 * H * W * sizeof(f16x8); }
+size_t sppfPoolLds(int H, int W) { return (size_t)4 * H * W * sizeof(f16x8); }
 void launchSppfPool(const View& x, const View& y1, const View& y2, const View& y3, int Bn,
                     hipStream_t st) {
   k_sppf_pool<<<dim3(x.C / 8, Bn), 256, sppfPoolLds(x.H, x.W), st>>>(x, y1, y2, y3);

@@ -65,14 +65,16 @@ __device__ __forceinline__ int keyAnchor(unsigned long long k) {
   return (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull));
 }
 
-// grid (anchor blocks, images): a wave never spans two images, so the survivors of a wave
-// are appended to the image's candidate list with one atomic (wave-aggregated).  The list
-// order depends on arrival; NMS sorts by key, so results do not.
+// grid (anchor blocks of one wave, images): a wave never spans two images, so the survivors
+// of a wave are appended to the image's candidate list with one atomic (wave-aggregated).
+// The list order depends on arrival; NMS sorts by key, so results do not.  One-wave blocks
+// spread the 8,400 anchors of a 640 frame over ~130 CUs, and survivors fetch their box bins
+// before the append, so the two memory latencies overlap.
 // OBB (k_decode_obb, engine/engine.cu:908-964): the angle view (channel 0 real) gives
 // theta = (sigmoid(t) - 0.25) * pi, the DFL distances are rotated by theta about the anchor
 // (dist2rbox), w = l + r, h = t + b, and the record is cx, cy, w, h, score, cls, theta.
 template <bool OBB>
-__global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict__ cand,
+__global__ __launch_bounds__(64) void k_decode(DecodeArgs a, float* __restrict__ cand,
                                                 unsigned long long* __restrict__ lst,
                                                 int* __restrict__ count,
                                                 const PostParams* __restrict__ prm, int cstride) {
@@ -109,6 +111,12 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict_
   }
   const float score = 1.f / (1.f + expf(-best));
   const bool keep = inside && score >= prm->conf;
+  const f16* bp = L.box.p + pix * L.box.s + L.box.o;
+  f16x8 bv[8];
+  if (keep) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) bv[u] = *(const f16x8*)(bp + 8 * u);
+  }
   const unsigned long long bal = __ballot(keep);
   if (bal) {
     const int leader = __ffsll((long long)bal) - 1;
@@ -121,11 +129,10 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict_
   }
   if (!keep) return;
 
-  const f16* bp = L.box.p + pix * L.box.s + L.box.o;
   float d[4];
 #pragma unroll
   for (int side = 0; side < 4; side++) {
-    const f16x8 v0 = *(const f16x8*)(bp + side * 16), v1 = *(const f16x8*)(bp + side * 16 + 8);
+    const f16x8 v0 = bv[2 * side], v1 = bv[2 * side + 1];
     float l[16];
 #pragma unroll
     for (int j = 0; j < 8; j++) { l[j] = (float)v0[j]; l[j + 8] = (float)v1[j]; }
@@ -175,11 +182,11 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a, float* __restrict_
 
 void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lst, int* count,
                   const PostParams* prm, int Bn, hipStream_t st) {
-  const dim3 grid((a.A + 255) / 256, Bn);
+  const dim3 grid((a.A + 63) / 64, Bn);
   if (a.obb)
-    k_decode<true><<<grid, 256, 0, st>>>(a, cand, lst, count, prm, 7);
+    k_decode<true><<<grid, 64, 0, st>>>(a, cand, lst, count, prm, 7);
   else
-    k_decode<false><<<grid, 256, 0, st>>>(a, cand, lst, count, prm, 6 + a.nm);
+    k_decode<false><<<grid, 64, 0, st>>>(a, cand, lst, count, prm, 6 + a.nm);
 }
 
 // ------------------------------------------------------------------ NMS
@@ -191,16 +198,19 @@ void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lst, int
 //  2. greedy suppression (k_nms semantics, engine/engine.cu:1091-1109: same class only,
 //     inter/union > thr with a union > 0 guard).  Suppression never crosses classes, so
 //     the greedy result is the union of independent per-class greedy passes: when every
-//     class has at most 64 candidates, each wave takes a share of the classes present,
-//     gathers a class's members in rank order with ballots (one lane per member), builds
-//     their suppression rows with ballots and resolves them by a bit scan; survivors are
-//     flagged by rank and a block prefix sum over the flags gives their output slots.
-//     Otherwise (a class with more than 64 candidates): 64 candidates per step, the block
+//     class has at most 128 candidates, the candidates are laid out class-major (rank order
+//     within a class), the whole block builds every class's suppression rows (a class is
+//     decided in two chunks of 64 members at most; one ballot per row, plus a row of
+//     first-chunk suppressors for second-chunk members), then one wave per class resolves
+//     its chunks by bit scans; survivors are flagged by rank and a block prefix sum over the
+//     flags gives their output slots.
+//     Otherwise (a class with more than 128 candidates): 64 candidates per step, the block
 //     building that step's 64x64 rows, wave 0 walking them, the block striking later
 //     candidates.  Both give exactly the sequential greedy result.
 //  3. the list counter is re-armed (zeroed) for the next frame.
 constexpr int NMS_THREADS = 1024;
 constexpr int NMS_CLASSES = 1024;            // class histogram size of the per-class path
+constexpr int NMS_PERCLASS_MAX = 128;        // largest class the per-class path takes (two chunks)
 
 // inter/union > thr, decided without the division unless the two sides are within a few
 // ulps (then the division decides, exactly as the reference writes it)
@@ -344,6 +354,11 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   __shared__ unsigned removed[NMS_CAP / 32];
   __shared__ unsigned long long rows[64];
   __shared__ short kept[64];
+  __shared__ int cstart[NMS_CLASSES];                          // class-major start of a class
+  __shared__ short perm[NMS_CAP];                              // class-major position -> rank
+  __shared__ float4 cbox[NMS_CAP];                             // boxes, class-major
+  __shared__ unsigned long long rows2[NMS_CAP];                // chunk suppression rows
+  __shared__ unsigned long long xrows[NMS_CAP];                // first-chunk suppressors
   __shared__ RankShared rs;
   __shared__ unsigned long long keptmask;
   __shared__ int nout, nkept;
@@ -355,7 +370,9 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   const int maxdet = min(prm->max_det, MAX_OUT);
   const int n = min(counts[img], A);
   const int m = min(n, NMS_CAP);
-  if (tid == 0) nout = 0;
+  if (tid == 0) { nout = 0; npresent = 0; maxClass = 0; }
+  chist[tid] = 0;
+  static_assert(NMS_CLASSES == NMS_THREADS, "one class bin per thread");
 
   // 1. the m best keys in rank order, parked in the box array's storage; every thread then
   //    lifts its entries (and their candidate records) into registers before the arrays
@@ -373,7 +390,7 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
       kr[u] = sorted[r];
       const float* rec = cimg + (size_t)keyAnchor(kr[u]) * cstride;
       br[u] = make_float4(rec[0], rec[1], rec[2], rec[3]);
-      cr[u] = (short)rec[5];
+      cr[u] = (short)min(max((int)rec[5], 0), NMS_CLASSES - 1);   // ids are < nc <= NMS_CLASSES
     }
   }
   __syncthreads();
@@ -384,6 +401,7 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
       skey[r] = kr[u];
       sbox[r] = br[u];
       scls[r] = cr[u];
+      atomicAdd(&chist[cr[u]], 1);
     }
   }
   __syncthreads();
@@ -398,67 +416,117 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     outidx[img * MAX_OUT + slot] = keyAnchor(skey[i]);
   };
 
-  // class histogram (classes present, largest class) for the per-class path
-  for (int c = tid; c < NMS_CLASSES; c += NMS_THREADS) chist[c] = 0;
-  if (tid == 0) { npresent = 0; maxClass = 0; }
-  __syncthreads();
-  bool perClass = true;
-  for (int i = tid; i < m; i += NMS_THREADS) {
-    const int c = scls[i];
-    if (c < 0 || c >= NMS_CLASSES) perClass = false;   // never for a valid model
-    else atomicAdd(&chist[c], 1);
-  }
-  perClass = __syncthreads_and(perClass);
-  for (int c = tid; c < NMS_CLASSES; c += NMS_THREADS) {
-    const int h = chist[c];
+  // 2. class-major layout.  Thread t owns class t: classes present, the largest class and
+  //    the exclusive prefix of the histogram (accumulated during the gather).
+  {
+    const int h = chist[tid];
     if (h > 0) {
-      present[atomicAdd(&npresent, 1)] = (short)c;
+      present[atomicAdd(&npresent, 1)] = (short)tid;
       atomicMax(&maxClass, h);
     }
+    int incl = h;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int off = 0;
+    for (int w = 0; w < wave; w++) off += wsum[w];
+    cstart[tid] = off + incl - h;
   }
   __syncthreads();
-  perClass = perClass && maxClass <= 64;
+  const bool perClass = maxClass <= NMS_PERCLASS_MAX;
 
   if (perClass) {
-    // 2a. per-class greedy: wave w takes present[w], present[w + 16], ...; `removed` holds
-    //     the kept flag of every candidate by rank (reused as a bit array)
+    // 2a. one wave per class lists the class's ranks in order (ballot append) with their boxes
     for (int pc = wave; pc < npresent; pc += NMS_THREADS / 64) {
       const int c = present[pc];
-      // members in rank order: lane t gets the t-th member's rank
-      int mine = -1, g = 0;
+      int g = cstart[c];
       for (int i0 = 0; i0 < m; i0 += 64) {
         const int i = i0 + lane;
         const bool in = i < m && scls[i] == c;
         const unsigned long long bal = __ballot(in);
-        const int before = __popcll(bal & ((1ull << lane) - 1ull));
-        // lane (g + before) of the wave receives member i: invert with a ds_bpermute-free
-        // scan -- each lane checks whether its slot falls in this chunk
-        const int slot = lane - g;
-        if (slot >= 0 && slot < __popcll(bal)) {
-          // the slot-th set bit of bal
-          unsigned long long b = bal;
-          for (int q = 0; q < slot; q++) b &= b - 1ull;
-          mine = i0 + __builtin_ctzll(b);
+        if (in) {
+          const int p = g + __popcll(bal & ((1ull << lane) - 1ull));
+          perm[p] = (short)i;
+          cbox[p] = sbox[i];
         }
         g += __popcll(bal);
       }
-      const float4 bx = mine >= 0 ? sbox[mine] : make_float4(0.f, 0.f, 0.f, 0.f);
-      // row of member t: later members it suppresses
-      unsigned long long row = 0ull;
-      for (int t = 0; t < g; t++) {
-        const float4 bt = make_float4(__shfl(bx.x, t), __shfl(bx.y, t), __shfl(bx.z, t), __shfl(bx.w, t));
-        const unsigned long long r = __ballot(lane > t && lane < g && suppresses(bt, bx, thr));
-        if (lane == t) row = r;
+    }
+    __syncthreads();
+    // 2b. suppression rows, block-parallel.  A class is decided in (at most two) chunks of 64
+    //     members: rows2[p] holds the later members of p's chunk that p suppresses and, for p
+    //     in a second chunk, xrows[p] the members of the first chunk that suppress p.  Wave w
+    //     takes a contiguous run of positions; lane L first loads the box and chunk geometry
+    //     of one position of the run, and the loop broadcasts them with readlane, so the only
+    //     LDS loads in the loop are a chunk's boxes when the chunk changes.
+    {
+      const int per = (m + NMS_THREADS / 64 - 1) / (NMS_THREADS / 64);
+      const int pb = wave * per, pe = min(m, pb + per);
+      int chunk0 = -1, nqc = 0;
+      float4 bj = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int sub = pb; sub < pe; sub += 64) {
+        const int p = sub + lane;
+        int q0 = 0, nq = 0, al = 0, sc = 0;
+        float4 bp = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (p < pe) {
+          const int c = scls[perm[p]];
+          sc = cstart[c];
+          const int a = p - sc;
+          q0 = sc + (a & ~63);
+          nq = min(64, chist[c] - (a & ~63));
+          al = a;
+          bp = cbox[p];
+        }
+        const int cnt = min(64, pe - sub);
+        for (int k = 0; k < cnt; k++) {
+          const int qk = __builtin_amdgcn_readlane(q0, k);
+          if (qk != chunk0) {
+            chunk0 = qk;
+            nqc = __builtin_amdgcn_readlane(nq, k);
+            if (lane < nqc) bj = cbox[qk + lane];
+          }
+          const float4 bi = make_float4(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.x), k)),
+                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.y), k)),
+                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.z), k)),
+                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.w), k)));
+          const int ak = __builtin_amdgcn_readlane(al, k);
+          const unsigned long long row = __ballot(lane < nqc && lane > (ak & 63) && suppresses(bi, bj, thr));
+          if (lane == 0) rows2[sub + k] = row;
+          if (ak >= 64) {                     // second chunk: suppressors among the first 64
+            const float4 b0 = cbox[__builtin_amdgcn_readlane(sc, k) + lane];
+            const unsigned long long xr = __ballot(suppresses(b0, bi, thr));
+            if (lane == 0) xrows[sub + k] = xr;
+          }
+        }
       }
-      unsigned long long todo = g >= 64 ? ~0ull : ((1ull << g) - 1ull), keep = 0ull;
-      while (todo) {
-        const int t = __builtin_ctzll(todo);
-        keep |= 1ull << t;
-        const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, t);
-        const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), t);
-        todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << t));
+    }
+    __syncthreads();
+    // 2c. per-class greedy, one wave per class: the first chunk's rows are resolved by a bit
+    //     scan; second-chunk members suppressed by a first-chunk survivor are struck before
+    //     its own scan.  `removed` holds the kept flag of every candidate by rank.
+    for (int pc = wave; pc < npresent; pc += NMS_THREADS / 64) {
+      const int c = present[pc];
+      const int sc = cstart[c], g = chist[c];
+      unsigned long long keep0 = 0ull;
+      for (int q0 = 0; q0 < g; q0 += 64) {
+        const int gq = min(64, g - q0);
+        const int mine = lane < gq ? perm[sc + q0 + lane] : 0;
+        const unsigned long long row = lane < gq ? rows2[sc + q0 + lane] : 0ull;
+        const bool rem = q0 > 0 && lane < gq && (xrows[sc + q0 + lane] & keep0) != 0ull;
+        unsigned long long todo = (gq >= 64 ? ~0ull : ((1ull << gq) - 1ull)) & ~__ballot(rem), keep = 0ull;
+        while (todo) {
+          const int t = __builtin_ctzll(todo);
+          keep |= 1ull << t;
+          const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, t);
+          const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), t);
+          todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << t));
+        }
+        if ((keep >> lane) & 1ull) atomicOr(&removed[mine >> 5], 1u << (mine & 31));
+        keep0 = keep;
       }
-      if ((keep >> lane) & 1ull) atomicOr(&removed[mine >> 5], 1u << (mine & 31));
     }
     __syncthreads();
     // 2b. output slots: exclusive prefix count of kept flags in rank order (thread t owns
