@@ -663,20 +663,46 @@ __global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f
   const int cols = (FIRST_TP - 1) * cs + 3, rows = (FIRST_RB - 1) * cs + 3;
   const int ix0 = ox0 * cs - cp, iy0 = oy0 * cs - cp;
 
-  // ---- stage input window, weights, biases
+  // ---- stage input window, weights, biases: every global load is issued before the first
+  //      LDS store (fully unrolled, bounds as predicates), so the block waits for one
+  //      memory round trip instead of one per window row
   const f16* xb = x.p + (size_t)img * x.H * x.W * x.s + x.o;
-  for (int r = 0; r < rows; r++) {
+  constexpr int QIT = (FIRST_COLS * 3 + 255) / 256;
+  f16 xv[FIRST_ROWS][QIT];
+#pragma unroll
+  for (int r = 0; r < FIRST_ROWS; r++) {
     const int iy = iy0 + r;
-    const bool rowin = iy >= 0 && iy < x.H;
+    const bool rowin = r < rows && iy >= 0 && iy < x.H;
     const f16* xrow = xb + (size_t)(rowin ? iy : 0) * x.W * x.s;
-    for (int q = threadIdx.x; q < cols * 3; q += 256) {
+#pragma unroll
+    for (int u = 0; u < QIT; u++) {
+      const int q = threadIdx.x + 256 * u;
       const int c = q / 3, ci = q - 3 * c;   // constant divisor: a multiply-high
       const int ix = ix0 + c;
-      tile[r][q] = (rowin && ix >= 0 && ix < x.W) ? xrow[ix * x.s + ci] : (f16)0.f;
+      xv[r][u] = (rowin && q < cols * 3 && ix >= 0 && ix < x.W) ? xrow[ix * x.s + ci] : (f16)0.f;
     }
   }
-  for (int e = threadIdx.x; e < nf * 16 * 27; e += 256) sw[e] = w[(size_t)cb * 27 + e];
-  for (int e = threadIdx.x; e < nf * 16; e += 256) sb[e] = bias[cb + e];
+  constexpr int WIT = (16 * NF * 27 + 255) / 256;
+  f16 wv[WIT];
+#pragma unroll
+  for (int u = 0; u < WIT; u++) {
+    const int e = threadIdx.x + 256 * u;
+    wv[u] = e < nf * 16 * 27 ? w[(size_t)cb * 27 + e] : (f16)0.f;
+  }
+  const float bv = (int)threadIdx.x < nf * 16 ? bias[cb + threadIdx.x] : 0.f;
+#pragma unroll
+  for (int r = 0; r < FIRST_ROWS; r++)
+#pragma unroll
+    for (int u = 0; u < QIT; u++) {
+      const int q = threadIdx.x + 256 * u;
+      if (r < rows && q < cols * 3) tile[r][q] = xv[r][u];
+    }
+#pragma unroll
+  for (int u = 0; u < WIT; u++) {
+    const int e = threadIdx.x + 256 * u;
+    if (e < nf * 16 * 27) sw[e] = wv[u];
+  }
+  if ((int)threadIdx.x < nf * 16) sb[threadIdx.x] = bv;
   __syncthreads();
 
   int toff[8];

@@ -192,25 +192,19 @@ void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lst, int
 // ------------------------------------------------------------------ NMS
 // One block (16 waves) per image, on the candidate list the decode kernel appended.
 //  1. selection + ranking by the total order (score desc, anchor asc) packed in one u64
-//     key: above NMS_CAP candidates a radix select keeps the NMS_CAP largest keys, then
-//     each key's rank (the number of larger keys, counted by several threads per key)
-//     places it in LDS; the list's arrival order therefore never matters
+//     key (selectAndRank below), so the list's arrival order never matters;
 //  2. greedy suppression (k_nms semantics, engine/engine.cu:1091-1109: same class only,
 //     inter/union > thr with a union > 0 guard).  Suppression never crosses classes, so
-//     the greedy result is the union of independent per-class greedy passes: when every
-//     class has at most 128 candidates, the candidates are laid out class-major (rank order
-//     within a class), the whole block builds every class's suppression rows (a class is
-//     decided in two chunks of 64 members at most; one ballot per row, plus a row of
-//     first-chunk suppressors for second-chunk members), then one wave per class resolves
-//     its chunks by bit scans; survivors are flagged by rank and a block prefix sum over the
-//     flags gives their output slots.
-//     Otherwise (a class with more than 128 candidates): 64 candidates per step, the block
-//     building that step's 64x64 rows, wave 0 walking them, the block striking later
-//     candidates.  Both give exactly the sequential greedy result.
+//     the greedy result is the union of independent per-class greedy passes: candidates
+//     are laid out class-major (rank order within a class), the whole block builds every
+//     class's suppression rows in chunks of 64 members (one ballot per row); a class of at
+//     most 64 members is then resolved by one wave with a bit scan, a larger one chunk by
+//     chunk with the whole block (a chunk's survivors strike the class's later members).
+//     This is exactly the sequential greedy result; survivors are flagged by rank and a
+//     block prefix sum over the flags gives their output slots;
 //  3. the list counter is re-armed (zeroed) for the next frame.
 constexpr int NMS_THREADS = 1024;
 constexpr int NMS_CLASSES = 1024;            // class histogram size of the per-class path
-constexpr int NMS_PERCLASS_MAX = 128;        // largest class the per-class path takes (two chunks)
 
 // inter/union > thr, decided without the division unless the two sides are within a few
 // ulps (then the division decides, exactly as the reference writes it)
@@ -275,14 +269,31 @@ __device__ void selectAndRank(const unsigned long long* __restrict__ lst, int n,
         }
       }
       __syncthreads();
-      if (tid == 0) {
-        int need = rs.need, cum = 0, sel = 0;
-        for (int b = 255; b >= 0; b--) {
-          if (cum + rs.hist[b] >= need) { sel = b; need -= cum; break; }
-          cum += rs.hist[b];
+      // the bin holding the need-th largest key: lane l of wave 0 owns bins 255-4l .. 252-4l
+      // (descending), a prefix sum over the lanes finds the one lane whose range holds it
+      if (tid < 64) {
+        int h[4], sum = 0;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          h[u] = rs.hist[255 - 4 * lane - u];
+          sum += h[u];
         }
-        rs.need = need;
-        rs.prefix = pre | ((unsigned long long)sel << shift);
+        int incl = sum;
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_up(incl, o);
+          if (lane >= o) incl += y;
+        }
+        const int need = rs.need, excl = incl - sum;
+        if (excl < need && need <= incl) {
+          int cum = excl, sel = 255 - 4 * lane - 3;
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            if (cum + h[u] >= need) { sel = 255 - 4 * lane - u; break; }
+            cum += h[u];
+          }
+          rs.need = need - cum;
+          rs.prefix = pre | ((unsigned long long)sel << shift);
+        }
       }
       __syncthreads();
     }
@@ -346,22 +357,20 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
                                                      int* __restrict__ rawcnt,
                                                      const PostParams* __restrict__ prm) {
   __shared__ unsigned long long skey[NMS_CAP];
-  __shared__ float4 sbox[NMS_CAP];
+  __shared__ float4 sbox[NMS_CAP];                 // boxes by rank, then a class's survivors
   __shared__ short scls[NMS_CAP];
   __shared__ int chist[NMS_CLASSES];
+  __shared__ int cstart[NMS_CLASSES];              // class-major start of a class
   __shared__ short present[NMS_CLASSES];
-  __shared__ int npresent, maxClass, wsum[NMS_THREADS / 64];
-  __shared__ unsigned removed[NMS_CAP / 32];
-  __shared__ unsigned long long rows[64];
-  __shared__ short kept[64];
-  __shared__ int cstart[NMS_CLASSES];                          // class-major start of a class
-  __shared__ short perm[NMS_CAP];                              // class-major position -> rank
-  __shared__ float4 cbox[NMS_CAP];                             // boxes, class-major
-  __shared__ unsigned long long rows2[NMS_CAP];                // chunk suppression rows
-  __shared__ unsigned long long xrows[NMS_CAP];                // first-chunk suppressors
+  __shared__ short perm[NMS_CAP];                  // class-major position -> rank
+  __shared__ float4 cbox[NMS_CAP];                 // boxes, class-major
+  __shared__ unsigned long long rows2[NMS_CAP];    // chunk suppression rows, class-major
+  __shared__ unsigned removed[NMS_CAP / 32];       // kept flags by rank
+  __shared__ unsigned struck[NMS_CAP / 32];        // suppressed flags, class-major (large classes)
+  __shared__ float4 stepBox[64];                   // survivors of a large class's chunk
+  __shared__ int npresent, nstep, wsum[NMS_THREADS / 64];
   __shared__ RankShared rs;
-  __shared__ unsigned long long keptmask;
-  __shared__ int nout, nkept;
+  static_assert(NMS_CLASSES == NMS_THREADS, "one class bin per thread");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int img = blockIdx.x;
@@ -370,13 +379,12 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   const int maxdet = min(prm->max_det, MAX_OUT);
   const int n = min(counts[img], A);
   const int m = min(n, NMS_CAP);
-  if (tid == 0) { nout = 0; npresent = 0; maxClass = 0; }
+  if (tid == 0) npresent = 0;
   chist[tid] = 0;
-  static_assert(NMS_CLASSES == NMS_THREADS, "one class bin per thread");
 
   // 1. the m best keys in rank order, parked in the box array's storage; every thread then
   //    lifts its entries (and their candidate records) into registers before the arrays
-  //    are written for good
+  //    are written for good, counting classes as it writes
   unsigned long long* sorted = reinterpret_cast<unsigned long long*>(sbox);
   selectAndRank(lists + (size_t)img * A, n, skey, sorted, rs);
   for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) removed[i] = 0u;
@@ -406,24 +414,12 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   }
   __syncthreads();
 
-  // writes survivor `i` (rank order) to output slot `slot`
-  auto emit = [&](int i, int slot) {
-    const float4 bi = sbox[i];
-    float* d = out + ((size_t)img * MAX_OUT + slot) * 6;
-    d[0] = bi.x; d[1] = bi.y; d[2] = bi.z; d[3] = bi.w;
-    d[4] = __uint_as_float((unsigned)(skey[i] >> 32));
-    d[5] = (float)scls[i];
-    outidx[img * MAX_OUT + slot] = keyAnchor(skey[i]);
-  };
-
-  // 2. class-major layout.  Thread t owns class t: classes present, the largest class and
-  //    the exclusive prefix of the histogram (accumulated during the gather).
+  // 2. class-major layout.  Thread t owns class t: classes present and the exclusive prefix
+  //    of the histogram; then one wave per class lists the class's ranks in order (ballot
+  //    append) with their boxes
   {
     const int h = chist[tid];
-    if (h > 0) {
-      present[atomicAdd(&npresent, 1)] = (short)tid;
-      atomicMax(&maxClass, h);
-    }
+    if (h > 0) present[atomicAdd(&npresent, 1)] = (short)tid;
     int incl = h;
     for (int o = 1; o < 64; o <<= 1) {
       const int y = __shfl_up(incl, o);
@@ -436,86 +432,105 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     cstart[tid] = off + incl - h;
   }
   __syncthreads();
-  const bool perClass = maxClass <= NMS_PERCLASS_MAX;
+  for (int pc = wave; pc < npresent; pc += NMS_THREADS / 64) {
+    const int c = present[pc];
+    int g = cstart[c];
+    for (int i0 = 0; i0 < m; i0 += 64) {
+      const int i = i0 + lane;
+      const bool in = i < m && scls[i] == c;
+      const unsigned long long bal = __ballot(in);
+      if (in) {
+        const int p = g + __popcll(bal & ((1ull << lane) - 1ull));
+        perm[p] = (short)i;
+        cbox[p] = sbox[i];
+      }
+      g += __popcll(bal);
+    }
+  }
+  __syncthreads();
 
-  if (perClass) {
-    // 2a. one wave per class lists the class's ranks in order (ballot append) with their boxes
-    for (int pc = wave; pc < npresent; pc += NMS_THREADS / 64) {
-      const int c = present[pc];
-      int g = cstart[c];
-      for (int i0 = 0; i0 < m; i0 += 64) {
-        const int i = i0 + lane;
-        const bool in = i < m && scls[i] == c;
-        const unsigned long long bal = __ballot(in);
-        if (in) {
-          const int p = g + __popcll(bal & ((1ull << lane) - 1ull));
-          perm[p] = (short)i;
-          cbox[p] = sbox[i];
+  // 3. suppression rows, block-parallel.  A class is decided in chunks of 64 members;
+  //    rows2[p] holds the later members of p's chunk that p suppresses.  Wave w takes a
+  //    contiguous run of positions; lane L first loads the box and chunk geometry of one
+  //    position of the run, and the loop broadcasts them with readlane, so the only LDS
+  //    loads in the loop are a chunk's boxes when the chunk changes.
+  {
+    const int per = (m + NMS_THREADS / 64 - 1) / (NMS_THREADS / 64);
+    const int pb = wave * per, pe = min(m, pb + per);
+    int chunk0 = -1, nqc = 0;
+    float4 bj = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int sub = pb; sub < pe; sub += 64) {
+      const int p = sub + lane;
+      int q0 = 0, nq = 0, al = 0;
+      float4 bp = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (p < pe) {
+        const int c = scls[perm[p]];
+        const int sc = cstart[c], a = p - sc;
+        q0 = sc + (a & ~63);
+        nq = min(64, chist[c] - (a & ~63));
+        al = a & 63;
+        bp = cbox[p];
+      }
+      const int cnt = min(64, pe - sub);
+      for (int k = 0; k < cnt; k++) {
+        const int qk = __builtin_amdgcn_readlane(q0, k);
+        if (qk != chunk0) {
+          chunk0 = qk;
+          nqc = __builtin_amdgcn_readlane(nq, k);
+          if (lane < nqc) bj = cbox[qk + lane];
         }
-        g += __popcll(bal);
+        const float4 bi = make_float4(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.x), k)),
+                                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.y), k)),
+                                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.z), k)),
+                                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.w), k)));
+        const int ak = __builtin_amdgcn_readlane(al, k);
+        const unsigned long long row = __ballot(lane < nqc && lane > ak && suppresses(bi, bj, thr));
+        if (lane == 0) rows2[sub + k] = row;
       }
     }
-    __syncthreads();
-    // 2b. suppression rows, block-parallel.  A class is decided in (at most two) chunks of 64
-    //     members: rows2[p] holds the later members of p's chunk that p suppresses and, for p
-    //     in a second chunk, xrows[p] the members of the first chunk that suppress p.  Wave w
-    //     takes a contiguous run of positions; lane L first loads the box and chunk geometry
-    //     of one position of the run, and the loop broadcasts them with readlane, so the only
-    //     LDS loads in the loop are a chunk's boxes when the chunk changes.
-    {
-      const int per = (m + NMS_THREADS / 64 - 1) / (NMS_THREADS / 64);
-      const int pb = wave * per, pe = min(m, pb + per);
-      int chunk0 = -1, nqc = 0;
-      float4 bj = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int sub = pb; sub < pe; sub += 64) {
-        const int p = sub + lane;
-        int q0 = 0, nq = 0, al = 0, sc = 0;
-        float4 bp = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (p < pe) {
-          const int c = scls[perm[p]];
-          sc = cstart[c];
-          const int a = p - sc;
-          q0 = sc + (a & ~63);
-          nq = min(64, chist[c] - (a & ~63));
-          al = a;
-          bp = cbox[p];
-        }
-        const int cnt = min(64, pe - sub);
-        for (int k = 0; k < cnt; k++) {
-          const int qk = __builtin_amdgcn_readlane(q0, k);
-          if (qk != chunk0) {
-            chunk0 = qk;
-            nqc = __builtin_amdgcn_readlane(nq, k);
-            if (lane < nqc) bj = cbox[qk + lane];
-          }
-          const float4 bi = make_float4(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.x), k)),
-                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.y), k)),
-                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.z), k)),
-                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.w), k)));
-          const int ak = __builtin_amdgcn_readlane(al, k);
-          const unsigned long long row = __ballot(lane < nqc && lane > (ak & 63) && suppresses(bi, bj, thr));
-          if (lane == 0) rows2[sub + k] = row;
-          if (ak >= 64) {                     // second chunk: suppressors among the first 64
-            const float4 b0 = cbox[__builtin_amdgcn_readlane(sc, k) + lane];
-            const unsigned long long xr = __ballot(suppresses(b0, bi, thr));
-            if (lane == 0) xrows[sub + k] = xr;
-          }
-        }
-      }
+  }
+  __syncthreads();
+
+  // 4. per-class greedy.  `removed` holds the kept flag of every candidate by rank.
+  //  4a. a class of at most 64 members is one chunk: one wave resolves its rows by a bit
+  //      scan (waves take the small classes round-robin)
+  for (int pc = wave; pc < npresent; pc += NMS_THREADS / 64) {
+    const int c = present[pc];
+    const int sc = cstart[c], g = chist[c];
+    if (g > 64) continue;                   // wave-uniform
+    const bool valid = lane < g;
+    const int mine = valid ? perm[sc + lane] : 0;
+    const unsigned long long row = valid ? rows2[sc + lane] : 0ull;
+    unsigned long long todo = g >= 64 ? ~0ull : ((1ull << g) - 1ull), keep = 0ull;
+    while (todo) {
+      const int t = __builtin_ctzll(todo);
+      keep |= 1ull << t;
+      const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, t);
+      const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), t);
+      todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << t));
     }
-    __syncthreads();
-    // 2c. per-class greedy, one wave per class: the first chunk's rows are resolved by a bit
-    //     scan; second-chunk members suppressed by a first-chunk survivor are struck before
-    //     its own scan.  `removed` holds the kept flag of every candidate by rank.
-    for (int pc = wave; pc < npresent; pc += NMS_THREADS / 64) {
-      const int c = present[pc];
-      const int sc = cstart[c], g = chist[c];
-      unsigned long long keep0 = 0ull;
-      for (int q0 = 0; q0 < g; q0 += 64) {
-        const int gq = min(64, g - q0);
-        const int mine = lane < gq ? perm[sc + q0 + lane] : 0;
-        const unsigned long long row = lane < gq ? rows2[sc + q0 + lane] : 0ull;
-        const bool rem = q0 > 0 && lane < gq && (xrows[sc + q0 + lane] & keep0) != 0ull;
+    if ((keep >> lane) & 1ull) atomicOr(&removed[mine >> 5], 1u << (mine & 31));
+  }
+  //  4b. a larger class goes chunk by chunk with the whole block: wave 0 resolves the chunk
+  //      (members struck by earlier chunks excluded), then every thread strikes later
+  //      members of the class that a survivor of the chunk suppresses (survivor boxes read
+  //      as LDS broadcasts).  A class stops once it has max_det survivors: a later survivor
+  //      of the class ranks below max_det others and never reaches the output.
+  for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) struck[i] = 0u;
+  __syncthreads();
+  for (int pc = 0; pc < npresent; pc++) {
+    const int c = present[pc];
+    const int sc = cstart[c], g = chist[c];
+    if (g <= 64) continue;                  // block-uniform
+    int K = 0;
+    for (int q0 = 0; q0 < g && K < maxdet; q0 += 64) {
+      const int gq = min(64, g - q0);
+      if (wave == 0) {
+        const int p = sc + q0 + lane;
+        const bool valid = lane < gq;
+        const int mine = valid ? perm[p] : 0;
+        const unsigned long long row = valid ? rows2[p] : 0ull;
+        const bool rem = valid && ((struck[p >> 5] >> (p & 31)) & 1u);
         unsigned long long todo = (gq >= 64 ? ~0ull : ((1ull << gq) - 1ull)) & ~__ballot(rem), keep = 0ull;
         while (todo) {
           const int t = __builtin_ctzll(todo);
@@ -524,90 +539,59 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
           const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), t);
           todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << t));
         }
-        if ((keep >> lane) & 1ull) atomicOr(&removed[mine >> 5], 1u << (mine & 31));
-        keep0 = keep;
-      }
-    }
-    __syncthreads();
-    // 2b. output slots: exclusive prefix count of kept flags in rank order (thread t owns
-    //     ranks 2t, 2t+1)
-    const int r0 = 2 * tid, r1 = 2 * tid + 1;
-    const int f0 = r0 < m ? (removed[r0 >> 5] >> (r0 & 31)) & 1 : 0;
-    const int f1 = r1 < m ? (removed[r1 >> 5] >> (r1 & 31)) & 1 : 0;
-    int v = f0 + f1, incl = v;
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(incl, o);
-      if (lane >= o) incl += y;
-    }
-    if (lane == 63) wsum[wave] = incl;
-    __syncthreads();
-    int off = 0;
-    for (int w = 0; w < wave; w++) off += wsum[w];
-    const int ex = off + incl - v;
-    if (f0 && ex < maxdet) emit(r0, ex);
-    if (f1 && ex + f0 < maxdet) emit(r1, ex + f0);
-    if (tid == NMS_THREADS - 1) nout = off + incl;
-    __syncthreads();
-  } else {
-    // 2'. 64 candidates per step
-    for (int cb = 0; cb * 64 < m; cb++) {
-      if (nout >= maxdet) break;
-      const int base = cb * 64;
-      const int nb = min(64, m - base);
-      // (a) in-block suppression rows: wave w builds rows w, w+16, ...; lane j of the wave
-      //     tests pair (i, j) and the row is the wave's ballot (no atomics, no clearing)
-      for (int i = wave; i < 64; i += NMS_THREADS / 64) {
-        const bool hit = lane > i && lane < nb && i < nb && scls[base + i] == scls[base + lane] &&
-                         suppresses(sbox[base + i], sbox[base + lane], thr);
-        const unsigned long long row = __ballot(hit);
-        if (lane == 0) rows[i] = row;
+        if ((keep >> lane) & 1ull) {
+          atomicOr(&removed[mine >> 5], 1u << (mine & 31));
+          stepBox[__popcll(keep & ((1ull << lane) - 1ull))] = cbox[p];
+        }
+        if (lane == 0) nstep = __popcll(keep);
       }
       __syncthreads();
-      // (b) wave 0 walks the survivors in rank order: the lowest alive bit is kept and
-      //     clears its row; one iteration per survivor (scalar bit scan + two readlanes)
-      if (wave == 0) {
-        const unsigned long long row = rows[lane];
-        const unsigned long long valid = nb >= 64 ? ~0ull : ((1ull << nb) - 1ull);
-        const unsigned rlo = __builtin_amdgcn_readfirstlane(removed[2 * cb]);
-        const unsigned rhi = __builtin_amdgcn_readfirstlane(removed[2 * cb + 1]);
-        unsigned long long todo = ~(((unsigned long long)rhi << 32) | rlo) & valid;
-        unsigned long long alive = 0ull;
-        while (todo) {
-          const int tt = __builtin_ctzll(todo);
-          alive |= 1ull << tt;
-          const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, tt);
-          const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), tt);
-          todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << tt));
-        }
-        const bool mine = (alive >> lane) & 1ull;
-        const int before = __popcll(alive & ((1ull << lane) - 1ull));
-        const int slot = nout + before;
-        if (mine) kept[before] = (short)lane;
-        if (mine && slot < maxdet) emit(base + lane, slot);
-        if (lane == 0) {
-          keptmask = alive;
-          nkept = __popcll(alive);
-          nout = nout + __popcll(alive);
-        }
-      }
-      __syncthreads();
-      // (c) strike later candidates that overlap a survivor of this block: pairs
-      //     (later j, kept i) spread over the block
-      const int K = nkept;
-      const int later = m - (base + 64);
-      if (K > 0 && later > 0) {
-        for (int p = tid; p < later * K; p += NMS_THREADS) {
-          const int j = base + 64 + p / K;
-          const int i = base + kept[p % K];
-          if ((removed[j >> 5] >> (j & 31)) & 1u) continue;
-          if (scls[i] == scls[j] && suppresses(sbox[i], sbox[j], thr)) atomicOr(&removed[j >> 5], 1u << (j & 31));
+      const int Kq = nstep;
+      K += Kq;
+      for (int p = sc + q0 + 64 + tid; p < sc + g && Kq > 0; p += NMS_THREADS) {
+        if ((struck[p >> 5] >> (p & 31)) & 1u) continue;
+        const float4 bp = cbox[p];
+        for (int k = 0; k < Kq; k++) {
+          if (suppresses(stepBox[k], bp, thr)) {
+            atomicOr(&struck[p >> 5], 1u << (p & 31));
+            break;
+          }
         }
       }
       __syncthreads();
     }
   }
-  if (tid == 0) {
-    outcnt[img] = min(nout, maxdet);
+  __syncthreads();
+
+  // 5. output slots: exclusive prefix count of kept flags in rank order (thread t owns
+  //    ranks 2t, 2t+1); records come from the candidate array
+  const int r0 = 2 * tid, r1 = 2 * tid + 1;
+  const int f0 = r0 < m ? (removed[r0 >> 5] >> (r0 & 31)) & 1 : 0;
+  const int f1 = r1 < m ? (removed[r1 >> 5] >> (r1 & 31)) & 1 : 0;
+  const int v = f0 + f1;
+  int incl = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int off = 0;
+  for (int w = 0; w < wave; w++) off += wsum[w];
+  const int ex = off + incl - v;
+  auto emit = [&](int i, int slot) {
+    const int an = keyAnchor(skey[i]);
+    const float* rec = cimg + (size_t)an * cstride;
+    float* d = out + ((size_t)img * MAX_OUT + slot) * 6;
+    d[0] = rec[0]; d[1] = rec[1]; d[2] = rec[2]; d[3] = rec[3];
+    d[4] = __uint_as_float((unsigned)(skey[i] >> 32));
+    d[5] = (float)scls[i];
+    outidx[img * MAX_OUT + slot] = an;
+  };
+  if (f0 && ex < maxdet) emit(r0, ex);
+  if (f1 && ex + f0 < maxdet) emit(r1, ex + f0);
+  if (tid == NMS_THREADS - 1) {
+    outcnt[img] = min(off + incl, maxdet);
     rawcnt[img] = n;
     counts[img] = 0;   // re-arm the decode list for the next frame
   }
