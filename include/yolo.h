@@ -122,7 +122,9 @@ int yolo_op_config(void* h, int k);
 int yolo_set_op_config(void* h, int k, int cfg);   /* also resets the op's split-K to 1 */
 /* Split-K factor of a GEMM CONV op (autotuned at create, 1 = none) and an override: the K
  * stages are divided over `splits` blocks per output tile whose fp32 partials are summed in
- * split order (deterministic).  The override is refused (-1) once graphs are captured
+ * split order (deterministic).  A negative value -S is a tail split: the output tiles that
+ * fill whole waves of the chip run unsplit and only the remaining tiles (the part-empty last
+ * wave) are split S ways.  The override is refused (-1) once graphs are captured
  * (YOLO_NOGRAPH handles only), for non-GEMM ops and for splits that leave a block empty. */
 int yolo_op_split(void* h, int k);
 int yolo_set_op_split(void* h, int k, int splits);

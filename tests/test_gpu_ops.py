@@ -255,6 +255,50 @@ def test_conv_split_k(tmp_path, shape):
     eng.close()
 
 
+def test_conv_tail_split(tmp_path):
+    """Tail split (negative split factor): the tiles of whole chip waves run unsplit and only
+    the part-empty last wave is split, at the max batch (4) and at smaller batches that reuse
+    the same setting (1 and 3: grids of less than a wave).  Every result is within the
+    per-op bar of the oracle, bit-identical across launches, and within fp32 summation-order
+    noise of the unsplit launch."""
+    H, W, cin, cout, k, s = 80, 80, 64, 64, 3, 1
+    d = str(tmp_path / "tail")
+    modelgen.write_single_conv(d, H, W, cin, cout, k, s, seed=9)
+    g = graphfile.load(d)
+    Bmax = 4
+    x = np.random.default_rng(3).standard_normal((Bmax, H, W, cin), dtype=np.float32).astype(np.float16)
+    eng = yolort.Engine(d, Bmax, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    eng.write(0, x)
+    ref = interp.Interp(g, Bmax)
+    ref.set_input(x.astype(np.float32))
+    ref.run_op(g.ops[0])
+    want = ref.view(g.ops[0].out)
+    tried = 0
+    for cfg in (17, 12, 7, 5, 16):
+        for B in (Bmax, 1, 3):
+            eng.set_op_config(0, cfg)
+            eng.run_op(0, B)
+            base = eng.read(g.ops[0].out, B)
+            for S in (-2, -3, -5, -8):
+                try:
+                    eng.set_op_split(0, S)
+                except ValueError:
+                    continue
+                assert eng.op_split(0) == S
+                eng.run_op(0, B)
+                got1 = eng.read(g.ops[0].out, B)
+                eng.run_op(0, B)
+                got2 = eng.read(g.ops[0].out, B)
+                assert np.array_equal(got1, got2), (cfg, B, S)
+                rel = post.rel_err(got1.astype(np.float32), want[:B])
+                print(f"cfg {cfg} B {B} S {S}: rel {rel:.2e}", flush=True)
+                assert rel <= TOL, (cfg, B, S, rel)
+                assert post.rel_err(got1.astype(np.float32), base.astype(np.float32)) <= 2e-3
+                tried += 1
+    assert tried >= 20
+    eng.close()
+
+
 @pytest.mark.parametrize("cout", [16, 32, 48, 96, 160, 256, 24])
 def test_conv_first(tmp_path, cout):
     """The stem conv (Cin 3, 3x3 s2): the MFMA kernel (Cout % 16 == 0, paired 16-byte stores

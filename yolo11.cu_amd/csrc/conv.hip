@@ -43,6 +43,8 @@
 //    a startup autotuner.
 #include "engine.hpp"
 
+#include <algorithm>
+
 namespace yolo {
 
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
@@ -111,7 +113,7 @@ template <int BM, int BN, int WM, int WN, int BK, int NS, bool KONE>
 __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     View x, View y, View r, const f16* __restrict__ w, const float* __restrict__ bias,
     int ksz, int cs, int cp, int act, int M, int N, int Ktot, int mtiles, int ntiles,
-    int xbytes, int splits, int spl, float* __restrict__ ws, int* __restrict__ cnt) {
+    int xbytes, int dp, int splits, int spl, float* __restrict__ ws, int* __restrict__ cnt) {
   constexpr int NW = WM * WN, NT = 64 * NW;
   constexpr int TM = BM / WM, TN = BN / WN;  // wave tile: pixels x channels
   constexpr int FM = TM / 16, FN = TN / 16;
@@ -129,12 +131,26 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
 
   __shared__ f16x8 ring[NS * SZ];   // NS stages of SZ chunks
 
-  // ---- block id -> (m tile, n tile): per-XCD contiguous ranges, N fastest
-  // split-K: blocks [s*nblk, (s+1)*nblk) take K stages [s*spl, s*spl + spl)
+  // ---- block id -> (m tile, n tile): per-XCD contiguous ranges, N fastest.
+  // Blocks [0, dp) each own a whole output tile (tiles 0 .. dp-1).  The remaining
+  // rem = nblk - dp tiles ("tail") are split over `splits` blocks each: block
+  // dp + s*rem + j takes K stages [s*spl, s*spl + spl) of tail tile j.  dp = nblk is plain
+  // data-parallel, dp = 0 split-K over every tile; a dp of whole chip waves leaves the
+  // last wave to the split tail, so it fills the chip instead of running part-empty.
   const int nblk = mtiles * ntiles;
-  const int split = blockIdx.x / nblk;
-  int id = blockIdx.x - split * nblk;
-  if (nblk >= 2 * NUM_XCD && nblk % NUM_XCD == 0) id = (id % NUM_XCD) * (nblk / NUM_XCD) + id / NUM_XCD;
+  const int rem = nblk - dp;
+  const bool tail = (int)blockIdx.x >= dp;
+  int split = 0, tsl = 0, id;
+  if (!tail) {
+    id = blockIdx.x;
+    if (dp >= 2 * NUM_XCD && dp % NUM_XCD == 0) id = (id % NUM_XCD) * (dp / NUM_XCD) + id / NUM_XCD;
+  } else {
+    const int q = blockIdx.x - dp;
+    split = q / rem;
+    tsl = q - split * rem;
+    if (rem >= 2 * NUM_XCD && rem % NUM_XCD == 0) tsl = (tsl % NUM_XCD) * (rem / NUM_XCD) + tsl / NUM_XCD;
+    id = dp + tsl;
+  }
   const int mt = id / ntiles, nt = id - mt * ntiles;
   const int bm = mt * BM, bn = nt * BN;
 
@@ -193,7 +209,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   // (ky, kx, ci) its tap and channel, toff = its element offset from the pixel's (0, 0) tap.
   const int Cin = x.C;
   const bool cbmajor = !KONE && ksz > 1 && Cin % BK == 0;
-  const int st0 = split * spl;   // first K stage of this block
+  const int nkt = (Ktot + BK - 1) / BK;         // K stages of a whole tile
+  const int st0 = tail ? split * spl : 0;       // first K stage of this block
   int kw = st0 * BK + 8 * c;
   int ci = 0, kx = 0, ky = 0, toff = 0;
   if (!KONE) {
@@ -303,7 +320,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     });
   };
 
-  const int nks = min((Ktot + BK - 1) / BK - st0, spl);   // this block's stages (>= 1)
+  const int nks = tail ? min(nkt - st0, spl) : nkt;   // this block's stages (>= 1)
   // Small wave tiles fetch their epilogue bias now, so its latency hides behind the K loop
   // (for short-K convs it would otherwise be a full extra global round trip at the end).
   // Lane channels: fragment i of a pair p holds n0(p) + 4h .. +3; unpaired: n0(i) .. +3.
@@ -358,18 +375,17 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   // layout, 16-byte stores), then the last block to arrive for the tile (device-scope
   // counter) sums all partials in split order -- deterministic whatever the arrival order --
   // resets the counter for the next launch and runs the epilogue.
-  if (splits > 1) {
+  if (tail && splits > 1) {
     __shared__ int lastBlock;
-    const int tile = mt * ntiles + nt;
     constexpr int TILE = BM * BN;
 #pragma unroll
     for (int i = 0; i < FN; i++)
 #pragma unroll
       for (int j = 0; j < FM; j++)
-        *(f32x4*)(ws + ((size_t)split * nblk + tile) * TILE + ((i * FM + j) * NT + t) * 4) = acc[i][j];
+        *(f32x4*)(ws + ((size_t)split * rem + tsl) * TILE + ((i * FM + j) * NT + t) * 4) = acc[i][j];
     __threadfence();
     __syncthreads();
-    if (t == 0) lastBlock = atomicAdd(&cnt[tile], 1) == splits - 1;
+    if (t == 0) lastBlock = atomicAdd(&cnt[tsl], 1) == splits - 1;
     __syncthreads();
     if (!lastBlock) return;
     __threadfence();
@@ -379,11 +395,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     for (int i = 0; i < FN; i++)
 #pragma unroll
       for (int j = 0; j < FM; j++) {
-        const float* src = ws + (size_t)tile * TILE + ((i * FM + j) * NT + t) * 4;
+        const float* src = ws + (size_t)tsl * TILE + ((i * FM + j) * NT + t) * 4;
         acc[i][j] = *(const f32x4*)src;
-        for (int sp = 1; sp < splits; sp++) acc[i][j] += *(const f32x4*)(src + (size_t)sp * nblk * TILE);
+        for (int sp = 1; sp < splits; sp++) acc[i][j] += *(const f32x4*)(src + (size_t)sp * rem * TILE);
       }
-    if (t == 0) cnt[tile] = 0;
+    if (t == 0) cnt[tsl] = 0;
   }
 
   // ---- epilogue
@@ -482,7 +498,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   X(26, 64, 32, 2, 2, 64, 8)          \
   X(27, 64, 64, 2, 2, 64, 6)          \
   X(28, 32, 32, 2, 2, 128, 4)         \
-  X(29, 64, 16, 4, 1, 128, 5)
+  X(29, 64, 16, 4, 1, 128, 5)         \
+  X(30, 256, 256, 2, 2, 64, 2)
 
 static const TileCfg kTiles[] = {
 #define X(i, bm, bn, wm, wn, bk, ns) {bm, bn, wm, wn, bk, ns},
@@ -522,18 +539,75 @@ int heuristicTile(int M, int N, int K) {
   return best < 0 ? 17 : best;
 }
 
+// Blocks of one tile config that fit on the chip at once (CUs x resident blocks per CU).
+template <int BM, int BN, int WM, int WN, int BK, int NS>
+static int tileSlotsOf(bool kone) {
+  static const int slots[2] = {
+      [] {
+        int dev = 0, cus = 0, per = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_conv_gemm<BM, BN, WM, WN, BK, NS, false>,
+                                                         64 * WM * WN, 0) != hipSuccess)
+          return 0;
+        return cus * per;
+      }(),
+      [] {
+        int dev = 0, cus = 0, per = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_conv_gemm<BM, BN, WM, WN, BK, NS, true>,
+                                                         64 * WM * WN, 0) != hipSuccess)
+          return 0;
+        return cus * per;
+      }()};
+  return slots[kone ? 1 : 0];
+}
+
 template <int BM, int BN, int WM, int WN, int BK, int NS>
 static void launchTile(bool kone, const View& x, const View& y, const View& r, const f16* w,
                        const float* bias, int k, int s, int p, int act, int M, int N, int Ktot,
-                       int xbytes, int splits, float* ws, int* cnt, hipStream_t st) {
+                       int xbytes, int dp, int splits, float* ws, int* cnt, hipStream_t st) {
   const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
   const int spl = splitStages(Ktot, BK, splits);
+  const int grid = dp + (mt * nt - dp) * splits;
   if (kone)
-    k_conv_gemm<BM, BN, WM, WN, BK, NS, true><<<mt * nt * splits, 64 * WM * WN, 0, st>>>(
-        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, splits, spl, ws, cnt);
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, true><<<grid, 64 * WM * WN, 0, st>>>(
+        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, dp, splits, spl, ws, cnt);
   else
-    k_conv_gemm<BM, BN, WM, WN, BK, NS, false><<<mt * nt * splits, 64 * WM * WN, 0, st>>>(
-        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, splits, spl, ws, cnt);
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, false><<<grid, 64 * WM * WN, 0, st>>>(
+        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, dp, splits, spl, ws, cnt);
+}
+
+int tileSlots(int cfg, bool kone) {
+  switch (cfg) {
+#define X(i, bm, bn, wm, wn, bk, ns) \
+    case i: return tileSlotsOf<bm, bn, wm, wn, bk, ns>(kone);
+    YOLO_TILES(X)
+#undef X
+    default: return 0;
+  }
+}
+
+// Split mode of a launch.  splits > 1: every tile split that many ways (dp = 0).
+// splits < -1 ("tail split"): the tiles that fill whole chip waves run unsplit and only the
+// rest -- fewer than one wave -- are split |splits| ways (when every tile fits in one wave,
+// the split is capped so the grid stays within one wave).  Otherwise no split (dp = tiles).
+void splitPlan(int cfg, bool kone, int tiles, int splits, int* dp, int* S) {
+  *dp = tiles;
+  *S = 1;
+  if (splits > 1) {
+    *dp = 0;
+    *S = splits;
+  } else if (splits < -1) {
+    const int P = tileSlots(cfg, kone);
+    if (P <= 0) return;
+    const int full = tiles / P * P;
+    if (full == tiles) return;
+    *dp = full;
+    *S = full > 0 ? -splits : std::max(1, std::min(-splits, P / tiles));
+    if (*S == 1) *dp = tiles;
+  }
 }
 
 // Byte offsets into the input and weight tensors are 32-bit buffer offsets; the loader
@@ -546,18 +620,27 @@ int splitStages(int Ktot, int BK, int splits) {
 }
 bool splitOk(int cfg, int Ktot, int splits) {
   if (splits == 1) return true;
-  if (cfg < 0 || cfg >= kNumTiles || splits < 1 || splits > MAX_SPLITS) return false;
+  const int S = splits < 0 ? -splits : splits;
+  if (cfg < 0 || cfg >= kNumTiles || S < 2 || S > MAX_SPLITS) return false;
   const int nks = (Ktot + kTiles[cfg].BK - 1) / kTiles[cfg].BK;
-  const int spl = splitStages(Ktot, kTiles[cfg].BK, splits);
-  return spl >= 1 && (splits - 1) * spl < nks;   // every split gets at least one stage
+  const int spl = splitStages(Ktot, kTiles[cfg].BK, S);
+  return spl >= 1 && (S - 1) * spl < nks;   // every split gets at least one stage
 }
-size_t splitWorkspaceBytes(int cfg, int M, int N, int splits) {
-  if (splits <= 1 || cfg < 0 || cfg >= kNumTiles) return 0;
+int splitTiles(int cfg, bool kone, int M, int N, int splits) {
+  if (cfg < 0 || cfg >= kNumTiles || splits == 1 || splits == -1) return 0;
   const TileCfg& tc = kTiles[cfg];
-  const size_t tiles = (size_t)((M + tc.BM - 1) / tc.BM) * ((N + tc.BN - 1) / tc.BN);
-  return tiles * splits * tc.BM * tc.BN * sizeof(float);
+  const int tiles = ((M + tc.BM - 1) / tc.BM) * ((N + tc.BN - 1) / tc.BN);
+  if (splits > 1) return tiles;
+  // tail split at this M or any smaller batch: fewer tiles than one chip wave are split
+  return std::min(tiles, std::max(tileSlots(cfg, kone), 1));
 }
-int splitTiles(int cfg, int M, int N) {
+size_t splitWorkspaceBytes(int cfg, bool kone, int M, int N, int splits) {
+  const size_t t = (size_t)splitTiles(cfg, kone, M, N, splits);
+  if (t == 0) return 0;
+  const TileCfg& tc = kTiles[cfg];
+  return t * (size_t)(splits < 0 ? -splits : splits) * tc.BM * tc.BN * sizeof(float);
+}
+int numTiles(int cfg, int M, int N) {
   const TileCfg& tc = kTiles[cfg];
   return ((M + tc.BM - 1) / tc.BM) * ((N + tc.BN - 1) / tc.BN);
 }
@@ -570,10 +653,12 @@ void launchConvGemm(int cfg, const View& x, const View& y, const View* res, cons
   const int xbytes = (int)((long)Bn * x.H * x.W * x.s * 2);
   View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
   if (cfg < 0 || cfg >= kNumTiles) cfg = heuristicTile(M, N, Ktot);
-  if (splits < 1 || !ws || !cnt || !splitOk(cfg, Ktot, splits)) splits = 1;
+  if (!ws || !cnt || !splitOk(cfg, Ktot, splits)) splits = 1;
+  int dp, S;
+  splitPlan(cfg, kone, numTiles(cfg, M, N), splits, &dp, &S);
   switch (cfg) {
 #define X(i, bm, bn, wm, wn, bk, ns) \
-    case i: launchTile<bm, bn, wm, wn, bk, ns>(kone, x, y, r, w, bias, k, s, p, act, M, N, Ktot, xbytes, splits, ws, cnt, st); break;
+    case i: launchTile<bm, bn, wm, wn, bk, ns>(kone, x, y, r, w, bias, k, s, p, act, M, N, Ktot, xbytes, dp, S, ws, cnt, st); break;
     YOLO_TILES(X)
 #undef X
     default: break;

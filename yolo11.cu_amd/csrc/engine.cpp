@@ -504,14 +504,15 @@ struct Engine {
     size_t wsTot = 0, cntTot = 0;
     for (OpDesc& op : ops) {
       op.wsOff = op.cntOff = -1;
-      if (op.kind != CONV || op.g != 1 || op.Cin == 3 || op.split <= 1) continue;
+      if (op.kind != CONV || op.g != 1 || op.Cin == 3 || op.split == 1 || op.split == -1) continue;
       View y = view(op.out);
       const int M = B * y.H * y.W, cfg = op.cfg >= 0 ? op.cfg : heuristicTile(M, op.Cout, op.k * op.k * op.Cin);
+      const bool kone = op.k == 1 && op.s == 1 && op.p == 0;
       op.cfg = cfg;
       op.wsOff = (long)(wsTot / sizeof(float));
       op.cntOff = (long)cntTot;
-      wsTot += (splitWorkspaceBytes(cfg, M, op.Cout, op.split) + 255) & ~(size_t)255;
-      cntTot += splitTiles(cfg, M, op.Cout);
+      wsTot += (splitWorkspaceBytes(cfg, kone, M, op.Cout, op.split) + 255) & ~(size_t)255;
+      cntTot += splitTiles(cfg, kone, M, op.Cout, op.split);
     }
     ensureSplitScratch(wsTot, cntTot);
   }
@@ -519,7 +520,9 @@ struct Engine {
   // ---------------------------------------------------------------- autotune
   // Time every eligible (tile shape, split-K factor) of every GEMM conv at the max batch
   // (2 warm-up launches, then the median of 7 individually timed ones) and keep the
-  // fastest; identical shapes share one measurement.  Splits are tried only while the tile grid leaves CUs idle.
+  // fastest; identical shapes share one measurement.  Splits of every tile are tried only
+  // while the tile grid is less than one chip wave; a grid of more than one wave whose last
+  // wave is part-empty tries tail splits that fill that wave.
   void autotune() {
     hipEvent_t e0, e1;
     HCK(hipEventCreate(&e0));
@@ -548,15 +551,27 @@ struct Engine {
       if (it != cache.end()) { op.cfg = it->second.first; op.split = it->second.second; continue; }
       int best = heuristicTile(M, N, K), bestSplit = 1;
       float bestMs = 1e30f;
+      const bool kone = op.k == 1 && op.s == 1 && op.p == 0;
       for (int cfg = 0; cfg < numTileConfigs(); cfg++) {
         if (!allowed[cfg] || !tileOk(cfg, M, N, K)) continue;
-        const int tiles = splitTiles(cfg, M, N);
-        for (int S : kSplits) {
-          if (S > 1 && (tiles * S > 1024 || tiles >= 256 || !splitOk(cfg, K, S))) continue;
+        const int tiles = numTiles(cfg, M, N), P = tileSlots(cfg, kone);
+        std::vector<int> cands;
+        for (int S : kSplits)
+          if (S == 1 || (tiles * S <= 1024 && tiles < P)) cands.push_back(S);
+        if (P > 0 && tiles > P && tiles % P != 0) {
+          // tail split: the part-empty last wave of `rem` tiles becomes ~P/rem times as
+          // many blocks, each with 1/S of the K stages
+          const int S = std::min(P / (tiles % P), MAX_SPLITS);
+          if (S >= 2) cands.push_back(-S);
+        }
+        std::sort(cands.begin(), cands.end());
+        cands.erase(std::unique(cands.begin(), cands.end()), cands.end());
+        for (int S : cands) {
+          if (S != 1 && !splitOk(cfg, K, S)) continue;
           op.cfg = cfg;
           op.split = S;
-          op.wsOff = op.cntOff = S > 1 ? 0 : -1;
-          if (S > 1) ensureSplitScratch(splitWorkspaceBytes(cfg, M, N, S), (size_t)tiles);
+          op.wsOff = op.cntOff = S != 1 ? 0 : -1;
+          if (S != 1) ensureSplitScratch(splitWorkspaceBytes(cfg, kone, M, N, S), (size_t)splitTiles(cfg, kone, M, N, S));
           for (int r = 0; r < 2; r++) runOp((int)k, B);
           float t[7];
           for (int r = 0; r < 7; r++) {
@@ -1061,7 +1076,8 @@ int yolo_set_op_split(void* h, int k, int splits) {
     const yolo::View y = e->view(op.out);
     const int M = e->B * y.H * y.W, K = op.k * op.k * op.Cin;
     const int cfg = op.cfg >= 0 ? op.cfg : yolo::heuristicTile(M, op.Cout, K);
-    if (splits < 1 || splits > yolo::MAX_SPLITS || !yolo::splitOk(cfg, K, splits)) return -1;
+    if (splits == 0 || splits > yolo::MAX_SPLITS || splits < -yolo::MAX_SPLITS || !yolo::splitOk(cfg, K, splits))
+      return -1;
     op.cfg = cfg;
     op.split = splits;
     e->assignSplits();

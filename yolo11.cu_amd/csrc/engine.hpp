@@ -27,7 +27,7 @@ struct OpDesc {
   int heads = 0, kd = 0, hd = 0;      // ATTN
   int stride = 0;                     // DECODE*
   int cfg = -1;                       // GEMM tile config (-1 = heuristic)
-  int split = 1;                      // GEMM split-K factor
+  int split = 1;                      // GEMM split-K factor (< -1: tail split, see conv.hip)
   long wsOff = -1, cntOff = -1;       // split-K workspace / counter offsets (engine-owned)
   int chain = 0;                      // MAXPOOL5: 3 = head of a fused SPPF chain,
                                       // -1 = pooled by the chain head in forward()
@@ -94,14 +94,18 @@ const TileCfg& tileConfig(int cfg);
 
 // ------------------------------------------------------------------ launchers
 // conv.hip
-// Split-K: `splits` > 1 partitions the K stages over that many blocks per output tile; `ws`
-// holds splits x tiles x BM x BN fp32 partials (splitWorkspaceBytes) and `cnt` one zeroed
-// counter per tile (splitTiles), which the kernel leaves zeroed again.
+// Split-K: `splits` > 1 partitions the K stages of every output tile over that many blocks;
+// `splits` < -1 does so only for the tiles left over after the last whole wave of the chip
+// (tail split, |splits| ways).  `ws` holds |splits| x splitTiles x BM x BN fp32 partials
+// (splitWorkspaceBytes) and `cnt` one zeroed counter per split tile (splitTiles), which the
+// kernel leaves zeroed again.  Both are sized for M and every smaller batch.
 constexpr int MAX_SPLITS = 16;
 int splitStages(int Ktot, int BK, int splits);
 bool splitOk(int cfg, int Ktot, int splits);
-size_t splitWorkspaceBytes(int cfg, int M, int N, int splits);
-int splitTiles(int cfg, int M, int N);
+int numTiles(int cfg, int M, int N);
+int tileSlots(int cfg, bool kone);
+int splitTiles(int cfg, bool kone, int M, int N, int splits);
+size_t splitWorkspaceBytes(int cfg, bool kone, int M, int N, int splits);
 void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
                     const float* bias, int k, int s, int p, int act, int Bn, int splits,
                     float* ws, int* cnt, hipStream_t st);
