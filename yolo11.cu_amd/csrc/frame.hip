@@ -205,6 +205,7 @@ void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lst, int
 //  3. the list counter is re-armed (zeroed) for the next frame.
 constexpr int NMS_THREADS = 1024;
 constexpr int NMS_CLASSES = 1024;            // class histogram size of the per-class path
+constexpr int NMS_WAVE_CLASS = 256;          // largest class one wave resolves alone
 
 // inter/union > thr, decided without the division unless the two sides are within a few
 // ulps (then the division decides, exactly as the reference writes it)
@@ -225,8 +226,9 @@ __device__ __forceinline__ bool suppresses(float4 a, float4 b, float thr) {
 
 // Selection + ranking shared by both NMS kernels.  Leaves the m = min(n, NMS_CAP) largest
 // keys of lst[0..n) in descending order in sorted[0..m):
-//  - above NMS_CAP candidates a radix select keeps the NMS_CAP largest keys (8 passes of
-//    8-bit histograms from the top byte; keys are unique, so exactly NMS_CAP are >= T).
+//  - above NMS_CAP candidates a radix select keeps the NMS_CAP largest keys (up to 8 passes
+//    of 8-bit histograms from the top byte, stopping once the selected bin holds exactly
+//    the keys still needed; keys are unique, so exactly NMS_CAP are >= T).
 //    Scores crowd into few bins, so lanes of a wave that share a bin add once
 //    (wave-aggregated atomics) instead of serialising on one LDS address;
 //  - up to 512 keys: rank = number of strictly larger keys, TPK threads (adjacent lanes)
@@ -238,7 +240,7 @@ __device__ __forceinline__ bool suppresses(float4 a, float4 b, float thr) {
 struct RankShared {
   int hist[256];
   unsigned long long prefix;
-  int need, count;
+  int need, count, done;
 };
 
 __device__ void selectAndRank(const unsigned long long* __restrict__ lst, int n,
@@ -246,7 +248,7 @@ __device__ void selectAndRank(const unsigned long long* __restrict__ lst, int n,
   const int tid = threadIdx.x, lane = tid & 63;
   const int m = min(n, NMS_CAP);
   if (n > NMS_CAP) {
-    if (tid == 0) { rs.prefix = 0ull; rs.need = NMS_CAP; rs.count = 0; }
+    if (tid == 0) { rs.prefix = 0ull; rs.need = NMS_CAP; rs.count = 0; rs.done = 0; }
     for (int p = 0; p < 8; p++) {
       const int shift = 56 - 8 * p;
       for (int i = tid; i < 256; i += NMS_THREADS) rs.hist[i] = 0;
@@ -293,9 +295,13 @@ __device__ void selectAndRank(const unsigned long long* __restrict__ lst, int n,
           }
           rs.need = need - cum;
           rs.prefix = pre | ((unsigned long long)sel << shift);
+          // the bin holds exactly the keys still needed: every key with this prefix is
+          // selected, so the prefix (lower bits zero) is already the threshold
+          if (cum + rs.hist[sel] == need) rs.done = 1;
         }
       }
       __syncthreads();
+      if (rs.done) break;   // block-uniform
     }
     const unsigned long long T = rs.prefix;
     for (int i = tid; i < n; i += NMS_THREADS) {
@@ -357,18 +363,21 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
                                                      int* __restrict__ rawcnt,
                                                      const PostParams* __restrict__ prm) {
   __shared__ unsigned long long skey[NMS_CAP];
-  __shared__ float4 sbox[NMS_CAP];                 // boxes by rank, then a class's survivors
+  __shared__ float4 sbox[NMS_CAP];                 // the rank-ordered keys during selection
   __shared__ short scls[NMS_CAP];
   __shared__ int chist[NMS_CLASSES];
   __shared__ int cstart[NMS_CLASSES];              // class-major start of a class
+  __shared__ int cfill[NMS_CLASSES];               // bucket fill counters
   __shared__ short present[NMS_CLASSES];
+  __shared__ short large[NMS_CLASSES];             // classes of more than 64 members
+  __shared__ __attribute__((aligned(16))) short bucket[NMS_CAP];   // ranks, grouped by class
   __shared__ short perm[NMS_CAP];                  // class-major position -> rank
   __shared__ float4 cbox[NMS_CAP];                 // boxes, class-major
   __shared__ unsigned long long rows2[NMS_CAP];    // chunk suppression rows, class-major
   __shared__ unsigned removed[NMS_CAP / 32];       // kept flags by rank
   __shared__ unsigned struck[NMS_CAP / 32];        // suppressed flags, class-major (large classes)
-  __shared__ float4 stepBox[64];                   // survivors of a large class's chunk
-  __shared__ int npresent, nstep, wsum[NMS_THREADS / 64];
+  __shared__ float4 stepBox[64];                   // survivors of a huge class's chunk
+  __shared__ int npresent, nlarge, nstep, wsum[NMS_THREADS / 64];
   __shared__ RankShared rs;
   static_assert(NMS_CLASSES == NMS_THREADS, "one class bin per thread");
 
@@ -379,15 +388,16 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   const int maxdet = min(prm->max_det, MAX_OUT);
   const int n = min(counts[img], A);
   const int m = min(n, NMS_CAP);
-  if (tid == 0) npresent = 0;
+  if (tid == 0) { npresent = 0; nlarge = 0; }
   chist[tid] = 0;
+  cfill[tid] = 0;
 
-  // 1. the m best keys in rank order, parked in the box array's storage; every thread then
-  //    lifts its entries (and their candidate records) into registers before the arrays
-  //    are written for good, counting classes as it writes
+  // 1. the m best keys in rank order (parked in the box array's storage); every thread
+  //    lifts its entries and their candidate records into registers, counting classes
   unsigned long long* sorted = reinterpret_cast<unsigned long long*>(sbox);
   selectAndRank(lists + (size_t)img * A, n, skey, sorted, rs);
   for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) removed[i] = 0u;
+  for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) struck[i] = 0u;
   unsigned long long kr[2] = {0ull, 0ull};
   float4 br[2];
   short cr[2] = {0, 0};
@@ -407,19 +417,20 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     const int r = tid + u * NMS_THREADS;
     if (r < m) {
       skey[r] = kr[u];
-      sbox[r] = br[u];
       scls[r] = cr[u];
       atomicAdd(&chist[cr[u]], 1);
     }
   }
   __syncthreads();
 
-  // 2. class-major layout.  Thread t owns class t: classes present and the exclusive prefix
-  //    of the histogram; then one wave per class lists the class's ranks in order (ballot
-  //    append) with their boxes
+  // 2. class-major layout (ranks grouped by class, rank order inside a class).  Thread t
+  //    owns class t: the classes present, the large ones, and the exclusive prefix of the
+  //    histogram.  Each rank then drops into its class's bucket (any order) and finds its
+  //    place in the class by counting the class members of smaller rank.
   {
     const int h = chist[tid];
     if (h > 0) present[atomicAdd(&npresent, 1)] = (short)tid;
+    if (h > 64) large[atomicAdd(&nlarge, 1)] = (short)tid;
     int incl = h;
     for (int o = 1; o < 64; o <<= 1) {
       const int y = __shfl_up(incl, o);
@@ -432,60 +443,88 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     cstart[tid] = off + incl - h;
   }
   __syncthreads();
-  for (int pc = wave; pc < npresent; pc += NMS_THREADS / 64) {
-    const int c = present[pc];
-    int g = cstart[c];
-    for (int i0 = 0; i0 < m; i0 += 64) {
-      const int i = i0 + lane;
-      const bool in = i < m && scls[i] == c;
-      const unsigned long long bal = __ballot(in);
-      if (in) {
-        const int p = g + __popcll(bal & ((1ull << lane) - 1ull));
-        perm[p] = (short)i;
-        cbox[p] = sbox[i];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int r = tid + u * NMS_THREADS;
+    if (r < m) bucket[cstart[cr[u]] + atomicAdd(&cfill[cr[u]], 1)] = (short)r;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int r = tid + u * NMS_THREADS;
+    if (r < m) {
+      const int sc = cstart[cr[u]], se = sc + chist[cr[u]];
+      int below = 0;
+      for (int c8 = sc & ~7; c8 < se; c8 += 8) {     // 16-byte reads of the class's bucket
+        const short4 lo = *reinterpret_cast<const short4*>(&bucket[c8]);
+        const short4 hi = *reinterpret_cast<const short4*>(&bucket[c8 + 4]);
+        const short v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) below += (c8 + e >= sc && c8 + e < se && v[e] < r) ? 1 : 0;
       }
-      g += __popcll(bal);
+      perm[sc + below] = (short)r;
+      cbox[sc + below] = br[u];
     }
   }
   __syncthreads();
 
-  // 3. suppression rows, block-parallel.  A class is decided in chunks of 64 members;
-  //    rows2[p] holds the later members of p's chunk that p suppresses.  Wave w takes a
-  //    contiguous run of positions; lane L first loads the box and chunk geometry of one
-  //    position of the run, and the loop broadcasts them with readlane, so the only LDS
-  //    loads in the loop are a chunk's boxes when the chunk changes.
-  {
-    const int per = (m + NMS_THREADS / 64 - 1) / (NMS_THREADS / 64);
-    const int pb = wave * per, pe = min(m, pb + per);
-    int chunk0 = -1, nqc = 0;
-    float4 bj = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int sub = pb; sub < pe; sub += 64) {
-      const int p = sub + lane;
-      int q0 = 0, nq = 0, al = 0;
-      float4 bp = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (p < pe) {
-        const int c = scls[perm[p]];
-        const int sc = cstart[c], a = p - sc;
-        q0 = sc + (a & ~63);
-        nq = min(64, chist[c] - (a & ~63));
-        al = a & 63;
-        bp = cbox[p];
+  // 3. suppression rows.  A class is decided in chunks of 64 members; rows2[p] holds the
+  //    later members of p's chunk that p suppresses.  Up to 512 candidates the work items
+  //    are (chunk, run of 8 positions): a wave takes items round-robin, lane j holds member
+  //    j of the chunk, and each position's row is one ballot (its box read as an LDS
+  //    broadcast); a class has ceil(g / 8) items (chunk boundaries fall on multiples of 8).
+  //    Above that every thread is busy anyway and one thread per position tests only the
+  //    later members of its chunk (half the tests of a square ballot).
+  if (m > 512) {
+    for (int p = tid; p < m; p += NMS_THREADS) {
+      const int c = scls[perm[p]];
+      const int sc = cstart[c], a = p - sc;
+      const int q0 = sc + (a & ~63), nq = min(64, chist[c] - (a & ~63));
+      const float4 bp = cbox[p];
+      unsigned long long row = 0ull;
+      for (int j = (a & 63) + 1; j < nq; j++)
+        if (suppresses(bp, cbox[q0 + j], thr)) row |= 1ull << j;
+      rows2[p] = row;
+    }
+  } else {
+    {
+      // the items of class c start at cfill[c] = exclusive prefix of ceil(chist / 8)
+      const int h = (chist[tid] + 7) >> 3;
+      int incl = h;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
       }
-      const int cnt = min(64, pe - sub);
-      for (int k = 0; k < cnt; k++) {
-        const int qk = __builtin_amdgcn_readlane(q0, k);
-        if (qk != chunk0) {
-          chunk0 = qk;
-          nqc = __builtin_amdgcn_readlane(nq, k);
-          if (lane < nqc) bj = cbox[qk + lane];
+      if (lane == 63) wsum[wave] = incl;
+      __syncthreads();
+      int off = 0;
+      for (int w = 0; w < wave; w++) off += wsum[w];
+      cfill[tid] = off + incl - h;             // cfill is free again: item start of class tid
+      if (tid == NMS_THREADS - 1) nstep = off + incl;
+    }
+    __syncthreads();
+    {
+      const int nitems = nstep;
+      for (int it = wave; it < nitems; it += NMS_THREADS / 64) {
+        // the class owning item `it`: the present class whose item range holds it
+        int c = -1;
+        for (int q = lane; q < npresent; q += 64) {
+          const int cq = present[q];
+          const int i0 = cfill[cq];
+          if (it >= i0 && it < i0 + ((chist[cq] + 7) >> 3)) c = cq;
         }
-        const float4 bi = make_float4(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.x), k)),
-                                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.y), k)),
-                                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.z), k)),
-                                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bp.w), k)));
-        const int ak = __builtin_amdgcn_readlane(al, k);
-        const unsigned long long row = __ballot(lane < nqc && lane > ak && suppresses(bi, bj, thr));
-        if (lane == 0) rows2[sub + k] = row;
+        const unsigned long long hb = __ballot(c >= 0);
+        c = __builtin_amdgcn_readlane(c, __builtin_ctzll(hb));
+        const int sc = cstart[c], g = chist[c];
+        const int a0 = (it - cfill[c]) * 8;    // first class member of the item
+        const int q0 = a0 & ~63, nq = min(64, g - q0);
+        const float4 bq = lane < nq ? cbox[sc + q0 + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int pe = min(a0 + 8, g);
+        for (int a = a0; a < pe; a++) {
+          const float4 bp = cbox[sc + a];      // LDS broadcast
+          const unsigned long long row = __ballot(lane < nq && lane > (a & 63) && suppresses(bp, bq, thr));
+          if (lane == 0) rows2[sc + a] = row;
+        }
       }
     }
   }
@@ -493,7 +532,7 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
 
   // 4. per-class greedy.  `removed` holds the kept flag of every candidate by rank.
   //  4a. a class of at most 64 members is one chunk: one wave resolves its rows by a bit
-  //      scan (waves take the small classes round-robin)
+  //      scan (waves take the classes round-robin)
   for (int pc = wave; pc < npresent; pc += NMS_THREADS / 64) {
     const int c = present[pc];
     const int sc = cstart[c], g = chist[c];
@@ -511,17 +550,60 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     }
     if ((keep >> lane) & 1ull) atomicOr(&removed[mine >> 5], 1u << (mine & 31));
   }
-  //  4b. a larger class goes chunk by chunk with the whole block: wave 0 resolves the chunk
-  //      (members struck by earlier chunks excluded), then every thread strikes later
-  //      members of the class that a survivor of the chunk suppresses (survivor boxes read
-  //      as LDS broadcasts).  A class stops once it has max_det survivors: a later survivor
-  //      of the class ranks below max_det others and never reaches the output.
-  for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) struck[i] = 0u;
-  __syncthreads();
-  for (int pc = 0; pc < npresent; pc++) {
-    const int c = present[pc];
+  //  4b. a class of 65 .. NMS_WAVE_CLASS members: one wave, chunk by chunk -- the chunk is
+  //      resolved by a bit scan (members struck by earlier chunks excluded), then the lanes
+  //      strike the class's later members that a survivor of the chunk suppresses
+  //      (survivor boxes broadcast by readlane).  Waves take such classes round-robin; a
+  //      class stops once it has max_det survivors (a later survivor ranks below max_det
+  //      others and never reaches the output).
+  for (int li = wave; li < nlarge; li += NMS_THREADS / 64) {
+    const int c = large[li];
     const int sc = cstart[c], g = chist[c];
-    if (g <= 64) continue;                  // block-uniform
+    if (g > NMS_WAVE_CLASS) continue;       // wave-uniform: 4c below
+    int K = 0;
+    for (int q0 = 0; q0 < g && K < maxdet; q0 += 64) {
+      const int gq = min(64, g - q0);
+      const int p = sc + q0 + lane;
+      const bool valid = lane < gq;
+      const int mine = valid ? perm[p] : 0;
+      const unsigned long long row = valid ? rows2[p] : 0ull;
+      const float4 bx = valid ? cbox[p] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const bool gone = valid && ((struck[p >> 5] >> (p & 31)) & 1u);
+      unsigned long long todo = (gq >= 64 ? ~0ull : ((1ull << gq) - 1ull)) & ~__ballot(gone), keep = 0ull;
+      while (todo) {
+        const int t = __builtin_ctzll(todo);
+        keep |= 1ull << t;
+        const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, t);
+        const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), t);
+        todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << t));
+      }
+      if ((keep >> lane) & 1ull) atomicOr(&removed[mine >> 5], 1u << (mine & 31));
+      K += __popcll(keep);
+      for (int p0 = sc + q0 + 64; p0 < sc + g; p0 += 64) {
+        const int pp = p0 + lane;
+        bool live = pp < sc + g && !((struck[pp >> 5] >> (pp & 31)) & 1u);
+        const float4 bq = live ? cbox[pp] : make_float4(0.f, 0.f, 0.f, 0.f);
+        bool hit = false;
+        for (unsigned long long kk = keep; kk && __ballot(live && !hit); kk &= kk - 1ull) {
+          const int t = __builtin_ctzll(kk);
+          const float4 bi = make_float4(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.x), t)),
+                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.y), t)),
+                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.z), t)),
+                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.w), t)));
+          if (live && !hit && suppresses(bi, bq, thr)) hit = true;
+        }
+        if (hit) atomicOr(&struck[pp >> 5], 1u << (pp & 31));
+      }
+    }
+  }
+  __syncthreads();
+  //  4c. a larger class goes chunk by chunk with the whole block: wave 0 resolves the chunk,
+  //      then every thread strikes later members of the class that a survivor of the chunk
+  //      suppresses (survivor boxes read as LDS broadcasts)
+  for (int li = 0; li < nlarge; li++) {
+    const int c = large[li];
+    const int sc = cstart[c], g = chist[c];
+    if (g <= NMS_WAVE_CLASS) continue;      // block-uniform
     int K = 0;
     for (int q0 = 0; q0 < g && K < maxdet; q0 += 64) {
       const int gq = min(64, g - q0);
@@ -530,8 +612,8 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
         const bool valid = lane < gq;
         const int mine = valid ? perm[p] : 0;
         const unsigned long long row = valid ? rows2[p] : 0ull;
-        const bool rem = valid && ((struck[p >> 5] >> (p & 31)) & 1u);
-        unsigned long long todo = (gq >= 64 ? ~0ull : ((1ull << gq) - 1ull)) & ~__ballot(rem), keep = 0ull;
+        const bool gone = valid && ((struck[p >> 5] >> (p & 31)) & 1u);
+        unsigned long long todo = (gq >= 64 ? ~0ull : ((1ull << gq) - 1ull)) & ~__ballot(gone), keep = 0ull;
         while (todo) {
           const int t = __builtin_ctzll(todo);
           keep |= 1ull << t;
