@@ -162,14 +162,16 @@ def test_conv_edge_shapes(tmp_path, shape, res):
     eng.close()
 
 
-@pytest.mark.parametrize("H,W,heads", [(20, 20, 2), (7, 7, 3), (20, 20, 6), (32, 32, 2), (5, 13, 1)])
-def test_attention_op(tmp_path, H, W, heads):
-    """ATTN alone: N = 400 (640 input), N = 49 / 65 (ragged key chunks), N = 1024."""
+@pytest.mark.parametrize("H,W,heads,B", [(20, 20, 2, 2), (7, 7, 3, 2), (20, 20, 6, 2), (32, 32, 2, 2),
+                                         (5, 13, 1, 2), (20, 20, 6, 8), (20, 20, 6, 24), (7, 7, 3, 40)])
+def test_attention_op(tmp_path, H, W, heads, B):
+    """ATTN alone: N = 400 (640 input), N = 49 / 65 (ragged key chunks, key parts with no
+    chunk), N = 1024 (streamed keys); grids of up to 128 / 512 / more blocks (4, 2 and 1 key
+    parts per query group)."""
     kd, hd = 32, 64
     d = str(tmp_path / "attn")
     modelgen.write_attention(d, H, W, heads, kd, hd)
     g = graphfile.load(d)
-    B = 2
     x = (np.random.default_rng(H * W).standard_normal((B, H, W, heads * (2 * kd + hd)), dtype=np.float32)
          * 2).astype(np.float16)
     eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
@@ -179,7 +181,7 @@ def test_attention_op(tmp_path, H, W, heads):
     got = eng.read(op.out, B).astype(np.float32)
     want = interp.attention(x.astype(np.float32), heads, kd, hd)
     rel = post.rel_err(got, want)
-    print(f"attention {H}x{W} heads={heads}: rel {rel:.2e}", flush=True)
+    print(f"attention {H}x{W} heads={heads} B={B}: rel {rel:.2e}", flush=True)
     assert rel <= TOL
     eng.close()
 

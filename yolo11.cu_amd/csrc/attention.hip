@@ -35,19 +35,26 @@ __device__ __forceinline__ int kswz(int row, int c) { return row * 4 + (c ^ ((ro
 // WHOLE: every key of the (image, head) is staged in LDS once (dynamic LDS, N <= ATT_WHOLE_MAX)
 // with all global loads in flight together, and the chunk loop then runs without barriers;
 // otherwise keys stream through a 64-key buffer, one barrier pair per chunk.
+// KS (WHOLE only): the key chunks of a query group are split over KS wave groups (chunks
+// kp, kp + KS, ...), each with its own online-softmax state; at the end the groups' (max,
+// sum, O) partials are merged through LDS.  Small grids (batch 1) use KS = 4, so four
+// waves share what one wave would walk alone.
 constexpr int ATT_WHOLE_MAX = 512;
 constexpr size_t ATT_WHOLE_LDS = 128 * 1024;   // dynamic LDS opt-in set by attentionInit()
 static bool attWholeOk = false;                 // the opt-in succeeded
 
-template <int HD, bool WHOLE>
-__global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int heads, float scale_log2) {
+template <int HD, bool WHOLE, int KS>
+__global__ __launch_bounds__(256 * KS) void k_attention(View qkv, View y, int N, int heads, float scale_log2) {
   constexpr int KD = 32;
   constexpr int CT = HD / 16;  // channel tiles of the output
+  constexpr int NT = 256 * KS;
+  static_assert(WHOLE || KS == 1, "key splits need every key in LDS");
   extern __shared__ f16x8 dyn[];
   __shared__ f16x8 sKs[WHOLE ? 1 : AK * 4];
   __shared__ f16 sVts[WHOLE ? 1 : HD * VT_PITCH];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int qw = wave & 3, kp = wave >> 2;   // query group, key part
   const int lr = lane & 15, lg = lane >> 4;
   const int h = blockIdx.y, img = blockIdx.z;
   const int per = 2 * KD + HD;
@@ -61,13 +68,13 @@ __global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int 
 
   // stage keys [k0, k0 + cnt) into LDS rows kbase.. (K as 4 swizzled 16-byte chunks, V^T)
   auto stage = [&](int k0, int cnt, int kbase) {
-    for (int i = t; i < cnt * 4; i += 256) {
+    for (int i = t; i < cnt * 4; i += NT) {
       const int key = i >> 2, c = i & 3;
       f16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0};
       if (k0 + key < N) kv = *(const f16x8*)(qkv.p + (imgbase + k0 + key) * qkv.s + qoff + KD + 8 * c);
       sK[kswz(kbase + key, c)] = kv;
     }
-    for (int i = t; i < cnt * (HD / 8); i += 256) {
+    for (int i = t; i < cnt * (HD / 8); i += NT) {
       const int key = i / (HD / 8), g = i - key * (HD / 8);
       f16x8 vv = {0, 0, 0, 0, 0, 0, 0, 0};
       if (k0 + key < N) vv = *(const f16x8*)(qkv.p + (imgbase + k0 + key) * qkv.s + qoff + 2 * KD + 8 * g);
@@ -77,7 +84,7 @@ __global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int 
   };
 
   // Q fragment: query lr of this wave, dims 8*lg .. 8*lg+7 (MFMA B operand)
-  const int q = blockIdx.x * AQ + wave * 16 + lr;
+  const int q = blockIdx.x * AQ + qw * 16 + lr;
   f16x8 fq = {0, 0, 0, 0, 0, 0, 0, 0};
   if (q < N) fq = *(const f16x8*)(qkv.p + (imgbase + q) * qkv.s + qoff + 8 * lg);
 
@@ -87,38 +94,50 @@ __global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int 
   for (int i = 0; i < CT; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (WHOLE) {
-    // every key at once: all global loads are issued before the first LDS store
-    constexpr int KIT = ATT_WHOLE_MAX * 4 / 256, VIT = ATT_WHOLE_MAX * (HD / 8) / 256;
-    f16x8 kv[KIT], vv[VIT];
+    // every key at once, all global loads issued before the first LDS store.  V goes in as
+    // items of 8 keys x 8 channels: 8 row loads, an in-register 8x8 transpose, and 8
+    // 16-byte V^T row stores
+    constexpr int KIT = (ATT_WHOLE_MAX * 4 + NT - 1) / NT;
+    constexpr int VIT = (ATT_WHOLE_MAX / 8 * (HD / 8) + NT - 1) / NT;
+    f16x8 kv[KIT], vv[VIT][8];
 #pragma unroll
     for (int u = 0; u < KIT; u++) {
-      const int i = t + 256 * u, key = i >> 2;
+      const int i = t + NT * u, key = i >> 2;
       kv[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
       if (key < N) kv[u] = *(const f16x8*)(qkv.p + (imgbase + key) * qkv.s + qoff + KD + 8 * (i & 3));
     }
 #pragma unroll
     for (int u = 0; u < VIT; u++) {
-      const int i = t + 256 * u, key = i / (HD / 8);
-      vv[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      if (key < N) vv[u] = *(const f16x8*)(qkv.p + (imgbase + key) * qkv.s + qoff + 2 * KD + 8 * (i % (HD / 8)));
+      const int i = t + NT * u, kb = i / (HD / 8), g = i - kb * (HD / 8);
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int key = 8 * kb + j;
+        vv[u][j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (key < N) vv[u][j] = *(const f16x8*)(qkv.p + (imgbase + key) * qkv.s + qoff + 2 * KD + 8 * g);
+      }
     }
 #pragma unroll
     for (int u = 0; u < KIT; u++) {
-      const int i = t + 256 * u, key = i >> 2;
+      const int i = t + NT * u, key = i >> 2;
       if (key < NP) sK[kswz(key, i & 3)] = kv[u];
     }
 #pragma unroll
     for (int u = 0; u < VIT; u++) {
-      const int i = t + 256 * u, key = i / (HD / 8), g = i % (HD / 8);
-      if (key < NP) {
+      const int i = t + NT * u, kb = i / (HD / 8), g = i - kb * (HD / 8);
+      if (8 * kb < NP) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) sVt[(8 * g + j) * vpitch + key] = vv[u][j];
+        for (int c = 0; c < 8; c++) {
+          f16x8 row;
+#pragma unroll
+          for (int j = 0; j < 8; j++) row[j] = vv[u][j][c];
+          *(f16x8*)(sVt + (8 * g + c) * vpitch + 8 * kb) = row;
+        }
       }
     }
     __syncthreads();
   }
 #pragma unroll 2
-  for (int ch = 0; ch < nchunk; ch++) {
+  for (int ch = kp; ch < nchunk; ch += KS) {
     const int k0 = ch * AK;
     const int kb = WHOLE ? k0 : 0;   // LDS row of this chunk's first key
     if (!WHOLE) {
@@ -178,6 +197,42 @@ __global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int 
     if (!WHOLE) __syncthreads();
   }
 
+  if constexpr (KS > 1) {
+    // merge the key parts: parts 1.. park (max, partial sum, O) in the (now free) key
+    // storage, part 0 rescales everything to the common max and adds
+    constexpr int REC = 2 + 4 * CT;   // floats per lane
+    float* park = reinterpret_cast<float*>(dyn);
+    __syncthreads();
+    if (kp > 0) {
+      float* rec = park + ((size_t)((kp - 1) * 4 + qw) * 64 + lane) * REC;
+      rec[0] = mrun;
+      rec[1] = lrun;
+#pragma unroll
+      for (int i = 0; i < CT; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) rec[2 + 4 * i + r] = oacc[i][r];
+    }
+    __syncthreads();
+    if (kp > 0) return;
+    float mt = mrun;
+#pragma unroll
+    for (int pp = 1; pp < KS; pp++) mt = fmaxf(mt, park[((size_t)((pp - 1) * 4 + qw) * 64 + lane) * REC]);
+    const float a0 = exp2f(mrun - mt);
+    lrun *= a0;
+#pragma unroll
+    for (int i = 0; i < CT; i++) oacc[i] *= a0;
+#pragma unroll
+    for (int pp = 1; pp < KS; pp++) {
+      const float* rec = park + ((size_t)((pp - 1) * 4 + qw) * 64 + lane) * REC;
+      const float ap = exp2f(rec[0] - mt);
+      lrun += rec[1] * ap;
+#pragma unroll
+      for (int i = 0; i < CT; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) oacc[i][r] += rec[2 + 4 * i + r] * ap;
+    }
+  }
+
   lrun += __shfl_xor(lrun, 16);
   lrun += __shfl_xor(lrun, 32);
   if (q >= N) return;
@@ -191,26 +246,42 @@ __global__ __launch_bounds__(256) void k_attention(View qkv, View y, int N, int 
   }
 }
 
+// dynamic LDS of a whole-key launch: the staged keys, or the merge records if larger
+template <int HD>
+static size_t attWholeLds(int N, int KS) {
+  const int NP = (N + AK - 1) / AK * AK;
+  const size_t stage = (size_t)NP * 4 * sizeof(f16x8) + (size_t)HD * (NP + 8) * sizeof(f16);
+  const size_t merge = KS > 1 ? (size_t)(KS - 1) * 4 * 64 * (2 + HD / 4) * sizeof(float) : 0;
+  return stage > merge ? stage : merge;
+}
+
 template <int HD>
 static void launchAttn(const View& qkv, const View& y, int N, int heads, float sl2, int Bn, hipStream_t st) {
   dim3 grid((N + AQ - 1) / AQ, heads, Bn);
-  const int NP = (N + AK - 1) / AK * AK;
-  const size_t lds = (size_t)NP * 4 * sizeof(f16x8) + (size_t)HD * (NP + 8) * sizeof(f16);
-  if (attWholeOk && N <= ATT_WHOLE_MAX && lds <= ATT_WHOLE_LDS)
-    k_attention<HD, true><<<grid, 256, lds, st>>>(qkv, y, N, heads, sl2);
-  else
-    k_attention<HD, false><<<grid, 256, 0, st>>>(qkv, y, N, heads, sl2);
+  const long blocks = (long)grid.x * grid.y * grid.z;
+  // key splits while the grid leaves most CUs idle
+  const int KS = blocks <= 128 ? 4 : blocks <= 512 ? 2 : 1;
+  if (attWholeOk && N <= ATT_WHOLE_MAX && attWholeLds<HD>(N, KS) <= ATT_WHOLE_LDS) {
+    const size_t lds = attWholeLds<HD>(N, KS);
+    if (KS == 4) k_attention<HD, true, 4><<<grid, 256 * 4, lds, st>>>(qkv, y, N, heads, sl2);
+    else if (KS == 2) k_attention<HD, true, 2><<<grid, 256 * 2, lds, st>>>(qkv, y, N, heads, sl2);
+    else k_attention<HD, true, 1><<<grid, 256, lds, st>>>(qkv, y, N, heads, sl2);
+  } else {
+    k_attention<HD, false, 1><<<grid, 256, 0, st>>>(qkv, y, N, heads, sl2);
+  }
 }
 
 // Whole-key kernels use more than the default 64 KiB of dynamic LDS; opt them in once per
 // process (a function attribute, not a stream operation).
 void attentionInit() {
   bool ok = true;
-#define ATT_ALLOW(HD)                                                                          \
-  ok = ok && hipFuncSetAttribute((const void*)k_attention<HD, true>,                           \
+#define ATT_ALLOW1(HD, KS)                                                                     \
+  ok = ok && hipFuncSetAttribute((const void*)k_attention<HD, true, KS>,                       \
                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)ATT_WHOLE_LDS) == hipSuccess;
+#define ATT_ALLOW(HD) ATT_ALLOW1(HD, 1) ATT_ALLOW1(HD, 2) ATT_ALLOW1(HD, 4)
   ATT_ALLOW(16) ATT_ALLOW(32) ATT_ALLOW(48) ATT_ALLOW(64) ATT_ALLOW(80) ATT_ALLOW(96) ATT_ALLOW(112) ATT_ALLOW(128)
 #undef ATT_ALLOW
+#undef ATT_ALLOW1
   (void)hipGetLastError();
   attWholeOk = ok;
 }

@@ -166,6 +166,7 @@ class Engine:
         if not self.h:
             raise RuntimeError(f"yolo_create_ex failed: {err.value.decode()}")
         self.max_batch = max_batch
+        self._getbuf = {}
 
     def close(self):
         if self.h:
@@ -246,17 +247,25 @@ class Engine:
     def sync(self):
         self.lib.yolo_sync(self.h)
 
+    def _records(self, fn, struct, nf: int, slot: int, cap: int) -> np.ndarray:
+        # the C structs are nf-1 floats then an int: read them through one reused float32
+        # buffer (a per-record Python loop costs more than the frame's NMS)
+        key = (struct, cap)
+        buf = self._getbuf.get(key)
+        if buf is None:
+            buf = self._getbuf[key] = np.empty((cap, nf), np.float32)
+        n = fn(self.h, slot, buf.ctypes.data_as(C.POINTER(struct)), cap)
+        out = buf[:n].astype(np.float64)
+        out[:, nf - 1] = buf[:n].view(np.int32)[:, nf - 1]
+        return out
+
     def get(self, slot: int = 0, cap: int = MAX_OUT) -> np.ndarray:
-        arr = (YoloDet * cap)()
-        n = self.lib.yolo_get(self.h, slot, arr, cap)
-        return np.array([(d.x1, d.y1, d.x2, d.y2, d.score, d.cls) for d in arr[:n]], np.float64).reshape(n, 6)
+        """Survivors as rows (x1, y1, x2, y2, score, cls) in original-image coords."""
+        return self._records(self.lib.yolo_get, YoloDet, 6, slot, cap)
 
     def get_obb(self, slot: int = 0, cap: int = MAX_OUT) -> np.ndarray:
         """OBB survivors as rows (cx, cy, w, h, theta, score, cls) in original-image coords."""
-        arr = (YoloObbDet * cap)()
-        n = self.lib.yolo_get_obb(self.h, slot, arr, cap)
-        return np.array([(d.x, d.y, d.w, d.h, d.angle, d.score, d.cls) for d in arr[:n]],
-                        np.float64).reshape(n, 7)
+        return self._records(self.lib.yolo_get_obb, YoloObbDet, 7, slot, cap)
 
     def raw_count(self, slot: int = 0) -> int:
         return self.lib.yolo_raw_count(self.h, slot)
