@@ -18,6 +18,8 @@ conv MFMA util %"):
   * yolo11n-obb at 1024 (15 classes, 1024x1024 frame) and yolo11n-seg at 640, batch 1:
     whole-frame graph, frame in HBM (side figures; the reference quotes 1.6 ms and 1.21 ms
     on an RTX 3060 Ti, README.md:80-81).
+  * yolo11m detect b1 with a 1080x1920 frame at IoU 0.7 and the five
+    isolated conv shapes at batch 1 and 32 (config 1): side figures.
   * cpu_baseline: the numpy fp32 per-op oracle (letterbox + every op + decode + NMS) for
     yolo11n batch 1 on this host's cores, bounded to ~15 s.
 
@@ -145,6 +147,68 @@ def bench_task(workdir, task, imgsz, nc, cls_bias, frame, steps, warmup, graph=T
     return dict(ms=ms, graph_ms=graph_ms, kept=kept, raw=raw)
 
 
+def bench_m(workdir, steps, warmup, graph=True):
+    """yolo11m detect b1, a 1080x1920 synthetic frame in HBM, whole-frame
+    graph (letterbox + net + DFL decode + NMS at conf 0.25 / IoU 0.7 / max 300)."""
+    import modelgen
+    import yolort
+    d = os.path.join(workdir, "yolo11m")
+    modelgen.write_model(d, "yolo11", "m", cls_bias=-8.0)
+    img = modelgen.synth_frame(1080, 1920, 20, 2)
+    eng = yolort.Engine(d, 1, 0 if graph else yolort.YOLO_NOGRAPH)
+    eng.set_thresholds(0.25, 0.7, 300)
+    dev = yolort.DeviceBuffer(img.nbytes)
+    eng.upload(dev, img)
+    if not graph:
+        for _ in range(warmup + steps):
+            eng.preprocess(dev.ptr, 1080, 1920, 0)
+            eng.run(1)
+            eng.get(0)
+        dev.free()
+        eng.close()
+        return None
+    eng.frame_graph([dev.ptr], [1080], [1920])
+    for _ in range(warmup):
+        eng.frame_run()
+        eng.get(0)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.frame_run()
+        dets = eng.get(0)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    graph_ms = eng.time_graph(1, 1, max(steps, 50))
+    kept, raw = len(dets), eng.raw_count(0)
+    dev.free()
+    eng.close()
+    return dict(ms=ms, graph_ms=graph_ms, kept=kept, raw=raw)
+
+
+def bench_sweep(workdir, iters):
+    """the five isolated conv shapes at batch 1 and 32 (autotuned tile and
+    split), TFLOP/s per shape from hipEvent timing on the engine stream."""
+    import numpy as np
+    import modelgen
+    import yolort
+    shapes = [(80, 80, 256, 256, 3, 1), (80, 80, 256, 512, 3, 2), (40, 40, 512, 256, 1, 1),
+              (20, 20, 512, 512, 3, 1), (20, 20, 1024, 512, 1, 1)]
+    out = {}
+    for (H, W, cin, cout, k, s) in shapes:
+        d = os.path.join(workdir, f"sweep_{H}_{cin}_{cout}_{k}_{s}")
+        modelgen.write_single_conv(d, H, W, cin, cout, k, s, seed=7)
+        Ho, Wo = (H + 2 * (k // 2) - k) // s + 1, (W + 2 * (k // 2) - k) // s + 1
+        for B in (1, 32):
+            eng = yolort.Engine(d, B, yolort.YOLO_NOGRAPH)
+            x = np.random.default_rng(11).standard_normal((B, H, W, cin), dtype=np.float32).astype(np.float16)
+            eng.write(0, x)
+            ms = float(eng.profile_ops(B, iters)[0])
+            fl = 2.0 * B * Ho * Wo * cout * k * k * cin
+            out[f"{k}x{k}s{s} {cin}->{cout} @{H}x{W} b{B}"] = {
+                "us": round(ms * 1e3, 2), "tflops": round(fl / ms / 1e9, 1),
+                "tile": eng.op_config(0), "split": eng.op_split(0)}
+            eng.close()
+    return out
+
+
 def bench_x(workdir, iters, graph=True):
     import modelgen
     import yolort
@@ -260,7 +324,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "n", "x", "conv", "obb", "seg"], default="all")
+    ap.add_argument("--only", choices=["all", "n", "x", "conv", "obb", "seg", "m", "sweep"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the same kernels stream-ordered (rocprofv3's kernel tracer "
@@ -284,6 +348,14 @@ def main():
         log("yolo11x b16 ...")
         out["x"] = bench_x(workdir, 20, not args.no_graph)
         log(out["x"])
+    if args.only in ("all", "m"):
+        log("yolo11m b1 1920x1080 e2e (IoU 0.7) ...")
+        out["m"] = bench_m(workdir, args.steps, args.warmup, not args.no_graph)
+        log(out["m"])
+    if args.only in ("all", "sweep") and not args.no_graph:
+        log("conv sweep (config 1) ...")
+        out["sweep"] = bench_sweep(workdir, 10)
+        log(out["sweep"])
     if args.only in ("all", "obb", "seg"):
         import modelgen
         if args.only in ("all", "obb"):
@@ -329,11 +401,13 @@ def main():
                               "raw_candidates": n["raw"], "stream_ops_ms": round(n["stream_ops_ms"], 4)}
     if x:
         line["yolo11x_b16"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in x.items()}
-    for key, name in (("obb", "yolo11n_obb_b1_1024"), ("seg", "yolo11n_seg_b1")):
+    for key, name in (("m", "yolo11m_b1_1080p_iou07"), ("obb", "yolo11n_obb_b1_1024"), ("seg", "yolo11n_seg_b1")):
         r = out.get(key)
         if r:
             line[name] = {"ms_per_frame": round(r["ms"], 4), "graph_ms": round(r["graph_ms"], 4),
                           "kept": r["kept"], "raw_candidates": r["raw"]}
+    if out.get("sweep"):
+        line["conv_sweep"] = out["sweep"]
     if conv:
         achieved = conv["flops"] / (conv["ms"] * 1e-3)
         line["roofline"] = {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": 2500.0,

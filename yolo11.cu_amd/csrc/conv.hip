@@ -124,6 +124,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   constexpr int NI = IA + IB;
   constexpr int SZ = (BM + BN) * CPR;        // chunks per stage: pixel rows, then weight rows
   constexpr bool PAIR = FN % 2 == 0;
+  constexpr bool PRE = KS > 1 && KS * (FN + FM) <= 15;   // all steps' fragment reads in flight
   static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be a multiple of 16");
   static_assert(NW % 4 == 0, "the per-thread chunk column is shared only for 4k waves");
   static_assert(QA % NW == 0 && QB % NW == 0, "every wave issues the same DMA count");
@@ -304,10 +305,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     static_for<FN>([&](auto I) { fa[I] = ds_read16<I * 16 * CPR * 16>(aB); });
     static_for<FM>([&](auto J) { fb[J] = ds_read16<J * 16 * CPR * 16>(aA); });
   };
-  // LDS returns in order: column j of MFMAs starts as soon as fb[j] has landed
-  auto mfmas = [&](f16x8 (&fa)[FN], f16x8 (&fb)[FM]) {
+  // LDS returns in order: column j of MFMAs starts as soon as fb[j] has landed; `later`
+  // reads (issued after this step's) may still be in flight
+  auto mfmas = [&](f16x8 (&fa)[FN], f16x8 (&fb)[FM], auto later) {
     static_for<FM>([&](auto J) {
-      lgkm_wait<FM - 1 - J>();
+      lgkm_wait<decltype(later)::value + FM - 1 - J>();
       if constexpr (J == 0) {
 #pragma unroll
         for (int i = 0; i < FN; i++) asm volatile("" : "+v"(fa[i]));
@@ -356,16 +358,27 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
         const f16x8* buf = ring + j * SZ;
         // first fragment reads go out before the DMA address arithmetic, which then hides
         // their latency
-        f16x8 fa[FN], fb[FM];
-        reads(buf, 0, fa, fb);
-        __builtin_amdgcn_sched_barrier(0);
-        if (k + NS - 1 < nks) issue(ring + ((j + NS - 1) % NS) * SZ);
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(fa, fb);
+        if constexpr (PRE) {
+          // small wave tiles: every MFMA step's fragments are requested at once, so the
+          // stage costs one LDS round trip instead of one per step
+          f16x8 fa[KS][FN], fb[KS][FM];
+          static_for<KS>([&](auto S) { reads(buf, S, fa[S], fb[S]); });
+          __builtin_amdgcn_sched_barrier(0);
+          if (k + NS - 1 < nks) issue(ring + ((j + NS - 1) % NS) * SZ);
+          __builtin_amdgcn_sched_barrier(0);
+          static_for<KS>([&](auto S) { mfmas(fa[S], fb[S], ic<(KS - 1 - S) * (FN + FM)>{}); });
+        } else {
+          f16x8 fa[FN], fb[FM];
+          reads(buf, 0, fa, fb);
+          __builtin_amdgcn_sched_barrier(0);
+          if (k + NS - 1 < nks) issue(ring + ((j + NS - 1) % NS) * SZ);
+          __builtin_amdgcn_sched_barrier(0);
+          mfmas(fa, fb, ic<0>{});
 #pragma unroll
-        for (int s = 1; s < KS; s++) {
-          reads(buf, s, fa, fb);
-          mfmas(fa, fb);
+          for (int s = 1; s < KS; s++) {
+            reads(buf, s, fa, fb);
+            mfmas(fa, fb, ic<0>{});
+          }
         }
       }
     });
@@ -498,8 +511,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   X(26, 64, 32, 2, 2, 64, 8)          \
   X(27, 64, 64, 2, 2, 64, 6)          \
   X(28, 32, 32, 2, 2, 128, 4)         \
-  X(29, 64, 16, 4, 1, 128, 5)         \
-  X(30, 256, 256, 2, 2, 64, 2)
+  X(29, 64, 16, 4, 1, 128, 5)
 
 static const TileCfg kTiles[] = {
 #define X(i, bm, bn, wm, wn, bk, ns) {bm, bn, wm, wn, bk, ns},
