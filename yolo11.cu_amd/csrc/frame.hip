@@ -228,9 +228,9 @@ __device__ __forceinline__ bool suppresses(float4 a, float4 b, float thr) {
 // keys of lst[0..n) in descending order in sorted[0..m):
 //  - above NMS_CAP candidates a radix select keeps the NMS_CAP largest keys (up to 8 passes
 //    of 8-bit histograms from the top byte, stopping once the selected bin holds exactly
-//    the keys still needed; keys are unique, so exactly NMS_CAP are >= T).
-//    Scores crowd into few bins, so lanes of a wave that share a bin add once
-//    (wave-aggregated atomics) instead of serialising on one LDS address;
+//    the keys still needed, and skipping the two anchor bytes that are constant below 2^16
+//    anchors; keys are unique, so exactly NMS_CAP are >= T).  A wave's two most crowded
+//    bins are added once each (wave-aggregated), the rest with plain LDS atomics;
 //  - up to 512 keys: rank = number of strictly larger keys, TPK threads (adjacent lanes)
 //    sharing a key's scan and adding their counts with shuffles; above that a bitonic sort
 //    (descending) of the keys padded with zeros to 1024 or 2048 (log2(P)(log2(P)+1)/2
@@ -243,7 +243,7 @@ struct RankShared {
   int need, count, done;
 };
 
-__device__ void selectAndRank(const unsigned long long* __restrict__ lst, int n,
+__device__ void selectAndRank(const unsigned long long* __restrict__ lst, int n, int A,
                               unsigned long long* skey, unsigned long long* sorted, RankShared& rs) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int m = min(n, NMS_CAP);
@@ -251,24 +251,37 @@ __device__ void selectAndRank(const unsigned long long* __restrict__ lst, int n,
     if (tid == 0) { rs.prefix = 0ull; rs.need = NMS_CAP; rs.count = 0; rs.done = 0; }
     for (int p = 0; p < 8; p++) {
       const int shift = 56 - 8 * p;
+      if (p == 4 && A <= 65536) {
+        // the low word is 0xFFFFFFFF - anchor: with fewer than 2^16 anchors its top two bytes
+        // are 0xFF for every key, so those two passes would select bin 255 twice
+        __syncthreads();
+        if (tid == 0) rs.prefix |= 0xFFFF0000ull;
+        p = 5;
+        continue;
+      }
       for (int i = tid; i < 256; i += NMS_THREADS) rs.hist[i] = 0;
       __syncthreads();
       const unsigned long long pre = rs.prefix;
-      for (int i0 = 0; i0 < n; i0 += NMS_THREADS) {
-        const int i = i0 + tid;
+      auto count = [&](unsigned long long k, bool valid) {
         int bin = -1;
-        if (i < n) {
-          const unsigned long long k = lst[i];
-          if (p == 0 || (k >> (shift + 8)) == (pre >> (shift + 8))) bin = (int)((k >> shift) & 255);
-        }
+        if (valid && (p == 0 || (k >> (shift + 8)) == (pre >> (shift + 8)))) bin = (int)((k >> shift) & 255);
+        // crowded bins (the leading bytes of scores) are added once per wave for the first
+        // two distinct bins; lanes left over hit spread-out bins with plain atomics
         unsigned long long todo = __ballot(bin >= 0);
-        while (todo) {
+#pragma unroll
+        for (int peel = 0; peel < 2 && todo; peel++) {
           const int leader = __ffsll((long long)todo) - 1;
           const int lb = __shfl(bin, leader);
           const unsigned long long same = __ballot(bin == lb);
           if (lane == leader) atomicAdd(&rs.hist[lb], __popcll(same));
+          if (bin == lb) bin = -1;
           todo &= ~same;
         }
+        if (bin >= 0) atomicAdd(&rs.hist[bin], 1);
+      };
+      for (int i0 = 0; i0 < n; i0 += NMS_THREADS) {
+        const int i = i0 + tid;
+        count(i < n ? lst[i] : 0ull, i < n);
       }
       __syncthreads();
       // the bin holding the need-th largest key: lane l of wave 0 owns bins 255-4l .. 252-4l
@@ -363,13 +376,14 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
                                                      int* __restrict__ rawcnt,
                                                      const PostParams* __restrict__ prm) {
   __shared__ unsigned long long skey[NMS_CAP];
-  __shared__ float4 sbox[NMS_CAP];                 // the rank-ordered keys during selection
+  __shared__ float4 sbox[NMS_CAP];                 // rank-ordered keys during selection, then boxes by rank
   __shared__ short scls[NMS_CAP];
   __shared__ int chist[NMS_CLASSES];
   __shared__ int cstart[NMS_CLASSES];              // class-major start of a class
   __shared__ int cfill[NMS_CLASSES];               // bucket fill counters
   __shared__ short present[NMS_CLASSES];
   __shared__ short large[NMS_CLASSES];             // classes of more than 64 members
+  __shared__ short lchunk[NMS_CAP / 64][NMS_CAP / 64];   // large-class members per 64-rank chunk
   __shared__ __attribute__((aligned(16))) short bucket[NMS_CAP];   // ranks, grouped by class
   __shared__ short perm[NMS_CAP];                  // class-major position -> rank
   __shared__ float4 cbox[NMS_CAP];                 // boxes, class-major
@@ -395,7 +409,7 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   // 1. the m best keys in rank order (parked in the box array's storage); every thread
   //    lifts its entries and their candidate records into registers, counting classes
   unsigned long long* sorted = reinterpret_cast<unsigned long long*>(sbox);
-  selectAndRank(lists + (size_t)img * A, n, skey, sorted, rs);
+  selectAndRank(lists + (size_t)img * A, n, A, skey, sorted, rs);
   for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) removed[i] = 0u;
   for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) struck[i] = 0u;
   unsigned long long kr[2] = {0ull, 0ull};
@@ -417,6 +431,7 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     const int r = tid + u * NMS_THREADS;
     if (r < m) {
       skey[r] = kr[u];
+      sbox[r] = br[u];
       scls[r] = cr[u];
       atomicAdd(&chist[cr[u]], 1);
     }
@@ -424,9 +439,12 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   __syncthreads();
 
   // 2. class-major layout (ranks grouped by class, rank order inside a class).  Thread t
-  //    owns class t: the classes present, the large ones, and the exclusive prefix of the
-  //    histogram.  Each rank then drops into its class's bucket (any order) and finds its
-  //    place in the class by counting the class members of smaller rank.
+  //    owns class t: the classes present, the large ones (> 64 members), and the exclusive
+  //    prefix of the histogram.  A rank of a small class drops into its class's bucket (any
+  //    order) and finds its place by counting the class members of smaller rank.  Large
+  //    classes are placed by 64-rank chunks: one ballot per (chunk, large class) counts the
+  //    class in the chunk, a prefix over chunks gives each chunk's start in the class, and
+  //    a member's place adds its ballot prefix within the chunk.
   {
     const int h = chist[tid];
     if (h > 0) present[atomicAdd(&npresent, 1)] = (short)tid;
@@ -443,16 +461,46 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     cstart[tid] = off + incl - h;
   }
   __syncthreads();
+  const int nch = (m + 63) >> 6;           // 64-rank chunks (<= 32)
 #pragma unroll
   for (int u = 0; u < 2; u++) {
     const int r = tid + u * NMS_THREADS;
-    if (r < m) bucket[cstart[cr[u]] + atomicAdd(&cfill[cr[u]], 1)] = (short)r;
+    if (r < m && chist[cr[u]] <= 64) bucket[cstart[cr[u]] + atomicAdd(&cfill[cr[u]], 1)] = (short)r;
+  }
+  for (int q = wave; q < nch; q += NMS_THREADS / 64) {
+    const int r = 64 * q + lane;
+    const int c = r < m ? scls[r] : -1;
+    for (int li = 0; li < nlarge; li++) {
+      const int cnt = __popcll(__ballot(c == large[li]));
+      if (lane == 0) lchunk[q][li] = (short)cnt;
+    }
   }
   __syncthreads();
+  if (tid < nlarge) {
+    int run = 0;
+    for (int q = 0; q < nch; q++) {
+      const int v = lchunk[q][tid];
+      lchunk[q][tid] = (short)run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  for (int q = wave; q < nch; q += NMS_THREADS / 64) {
+    const int r = 64 * q + lane;
+    const int c = r < m ? scls[r] : -1;
+    for (int li = 0; li < nlarge; li++) {
+      const unsigned long long bal = __ballot(c == large[li]);
+      if (c == large[li]) {
+        const int pos = cstart[c] + lchunk[q][li] + __popcll(bal & ((1ull << lane) - 1ull));
+        perm[pos] = (short)r;
+        cbox[pos] = sbox[r];
+      }
+    }
+  }
 #pragma unroll
   for (int u = 0; u < 2; u++) {
     const int r = tid + u * NMS_THREADS;
-    if (r < m) {
+    if (r < m && chist[cr[u]] <= 64) {
       const int sc = cstart[cr[u]], se = sc + chist[cr[u]];
       int below = 0;
       for (int c8 = sc & ~7; c8 < se; c8 += 8) {     // 16-byte reads of the class's bucket
@@ -757,7 +805,7 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms_obb(const float* __restrict
   const float skipK = bstar > 0.f ? 8.f * bstar : INFINITY;
 
   unsigned long long* sorted = reinterpret_cast<unsigned long long*>(regionA);
-  selectAndRank(lists + (size_t)img * A, n, regionB, sorted, rs);
+  selectAndRank(lists + (size_t)img * A, n, A, regionB, sorted, rs);
   for (int i = tid; i < NMS_CAP / 32; i += NMS_THREADS) dead[i] = 0u;
   cstart[tid] = 0;
   if (tid == 0) npresent = 0;
@@ -934,45 +982,88 @@ void launchNms(const float* cand, unsigned long long* lists, int* counts, int A,
 
 // ------------------------------------------------------------------ masks
 // Survivor masks at proto resolution (k_mask_assemble, engine/engine.cu:1125-1158):
-// logit = coef . proto (fp32), pixel kept iff inside the box scaled to proto resolution
-// (half-open float compares) and logit > 0.  One block per (survivor slot, image); slots
-// past the image's count exit, so the fixed grid can live in a graph.
+// logit = coef . proto (fp32, channels summed in order), pixel kept iff inside the box scaled
+// to proto resolution (half-open float compares) and logit > 0.
+// Grid (pixel tiles of 1024, groups of MSK_GROUP survivor slots, images): each thread keeps
+// the proto vectors of 4 consecutive pixels in registers and walks the group's survivors
+// (coefficients and boxes staged in LDS, read as broadcasts), writing 4 mask bytes per
+// survivor in one store.  The proto is read once per survivor group instead of once per
+// survivor.  Groups past the image's count exit, so the fixed grid can live in a graph.
+constexpr int MSK_GROUP = 32;
+constexpr int MSK_PIX = 4;
+
+template <int NMC>   // 8-channel chunks of the proto (nm / 8)
 __global__ __launch_bounds__(256) void k_masks(View proto, const float* __restrict__ cand, int cstride,
-                                               int A, int nm, const int* __restrict__ outidx,
+                                               int A, const int* __restrict__ outidx,
                                                const int* __restrict__ outcnt,
                                                const float* __restrict__ outdets,
                                                uint8_t* __restrict__ masks, float rx, float ry) {
-  const int d = blockIdx.x, img = blockIdx.y;
-  if (d >= outcnt[img]) return;
-  __shared__ float co[64];
-  const int an = outidx[img * MAX_OUT + d];
-  const float* cf = cand + ((size_t)img * A + an) * cstride + 6;
-  if ((int)threadIdx.x < nm) co[threadIdx.x] = cf[threadIdx.x];
-  __syncthreads();
-  const float* det = outdets + ((size_t)img * MAX_OUT + d) * 6;
-  const float bx1 = det[0] * rx, by1 = det[1] * ry, bx2 = det[2] * rx, by2 = det[3] * ry;
-  const int Ph = proto.H, Pw = proto.W;
-  uint8_t* mo = masks + ((size_t)img * MAX_OUT + d) * Ph * Pw;
-  const f16* pimg = proto.p + (size_t)img * Ph * Pw * proto.s + proto.o;
-  for (int p = threadIdx.x; p < Ph * Pw; p += blockDim.x) {
-    const int px = p % Pw, py = p / Pw;
-    const f16* pp = pimg + (size_t)p * proto.s;
-    float acc = 0.f;
-    for (int c0 = 0; c0 < nm; c0 += 8) {
-      const f16x8 v = *(const f16x8*)(pp + c0);
+  constexpr int NM = 8 * NMC;
+  const int img = blockIdx.z, d0 = blockIdx.y * MSK_GROUP;
+  const int cnt = outcnt[img];
+  if (d0 >= cnt) return;   // block-uniform
+  const int nd = min(MSK_GROUP, cnt - d0);
+  __shared__ float co[MSK_GROUP][NM];
+  __shared__ float4 bb[MSK_GROUP];
+  const int t = threadIdx.x;
+  for (int i = t; i < nd * NM; i += 256) {
+    const int sv = i / NM, c = i - sv * NM;
+    const int an = outidx[img * MAX_OUT + d0 + sv];
+    co[sv][c] = cand[((size_t)img * A + an) * cstride + 6 + c];
+  }
+  if (t < nd) {
+    const float* det = outdets + ((size_t)img * MAX_OUT + d0 + t) * 6;
+    bb[t] = make_float4(det[0] * rx, det[1] * ry, det[2] * rx, det[3] * ry);
+  }
+  const int Ph = proto.H, Pw = proto.W, HW = Ph * Pw;
+  const int p0 = (blockIdx.x * 256 + t) * MSK_PIX;
+  const f16* pimg = proto.p + (size_t)img * HW * proto.s + proto.o;
+  f16x8 pv[MSK_PIX][NMC];
+  float fx[MSK_PIX], fy[MSK_PIX];
 #pragma unroll
-      for (int j = 0; j < 8; j++) acc = acc + co[c0 + j] * (float)v[j];
+  for (int u = 0; u < MSK_PIX; u++) {
+    const int p = min(p0 + u, HW - 1);
+#pragma unroll
+    for (int k = 0; k < NMC; k++) pv[u][k] = *(const f16x8*)(pimg + (size_t)p * proto.s + 8 * k);
+    fx[u] = (float)(p % Pw);
+    fy[u] = (float)(p / Pw);
+  }
+  __syncthreads();
+  if (p0 >= HW) return;
+  const bool whole = p0 + MSK_PIX <= HW && HW % MSK_PIX == 0;
+  for (int sv = 0; sv < nd; sv++) {
+    const float4 b = bb[sv];
+    unsigned word = 0u;
+#pragma unroll
+    for (int u = 0; u < MSK_PIX; u++) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < NMC; k++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc = acc + co[sv][8 * k + j] * (float)pv[u][k][j];
+      const bool in = fx[u] >= b.x && fx[u] < b.z && fy[u] >= b.y && fy[u] < b.w;
+      word |= (in && acc > 0.f ? 1u : 0u) << (8 * u);
     }
-    const bool in = (float)px >= bx1 && (float)px < bx2 && (float)py >= by1 && (float)py < by2;
-    mo[p] = (in && acc > 0.f) ? 1 : 0;
+    uint8_t* mo = masks + ((size_t)img * MAX_OUT + d0 + sv) * HW + p0;
+    if (whole) {
+      *(unsigned*)mo = word;
+    } else {
+      for (int u = 0; u < MSK_PIX && p0 + u < HW; u++) mo[u] = (uint8_t)(word >> (8 * u));
+    }
   }
 }
 
 void launchMasks(const View& proto, const float* cand, int cstride, int A, int nm,
                  const int* outidx, const int* outcnt, const float* outdets, uint8_t* masks,
                  float rx, float ry, int Bn, hipStream_t st) {
-  k_masks<<<dim3(MAX_OUT, Bn), 256, 0, st>>>(proto, cand, cstride, A, nm, outidx, outcnt, outdets,
-                                            masks, rx, ry);
+  const int HW = proto.H * proto.W;
+  dim3 grid((HW + 256 * MSK_PIX - 1) / (256 * MSK_PIX), (MAX_OUT + MSK_GROUP - 1) / MSK_GROUP, Bn);
+  switch (nm / 8) {
+#define MSK(n) case n: k_masks<n><<<grid, 256, 0, st>>>(proto, cand, cstride, A, outidx, outcnt, outdets, masks, rx, ry); break;
+    MSK(1) MSK(2) MSK(3) MSK(4) MSK(5) MSK(6) MSK(7) MSK(8)
+#undef MSK
+    default: break;
+  }
 }
 
 }  // namespace yolo
