@@ -13,8 +13,8 @@ conv MFMA util %"):
     from per-op hipEvent timing.
   * roofline: the implicit-GEMM conv kernel on the isolated-conv-sweep shape
     3x3 s1 256->256 @80x80, batch 32, timed with hipEvents on the
-    engine stream; `traffic` = HBM bytes per launch from the committed PMC pass
-    (profiles/conv_gemm_c1_traffic.json) when the autotuner picks the tile it measured.
+    engine stream; `traffic` = HBM bytes per launch of the tile the autotuner picked, from
+    the committed per-tile PMC passes (profiles/conv_gemm_c1_traffic.json).
   * yolo11n-obb at 1024 (15 classes, 1024x1024 frame) and yolo11n-seg at 640, batch 1:
     whole-frame graph, frame in HBM (side figures; the reference quotes 1.6 ms and 1.21 ms
     on an RTX 3060 Ti, README.md:80-81).
@@ -47,15 +47,15 @@ def log(*a):
 
 
 def measured_traffic(cfg):
-    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 PMC pass
-    (FETCH_SIZE and WRITE_SIZE scaled by a plain copy of known size), when this run's
-    autotuner picked the tile that pass measured; otherwise None."""
+    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 PMC passes
+    (FETCH_SIZE and WRITE_SIZE per tile config, each scaled by a plain copy of known size)
+    for the tile this run's autotuner picked; None if that tile has no measurement."""
     path = os.path.join(ROOT, "profiles", "conv_gemm_c1_traffic.json")
     try:
         rec = json.load(open(path))
-    except (OSError, ValueError):
+        return int(rec["per_cfg"][str(cfg)]["traffic_bytes"])
+    except (OSError, ValueError, KeyError):
         return None
-    return int(rec["traffic_bytes"]) if rec.get("cfg") == cfg else None
 
 
 def conv_flops(eng, k):

@@ -415,28 +415,34 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     if (t == 0) cnt[tsl] = 0;
   }
 
-  // ---- epilogue
+  // ---- epilogue.  Pixel rows outer, fragment pairs inner: the pairs of a wave cover
+  // consecutive 64-byte runs of a pixel's channels, so each cache line is completed by
+  // back-to-back stores instead of being written back half-filled.
   if constexpr (PAIR) {
     // fragments (2p, 2p+1): lane holds channels n0 .. n0+7 of pixel m
+    float b[FN / 2][8];
 #pragma unroll
     for (int p = 0; p < FN / 2; p++) {
       const int n0 = bn + wn * TN + 32 * p + 8 * lg;
-      if (n0 >= N) continue;  // N % 8 == 0: all 8 channels valid or none
-      float b[8];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        b[e] = BPRE ? bpre[BPRE ? 2 * p : 0][e] : bias[n0 + e];
-        b[4 + e] = BPRE ? bpre[BPRE ? 2 * p + 1 : 0][e] : bias[n0 + 4 + e];
+        b[p][e] = BPRE ? bpre[BPRE ? 2 * p : 0][e] : (n0 < N ? bias[n0 + e] : 0.f);
+        b[p][4 + e] = BPRE ? bpre[BPRE ? 2 * p + 1 : 0][e] : (n0 < N ? bias[n0 + 4 + e] : 0.f);
       }
+    }
 #pragma unroll
-      for (int jj = 0; jj < FM; jj++) {
-        const int m = bm + wm * TM + jj * 16 + lr;
-        if (m >= M) continue;
+    for (int jj = 0; jj < FM; jj++) {
+      const int m = bm + wm * TM + jj * 16 + lr;
+      if (m >= M) continue;
+#pragma unroll
+      for (int p = 0; p < FN / 2; p++) {
+        const int n0 = bn + wn * TN + 32 * p + 8 * lg;
+        if (n0 >= N) continue;  // N % 8 == 0: all 8 channels valid or none
         float v[8];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          v[e] = acc[2 * p][jj][e] + b[e];
-          v[4 + e] = acc[2 * p + 1][jj][e] + b[4 + e];
+          v[e] = acc[2 * p][jj][e] + b[p][e];
+          v[4 + e] = acc[2 * p + 1][jj][e] + b[p][4 + e];
         }
         if (act == 1) {
 #pragma unroll
@@ -455,18 +461,23 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     }
   } else {
     // single fragment: lane holds channels n0 .. n0+3 of pixel m
+    float b[FN][4];
 #pragma unroll
     for (int i = 0; i < FN; i++) {
       const int n0 = bn + wn * TN + i * 16 + 4 * lg;
-      if (n0 >= N) continue;
-      const float b0 = BPRE ? bpre[BPRE ? i : 0][0] : bias[n0], b1 = BPRE ? bpre[BPRE ? i : 0][1] : bias[n0 + 1];
-      const float b2 = BPRE ? bpre[BPRE ? i : 0][2] : bias[n0 + 2], b3 = BPRE ? bpre[BPRE ? i : 0][3] : bias[n0 + 3];
 #pragma unroll
-      for (int jj = 0; jj < FM; jj++) {
-        const int m = bm + wm * TM + jj * 16 + lr;
-        if (m >= M) continue;
-        float v0 = acc[i][jj][0] + b0, v1 = acc[i][jj][1] + b1;
-        float v2 = acc[i][jj][2] + b2, v3 = acc[i][jj][3] + b3;
+      for (int e = 0; e < 4; e++) b[i][e] = BPRE ? bpre[BPRE ? i : 0][e] : (n0 < N ? bias[n0 + e] : 0.f);
+    }
+#pragma unroll
+    for (int jj = 0; jj < FM; jj++) {
+      const int m = bm + wm * TM + jj * 16 + lr;
+      if (m >= M) continue;
+#pragma unroll
+      for (int i = 0; i < FN; i++) {
+        const int n0 = bn + wn * TN + i * 16 + 4 * lg;
+        if (n0 >= N) continue;
+        float v0 = acc[i][jj][0] + b[i][0], v1 = acc[i][jj][1] + b[i][1];
+        float v2 = acc[i][jj][2] + b[i][2], v3 = acc[i][jj][3] + b[i][3];
         if (act == 1) { v0 = silu(v0); v1 = silu(v1); v2 = silu(v2); v3 = silu(v3); }
         if (r.p) {
           const f16x4 rv = *(const f16x4*)(r.p + (size_t)m * r.s + r.o + n0);
