@@ -18,8 +18,9 @@ conv MFMA util %"):
   * yolo11n-obb at 1024 (15 classes, 1024x1024 frame) and yolo11n-seg at 640, batch 1:
     whole-frame graph, frame in HBM (side figures; the reference quotes 1.6 ms and 1.21 ms
     on an RTX 3060 Ti, README.md:80-81).
-  * yolo11m detect b1 with a 1080x1920 frame at IoU 0.7 and the five
-    isolated conv shapes at batch 1 and 32 (config 1): side figures.
+  * yolo11m detect b1 with a 1080x1920 frame at IoU 0.7, the five
+    isolated conv shapes at batch 1 and 32 (config 1), and yolo11n-cls at 224 (whole-frame
+    graph with the classify preprocess): side figures.
   * cpu_baseline: the numpy fp32 per-op oracle (letterbox + every op + decode + NMS) for
     yolo11n batch 1 on this host's cores, bounded to ~15 s.
 
@@ -183,6 +184,40 @@ def bench_m(workdir, steps, warmup, graph=True):
     return dict(ms=ms, graph_ms=graph_ms, kept=kept, raw=raw)
 
 
+def bench_cls(workdir, steps, warmup, graph=True):
+    """yolo11n-cls (1000 classes) at 224, batch 1: whole-frame graph (antialiased resize +
+    centre crop of an 810x1080 frame in HBM, network, probabilities copy) + top-5 fetch."""
+    import modelgen
+    import yolort
+    d = os.path.join(workdir, "yolo11n-cls")
+    modelgen.write_model(d, "yolo11", "n", "classify", 1000, 224, 0)
+    img = modelgen.synth_frame(810, 1080, 20, 1)
+    eng = yolort.Engine(d, 1, 0 if graph else yolort.YOLO_NOGRAPH)
+    dev = yolort.DeviceBuffer(img.nbytes)
+    eng.upload(dev, img)
+    if not graph:
+        for _ in range(warmup + steps):
+            eng.preprocess_cls(dev.ptr, 810, 1080, 0)
+            eng.run(1)
+            eng.get_cls(0, 5)
+        dev.free()
+        eng.close()
+        return None
+    eng.frame_graph([dev.ptr], [810], [1080])
+    for _ in range(warmup):
+        eng.frame_run()
+        eng.get_cls(0, 5)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.frame_run()
+        ids, _ = eng.get_cls(0, 5)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    graph_ms = eng.time_graph(1, 1, max(steps, 50))
+    dev.free()
+    eng.close()
+    return dict(ms=ms, graph_ms=graph_ms, top1=int(ids[0]))
+
+
 def bench_sweep(workdir, iters):
     """the five isolated conv shapes at batch 1 and 32 (autotuned tile and
     split), TFLOP/s per shape from hipEvent timing on the engine stream."""
@@ -324,7 +359,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "n", "x", "conv", "obb", "seg", "m", "sweep"], default="all")
+    ap.add_argument("--only", choices=["all", "n", "x", "conv", "obb", "seg", "m", "sweep", "cls"],
+                    default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the same kernels stream-ordered (rocprofv3's kernel tracer "
@@ -352,6 +388,10 @@ def main():
         log("yolo11m b1 1920x1080 e2e (IoU 0.7) ...")
         out["m"] = bench_m(workdir, args.steps, args.warmup, not args.no_graph)
         log(out["m"])
+    if args.only in ("all", "cls"):
+        log("yolo11n-cls b1 @224 e2e ...")
+        out["cls"] = bench_cls(workdir, args.steps, args.warmup, not args.no_graph)
+        log(out["cls"])
     if args.only in ("all", "sweep") and not args.no_graph:
         log("conv sweep (config 1) ...")
         out["sweep"] = bench_sweep(workdir, 10)
@@ -406,6 +446,10 @@ def main():
         if r:
             line[name] = {"ms_per_frame": round(r["ms"], 4), "graph_ms": round(r["graph_ms"], 4),
                           "kept": r["kept"], "raw_candidates": r["raw"]}
+    if out.get("cls"):
+        r = out["cls"]
+        line["yolo11n_cls_b1_224"] = {"ms_per_frame": round(r["ms"], 4), "graph_ms": round(r["graph_ms"], 4),
+                                      "top1": r["top1"]}
     if out.get("sweep"):
         line["conv_sweep"] = out["sweep"]
     if conv:

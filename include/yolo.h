@@ -53,10 +53,10 @@ void yolo_sync(void* h);
 /* engine/yolo.h:29-30 -- detections of a slot in original-image coordinates; returns
  * min(count, cap). */
 int yolo_get(void* h, int slot, YoloDet* out, int cap);
-/* engine/yolo.h:31-35 -- classify models are not supported by this engine: the graph loader
- * rejects task "classify", so these are never reached with a classify handle;
- * yolo_preprocess_cls is a no-op and yolo_get_cls returns 0 (the reference's value for a
- * non-classify handle, engine/engine.cu:1772). */
+/* engine/yolo.h:31-35 -- classify models: resize the shortest edge to S with the antialiased
+ * bilinear filter, centre-crop S x S, /255, into batch slot `slot` (async on the engine
+ * stream); yolo_get_cls writes the top-k class ids and probabilities of a slot after a run
+ * and returns min(k, nc), or 0 on a non-classify handle (engine/engine.cu:1758-1773). */
 void yolo_preprocess_cls(void* h, const unsigned char* dev_bgr, int height, int width, int slot);
 int yolo_get_cls(void* h, int slot, int* ids, float* probs, int k);
 /* engine/yolo.h:36-38 */

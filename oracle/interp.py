@@ -18,6 +18,10 @@ Per-op semantics (reference line they restate) and what pins each one:
   COPYC     channel copy                             :490-491
   ATTN      softmax(q^T k * kd^-1/2), v @ att^T      :492-500   pinned vs
             F.scaled_dot_product_attention and row-sum / permutation invariants
+  GAP       mean over H, W                           :501-502   pinned vs
+            F.adaptive_avg_pool2d(1)
+  SOFTMAX   softmax over channels                    :503-504   pinned vs torch.softmax
+            and the sum-to-one / shift-invariance properties
 Epilogue order for a fused residual is act then +res (engine/engine.cu:471-478); the
 unfused graph expresses the same thing as CONV followed by ADD.
 """
@@ -87,6 +91,17 @@ def ps2(x: np.ndarray) -> np.ndarray:
             q = 2 * di + dj
             y[:, di::2, dj::2, :] = x[..., q * C:(q + 1) * C]
     return y
+
+
+def gap(x: np.ndarray) -> np.ndarray:
+    """[B, H, W, C] -> [B, 1, 1, C] mean over H and W (fp32)."""
+    return x.mean(axis=(1, 2), keepdims=True, dtype=np.float64).astype(F32)
+
+
+def softmax_ch(x: np.ndarray) -> np.ndarray:
+    """Softmax over the channel axis of [B, 1, 1, C] (fp32 math, max-shifted)."""
+    e = np.exp((x - x.max(axis=-1, keepdims=True)).astype(F32))
+    return (e / e.sum(axis=-1, keepdims=True, dtype=F32)).astype(F32)
 
 
 def attention(qkv: np.ndarray, heads: int, kd: int, hd: int) -> np.ndarray:
@@ -160,6 +175,12 @@ class Interp:
             return op.out
         if op.kind == "ATTN":
             self.write(op.out, attention(self.view(op.a), op.heads, op.kd, op.hd))
+            return op.out
+        if op.kind == "GAP":     # export/export.py:501-502: mean over H, W
+            self.write(op.out, gap(self.view(op.a)))
+            return op.out
+        if op.kind == "SOFTMAX":  # export/export.py:503-504: softmax over channels
+            self.write(op.out, softmax_ch(self.view(op.a)))
             return op.out
         if op.kind in ("DECODE", "DECODESEG", "DECODEOBB"):
             # DECODESEG: coef = mask coefficients; DECODEOBB: coef = angle view

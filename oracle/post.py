@@ -34,6 +34,19 @@ probiou         placement).  Pinned by the Bhattacharyya distance between two Ga
                 R^T, rotation invariance, theta ~ theta + pi, (w, h, theta) ~ (h, w,
                 theta + pi/2), identical boxes (bd clamped at eps) and far boxes (clamped
                 at 100).
+cls_geom        classify host geometry, engine/engine.cu:1036-1046 (torchvision Resize(S):
+                short edge -> S, long edge S * long // short; CenterCrop offsets rounded half
+                to even).  Pinned by hand cases against Python's round().
+preprocess_cls  k_preprocess_cls, engine/engine.cu:1000-1034: PIL-style antialiased bilinear
+                (triangle filter whose support widens by the downscale factor), centre crop,
+                BGR->RGB, /255.  Evaluated in fp32 in the kernel's operation order, so the
+                engine must match it bit for bit.  Pinned by: a float64 separable
+                triangle-filter resize written from the filter's definition (agreement to
+                fp32 rounding), constant frames (exactly constant output), the scale-1
+                identity, and PIL's own antialiased BILINEAR resize (uint8 output, within
+                one level).
+topk            the reference's top-k insertion (engine/engine.cu:1593-1606): descending,
+                lower class id first among equal probabilities.  Pinned vs a stable argsort.
 nms_obb         k_nms_obb, engine/engine.cu:1178-1252: ultralytics fast-NMS (a suppressed
                 box still suppresses; iou >= thr; same class only).  Ranked and capped by
                 the same total order as nms.  Pinned by brute force on tiny sets, a chain
@@ -46,6 +59,67 @@ import math
 import numpy as np
 
 F32 = np.float32
+
+
+# ----------------------------------------------------------------------------- classify
+def cls_geom(S: int, sh: int, sw: int):
+    """(rh, rw, top, left): resize the short edge to S, centre-crop S x S."""
+    if sw <= sh:
+        rw, rh = S, S * sh // sw
+    else:
+        rh, rw = S, S * sw // sh
+    return rh, rw, int(round((rh - S) / 2)), int(round((rw - S) / 2))
+
+
+def preprocess_cls(src: np.ndarray, S: int) -> np.ndarray:
+    """BGR u8 [sh, sw, 3] -> RGB float32 [S, S, 3] (fp16-rounded): the kernel's fp32
+    arithmetic, vectorised over destination pixels, in the kernel's summation order."""
+    sh, sw = src.shape[:2]
+    rh, rw, top, left = cls_geom(S, sh, sw)
+    fy, fx = F32(sh) / F32(rh), F32(sw) / F32(rw)
+    ry, rx = max(fy, F32(1.0)), max(fx, F32(1.0))
+    oy = np.arange(S)
+    cy = ((oy + top).astype(F32) + F32(0.5)) * fy                 # per output row
+    cx = ((oy + left).astype(F32) + F32(0.5)) * fx                # per output column
+    ya = np.maximum(0, (cy - ry + F32(0.5)).astype(np.int64))
+    yb = np.minimum(sh, (cy + ry + F32(0.5)).astype(np.int64))
+    xa = np.maximum(0, (cx - rx + F32(0.5)).astype(np.int64))
+    xb = np.minimum(sw, (cx + rx + F32(0.5)).astype(np.int64))
+
+    def tri(d, r):
+        return np.maximum(F32(0.0), F32(1.0) - np.abs(d).astype(F32) / r).astype(F32)
+
+    ny = np.zeros(S, F32)
+    for k in range(int((yb - ya).max())):
+        i = ya + k
+        ny = np.where(i < yb, ny + tri(i.astype(F32) + F32(0.5) - cy, ry), ny).astype(F32)
+    nx = np.zeros(S, F32)
+    for k in range(int((xb - xa).max())):
+        j = xa + k
+        nx = np.where(j < xb, nx + tri(j.astype(F32) + F32(0.5) - cx, rx), nx).astype(F32)
+    srcf = src.astype(F32)
+    acc = np.zeros((S, S, 3), F32)            # b, g, r sums per destination pixel
+    for ki in range(int((yb - ya).max())):
+        i = ya + ki                                                       # [S] rows
+        wy = tri(i.astype(F32) + F32(0.5) - cy, ry)
+        vi = i < yb
+        rows = srcf[np.minimum(i, sh - 1)]                                # [S, sw, 3]
+        for kj in range(int((xb - xa).max())):
+            j = xa + kj                                                   # [S] cols
+            wx = tri(j.astype(F32) + F32(0.5) - cx, rx)
+            w = (wy[:, None] * wx[None, :]).astype(F32)                   # [S, S]
+            px = rows[:, np.minimum(j, sw - 1)]                           # [S, S, 3]
+            ok = (vi[:, None] & (j < xb)[None, :])[..., None]
+            acc = np.where(ok, acc + (w[..., None] * px).astype(F32), acc).astype(F32)
+    inv = F32(1.0) / (ny[:, None] * nx[None, :] * F32(255.0))
+    out = (acc * inv[..., None]).astype(F32)[..., ::-1]                  # BGR -> RGB
+    return out.astype(np.float16).astype(F32)
+
+
+def topk(probs: np.ndarray, k: int):
+    """(ids, probs) of the k largest, lower id first among equals."""
+    order = np.argsort(-probs.astype(np.float64), kind="stable")[:k]
+    return order.astype(np.int32), probs[order].astype(F32)
 
 
 # ----------------------------------------------------------------------------- letterbox

@@ -1,4 +1,5 @@
-// Bandwidth-bound NHWC view kernels: ADD, MAXPOOL5 (and the fused SPPF pool chain),\n// UPSAMPLE2, COPYC, PS2.
+// Bandwidth-bound NHWC view kernels: ADD, MAXPOOL5 (and the fused SPPF pool chain),
+// UPSAMPLE2, COPYC, PS2, and the classify head's GAP and channel softmax.
 // Each thread moves one 8-channel group (16 bytes) of one pixel; the loader guarantees
 // every view offset, width and row stride is a multiple of 8 halves, so all accesses
 // are aligned 128-bit loads/stores.  Semantics follow the reference ops
@@ -178,6 +179,67 @@ void launchCopyC(const View& x, const View& y, int Bn, hipStream_t st) {
 void launchPS2(const View& x, const View& y, int Bn, hipStream_t st) {
   int total = Bn * y.H * y.W * (y.C / 8);
   k_ps2<<<grid(total), 256, 0, st>>>(x, y, total);
+}
+
+// ------------------------------------------------------------------ classify head
+// GAP (k_gap, engine/engine.cu:734-744): [H,W,C] -> [1,1,C], mean over H*W with fp32
+// accumulation in pixel order.  One thread per (image, 8-channel group): 16-byte loads of
+// the group at every pixel, all in flight 4 at a time.
+__global__ __launch_bounds__(256) void k_gap(View x, View y, int total) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int cg = x.C >> 3;
+  const int img = idx / cg, c = (idx - img * cg) << 3;
+  const int HW = x.H * x.W;
+  const size_t pix0 = (size_t)img * HW;
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int p = 0;
+  for (; p + 4 <= HW; p += 4) {
+    f16x8 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) v[u] = ld8(x, pix0 + p + u, c);
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) s[j] += (float)v[u][j];
+  }
+  for (; p < HW; p++) {
+    const f16x8 v = ld8(x, pix0 + p, c);
+#pragma unroll
+    for (int j = 0; j < 8; j++) s[j] += (float)v[j];
+  }
+  f16x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; j++) o[j] = (f16)(s[j] / (float)HW);
+  st8(y, img, c, o);
+}
+
+// Channel softmax of a [1,1,C] view (k_softmax_ch, engine/engine.cu:746-781): one wave per
+// image, max and sum as butterfly (xor-shuffle) reductions, fp32 math, fp16 out:
+// y = exp(x - max) * (1 / sum).
+__global__ __launch_bounds__(64) void k_softmax_ch(View x, View y) {
+  const int img = blockIdx.x, lane = threadIdx.x;
+  const int C = x.C;
+  const f16* xp = x.p + (size_t)img * x.s + x.o;
+  float mx = -INFINITY;
+  for (int c = lane; c < C; c += 64) mx = fmaxf(mx, (float)xp[c]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  float sum = 0.f;
+  for (int c = lane; c < C; c += 64) sum += expf((float)xp[c] - mx);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+  const float inv = 1.f / sum;
+  f16* yp = y.p + (size_t)img * y.s + y.o;
+  for (int c = lane; c < C; c += 64) yp[c] = (f16)(expf((float)xp[c] - mx) * inv);
+}
+
+void launchGap(const View& x, const View& y, int Bn, hipStream_t st) {
+  const int total = Bn * (x.C / 8);
+  k_gap<<<(total + 255) / 256, 256, 0, st>>>(x, y, total);
+}
+void launchSoftmaxCh(const View& x, const View& y, int Bn, hipStream_t st) {
+  k_softmax_ch<<<Bn, 64, 0, st>>>(x, y);
 }
 
 }  // namespace yolo

@@ -53,6 +53,19 @@ struct SlotGeom {
   int top = 0, left = 0;
 };
 
+// Classify geometry (torchvision Resize(S) + CenterCrop(S), engine/engine.cu:1036-1046):
+// the shortest edge becomes S and the long edge S * long / short (integer truncation); the
+// crop offsets round half to even, as Python's round() does.
+struct ClsGeom {
+  int rh, rw, top, left;
+};
+static ClsGeom clsGeom(int S, int sh, int sw) {
+  const long rh = sw <= sh ? (long)S * sh / sw : S;
+  const long rw = sw <= sh ? S : (long)S * sw / sh;
+  auto half = [](long d) { return (int)(d / 2 + ((d & 1) && ((d / 2) & 1) ? 1 : 0)); };
+  return ClsGeom{(int)rh, (int)rw, half(rh - S), half(rw - S)};
+}
+
 struct Engine {
   GraphDesc g;
   std::vector<OpDesc> ops;
@@ -84,6 +97,7 @@ struct Engine {
   PostParams hparams{0.25f, 0.45f, MAX_OUT, 0};
   // pinned mirror of `results` (filled inside the graph)
   void* h_results = nullptr;
+  f16* h_probs = nullptr;             // classify: pinned [B][nc] probabilities (in the graph)
   float* h_out = nullptr;
   int* h_cnt = nullptr;
   int* h_rawcnt = nullptr;
@@ -132,6 +146,8 @@ struct Engine {
     masks = nullptr; params = nullptr; splitWs = nullptr; splitCnt = nullptr;
     splitWsBytes = splitCntN = 0;
     if (h_results) (void)hipHostFree(h_results);
+    if (h_probs) (void)hipHostFree(h_probs);
+    h_probs = nullptr;
     h_results = nullptr; h_out = nullptr; h_cnt = nullptr; h_rawcnt = nullptr;
     for (hipEvent_t e : opEvent)
       if (e) (void)hipEventDestroy(e);
@@ -372,6 +388,10 @@ struct Engine {
     h_cnt = (int*)h_results;
     h_rawcnt = h_cnt + B;
     h_out = (float*)((char*)h_results + detOff);
+    if (g.cls) {
+      HCK(hipHostMalloc((void**)&h_probs, (size_t)B * g.nc * sizeof(f16), hipHostMallocDefault));
+      memset(h_probs, 0, (size_t)B * g.nc * sizeof(f16));
+    }
     // decode levels in op order
     dec = DecodeArgs{};
     int base = 0;
@@ -435,11 +455,18 @@ struct Engine {
         // tensor is final by then)
         if (k == lastDecode) launchDecode(dec, cand, nmsScratch, nmsCount, params, Bn, s);
         break;
+      case GAP: launchGap(view(op.a), view(op.out), Bn, s); break;
+      case SOFTMAX: launchSoftmaxCh(view(op.a), view(op.out), Bn, s); break;
       default: break;   // MASKS is declarative; assembly runs after NMS
     }
   }
 
   void post(int Bn) {
+    if (g.cls) {   // no decode/NMS: the probabilities go to pinned memory (engine/engine.cu:1458)
+      HCK(hipMemcpyAsync(h_probs, bufp[g.tens[g.probsTen].buf], (size_t)Bn * g.nc * sizeof(f16),
+                         hipMemcpyDeviceToHost, st));
+      return;
+    }
     if (g.numAnchors == 0) return;   // no detection head (single-op graphs)
     if (g.obb)
       launchNmsObb(cand, nmsScratch, nmsCount, g.numAnchors, outdets, outidx, outcnt, rawcnt, params, Bn, st);
@@ -621,10 +648,15 @@ struct Engine {
       const uint8_t* src = frames[s].first;
       if (host && host[s])
         HCK(hipMemcpyAsync((void*)src, host[s], (size_t)hs[s] * ws[s] * 3, hipMemcpyHostToDevice, st));
+      f16* dst = bufp[g.tens[0].buf] + (size_t)s * ib.H * ib.W * 3;
+      if (g.cls) {
+        const ClsGeom cg = clsGeom(ib.H, hs[s], ws[s]);
+        launchPreprocessCls(src, hs[s], ws[s], dst, ib.H, cg.rh, cg.rw, cg.top, cg.left, st);
+        continue;
+      }
       const SlotGeom& sg = frames[s].second;
       int nh = (int)roundf(hs[s] * sg.scale), nw = (int)roundf(ws[s] * sg.scale);
-      launchPreprocess(src, hs[s], ws[s], bufp[g.tens[0].buf] + (size_t)s * ib.H * ib.W * 3, ib.H, ib.W,
-                       sg.scale, sg.top, sg.left, nh, nw, st);
+      launchPreprocess(src, hs[s], ws[s], dst, ib.H, ib.W, sg.scale, sg.top, sg.left, nh, nw, st);
     }
   }
 
@@ -839,7 +871,7 @@ int yolo_graph_check(const char* model_dir, char* err, int errlen) {
   return (int)g.ops.size();
 }
 
-int yolo_task(void* h) { return E(h)->g.seg ? 3 : (E(h)->g.obb ? 1 : 0); }
+int yolo_task(void* h) { return E(h)->g.seg ? 3 : (E(h)->g.obb ? 1 : (E(h)->g.cls ? 2 : 0)); }
 
 float yolo_exec_ms(void* h, int B) {
   Engine* e = E(h);
@@ -904,12 +936,43 @@ int yolo_get(void* h, int slot, YoloDet* out, int cap) {
 }
 
 void yolo_preprocess_cls(void* h, const unsigned char* dev_bgr, int height, int width, int slot) {
-  (void)h; (void)dev_bgr; (void)height; (void)width; (void)slot;
+  Engine* e = E(h);
+  try {
+    if (slot < 0 || slot >= e->B) throw Failure("slot out of range");
+    if (e->g.bufs[e->g.tens[0].buf].C != 3) throw Failure("classify preprocess needs a 3-channel input tensor");
+    const yolo::BufDesc& ib = e->g.bufs[e->g.tens[0].buf];
+    if (ib.H != ib.W) throw Failure("classify preprocess needs a square input");
+    const yolo::ClsGeom cg = yolo::clsGeom(ib.H, height, width);
+    yolo::launchPreprocessCls(dev_bgr, height, width, e->bufp[e->g.tens[0].buf] + (size_t)slot * ib.H * ib.W * 3,
+                              ib.H, cg.rh, cg.rw, cg.top, cg.left, e->st);
+    HCK(hipGetLastError());
+  } catch (const std::exception& ex) {
+    fatal(ex);
+  }
 }
 
+// Top-k class ids and probabilities of a slot from the pinned fp16 probabilities: insertion
+// into k ranked slots with a strict comparison, so among equal probabilities the lower class
+// id ranks first (engine/engine.cu:1593-1606).  Returns min(k, nc); 0 for non-classify
+// handles (engine/engine.cu:1768-1773).
 int yolo_get_cls(void* h, int slot, int* ids, float* probs, int k) {
-  (void)h; (void)slot; (void)ids; (void)probs; (void)k;
-  return 0;
+  Engine* e = E(h);
+  if (!e->g.cls || slot < 0 || slot >= e->B || k <= 0) return 0;
+  k = std::min(k, e->g.nc);
+  for (int i = 0; i < k; i++) { ids[i] = -1; probs[i] = -1.f; }
+  const yolo::f16* p = e->h_probs + (size_t)slot * e->g.nc;
+  for (int c = 0; c < e->g.nc; c++) {
+    const float v = (float)p[c];
+    for (int i = 0; i < k; i++) {
+      if (v > probs[i]) {
+        for (int j = k - 1; j > i; j--) { probs[j] = probs[j - 1]; ids[j] = ids[j - 1]; }
+        probs[i] = v;
+        ids[i] = c;
+        break;
+      }
+    }
+  }
+  return k;
 }
 
 void yolo_slot_geom(void* h, int slot, float* scale, int* top, int* left) {

@@ -41,8 +41,9 @@ struct GraphDesc {
   std::vector<TenDesc> tens;
   std::vector<OpDesc> ops;
   // derived by validate()
-  bool seg = false, obb = false;
+  bool seg = false, obb = false, cls = false;
   int nm = 0, protoTen = -1;
+  int probsTen = -1;                  // classify: the SOFTMAX output ([1,1,nc] buffer)
   int detStride = 6;                  // floats per candidate record
   int outK = 6;                       // floats per output record (OBB 7)
   int numAnchors = 0;                 // sum of H*W over the DECODE levels
@@ -127,11 +128,15 @@ void launchSppfPool(const View& x, const View& y1, const View& y2, const View& y
 void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st);
 void launchCopyC(const View& x, const View& y, int Bn, hipStream_t st);
 void launchPS2(const View& x, const View& y, int Bn, hipStream_t st);
+void launchGap(const View& x, const View& y, int Bn, hipStream_t st);
+void launchSoftmaxCh(const View& x, const View& y, int Bn, hipStream_t st);
 // attention.hip
 void attentionInit();
 void launchAttention(const View& qkv, const View& y, int heads, int kd, int hd, int Bn,
                      hipStream_t st);
 // frame.hip
+void launchPreprocessCls(const uint8_t* src, int sh, int sw, f16* dst, int S, int rh, int rw, int top,
+                         int left, hipStream_t st);
 void launchPreprocess(const uint8_t* src, int sh, int sw, f16* dst, int dh, int dw, float scale,
                       int top, int left, int nh, int nw, hipStream_t st);
 // Decode appends each image's survivors as packed (score, anchor) keys to lists[img*A ..]

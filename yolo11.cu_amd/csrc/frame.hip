@@ -50,6 +50,57 @@ void launchPreprocess(const uint8_t* src, int sh, int sw, f16* dst, int dh, int 
   k_letterbox<<<(dh * dw + 255) / 256, 256, 0, st>>>(src, sh, sw, dst, dh, dw, scale, top, left, nh, nw);
 }
 
+// ------------------------------------------------------------------ classify preprocess
+// BGR u8 HWC (sh x sw) -> RGB fp16 NHWC (S x S), /255: resize the shortest edge to S with
+// the antialiased bilinear (triangle) filter of PIL / torchvision, whose support widens by
+// the scale when downscaling, then centre-crop S x S (k_preprocess_cls,
+// engine/engine.cu:1000-1034; the host gives the resized size rh x rw and the crop offsets).
+// One thread per destination pixel; the tap weights and sums are evaluated in the
+// reference's order so the fp32 result is reproducible bit for bit.
+__global__ __launch_bounds__(256) void k_preprocess_cls(const uint8_t* __restrict__ src, int sh, int sw,
+                                                        f16* __restrict__ dst, int S, int rh, int rw,
+                                                        int top, int left) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= S * S) return;
+  const int ox = idx % S, oy = idx / S;
+  const float fy = (float)sh / (float)rh, fx = (float)sw / (float)rw;   // source px per resized px
+  const float ry = fmaxf(fy, 1.f), rx = fmaxf(fx, 1.f);                 // filter radius
+  const float cy = ((float)(oy + top) + 0.5f) * fy, cx = ((float)(ox + left) + 0.5f) * fx;
+  const int ya = max(0, (int)(cy - ry + 0.5f)), yb = min(sh, (int)(cy + ry + 0.5f));
+  const int xa = max(0, (int)(cx - rx + 0.5f)), xb = min(sw, (int)(cx + rx + 0.5f));
+  auto tri = [](float d, float r) { return fmaxf(0.f, 1.f - fabsf(d) / r); };
+  float ny = 0.f, nx = 0.f;
+  for (int i = ya; i < yb; i++) ny += tri((float)i + 0.5f - cy, ry);
+  for (int j = xa; j < xb; j++) nx += tri((float)j + 0.5f - cx, rx);
+  float sb = 0.f, sg = 0.f, sr = 0.f;
+  for (int i = ya; i < yb; i++) {
+    const float wy = tri((float)i + 0.5f - cy, ry);
+    const uint8_t* row = src + (size_t)i * sw * 3;
+    for (int j = xa; j < xb; j++) {
+      const float w = wy * tri((float)j + 0.5f - cx, rx);
+      const uint8_t* px = row + (size_t)j * 3;
+      sb += w * (float)px[0];
+      sg += w * (float)px[1];
+      sr += w * (float)px[2];
+    }
+  }
+  const float inv = 1.f / (ny * nx * 255.f);
+  // the products are rounded to fp32 before the fp16 conversion: without the barrier the
+  // compiler fuses multiply and conversion (v_fma_mixlo_f16, one rounding), which differs
+  // from the reference's two roundings near fp16 midpoints
+  float vr = sr * inv, vg = sg * inv, vb = sb * inv;
+  asm volatile("" : "+v"(vr), "+v"(vg), "+v"(vb));
+  f16* o = dst + (size_t)idx * 3;
+  o[0] = (f16)vr;
+  o[1] = (f16)vg;
+  o[2] = (f16)vb;
+}
+
+void launchPreprocessCls(const uint8_t* src, int sh, int sw, f16* dst, int S, int rh, int rw, int top,
+                         int left, hipStream_t st) {
+  k_preprocess_cls<<<(S * S + 255) / 256, 256, 0, st>>>(src, sh, sw, dst, S, rh, rw, top, left);
+}
+
 // ------------------------------------------------------------------ decode
 // One thread per anchor over all levels of all images (one launch instead of one per
 // level).  Per anchor (k_decode, engine/engine.cu:844-906): first-max argmax over the nc

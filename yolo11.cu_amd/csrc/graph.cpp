@@ -127,10 +127,11 @@ bool validateGraph(GraphDesc& g, std::string& err) {
   const Shape in = shp(0);
   if (g.imgsz && (in.H != g.imgsz || in.W != g.imgsz)) return bad("imgsz header mismatch");
   if (g.tens[0].coff != 0) return bad("input tensor must start at channel 0 of its buffer");
-  if (g.task == "classify") return bad("task classify is not supported by this engine");
-  if (g.task != "detect" && g.task != "segment" && g.task != "obb") return bad("unknown task " + g.task);
+  if (g.task != "detect" && g.task != "segment" && g.task != "obb" && g.task != "classify")
+    return bad("unknown task " + g.task);
   g.seg = g.task == "segment";
   g.obb = g.task == "obb";
+  g.cls = g.task == "classify";
 
   int nlev = 0;
   g.numAnchors = 0;
@@ -196,9 +197,26 @@ bool validateGraph(GraphDesc& g, std::string& err) {
         if (!al8(op.a) || !al8(op.out)) return bad(at + "ATTN needs 8-aligned views");
         break;
       }
+      case GAP: {
+        if (!tenOk(op.a) || !tenOk(op.out)) return bad(at + "tensor id out of range");
+        Shape x = shp(op.a), y = shp(op.out);
+        if (y.H != 1 || y.W != 1 || y.C != x.C) return bad(at + "GAP output must be [1,1,C] of its input's C");
+        if (!al8(op.a) || !al8(op.out)) return bad(at + "GAP needs 8-aligned views");
+        break;
+      }
+      case SOFTMAX: {
+        if (!tenOk(op.a) || !tenOk(op.out)) return bad(at + "tensor id out of range");
+        Shape x = shp(op.a), y = shp(op.out);
+        if (x.H != 1 || x.W != 1 || y.H != 1 || y.W != 1 || x.C != y.C)
+          return bad(at + "SOFTMAX works on [1,1,C] views of equal C");
+        if (!g.cls) return bad(at + "SOFTMAX needs task=classify");
+        g.probsTen = op.out;
+        break;
+      }
       case DECODE:
       case DECODESEG:
       case DECODEOBB: {
+        if (g.cls) return bad(at + "classify graphs have no DECODE ops");
         if (!tenOk(op.a) || !tenOk(op.b)) return bad(at + "tensor id out of range");
         Shape bx = shp(op.a), c = shp(op.b);
         if (bx.C != 64) return bad(at + "DECODE box view must have 64 channels (4 x reg_max 16)");
@@ -237,7 +255,7 @@ bool validateGraph(GraphDesc& g, std::string& err) {
         break;
       }
       default:
-        return bad(at + "op kind not supported by this engine (GAP/SOFTMAX)");
+        return bad(at + "unknown op kind");
     }
   }
   if (g.seg) {
@@ -247,6 +265,16 @@ bool validateGraph(GraphDesc& g, std::string& err) {
       if (op.kind == DECODESEG && shp(op.out).C != g.nm) return bad("DECODESEG coef count != proto channels");
   }
   if (g.obb && g.protoTen >= 0) return bad("obb graphs carry no MASKS op");
+  if (g.cls) {
+    // engine/engine.cu:180-190: the probabilities are fetched per image at buffer stride,
+    // so they must be a standalone full-width [1,1,nc] buffer
+    if (g.probsTen < 0) return bad("classify graph without SOFTMAX");
+    if (g.protoTen >= 0) return bad("classify graphs carry no MASKS op");
+    const auto& T = g.tens[g.probsTen];
+    const auto& Bf = g.bufs[T.buf];
+    if (T.coff || T.C != Bf.C || Bf.H != 1 || Bf.W != 1 || T.C != g.nc)
+      return bad("probs tensor must be a standalone [1,1,nc] buffer");
+  }
   g.detStride = g.obb ? 7 : 6 + (g.seg ? g.nm : 0);
   g.outK = g.obb ? 7 : 6;
   return true;

@@ -317,6 +317,40 @@ class ModelGraph:
                     o[:, di::2, dj::2, :] = u[..., q * C:(q + 1) * C]
         return out
 
+    def gap(self, x, out):
+        """Global average pool [H,W,C] -> [1,1,C] (export/export.py:199-202)."""
+        H, W, C = self.shape(x)
+        assert self.shape(out) == (1, 1, C)
+        self.ops.append(("GAP", x, out))
+        if self.cal:
+            self.val(out)[...] = self.val(x).mean(axis=(1, 2), keepdims=True)
+        return out
+
+    def linear(self, x, O: int):
+        """nn.Linear(I, O) on a [1,1,I] tensor as a 1x1 CONV (export/export.py:208-217):
+        weights N(0, 1/I), bias U(+-1/sqrt(I)) (torch's default bias range), no activation."""
+        H, W, I = self.shape(x)
+        assert (H, W) == (1, 1)
+        out = self.newt(1, 1, O)
+        w = self.rng.standard_normal((O, 1, 1, I), dtype=np.float32) / np.float32(math.sqrt(I))
+        bound = 1.0 / math.sqrt(I)
+        b = self.rng.uniform(-bound, bound, O).astype(np.float32)
+        woff, boff = self.add_weight(w, b)
+        self.ops.append(("CONV", x, out, 1, 1, 0, 1, ACT_NONE, I, O, woff, boff))
+        if self.cal:
+            self.val(out)[...] = self.val(x) @ w.reshape(O, I).T + b
+        return out
+
+    def softmax(self, x, out):
+        """Channel softmax of a [1,1,C] tensor (export/export.py:204-206)."""
+        assert self.shape(x) == self.shape(out)
+        self.ops.append(("SOFTMAX", x, out))
+        if self.cal:
+            v = self.val(x)
+            e = np.exp(v - v.max(axis=-1, keepdims=True))
+            self.val(out)[...] = e / e.sum(axis=-1, keepdims=True)
+        return out
+
     # -- serialisation (export/export.py:709-719) -------------------------------------
     def write(self, path: str, task: str, nc: int, imgsz: int):
         os.makedirs(path, exist_ok=True)
@@ -454,7 +488,10 @@ def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc
                 calibrate: bool = True) -> ModelInfo:
     """Builds the flat op graph of a seeded random-init YOLO model (export/export.py:317-441)."""
     assert arch in SCALES and scale in SCALES[arch], (arch, scale)
-    assert task in ("detect", "segment", "obb"), task
+    assert task in ("detect", "segment", "obb", "classify"), task
+    cls_task = task == "classify"
+    assert not cls_task or arch == "yolo11", "classify models: yolo11 only"
+
     assert imgsz % 32 == 0
     depth, width, max_ch = SCALES[arch][scale]
     v11 = arch == "yolo11"
@@ -466,7 +503,10 @@ def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc
     # resolve module args (parse_model rules)
     layers = []
     ch, hw = {-1: 3}, {-1: S}
-    for i, (f, n, m, args) in enumerate(LAYERS[arch]):
+    # yolo11-cls: the detect backbone's layers 0-8, then C2PSA (no SPPF, no neck), then
+    # the Classify head (docs/specs/cls.md:29-41)
+    table = LAYERS[arch][:9] + [(-1, 2, "C2PSA", [1024])] if cls_task else LAYERS[arch]
+    for i, (f, n, m, args) in enumerate(table):
         srcs = [(i - 1 if j == -1 else j) for j in ([f] if isinstance(f, int) else f)]
         n_ = max(round(n * depth), 1) if n > 1 else n
         c1 = ch[srcs[0]]
@@ -529,6 +569,15 @@ def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc
                 g.copyc(outs[s], g.ten(catbuf[i], off, ch[s]))
             y = g.ten(catbuf[i], 0, ch[i])
         outs[i] = y
+
+    if cls_task:
+        # Classify (export/export.py:391-398): Conv(c1, 1280, 1) -> GAP -> Linear(1280, nc)
+        # -> softmax; the head width 1280 is fixed (docs/specs/cls.md:53-54)
+        h = g.conv(outs[n_body - 1], ConvSpec(ch[n_body - 1], 1280, 1))
+        gp = g.gap(h, g.newt(1, 1, 1280))
+        logits = g.linear(gp, nc)
+        g.softmax(logits, g.newt(1, 1, nc))
+        return ModelInfo(arch, scale, task, nc, imgsz, g, seed, cls_bias)
 
     # Detect / Segment / OBB head (export/export.py:400-438)
     feats_idx = HEAD_FROM[arch]

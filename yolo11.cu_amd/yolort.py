@@ -267,6 +267,17 @@ class Engine:
         """OBB survivors as rows (cx, cy, w, h, theta, score, cls) in original-image coords."""
         return self._records(self.lib.yolo_get_obb, YoloObbDet, 7, slot, cap)
 
+    def preprocess_cls(self, dev_ptr: int, h: int, w: int, slot: int = 0):
+        self.lib.yolo_preprocess_cls(self.h, dev_ptr, h, w, slot)
+
+    def get_cls(self, slot: int = 0, k: int = 5) -> tuple[np.ndarray, np.ndarray]:
+        """Top-k (class ids, probabilities) of a classify handle's slot."""
+        ids = np.empty(k, np.int32)
+        probs = np.empty(k, np.float32)
+        n = self.lib.yolo_get_cls(self.h, slot, ids.ctypes.data_as(C.POINTER(C.c_int)),
+                                  probs.ctypes.data_as(C.POINTER(C.c_float)), k)
+        return ids[:n].copy(), probs[:n].copy()
+
     def raw_count(self, slot: int = 0) -> int:
         return self.lib.yolo_raw_count(self.h, slot)
 
