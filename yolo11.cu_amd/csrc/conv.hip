@@ -109,7 +109,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
-template <int BM, int BN, int WM, int WN, int BK, int NS, bool KONE>
+template <int BM, int BN, int WM, int WN, int BK, int NS, int KM>
 __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     View x, View y, View r, const f16* __restrict__ w, const float* __restrict__ bias,
     int ksz, int cs, int cp, int act, int M, int N, int Ktot, int mtiles, int ntiles,
@@ -170,6 +170,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   __amdgpu_buffer_rsrc_t rw =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(w), (short)0, N * Ktot * 2, 0x00020000);
 
+  constexpr bool KONE = KM == KM_ONE;
+  const int Cin = x.C;
+  const int c8 = 8 * c;   // this thread's channel offset inside every stage's BK channels
   int apb[IA], aiy[IA], aix[IA];
   bool aok[IA];
 #pragma unroll
@@ -200,74 +203,119 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
     bw[i] = bok[i] ? n * Ktot : 0;
   }
 
-  // K order.  Tap-major (the weights' memory order, k = (ky*ksz + kx)*Cin + ci) for 1x1
-  // convs and when Cin is not a multiple of BK; otherwise channel-block-major: stage
-  // (cb, tap) covers channels [cb*BK, cb*BK + BK) of tap `tap`, all taps of one channel
-  // block before the next.  The reduction is order-free; channel-block-major keeps a block's
-  // live input window at BK channels (about 20 KB for a 128-pixel tile at BK = 32) instead
-  // of all Cin channels, so the 9 taps re-read it from L2 rather than HBM.
-  // State of this thread's chunk for the next stage to issue: kw = flat k in the weight row,
-  // (ky, kx, ci) its tap and channel, toff = its element offset from the pixel's (0, 0) tap.
-  const int Cin = x.C;
-  const bool cbmajor = !KONE && ksz > 1 && Cin % BK == 0;
   const int nkt = (Ktot + BK - 1) / BK;         // K stages of a whole tile
   const int st0 = tail ? split * spl : 0;       // first K stage of this block
-  int kw = st0 * BK + 8 * c;
-  int ci = 0, kx = 0, ky = 0, toff = 0;
-  if (!KONE) {
-    int tap;
-    if (cbmajor) {
-      const int taps = ksz * ksz, cb = st0 / taps;
-      tap = st0 - cb * taps;
-      ci = cb * BK + 8 * c;
-    } else {
-      ci = kw % Cin;
-      tap = kw / Cin;
-    }
-    ky = tap / ksz;
-    kx = tap - ky * ksz;
-    kw = (ky * ksz + kx) * Cin + ci;
-    toff = (ky * x.W + kx) * x.s + ci;
-  }
-  const int rowstep = (x.W - ksz) * x.s;              // last tap of a row -> first of the next
-  const int cbstep = BK - ksz * x.W * x.s;            // last tap -> (0, 0) of the next channel block
+  const int rowstep = (x.W - ksz) * x.s;        // last tap of a row -> first of the next
+  const int cbstep = BK - ksz * x.W * x.s;      // last tap -> (0, 0) of the next channel block
   const int kwstep = BK - ksz * ksz * Cin;
 
-  auto issue = [&](f16x8* buf) {
-    const bool kin = kw < Ktot;
+  // Byte offsets of this thread's chunks at K position 0; rows outside M (and output
+  // channels outside N) start at OOB_OFF, which stays past num_records after any K offset
+  // (K offsets are far below 2^31), so their loads return zeros without a per-load test.
+  unsigned a2[IA], b2[IB];
+#pragma unroll
+  for (int i = 0; i < IA; i++) a2[i] = aok[i] ? 2u * (unsigned)(apb[i] + c8) : OOB_OFF;
+#pragma unroll
+  for (int i = 0; i < IB; i++) b2[i] = bok[i] ? 2u * (unsigned)(bw[i] + c8) : OOB_OFF;
+
+  // KM_ONE: stage st covers channels [st*BK, st*BK + BK); uk (uniform) is its first one.
+  // KM_UNI: channel-block-major order -- stage (cb, tap) covers channels [cb*BK, cb*BK + BK)
+  //   of tap `tap`, all taps of one channel block before the next.  The reduction is
+  //   order-free; this order keeps a block's live input window at BK channels (about 20 KB
+  //   for a 128-pixel tile at BK = 32) instead of all Cin, so the taps re-read it from L2
+  //   rather than HBM.  Every lane of a stage shares (cb, ky, kx): the walk is scalar, and
+  //   bit `tap` of tapok[i] says whether that tap of row i lies inside the image.
+  // KM_GEN: tap-major (the weights' memory order, k = (ky*ksz + kx)*Cin + ci); a stage may
+  //   straddle taps, so each lane tracks kw (flat k in the weight row), (ky, kx, ci) and
+  //   toff (element offset from the pixel's (0, 0) tap) itself.
+  int uk = 0, utoff = 0, utap = 0, uky = 0, ukx = 0;   // wave-uniform
+  unsigned tapok[KM == KM_UNI ? IA : 1];
+  int kw = 0, ci = 0, kx = 0, ky = 0, toff = 0;       // per lane (KM_GEN)
+  const int klim = Ktot - c8;   // KM_ONE: stage st is inside K for this lane iff st*BK < klim
+  if constexpr (KM == KM_ONE) {
+    uk = st0 * BK;
+  } else if constexpr (KM == KM_UNI) {
+    const int taps = ksz * ksz, cb = st0 / taps;
+    utap = st0 - cb * taps;
+    uky = utap / ksz;
+    ukx = utap - uky * ksz;
+    uk = utap * Cin + cb * BK;
+    utoff = (uky * x.W + ukx) * x.s + cb * BK;
 #pragma unroll
     for (int i = 0; i < IA; i++) {
-      unsigned off;
-      if (KONE) {
-        off = (aok[i] && kin) ? 2u * (unsigned)(apb[i] + kw) : OOB_OFF;
-      } else {
-        const int iy = aiy[i] + ky, ix = aix[i] + kx;
-        const bool ok = aok[i] && kin && (unsigned)iy < (unsigned)x.H && (unsigned)ix < (unsigned)x.W;
-        off = ok ? 2u * (unsigned)(apb[i] + toff) : OOB_OFF;
+      unsigned rows = 0, cols = 0, bits = 0;
+      for (int q = 0; q < ksz; q++) {
+        rows |= ((unsigned)(aiy[i] + q) < (unsigned)x.H ? 1u : 0u) << q;
+        cols |= ((unsigned)(aix[i] + q) < (unsigned)x.W ? 1u : 0u) << q;
       }
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(buf + (i * NW + wave) * 64), 16, off, 0, 0, 0);
+      for (int q = 0; q < ksz; q++)
+        if (rows >> q & 1u) bits |= cols << (q * ksz);
+      tapok[i] = aok[i] ? bits : 0u;
     }
+  } else {
+    kw = st0 * BK + c8;
+    ci = kw % Cin;
+    const int tap = kw / Cin;
+    ky = tap / ksz;
+    kx = tap - ky * ksz;
+    toff = (ky * x.W + kx) * x.s + ci;
+  }
+
+  auto issue = [&](f16x8* buf) {
+    if constexpr (KM == KM_ONE) {
+      const bool kin = uk < klim;
+      const unsigned ku = 2u * (unsigned)uk;
 #pragma unroll
-    for (int i = 0; i < IB; i++) {
-      const unsigned off = (bok[i] && kin) ? 2u * (unsigned)(bw[i] + kw) : OOB_OFF;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(buf + (QA + i * NW + wave) * 64), 16, off, 0, 0, 0);
-    }
-    if (KONE) {
-      kw += BK;
-    } else if (cbmajor) {
-      kw += Cin;
-      toff += x.s;
-      if (++kx == ksz) {
-        kx = 0;
-        toff += rowstep;
-        if (++ky == ksz) {
-          ky = 0;
-          ci += BK;
-          toff += cbstep;
-          kw += kwstep;
+      for (int i = 0; i < IA; i++) {
+        const unsigned off = kin ? a2[i] + ku : OOB_OFF;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(buf + (i * NW + wave) * 64), 16, off, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < IB; i++) {
+        const unsigned off = kin ? b2[i] + ku : OOB_OFF;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(buf + (QA + i * NW + wave) * 64), 16, off, 0, 0, 0);
+      }
+      uk += BK;
+    } else if constexpr (KM == KM_UNI) {
+      // Cin % BK == 0: every issued stage (< nkt) is inside K for every lane
+      const unsigned tu = 2u * (unsigned)utoff, ku = 2u * (unsigned)uk;
+#pragma unroll
+      for (int i = 0; i < IA; i++) {
+        const unsigned off = (tapok[i] >> utap & 1u) ? a2[i] + tu : OOB_OFF;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(buf + (i * NW + wave) * 64), 16, off, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < IB; i++) {
+        const unsigned off = b2[i] + ku;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(buf + (QA + i * NW + wave) * 64), 16, off, 0, 0, 0);
+      }
+      uk += Cin;
+      utoff += x.s;
+      utap++;
+      if (++ukx == ksz) {
+        ukx = 0;
+        utoff += rowstep;
+        if (++uky == ksz) {
+          uky = 0;
+          utap = 0;
+          utoff += cbstep;
+          uk += kwstep;
         }
       }
     } else {
+      const bool kin = kw < Ktot;
+#pragma unroll
+      for (int i = 0; i < IA; i++) {
+        const int iy = aiy[i] + ky, ix = aix[i] + kx;
+        const bool ok = aok[i] && kin && (unsigned)iy < (unsigned)x.H && (unsigned)ix < (unsigned)x.W;
+        const unsigned off = ok ? 2u * (unsigned)(apb[i] + toff) : OOB_OFF;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(buf + (i * NW + wave) * 64), 16, off, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < IB; i++) {
+        const unsigned off = (bok[i] && kin) ? 2u * (unsigned)(bw[i] + kw) : OOB_OFF;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(buf + (QA + i * NW + wave) * 64), 16, off, 0, 0, 0);
+      }
       kw += BK;
       ci += BK;
       toff += BK;
@@ -563,49 +611,52 @@ int heuristicTile(int M, int N, int K) {
 }
 
 // Blocks of one tile config that fit on the chip at once (CUs x resident blocks per CU).
+template <int BM, int BN, int WM, int WN, int BK, int NS, int KM>
+static int slotsOf() {
+  int dev = 0, cus = 0, per = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_conv_gemm<BM, BN, WM, WN, BK, NS, KM>, 64 * WM * WN,
+                                                   0) != hipSuccess)
+    return 0;
+  return cus * per;
+}
 template <int BM, int BN, int WM, int WN, int BK, int NS>
-static int tileSlotsOf(bool kone) {
-  static const int slots[2] = {
-      [] {
-        int dev = 0, cus = 0, per = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_conv_gemm<BM, BN, WM, WN, BK, NS, false>,
-                                                         64 * WM * WN, 0) != hipSuccess)
-          return 0;
-        return cus * per;
-      }(),
-      [] {
-        int dev = 0, cus = 0, per = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_conv_gemm<BM, BN, WM, WN, BK, NS, true>,
-                                                         64 * WM * WN, 0) != hipSuccess)
-          return 0;
-        return cus * per;
-      }()};
-  return slots[kone ? 1 : 0];
+static int tileSlotsOf(int km) {
+  static const int slots[3] = {slotsOf<BM, BN, WM, WN, BK, NS, KM_ONE>(), slotsOf<BM, BN, WM, WN, BK, NS, KM_UNI>(),
+                               slotsOf<BM, BN, WM, WN, BK, NS, KM_GEN>()};
+  return slots[km];
 }
 
 template <int BM, int BN, int WM, int WN, int BK, int NS>
-static void launchTile(bool kone, const View& x, const View& y, const View& r, const f16* w,
+static void launchTile(int km, const View& x, const View& y, const View& r, const f16* w,
                        const float* bias, int k, int s, int p, int act, int M, int N, int Ktot,
                        int xbytes, int dp, int splits, float* ws, int* cnt, hipStream_t st) {
   const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
   const int spl = splitStages(Ktot, BK, splits);
   const int grid = dp + (mt * nt - dp) * splits;
-  if (kone)
-    k_conv_gemm<BM, BN, WM, WN, BK, NS, true><<<grid, 64 * WM * WN, 0, st>>>(
+  if (km == KM_ONE)
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, KM_ONE><<<grid, 64 * WM * WN, 0, st>>>(
+        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, dp, splits, spl, ws, cnt);
+  else if (km == KM_UNI)
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, KM_UNI><<<grid, 64 * WM * WN, 0, st>>>(
         x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, dp, splits, spl, ws, cnt);
   else
-    k_conv_gemm<BM, BN, WM, WN, BK, NS, false><<<grid, 64 * WM * WN, 0, st>>>(
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, KM_GEN><<<grid, 64 * WM * WN, 0, st>>>(
         x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, dp, splits, spl, ws, cnt);
 }
 
-int tileSlots(int cfg, bool kone) {
+int convKMode(int cfg, int k, int s, int p, int Cin) {
+  if (k == 1 && s == 1 && p == 0) return KM_ONE;
+  const int BK = cfg >= 0 && cfg < kNumTiles ? kTiles[cfg].BK : 0;
+  return BK > 0 && Cin % BK == 0 && k * k <= 32 ? KM_UNI : KM_GEN;
+}
+
+int tileSlots(int cfg, int km) {
+  if (km < KM_ONE || km > KM_GEN) return 0;
   switch (cfg) {
 #define X(i, bm, bn, wm, wn, bk, ns) \
-    case i: return tileSlotsOf<bm, bn, wm, wn, bk, ns>(kone);
+    case i: return tileSlotsOf<bm, bn, wm, wn, bk, ns>(km);
     YOLO_TILES(X)
 #undef X
     default: return 0;
@@ -616,14 +667,14 @@ int tileSlots(int cfg, bool kone) {
 // splits < -1 ("tail split"): the tiles that fill whole chip waves run unsplit and only the
 // rest -- fewer than one wave -- are split |splits| ways (when every tile fits in one wave,
 // the split is capped so the grid stays within one wave).  Otherwise no split (dp = tiles).
-void splitPlan(int cfg, bool kone, int tiles, int splits, int* dp, int* S) {
+void splitPlan(int cfg, int km, int tiles, int splits, int* dp, int* S) {
   *dp = tiles;
   *S = 1;
   if (splits > 1) {
     *dp = 0;
     *S = splits;
   } else if (splits < -1) {
-    const int P = tileSlots(cfg, kone);
+    const int P = tileSlots(cfg, km);
     if (P <= 0) return;
     const int full = tiles / P * P;
     if (full == tiles) return;
@@ -649,16 +700,16 @@ bool splitOk(int cfg, int Ktot, int splits) {
   const int spl = splitStages(Ktot, kTiles[cfg].BK, S);
   return spl >= 1 && (S - 1) * spl < nks;   // every split gets at least one stage
 }
-int splitTiles(int cfg, bool kone, int M, int N, int splits) {
+int splitTiles(int cfg, int km, int M, int N, int splits) {
   if (cfg < 0 || cfg >= kNumTiles || splits == 1 || splits == -1) return 0;
   const TileCfg& tc = kTiles[cfg];
   const int tiles = ((M + tc.BM - 1) / tc.BM) * ((N + tc.BN - 1) / tc.BN);
   if (splits > 1) return tiles;
   // tail split at this M or any smaller batch: fewer tiles than one chip wave are split
-  return std::min(tiles, std::max(tileSlots(cfg, kone), 1));
+  return std::min(tiles, std::max(tileSlots(cfg, km), 1));
 }
-size_t splitWorkspaceBytes(int cfg, bool kone, int M, int N, int splits) {
-  const size_t t = (size_t)splitTiles(cfg, kone, M, N, splits);
+size_t splitWorkspaceBytes(int cfg, int km, int M, int N, int splits) {
+  const size_t t = (size_t)splitTiles(cfg, km, M, N, splits);
   if (t == 0) return 0;
   const TileCfg& tc = kTiles[cfg];
   return t * (size_t)(splits < 0 ? -splits : splits) * tc.BM * tc.BN * sizeof(float);
@@ -672,16 +723,16 @@ void launchConvGemm(int cfg, const View& x, const View& y, const View* res, cons
                     const float* bias, int k, int s, int p, int act, int Bn, int splits,
                     float* ws, int* cnt, hipStream_t st) {
   const int M = Bn * y.H * y.W, N = y.C, Ktot = k * k * x.C;
-  const bool kone = (k == 1 && s == 1 && p == 0);
   const int xbytes = (int)((long)Bn * x.H * x.W * x.s * 2);
   View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
   if (cfg < 0 || cfg >= kNumTiles) cfg = heuristicTile(M, N, Ktot);
+  const int km = convKMode(cfg, k, s, p, x.C);
   if (!ws || !cnt || !splitOk(cfg, Ktot, splits)) splits = 1;
   int dp, S;
-  splitPlan(cfg, kone, numTiles(cfg, M, N), splits, &dp, &S);
+  splitPlan(cfg, km, numTiles(cfg, M, N), splits, &dp, &S);
   switch (cfg) {
 #define X(i, bm, bn, wm, wn, bk, ns) \
-    case i: launchTile<bm, bn, wm, wn, bk, ns>(kone, x, y, r, w, bias, k, s, p, act, M, N, Ktot, xbytes, dp, S, ws, cnt, st); break;
+    case i: launchTile<bm, bn, wm, wn, bk, ns>(km, x, y, r, w, bias, k, s, p, act, M, N, Ktot, xbytes, dp, S, ws, cnt, st); break;
     YOLO_TILES(X)
 #undef X
     default: break;

@@ -534,12 +534,12 @@ struct Engine {
       if (op.kind != CONV || op.g != 1 || op.Cin == 3 || op.split == 1 || op.split == -1) continue;
       View y = view(op.out);
       const int M = B * y.H * y.W, cfg = op.cfg >= 0 ? op.cfg : heuristicTile(M, op.Cout, op.k * op.k * op.Cin);
-      const bool kone = op.k == 1 && op.s == 1 && op.p == 0;
+      const int km = convKMode(cfg, op.k, op.s, op.p, op.Cin);
       op.cfg = cfg;
       op.wsOff = (long)(wsTot / sizeof(float));
       op.cntOff = (long)cntTot;
-      wsTot += (splitWorkspaceBytes(cfg, kone, M, op.Cout, op.split) + 255) & ~(size_t)255;
-      cntTot += splitTiles(cfg, kone, M, op.Cout, op.split);
+      wsTot += (splitWorkspaceBytes(cfg, km, M, op.Cout, op.split) + 255) & ~(size_t)255;
+      cntTot += splitTiles(cfg, km, M, op.Cout, op.split);
     }
     ensureSplitScratch(wsTot, cntTot);
   }
@@ -578,10 +578,10 @@ struct Engine {
       if (it != cache.end()) { op.cfg = it->second.first; op.split = it->second.second; continue; }
       int best = heuristicTile(M, N, K), bestSplit = 1;
       float bestMs = 1e30f;
-      const bool kone = op.k == 1 && op.s == 1 && op.p == 0;
       for (int cfg = 0; cfg < numTileConfigs(); cfg++) {
         if (!allowed[cfg] || !tileOk(cfg, M, N, K)) continue;
-        const int tiles = numTiles(cfg, M, N), P = tileSlots(cfg, kone);
+        const int km = convKMode(cfg, op.k, op.s, op.p, op.Cin);
+        const int tiles = numTiles(cfg, M, N), P = tileSlots(cfg, km);
         std::vector<int> cands;
         for (int S : kSplits)
           if (S == 1 || (tiles * S <= 1024 && tiles < P)) cands.push_back(S);
@@ -598,7 +598,7 @@ struct Engine {
           op.cfg = cfg;
           op.split = S;
           op.wsOff = op.cntOff = S != 1 ? 0 : -1;
-          if (S != 1) ensureSplitScratch(splitWorkspaceBytes(cfg, kone, M, N, S), (size_t)splitTiles(cfg, kone, M, N, S));
+          if (S != 1) ensureSplitScratch(splitWorkspaceBytes(cfg, km, M, N, S), (size_t)splitTiles(cfg, km, M, N, S));
           for (int r = 0; r < 2; r++) runOp((int)k, B);
           float t[7];
           for (int r = 0; r < 7; r++) {

@@ -103,10 +103,17 @@ const TileCfg& tileConfig(int cfg);
 constexpr int MAX_SPLITS = 16;
 int splitStages(int Ktot, int BK, int splits);
 bool splitOk(int cfg, int Ktot, int splits);
+// K iteration mode of a GEMM conv under tile config `cfg` (the kernel is specialised on it):
+// KM_ONE  1x1 stride-1 unpadded -- a K stage is BK consecutive channels of one pixel;
+// KM_UNI  Cin % BK == 0 (at most 32 taps) -- every stage lies inside one tap, the
+//         (channel block, tap) walk is wave-uniform;
+// KM_GEN  otherwise -- stages straddle taps, tracked per lane.
+constexpr int KM_ONE = 0, KM_UNI = 1, KM_GEN = 2;
+int convKMode(int cfg, int k, int s, int p, int Cin);
 int numTiles(int cfg, int M, int N);
-int tileSlots(int cfg, bool kone);
-int splitTiles(int cfg, bool kone, int M, int N, int splits);
-size_t splitWorkspaceBytes(int cfg, bool kone, int M, int N, int splits);
+int tileSlots(int cfg, int km);
+int splitTiles(int cfg, int km, int M, int N, int splits);
+size_t splitWorkspaceBytes(int cfg, int km, int M, int N, int splits);
 void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
                     const float* bias, int k, int s, int p, int act, int Bn, int splits,
                     float* ws, int* cnt, hipStream_t st);
