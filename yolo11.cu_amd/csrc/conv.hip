@@ -570,7 +570,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   X(26, 64, 32, 2, 2, 64, 8)          \
   X(27, 64, 64, 2, 2, 64, 6)          \
   X(28, 32, 32, 2, 2, 128, 4)         \
-  X(29, 64, 16, 4, 1, 128, 5)
+  X(29, 64, 16, 4, 1, 128, 5)         \
+  X(30, 256, 256, 4, 4, 32, 3)        \
+  X(31, 256, 256, 4, 4, 64, 2)
 
 static const TileCfg kTiles[] = {
 #define X(i, bm, bn, wm, wn, bk, ns) {bm, bn, wm, wn, bk, ns},
