@@ -1,0 +1,122 @@
+"""The gRPC server with real engines on the GPU: concurrent requests over 127.0.0.1 for a detect,
+a segment and a classify model in one process; every response is checked against a direct
+engine handle run on the same decoded pixels, to the parity bar (same kept count, classes and
+order; box IoU >= 0.99, |d score| <= 5e-3; mask IoU >= 0.99; same top-5)."""
+import io
+from concurrent.futures import ThreadPoolExecutor
+
+import grpc
+import numpy as np
+import pytest
+from PIL import Image
+
+import modelgen
+import yolort
+import yoloserve
+
+pytestmark = pytest.mark.gpu
+FLAGS = yolort.YOLO_NOTUNE
+
+
+def _encode(img_bgr, fmt):
+    buf = io.BytesIO()
+    kw = {"quality": 92} if fmt == "JPEG" else {}
+    Image.fromarray(img_bgr[..., ::-1].copy()).save(buf, format=fmt, **kw)
+    return buf.getvalue()
+
+
+def _direct(eng, img):
+    dev = yolort.DeviceBuffer(img.nbytes)
+    eng.upload(dev, img)
+    h, w = img.shape[:2]
+    if eng.task() == 2:
+        eng.preprocess_cls(dev.ptr, h, w, 0)
+    else:
+        eng.preprocess(dev.ptr, h, w, 0)
+    eng.run(1)
+    out = {"boxes": eng.get(0) if eng.task() != 2 else None}
+    if eng.task() == 2:
+        out["cls"] = eng.get_cls(0, 5)
+    if eng.task() == 3:
+        out["masks"] = [eng.get_mask(0, j) for j in range(len(out["boxes"]))]
+        out["geom"] = eng.slot_geom(0)
+    dev.free()
+    return out
+
+
+def _mask_iou(a, b):
+    a, b = a != 0, b != 0
+    u = int((a | b).sum())
+    return 1.0 if u == 0 else int((a & b).sum()) / u
+
+
+def _iou(a, b):
+    ix = max(0.0, min(a[2], b[2]) - max(a[0], b[0]))
+    iy = max(0.0, min(a[3], b[3]) - max(a[1], b[1]))
+    inter = ix * iy
+    u = (a[2] - a[0]) * (a[3] - a[1]) + (b[2] - b[0]) * (b[3] - b[1]) - inter
+    return inter / u if u > 0 else 1.0
+
+
+def test_server_matches_direct_engine(models):
+    dirs = {"det": models("yolo11", "n"), "seg": models("yolo11", "n", "segment"),
+            "cls": models("yolo11", "n", "classify", imgsz=224, nc=1000)}
+    limits = {"det": 4, "seg": 2, "cls": 3}
+    served = [yoloserve.Model(n, yolort.Engine(d, limits[n], FLAGS), limits[n]) for n, d in dirs.items()]
+    direct = {n: yolort.Engine(d, 1, FLAGS) for n, d in dirs.items()}
+    srv = yoloserve.Server(served, target_ms=20.0, log=lambda *a: None)
+    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0")
+    cl = yoloserve.Client(f"127.0.0.1:{port}")
+    try:
+        frames = [modelgen.synth_frame(480 + 40 * (i % 3), 640 + 64 * (i % 2), 20, 300 + i) for i in range(12)]
+        route = [["det", "seg", "cls", ""][i % 4] for i in range(12)]
+        fmt = ["PNG"] * 11 + ["JPEG"]
+        payload = [_encode(f, fm) for f, fm in zip(frames, fmt)]
+        print("server: 12 concurrent requests over det/seg/cls", flush=True)
+        with ThreadPoolExecutor(12) as ex:
+            resps = list(ex.map(lambda i: cl.detect(payload[i], route[i], timeout=120), range(12)))
+        for i, r in enumerate(resps):
+            name = route[i] or "det"
+            img = yoloserve.decode_image(payload[i])          # the server's own decoder
+            want = _direct(direct[name], img)
+            assert 1 <= r.batch <= limits[name]
+            if name == "cls":
+                assert r.task == "classify"
+                ids, probs = want["cls"]
+                assert [c.id for c in r.classes] == ids.tolist()
+                assert np.abs(np.array([c.prob for c in r.classes]) - probs).max() <= 5e-3
+                continue
+            assert r.task == ("segment" if name == "seg" else "detect")
+            wb = want["boxes"]
+            assert len(r.boxes) == len(wb), (i, len(r.boxes), len(wb))
+            for bx, w in zip(r.boxes, wb):
+                assert bx.cls == int(w[5])
+                assert abs(bx.score - w[4]) <= 5e-3
+                assert _iou((bx.x1, bx.y1, bx.x2, bx.y2), w[:4]) >= 0.99
+            if name == "seg":
+                assert (r.mask_h, r.mask_w) == direct["seg"].mask_dim()
+                sc, top, left = want["geom"]
+                assert abs(r.lb_scale - sc) <= 1e-6 and (r.lb_top, r.lb_left) == (top, left)
+                n = r.mask_h * r.mask_w
+                for mk, wm in zip(r.masks, want["masks"]):
+                    got = yoloserve.rle_decode(mk.rle, n).reshape(r.mask_h, r.mask_w)
+                    assert _mask_iou(got, wm) >= 0.99
+        # error paths through the real server
+        with pytest.raises(grpc.RpcError) as ei:
+            cl.detect(payload[0], "yolo-missing")
+        assert ei.value.code() == grpc.StatusCode.INVALID_ARGUMENT
+        with pytest.raises(grpc.RpcError) as ei:
+            cl.detect(b"\x89PNG\r\n\x1a\nbroken", "det")
+        assert ei.value.details() == "image decode failed"
+        # a short closed-loop load on the detect model
+        stats = yoloserve.bench(f"127.0.0.1:{port}", payload[:8:4], "det", concurrency=16, seconds=2.0)
+        print(f"server bench (yolo11n, 16 callers, PNG 480-560x640-704): {stats}", flush=True)
+        assert stats["requests"] > 0
+    finally:
+        cl.close()
+        gs.stop(0)
+        srv.stop()
+        for m in served:
+            m.eng.close()
+        for e in direct.values():
+            e.close()

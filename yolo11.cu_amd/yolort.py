@@ -244,6 +244,10 @@ class Engine:
     def run(self, B: int = 1):
         self.lib.yolo_run(self.h, B)
 
+    def run_async(self, B: int = 1):
+        """Launches the batch-B graph on the engine stream and returns; `sync` waits."""
+        self.lib.yolo_run_async(self.h, B)
+
     def sync(self):
         self.lib.yolo_sync(self.h)
 
