@@ -319,6 +319,57 @@ def bench_conv(workdir, iters):
                 copy_gbs=copy_bytes / copy_ms / 1e6)
 
 
+def bench_serve(workdir, seconds=4.0, procs=4, callers=16):
+    """The gRPC server (yoloserve) with yolo11n, max batch 16, target 50 ms (the reference
+    server's defaults, server/serve.cpp:344-346), decode on the request threads, under a closed loop of
+    `procs` client processes x `callers` threads sending 640x640 JPEG frames over 127.0.0.1.
+    Throughput is the sum over the client processes; p50 is the median of their medians,
+    p99 the worst of their p99s."""
+    import io
+    import subprocess
+    import modelgen
+    import yolort
+    import yoloserve
+    from PIL import Image
+    d = os.path.join(workdir, "yolo11n_serve")
+    modelgen.write_model(d, "yolo11", "n", cls_bias=-8.0)
+    paths = []
+    for i in range(16):
+        p = os.path.join(workdir, f"serve_{i}.jpg")
+        Image.fromarray(modelgen.synth_frame(640, 640, 50, 500 + i)[..., ::-1].copy()).save(p, "JPEG", quality=90)
+        paths.append(p)
+    models = [yoloserve.Model("yolo11n", yolort.Engine(d, 16), 16)]
+    srv = yoloserve.Server(models, target_ms=50.0, log=lambda *a: None)
+    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0")
+    script = os.path.join(ROOT, "yolo11.cu_amd", "yoloserve.py")
+    imgs = sum([["--image", p] for p in paths], [])
+
+    def load(secs):
+        cmd = [sys.executable, script, "bench", "--addr", f"127.0.0.1:{port}", "--concurrency", str(callers),
+               "--seconds", str(secs)] + imgs
+        ps = [subprocess.Popen(cmd, stdout=subprocess.PIPE, text=True) for _ in range(procs)]
+        res = []
+        for p in ps:
+            out, _ = p.communicate(timeout=secs + 120)
+            if p.returncode != 0:
+                raise RuntimeError(f"client process failed ({p.returncode})")
+            res.append(json.loads(out.strip().splitlines()[-1]))
+        return res
+
+    try:
+        load(1.0)                                        # warm-up (connections, graphs)
+        res = load(seconds)
+    finally:
+        gs.stop(0)
+        srv.stop()
+        models[0].eng.close()
+    import numpy as np
+    return dict(clients=procs * callers, client_procs=procs, img_per_s=sum(r["img_per_s"] for r in res),
+                p50_ms=float(np.median([r["p50_ms"] for r in res])), p99_ms=max(r["p99_ms"] for r in res),
+                mean_batch=float(np.mean([r["mean_batch"] for r in res])), requests=sum(r["requests"] for r in res),
+                exec_ms_b16=round(models[0].exec_ms, 4), frames="640x640 JPEG q90, decoded by PIL on the server")
+
+
 def cpu_baseline(budget_s=15.0):
     import numpy as np
     import modelgen
@@ -359,7 +410,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "n", "x", "conv", "obb", "seg", "m", "sweep", "cls"],
+    ap.add_argument("--only", choices=["all", "n", "x", "conv", "obb", "seg", "m", "sweep", "cls", "serve"],
                     default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
@@ -408,6 +459,10 @@ def main():
             out["seg"] = bench_task(workdir, "segment", 640, 80, -8.0, modelgen.synth_polygons(640, 640, 30, 4),
                                     args.steps, args.warmup, not args.no_graph)
             log(out["seg"])
+    if args.only in ("all", "serve") and not args.no_graph:
+        log("gRPC server, yolo11n, 4 client processes x 16 callers ...")
+        out["serve"] = bench_serve(workdir)
+        log(out["serve"])
     if args.no_graph:
         log("stream-ordered profiling pass done")
         return
@@ -452,6 +507,9 @@ def main():
                                       "top1": r["top1"]}
     if out.get("sweep"):
         line["conv_sweep"] = out["sweep"]
+    if out.get("serve"):
+        line["grpc_server_yolo11n"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                       for k, v in out["serve"].items()}
     if conv:
         achieved = conv["flops"] / (conv["ms"] * 1e-3)
         line["roofline"] = {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": 2500.0,

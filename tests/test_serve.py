@@ -221,7 +221,7 @@ def test_grpc_roundtrip_fake_engines():
     names = ["det", "seg", "cls", "obb"]
     engs = [FakeEngine(0), FakeEngine(3), FakeEngine(2), FakeEngine(1)]
     models = [yoloserve.Model(n, e, 4) for n, e in zip(names, engs)]
-    srv = FakeServer(models, target_ms=40.0, decoders=2, log=lambda *a: None)
+    srv = FakeServer(models, target_ms=40.0, log=lambda *a: None)
     gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0", workers=48)
     cl = yoloserve.Client(f"127.0.0.1:{port}")
     try:
@@ -283,7 +283,7 @@ def test_grpc_roundtrip_fake_engines():
 def test_deadline_fires_partial_batch():
     """A lone request is answered once its slack is used up, not when a batch fills."""
     eng = FakeEngine(0)
-    srv = FakeServer([yoloserve.Model("det", eng, 16)], target_ms=30.0, decoders=1, log=lambda *a: None)
+    srv = FakeServer([yoloserve.Model("det", eng, 16)], target_ms=30.0, log=lambda *a: None)
     try:
         t0 = time.monotonic()
         req = srv.submit(_png((5, 6, 7)))

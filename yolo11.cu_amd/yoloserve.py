@@ -14,13 +14,17 @@ the same C ABI; gRPC C++ and protoc are not available here):
   request would miss `--target-ms` if the batcher waited for a full batch, given that model's
   calibrated `yolo_exec_ms(maxB)`, a decode-time EMA and a 1 ms margin; batches never mix
   models (server/serve.cpp:163-191);
-* two-stage pipeline: batch k+1 is decoded on a CPU pool while the GPU runs batch k
-  (server/serve.cpp:264-302).  The decoder is PIL for every format (the reference decodes
-  JPEG with nvJPEG and PNG with stb; pixel values of a lossy JPEG can differ by decoder);
+* decode overlaps the GPU (server/serve.cpp:264-302), here one step earlier: every request
+  is decoded on its own gRPC handler thread as it arrives, so the batcher collects ready
+  pixels and the worker only stages them and launches, while the next batch's images decode
+  during the current batch's GPU time.  The decoder is PIL for every format (the reference
+  decodes JPEG with nvJPEG and PNG with stb; pixel values of a lossy JPEG can differ by
+  decoder).  An undecodable image is answered at once and never takes a batch slot;
 * responses carry the task's fields -- boxes, rotated boxes, top-5 classes, or boxes plus
   RLE masks at proto resolution with the letterbox geometry -- and queue_ms, infer_ms and
   the batch size (server/serve.cpp:193-256); an undecodable image is INVALID_ARGUMENT
-  "image decode failed".
+  "image decode failed".  The slack formula's decode term is an EMA of the worker's per-batch
+  staging time (upload + preprocess).
 
 All engine calls happen on the one worker thread (the engine handle is not thread-safe);
 gRPC handler threads only enqueue and wait.
@@ -30,6 +34,7 @@ from __future__ import annotations
 import argparse
 import collections
 import io
+import json
 import os
 import sys
 import threading
@@ -75,10 +80,18 @@ def decode_image(data: bytes) -> np.ndarray | None:
     try:
         from PIL import Image
         with Image.open(io.BytesIO(data)) as im:
-            rgb = np.asarray(im.convert("RGB"))
-        if rgb.ndim != 3 or rgb.shape[0] < 1 or rgb.shape[1] < 1:
+            if im.mode != "RGB":
+                im = im.convert("RGB")
+            w, h = im.size
+            rgb = np.frombuffer(im.tobytes(), np.uint8).reshape(h, w, 3)
+        if h < 1 or w < 1:
             return None
-        return np.ascontiguousarray(rgb[..., ::-1])
+        # three plane copies: numpy runs them without the GIL, unlike a reversed-stride copy
+        bgr = np.empty_like(rgb)
+        bgr[..., 0] = rgb[..., 2]
+        bgr[..., 1] = rgb[..., 1]
+        bgr[..., 2] = rgb[..., 0]
+        return bgr
     except Exception:
         return None
 
@@ -116,10 +129,10 @@ def parse_dir_spec(spec: str, max_batch: int) -> tuple[str, str, int]:
 # ------------------------------------------------------------------ server
 
 class _Request:
-    __slots__ = ("data", "arrival", "resp", "error", "done")
+    __slots__ = ("img", "arrival", "resp", "error", "done")
 
-    def __init__(self, data: bytes):
-        self.data = data
+    def __init__(self):
+        self.img = None
         self.arrival = time.monotonic()
         self.resp = pb.DetectResponse()
         self.error = None
@@ -141,19 +154,17 @@ class Model:
 
 
 class Server:
-    """Batcher + decode pool + engine worker.  `submit` is called from any thread."""
+    """Batcher + engine worker.  `submit` (decode + enqueue) is called from any thread."""
 
-    def __init__(self, models: list[Model], target_ms: float = 50.0, decoders: int | None = None,
-                 log=print):
+    def __init__(self, models: list[Model], target_ms: float = 50.0, log=print):
         if not models:
             raise ValueError("no models")
         self.models = models
         self.by_name = {m.name: i for i, m in enumerate(models)}
         self.target_ms = float(target_ms)
-        self.decode_ema = 2.0
+        self.stage_ema = 1.0
         self.log = log
         self.cv = threading.Condition()
-        self.pool = ThreadPoolExecutor(max_workers=decoders or min(8, max(2, (os.cpu_count() or 4) - 2)))
         self.buffers: dict[int, object] = {}
         self.served = 0
         self._stop = False
@@ -188,8 +199,16 @@ class Server:
         return self.by_name[name]
 
     def submit(self, image: bytes, model: str = "") -> _Request:
-        r = _Request(image)
+        """Decodes on the calling thread, then queues; the returned request's `done` is set
+        when its response (or error) is ready."""
         mi = self.model_index(model)
+        r = _Request()
+        r.img = decode_image(image)
+        if r.img is None:
+            r.error = "image decode failed"
+            r.resp.task = self.models[mi].task_name
+            r.done.set()
+            return r
         with self.cv:
             if self._stop:
                 r.error = "server shutting down"
@@ -207,7 +226,7 @@ class Server:
                     return None
                 qs = [(len(m.queue), m.queue[0].arrival if m.queue else 0.0, m.max_batch, m.exec_ms)
                       for m in self.models]
-                pick, fire, slack = pick_queue(qs, time.monotonic(), self.target_ms, self.decode_ema)
+                pick, fire, slack = pick_queue(qs, time.monotonic(), self.target_ms, self.stage_ema)
                 if pick >= 0 and fire:
                     break
                 self.cv.wait(None if pick < 0 else min(max(slack, 0.0) * 1e-3, 2e-4))
@@ -223,19 +242,18 @@ class Server:
                 if got is None:
                     break
                 mi, batch = got
-                t0 = time.monotonic()
-                imgs = list(self.pool.map(decode_image, [r.data for r in batch]))   # || GPU on prev
-                self.decode_ema = 0.9 * self.decode_ema + 0.1 * (time.monotonic() - t0) * 1e3
                 if prev is not None:
                     self._finish(*prev)
                     prev = None
                 m = self.models[mi]
-                for i, img in enumerate(imgs):
-                    if img is not None:
-                        self._stage(m, i, img)
+                t0 = time.monotonic()
+                for i, r in enumerate(batch):
+                    self._stage(m, i, r.img)
+                    r.img = None
                 launch = time.monotonic()
+                self.stage_ema = 0.9 * self.stage_ema + 0.1 * (launch - t0) * 1e3
                 m.eng.run_async(len(batch))
-                prev = (mi, batch, [img is not None for img in imgs], launch)
+                prev = (mi, batch, launch)
                 with self.cv:
                     idle = all(not q.queue for q in self.models)
                 if idle:                  # no traffic behind it: answer now
@@ -259,17 +277,14 @@ class Server:
                     r.error = "server shutting down"
                     r.done.set()
 
-    def _finish(self, mi: int, batch: list, ok: list, launch: float):
+    def _finish(self, mi: int, batch: list, launch: float):
         m = self.models[mi]
         m.eng.sync()
         infer_ms = (time.monotonic() - launch) * 1e3
         for i, r in enumerate(batch):
             resp = r.resp
             resp.task = m.task_name
-            if ok[i]:
-                self._fill(m, i, resp)
-            else:
-                r.error = "image decode failed"
+            self._fill(m, i, resp)
             resp.queue_ms = (launch - r.arrival) * 1e3
             resp.infer_ms = infer_ms
             resp.batch = len(batch)
@@ -309,7 +324,6 @@ class Server:
             self._stop = True
             self.cv.notify_all()
         self._worker.join()
-        self.pool.shutdown(wait=True)
         for b in self.buffers.values():
             b.free()
         self.buffers.clear()
@@ -382,17 +396,18 @@ def bench(addr: str, images: list[bytes], model: str = "", concurrency: int = 32
     """Closed-loop load: `concurrency` callers each send the next image as soon as the last
     answer arrives; returns throughput and latency percentiles."""
     cl = Client(addr)
-    lat, lock = [], threading.Lock()
+    lat, batches, lock = [], [], threading.Lock()
     stop_at = time.monotonic() + seconds
 
     def caller(k):
         i = k
         while time.monotonic() < stop_at:
             t0 = time.monotonic()
-            cl.detect(images[i % len(images)], model)
+            r = cl.detect(images[i % len(images)], model)
             dt = (time.monotonic() - t0) * 1e3
             with lock:
                 lat.append(dt)
+                batches.append(r.batch)
             i += concurrency
 
     t0 = time.monotonic()
@@ -402,7 +417,7 @@ def bench(addr: str, images: list[bytes], model: str = "", concurrency: int = 32
     cl.close()
     a = np.array(lat)
     return dict(requests=int(a.size), img_per_s=a.size / wall, p50_ms=float(np.percentile(a, 50)),
-                p99_ms=float(np.percentile(a, 99)), concurrency=concurrency)
+                p99_ms=float(np.percentile(a, 99)), mean_batch=float(np.mean(batches)), concurrency=concurrency)
 
 
 def main(argv=None):
@@ -416,7 +431,7 @@ def main(argv=None):
         ap.add_argument("--seconds", type=float, default=10.0)
         a = ap.parse_args(argv[1:])
         imgs = [open(p, "rb").read() for p in a.image]
-        print(bench(a.addr, imgs, a.model, a.concurrency, a.seconds), flush=True)
+        print(json.dumps(bench(a.addr, imgs, a.model, a.concurrency, a.seconds)), flush=True)
         return 0
     ap = argparse.ArgumentParser(prog="yoloserve", description="gRPC yolo.Yolo/Detect server")
     ap.add_argument("--dir", action="append", default=[], help="model dir[:max batch]; repeatable")
