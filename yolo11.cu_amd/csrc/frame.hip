@@ -257,13 +257,22 @@ void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lst, int
 constexpr int NMS_THREADS = 1024;
 constexpr int NMS_CLASSES = 1024;            // class histogram size of the per-class path
 constexpr int NMS_WAVE_CLASS = 256;          // largest class one wave resolves alone
+constexpr int NMS_THREAD_CLASS = 16;         // up to 512 candidates: per-thread rows up to this class size
 
 // inter/union > thr, decided without the division unless the two sides are within a few
 // ulps (then the division decides, exactly as the reference writes it)
+// A value every lane of the wave holds (an LDS word read at a uniform address), moved to a
+// scalar register so the control flow that depends on it stays scalar.
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// (compare-selects rather than fmaxf/fminf: box coordinates are finite, and the selects need
+// no NaN canonicalisation of their operands)
+__device__ __forceinline__ float fmx(float a, float b) { return a > b ? a : b; }
+__device__ __forceinline__ float fmn(float a, float b) { return a < b ? a : b; }
 __device__ __forceinline__ bool suppresses(float4 a, float4 b, float thr) {
-  const float xx1 = fmaxf(a.x, b.x), yy1 = fmaxf(a.y, b.y);
-  const float xx2 = fminf(a.z, b.z), yy2 = fminf(a.w, b.w);
-  const float w = fmaxf(0.f, xx2 - xx1), h = fmaxf(0.f, yy2 - yy1);
+  const float xx1 = fmx(a.x, b.x), yy1 = fmx(a.y, b.y);
+  const float xx2 = fmn(a.z, b.z), yy2 = fmn(a.w, b.w);
+  const float w = fmx(0.f, xx2 - xx1), h = fmx(0.f, yy2 - yy1);
   const float inter = w * h;
   const float aarea = (a.z - a.x) * (a.w - a.y);
   const float barea = (b.z - b.x) * (b.w - b.y);
@@ -446,7 +455,8 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   __shared__ RankShared rs;
   static_assert(NMS_CLASSES == NMS_THREADS, "one class bin per thread");
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: loops over waves stay scalar
   const int img = blockIdx.x;
   const float* cimg = cand + (size_t)img * A * cstride;
   const float thr = prm->iou;
@@ -568,10 +578,12 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   __syncthreads();
 
   // 3. suppression rows.  A class is decided in chunks of 64 members; rows2[p] holds the
-  //    later members of p's chunk that p suppresses.  Up to 512 candidates the work items
-  //    are (chunk, run of 8 positions): a wave takes items round-robin, lane j holds member
-  //    j of the chunk, and each position's row is one ballot (its box read as an LDS
-  //    broadcast); a class has ceil(g / 8) items (chunk boundaries fall on multiples of 8).
+  //    later members of p's chunk that p suppresses.  Up to 512 candidates, classes of at
+  //    most NMS_THREAD_CLASS members take one thread per member; the larger ones are split
+  //    into work items (chunk, run of 8 positions): a wave takes items round-robin, lane j
+  //    holds member j of the chunk, and each position's row is one ballot (its box read as
+  //    an LDS broadcast); a class has ceil(g / 8) items (chunk boundaries fall on multiples
+  //    of 8).
   //    Above that every thread is busy anyway and one thread per position tests only the
   //    later members of its chunk (half the tests of a square ballot).
   if (m > 512) {
@@ -586,9 +598,24 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
       rows2[p] = row;
     }
   } else {
+    // A class of at most NMS_THREAD_CLASS members: one thread per member tests the later
+    // members (a 64-lane ballot would leave most lanes idle); larger classes: wave items.
+    if (tid < m) {
+      const int c = scls[perm[tid]];
+      const int g = chist[c];
+      if (g <= NMS_THREAD_CLASS) {
+        const int sc = cstart[c], a = tid - sc;
+        const float4 bp = cbox[tid];
+        unsigned long long row = 0ull;
+        for (int j = a + 1; j < g; j++)
+          if (suppresses(bp, cbox[sc + j], thr)) row |= 1ull << j;
+        rows2[tid] = row;
+      }
+    }
     {
-      // the items of class c start at cfill[c] = exclusive prefix of ceil(chist / 8)
-      const int h = (chist[tid] + 7) >> 3;
+      // the items of class c start at cfill[c] = exclusive prefix of ceil(chist / 8) over the
+      // classes above NMS_THREAD_CLASS
+      const int h = chist[tid] > NMS_THREAD_CLASS ? (chist[tid] + 7) >> 3 : 0;
       int incl = h;
       for (int o = 1; o < 64; o <<= 1) {
         const int y = __shfl_up(incl, o);
@@ -600,29 +627,30 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
       for (int w = 0; w < wave; w++) off += wsum[w];
       cfill[tid] = off + incl - h;             // cfill is free again: item start of class tid
       if (tid == NMS_THREADS - 1) nstep = off + incl;
+      // item -> class table in `bucket` (free after the layout; at most m/8 + m <= 576 items)
+      for (int i = 0; i < h; i++) bucket[off + incl - h + i] = (short)tid;
     }
     __syncthreads();
     {
-      const int nitems = nstep;
+      const int nitems = uni(nstep);
       for (int it = wave; it < nitems; it += NMS_THREADS / 64) {
-        // the class owning item `it`: the present class whose item range holds it
-        int c = -1;
-        for (int q = lane; q < npresent; q += 64) {
-          const int cq = present[q];
-          const int i0 = cfill[cq];
-          if (it >= i0 && it < i0 + ((chist[cq] + 7) >> 3)) c = cq;
-        }
-        const unsigned long long hb = __ballot(c >= 0);
-        c = __builtin_amdgcn_readlane(c, __builtin_ctzll(hb));
-        const int sc = cstart[c], g = chist[c];
-        const int a0 = (it - cfill[c]) * 8;    // first class member of the item
+        const int c = uni(bucket[it]);
+        const int sc = uni(cstart[c]), g = uni(chist[c]);
+        const int a0 = (it - uni(cfill[c])) * 8;    // first class member of the item
         const int q0 = a0 & ~63, nq = min(64, g - q0);
         const float4 bq = lane < nq ? cbox[sc + q0 + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
         const int pe = min(a0 + 8, g);
-        for (int a = a0; a < pe; a++) {
-          const float4 bp = cbox[sc + a];      // LDS broadcast
-          const unsigned long long row = __ballot(lane < nq && lane > (a & 63) && suppresses(bp, bq, thr));
-          if (lane == 0) rows2[sc + a] = row;
+        // the item's (up to 8) row boxes are LDS broadcasts requested together
+        float4 bp[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) bp[e] = cbox[sc + min(a0 + e, pe - 1)];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int a = a0 + e;
+          if (a < pe) {
+            const unsigned long long row = __ballot(lane < nq && lane > (a & 63) && suppresses(bp[e], bq, thr));
+            if (lane == 0) rows2[sc + a] = row;
+          }
         }
       }
     }
@@ -632,9 +660,10 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   // 4. per-class greedy.  `removed` holds the kept flag of every candidate by rank.
   //  4a. a class of at most 64 members is one chunk: one wave resolves its rows by a bit
   //      scan (waves take the classes round-robin)
-  for (int pc = wave; pc < npresent; pc += NMS_THREADS / 64) {
-    const int c = present[pc];
-    const int sc = cstart[c], g = chist[c];
+  const int npres = uni(npresent), nlrg = uni(nlarge);
+  for (int pc = wave; pc < npres; pc += NMS_THREADS / 64) {
+    const int c = uni(present[pc]);
+    const int sc = uni(cstart[c]), g = uni(chist[c]);
     if (g > 64) continue;                   // wave-uniform
     const bool valid = lane < g;
     const int mine = valid ? perm[sc + lane] : 0;
@@ -655,9 +684,9 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   //      (survivor boxes broadcast by readlane).  Waves take such classes round-robin; a
   //      class stops once it has max_det survivors (a later survivor ranks below max_det
   //      others and never reaches the output).
-  for (int li = wave; li < nlarge; li += NMS_THREADS / 64) {
-    const int c = large[li];
-    const int sc = cstart[c], g = chist[c];
+  for (int li = wave; li < nlrg; li += NMS_THREADS / 64) {
+    const int c = uni(large[li]);
+    const int sc = uni(cstart[c]), g = uni(chist[c]);
     if (g > NMS_WAVE_CLASS) continue;       // wave-uniform: 4c below
     int K = 0;
     for (int q0 = 0; q0 < g && K < maxdet; q0 += 64) {
@@ -699,9 +728,9 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   //  4c. a larger class goes chunk by chunk with the whole block: wave 0 resolves the chunk,
   //      then every thread strikes later members of the class that a survivor of the chunk
   //      suppresses (survivor boxes read as LDS broadcasts)
-  for (int li = 0; li < nlarge; li++) {
-    const int c = large[li];
-    const int sc = cstart[c], g = chist[c];
+  for (int li = 0; li < nlrg; li++) {
+    const int c = uni(large[li]);
+    const int sc = uni(cstart[c]), g = uni(chist[c]);
     if (g <= NMS_WAVE_CLASS) continue;      // block-uniform
     int K = 0;
     for (int q0 = 0; q0 < g && K < maxdet; q0 += 64) {
@@ -727,7 +756,7 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
         if (lane == 0) nstep = __popcll(keep);
       }
       __syncthreads();
-      const int Kq = nstep;
+      const int Kq = uni(nstep);
       K += Kq;
       for (int p = sc + q0 + 64 + tid; p < sc + g && Kq > 0; p += NMS_THREADS) {
         if ((struck[p >> 5] >> (p & 31)) & 1u) continue;
@@ -845,7 +874,8 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms_obb(const float* __restrict
   __shared__ unsigned queue[NMS_THREADS / 64][OBB_QUEUE];
   static_assert(NMS_CLASSES == NMS_THREADS, "one class bin per thread");
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: loops over waves stay scalar
   const int img = blockIdx.x;
   const float* cimg = cand + (size_t)img * A * 7;
   const float thr = prm->iou;
