@@ -324,6 +324,34 @@ def test_conv_first(tmp_path, cout):
     eng.close()
 
 
+@pytest.mark.parametrize("H,W,C,s,B,res", [(80, 80, 384, 1, 16, False), (41, 43, 256, 1, 16, True),
+                                            (81, 79, 128, 2, 32, False), (20, 21, 64, 1, 2, True),
+                                            (13, 11, 32, 2, 3, False)])
+def test_dwconv(tmp_path, H, W, C, s, B, res):
+    """Depthwise 3x3 (bias, SiLU, optional residual): the 4-pixels-per-thread kernel (large
+    launches: stride 1 and 2, widths not a multiple of 4) and the one-pixel kernel (small
+    launches) against the oracle on the first and last image of the batch."""
+    d = str(tmp_path / "dw")
+    modelgen.write_single_conv(d, H, W, C, C, 3, s, seed=C + s, dw=True, residual=res)
+    g = graphfile.load(d)
+    x = np.random.default_rng(C).standard_normal((B, H, W, C), dtype=np.float32).astype(np.float16)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    ops = [graphfile.Op(**vars(o)) for o in graphfile.fuse_adds(g.ops)]
+    assert eng.num_ops == len(ops) == 1
+    eng.write(0, x)
+    eng.run_op(0, B)
+    pick = [0, B - 1]
+    got = eng.read(ops[0].out, B)[pick].astype(np.float32)
+    ref = interp.Interp(g, len(pick))
+    ref.set_input(x[pick].astype(np.float32))
+    for op in ops:
+        ref.run_op(op)
+    rel = post.rel_err(got, ref.view(ops[0].out))
+    print(f"dwconv {H}x{W}x{C} s{s} b{B} res={res}: rel {rel:.2e}", flush=True)
+    assert rel <= TOL
+    eng.close()
+
+
 @pytest.mark.parametrize("ncls", [1, 12, 20, 80])
 def test_nms_paths_crafted_heads(models, ncls):
     """Decode + NMS on crafted head tensors that drive each NMS path: one class (over 2048

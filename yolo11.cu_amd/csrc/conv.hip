@@ -1011,10 +1011,93 @@ __global__ __launch_bounds__(256) void k_dwconv(View x, View y, View r, const f1
   *(f16x8*)(y.p + (size_t)m * y.s + y.o + c) = o;
 }
 
+// 3x3 depthwise, DWPX consecutive output pixels of one row per thread (8 channels): the
+// (DWPX-1)*CS + 3 input columns of each of the 3 rows are loaded once and shared by the
+// outputs that overlap them (18 instead of 36 tap loads per 4 outputs at stride 1), and the
+// 9 weight vectors and the bias once per DWPX outputs.  Taps outside the image read a
+// clamped address and are zeroed by a select, so every load of a row is in flight together.
+constexpr int DWPX = 4;
+template <int CS>   // stride 1 or 2
+__global__ __launch_bounds__(256) void k_dwconv3x4(View x, View y, View r, const f16* __restrict__ w,
+                                                      const float* __restrict__ bias, int cp, int act,
+                                                      int total) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int cg = y.C >> 3, xq = (y.W + DWPX - 1) / DWPX;
+  const int g = idx % cg;
+  int rest = idx / cg;
+  const int q = rest % xq;
+  rest /= xq;
+  const int oy = rest % y.H, img = rest / y.H;
+  const int c = g << 3, ox0 = q * DWPX;
+  constexpr int NCOL = (DWPX - 1) * CS + 3;
+  float a[DWPX][8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const float b = bias[c + j];
+#pragma unroll
+    for (int o = 0; o < DWPX; o++) a[o][j] = b;
+  }
+  const int ix0 = ox0 * CS - cp;
+  // one kernel row at a time: its NCOL input columns and 3 weight vectors are in flight
+  // together, and only one row's operands are live
+#pragma unroll 1
+  for (int ky = 0; ky < 3; ky++) {
+    f16x8 wv[3];
+#pragma unroll
+    for (int kx = 0; kx < 3; kx++) wv[kx] = *(const f16x8*)(w + (size_t)(ky * 3 + kx) * y.C + c);
+    const int iy = oy * CS - cp + ky;
+    const bool rowok = iy >= 0 && iy < x.H;
+    const size_t rowbase = ((size_t)(img * x.H + min(max(iy, 0), x.H - 1)) * x.W) * x.s + x.o + c;
+    f16x8 col[NCOL];
+    bool ok[NCOL];
+#pragma unroll
+    for (int i = 0; i < NCOL; i++) {
+      const int ix = ix0 + i;
+      ok[i] = rowok && ix >= 0 && ix < x.W;
+      col[i] = *(const f16x8*)(x.p + rowbase + (size_t)min(max(ix, 0), x.W - 1) * x.s);
+    }
+#pragma unroll
+    for (int o = 0; o < DWPX; o++)
+#pragma unroll
+      for (int kx = 0; kx < 3; kx++) {
+        const int i = o * CS + kx;
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[o][j] += ok[i] ? (float)col[i][j] * (float)wv[kx][j] : 0.f;
+      }
+  }
+  const int m0 = (img * y.H + oy) * y.W + ox0;
+#pragma unroll
+  for (int o = 0; o < DWPX; o++) {
+    if (ox0 + o >= y.W) break;
+    const int m = m0 + o;
+    f16x8 rv = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (r.p) rv = *(const f16x8*)(r.p + (size_t)m * r.s + r.o + c);
+    f16x8 out;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      float v = act == 1 ? silu(a[o][j]) : a[o][j];
+      if (r.p) v += (float)rv[j];
+      out[j] = (f16)v;
+    }
+    *(f16x8*)(y.p + (size_t)m * y.s + y.o + c) = out;
+  }
+}
+
 void launchDwConv(const View& x, const View& y, const View* res, const f16* wt_kkc,
                   const float* bias, int k, int s, int p, int act, int Bn, hipStream_t st) {
   const int total = Bn * y.H * y.W * (y.C / 8);
   View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
+  // the multi-pixel kernel once a launch has work for several waves of blocks on every CU
+  // (below that, one pixel per thread keeps more threads, which hides latency better)
+  if (k == 3 && (s == 1 || s == 2) && total >= 256 * 256 * 8) {
+    const int total4 = Bn * y.H * ((y.W + DWPX - 1) / DWPX) * (y.C / 8);
+    if (s == 1)
+      k_dwconv3x4<1><<<(total4 + 255) / 256, 256, 0, st>>>(x, y, r, wt_kkc, bias, p, act, total4);
+    else
+      k_dwconv3x4<2><<<(total4 + 255) / 256, 256, 0, st>>>(x, y, r, wt_kkc, bias, p, act, total4);
+    return;
+  }
   k_dwconv<<<(total + 255) / 256, 256, 0, st>>>(x, y, r, wt_kkc, bias, k, s, p, act, total);
 }
 
