@@ -644,20 +644,24 @@ struct Engine {
   void preprocessFrames(int Bn, const std::vector<std::pair<const uint8_t*, SlotGeom>>& frames,
                         const unsigned char* const* host, const int* hs, const int* ws) {
     const BufDesc& ib = g.bufs[g.tens[0].buf];
-    for (int s = 0; s < Bn; s++) {
-      const uint8_t* src = frames[s].first;
+    for (int s = 0; s < Bn; s++)
       if (host && host[s])
-        HCK(hipMemcpyAsync((void*)src, host[s], (size_t)hs[s] * ws[s] * 3, hipMemcpyHostToDevice, st));
-      f16* dst = bufp[g.tens[0].buf] + (size_t)s * ib.H * ib.W * 3;
-      if (g.cls) {
+        HCK(hipMemcpyAsync((void*)frames[s].first, host[s], (size_t)hs[s] * ws[s] * 3, hipMemcpyHostToDevice, st));
+    if (g.cls) {
+      for (int s = 0; s < Bn; s++) {
         const ClsGeom cg = clsGeom(ib.H, hs[s], ws[s]);
-        launchPreprocessCls(src, hs[s], ws[s], dst, ib.H, cg.rh, cg.rw, cg.top, cg.left, st);
-        continue;
+        launchPreprocessCls(frames[s].first, hs[s], ws[s], bufp[g.tens[0].buf] + (size_t)s * ib.H * ib.W * 3,
+                            ib.H, cg.rh, cg.rw, cg.top, cg.left, st);
       }
-      const SlotGeom& sg = frames[s].second;
-      int nh = (int)roundf(hs[s] * sg.scale), nw = (int)roundf(ws[s] * sg.scale);
-      launchPreprocess(src, hs[s], ws[s], dst, ib.H, ib.W, sg.scale, sg.top, sg.left, nh, nw, st);
+      return;
     }
+    std::vector<LetterboxSlot> slots(Bn);
+    for (int s = 0; s < Bn; s++) {
+      const SlotGeom& sg = frames[s].second;
+      slots[s] = LetterboxSlot{frames[s].first, hs[s], ws[s], sg.top, sg.left, (int)roundf(hs[s] * sg.scale),
+                               (int)roundf(ws[s] * sg.scale), s, sg.scale};
+    }
+    launchPreprocessBatch(slots.data(), Bn, bufp[g.tens[0].buf], ib.H, ib.W, st);
   }
 
   // Batch-Bn graph: [frame prologue] + network + post, by default one single-stream

@@ -144,6 +144,16 @@ void launchAttention(const View& qkv, const View& y, int heads, int kd, int hd, 
 // frame.hip
 void launchPreprocessCls(const uint8_t* src, int sh, int sw, f16* dst, int S, int rh, int rw, int top,
                          int left, hipStream_t st);
+// Letterbox of several frames in one launch (the frame graph's prologue): per-slot source,
+// geometry and destination image index, passed by value in chunks of LETTERBOX_BATCH.
+struct LetterboxSlot {
+  const uint8_t* src;
+  int sh, sw, top, left, nh, nw, index;
+  float scale;
+};
+constexpr int LETTERBOX_BATCH = 64;   // 64 x 40 bytes of kernel arguments
+struct LetterboxBatch { LetterboxSlot slot[LETTERBOX_BATCH]; };
+void launchPreprocessBatch(const LetterboxSlot* slots, int n, f16* dst, int dh, int dw, hipStream_t st);
 void launchPreprocess(const uint8_t* src, int sh, int sw, f16* dst, int dh, int dw, float scale,
                       int top, int left, int nh, int nw, hipStream_t st);
 // Decode appends each image's survivors as packed (score, anchor) keys to lists[img*A ..]

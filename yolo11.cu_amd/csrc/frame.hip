@@ -12,11 +12,11 @@ typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 // BGR u8 HWC (sh x sw) -> RGB fp16 NHWC (dh x dw), /255, pad 114, bilinear with the
 // half-pixel map src = (dst + 0.5)/scale - 0.5 and replicate-clamped edges
 // (k_preprocess, engine/engine.cu:966-998).  One thread per destination pixel.
-__global__ __launch_bounds__(256) void k_letterbox(const uint8_t* __restrict__ src, int sh, int sw,
-                                                   f16* __restrict__ dst, int dh, int dw, float scale,
-                                                   int top, int left, int nh, int nw) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= dh * dw) return;
+// One letterbox output pixel: bilinear sample of the scaled image, pad 114 outside it, BGR ->
+// RGB, /255.
+__device__ __forceinline__ void letterboxPixel(const uint8_t* __restrict__ src, int sh, int sw,
+                                               f16* __restrict__ dst, int dw, float scale, int top,
+                                               int left, int nh, int nw, int idx) {
   const int x = idx % dw, y = idx / dw;
   float r, g, b;
   if (y < top || y >= top + nh || x < left || x >= left + nw) {
@@ -45,9 +45,37 @@ __global__ __launch_bounds__(256) void k_letterbox(const uint8_t* __restrict__ s
   o[2] = (f16)(b / 255.f);
 }
 
+__global__ __launch_bounds__(256) void k_letterbox(const uint8_t* __restrict__ src, int sh, int sw,
+                                                   f16* __restrict__ dst, int dh, int dw, float scale,
+                                                   int top, int left, int nh, int nw) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= dh * dw) return;
+  letterboxPixel(src, sh, sw, dst, dw, scale, top, left, nh, nw, idx);
+}
+
+// All frames of a batch in one launch (blockIdx.y = slot within the chunk); each slot has its
+// own source and geometry, and writes its image of the dh x dw x 3 input batch.
+__global__ __launch_bounds__(256) void k_letterbox_batch(LetterboxBatch lb, f16* __restrict__ dst, int dh,
+                                                         int dw) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= dh * dw) return;
+  const LetterboxSlot& s = lb.slot[blockIdx.y];
+  letterboxPixel(s.src, s.sh, s.sw, dst + (size_t)s.index * dh * dw * 3, dw, s.scale, s.top, s.left, s.nh,
+                 s.nw, idx);
+}
+
 void launchPreprocess(const uint8_t* src, int sh, int sw, f16* dst, int dh, int dw, float scale,
                       int top, int left, int nh, int nw, hipStream_t st) {
   k_letterbox<<<(dh * dw + 255) / 256, 256, 0, st>>>(src, sh, sw, dst, dh, dw, scale, top, left, nh, nw);
+}
+
+void launchPreprocessBatch(const LetterboxSlot* slots, int n, f16* dst, int dh, int dw, hipStream_t st) {
+  for (int s0 = 0; s0 < n; s0 += LETTERBOX_BATCH) {
+    LetterboxBatch lb;
+    const int k = n - s0 < LETTERBOX_BATCH ? n - s0 : LETTERBOX_BATCH;
+    for (int i = 0; i < k; i++) lb.slot[i] = slots[s0 + i];
+    k_letterbox_batch<<<dim3((dh * dw + 255) / 256, k), 256, 0, st>>>(lb, dst, dh, dw);
+  }
 }
 
 // ------------------------------------------------------------------ classify preprocess
