@@ -301,12 +301,13 @@ def test_conv_tail_split(tmp_path):
     eng.close()
 
 
+@pytest.mark.parametrize("HW", [(37, 48), (37, 45)])
 @pytest.mark.parametrize("cout", [16, 32, 48, 96, 160, 256, 24])
-def test_conv_first(tmp_path, cout):
-    """The stem conv (Cin 3, 3x3 s2): the MFMA kernel (Cout % 16 == 0, paired 16-byte stores
-    when Cout % 32 == 0) and the direct kernel (Cout 24) against the oracle, with ragged
-    image edges and a batch."""
-    H, W, B = 37, 45, 2
+def test_conv_first(tmp_path, cout, HW):
+    """The stem conv (Cin 3, 3x3 s2): the MFMA kernel (Cout % 16 == 0 and input rows of whole
+    16-byte vectors, W % 8 == 0; paired 16-byte stores when Cout % 32 == 0) and the direct
+    kernel (Cout 24, or W = 45) against the oracle, with ragged image edges and a batch."""
+    (H, W), B = HW, 2
     d = str(tmp_path / "stem")
     modelgen.write_single_conv(d, H, W, 3, cout, 3, 2, seed=cout)
     g = graphfile.load(d)

@@ -107,7 +107,9 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+// x * sigmoid(x) with the hardware reciprocal (1 ulp) instead of an IEEE divide: the result
+// is rounded to fp16 next, and the divide's fix-up sequence is most of the epilogue's VALU.
+__device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
 template <int BM, int BN, int WM, int WN, int BK, int NS, int KM>
 __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
@@ -805,6 +807,10 @@ constexpr int FIRST_TP = 128;                        // output columns per block
 constexpr int FIRST_RB = 4;                          // output rows per block
 constexpr int FIRST_COLS = (FIRST_TP - 1) * 2 + 3;   // input columns (stride <= 2)
 constexpr int FIRST_ROWS = (FIRST_RB - 1) * 2 + 3;   // input rows (stride <= 2)
+// a window row is staged as 16-byte vectors from the 8-element boundary at or below its
+// first element: up to 7 leading elements, so FIRST_NV vectors per row
+constexpr int FIRST_NV = (7 + FIRST_COLS * 3 + 7) / 8;
+constexpr int FIRST_PITCH = FIRST_NV * 8;            // LDS row pitch (elements)
 
 template <bool PAIR>
 __global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f16* __restrict__ w,
@@ -812,7 +818,7 @@ __global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f
                                                          int cp, int act, int ncb) {
   constexpr int NF = 8;   // 16-channel fragments per block (128 channels)
   constexpr int OPITCH = 16 * NF + 8;
-  __shared__ f16 tile[FIRST_ROWS][FIRST_COLS * 3];
+  __shared__ __attribute__((aligned(16))) f16 tile[FIRST_ROWS][FIRST_PITCH];
   __shared__ f16 sw[16 * NF * 27];
   __shared__ float sb[16 * NF];
   __shared__ __attribute__((aligned(16))) f16 ostage[4][16 * OPITCH];
@@ -821,27 +827,38 @@ __global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f
   const int ox0 = blockIdx.x * FIRST_TP, oy0 = blockIdx.y * FIRST_RB;
   const int img = blockIdx.z / ncb, cb = (blockIdx.z - img * ncb) * 16 * NF;
   const int nf = min(NF, (y.C - cb) / 16);
-  const int cols = (FIRST_TP - 1) * cs + 3, rows = (FIRST_RB - 1) * cs + 3;
+  const int rows = (FIRST_RB - 1) * cs + 3;
   const int ix0 = ox0 * cs - cp, iy0 = oy0 * cs - cp;
 
   // ---- stage input window, weights, biases: every global load is issued before the first
   //      LDS store (fully unrolled, bounds as predicates), so the block waits for one
-  //      memory round trip instead of one per window row
+  //      memory round trip instead of one per window row.  The window rows are read as
+  //      16-byte vectors: element e of a row (e = 3 * column + channel, from the image's
+  //      column 0) lands at tile offset e - e0, e0 = the 8-aligned element at or below the
+  //      window's first element ix0 * 3; vectors wholly inside the row are one load, the
+  //      (at most two) vectors at the image edges are assembled element by element.
   const f16* xb = x.p + (size_t)img * x.H * x.W * x.s + x.o;
-  constexpr int QIT = (FIRST_COLS * 3 + 255) / 256;
-  f16 xv[FIRST_ROWS][QIT];
+  const int rowlen = x.W * 3;
+  const int e0 = ((ix0 * 3) >> 3) << 3;                // floor to a multiple of 8 (ix0 may be < 0)
+  const int shift = ix0 * 3 - e0;                      // 0 .. 7
+  constexpr int VIT = (FIRST_ROWS * FIRST_NV + 255) / 256;
+  f16x8 xv[VIT];
 #pragma unroll
-  for (int r = 0; r < FIRST_ROWS; r++) {
-    const int iy = iy0 + r;
+  for (int u = 0; u < VIT; u++) {
+    const int t = threadIdx.x + 256 * u;
+    const int r = t / FIRST_NV, v = t - r * FIRST_NV;
+    const int iy = iy0 + r, e = e0 + 8 * v;
     const bool rowin = r < rows && iy >= 0 && iy < x.H;
-    const f16* xrow = xb + (size_t)(rowin ? iy : 0) * x.W * x.s;
+    const f16* xrow = xb + (size_t)(rowin ? iy : 0) * x.W * 3;
+    f16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (rowin && e >= 0 && e + 8 <= rowlen) {
+      val = *(const f16x8*)(xrow + e);
+    } else if (rowin) {
 #pragma unroll
-    for (int u = 0; u < QIT; u++) {
-      const int q = threadIdx.x + 256 * u;
-      const int c = q / 3, ci = q - 3 * c;   // constant divisor: a multiply-high
-      const int ix = ix0 + c;
-      xv[r][u] = (rowin && q < cols * 3 && ix >= 0 && ix < x.W) ? xrow[ix * x.s + ci] : (f16)0.f;
+      for (int j = 0; j < 8; j++)
+        if (e + j >= 0 && e + j < rowlen) val[j] = xrow[e + j];
     }
+    xv[u] = val;
   }
   constexpr int WIT = (16 * NF * 27 + 255) / 256;
   f16 wv[WIT];
@@ -852,12 +869,11 @@ __global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f
   }
   const float bv = (int)threadIdx.x < nf * 16 ? bias[cb + threadIdx.x] : 0.f;
 #pragma unroll
-  for (int r = 0; r < FIRST_ROWS; r++)
-#pragma unroll
-    for (int u = 0; u < QIT; u++) {
-      const int q = threadIdx.x + 256 * u;
-      if (r < rows && q < cols * 3) tile[r][q] = xv[r][u];
-    }
+  for (int u = 0; u < VIT; u++) {
+    const int t = threadIdx.x + 256 * u;
+    const int r = t / FIRST_NV, v = t - r * FIRST_NV;
+    if (r < FIRST_ROWS) *(f16x8*)&tile[r][8 * v] = xv[u];
+  }
 #pragma unroll
   for (int u = 0; u < WIT; u++) {
     const int e = threadIdx.x + 256 * u;
@@ -872,7 +888,7 @@ __global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f
   for (int j = 0; j < 8; j++) {
     const int k = 8 * lg + j, t = k / 3, ci = k - 3 * t;
     tok[j] = k < 27;
-    toff[j] = tok[j] ? (t / 3) * (FIRST_COLS * 3) + (t % 3) * 3 + ci : 0;
+    toff[j] = tok[j] ? (t / 3) * FIRST_PITCH + (t % 3) * 3 + ci + shift : 0;
   }
   f16x8 fw[NF];
   float bb[NF][4];
@@ -906,7 +922,7 @@ __global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f
       const int p = pbase + lr;
       f16x8 fb;
 #pragma unroll
-      for (int j = 0; j < 8; j++) fb[j] = tok[j] ? tflat[rr * cs * (FIRST_COLS * 3) + toff[j] + 3 * cs * p] : (f16)0.f;
+      for (int j = 0; j < 8; j++) fb[j] = tok[j] ? tflat[rr * cs * FIRST_PITCH + toff[j] + 3 * cs * p] : (f16)0.f;
 #pragma unroll
       for (int f = 0; f < NF; f++) {
         if (f >= nf) break;
@@ -938,7 +954,9 @@ __global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f
 void launchConvFirst(const View& x, const View& y, const f16* w, const float* bias, int s, int p,
                      int act, int Bn, hipStream_t st) {
   const int M = Bn * y.H * y.W;
-  if (y.C % 16 == 0 && s >= 1 && s <= 2) {
+  // the MFMA form stages input rows as 16-byte vectors: a dense 3-channel input whose rows
+  // are 16-byte multiples
+  if (y.C % 16 == 0 && s >= 1 && s <= 2 && x.s == 3 && x.o == 0 && (x.W * 3) % 8 == 0) {
     const int ncb = (y.C + 127) / 128;
     dim3 grid((y.W + FIRST_TP - 1) / FIRST_TP, (y.H + FIRST_RB - 1) / FIRST_RB, Bn * ncb);
     if (y.C % 32 == 0)
