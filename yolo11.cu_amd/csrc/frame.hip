@@ -740,13 +740,23 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
         bool live = pp < sc + g && !((struck[pp >> 5] >> (pp & 31)) & 1u);
         const float4 bq = live ? cbox[pp] : make_float4(0.f, 0.f, 0.f, 0.f);
         bool hit = false;
-        for (unsigned long long kk = keep; kk && __ballot(live && !hit); kk &= kk - 1ull) {
-          const int t = __builtin_ctzll(kk);
-          const float4 bi = make_float4(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.x), t)),
-                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.y), t)),
-                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.z), t)),
-                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.w), t)));
-          if (live && !hit && suppresses(bi, bq, thr)) hit = true;
+        // up to 4 survivors per round (independent tests; a member is struck when any
+        // survivor of the chunk suppresses it, whatever the order)
+        for (unsigned long long kk = keep; kk && __ballot(live && !hit);) {
+          bool h = false;
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            if (kk) {
+              const int t = __builtin_ctzll(kk);
+              kk &= kk - 1ull;
+              const float4 bi = make_float4(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.x), t)),
+                                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.y), t)),
+                                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.z), t)),
+                                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.w), t)));
+              h |= suppresses(bi, bq, thr);
+            }
+          }
+          if (live && h) hit = true;
         }
         if (hit) atomicOr(&struck[pp >> 5], 1u << (pp & 31));
       }
@@ -789,8 +799,14 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
       for (int p = sc + q0 + 64 + tid; p < sc + g && Kq > 0; p += NMS_THREADS) {
         if ((struck[p >> 5] >> (p & 31)) & 1u) continue;
         const float4 bp = cbox[p];
-        for (int k = 0; k < Kq; k++) {
-          if (suppresses(stepBox[k], bp, thr)) {
+        for (int k = 0; k < Kq; k += 4) {   // 4 survivor boxes per round, requested together
+          float4 sb[4];
+#pragma unroll
+          for (int u = 0; u < 4; u++) sb[u] = stepBox[min(k + u, Kq - 1)];
+          bool h = false;
+#pragma unroll
+          for (int u = 0; u < 4; u++) h |= k + u < Kq && suppresses(sb[u], bp, thr);
+          if (h) {
             atomicOr(&struck[p >> 5], 1u << (p & 31));
             break;
           }
