@@ -353,6 +353,46 @@ def test_dwconv(tmp_path, H, W, C, s, B, res):
     eng.close()
 
 
+@pytest.mark.parametrize("H,W,Cin,Cout,B,res", [(160, 160, 48, 48, 2, False), (37, 45, 32, 32, 3, True),
+                                                (20, 21, 64, 64, 2, True), (8, 8, 8, 16, 1, False),
+                                                (33, 17, 24, 48, 2, False), (40, 40, 64, 16, 2, False)])
+def test_conv_halo(tmp_path, H, W, Cin, Cout, B, res):
+    """The LDS-halo 3x3 kernel (op config CFG_HALO): ragged 4x16 output tiles, channel counts
+    from 8 to 64 (one or two 32-channel chunks, 1-4 output fragments), bias + SiLU and the
+    fused residual, against the oracle."""
+    d = str(tmp_path / "halo")
+    modelgen.write_single_conv(d, H, W, Cin, Cout, 3, 1, seed=Cin + Cout, residual=res)
+    g = graphfile.load(d)
+    x = np.random.default_rng(Cin).standard_normal((B, H, W, Cin), dtype=np.float32).astype(np.float16)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    ops = [graphfile.Op(**vars(o)) for o in graphfile.fuse_adds(g.ops)]
+    assert eng.num_ops == len(ops) == 1
+    eng.set_op_config(0, yolort.CFG_HALO)
+    assert eng.op_config(0) == yolort.CFG_HALO
+    eng.write(0, x)
+    eng.run_op(0, B)
+    got = eng.read(ops[0].out, B).astype(np.float32)
+    ref = interp.Interp(g, B)
+    ref.set_input(x.astype(np.float32))
+    ref.run_op(ops[0])
+    rel = post.rel_err(got, ref.view(ops[0].out))
+    print(f"halo {H}x{W} {Cin}->{Cout} b{B} res={res}: rel {rel:.2e}", flush=True)
+    assert rel <= TOL
+    eng.close()
+
+
+def test_conv_halo_rejects(tmp_path):
+    """The halo config is refused where the kernel does not apply (stride 2, 1x1, over 64
+    channels, Cout not a multiple of 16)."""
+    for i, (cin, cout, k, s) in enumerate([(32, 32, 3, 2), (32, 32, 1, 1), (96, 32, 3, 1), (32, 24, 3, 1)]):
+        d = str(tmp_path / f"r{i}")
+        modelgen.write_single_conv(d, 16, 16, cin, cout, k, s, seed=1)
+        eng = yolort.Engine(d, 1, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+        with pytest.raises(ValueError):
+            eng.set_op_config(0, yolort.CFG_HALO)
+        eng.close()
+
+
 @pytest.mark.parametrize("ncls", [1, 12, 20, 80])
 def test_nms_paths_crafted_heads(models, ncls):
     """Decode + NMS on crafted head tensors that drive each NMS path: one class (over 2048

@@ -968,6 +968,156 @@ void launchConvFirst(const View& x, const View& y, const f16* w, const float* bi
   }
 }
 
+// ------------------------------------------------------------------ 3x3 halo conv
+// Stride-1 3x3 convs with few channels (Cin <= 64, Cout <= 64).  The GEMM re-fetches each
+// input pixel for all 9 taps through small tiles (~36 bytes into LDS per output at 48
+// channels); here a persistent block (one per CU) keeps all 9 taps' weights in LDS and, per
+// 4 x 16-pixel output tile, stages the 6 x 18-pixel input halo once and serves every tap
+// from it.  The next tile's halo is fetched into registers while the current one computes.
+// Wave w computes output row w of the tile: lane (lr, lg) builds the pixel fragment of column
+// lr (input channels 8lg..8lg+7 of a 32-channel chunk) and the weight fragments of output
+// channels f*16 + lr, as in the GEMM (MFMA 16x16x32, fp32 accumulate).  Padded channel
+// pitch (32*KC + 8) keeps the 16 lanes of a fragment off each other's LDS banks.
+constexpr int HALO_TH = 4, HALO_TW = 16;
+constexpr int HALO_HH = HALO_TH + 2, HALO_HW = HALO_TW + 2;
+
+template <int KC, int FN>   // KC: 32-channel input chunks (Cin <= 32*KC); FN: 16-channel output fragments
+__global__ __launch_bounds__(256) void k_conv3x3_halo(View x, View y, View r, const f16* __restrict__ w,
+                                                      const float* __restrict__ bias, int act, int Bn,
+                                                      int tilesX, int tilesY) {
+  constexpr int CP = 32 * KC + 8;             // channel pitch of halo pixels and weight rows
+  constexpr int NO = 16 * FN;
+  constexpr int VPP = 4 * KC;                 // 8-channel vectors per staged pixel
+  constexpr int HV = HALO_HH * HALO_HW * VPP;
+  constexpr int HIT = (HV + 255) / 256;
+  __shared__ __attribute__((aligned(16))) f16 wl[9 * NO * CP];
+  __shared__ __attribute__((aligned(16))) f16 hl[HALO_HH * HALO_HW * CP];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int Cin = x.C, Cout = y.C;
+
+  // weights OHWI [Cout][3][3][Cin] -> wl[tap][o][c], zero past Cin / Cout
+  for (int e = t; e < 9 * NO * VPP; e += 256) {
+    const int v = e % VPP, rest = e / VPP, o = rest % NO, tap = rest / NO;
+    const int c0 = 8 * v;
+    f16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (o < Cout && c0 < Cin) val = *(const f16x8*)(w + ((size_t)o * 9 + tap) * Cin + c0);
+    *(f16x8*)&wl[(tap * NO + o) * CP + c0] = val;
+  }
+  float bb[FN][4];
+#pragma unroll
+  for (int f = 0; f < FN; f++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int c = f * 16 + 4 * lg + e;
+      bb[f][e] = c < Cout ? bias[c] : 0.f;
+    }
+
+  const int perImg = tilesX * tilesY, ntiles = Bn * perImg;
+  f16x8 pre[HIT];
+  auto fetch = [&](int tile) {                // global -> registers (zeros outside the image)
+    const bool live = tile < ntiles;
+    const int img = live ? tile / perImg : 0, rem = live ? tile - img * perImg : 0;
+    const int ty = rem / tilesX, tx = rem - ty * tilesX;
+    const int y0 = ty * HALO_TH - 1, x0 = tx * HALO_TW - 1;
+#pragma unroll
+    for (int u = 0; u < HIT; u++) {
+      const int e = t + 256 * u;
+      const int v = e % VPP, pix = e / VPP;
+      const int hy = pix / HALO_HW, hx = pix - hy * HALO_HW;
+      const int iy = y0 + hy, ix = x0 + hx, c0 = 8 * v;
+      f16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (live && e < HV && iy >= 0 && iy < x.H && ix >= 0 && ix < x.W && c0 < Cin)
+        val = *(const f16x8*)(x.p + ((size_t)(img * x.H + iy) * x.W + ix) * x.s + x.o + c0);
+      pre[u] = val;
+    }
+  };
+
+  int tile = blockIdx.x;
+  fetch(tile);
+  for (; tile < ntiles; tile += gridDim.x) {
+    __syncthreads();                          // every wave is done with the previous halo
+#pragma unroll
+    for (int u = 0; u < HIT; u++) {
+      const int e = t + 256 * u;
+      if (e < HV) *(f16x8*)&hl[(e / VPP) * CP + 8 * (e % VPP)] = pre[u];
+    }
+    __syncthreads();
+    fetch(tile + gridDim.x);                  // next halo in flight while this tile computes
+
+    f32x4 acc[FN];
+#pragma unroll
+    for (int f = 0; f < FN; f++) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tap = 0; tap < 9; tap++) {
+      const int ky = tap / 3, kx = tap - 3 * ky;
+#pragma unroll
+      for (int kc = 0; kc < KC; kc++) {
+        const f16x8 pf = *(const f16x8*)&hl[((wave + ky) * HALO_HW + lr + kx) * CP + kc * 32 + 8 * lg];
+#pragma unroll
+        for (int f = 0; f < FN; f++) {
+          const f16x8 wf = *(const f16x8*)&wl[(tap * NO + f * 16 + lr) * CP + kc * 32 + 8 * lg];
+          acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, pf, acc[f], 0, 0, 0);
+        }
+      }
+    }
+
+    // lane holds output channels f*16 + 4lg .. +3 of pixel (row wave, column lr) of the tile
+    const int img = tile / perImg, rem = tile - img * perImg;
+    const int ty = rem / tilesX, tx = rem - ty * tilesX;
+    const int oy = ty * HALO_TH + wave, ox = tx * HALO_TW + lr;
+    if (oy < y.H && ox < y.W) {
+      const size_t m = (size_t)(img * y.H + oy) * y.W + ox;
+#pragma unroll
+      for (int f = 0; f < FN; f++) {
+        const int c = f * 16 + 4 * lg;
+        if (c >= Cout) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          v[e] = acc[f][e] + bb[f][e];
+          if (act == 1) v[e] = silu(v[e]);
+        }
+        if (r.p) {
+          const f16x4 rv = *(const f16x4*)(r.p + m * r.s + r.o + c);
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[e] += (float)rv[e];
+        }
+        const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+        *(f16x4*)(y.p + m * y.s + y.o + c) = o;
+      }
+    }
+  }
+}
+
+bool convHaloOk(const View& x, const View& y, const View* r, int k, int s, int p) {
+  return k == 3 && s == 1 && p == 1 && x.H == y.H && x.W == y.W && x.C >= 8 && x.C <= 64 && x.C % 8 == 0 &&
+         y.C >= 16 && y.C <= 64 && y.C % 16 == 0 && x.s % 8 == 0 && x.o % 8 == 0 && y.s % 4 == 0 &&
+         y.o % 4 == 0 && (!r || (r->s % 4 == 0 && r->o % 4 == 0));
+}
+
+void launchConvHalo(const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
+                    int Bn, hipStream_t st) {
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 256;
+    return n;
+  }();
+  const View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
+  const int tilesX = (y.W + HALO_TW - 1) / HALO_TW, tilesY = (y.H + HALO_TH - 1) / HALO_TH;
+  const int ntiles = Bn * tilesX * tilesY;
+  const int grid = ntiles < 2 * cus ? ntiles : 2 * cus;   // persistent: about two blocks per CU
+  const int kc = x.C <= 32 ? 1 : 2, fn = y.C / 16;
+#define HALO_CASE(KC, FN) \
+  if (kc == KC && fn == FN) { k_conv3x3_halo<KC, FN><<<grid, 256, 0, st>>>(x, y, r, w, bias, act, Bn, tilesX, tilesY); return; }
+  HALO_CASE(1, 1) HALO_CASE(1, 2) HALO_CASE(1, 3) HALO_CASE(1, 4)
+  HALO_CASE(2, 1) HALO_CASE(2, 2) HALO_CASE(2, 3) HALO_CASE(2, 4)
+#undef HALO_CASE
+}
+
 // ------------------------------------------------------------------ depthwise conv
 // One thread per (pixel, 8-channel group); weights were repacked on the host from
 // [C][k][k] to [k*k][C] so each tap is one 16-byte load (the reference does the same

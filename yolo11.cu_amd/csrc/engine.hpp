@@ -117,6 +117,12 @@ size_t splitWorkspaceBytes(int cfg, int km, int M, int N, int splits);
 void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
                     const float* bias, int k, int s, int p, int act, int Bn, int splits,
                     float* ws, int* cnt, hipStream_t st);
+// 3x3 stride-1 convs with Cin <= 64 and Cout <= 64 (Cout % 16 == 0): the LDS-halo kernel, an
+// autotune candidate selected by the op config CFG_HALO.
+constexpr int CFG_HALO = 1000;
+bool convHaloOk(const View& x, const View& y, const View* r, int k, int s, int p);
+void launchConvHalo(const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
+                    int Bn, hipStream_t st);
 void launchConvFirst(const View& x, const View& y, const f16* w, const float* bias, int s, int p,
                      int act, int Bn, hipStream_t st);
 void launchDwConv(const View& x, const View& y, const View* res, const f16* wt_kkc,
