@@ -98,9 +98,10 @@ def test_yolo11n_seg_ops_resync(models):
 @pytest.mark.parametrize("B", [1, 32])
 @pytest.mark.parametrize("shape", [
     (80, 80, 256, 256, 3, 1), (80, 80, 256, 512, 3, 2), (40, 40, 512, 256, 1, 1),
-    (20, 20, 512, 512, 3, 1), (20, 20, 1024, 512, 1, 1)])
+    (20, 20, 512, 512, 3, 1), (20, 20, 1024, 512, 1, 1), (40, 40, 96, 192, 3, 1)])
 def test_conv_sweep(tmp_path, shape, B):
-    """Config 1: the isolated conv sweep, bias + SiLU epilogue, every tile config."""
+    """Config 1: the isolated conv sweep, bias + SiLU epilogue, every tile config; the last
+    shape is N = 192 exactly with Cin not a multiple of 64 (tap-straddling K stages)."""
     H, W, cin, cout, k, s = shape
     d = str(tmp_path / "conv")
     modelgen.write_single_conv(d, H, W, cin, cout, k, s, seed=7)

@@ -574,7 +574,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   X(28, 32, 32, 2, 2, 128, 4)         \
   X(29, 64, 16, 4, 1, 128, 5)         \
   X(30, 256, 256, 4, 4, 32, 3)        \
-  X(31, 256, 256, 4, 4, 64, 2)
+  X(31, 256, 256, 4, 4, 64, 2)       \
+  X(32, 128, 192, 2, 2, 32, 3)
 
 static const TileCfg kTiles[] = {
 #define X(i, bm, bn, wm, wn, bk, ns) {bm, bn, wm, wn, bk, ns},
