@@ -3,11 +3,12 @@
 
 Workloads (BASELINE.json metric "e2e ms/frame & FPS @640 fp16 (yolo11n b1, yolo11x b16);
 conv MFMA util %"):
-  * primary (value): yolo11n detect, batch 1, 810x1080 synthetic BGR frame already in HBM;
-    one step = one launch of the whole-frame graph (letterbox + net + DFL decode + NMS +
-    D2H of the results into pinned memory) + wait + host fetch of the detections, the
-    loop of the reference's `pipeline` mode (engine/engine.cu:2020-2031) minus the PCIe
-    upload (the PCIe-inclusive figure is reported separately).
+  * primary (value): yolo11n detect, batch 1, 810x1080 synthetic BGR frame in pinned host
+    memory; one step = one launch of the whole-frame graph (H2D of the raw frame +
+    letterbox + net + DFL decode + NMS + D2H of the results into pinned memory) + wait +
+    host fetch of the detections: the loop of the reference's `pipeline` mode
+    (engine/engine.cu:1992-2031).  The same loop with the frame already in HBM is a side
+    figure.
   * yolo11x detect, batch 16, sixteen 640x640 frames in HBM: whole-frame graph
     throughput, and conv MFMA utilisation = sum(conv FLOPs) / (sum(conv time) * peak)
     from per-op hipEvent timing.
@@ -15,14 +16,16 @@ conv MFMA util %"):
     3x3 s1 256->256 @80x80, batch 32, timed with hipEvents on the
     engine stream; `traffic` = HBM bytes per launch of the tile the autotuner picked, from
     the committed per-tile PMC passes (profiles/conv_gemm_c1_traffic.json).
+  * prepost_roofline: letterbox, decode and mask assembly against the HBM roofline, NMS time.
   * yolo11n-obb at 1024 (15 classes, 1024x1024 frame) and yolo11n-seg at 640, batch 1:
     whole-frame graph, frame in HBM (side figures; the reference quotes 1.6 ms and 1.21 ms
     on an RTX 3060 Ti, README.md:80-81).
-  * yolo11m detect b1 with a 1080x1920 frame at IoU 0.7, the five
-    isolated conv shapes at batch 1 and 32 (config 1), and yolo11n-cls at 224 (whole-frame
-    graph with the classify preprocess): side figures.
-  * cpu_baseline: the numpy fp32 per-op oracle (letterbox + every op + decode + NMS) for
-    yolo11n batch 1 on this host's cores, bounded to ~15 s.
+  * yolo11m detect b1 with a 1080x1920 frame at IoU 0.7 (H2D included),
+    the five isolated conv shapes at batch 1 and 32 (config 1), and yolo11n-cls at 224
+    (whole-frame graph with the classify preprocess): side figures.
+  * cpu_baseline: the reference's CPU path, a torch fp32 per-op interpreter of the graph
+    plus CPU letterbox/decode/NMS (oracle/torchref.py), for yolo11n batch 1 on this host's
+    cores, in a separate process, bounded to ~15 s.
 
 Weights are seeded random-init (no checkpoints offline); data are synthetic frames.
 """
@@ -66,6 +69,11 @@ def conv_flops(eng, k):
 
 
 def bench_n(workdir, steps, warmup, graph=True):
+    """yolo11n b1.  The headline step is the reference's `pipeline` loop
+    (engine/engine.cu:1992-2031): one whole-frame graph holding the H2D of the raw 810x1080
+    frame from pinned host memory, letterbox, network, decode, NMS and the result copy, then
+    a wait and the host fetch of the detections.  The same loop with the frame already in
+    HBM, the graph alone (hipEvents), and the pre/post stages are side figures."""
     import modelgen
     import yolort
     d = os.path.join(workdir, "yolo11n")
@@ -82,34 +90,35 @@ def bench_n(workdir, steps, warmup, graph=True):
         dev.free()
         eng.close()
         return None
+
+    def loop():
+        for _ in range(warmup):
+            eng.frame_run()
+            eng.get(0)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            eng.frame_run()
+            dets = eng.get(0)
+        return (time.perf_counter() - t0) * 1e3 / steps, dets
+
+    # frame already in HBM
     eng.frame_graph([dev.ptr], [810], [1080])
-    for _ in range(warmup):
-        eng.frame_run()
-        eng.get(0)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        eng.frame_run()
-        dets = eng.get(0)
-    ms = (time.perf_counter() - t0) * 1e3 / steps
-    graph_ms = eng.time_graph(1, 1, max(steps, 50))
-    kept, raw = len(dets), eng.raw_count(0)
-    # PCIe-inclusive variant: the raw frame is uploaded from pinned memory inside the graph
+    ms_hbm, _ = loop()
+    graph_ms_hbm = eng.time_graph(1, 1, max(steps, 50))
+    stages = eng.profile_stages(50)
+    # headline: the raw frame is uploaded from pinned memory inside the graph
     pin = yolort.PinnedBuffer(img.shape)
     pin.array[...] = img
     eng.frame_graph([dev.ptr], [810], [1080], [pin.ptr])
-    for _ in range(warmup):
-        eng.frame_run()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        eng.frame_run()
-        eng.get(0)
-    ms_pcie = (time.perf_counter() - t0) * 1e3 / steps
+    ms, dets = loop()
+    graph_ms = eng.time_graph(1, 1, max(steps, 50))
+    kept, raw = len(dets), eng.raw_count(0)
     per_op = eng.profile_ops(1, 20)
     pin.free()
     dev.free()
     eng.close()
-    return dict(ms=ms, graph_ms=graph_ms, ms_pcie=ms_pcie, kept=kept, raw=raw,
-                stream_ops_ms=float(per_op.sum()))
+    return dict(ms=ms, graph_ms=graph_ms, ms_hbm=ms_hbm, graph_ms_hbm=graph_ms_hbm, kept=kept, raw=raw,
+                stream_ops_ms=float(per_op.sum()), stages=stages, frame=(810, 1080), A=8400, ncpad=80)
 
 
 def bench_task(workdir, task, imgsz, nc, cls_bias, frame, steps, warmup, graph=True):
@@ -143,9 +152,10 @@ def bench_task(workdir, task, imgsz, nc, cls_bias, frame, steps, warmup, graph=T
     ms = (time.perf_counter() - t0) * 1e3 / steps
     graph_ms = eng.time_graph(1, 1, max(steps, 50))
     kept, raw = len(dets), eng.raw_count(0)
+    stages = eng.profile_stages(50)
     dev.free()
     eng.close()
-    return dict(ms=ms, graph_ms=graph_ms, kept=kept, raw=raw)
+    return dict(ms=ms, graph_ms=graph_ms, kept=kept, raw=raw, stages=stages)
 
 
 def bench_m(workdir, steps, warmup, graph=True):
@@ -168,20 +178,28 @@ def bench_m(workdir, steps, warmup, graph=True):
         dev.free()
         eng.close()
         return None
+    def loop():
+        for _ in range(warmup):
+            eng.frame_run()
+            eng.get(0)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            eng.frame_run()
+            dets = eng.get(0)
+        return (time.perf_counter() - t0) * 1e3 / steps, dets
+
     eng.frame_graph([dev.ptr], [1080], [1920])
-    for _ in range(warmup):
-        eng.frame_run()
-        eng.get(0)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        eng.frame_run()
-        dets = eng.get(0)
-    ms = (time.perf_counter() - t0) * 1e3 / steps
+    ms_hbm, _ = loop()
+    pin = yolort.PinnedBuffer(img.shape)
+    pin.array[...] = img
+    eng.frame_graph([dev.ptr], [1080], [1920], [pin.ptr])
+    ms, dets = loop()
     graph_ms = eng.time_graph(1, 1, max(steps, 50))
     kept, raw = len(dets), eng.raw_count(0)
+    pin.free()
     dev.free()
     eng.close()
-    return dict(ms=ms, graph_ms=graph_ms, kept=kept, raw=raw)
+    return dict(ms=ms, graph_ms=graph_ms, ms_hbm=ms_hbm, kept=kept, raw=raw)
 
 
 def bench_cls(workdir, steps, warmup, graph=True):
@@ -371,38 +389,54 @@ def bench_serve(workdir, seconds=4.0, procs=4, callers=16):
 
 
 def cpu_baseline(budget_s=15.0):
-    import numpy as np
-    import modelgen
-    from oracle import graphfile, interp, post
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        cores = os.cpu_count()
-    with tempfile.TemporaryDirectory() as d:
-        modelgen.write_model(d, "yolo11", "n", cls_bias=-8.0)
-        g = graphfile.load(d)
-        img = modelgen.synth_frame(810, 1080, 20, 1)
+    """The reference's CPU path -- a torch fp32 per-op interpreter of the graph
+    (export/export.py:446-526, restated in oracle/torchref.py) plus the CPU letterbox,
+    decode and NMS -- timed on the yolo11n batch-1 frame of config 0, in a separate
+    process that never loads the GPU library, with every core this process may use."""
+    import subprocess
+    script = os.path.join(ROOT, "oracle", "torchref.py")
+    r = subprocess.run([sys.executable, script, "--seconds", str(budget_s)], capture_output=True,
+                       text=True, timeout=budget_s + 300)
+    if r.returncode != 0:
+        raise RuntimeError(f"cpu baseline failed ({r.returncode}): {r.stderr[-2000:]}")
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    return dict(value=round(1e3 / res["ms"], 3), unit="frames/s", cores=int(res["threads"]), kind="port",
+                impl="torch fp32 per-op interpreter (export/export.py:446-526) + numpy letterbox/decode/NMS",
+                host_cpu_count=res["cpu_count"], affinity_cpus=res["affinity"],
+                sample=f"yolo11n b1 810x1080 frame, letterbox + 112 ops + decode + NMS on the CPU; median of "
+                       f"{res['frames']} frames = {res['ms']:.1f} ms/frame ({res['threads']} torch threads)")
 
-        def frame():
-            x = post.letterbox(img, 640, 640)[None]
-            I = interp.Interp(g, 1)
-            I.set_input(x)
-            I.run()
-            heads = [(b[0], c[0], None, s) for b, c, _, s in I.heads_in]
-            return post.detect(heads, 80)
 
-        frame()
-        times = []
-        t_start = time.perf_counter()
-        while time.perf_counter() - t_start < budget_s and len(times) < 50:
-            t0 = time.perf_counter()
-            frame()
-            times.append(time.perf_counter() - t0)
-    ms = float(np.median(times)) * 1e3
-    return dict(value=round(1e3 / ms, 3), unit="frames/s", cores=int(cores), kind="port",
-                sample=f"yolo11n b1 810x1080 frame, letterbox+109 ops+decode+NMS, numpy fp32; "
-                       f"median of {len(times)} frames = {ms:.1f} ms/frame")
+def prepost_roofline(n, seg):
+    """Achieved HBM bandwidth of the pre/post kernels against the 8 TB/s roofline, from the
+    stage times (hipEvents, stream-ordered) and their algorithmic bytes:
+      letterbox  sh*sw*3 (u8 frame) + S*S*3*2 (fp16 input tensor)
+      decode     A*(64 + ncpad)*2 (box bins + class logits, fp16) + 24 per candidate
+      masks      Ph*Pw*nm*2 (proto, fp16) + survivors*Ph*Pw (u8 masks)
+    NMS is latency-bound: its time is reported, not a bandwidth."""
+    out = {}
+    if n:
+        st = n["stages"]
+        sh, sw = n["frame"]
+        lb = sh * sw * 3 + 640 * 640 * 3 * 2
+        dec = n["A"] * (64 + n["ncpad"]) * 2 + 24 * n["raw"]
+        for name, nbytes in (("letterbox", lb), ("decode", dec)):
+            us = st[name] * 1e3
+            gbs = nbytes / (us * 1e-6) / 1e9
+            out[name] = {"workload": "yolo11n b1 810x1080", "us": round(us, 2), "bytes": int(nbytes),
+                         "GB/s": round(gbs, 1), "frac": round(gbs * 1e9 / PEAK_HBM, 4)}
+        out["nms"] = {"workload": f"yolo11n b1, {n['raw']} candidates", "us": round(st["nms"] * 1e3, 2),
+                      "bound": "latency"}
+    if seg:
+        st = seg["stages"]
+        nbytes = 160 * 160 * 32 * 2 + seg["kept"] * 160 * 160
+        us = st["masks"] * 1e3
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out["masks"] = {"workload": f"yolo11n-seg b1, {seg['kept']} survivors", "us": round(us, 2),
+                        "bytes": int(nbytes), "GB/s": round(gbs, 1), "frac": round(gbs * 1e9 / PEAK_HBM, 4)}
+        out["nms_seg"] = {"workload": f"yolo11n-seg b1, {seg['raw']} candidates", "us": round(st["nms"] * 1e3, 2),
+                          "bound": "latency"}
+    return out
 
 
 def main():
@@ -487,12 +521,14 @@ def main():
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic frames, seeded random-init weights",
-        "config": {"workload": "yolo11n detect b1 e2e (letterbox+net+decode+NMS, frame in HBM)",
+        "config": {"workload": "yolo11n detect b1 e2e: H2D of the raw frame from pinned memory + letterbox + "
+                               "net + DFL decode + NMS + result copy in one hipGraph, wait, host fetch",
                    "imgsz": 640, "frame": "810x1080 u8 BGR", "batch": 1},
     }
     if n:
         line["yolo11n_b1"] = {"ms_per_frame": round(n["ms"], 4), "graph_ms": round(n["graph_ms"], 4),
-                              "ms_per_frame_pcie": round(n["ms_pcie"], 4), "kept": n["kept"],
+                              "ms_per_frame_frame_in_hbm": round(n["ms_hbm"], 4),
+                              "graph_ms_frame_in_hbm": round(n["graph_ms_hbm"], 4), "kept": n["kept"],
                               "raw_candidates": n["raw"], "stream_ops_ms": round(n["stream_ops_ms"], 4)}
     if x:
         line["yolo11x_b16"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in x.items()}
@@ -501,6 +537,10 @@ def main():
         if r:
             line[name] = {"ms_per_frame": round(r["ms"], 4), "graph_ms": round(r["graph_ms"], 4),
                           "kept": r["kept"], "raw_candidates": r["raw"]}
+            if "ms_hbm" in r:
+                line[name]["ms_per_frame_frame_in_hbm"] = round(r["ms_hbm"], 4)
+            else:
+                line[name]["frame"] = "in HBM"
     if out.get("cls"):
         r = out["cls"]
         line["yolo11n_cls_b1_224"] = {"ms_per_frame": round(r["ms"], 4), "graph_ms": round(r["graph_ms"], 4),
@@ -510,6 +550,9 @@ def main():
     if out.get("serve"):
         line["grpc_server_yolo11n"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                        for k, v in out["serve"].items()}
+    pp = prepost_roofline(n, out.get("seg"))
+    if pp:
+        line["prepost_roofline"] = pp
     if conv:
         achieved = conv["flops"] / (conv["ms"] * 1e-3)
         line["roofline"] = {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": 2500.0,

@@ -112,6 +112,9 @@ int yolo_tensor_shape(void* h, int t, int* hwc);
 /* Copy tensor t of the first B images to/from contiguous host fp16 [B][H][W][C]. */
 int yolo_read_tensor(void* h, int t, int B, void* host_f16);
 int yolo_write_tensor(void* h, int t, int B, const void* host_f16);
+/* The same for images first .. first+n-1 only. */
+int yolo_read_tensor_slots(void* h, int t, int first, int n, void* host_f16);
+int yolo_write_tensor_slots(void* h, int t, int first, int n, const void* host_f16);
 /* Run op k alone for B images on the engine stream and wait.  Returns 0 or -1. */
 int yolo_run_op(void* h, int k, int B);
 /* Run NMS (+ masks) and the result copies for B images after the DECODE ops ran. */
@@ -153,6 +156,11 @@ float yolo_time_graph(void* h, int which, int B, int iters);
  * inside a preceding op's launch (the second and third MAXPOOL5 of a fused SPPF chain)
  * reports only its event overhead. */
 int yolo_profile_ops(void* h, int B, int iters, float* ms);
+/* Average ms of the frame's pre/post stages over `iters` stream-ordered passes of the frame
+ * set by yolo_frame_graph (frames in device memory, no H2D): ms[0] letterbox of all slots,
+ * ms[1] decode (all levels, one launch), ms[2] NMS, ms[3] mask assembly (0 without a proto).
+ * -1 on classify handles or before yolo_frame_graph. */
+int yolo_profile_stages(void* h, int iters, float* ms);
 
 /* Allocation helpers (device / pinned host) and copies on the engine stream. */
 void* yolo_dev_alloc(size_t bytes);

@@ -112,4 +112,5 @@ def test_label_jsonl_and_coco(server, tmp_path, capsys):
     assert len(doc["categories"]) == 15 and len(doc["annotations"][0]["segmentation"][0]) == 8
     # bench mode
     assert yololabel.main(paths[:1] + ["--server", server, "--bench", "20", "-c", "8"]) == 0
-    assert "imgs in" in capsys.readouterr().out
+    out = capsys.readouterr().out
+    assert "20 requests, 8 callers" in out and "img/s" in out and "server batch" in out

@@ -258,8 +258,10 @@ static size_t attWholeLds(int N, int KS) {
 template <int HD>
 static void launchAttn(const View& qkv, const View& y, int N, int heads, float sl2, int Bn, hipStream_t st) {
   dim3 grid((N + AQ - 1) / AQ, heads, Bn);
-  const long blocks = (long)grid.x * grid.y * grid.z;
-  // key splits while the grid leaves most CUs idle
+  // key splits while one image's grid leaves most CUs idle.  Decided per image, not per
+  // launch, so an image's result does not depend on the batch it runs in (the splits change
+  // the softmax merge order).
+  const long blocks = (long)grid.x * grid.y;
   const int KS = blocks <= 128 ? 4 : blocks <= 512 ? 2 : 1;
   if (attWholeOk && N <= ATT_WHOLE_MAX && attWholeLds<HD>(N, KS) <= ATT_WHOLE_LDS) {
     const size_t lds = attWholeLds<HD>(N, KS);

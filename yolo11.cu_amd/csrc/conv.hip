@@ -1123,6 +1123,10 @@ void launchConvHalo(const View& x, const View& y, const View* res, const f16* w,
 // One thread per (pixel, 8-channel group); weights were repacked on the host from
 // [C][k][k] to [k*k][C] so each tap is one 16-byte load (the reference does the same
 // repack, engine/engine.cu:198-209).  fp32 accumulation; optional residual after act.
+// Both depthwise kernels accumulate bias + taps in row-major tap order with one fused
+// multiply-add per tap (an out-of-image tap contributes fma(0, w, a) = a), so whichever
+// kernel a launch size selects, a pixel's value is the same bit for bit: an image's result
+// does not depend on the batch it runs in.
 __global__ __launch_bounds__(256) void k_dwconv(View x, View y, View r, const f16* __restrict__ w,
                                                 const float* __restrict__ bias, int ksz, int cs,
                                                 int cp, int act, int total) {
@@ -1153,7 +1157,7 @@ __global__ __launch_bounds__(256) void k_dwconv(View x, View y, View r, const f1
 #pragma unroll
     for (int t = 0; t < 9; t++)
 #pragma unroll
-      for (int j = 0; j < 8; j++) a[j] += ok[t] ? (float)xv[t][j] * (float)wv[t][j] : 0.f;
+      for (int j = 0; j < 8; j++) a[j] = fmaf(ok[t] ? (float)xv[t][j] : 0.f, (float)wv[t][j], a[j]);
   } else {
     for (int ky = 0; ky < ksz; ky++) {
       const int iy = oy * cs - cp + ky;
@@ -1164,7 +1168,7 @@ __global__ __launch_bounds__(256) void k_dwconv(View x, View y, View r, const f1
         const f16x8 xv = *(const f16x8*)(x.p + ((size_t)(img * x.H + iy) * x.W + ix) * x.s + x.o + c);
         const f16x8 wv = *(const f16x8*)(w + (size_t)(ky * ksz + kx) * y.C + c);
 #pragma unroll
-        for (int j = 0; j < 8; j++) a[j] += (float)xv[j] * (float)wv[j];
+        for (int j = 0; j < 8; j++) a[j] = fmaf((float)xv[j], (float)wv[j], a[j]);
       }
     }
   }
@@ -1232,7 +1236,7 @@ __global__ __launch_bounds__(256) void k_dwconv3x4(View x, View y, View r, const
       for (int kx = 0; kx < 3; kx++) {
         const int i = o * CS + kx;
 #pragma unroll
-        for (int j = 0; j < 8; j++) a[o][j] += ok[i] ? (float)col[i][j] * (float)wv[kx][j] : 0.f;
+        for (int j = 0; j < 8; j++) a[o][j] = fmaf(ok[i] ? (float)col[i][j] : 0.f, (float)wv[kx][j], a[o][j]);
       }
   }
   const int m0 = (img * y.H + oy) * y.W + ox0;

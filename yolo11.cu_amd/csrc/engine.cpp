@@ -109,6 +109,9 @@ struct Engine {
   std::vector<float> execMs;
   hipGraphExec_t frameGraph = nullptr;
   int frameB = 0;
+  // the frame graph's device sources and sizes (for stage timing outside the graph)
+  std::vector<std::pair<const uint8_t*, SlotGeom>> frameSrc;
+  std::vector<int> frameH, frameW;
   std::vector<SlotGeom> slots;
   std::vector<SlotGeom> frameSlots;
   // branch concurrency: ops are spread over the main stream and NSIDE side streams by a
@@ -551,8 +554,10 @@ struct Engine {
   // Time every eligible (tile shape, split-K factor) of every GEMM conv at the max batch
   // (2 warm-up launches, then the median of 7 individually timed ones) and keep the
   // fastest; identical shapes share one measurement.  Splits of every tile are tried only
-  // while the tile grid is less than one chip wave; a grid of more than one wave whose last
-  // wave is part-empty tries tail splits that fill that wave.
+  // while the tile grid is less than one chip wave.  Tail splits are not candidates: which
+  // tiles they split depends on the batch, so an image's sums would depend on the batch it
+  // runs in (every choice made here keeps a batch-1 run of a frame bit-identical to its
+  // slot in a larger batch); yolo_set_op_split still selects them.
   void autotune() {
     hipEvent_t e0, e1;
     HCK(hipEventCreate(&e0));
@@ -592,12 +597,6 @@ struct Engine {
         std::vector<int> cands;
         for (int S : kSplits)
           if (S == 1 || (tiles * S <= 1024 && tiles < P)) cands.push_back(S);
-        if (P > 0 && tiles > P && tiles % P != 0) {
-          // tail split: the part-empty last wave of `rem` tiles becomes ~P/rem times as
-          // many blocks, each with 1/S of the K stages
-          const int S = std::min(P / (tiles % P), MAX_SPLITS);
-          if (S >= 2) cands.push_back(-S);
-        }
         std::sort(cands.begin(), cands.end());
         cands.erase(std::unique(cands.begin(), cands.end()), cands.end());
         for (int S : cands) {
@@ -1079,28 +1078,36 @@ int yolo_tensor_shape(void* h, int t, int* hwc) {
   return 0;
 }
 
-int yolo_read_tensor(void* h, int t, int B, void* host_f16) {
+int yolo_read_tensor_slots(void* h, int t, int first, int n, void* host_f16) {
   return guarded([&] {
     Engine* e = E(h);
-    if (t < 0 || t >= (int)e->g.tens.size() || B < 1 || B > e->B) return -1;
+    if (t < 0 || t >= (int)e->g.tens.size() || first < 0 || n < 1 || first + n > e->B) return -1;
     yolo::View v = e->view(t);
+    const size_t img = (size_t)v.H * v.W * v.s;
     HCK(hipStreamSynchronize(e->st));
-    HCK(hipMemcpy2D(host_f16, v.C * 2, v.p + v.o, (size_t)v.s * 2, v.C * 2, (size_t)B * v.H * v.W,
-                    hipMemcpyDeviceToHost));
+    HCK(hipMemcpy2D(host_f16, v.C * 2, v.p + first * img + v.o, (size_t)v.s * 2, v.C * 2,
+                    (size_t)n * v.H * v.W, hipMemcpyDeviceToHost));
     return 0;
   });
 }
 
-int yolo_write_tensor(void* h, int t, int B, const void* host_f16) {
+int yolo_write_tensor_slots(void* h, int t, int first, int n, const void* host_f16) {
   return guarded([&] {
     Engine* e = E(h);
-    if (t < 0 || t >= (int)e->g.tens.size() || B < 1 || B > e->B) return -1;
+    if (t < 0 || t >= (int)e->g.tens.size() || first < 0 || n < 1 || first + n > e->B) return -1;
     yolo::View v = e->view(t);
+    const size_t img = (size_t)v.H * v.W * v.s;
     HCK(hipStreamSynchronize(e->st));
-    HCK(hipMemcpy2D(v.p + v.o, (size_t)v.s * 2, host_f16, v.C * 2, v.C * 2, (size_t)B * v.H * v.W,
-                    hipMemcpyHostToDevice));
+    HCK(hipMemcpy2D(v.p + first * img + v.o, (size_t)v.s * 2, host_f16, v.C * 2, v.C * 2,
+                    (size_t)n * v.H * v.W, hipMemcpyHostToDevice));
     return 0;
   });
+}
+
+int yolo_read_tensor(void* h, int t, int B, void* host_f16) { return yolo_read_tensor_slots(h, t, 0, B, host_f16); }
+
+int yolo_write_tensor(void* h, int t, int B, const void* host_f16) {
+  return yolo_write_tensor_slots(h, t, 0, B, host_f16);
 }
 
 int yolo_run_op(void* h, int k, int B) {
@@ -1214,6 +1221,9 @@ int yolo_frame_graph(void* h, int B, const unsigned char* const* dev_bgr, const 
     e->frameGraph = nullptr;
     e->frameGraph = e->capture(B, &frames, host_bgr, heights, widths);
     e->frameB = B;
+    e->frameSrc = frames;
+    e->frameH.assign(heights, heights + B);
+    e->frameW.assign(widths, widths + B);
     for (int s = 0; s < B; s++) e->slots[s] = frames[s].second;
     return 0;
   });
@@ -1288,6 +1298,53 @@ int yolo_profile_ops(void* h, int B, int iters, float* ms) {
     HCK(hipMemsetAsync(e->nmsCount, 0, (size_t)e->B * sizeof(int), e->st));
     for (auto& x : ev) hipEventDestroy(x);
     for (int k = 0; k < n; k++) ms[k] = (float)(acc[k] / iters);
+    return 0;
+  });
+}
+
+int yolo_profile_stages(void* h, int iters, float* ms) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (!e->frameGraph || iters < 1 || e->g.cls || e->g.numAnchors == 0) return -1;
+    const int Bn = e->frameB, n = (int)e->ops.size();
+    hipEvent_t ev[7];
+    for (auto& x : ev) HCK(hipEventCreate(&x));
+    double acc[4] = {0, 0, 0, 0};
+    HCK(hipMemsetAsync(e->nmsCount, 0, (size_t)e->B * sizeof(int), e->st));
+    for (int it = 0; it < iters; it++) {
+      HCK(hipEventRecord(ev[0], e->st));
+      e->preprocessFrames(Bn, e->frameSrc, nullptr, e->frameH.data(), e->frameW.data());
+      HCK(hipEventRecord(ev[1], e->st));
+      for (int k = 0; k < n; k++) {
+        if (e->ops[k].chain < 0) continue;
+        if (k == e->lastDecode) HCK(hipEventRecord(ev[2], e->st));
+        e->runOp(k, Bn);
+        if (k == e->lastDecode) HCK(hipEventRecord(ev[3], e->st));
+      }
+      HCK(hipEventRecord(ev[4], e->st));
+      if (e->g.obb)
+        yolo::launchNmsObb(e->cand, e->nmsScratch, e->nmsCount, e->g.numAnchors, e->outdets, e->outidx, e->outcnt,
+                           e->rawcnt, e->params, Bn, e->st);
+      else
+        yolo::launchNms(e->cand, e->nmsScratch, e->nmsCount, e->g.numAnchors, e->cstride, e->outdets, e->outidx,
+                        e->outcnt, e->rawcnt, e->params, Bn, e->st);
+      HCK(hipEventRecord(ev[5], e->st));
+      if (e->g.protoTen >= 0) {
+        yolo::View pr = e->view(e->g.protoTen);
+        const yolo::BufDesc& ib = e->g.bufs[e->g.tens[0].buf];
+        yolo::launchMasks(pr, e->cand, e->cstride, e->g.numAnchors, e->g.nm, e->outidx, e->outcnt, e->outdets,
+                          e->masks, (float)pr.W / ib.W, (float)pr.H / ib.H, Bn, e->st);
+      }
+      HCK(hipEventRecord(ev[6], e->st));
+      HCK(hipEventSynchronize(ev[6]));
+      float t;
+      HCK(hipEventElapsedTime(&t, ev[0], ev[1])); acc[0] += t;
+      HCK(hipEventElapsedTime(&t, ev[2], ev[3])); acc[1] += t;
+      HCK(hipEventElapsedTime(&t, ev[4], ev[5])); acc[2] += t;
+      HCK(hipEventElapsedTime(&t, ev[5], ev[6])); acc[3] += t;
+    }
+    for (auto& x : ev) (void)hipEventDestroy(x);
+    for (int i = 0; i < 4; i++) ms[i] = (float)(acc[i] / iters);
     return 0;
   });
 }

@@ -100,6 +100,13 @@ class ConvSpec:
     act: int = ACT_SILU
     bn: bool = True             # ultralytics Conv (BN folded) vs plain nn.Conv2d
     bias: float | None = None   # constant bias override (Detect.bias_init)
+    name: str = ""              # module path in an ultralytics state_dict ("model.2.m.0.cv1")
+
+
+def fold_bn(w: np.ndarray, gamma: np.ndarray, beta: np.ndarray, mean: np.ndarray, var: np.ndarray):
+    """BatchNorm folded into the preceding conv (eval mode, eps BN_EPS): w [O, ...], -> (w', b')."""
+    scale = gamma / np.sqrt(var + np.float32(BN_EPS))
+    return (w * scale.reshape((-1,) + (1,) * (w.ndim - 1))).astype(np.float32), (beta - mean * scale).astype(np.float32)
 
 
 def _conv_nhwc(x: np.ndarray, w: np.ndarray, s: int, p: int, g: int) -> np.ndarray:
@@ -130,7 +137,12 @@ class ModelGraph:
     With a calibration frame, every emitted op is also evaluated (fp32, batch 1) so each
     BatchNorm can be folded with the running statistics of its own conv output."""
 
-    def __init__(self, seed: int, calib: np.ndarray | None = None):
+    def __init__(self, seed: int, calib: np.ndarray | None = None, source=None, record: dict | None = None):
+        # source: parameters come from a checkpoint (convert.StateDictSource) instead of the
+        # seeded generator; record: the generator's unfolded parameters are stored into this
+        # dict under ultralytics state_dict names (the inverse of a checkpoint import)
+        self.source = source
+        self.record = record
         self.rng = np.random.default_rng(seed)
         self.bufs: list[tuple[int, int, int]] = []
         self.tens: list[tuple[int, int, int]] = []
@@ -183,6 +195,8 @@ class ModelGraph:
     # -- random parameters ----------------------------------------------------------
     def _conv_params(self, sp: ConvSpec, x_val: np.ndarray | None):
         """Returns torch-layout weight [O, I/g, k, k] (fp32, BN folded) and bias [O]."""
+        if self.source is not None:
+            return self.source.conv(sp)
         ig = sp.c1 // sp.g
         fan_in = ig * sp.k * sp.k
         w = self.rng.standard_normal((sp.c2, ig, sp.k, sp.k), dtype=np.float32) / np.float32(math.sqrt(fan_in))
@@ -195,14 +209,18 @@ class ModelGraph:
                 z = _conv_nhwc(x_val[..., :sp.c1], w, sp.s, autopad(sp.k), sp.g)
                 mean = z.mean(axis=(0, 1, 2)).astype(np.float32)
                 var = z.var(axis=(0, 1, 2)).astype(np.float32)
-            scale = gamma / np.sqrt(var + np.float32(BN_EPS))
-            w = w * scale[:, None, None, None]
-            b = beta - mean * scale
+            if self.record is not None:
+                self.record.update({f"{sp.name}.conv.weight": w.copy(), f"{sp.name}.bn.weight": gamma,
+                                    f"{sp.name}.bn.bias": beta, f"{sp.name}.bn.running_mean": mean,
+                                    f"{sp.name}.bn.running_var": var})
+            w, b = fold_bn(w, gamma, beta, mean, var)
         else:
             bound = 1.0 / math.sqrt(fan_in)
             b = self.rng.uniform(-bound, bound, sp.c2).astype(np.float32)
         if sp.bias is not None:
             b = np.full(sp.c2, sp.bias, np.float32)
+        if self.record is not None and not sp.bn:
+            self.record.update({f"{sp.name}.weight": w.copy(), f"{sp.name}.bias": b.copy()})
         return w.astype(np.float32), b.astype(np.float32)
 
     def _eval_conv(self, x, w, b, sp: ConvSpec, out):
@@ -291,14 +309,19 @@ class ModelGraph:
             self.val(out)[...] = self.val(x)
         return out
 
-    def conv_transpose2(self, x, c_out: int, out=None):
+    def conv_transpose2(self, x, c_out: int, out=None, name: str = ""):
         """ConvTranspose2d(Cin -> C, k=2, s=2) emitted as a 1x1 CONV to 4C (quadrant-major
         rows q*C + o, q = 2*di + dj) followed by PS2 (export/export.py:166-181)."""
         H, W, Cin = self.shape(x)
         C = c_out
-        wt = self.rng.standard_normal((Cin, C, 2, 2), dtype=np.float32) / np.float32(math.sqrt(Cin))
-        bound = 1.0 / math.sqrt(Cin)
-        bt = self.rng.uniform(-bound, bound, C).astype(np.float32)
+        if self.source is not None:
+            wt, bt = self.source.conv_transpose(name, Cin, C)
+        else:
+            wt = self.rng.standard_normal((Cin, C, 2, 2), dtype=np.float32) / np.float32(math.sqrt(Cin))
+            bound = 1.0 / math.sqrt(Cin)
+            bt = self.rng.uniform(-bound, bound, C).astype(np.float32)
+            if self.record is not None:
+                self.record.update({f"{name}.weight": wt.copy(), f"{name}.bias": bt.copy()})
         self.last_convt = (wt.copy(), bt.copy())
         w = wt.transpose(2, 3, 1, 0).reshape(4 * C, 1, 1, Cin)
         b = np.tile(bt, 4)
@@ -326,15 +349,21 @@ class ModelGraph:
             self.val(out)[...] = self.val(x).mean(axis=(1, 2), keepdims=True)
         return out
 
-    def linear(self, x, O: int):
+    def linear(self, x, O: int, name: str = ""):
         """nn.Linear(I, O) on a [1,1,I] tensor as a 1x1 CONV (export/export.py:208-217):
         weights N(0, 1/I), bias U(+-1/sqrt(I)) (torch's default bias range), no activation."""
         H, W, I = self.shape(x)
         assert (H, W) == (1, 1)
         out = self.newt(1, 1, O)
-        w = self.rng.standard_normal((O, 1, 1, I), dtype=np.float32) / np.float32(math.sqrt(I))
-        bound = 1.0 / math.sqrt(I)
-        b = self.rng.uniform(-bound, bound, O).astype(np.float32)
+        if self.source is not None:
+            w, b = self.source.linear(name, I, O)
+            w = w.reshape(O, 1, 1, I)
+        else:
+            w = self.rng.standard_normal((O, 1, 1, I), dtype=np.float32) / np.float32(math.sqrt(I))
+            bound = 1.0 / math.sqrt(I)
+            b = self.rng.uniform(-bound, bound, O).astype(np.float32)
+            if self.record is not None:
+                self.record.update({f"{name}.weight": w.reshape(O, I).copy(), f"{name}.bias": b.copy()})
         woff, boff = self.add_weight(w, b)
         self.ops.append(("CONV", x, out, 1, 1, 0, 1, ACT_NONE, I, O, woff, boff))
         if self.cal:
@@ -371,65 +400,65 @@ class ModelGraph:
 # ---------------------------------------------------------------------------------------
 # module decomposition (export/export.py:222-302)
 
-def _bottleneck(g, x, c1, c2, shortcut, e, out):
+def _bottleneck(g, x, c1, c2, shortcut, e, out, name=""):
     c_ = int(c2 * e)
-    t = g.conv(x, ConvSpec(c1, c_, 3))
-    g.conv(t, ConvSpec(c_, c2, 3), out=out)
+    t = g.conv(x, ConvSpec(c1, c_, 3, name=f"{name}.cv1"))
+    g.conv(t, ConvSpec(c_, c2, 3, name=f"{name}.cv2"), out=out)
     if shortcut and c1 == c2:
         g.add(out, x, out)
     return out
 
 
-def _c3k(g, x, c1, c2, n, shortcut, out):
+def _c3k(g, x, c1, c2, n, shortcut, out, name=""):
     H, W, _ = g.shape(x)
     c_ = int(c2 * 0.5)
     cat = g.buf(H, W, 2 * c_)
-    cur = g.conv(x, ConvSpec(c1, c_, 1))
+    cur = g.conv(x, ConvSpec(c1, c_, 1, name=f"{name}.cv1"))
     for j in range(n):
         dst = g.ten(cat, 0, c_) if j == n - 1 else g.newt(H, W, c_)
-        _bottleneck(g, cur, c_, c_, shortcut, 1.0, dst)
+        _bottleneck(g, cur, c_, c_, shortcut, 1.0, dst, f"{name}.m.{j}")
         cur = dst
-    g.conv(x, ConvSpec(c1, c_, 1), out=g.ten(cat, c_, c_))
-    g.conv(g.ten(cat, 0, 2 * c_), ConvSpec(2 * c_, c2, 1), out=out)
+    g.conv(x, ConvSpec(c1, c_, 1, name=f"{name}.cv2"), out=g.ten(cat, c_, c_))
+    g.conv(g.ten(cat, 0, 2 * c_), ConvSpec(2 * c_, c2, 1, name=f"{name}.cv3"), out=out)
     return out
 
 
-def _c2f(g, x, c1, c2, n, c3k, e, shortcut, v11, out):
+def _c2f(g, x, c1, c2, n, c3k, e, shortcut, v11, out, name=""):
     """C3k2 (v11) / C2f (v8): cv1 -> split -> n blocks chained -> concat -> cv2."""
     H, W, _ = g.shape(x)
     c = int(c2 * e)
     cat = g.buf(H, W, (2 + n) * c)
-    g.conv(x, ConvSpec(c1, 2 * c, 1), out=g.ten(cat, 0, 2 * c))
+    g.conv(x, ConvSpec(c1, 2 * c, 1, name=f"{name}.cv1"), out=g.ten(cat, 0, 2 * c))
     prev = g.ten(cat, c, c)
     for j in range(n):
         dst = g.ten(cat, (2 + j) * c, c)
         if c3k:
-            _c3k(g, prev, c, c, 2, shortcut, dst)
+            _c3k(g, prev, c, c, 2, shortcut, dst, f"{name}.m.{j}")
         else:
             # C3k2's Bottleneck keeps e=0.5; C2f's uses e=1.0
-            _bottleneck(g, prev, c, c, shortcut, 0.5 if v11 else 1.0, dst)
+            _bottleneck(g, prev, c, c, shortcut, 0.5 if v11 else 1.0, dst, f"{name}.m.{j}")
         prev = dst
-    return g.conv(g.ten(cat, 0, (2 + n) * c), ConvSpec((2 + n) * c, c2, 1), out=out)
+    return g.conv(g.ten(cat, 0, (2 + n) * c), ConvSpec((2 + n) * c, c2, 1, name=f"{name}.cv2"), out=out)
 
 
-def _sppf(g, x, c1, c2, out):
+def _sppf(g, x, c1, c2, out, name=""):
     H, W, _ = g.shape(x)
     c_ = c1 // 2
     cat = g.buf(H, W, 4 * c_)
-    g.conv(x, ConvSpec(c1, c_, 1), out=g.ten(cat, 0, c_))
+    g.conv(x, ConvSpec(c1, c_, 1, name=f"{name}.cv1"), out=g.ten(cat, 0, c_))
     for j in range(3):
         g.maxpool5(g.ten(cat, j * c_, c_), g.ten(cat, (j + 1) * c_, c_))
-    return g.conv(g.ten(cat, 0, 4 * c_), ConvSpec(4 * c_, c2, 1), out=out)
+    return g.conv(g.ten(cat, 0, 4 * c_), ConvSpec(4 * c_, c2, 1, name=f"{name}.cv2"), out=out)
 
 
-def _psablock(g, xio, c):
+def _psablock(g, xio, c, name=""):
     """x = x + attn(x); x = x + ffn(x), in place on view xio (export/export.py:269-290)."""
     H, W, C = g.shape(xio)
     heads = c // 64
     hd = c // heads
     kd = int(hd * 0.5)
     per = 2 * kd + hd
-    qkv = g.conv(xio, ConvSpec(c, c + 2 * kd * heads, 1, act=ACT_NONE))
+    qkv = g.conv(xio, ConvSpec(c, c + 2 * kd * heads, 1, act=ACT_NONE, name=f"{name}.attn.qkv"))
     qb = g.tens[qkv][0]
     vbuf = g.buf(H, W, C)
     for h in range(heads):
@@ -448,25 +477,25 @@ def _psablock(g, xio, c):
                 e = np.exp(sc - sc.max(1, keepdims=True))
                 o[i, :, h * hd:(h + 1) * hd] = (e / e.sum(1, keepdims=True)) @ v
         g.val(ao)[...] = o.reshape(nb, H, W, heads * hd)
-    pe = g.conv(vt, ConvSpec(c, c, 3, g=c, act=ACT_NONE))
+    pe = g.conv(vt, ConvSpec(c, c, 3, g=c, act=ACT_NONE, name=f"{name}.attn.pe"))
     g.add(ao, pe, ao)
-    pr = g.conv(ao, ConvSpec(c, c, 1, act=ACT_NONE))
+    pr = g.conv(ao, ConvSpec(c, c, 1, act=ACT_NONE, name=f"{name}.attn.proj"))
     g.add(xio, pr, xio)
-    f1 = g.conv(xio, ConvSpec(c, 2 * c, 1))
-    f2 = g.conv(f1, ConvSpec(2 * c, c, 1, act=ACT_NONE))
+    f1 = g.conv(xio, ConvSpec(c, 2 * c, 1, name=f"{name}.ffn.0"))
+    f2 = g.conv(f1, ConvSpec(2 * c, c, 1, act=ACT_NONE, name=f"{name}.ffn.1"))
     g.add(xio, f2, xio)
     return xio
 
 
-def _c2psa(g, x, c1, c2, n, out):
+def _c2psa(g, x, c1, c2, n, out, name=""):
     H, W, _ = g.shape(x)
     c = int(c1 * 0.5)
     cat = g.buf(H, W, 2 * c)
-    g.conv(x, ConvSpec(c1, 2 * c, 1), out=g.ten(cat, 0, 2 * c))
+    g.conv(x, ConvSpec(c1, 2 * c, 1, name=f"{name}.cv1"), out=g.ten(cat, 0, 2 * c))
     b = g.ten(cat, c, c)
-    for _ in range(n):
-        _psablock(g, b, c)
-    return g.conv(g.ten(cat, 0, 2 * c), ConvSpec(2 * c, c1, 1), out=out)
+    for j in range(n):
+        _psablock(g, b, c, f"{name}.m.{j}")
+    return g.conv(g.ten(cat, 0, 2 * c), ConvSpec(2 * c, c1, 1, name=f"{name}.cv2"), out=out)
 
 
 # ---------------------------------------------------------------------------------------
@@ -485,7 +514,7 @@ class ModelInfo:
 
 def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc: int = 80,
                 imgsz: int = 640, seed: int = 0, cls_bias: float = -3.0, nm: int = 32,
-                calibrate: bool = True) -> ModelInfo:
+                calibrate: bool = True, source=None, record: dict | None = None) -> ModelInfo:
     """Builds the flat op graph of a seeded random-init YOLO model (export/export.py:317-441)."""
     assert arch in SCALES and scale in SCALES[arch], (arch, scale)
     assert task in ("detect", "segment", "obb", "classify"), task
@@ -496,8 +525,8 @@ def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc
     depth, width, max_ch = SCALES[arch][scale]
     v11 = arch == "yolo11"
     S = imgsz
-    calib = calibration_frames(S, seed) if calibrate else None
-    g = ModelGraph(seed, calib)
+    calib = calibration_frames(S, seed) if calibrate and source is None else None
+    g = ModelGraph(seed, calib, source, record)
     x0 = g.newt(S, S, 3)
 
     # resolve module args (parse_model rules)
@@ -552,16 +581,17 @@ def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc
         m = sp["m"]
         xin = outs[sp["srcs"][0]]
         dst = g.ten(*feed[i]) if i in feed else None
+        mn = f"model.{i}"
         if m == "Conv":
-            y = g.conv(xin, ConvSpec(sp["c1"], sp["c2"], sp["k"], sp["s"]), out=dst)
+            y = g.conv(xin, ConvSpec(sp["c1"], sp["c2"], sp["k"], sp["s"], name=mn), out=dst)
         elif m == "C2PSA":
-            y = _c2psa(g, xin, sp["c1"], sp["c2"], sp["n"], dst)
+            y = _c2psa(g, xin, sp["c1"], sp["c2"], sp["n"], dst, mn)
         elif m == "SPPF":
-            y = _sppf(g, xin, sp["c1"], sp["c2"], dst)
+            y = _sppf(g, xin, sp["c1"], sp["c2"], dst, mn)
         elif m == "C3k2":
-            y = _c2f(g, xin, sp["c1"], sp["c2"], sp["n"], sp["c3k"], sp["e"], True, True, dst)
+            y = _c2f(g, xin, sp["c1"], sp["c2"], sp["n"], sp["c3k"], sp["e"], True, True, dst, mn)
         elif m == "C2f":
-            y = _c2f(g, xin, sp["c1"], sp["c2"], sp["n"], False, 0.5, sp["shortcut"], False, dst)
+            y = _c2f(g, xin, sp["c1"], sp["c2"], sp["n"], False, 0.5, sp["shortcut"], False, dst, mn)
         elif m == "Upsample":
             y = g.upsample2(xin, dst if dst is not None else g.newt(hw[i], hw[i], ch[i]))
         else:
@@ -573,9 +603,10 @@ def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc
     if cls_task:
         # Classify (export/export.py:391-398): Conv(c1, 1280, 1) -> GAP -> Linear(1280, nc)
         # -> softmax; the head width 1280 is fixed (docs/specs/cls.md:53-54)
-        h = g.conv(outs[n_body - 1], ConvSpec(ch[n_body - 1], 1280, 1))
+        hn = f"model.{n_body}"
+        h = g.conv(outs[n_body - 1], ConvSpec(ch[n_body - 1], 1280, 1, name=f"{hn}.conv"))
         gp = g.gap(h, g.newt(1, 1, 1280))
-        logits = g.linear(gp, nc)
+        logits = g.linear(gp, nc, f"{hn}.linear")
         g.softmax(logits, g.newt(1, 1, nc))
         return ModelInfo(arch, scale, task, nc, imgsz, g, seed, cls_bias)
 
@@ -591,35 +622,37 @@ def build_model(arch: str = "yolo11", scale: str = "n", task: str = "detect", nc
     seg = task == "segment"
     obb = task == "obb"
     c4o = max(chs[0] // 4, 1)            # OBB angle branch width, ne = 1 (docs/specs/obb.md:60-61)
+    hn = f"model.{n_body}"
     if seg:
         npr = ceil8(min(256, max_ch) * width)
-        t = g.conv(feats[0], ConvSpec(chs[0], npr, 3))
-        t = g.conv_transpose2(t, npr)
-        t = g.conv(t, ConvSpec(npr, npr, 3))
-        t_proto = g.conv(t, ConvSpec(npr, nm, 1))
+        t = g.conv(feats[0], ConvSpec(chs[0], npr, 3, name=f"{hn}.proto.cv1"))
+        t = g.conv_transpose2(t, npr, name=f"{hn}.proto.upsample")
+        t = g.conv(t, ConvSpec(npr, npr, 3, name=f"{hn}.proto.cv2"))
+        t_proto = g.conv(t, ConvSpec(npr, nm, 1, name=f"{hn}.proto.cv3"))
         c4 = max(chs[0] // 4, nm)
     for i, (f, cx, st) in enumerate(zip(feats, chs, strides)):
-        b = g.conv(f, ConvSpec(cx, c2h, 3))
-        b = g.conv(b, ConvSpec(c2h, c2h, 3))
-        b = g.conv(b, ConvSpec(c2h, 4 * reg_max, 1, act=ACT_NONE, bn=False, bias=1.0))
+        bn_, cn_, an_ = f"{hn}.cv2.{i}", f"{hn}.cv3.{i}", f"{hn}.cv4.{i}"
+        b = g.conv(f, ConvSpec(cx, c2h, 3, name=f"{bn_}.0"))
+        b = g.conv(b, ConvSpec(c2h, c2h, 3, name=f"{bn_}.1"))
+        b = g.conv(b, ConvSpec(c2h, 4 * reg_max, 1, act=ACT_NONE, bn=False, bias=1.0, name=f"{bn_}.2"))
         if v11:
-            c = g.conv_pad(f, ConvSpec(cx, cx, 3, g=cx))
-            c = g.conv_pad(c, ConvSpec(cx, c3h, 1))
-            c = g.conv_pad(c, ConvSpec(c3h, c3h, 3, g=c3h))
-            c = g.conv_pad(c, ConvSpec(c3h, c3h, 1))
+            c = g.conv_pad(f, ConvSpec(cx, cx, 3, g=cx, name=f"{cn_}.0.0"))
+            c = g.conv_pad(c, ConvSpec(cx, c3h, 1, name=f"{cn_}.0.1"))
+            c = g.conv_pad(c, ConvSpec(c3h, c3h, 3, g=c3h, name=f"{cn_}.1.0"))
+            c = g.conv_pad(c, ConvSpec(c3h, c3h, 1, name=f"{cn_}.1.1"))
         else:
-            c = g.conv_pad(f, ConvSpec(cx, c3h, 3))
-            c = g.conv_pad(c, ConvSpec(c3h, c3h, 3))
-        c = g.conv_pad(c, ConvSpec(c3h, nc, 1, act=ACT_NONE, bn=False, bias=cls_bias), ncpad)
+            c = g.conv_pad(f, ConvSpec(cx, c3h, 3, name=f"{cn_}.0"))
+            c = g.conv_pad(c, ConvSpec(c3h, c3h, 3, name=f"{cn_}.1"))
+        c = g.conv_pad(c, ConvSpec(c3h, nc, 1, act=ACT_NONE, bn=False, bias=cls_bias, name=f"{cn_}.2"), ncpad)
         if seg:
-            mc = g.conv(f, ConvSpec(cx, c4, 3))
-            mc = g.conv(mc, ConvSpec(c4, c4, 3))
-            mc = g.conv(mc, ConvSpec(c4, nm, 1, act=ACT_NONE, bn=False))
+            mc = g.conv(f, ConvSpec(cx, c4, 3, name=f"{an_}.0"))
+            mc = g.conv(mc, ConvSpec(c4, c4, 3, name=f"{an_}.1"))
+            mc = g.conv(mc, ConvSpec(c4, nm, 1, act=ACT_NONE, bn=False, name=f"{an_}.2"))
             g.ops.append(("DECODESEG", b, c, mc, st))
         elif obb:
-            a = g.conv(f, ConvSpec(cx, c4o, 3))
-            a = g.conv(a, ConvSpec(c4o, c4o, 3))
-            a = g.conv_pad(a, ConvSpec(c4o, 1, 1, act=ACT_NONE, bn=False), 8)
+            a = g.conv(f, ConvSpec(cx, c4o, 3, name=f"{an_}.0"))
+            a = g.conv(a, ConvSpec(c4o, c4o, 3, name=f"{an_}.1"))
+            a = g.conv_pad(a, ConvSpec(c4o, 1, 1, act=ACT_NONE, bn=False, name=f"{an_}.2"), 8)
             g.ops.append(("DECODEOBB", b, c, a, st))
         else:
             g.ops.append(("DECODE", b, c, st))

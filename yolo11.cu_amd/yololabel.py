@@ -1,26 +1,33 @@
-"""Labeling client for the detection server (the reference's client/label.py, same CLI).
+"""Labeling client for the detection server (the CLI of the reference's client/label.py).
 
     python yolo11.cu_amd/yololabel.py imgs/*.jpg --out labels.jsonl      # JSONL, one line per image
     python yolo11.cu_amd/yololabel.py imgs/*.jpg --coco labels.json      # COCO annotations
     python yolo11.cu_amd/yololabel.py bus.jpg --bench 2000 -c 64          # throughput / latency
 
 Talks to `yolo.Yolo/Detect` through the run-time schema (no generated stubs or grpc_tools).
-JSONL records carry the task and its fields as the reference client writes them
-(client/label.py:57-71).  COCO export (client/label.py:118-163): boxes as xywh, OBB as the
-4-corner polygon plus its axis-aligned box, and -- instead of cv2 contour polygons, which need
-OpenCV -- segment masks as COCO uncompressed RLE in original-image pixels: each original pixel
-maps through the letterbox (x * scale + left, at 4 letterbox pixels per mask pixel) to the
-mask pixel that covers it; counts are column-major as COCO defines them.
+
+Outputs keep the reference client's formats, since other tools read them: the JSONL record
+keys per task (client/label.py:63-76) and the COCO field names and class tables
+(client/label.py:86-101,118-163).  The code is this module's own:
+
+* a response becomes a record through one table, RESULT_FIELDS (repeated response field ->
+  the message fields copied), the first non-empty repeated field naming the record's kind;
+* COCO annotations are built per record kind; OBB corners come from one rotation of the
+  half-extent corners (numpy); segment masks -- instead of OpenCV contour polygons, which
+  need cv2 -- are COCO uncompressed RLE in original-image pixels: each original pixel maps
+  through the letterbox (x * scale + left, at 4 letterbox pixels per mask pixel) to the mask
+  pixel that covers it, counts column-major as COCO defines them;
+* --bench runs `concurrency` closed-loop callers that share one request counter and report
+  per-request latency percentiles and the server's mean batch size.
 """
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
+import threading
 import time
-from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -38,23 +45,28 @@ DOTA15 = ("plane ship storage_tank baseball_diamond tennis_court basketball_cour
           "bridge large_vehicle small_vehicle helicopter roundabout soccer_ball_field swimming_pool").split()
 PROTO_STRIDE = 4          # letterbox pixels per proto-mask pixel
 
+# repeated response field -> message fields copied into the record, in precedence order: a
+# response carries exactly one kind of result (classify, obb, detect/segment)
+RESULT_FIELDS = (
+    ("classes", ("id", "prob")),
+    ("rboxes", ("cx", "cy", "w", "h", "angle", "score", "cls")),
+    ("boxes", ("x1", "y1", "x2", "y2", "score", "cls")),
+)
+
 
 def record(resp) -> dict:
     """The JSONL record of one response (without the image path)."""
-    out = {"task": resp.task or "detect"}
-    if resp.classes:
-        out["classes"] = [{"id": c.id, "prob": c.prob} for c in resp.classes]
-    elif resp.rboxes:
-        out["rboxes"] = [{"cx": b.cx, "cy": b.cy, "w": b.w, "h": b.h, "angle": b.angle, "score": b.score,
-                          "cls": b.cls} for b in resp.rboxes]
-    else:
-        out["boxes"] = [{"x1": b.x1, "y1": b.y1, "x2": b.x2, "y2": b.y2, "score": b.score, "cls": b.cls}
-                        for b in resp.boxes]
-        if resp.masks:
-            out["mask_h"], out["mask_w"] = resp.mask_h, resp.mask_w
-            out["letterbox"] = {"scale": resp.lb_scale, "top": resp.lb_top, "left": resp.lb_left}
-            out["masks"] = [list(m.rle) for m in resp.masks]
-    return out
+    rec = {"task": resp.task or "detect"}
+    for name, keys in RESULT_FIELDS:
+        msgs = getattr(resp, name)
+        if len(msgs) or name == "boxes":
+            rec[name] = [dict(zip(keys, (getattr(m, k) for k in keys))) for m in msgs]
+            break
+    if "boxes" in rec and len(resp.masks):
+        rec.update(mask_h=resp.mask_h, mask_w=resp.mask_w,
+                   letterbox={"scale": resp.lb_scale, "top": resp.lb_top, "left": resp.lb_left},
+                   masks=[list(m.rle) for m in resp.masks])
+    return rec
 
 
 def rle_to_mask(runs, h: int, w: int) -> np.ndarray:
@@ -87,48 +99,123 @@ def coco_rle(mask: np.ndarray) -> dict:
     return {"counts": runs.astype(int).tolist(), "size": [int(mask.shape[0]), int(mask.shape[1])]}
 
 
+# half-extent signs of the four corners, counter-clockwise from the (-w/2, -h/2) corner
+_CORNER_SIGNS = np.array([[-1.0, -1.0], [1.0, -1.0], [1.0, 1.0], [-1.0, 1.0]])
+
+
 def obb_corners(b: dict):
-    ca, sa = math.cos(b["angle"]), math.sin(b["angle"])
-    hw, hh = b["w"] / 2, b["h"] / 2
-    return [(b["cx"] + dx * ca - dy * sa, b["cy"] + dx * sa + dy * ca)
-            for dx, dy in ((-hw, -hh), (hw, -hh), (hw, hh), (-hw, hh))]
+    """Corners of a rotated box (cx, cy, w, h, angle in radians) as four (x, y) tuples."""
+    c, s = np.cos(b["angle"]), np.sin(b["angle"])
+    rot = np.array([[c, -s], [s, c]])
+    pts = (_CORNER_SIGNS * (0.5 * np.array([b["w"], b["h"]]))) @ rot.T + np.array([b["cx"], b["cy"]])
+    return [(float(x), float(y)) for x, y in pts]
+
+
+def _xywh(x0, y0, x1, y1) -> list:
+    return [round(float(v), 2) for v in (x0, y0, x1 - x0, y1 - y0)]
+
+
+def _box_annotations(res: dict, hw: tuple[int, int]):
+    """(category, score, bbox, area, segmentation | None) per box of a detect/segment record."""
+    for j, b in enumerate(res.get("boxes", [])):
+        bbox = _xywh(b["x1"], b["y1"], b["x2"], b["y2"])
+        seg = None
+        if "masks" in res:
+            m = rle_to_mask(res["masks"][j], res["mask_h"], res["mask_w"])
+            seg = coco_rle(mask_to_original(m, res["letterbox"], *hw))
+        yield b["cls"], b["score"], bbox, round((b["x2"] - b["x1"]) * (b["y2"] - b["y1"]), 2), seg
+
+
+def _rbox_annotations(res: dict, hw: tuple[int, int]):
+    """The same for an OBB record: the corner polygon and its axis-aligned bounds."""
+    for b in res.get("rboxes", []):
+        pts = np.array(obb_corners(b))
+        lo, hi = pts.min(0), pts.max(0)
+        poly = [round(float(v), 2) for v in pts.ravel()]
+        yield b["cls"], b["score"], _xywh(lo[0], lo[1], hi[0], hi[1]), round(b["w"] * b["h"], 2), [poly]
 
 
 def coco(results: dict, sizes: dict) -> dict:
     """COCO annotations for {path: record}; `sizes` maps path -> (h, w) of the original image."""
     images, anns = [], []
-    aid = 1
-    for iid, (path, res) in enumerate(sorted(results.items()), 1):
-        h, w = sizes[path]
-        images.append({"id": iid, "file_name": os.path.basename(path), "height": h, "width": w})
-        for j, b in enumerate(res.get("boxes", [])):
-            bw, bh = b["x2"] - b["x1"], b["y2"] - b["y1"]
-            a = {"id": aid, "image_id": iid, "category_id": b["cls"], "iscrowd": 0, "score": round(b["score"], 4),
-                 "bbox": [round(b["x1"], 2), round(b["y1"], 2), round(bw, 2), round(bh, 2)],
-                 "area": round(bw * bh, 2)}
-            if "masks" in res:
-                m = rle_to_mask(res["masks"][j], res["mask_h"], res["mask_w"])
-                a["segmentation"] = coco_rle(mask_to_original(m, res["letterbox"], h, w))
-            anns.append(a)
-            aid += 1
-        for b in res.get("rboxes", []):
-            pts = obb_corners(b)
-            xs, ys = [p[0] for p in pts], [p[1] for p in pts]
-            anns.append({"id": aid, "image_id": iid, "category_id": b["cls"], "iscrowd": 0,
-                         "score": round(b["score"], 4),
-                         "segmentation": [[round(v, 2) for p in pts for v in p]],
-                         "bbox": [round(min(xs), 2), round(min(ys), 2), round(max(xs) - min(xs), 2),
-                                  round(max(ys) - min(ys), 2)],
-                         "area": round(b["w"] * b["h"], 2)})
-            aid += 1
+    for iid, path in enumerate(sorted(results), 1):
+        res, hw = results[path], sizes[path]
+        images.append({"id": iid, "file_name": os.path.basename(path), "height": hw[0], "width": hw[1]})
+        for gen in (_box_annotations, _rbox_annotations):
+            for cat, score, bbox, area, seg in gen(res, hw):
+                a = {"id": len(anns) + 1, "image_id": iid, "category_id": cat, "iscrowd": 0,
+                     "score": round(score, 4), "bbox": bbox, "area": area}
+                if seg is not None:
+                    a["segmentation"] = seg
+                anns.append(a)
     names = DOTA15 if any(r.get("task") == "obb" for r in results.values()) else COCO80
-    return {"images": images, "annotations": anns, "categories": [{"id": i, "name": n} for i, n in enumerate(names)]}
+    return {"images": images, "annotations": anns,
+            "categories": [{"id": i, "name": n} for i, n in enumerate(names)]}
 
 
 def image_size(path: str) -> tuple[int, int]:
     from PIL import Image
     with Image.open(path) as im:
         return im.size[1], im.size[0]
+
+
+class _Load:
+    """Closed-loop load: `callers` threads take request numbers from one shared counter
+    until `total` requests were sent; each records its latency and the batch it rode in."""
+
+    def __init__(self, call, request, total: int, callers: int):
+        self.call, self.request, self.total, self.callers = call, request, total, callers
+        self.lock = threading.Lock()
+        self.sent = 0
+        self.lat_ms = np.zeros(total)
+        self.batch = np.zeros(total)
+
+    def _caller(self):
+        while True:
+            with self.lock:
+                i = self.sent
+                if i >= self.total:
+                    return
+                self.sent += 1
+            t = time.perf_counter()
+            resp = self.call(self.request)
+            self.lat_ms[i] = (time.perf_counter() - t) * 1e3
+            self.batch[i] = resp.batch
+
+    def run(self) -> dict:
+        threads = [threading.Thread(target=self._caller, daemon=True) for _ in range(self.callers)]
+        t = time.perf_counter()
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join()
+        wall = time.perf_counter() - t
+        p50, p95, p99 = np.percentile(self.lat_ms, [50, 95, 99])
+        return {"requests": self.total, "seconds": wall, "img_per_s": self.total / wall, "p50_ms": p50,
+                "p95_ms": p95, "p99_ms": p99, "mean_batch": float(self.batch.mean())}
+
+
+def _label_all(call, model: str, paths: list[str], callers: int) -> dict:
+    """One request per image over `callers` threads; {path: record}."""
+    out, lock, todo = {}, threading.Lock(), list(reversed(paths))
+
+    def worker():
+        while True:
+            with lock:
+                if not todo:
+                    return
+                p = todo.pop()
+            with open(p, "rb") as f:
+                rec = record(call(pb.DetectRequest(image=f.read(), model=model)))
+            with lock:
+                out[p] = rec
+
+    threads = [threading.Thread(target=worker, daemon=True) for _ in range(max(1, min(callers, len(paths))))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    return out
 
 
 def main(argv=None) -> int:
@@ -147,50 +234,32 @@ def main(argv=None) -> int:
                                           ("grpc.max_send_message_length", 64 << 20)])
     call = ch.unary_unary(pb.FULL_METHOD, request_serializer=pb.DetectRequest.SerializeToString,
                           response_deserializer=pb.DetectResponse.FromString)
-
-    if a.bench:
-        data = open(a.images[0], "rb").read()
-        call(pb.DetectRequest(image=data, model=a.model))          # warm-up
-        lat, batches = [], []
-
-        def one(_):
-            t0 = time.perf_counter()
-            r = call(pb.DetectRequest(image=data, model=a.model))
-            lat.append((time.perf_counter() - t0) * 1e3)
-            batches.append(r.batch)
-
-        t0 = time.perf_counter()
-        with ThreadPoolExecutor(a.concurrency) as ex:
-            list(ex.map(one, range(a.bench)))
-        dt = time.perf_counter() - t0
-        q = np.percentile(np.array(lat), [50, 95, 99])
-        print(f"{len(lat)} imgs in {dt:.2f}s = {len(lat) / dt:,.0f} img/s   latency p50={q[0]:.1f} "
-              f"p95={q[1]:.1f} p99={q[2]:.1f} ms   avg batch={np.mean(batches):.1f}", flush=True)
+    try:
+        if a.bench:
+            with open(a.images[0], "rb") as f:
+                req = pb.DetectRequest(image=f.read(), model=a.model)
+            call(req)                                             # connection + graph warm-up
+            st = _Load(call, req, a.bench, a.concurrency).run()
+            print(f"bench {a.images[0]}: {st['requests']} requests, {a.concurrency} callers, "
+                  f"{st['seconds']:.2f} s -> {st['img_per_s']:,.0f} img/s | latency ms p50 {st['p50_ms']:.1f} "
+                  f"p95 {st['p95_ms']:.1f} p99 {st['p99_ms']:.1f} | server batch {st['mean_batch']:.1f}",
+                  flush=True)
+            return 0
+        t = time.perf_counter()
+        results = _label_all(call, a.model, a.images, a.concurrency)
+        wall = time.perf_counter() - t
+    finally:
         ch.close()
-        return 0
-
-    results = {}
-
-    def label(path):
-        r = call(pb.DetectRequest(image=open(path, "rb").read(), model=a.model))
-        results[path] = record(r)
-
-    t0 = time.perf_counter()
-    with ThreadPoolExecutor(a.concurrency) as ex:
-        list(ex.map(label, a.images))
-    dt = time.perf_counter() - t0
-    ch.close()
-    print(f"labeled {len(a.images)} images in {dt:.2f}s ({len(a.images) / dt:,.0f} img/s)", flush=True)
+    print(f"{len(results)} images -> {a.server} in {wall:.2f} s ({len(results) / wall:,.0f} img/s)", flush=True)
     if a.coco:
         doc = coco(results, {p: image_size(p) for p in results})
         with open(a.coco, "w") as f:
             json.dump(doc, f)
-        print(f"wrote {a.coco} ({len(doc['annotations'])} annotations)")
+        print(f"COCO: {a.coco}, {len(doc['images'])} images, {len(doc['annotations'])} annotations")
     if a.out:
         with open(a.out, "w") as f:
-            for p in a.images:
-                f.write(json.dumps({"image": p, **results[p]}) + "\n")
-        print(f"wrote {a.out}")
+            f.writelines(json.dumps({"image": p, **results[p]}) + "\n" for p in a.images)
+        print(f"JSONL: {a.out}, {len(a.images)} records")
     return 0
 
 

@@ -61,6 +61,8 @@ _SIGS = {
     "yolo_tensor_shape": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int)]),
     "yolo_read_tensor": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     "yolo_write_tensor": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    "yolo_read_tensor_slots": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "yolo_write_tensor_slots": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "yolo_run_op": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
     "yolo_run_post": (C.c_int, [C.c_void_p, C.c_int]),
     "yolo_op_config": (C.c_int, [C.c_void_p, C.c_int]),
@@ -75,6 +77,7 @@ _SIGS = {
     "yolo_frame_launch": (C.c_int, [C.c_void_p]),
     "yolo_time_graph": (C.c_float, [C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "yolo_profile_ops": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_float)]),
+    "yolo_profile_stages": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_float)]),
     "yolo_dev_alloc": (C.c_void_p, [C.c_size_t]),
     "yolo_dev_free": (None, [C.c_void_p]),
     "yolo_host_alloc": (C.c_void_p, [C.c_size_t]),
@@ -212,6 +215,21 @@ class Engine:
         if self.lib.yolo_write_tensor(self.h, t, arr.shape[0], arr.ctypes.data) != 0:
             raise RuntimeError("yolo_write_tensor failed")
 
+    def read_slots(self, t: int, first: int, n: int = 1) -> np.ndarray:
+        """Tensor t of images first .. first+n-1 as [n, H, W, C] fp16."""
+        H, W, Cc = self.tensor_shape(t)
+        out = np.empty((n, H, W, Cc), np.float16)
+        if self.lib.yolo_read_tensor_slots(self.h, t, first, n, out.ctypes.data) != 0:
+            raise RuntimeError("yolo_read_tensor_slots failed")
+        return out
+
+    def write_slots(self, t: int, first: int, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr, dtype=np.float16)
+        H, W, Cc = self.tensor_shape(t)
+        assert arr.shape[1:] == (H, W, Cc), (arr.shape, (H, W, Cc))
+        if self.lib.yolo_write_tensor_slots(self.h, t, first, arr.shape[0], arr.ctypes.data) != 0:
+            raise RuntimeError("yolo_write_tensor_slots failed")
+
     def run_op(self, k: int, B: int = 1):
         if self.lib.yolo_run_op(self.h, k, B) != 0:
             raise RuntimeError(f"yolo_run_op({k}) failed")
@@ -334,6 +352,13 @@ class Engine:
         if self.lib.yolo_profile_ops(self.h, B, iters, out) != 0:
             raise RuntimeError("yolo_profile_ops failed")
         return np.array(out, np.float64)
+
+    def profile_stages(self, iters: int) -> dict:
+        """ms of the frame graph's letterbox, decode, NMS and mask stages (stream-ordered)."""
+        out = (C.c_float * 4)()
+        if self.lib.yolo_profile_stages(self.h, iters, out) != 0:
+            raise RuntimeError("yolo_profile_stages failed")
+        return dict(letterbox=out[0], decode=out[1], nms=out[2], masks=out[3])
 
     def upload(self, buf: DeviceBuffer, arr: np.ndarray):
         arr = np.ascontiguousarray(arr)
