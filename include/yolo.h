@@ -170,6 +170,29 @@ void yolo_host_free(void* p);
 int yolo_copy_h2d(void* h, void* dst, const void* src, size_t bytes);
 int yolo_copy_d2h(void* h, void* dst, const void* src, size_t bytes);
 
+/* Decode + NMS of caller-provided detect heads that allocates nothing.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops that forbid hipMalloc) and have their own network output.  It is
+ * the handle-free form of a detect handle's DECODE ops + yolo_run_post, with the same kernels
+ * and results: box views hold 64 DFL bins, cls views ceil8(nc) logits (pad channels
+ * ignored), NHWC fp16 with a row stride and first channel in halves (multiples of 8,
+ * 16-byte aligned base).  Outputs (device memory): dets [B][300][6] letterbox-space
+ * x1 y1 x2 y2 score cls in NMS order, counts [B] kept, raw_counts [B] (may be NULL)
+ * candidates that passed conf.  Asynchronous on `stream`.  Scratch is one fixed device
+ * array per GPU (YOLO_STATIC_MAX_ANCHOR_SLOTS anchors over the batch, at most
+ * YOLO_STATIC_MAX_BATCH images; about 5.3 MB): larger inputs are refused with -1, and calls
+ * that overlap on one GPU race.  Returns 0 or -1 (message on stderr). */
+#define YOLO_STATIC_MAX_BATCH 64
+#define YOLO_STATIC_MAX_ANCHOR_SLOTS 163840
+typedef struct {
+  const void* box;                 /* [B][H][W][box_stride] fp16, bins at box_off..+64     */
+  const void* cls;                 /* [B][H][W][cls_stride] fp16, logits at cls_off..+nc   */
+  int H, W, stride;                /* grid size and stride (pixels per cell) of the level  */
+  int box_stride, box_off, cls_stride, cls_off;
+} YoloHeadLevel;
+int yolo_detect_static(const YoloHeadLevel* levels, int nlev, int B, int nc, float conf, float iou,
+                       int max_det, float* dets, int* counts, int* raw_counts, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,6 +32,7 @@ SOURCES = {
     "elementwise.hip": DEV_FLAGS,
     "attention.hip": DEV_FLAGS,
     "frame.hip": DEV_FLAGS + ["-ffp-contract=off"],
+    "noalloc.hip": DEV_FLAGS,
     "graph.cpp": HOST_FLAGS,
     "engine.cpp": HOST_FLAGS,
 }

@@ -34,6 +34,12 @@ class YoloObbDet(C.Structure):
                 ("angle", C.c_float), ("score", C.c_float), ("cls", C.c_int)]
 
 
+class YoloHeadLevel(C.Structure):
+    _fields_ = [("box", C.c_void_p), ("cls", C.c_void_p), ("H", C.c_int), ("W", C.c_int),
+                ("stride", C.c_int), ("box_stride", C.c_int), ("box_off", C.c_int),
+                ("cls_stride", C.c_int), ("cls_off", C.c_int)]
+
+
 _SIGS = {
     "yolo_create": (C.c_void_p, [C.c_char_p, C.c_int]),
     "yolo_task": (C.c_int, [C.c_void_p]),
@@ -84,6 +90,8 @@ _SIGS = {
     "yolo_host_free": (None, [C.c_void_p]),
     "yolo_copy_h2d": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
     "yolo_copy_d2h": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+    "yolo_detect_static": (C.c_int, [C.POINTER(YoloHeadLevel), C.c_int, C.c_int, C.c_int, C.c_float,
+                                     C.c_float, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
 }
 
 _lib = None
@@ -365,6 +373,17 @@ class Engine:
         assert arr.nbytes <= buf.nbytes
         if self.lib.yolo_copy_h2d(self.h, buf.ptr, arr.ctypes.data, arr.nbytes) != 0:
             raise RuntimeError("yolo_copy_h2d failed")
+
+
+def detect_static(levels, B: int, nc: int, conf: float, iou: float, max_det: int, dets_ptr: int,
+                  counts_ptr: int, raw_ptr: int | None = None, stream: int | None = None) -> int:
+    """yolo_detect_static: decode + NMS of device head tensors with no allocation.
+    `levels`: (box_ptr, cls_ptr, H, W, stride, box_stride, box_off, cls_stride, cls_off) per
+    level.  Returns the entry point's status (0 or -1)."""
+    lib = load()
+    arr = (YoloHeadLevel * len(levels))(*[YoloHeadLevel(*lv) for lv in levels])
+    return lib.yolo_detect_static(arr, len(levels), B, nc, conf, iou, max_det, dets_ptr, counts_ptr,
+                                  raw_ptr, stream)
 
 
 def graph_check(model_dir: str) -> tuple[int, str]:
