@@ -83,6 +83,8 @@ int yolo_get_mask(void* h, int slot, int det, unsigned char* out);
 #define YOLO_DAGGRAPH 16   /* graphs are a dependency DAG of per-op kernel nodes (independent
                               branches may run concurrently) instead of one single-stream
                               capture; slower for batch 1 on ROCm 7.2                      */
+#define YOLO_NOGROUP 32    /* one op per launch: no grouped launches of independent convs /
+                              copies (results are identical either way)                    */
 
 /* Error-returning create: NULL on failure with a message in err (if non-NULL). */
 void* yolo_create_ex(const char* model_dir, int max_batch, int flags, char* err, int errlen);

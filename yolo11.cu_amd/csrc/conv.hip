@@ -111,11 +111,27 @@ __device__ __forceinline__ void static_for(F&& f) {
 // is rounded to fp16 next, and the divide's fix-up sequence is most of the epilogue's VALU.
 __device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
+// One launch computes up to GEMM_GROUP independent convs of one tile configuration and K mode
+// (the host groups ops that no dependency orders, e.g. the three levels of a detection head):
+// problem j owns blocks [blk0_j, blk0_{j+1}).  Every problem is computed exactly as a launch of
+// it alone would compute it, so grouping never changes a result.  Split-K is single-problem.
 template <int BM, int BN, int WM, int WN, int BK, int NS, int KM>
-__global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
-    View x, View y, View r, const f16* __restrict__ w, const float* __restrict__ bias,
-    int ksz, int cs, int cp, int act, int M, int N, int Ktot, int mtiles, int ntiles,
-    int xbytes, int dp, int splits, int spl, float* __restrict__ ws, int* __restrict__ cnt) {
+__global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(const GemmLaunch L) {
+  int pj = 0;
+#pragma unroll
+  for (int q = 1; q < GEMM_GROUP; q++)
+    if (q < L.n && (int)blockIdx.x >= L.p[q].blk0) pj = q;
+  pj = __builtin_amdgcn_readfirstlane(pj);
+  const GemmProblem& P = L.p[pj];
+  const View x = P.x, y = P.y, r = P.r;
+  const f16* __restrict__ w = P.w;
+  const float* __restrict__ bias = P.bias;
+  const int ksz = P.ksz, cs = P.cs, cp = P.cp, act = P.act, M = P.M, N = P.N, Ktot = P.Ktot;
+  const int mtiles = P.mtiles, ntiles = P.ntiles, xbytes = P.xbytes;
+  const int bid = (int)blockIdx.x - P.blk0;
+  const int dp = L.n > 1 ? mtiles * ntiles : L.dp, splits = L.splits, spl = L.spl;
+  float* __restrict__ ws = L.ws;
+  int* __restrict__ cnt = L.cnt;
   constexpr int NW = WM * WN, NT = 64 * NW;
   constexpr int TM = BM / WM, TN = BN / WN;  // wave tile: pixels x channels
   constexpr int FM = TM / 16, FN = TN / 16;
@@ -142,13 +158,13 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(
   // last wave to the split tail, so it fills the chip instead of running part-empty.
   const int nblk = mtiles * ntiles;
   const int rem = nblk - dp;
-  const bool tail = (int)blockIdx.x >= dp;
+  const bool tail = bid >= dp;
   int split = 0, tsl = 0, id;
   if (!tail) {
-    id = blockIdx.x;
+    id = bid;
     if (dp >= 2 * NUM_XCD && dp % NUM_XCD == 0) id = (id % NUM_XCD) * (dp / NUM_XCD) + id / NUM_XCD;
   } else {
-    const int q = blockIdx.x - dp;
+    const int q = bid - dp;
     split = q / rem;
     tsl = q - split * rem;
     if (rem >= 2 * NUM_XCD && rem % NUM_XCD == 0) tsl = (tsl % NUM_XCD) * (rem / NUM_XCD) + tsl / NUM_XCD;
@@ -634,21 +650,23 @@ static int tileSlotsOf(int km) {
 }
 
 template <int BM, int BN, int WM, int WN, int BK, int NS>
-static void launchTile(int km, const View& x, const View& y, const View& r, const f16* w,
-                       const float* bias, int k, int s, int p, int act, int M, int N, int Ktot,
-                       int xbytes, int dp, int splits, float* ws, int* cnt, hipStream_t st) {
-  const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
-  const int spl = splitStages(Ktot, BK, splits);
-  const int grid = dp + (mt * nt - dp) * splits;
+static void launchTile(int km, const GemmLaunch& L, int grid, hipStream_t st) {
   if (km == KM_ONE)
-    k_conv_gemm<BM, BN, WM, WN, BK, NS, KM_ONE><<<grid, 64 * WM * WN, 0, st>>>(
-        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, dp, splits, spl, ws, cnt);
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, KM_ONE><<<grid, 64 * WM * WN, 0, st>>>(L);
   else if (km == KM_UNI)
-    k_conv_gemm<BM, BN, WM, WN, BK, NS, KM_UNI><<<grid, 64 * WM * WN, 0, st>>>(
-        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, dp, splits, spl, ws, cnt);
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, KM_UNI><<<grid, 64 * WM * WN, 0, st>>>(L);
   else
-    k_conv_gemm<BM, BN, WM, WN, BK, NS, KM_GEN><<<grid, 64 * WM * WN, 0, st>>>(
-        x, y, r, w, bias, k, s, p, act, M, N, Ktot, mt, nt, xbytes, dp, splits, spl, ws, cnt);
+    k_conv_gemm<BM, BN, WM, WN, BK, NS, KM_GEN><<<grid, 64 * WM * WN, 0, st>>>(L);
+}
+
+static void launchCfg(int cfg, int km, const GemmLaunch& L, int grid, hipStream_t st) {
+  switch (cfg) {
+#define X(i, bm, bn, wm, wn, bk, ns) \
+    case i: launchTile<bm, bn, wm, wn, bk, ns>(km, L, grid, st); break;
+    YOLO_TILES(X)
+#undef X
+    default: break;
+  }
 }
 
 int convKMode(int cfg, int k, int s, int p, int Cin) {
@@ -724,24 +742,68 @@ int numTiles(int cfg, int M, int N) {
   return ((M + tc.BM - 1) / tc.BM) * ((N + tc.BN - 1) / tc.BN);
 }
 
+static GemmProblem gemmProblem(int cfg, const ConvJob& j, int Bn, int blk0) {
+  const TileCfg& tc = kTiles[cfg];
+  GemmProblem P;
+  P.x = j.x;
+  P.y = j.y;
+  P.r = j.res ? *j.res : View{nullptr, 0, 0, 0, 0, 0};
+  P.w = j.w;
+  P.bias = j.bias;
+  P.ksz = j.k;
+  P.cs = j.s;
+  P.cp = j.p;
+  P.act = j.act;
+  P.M = Bn * j.y.H * j.y.W;
+  P.N = j.y.C;
+  P.Ktot = j.k * j.k * j.x.C;
+  P.mtiles = (P.M + tc.BM - 1) / tc.BM;
+  P.ntiles = (P.N + tc.BN - 1) / tc.BN;
+  P.xbytes = (int)((long)Bn * j.x.H * j.x.W * j.x.s * 2);
+  P.blk0 = blk0;
+  return P;
+}
+
 void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
                     const float* bias, int k, int s, int p, int act, int Bn, int splits,
                     float* ws, int* cnt, hipStream_t st) {
   const int M = Bn * y.H * y.W, N = y.C, Ktot = k * k * x.C;
-  const int xbytes = (int)((long)Bn * x.H * x.W * x.s * 2);
-  View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
   if (cfg < 0 || cfg >= kNumTiles) cfg = heuristicTile(M, N, Ktot);
   const int km = convKMode(cfg, k, s, p, x.C);
   if (!ws || !cnt || !splitOk(cfg, Ktot, splits)) splits = 1;
   int dp, S;
   splitPlan(cfg, km, numTiles(cfg, M, N), splits, &dp, &S);
-  switch (cfg) {
-#define X(i, bm, bn, wm, wn, bk, ns) \
-    case i: launchTile<bm, bn, wm, wn, bk, ns>(km, x, y, r, w, bias, k, s, p, act, M, N, Ktot, xbytes, dp, S, ws, cnt, st); break;
-    YOLO_TILES(X)
-#undef X
-    default: break;
+  GemmLaunch L{};
+  L.p[0] = gemmProblem(cfg, ConvJob{x, y, res, w, bias, k, s, p, act}, Bn, 0);
+  L.n = 1;
+  L.dp = dp;
+  L.splits = S;
+  L.spl = splitStages(Ktot, kTiles[cfg].BK, S);
+  L.ws = ws;
+  L.cnt = cnt;
+  launchCfg(cfg, km, L, dp + (L.p[0].mtiles * L.p[0].ntiles - dp) * S, st);
+}
+
+bool convGroupOk(int cfg, const ConvJob* jobs, int n) {
+  if (cfg < 0 || cfg >= kNumTiles || n < 1 || n > GEMM_GROUP) return false;
+  const int km = convKMode(cfg, jobs[0].k, jobs[0].s, jobs[0].p, jobs[0].x.C);
+  for (int i = 0; i < n; i++)
+    if (convKMode(cfg, jobs[i].k, jobs[i].s, jobs[i].p, jobs[i].x.C) != km) return false;
+  return true;
+}
+
+void launchConvGemmGroup(int cfg, const ConvJob* jobs, int n, int Bn, hipStream_t st) {
+  GemmLaunch L{};
+  int blocks = 0;
+  for (int i = 0; i < n; i++) {
+    L.p[i] = gemmProblem(cfg, jobs[i], Bn, blocks);
+    blocks += L.p[i].mtiles * L.p[i].ntiles;
   }
+  L.n = n;
+  L.dp = 0;
+  L.splits = 1;
+  L.spl = 1;
+  launchCfg(cfg, convKMode(cfg, jobs[0].k, jobs[0].s, jobs[0].p, jobs[0].x.C), L, blocks, st);
 }
 
 // ------------------------------------------------------------------ first conv (Cin = 3)
@@ -1127,10 +1189,33 @@ void launchConvHalo(const View& x, const View& y, const View* res, const f16* w,
 // multiply-add per tap (an out-of-image tap contributes fma(0, w, a) = a), so whichever
 // kernel a launch size selects, a pixel's value is the same bit for bit: an image's result
 // does not depend on the batch it runs in.
-__global__ __launch_bounds__(256) void k_dwconv(View x, View y, View r, const f16* __restrict__ w,
-                                                const float* __restrict__ bias, int ksz, int cs,
-                                                int cp, int act, int total) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+// Problem of a depthwise launch: up to DW_GROUP independent convs per launch, problem j
+// owning the blocks from blk0 (the same grouping as the GEMM launches).
+struct DwProblem {
+  View x, y, r;
+  const f16* w;
+  const float* bias;
+  int ksz, cs, cp, act, total, blk0;
+};
+struct DwLaunch {
+  DwProblem p[DW_GROUP];
+  int n;
+};
+__device__ __forceinline__ const DwProblem& dwProblem(const DwLaunch& L) {
+  int pj = 0;
+#pragma unroll
+  for (int q = 1; q < DW_GROUP; q++)
+    if (q < L.n && (int)blockIdx.x >= L.p[q].blk0) pj = q;
+  return L.p[__builtin_amdgcn_readfirstlane(pj)];
+}
+
+__global__ __launch_bounds__(256) void k_dwconv(const DwLaunch L) {
+  const DwProblem& P = dwProblem(L);
+  const View x = P.x, y = P.y, r = P.r;
+  const f16* __restrict__ w = P.w;
+  const float* __restrict__ bias = P.bias;
+  const int ksz = P.ksz, cs = P.cs, cp = P.cp, act = P.act, total = P.total;
+  const int idx = ((int)blockIdx.x - P.blk0) * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   const int cg = y.C >> 3;
   const int g = idx % cg, m = idx / cg;
@@ -1191,10 +1276,13 @@ __global__ __launch_bounds__(256) void k_dwconv(View x, View y, View r, const f1
 // clamped address and are zeroed by a select, so every load of a row is in flight together.
 constexpr int DWPX = 4;
 template <int CS>   // stride 1 or 2
-__global__ __launch_bounds__(256) void k_dwconv3x4(View x, View y, View r, const f16* __restrict__ w,
-                                                      const float* __restrict__ bias, int cp, int act,
-                                                      int total) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void k_dwconv3x4(const DwLaunch L) {
+  const DwProblem& P = dwProblem(L);
+  const View x = P.x, y = P.y, r = P.r;
+  const f16* __restrict__ w = P.w;
+  const float* __restrict__ bias = P.bias;
+  const int cp = P.cp, act = P.act, total = P.total;
+  const int idx = ((int)blockIdx.x - P.blk0) * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   const int cg = y.C >> 3, xq = (y.W + DWPX - 1) / DWPX;
   const int g = idx % cg;
@@ -1257,21 +1345,47 @@ __global__ __launch_bounds__(256) void k_dwconv3x4(View x, View y, View r, const
   }
 }
 
+// The multi-pixel kernel once a launch has work for several waves of blocks on every CU (below
+// that, one pixel per thread keeps more threads, which hides latency better).  Both kernels
+// give the same values, so the choice is free per launch.
+static bool dwMulti(const ConvJob& j, int Bn) {
+  return j.k == 3 && (j.s == 1 || j.s == 2) && Bn * j.y.H * j.y.W * (j.y.C / 8) >= 256 * 256 * 8;
+}
+
+void launchDwConvGroup(const ConvJob* jobs, int n, int Bn, hipStream_t st) {
+  bool multi = true;
+  for (int i = 0; i < n; i++) multi = multi && dwMulti(jobs[i], Bn) && jobs[i].s == jobs[0].s;
+  DwLaunch L{};
+  int blocks = 0;
+  for (int i = 0; i < n; i++) {
+    const ConvJob& j = jobs[i];
+    DwProblem& P = L.p[i];
+    P.x = j.x;
+    P.y = j.y;
+    P.r = j.res ? *j.res : View{nullptr, 0, 0, 0, 0, 0};
+    P.w = j.w;
+    P.bias = j.bias;
+    P.ksz = j.k;
+    P.cs = j.s;
+    P.cp = j.p;
+    P.act = j.act;
+    P.total = multi ? Bn * j.y.H * ((j.y.W + DWPX - 1) / DWPX) * (j.y.C / 8) : Bn * j.y.H * j.y.W * (j.y.C / 8);
+    P.blk0 = blocks;
+    blocks += (P.total + 255) / 256;
+  }
+  L.n = n;
+  if (!multi)
+    k_dwconv<<<blocks, 256, 0, st>>>(L);
+  else if (jobs[0].s == 1)
+    k_dwconv3x4<1><<<blocks, 256, 0, st>>>(L);
+  else
+    k_dwconv3x4<2><<<blocks, 256, 0, st>>>(L);
+}
+
 void launchDwConv(const View& x, const View& y, const View* res, const f16* wt_kkc,
                   const float* bias, int k, int s, int p, int act, int Bn, hipStream_t st) {
-  const int total = Bn * y.H * y.W * (y.C / 8);
-  View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
-  // the multi-pixel kernel once a launch has work for several waves of blocks on every CU
-  // (below that, one pixel per thread keeps more threads, which hides latency better)
-  if (k == 3 && (s == 1 || s == 2) && total >= 256 * 256 * 8) {
-    const int total4 = Bn * y.H * ((y.W + DWPX - 1) / DWPX) * (y.C / 8);
-    if (s == 1)
-      k_dwconv3x4<1><<<(total4 + 255) / 256, 256, 0, st>>>(x, y, r, wt_kkc, bias, p, act, total4);
-    else
-      k_dwconv3x4<2><<<(total4 + 255) / 256, 256, 0, st>>>(x, y, r, wt_kkc, bias, p, act, total4);
-    return;
-  }
-  k_dwconv<<<(total + 255) / 256, 256, 0, st>>>(x, y, r, wt_kkc, bias, k, s, p, act, total);
+  const ConvJob j{x, y, res, wt_kkc, bias, k, s, p, act};
+  launchDwConvGroup(&j, 1, Bn, st);
 }
 
 }  // namespace yolo

@@ -133,9 +133,22 @@ __global__ __launch_bounds__(256) void k_upsample2(View x, View y, int total) {
   st8(y, m, g * 8, ld8(x, (size_t)(img * x.H + (oy >> 1)) * x.W + (ox >> 1), g * 8));
 }
 
-__global__ __launch_bounds__(256) void k_copyc(View x, View y, int total) {
-  int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
+// Up to COPY_GROUP independent channel copies per launch (the per-head V gathers of an
+// attention block): copy j owns the blocks from blk0[j].
+struct CopyLaunch {
+  View x[COPY_GROUP], y[COPY_GROUP];
+  int total[COPY_GROUP], blk0[COPY_GROUP];
+  int n;
+};
+__global__ __launch_bounds__(256) void k_copyc(const CopyLaunch L) {
+  int pj = 0;
+#pragma unroll
+  for (int q = 1; q < COPY_GROUP; q++)
+    if (q < L.n && (int)blockIdx.x >= L.blk0[q]) pj = q;
+  pj = __builtin_amdgcn_readfirstlane(pj);
+  const View x = L.x[pj], y = L.y[pj];
+  int idx = ((int)blockIdx.x - L.blk0[pj]) * blockDim.x + threadIdx.x;
+  if (idx >= L.total[pj]) return;
   int cg = y.C >> 3, g = idx % cg;
   size_t m = idx / cg;
   st8(y, m, g * 8, ld8(x, m, g * 8));
@@ -172,10 +185,20 @@ void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st) {
   int total = Bn * y.H * y.W * (y.C / 8);
   k_upsample2<<<grid(total), 256, 0, st>>>(x, y, total);
 }
-void launchCopyC(const View& x, const View& y, int Bn, hipStream_t st) {
-  int total = Bn * y.H * y.W * (y.C / 8);
-  k_copyc<<<grid(total), 256, 0, st>>>(x, y, total);
+void launchCopyCGroup(const View* xs, const View* ys, int n, int Bn, hipStream_t st) {
+  CopyLaunch L{};
+  int blocks = 0;
+  for (int i = 0; i < n; i++) {
+    L.x[i] = xs[i];
+    L.y[i] = ys[i];
+    L.total[i] = Bn * ys[i].H * ys[i].W * (ys[i].C / 8);
+    L.blk0[i] = blocks;
+    blocks += grid(L.total[i]);
+  }
+  L.n = n;
+  k_copyc<<<blocks, 256, 0, st>>>(L);
 }
+void launchCopyC(const View& x, const View& y, int Bn, hipStream_t st) { launchCopyCGroup(&x, &y, 1, Bn, st); }
 void launchPS2(const View& x, const View& y, int Bn, hipStream_t st) {
   int total = Bn * y.H * y.W * (y.C / 8);
   k_ps2<<<grid(total), 256, 0, st>>>(x, y, total);

@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <deque>
 #include <map>
 #include <stdexcept>
 #include <string>
@@ -466,6 +467,193 @@ struct Engine {
     }
   }
 
+  // ---------------------------------------------------------------- launch units
+  // forward() runs the ops as a list of units: one op, or a group of independent ops of one
+  // kernel kind launched together (GEMM convs sharing a tile config and K mode, depthwise
+  // convs, channel copies).  A group's launch computes every member exactly as a launch of
+  // it alone does (grouped kernels only partition their blocks), so grouping changes launch
+  // counts, never results.
+  enum { GK_NONE = 0, GK_GEMM, GK_DW, GK_COPY };
+  struct Unit {
+    std::vector<int> ops;
+    int kind = GK_NONE;
+  };
+  std::vector<Unit> units;
+  int groupKind(int k) const {
+    const OpDesc& op = ops[k];
+    if (op.chain < 0) return GK_NONE;
+    if (op.kind == COPYC) return GK_COPY;
+    if (op.kind != CONV) return GK_NONE;
+    if (op.g > 1) return GK_DW;
+    if (op.Cin == 3 || op.cfg == CFG_HALO) return GK_NONE;
+    return GK_GEMM;
+  }
+  ConvJob convJob(int k) {
+    const OpDesc& op = ops[k];
+    jobRes.push_back(op.b >= 0 ? view(op.b) : View{});
+    return ConvJob{view(op.a), view(op.out), op.b >= 0 ? &jobRes.back() : nullptr, weights + op.woff,
+                   bias + op.boff, op.k, op.s, op.p, op.act};
+  }
+  std::deque<View> jobRes;   // residual views the jobs of one launch point at
+  void launchGroup(int kind, const std::vector<int>& m, int cfg, int Bn, hipStream_t s) {
+    jobRes.clear();
+    if (kind == GK_COPY) {
+      View xs[COPY_GROUP], ys[COPY_GROUP];
+      for (size_t i = 0; i < m.size(); i++) { xs[i] = view(ops[m[i]].a); ys[i] = view(ops[m[i]].out); }
+      launchCopyCGroup(xs, ys, (int)m.size(), Bn, s);
+      return;
+    }
+    ConvJob jobs[GEMM_GROUP > DW_GROUP ? GEMM_GROUP : DW_GROUP];
+    for (size_t i = 0; i < m.size(); i++) jobs[i] = convJob(m[i]);
+    if (kind == GK_DW)
+      launchDwConvGroup(jobs, (int)m.size(), Bn, s);
+    else
+      launchConvGemmGroup(cfg, jobs, (int)m.size(), Bn, s);
+  }
+  void runUnit(const Unit& u, int Bn, hipStream_t s = nullptr) {
+    if (!s) s = st;
+    bool together = u.ops.size() > 1;
+    if (together && u.kind == GK_GEMM)   // (per-op overrides since planning launch one by one)
+      for (int i : u.ops) together = together && ops[i].cfg == ops[u.ops[0]].cfg && ops[i].split == 1;
+    if (!together) {
+      for (int i : u.ops)
+        if (ops[i].chain >= 0) runOp(i, Bn, s);
+      return;
+    }
+    launchGroup(u.kind, u.ops, ops[u.ops[0]].cfg, Bn, s);
+  }
+  static int groupMax(int kind) { return kind == GK_GEMM ? GEMM_GROUP : kind == GK_DW ? DW_GROUP : COPY_GROUP; }
+
+  // Groups ops that no dependency orders, in two passes over the unit list (each unit is
+  // atomic: its accesses are its members' accesses, its place its first member's place).
+  // A single-op unit takes later single-op units of its kind (within 40 units) that conflict
+  // with neither the group nor any unit they would move ahead of.  Pass 1 only takes ops of
+  // the same shape class (GEMM: same kernel size, stride and output width -- the levels of a
+  // detection head, the twin 1x1 convs of a C3k block); pass 2 any GEMM conv of the same K
+  // mode.  Depthwise convs and copies always group; a GEMM group must find one tile config
+  // that runs it faster than its members' own tuned configs launched one after another
+  // (timed at the max batch like the autotuner; the full candidate set first, then shorter
+  // prefixes).  Without tuning GEMM ops stay single.
+  bool unitConflict(const Unit& a, const Unit& b) const {
+    for (int i : a.ops)
+      for (int j : b.ops)
+        if (conflict(i, j)) return true;
+    return false;
+  }
+  bool sameClass(int i, int j) const {
+    const OpDesc &a = ops[i], &b = ops[j];
+    return a.k == b.k && a.s == b.s && a.Cout == b.Cout && a.act == b.act;
+  }
+  void mergePass(bool strict, bool tune, hipEvent_t e0, hipEvent_t e1) {
+    auto timeIt = [&](auto&& launch) {
+      for (int r = 0; r < 2; r++) launch();
+      float t[7];
+      for (int r = 0; r < 7; r++) {
+        HCK(hipEventRecord(e0, st));
+        launch();
+        HCK(hipEventRecord(e1, st));
+        HCK(hipEventSynchronize(e1));
+        HCK(hipEventElapsedTime(&t[r], e0, e1));
+      }
+      std::sort(t, t + 7);
+      return t[3];
+    };
+    std::vector<Unit> out;
+    std::vector<char> taken(units.size(), 0);
+    for (size_t a = 0; a < units.size(); a++) {
+      if (taken[a]) continue;
+      taken[a] = 1;
+      Unit u = units[a];
+      const int kind = u.ops.size() == 1 ? groupKind(u.ops[0]) : GK_NONE;
+      if (kind == GK_NONE || (kind == GK_GEMM && !tune) || (kind != GK_GEMM && !strict)) {
+        out.push_back(u);
+        continue;
+      }
+      const int k = u.ops[0];
+      std::vector<size_t> cand;
+      for (size_t b = a + 1; b < units.size() && b <= a + 40 && (int)cand.size() + 1 < groupMax(kind); b++) {
+        if (taken[b] || units[b].ops.size() != 1) continue;
+        const int j = units[b].ops[0];
+        if (groupKind(j) != kind || (strict && kind == GK_GEMM && !sameClass(k, j))) continue;
+        bool ok = !unitConflict(u, units[b]);
+        for (size_t c : cand) ok = ok && !unitConflict(units[c], units[b]);
+        for (size_t c = a + 1; c < b && ok; c++)
+          if (!taken[c] && std::find(cand.begin(), cand.end(), c) == cand.end() && unitConflict(units[c], units[b]))
+            ok = false;
+        if (ok) cand.push_back(b);
+      }
+      if (kind == GK_GEMM) {
+        // the longest prefix of the candidates that one tile config runs faster together
+        size_t keep = 0;
+        int keepCfg = -1;
+        for (size_t m = cand.size(); m >= 1 && keepCfg < 0; m--) {
+          std::vector<int> grp{k};
+          for (size_t i = 0; i < m; i++) grp.push_back(units[cand[i]].ops[0]);
+          const float sep = timeIt([&] { for (int i : grp) runOp(i, B); });
+          jobRes.clear();
+          std::vector<ConvJob> jobs;
+          for (int i : grp) jobs.push_back(convJob(i));
+          float best = sep;
+          for (int cfg = 0; cfg < numTileConfigs(); cfg++) {
+            bool fits = convGroupOk(cfg, jobs.data(), (int)jobs.size());
+            for (int i : grp) {
+              const View y = view(ops[i].out);
+              fits = fits && tileOk(cfg, B * y.H * y.W, ops[i].Cout, ops[i].k * ops[i].k * ops[i].Cin);
+            }
+            if (!fits) continue;
+            const float t = timeIt([&] { launchConvGemmGroup(cfg, jobs.data(), (int)jobs.size(), B, st); });
+            if (t < best) { best = t; keepCfg = cfg; keep = m; }
+          }
+        }
+        cand.resize(keep);
+        if (keepCfg >= 0) {
+          ops[k].cfg = keepCfg;
+          ops[k].split = 1;
+          for (size_t c : cand) {
+            OpDesc& o = ops[units[c].ops[0]];
+            o.cfg = keepCfg;
+            o.split = 1;
+          }
+        }
+      }
+      for (size_t c : cand) {
+        taken[c] = 1;
+        u.ops.push_back(units[c].ops[0]);
+      }
+      if (u.ops.size() > 1) u.kind = kind;
+      out.push_back(u);
+    }
+    units = out;
+  }
+  void planUnits(bool tune) {
+    computeAccesses();
+    units.clear();
+    for (int k = 0; k < (int)ops.size(); k++) units.push_back({{k}, GK_NONE});
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (tune) {
+      HCK(hipEventCreate(&e0));
+      HCK(hipEventCreate(&e1));
+    }
+    mergePass(true, tune, e0, e1);
+    mergePass(false, tune, e0, e1);
+    for (Unit& u : units)
+      for (int i : u.ops) ops[i].wsOff = ops[i].cntOff = -1;
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    HCK(hipGetLastError());
+    if (getenv("YOLO_PRINT_UNITS")) {   // the plan, for inspection: grouped units only
+      int launches = 0;
+      for (const Unit& u : units) launches += u.ops.size() > 1 || ops[u.ops[0]].chain >= 0;
+      fprintf(stderr, "yolo: %zu ops in %d launches (B=%d)\n", ops.size(), launches, B);
+      for (const Unit& u : units)
+        if (u.ops.size() > 1) {
+          fprintf(stderr, "  group kind %d cfg %d:", u.kind, ops[u.ops[0]].cfg);
+          for (int i : u.ops) fprintf(stderr, " %d", i);
+          fprintf(stderr, "\n");
+        }
+    }
+  }
+
   void post(int Bn) {
     if (g.cls) {   // no decode/NMS: the probabilities go to pinned memory (engine/engine.cu:1458)
       HCK(hipMemcpyAsync(h_probs, bufp[g.tens[g.probsTen].buf], (size_t)Bn * g.nc * sizeof(f16),
@@ -492,8 +680,7 @@ struct Engine {
   // per-op child graphs built in capture() instead.
   void forward(int Bn, bool branches = true) {
     if (side.empty() || !branches) {
-      for (size_t k = 0; k < ops.size(); k++)
-        if (ops[k].chain >= 0) runOp((int)k, Bn);
+      for (const Unit& u : units) runUnit(u, Bn);
     } else {
       auto strm = [&](int s) { return s == 0 ? st : side[s - 1]; };
       HCK(hipEventRecord(forkEv, st));
@@ -833,6 +1020,13 @@ Engine* create(const char* dir, int maxB, int flags) {
       e->createStreams();
     }
     if (!(flags & YOLO_NOTUNE)) e->autotune();
+    // grouped launches for the single-stream plan (the DAG and side-stream plans keep one op
+    // per launch); the group tuning may move ops off split-K, so splits are assigned after it
+    e->planUnits(!(flags & (YOLO_NOTUNE | YOLO_DAGGRAPH | YOLO_BRANCHES | YOLO_NOGROUP)));
+    if (flags & (YOLO_DAGGRAPH | YOLO_BRANCHES | YOLO_NOGROUP)) {
+      e->units.clear();
+      for (int k = 0; k < (int)e->ops.size(); k++) e->units.push_back({{k}, 0});
+    }
     e->assignSplits();
     if (flags & YOLO_DAGGRAPH) e->planDag();
     if (!(flags & YOLO_NOGRAPH)) e->buildGraphs();

@@ -95,6 +95,29 @@ const TileCfg& tileConfig(int cfg);
 
 // ------------------------------------------------------------------ launchers
 // conv.hip
+// One conv as the GEMM launchers take it.
+struct ConvJob {
+  View x, y;
+  const View* res;
+  const f16* w;
+  const float* bias;
+  int k, s, p, act;
+};
+// Kernel arguments of one implicit-GEMM launch: up to GEMM_GROUP independent convs (problem j
+// owns the blocks from blk0), or one conv with split-K (dp, splits, spl, ws, cnt).
+constexpr int GEMM_GROUP = 4;
+struct GemmProblem {
+  View x, y, r;
+  const f16* w;
+  const float* bias;
+  int ksz, cs, cp, act, M, N, Ktot, mtiles, ntiles, xbytes, blk0;
+};
+struct GemmLaunch {
+  GemmProblem p[GEMM_GROUP];
+  int n, dp, splits, spl;
+  float* ws;
+  int* cnt;
+};
 // Split-K: `splits` > 1 partitions the K stages of every output tile over that many blocks;
 // `splits` < -1 does so only for the tiles left over after the last whole wave of the chip
 // (tail split, |splits| ways).  `ws` holds |splits| x splitTiles x BM x BN fp32 partials
@@ -117,6 +140,10 @@ size_t splitWorkspaceBytes(int cfg, int km, int M, int N, int splits);
 void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
                     const float* bias, int k, int s, int p, int act, int Bn, int splits,
                     float* ws, int* cnt, hipStream_t st);
+// n independent convs in one launch under tile config `cfg` (all in the same K mode, which
+// convGroupOk checks), no split-K; each result equals a launch of that conv alone.
+bool convGroupOk(int cfg, const ConvJob* jobs, int n);
+void launchConvGemmGroup(int cfg, const ConvJob* jobs, int n, int Bn, hipStream_t st);
 // 3x3 stride-1 convs with Cin <= 64 and Cout <= 64 (Cout % 16 == 0): the LDS-halo kernel, an
 // autotune candidate selected by the op config CFG_HALO.
 constexpr int CFG_HALO = 1000;
@@ -127,6 +154,9 @@ void launchConvFirst(const View& x, const View& y, const f16* w, const float* bi
                      int act, int Bn, hipStream_t st);
 void launchDwConv(const View& x, const View& y, const View* res, const f16* wt_kkc,
                   const float* bias, int k, int s, int p, int act, int Bn, hipStream_t st);
+// n independent depthwise convs in one launch (k_dwconv / k_dwconv3x4 both give the same values)
+constexpr int DW_GROUP = 4;
+void launchDwConvGroup(const ConvJob* jobs, int n, int Bn, hipStream_t st);
 int heuristicTile(int M, int N, int K);
 bool tileOk(int cfg, int M, int N, int K);
 bool convGemmFits(long inBytes, long wBytes);
@@ -140,6 +170,9 @@ void launchSppfPool(const View& x, const View& y1, const View& y2, const View& y
                     hipStream_t st);
 void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st);
 void launchCopyC(const View& x, const View& y, int Bn, hipStream_t st);
+// n independent channel copies in one launch
+constexpr int COPY_GROUP = 8;
+void launchCopyCGroup(const View* xs, const View* ys, int n, int Bn, hipStream_t st);
 void launchPS2(const View& x, const View& y, int Bn, hipStream_t st);
 void launchGap(const View& x, const View& y, int Bn, hipStream_t st);
 void launchSoftmaxCh(const View& x, const View& y, int Bn, hipStream_t st);
