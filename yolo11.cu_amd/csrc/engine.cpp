@@ -645,8 +645,9 @@ struct Engine {
       int launches = 0;
       for (const Unit& u : units) launches += u.ops.size() > 1 || ops[u.ops[0]].chain >= 0;
       fprintf(stderr, "yolo: %zu ops in %d launches (B=%d)\n", ops.size(), launches, B);
+      const bool all = atoi(getenv("YOLO_PRINT_UNITS")) > 1;
       for (const Unit& u : units)
-        if (u.ops.size() > 1) {
+        if (u.ops.size() > 1 || (all && ops[u.ops[0]].chain >= 0)) {
           fprintf(stderr, "  group kind %d cfg %d:", u.kind, ops[u.ops[0]].cfg);
           for (int i : u.ops) fprintf(stderr, " %d", i);
           fprintf(stderr, "\n");
