@@ -10,8 +10,10 @@ conv MFMA util %"):
     (engine/engine.cu:1992-2031).  The same loop with the frame already in HBM is a side
     figure.
   * yolo11x detect, batch 16, sixteen 640x640 frames in HBM: whole-frame graph
-    throughput, and conv MFMA utilisation = sum(conv FLOPs) / (sum(conv time) * peak)
-    from per-op hipEvent timing.
+    throughput, and conv MFMA utilisation = sum(conv FLOPs) / (sum(conv kernel time) * peak),
+    the kernel time of each launch unit (one conv or a grouped launch, as the graph runs
+    them) from hipEvents around 5 back-to-back launches; the same ratio with stream-ordered
+    per-op events (launch gaps included) is reported beside it.
   * roofline: the implicit-GEMM conv kernel on the isolated-conv-sweep shape
     3x3 s1 256->256 @80x80, batch 32, timed with hipEvents on the
     engine stream; `traffic` = HBM bytes per launch of the tile the autotuner picked, from
@@ -290,21 +292,26 @@ def bench_x(workdir, iters, graph=True):
     for _ in range(3):
         eng.frame_run()
     ms = eng.time_graph(1, B, iters)
+    kept = [len(eng.get(s)) for s in range(B)]
     per_op = eng.profile_ops(B, max(3, iters // 4))
-    conv_f, conv_t, attn_t = 0.0, 0.0, 0.0
+    # kernel time per launch unit (grouped launches as the graph runs them), each unit run
+    # 5 times back to back so the per-launch gaps of a stream-ordered pass are excluded
+    per_unit = eng.profile_units(B, 2, 5)
+    conv_f, conv_t, conv_t_ev, attn_t = 0.0, 0.0, 0.0, 0.0
     for k in range(eng.num_ops):
         info = eng.op_info(k)
         if info["kind"] == "CONV":
             conv_f += B * conv_flops(eng, k)
-            conv_t += per_op[k] * 1e-3
+            conv_t += per_unit[k] * 1e-3
+            conv_t_ev += per_op[k] * 1e-3
         elif info["kind"] == "ATTN":
-            attn_t += per_op[k] * 1e-3
-    kept = [len(eng.get(s)) for s in range(B)]
+            attn_t += per_unit[k] * 1e-3
     for b in devs:
         b.free()
     eng.close()
     return dict(ms_per_batch=ms, img_per_s=B * 1e3 / ms, conv_tflops=conv_f / conv_t / 1e12,
                 conv_mfma_util=conv_f / conv_t / PEAK_FP16, conv_ms=conv_t * 1e3,
+                conv_mfma_util_stream_events=conv_f / conv_t_ev / PEAK_FP16, conv_ms_stream_events=conv_t_ev * 1e3,
                 attn_ms=attn_t * 1e3, stream_ops_ms=float(per_op.sum()), kept_min=min(kept),
                 kept_max=max(kept))
 

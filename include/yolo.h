@@ -158,6 +158,12 @@ float yolo_time_graph(void* h, int which, int B, int iters);
  * inside a preceding op's launch (the second and third MAXPOOL5 of a fused SPPF chain)
  * reports only its event overhead. */
 int yolo_profile_ops(void* h, int B, int iters, float* ms);
+/* Kernel time per launch unit: each unit (one op, or a group of independent ops launched
+ * together) runs `reps` times back to back between two events, so the per-launch gaps of a
+ * stream-ordered pass are not counted; ms[k] is the average per run over `iters` passes,
+ * reported on the unit's first op (0 on the other members, on decode ops and on pooled ops
+ * of a fused SPPF chain).  Activations are left in an unspecified state. */
+int yolo_profile_units(void* h, int B, int iters, int reps, float* ms);
 /* Average ms of the frame's pre/post stages over `iters` stream-ordered passes of the frame
  * set by yolo_frame_graph (frames in device memory, no H2D): ms[0] letterbox of all slots,
  * ms[1] decode (all levels, one launch), ms[2] NMS, ms[3] mask assembly (0 without a proto).

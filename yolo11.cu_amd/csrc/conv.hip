@@ -591,7 +591,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(const GemmLaunch L) 
   X(29, 64, 16, 4, 1, 128, 5)         \
   X(30, 256, 256, 4, 4, 32, 3)        \
   X(31, 256, 256, 4, 4, 64, 2)       \
-  X(32, 128, 192, 2, 2, 32, 3)
+  X(32, 128, 192, 2, 2, 32, 3)       \
+  X(33, 64, 192, 2, 2, 32, 4)        \
+  X(34, 128, 96, 2, 2, 64, 2)        \
+  X(35, 256, 96, 4, 1, 64, 2)        \
+  X(36, 64, 96, 2, 2, 64, 3)
 
 static const TileCfg kTiles[] = {
 #define X(i, bm, bn, wm, wn, bk, ns) {bm, bn, wm, wn, bk, ns},

@@ -1497,6 +1497,35 @@ int yolo_profile_ops(void* h, int B, int iters, float* ms) {
   });
 }
 
+int yolo_profile_units(void* h, int B, int iters, int reps, float* ms) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (B < 1 || B > e->B || iters < 1 || reps < 1) return -1;
+    const int n = (int)e->ops.size();
+    std::vector<double> acc(n, 0.0);
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    for (int it = 0; it < iters; it++)
+      for (const auto& u : e->units) {
+        const int k0 = u.ops[0];
+        if (yolo::isDecode(e->ops[k0].kind) || e->ops[k0].chain < 0) continue;
+        e->runUnit(u, B);   // warm: caches, clocks
+        HCK(hipEventRecord(e0, e->st));
+        for (int r = 0; r < reps; r++) e->runUnit(u, B);
+        HCK(hipEventRecord(e1, e->st));
+        HCK(hipEventSynchronize(e1));
+        float t = 0.f;
+        HCK(hipEventElapsedTime(&t, e0, e1));
+        acc[k0] += t / reps;
+      }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    for (int k = 0; k < n; k++) ms[k] = (float)(acc[k] / iters);
+    return 0;
+  });
+}
+
 int yolo_profile_stages(void* h, int iters, float* ms) {
   return guarded([&] {
     Engine* e = E(h);

@@ -84,6 +84,7 @@ _SIGS = {
     "yolo_time_graph": (C.c_float, [C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "yolo_profile_ops": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "yolo_profile_stages": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_float)]),
+    "yolo_profile_units": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "yolo_dev_alloc": (C.c_void_p, [C.c_size_t]),
     "yolo_dev_free": (None, [C.c_void_p]),
     "yolo_host_alloc": (C.c_void_p, [C.c_size_t]),
@@ -359,6 +360,14 @@ class Engine:
         out = (C.c_float * n)()
         if self.lib.yolo_profile_ops(self.h, B, iters, out) != 0:
             raise RuntimeError("yolo_profile_ops failed")
+        return np.array(out, np.float64)
+
+    def profile_units(self, B: int, iters: int, reps: int) -> np.ndarray:
+        """Kernel ms per launch unit (reported on its first op), units repeated back to back."""
+        n = self.num_ops
+        out = (C.c_float * n)()
+        if self.lib.yolo_profile_units(self.h, B, iters, reps, out) != 0:
+            raise RuntimeError("yolo_profile_units failed")
         return np.array(out, np.float64)
 
     def profile_stages(self, iters: int) -> dict:
