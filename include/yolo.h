@@ -85,6 +85,9 @@ int yolo_get_mask(void* h, int slot, int det, unsigned char* out);
                               capture; slower for batch 1 on ROCm 7.2                      */
 #define YOLO_NOGROUP 32    /* one op per launch: no grouped launches of independent convs /
                               copies (results are identical either way)                    */
+#define YOLO_NMS_BLOCK 64  /* detect / segment NMS in one block per image (one launch)
+                              instead of the multi-block pipeline (six launches spread over
+                              the GPU); identical results                                  */
 
 /* Error-returning create: NULL on failure with a message in err (if non-NULL). */
 void* yolo_create_ex(const char* model_dir, int max_batch, int flags, char* err, int errlen);

@@ -394,16 +394,18 @@ def test_conv_halo_rejects(tmp_path):
         eng.close()
 
 
+@pytest.mark.parametrize("nmsflag", [0, yolort.YOLO_NMS_BLOCK], ids=["multi", "block"])
 @pytest.mark.parametrize("ncls", [1, 12, 20, 80])
-def test_nms_paths_crafted_heads(models, ncls):
+def test_nms_paths_crafted_heads(models, ncls, nmsflag):
     """Decode + NMS on crafted head tensors that drive each NMS path: one class (over 2048
-    candidates: radix select, then the 64-per-step blockwise path), 12 classes (~170 per
-    class: blockwise), 20 classes (50-120 per class: the per-class path with two chunks) and
-    80 classes (one chunk per class).  Exact: same raw count, survivors, order and classes
-    as the oracle."""
+    candidates: threshold selection, then one class of 32 chunks whose mask columns are too
+    large for LDS), 12 classes (~170 per class), 20 classes (50-120 per class: two chunks)
+    and 80 classes (one chunk per class); through the multi-block pipeline (the default)
+    and the one-block kernel (YOLO_NMS_BLOCK).  Exact: same raw count, survivors, order and
+    classes as the oracle."""
     d = models("yolo11", "n")
     g = graphfile.load(d)
-    eng = yolort.Engine(d, 1, yolort.YOLO_NOFUSE | yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    eng = yolort.Engine(d, 1, yolort.YOLO_NOFUSE | yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH | nmsflag)
     rng = np.random.default_rng(ncls)
     dec = [(k, op) for k, op in enumerate(g.ops) if op.kind == "DECODE"]
     heads = []
@@ -431,4 +433,40 @@ def test_nms_paths_crafted_heads(models, ncls):
         np.testing.assert_array_equal(got[:, 5].astype(int), want["cls"])
         np.testing.assert_allclose(got[:, 4], want["score"], rtol=0, atol=2e-6)
         np.testing.assert_allclose(got[:, :4], want["box"], rtol=0, atol=2e-3)
+    eng.close()
+
+
+@pytest.mark.parametrize("nmsflag", [0, yolort.YOLO_NMS_BLOCK], ids=["multi", "block"])
+def test_nms_tied_scores(models, nmsflag):
+    """Every anchor of every level has the same score in one of two classes (8400 candidates,
+    4200 per class): the NMS_CAP best are the lowest anchors, so the selection must narrow
+    down to the anchor bits of the keys.  Exact against the oracle."""
+    d = models("yolo11", "n")
+    g = graphfile.load(d)
+    eng = yolort.Engine(d, 1, yolort.YOLO_NOFUSE | yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH | nmsflag)
+    rng = np.random.default_rng(7)
+    dec = [(k, op) for k, op in enumerate(g.ops) if op.kind == "DECODE"]
+    heads = []
+    for _, op in dec:
+        H, W, C = eng.tensor_shape(op.b)
+        cls = np.full((1, H, W, C), -20.0, np.float32)
+        pick = rng.integers(0, 2, (H, W))
+        cls[0, np.arange(H)[:, None], np.arange(W)[None, :], pick] = 1.5
+        box = rng.normal(0.0, 1.5, (1, H, W, 64)).astype(np.float32)
+        box[..., 2::16] += 2.0
+        eng.write(op.b, cls)
+        eng.write(op.a, box)
+        heads.append((box[0].astype(np.float16).astype(np.float32),
+                      cls[0].astype(np.float16).astype(np.float32), None, op.stride))
+    eng.set_thresholds(0.25, 0.45, 300)
+    eng.run_op(dec[-1][0], 1)
+    eng.run_post(1)
+    want = post.detect(heads, 80, 0.25, 0.45)
+    got = eng.get(0)
+    print(f"tied scores: raw {eng.raw_count(0)} / {want['n_raw']}, kept {len(got)} / {len(want['score'])}", flush=True)
+    assert want["n_raw"] == 8400 and eng.raw_count(0) == want["n_raw"]
+    assert len(got) == len(want["score"])
+    np.testing.assert_array_equal(got[:, 5].astype(int), want["cls"])
+    np.testing.assert_allclose(got[:, 4], want["score"], rtol=0, atol=2e-6)
+    np.testing.assert_allclose(got[:, :4], want["box"], rtol=0, atol=2e-3)
     eng.close()

@@ -19,8 +19,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 # packed-fp32 instructions are disabled for all device code (some of their forms have
-# produced wrong results on this hardware pool); frame.hip also disables FMA contraction
-# so its fp32 arithmetic rounds exactly as written.
+# produced wrong results on this hardware pool); frame.hip and nms.hip also disable FMA
+# contraction so their fp32 arithmetic rounds exactly as written.
 DEV_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include"]
@@ -32,6 +32,7 @@ SOURCES = {
     "elementwise.hip": DEV_FLAGS,
     "attention.hip": DEV_FLAGS,
     "frame.hip": DEV_FLAGS + ["-ffp-contract=off"],
+    "nms.hip": DEV_FLAGS + ["-ffp-contract=off"],
     "noalloc.hip": DEV_FLAGS,
     "graph.cpp": HOST_FLAGS,
     "engine.cpp": HOST_FLAGS,

@@ -81,6 +81,8 @@ struct Engine {
   float* cand = nullptr;
   int* nmsCount = nullptr;            // per-image decode list length (NMS re-arms it)
   unsigned long long* nmsScratch = nullptr;
+  NmsImage* nmsWork = nullptr;        // multi-block NMS workspace, one record per image
+  bool nmsBlock = false;              // YOLO_NMS_BLOCK: one-block NMS (no workspace)
   // results: [outcnt B][rawcnt B] then (256-aligned) outdets B*MAX_OUT*outK in one block, so
   // one copy brings everything the host reads back
   void* results = nullptr;
@@ -140,12 +142,12 @@ struct Engine {
     graphs.clear();
     if (frameGraph) (void)hipGraphExecDestroy(frameGraph);
     frameGraph = nullptr;
-    void* dptrs[] = {arena, weights, bias, cand, nmsCount, nmsScratch, results, outidx, masks, params,
-                     splitWs, splitCnt};
+    void* dptrs[] = {arena, weights, bias, cand, nmsCount, nmsScratch, nmsWork, results, outidx, masks,
+                     params, splitWs, splitCnt};
     for (void* p : dptrs)
       if (p) (void)hipFree(p);
     arena = nullptr; weights = nullptr; bias = nullptr; cand = nullptr; nmsCount = nullptr;
-    nmsScratch = nullptr; results = nullptr; outdets = nullptr; outidx = nullptr; outcnt = nullptr;
+    nmsScratch = nullptr; nmsWork = nullptr; results = nullptr; outdets = nullptr; outidx = nullptr; outcnt = nullptr;
     rawcnt = nullptr;
     masks = nullptr; params = nullptr; splitWs = nullptr; splitCnt = nullptr;
     splitWsBytes = splitCntN = 0;
@@ -370,6 +372,10 @@ struct Engine {
     HCK(hipMalloc(&nmsCount, (size_t)B * sizeof(int)));
     HCK(hipMemset(nmsCount, 0, (size_t)B * sizeof(int)));
     HCK(hipMalloc(&nmsScratch, (size_t)B * nmsScratchBytes(A)));
+    if (g.numAnchors > 0 && !g.obb && !nmsBlock) {
+      HCK(hipMalloc(&nmsWork, (size_t)B * sizeof(NmsImage)));
+      HCK(hipMemset(nmsWork, 0, (size_t)B * sizeof(NmsImage)));
+    }
     detOff = ((size_t)2 * B * sizeof(int) + 255) & ~(size_t)255;
     const size_t resBytes = detOff + (size_t)B * MAX_OUT * g.outK * sizeof(float);
     HCK(hipMalloc(&results, resBytes));
@@ -664,6 +670,9 @@ struct Engine {
     if (g.numAnchors == 0) return;   // no detection head (single-op graphs)
     if (g.obb)
       launchNmsObb(cand, nmsScratch, nmsCount, g.numAnchors, outdets, outidx, outcnt, rawcnt, params, Bn, st);
+    else if (nmsWork)
+      launchNmsMulti(cand, nmsScratch, nmsCount, g.numAnchors, cstride, outdets, outidx, outcnt, rawcnt, params,
+                     nmsWork, Bn, st);
     else
       launchNms(cand, nmsScratch, nmsCount, g.numAnchors, cstride, outdets, outidx, outcnt, rawcnt, params, Bn, st);
     if (g.protoTen >= 0) {
@@ -1014,6 +1023,7 @@ void setErr(char* err, int errlen, const char* msg) {
 
 Engine* create(const char* dir, int maxB, int flags) {
   auto* e = new Engine();
+  e->nmsBlock = (flags & YOLO_NMS_BLOCK) != 0;
   try {
     e->load(dir, maxB, !(flags & YOLO_NOFUSE));
     if (flags & YOLO_BRANCHES) {
@@ -1549,6 +1559,9 @@ int yolo_profile_stages(void* h, int iters, float* ms) {
       if (e->g.obb)
         yolo::launchNmsObb(e->cand, e->nmsScratch, e->nmsCount, e->g.numAnchors, e->outdets, e->outidx, e->outcnt,
                            e->rawcnt, e->params, Bn, e->st);
+      else if (e->nmsWork)
+        yolo::launchNmsMulti(e->cand, e->nmsScratch, e->nmsCount, e->g.numAnchors, e->cstride, e->outdets,
+                             e->outidx, e->outcnt, e->rawcnt, e->params, e->nmsWork, Bn, e->st);
       else
         yolo::launchNms(e->cand, e->nmsScratch, e->nmsCount, e->g.numAnchors, e->cstride, e->outdets, e->outidx,
                         e->outcnt, e->rawcnt, e->params, Bn, e->st);

@@ -77,6 +77,38 @@ struct PostParams {
 
 constexpr int MAX_OUT = 300;          // output records per image (engine/engine.cu:28)
 constexpr int NMS_CAP = 2048;         // top-ranked candidates that enter NMS
+constexpr int NMS_CLASSES = 1024;     // class ids the NMS kernels bin (ids are < nc <= 1024)
+constexpr int NMS_SLACK = 256;        // selected keys beyond NMS_CAP (the boundary bin's ties)
+constexpr int NMS_SEL = NMS_CAP + NMS_SLACK;
+constexpr int NMS_MASK_WORDS = NMS_CAP * (NMS_CAP / 64);   // bound of one image's mask columns
+constexpr int NMS_RANK_SPLIT = 4;     // parts of the selection one rank block compares against
+
+// Per-image device workspace of the multi-block NMS (one array of Bn of these).
+//  sel*   the selected candidates (a superset of the NMS_CAP best keys), in arrival order:
+//         key, box, class; selRank[p][i]: (rank << 16 | rank within the class) of key i
+//         counted over part p of the selection
+//  rIdx   rank -> selected index; cRank / cBox: class-major position -> rank / box
+//  cls    present classes in class order: (first class-major position, members, first
+//         mask word, -); tile: the class's (first position, members, first mask word) and
+//         row chunk << 5 | column chunk
+//  mask   per class, column d (members 64d .. 64d+63 as suppressed candidates) holds one
+//         word per member i < min(members, 64(d+1)): bit j set iff member i suppresses
+//         member 64d + j (i ranked above it); column d starts 32 d (d + 1) words in
+//  kept   survivor flags by rank (cleared by the emit kernel for the next frame)
+struct NmsImage {
+  unsigned long long selKey[NMS_SEL];
+  float4 selBox[NMS_SEL];
+  int selCls[NMS_SEL];
+  unsigned selRank[NMS_RANK_SPLIT][NMS_SEL];
+  int rIdx[NMS_CAP];
+  int cRank[NMS_CAP];
+  float4 cBox[NMS_CAP];
+  int4 cls[NMS_CLASSES];
+  int4 tile[NMS_CAP];
+  unsigned kept[NMS_CAP / 32];
+  int selN, nClasses, nTiles, pad;
+  unsigned long long mask[NMS_MASK_WORDS];
+};
 
 // Detection levels handled by one decode launch.
 struct DecodeLevel {
@@ -202,6 +234,13 @@ void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lists, i
 void launchNms(const float* cand, unsigned long long* lists, int* counts, int A, int cstride,
                float* out, int* outidx, int* outcnt, int* rawcnt, const PostParams* prm, int Bn,
                hipStream_t st);
+// The same NMS (identical results) spread over many CUs: selection, a counting rank, the
+// class layout, suppression masks, per-class greedy and the output are six launches over a
+// workspace of Bn NmsImage records (zeroed once at allocation; every launch leaves it ready
+// for the next frame).
+void launchNmsMulti(const float* cand, unsigned long long* lists, int* counts, int A, int cstride,
+                    float* out, int* outidx, int* outcnt, int* rawcnt, const PostParams* prm,
+                    NmsImage* ws, int Bn, hipStream_t st);
 // Rotated NMS over 7-float OBB records (cx, cy, w, h, score, cls, theta); output records
 // have the same layout.
 void launchNmsObb(const float* cand, unsigned long long* lists, int* counts, int A, float* out,

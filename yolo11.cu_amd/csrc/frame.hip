@@ -2,7 +2,7 @@
 // Built with -ffp-contract=off so every fp32 expression rounds exactly as written; the
 // CPU oracle evaluates the same expressions in the same order and NMS decisions
 // (inter/union > thr) are then reproducible bit for bit.
-#include "engine.hpp"
+#include "boxes.hpp"
 
 namespace yolo {
 
@@ -136,14 +136,6 @@ void launchPreprocessCls(const uint8_t* src, int sh, int sw, f16* dst, int S, in
 // expectation per side, xyxy = (x + 0.5 -+ d) * stride.  Every anchor owns record
 // `anchor` of the candidate array; survivors append a packed (score, anchor) key to the
 // image's list, which NMS ranks, so results do not depend on thread scheduling.
-__device__ __forceinline__ unsigned long long packKey(float score, int anchor) {
-  return ((unsigned long long)__float_as_uint(score) << 32) | (unsigned)(0xFFFFFFFFu - (unsigned)anchor);
-}
-
-__device__ __forceinline__ int keyAnchor(unsigned long long k) {
-  return (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull));
-}
-
 // grid (anchor blocks of one wave, images): a wave never spans two images, so the survivors
 // of a wave are appended to the image's candidate list with one atomic (wave-aggregated).
 // The list order depends on arrival; NMS sorts by key, so results do not.  One-wave blocks
@@ -283,34 +275,8 @@ void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lst, int
 //     block prefix sum over the flags gives their output slots;
 //  3. the list counter is re-armed (zeroed) for the next frame.
 constexpr int NMS_THREADS = 1024;
-constexpr int NMS_CLASSES = 1024;            // class histogram size of the per-class path
 constexpr int NMS_WAVE_CLASS = 256;          // largest class one wave resolves alone
 constexpr int NMS_THREAD_CLASS = 16;         // up to 512 candidates: per-thread rows up to this class size
-
-// inter/union > thr, decided without the division unless the two sides are within a few
-// ulps (then the division decides, exactly as the reference writes it)
-// A value every lane of the wave holds (an LDS word read at a uniform address), moved to a
-// scalar register so the control flow that depends on it stays scalar.
-__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
-
-// (compare-selects rather than fmaxf/fminf: box coordinates are finite, and the selects need
-// no NaN canonicalisation of their operands)
-__device__ __forceinline__ float fmx(float a, float b) { return a > b ? a : b; }
-__device__ __forceinline__ float fmn(float a, float b) { return a < b ? a : b; }
-__device__ __forceinline__ bool suppresses(float4 a, float4 b, float thr) {
-  const float xx1 = fmx(a.x, b.x), yy1 = fmx(a.y, b.y);
-  const float xx2 = fmn(a.z, b.z), yy2 = fmn(a.w, b.w);
-  const float w = fmx(0.f, xx2 - xx1), h = fmx(0.f, yy2 - yy1);
-  const float inter = w * h;
-  const float aarea = (a.z - a.x) * (a.w - a.y);
-  const float barea = (b.z - b.x) * (b.w - b.y);
-  const float ua = aarea + barea - inter;
-  if (!(ua > 0.f)) return false;
-  const float p = thr * ua;
-  if (inter > p * 1.000001f) return true;
-  if (inter < p * 0.999999f) return false;
-  return inter / ua > thr;
-}
 
 // Selection + ranking shared by both NMS kernels.  Leaves the m = min(n, NMS_CAP) largest
 // keys of lst[0..n) in descending order in sorted[0..m):

@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(HERE, "libyolo11_amd.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "yolo.h")
 
 YOLO_NOFUSE, YOLO_NOTUNE, YOLO_NOGRAPH, YOLO_BRANCHES, YOLO_DAGGRAPH, YOLO_NOGROUP = 1, 2, 4, 8, 16, 32
+YOLO_NMS_BLOCK = 64
 CFG_HALO = 1000   # op config of the LDS-halo 3x3 kernel (small-channel stride-1 convs)
 OP_KINDS = ["CONV", "ADD", "MAXPOOL5", "UPSAMPLE2", "COPYC", "ATTN", "DECODE", "GAP", "SOFTMAX",
             "DECODEOBB", "PS2", "DECODESEG", "MASKS"]
