@@ -85,9 +85,9 @@ int yolo_get_mask(void* h, int slot, int det, unsigned char* out);
                               capture; slower for batch 1 on ROCm 7.2                      */
 #define YOLO_NOGROUP 32    /* one op per launch: no grouped launches of independent convs /
                               copies (results are identical either way)                    */
-#define YOLO_NMS_BLOCK 64  /* detect / segment NMS in one block per image (one launch)
-                              instead of the multi-block pipeline (six launches spread over
-                              the GPU); identical results                                  */
+#define YOLO_NMS_BLOCK 64  /* NMS (detect, segment, rotated) in one block per image (one
+                              launch) instead of the multi-block pipeline (six launches
+                              spread over the GPU); identical results                      */
 
 /* Error-returning create: NULL on failure with a message in err (if non-NULL). */
 void* yolo_create_ex(const char* model_dir, int max_batch, int flags, char* err, int errlen);
@@ -147,7 +147,10 @@ int yolo_tile_config(int cfg, int* out);
 /* Whole-frame graph -- the reference's `pipeline` mode (engine/engine.cu:1974-2032):
  * one graph holding [H2D of each raw frame] + letterbox of each slot + network + decode +
  * NMS + result copies.  host_bgr may be NULL (frames already in device memory) or an
- * array of B pinned host pointers.  Replaces any previous frame graph. */
+ * array of B pinned host pointers.  Replaces any previous frame graph.  Two variants are
+ * captured (unless YOLO_NMS_BLOCK): the launch takes the one-block NMS while the previous
+ * frame's results showed at most 512 candidates in every slot, else the multi-block NMS;
+ * the detections are identical either way. */
 int yolo_frame_graph(void* h, int B, const unsigned char* const* dev_bgr,
                      const unsigned char* const* host_bgr, const int* heights, const int* widths);
 int yolo_frame_run(void* h);       /* launch + wait */

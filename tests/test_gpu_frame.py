@@ -161,3 +161,33 @@ def test_dag_graph_equals_serial_graph(models, task):
         for x, y in zip(a, b):
             np.testing.assert_array_equal(x, y)
     assert len(res["dag"][0][0]) > 0
+
+
+def test_frame_graph_nms_variants(models):
+    """The frame graph holds both NMS variants and picks by the previous frame's candidate
+    count: a sparse frame (294 candidates) and a crowded one (conf 0.05: thousands) alternate
+    on one handle; every run must equal a YOLO_NMS_BLOCK handle's run of the same frame."""
+    d = models("yolo11", "n")
+    img = modelgen.synth_frame(810, 1080, 20, 1)
+    engs = [yolort.Engine(d, 1), yolort.Engine(d, 1, yolort.YOLO_NMS_BLOCK)]
+    bufs = []
+    for e in engs:
+        b = yolort.DeviceBuffer(img.nbytes)
+        e.upload(b, img)
+        e.frame_graph([b.ptr], [810], [1080])
+        bufs.append(b)
+    raws = {}
+    for conf in (0.25, 0.05, 0.05, 0.25, 0.25, 0.05):
+        outs = []
+        for e in engs:
+            e.set_thresholds(conf, 0.45, 300)
+            e.frame_run()
+            outs.append((e.get(0), e.raw_count(0)))
+        print(f"conf {conf}: raw {outs[0][1]}, kept {len(outs[0][0])}", flush=True)
+        assert outs[0][1] == outs[1][1]
+        np.testing.assert_array_equal(outs[0][0], outs[1][0])
+        raws[conf] = outs[0][1]
+    assert raws[0.25] <= 512 < raws[0.05]   # both variants were taken
+    for b, e in zip(bufs, engs):
+        b.free()
+        e.close()

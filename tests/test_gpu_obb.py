@@ -67,14 +67,15 @@ def _check_post(eng, heads, nc, conf, iou):
     np.testing.assert_allclose(got[:, 4], want["theta"], rtol=0, atol=2e-6)
 
 
-def test_obb_ops_resync_and_post(models):
+@pytest.mark.parametrize("nmsflag", [0, yolort.YOLO_NMS_BLOCK], ids=["multi", "block"])
+def test_obb_ops_resync_and_post(models, nmsflag):
     d = _model(models)
     g = graphfile.load(d)
     img = modelgen.synth_frame(1024, 1024, 50, 7)
     x = post.letterbox(img, 1024, 1024)[None]
     ref = interp.Interp(g, 1, round_fp16=True)
     ref.set_input(x)
-    eng = yolort.Engine(d, 1, yolort.YOLO_NOFUSE | yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    eng = yolort.Engine(d, 1, yolort.YOLO_NOFUSE | yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH | nmsflag)
     assert eng.task() == 1
     eng.write(0, ref.view(0))
     rels, last_decode = [], -1

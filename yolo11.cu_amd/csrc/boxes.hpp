@@ -45,4 +45,29 @@ __device__ __forceinline__ bool suppresses(float4 a, float4 b, float thr) {
   return inter / ua > thr;
 }
 
+// probiou of two rotated boxes as Gaussians (centre x, y; covariance [[A, C], [C, B]];
+// det = max(A*B - C*C, 0)): the ultralytics batch_probiou expression that k_nms_obb
+// evaluates (engine/engine.cu:1160-1176), eps 1e-7 in the t1/t2 denominator, in the t3
+// sqrt denominator and added to the log argument, bd clamped to [eps, 100].
+__device__ __forceinline__ float probiou(float2 p1, float4 g1, float det1, float2 p2, float4 g2,
+                                         float det2) {
+  const float eps = 1e-7f;
+  const float dx = p1.x - p2.x, dy = p1.y - p2.y;
+  const float sA = g1.x + g2.x, sB = g1.y + g2.y, sC = g1.z + g2.z;
+  const float disc = sA * sB - sC * sC;
+  const float den = disc + eps;
+  const float t1 = 0.25f * (sA * dy * dy + sB * dx * dx) / den;
+  const float t2 = 0.5f * (sC * (-dx) * dy) / den;
+  const float t3 = 0.5f * logf(disc / (4.f * sqrtf(det1 * det2) + eps) + eps);
+  const float bd = fminf(fmaxf(t1 + t2 + t3, eps), 100.f);
+  return 1.f - sqrtf(1.f - expf(-bd) + eps);
+}
+
+// The far-pair bound of the rotated NMS: for covariances with determinant >= OBB_DET_MIN and
+// condition number below ~1e4 (det >= OBB_COND * trace^2), bd >= |d|^2 / (4 trace(S1 + S2)),
+// and probiou >= thr needs bd <= B* = -ln(1 + eps - (1 - thr)^2), so |d|^2 > 8 B* trace
+// (a factor-2 margin over fp32 rounding) rules a pair out; used for 0.05 <= thr <= 0.95.
+constexpr float OBB_DET_MIN = 1.f;
+constexpr float OBB_COND = 1e-4f;
+
 }  // namespace yolo

@@ -111,6 +111,11 @@ struct Engine {
   std::vector<hipGraphExec_t> graphs;
   std::vector<float> execMs;
   hipGraphExec_t frameGraph = nullptr;
+  // The same frame graph with the one-block NMS: yolo_frame_run / _launch take it while the
+  // previous frame had at most NMS_BLOCK_MAX candidates in every slot (the one launch beats
+  // the multi-block pipeline's six on sparse frames; results are identical either way).
+  hipGraphExec_t frameGraphBlock = nullptr;
+  bool capBlock = false;              // capture(): post() records the one-block NMS
   int frameB = 0;
   // the frame graph's device sources and sizes (for stage timing outside the graph)
   std::vector<std::pair<const uint8_t*, SlotGeom>> frameSrc;
@@ -141,7 +146,8 @@ struct Engine {
       if (ge) (void)hipGraphExecDestroy(ge);
     graphs.clear();
     if (frameGraph) (void)hipGraphExecDestroy(frameGraph);
-    frameGraph = nullptr;
+    if (frameGraphBlock) (void)hipGraphExecDestroy(frameGraphBlock);
+    frameGraph = frameGraphBlock = nullptr;
     void* dptrs[] = {arena, weights, bias, cand, nmsCount, nmsScratch, nmsWork, results, outidx, masks,
                      params, splitWs, splitCnt};
     for (void* p : dptrs)
@@ -372,7 +378,7 @@ struct Engine {
     HCK(hipMalloc(&nmsCount, (size_t)B * sizeof(int)));
     HCK(hipMemset(nmsCount, 0, (size_t)B * sizeof(int)));
     HCK(hipMalloc(&nmsScratch, (size_t)B * nmsScratchBytes(A)));
-    if (g.numAnchors > 0 && !g.obb && !nmsBlock) {
+    if (g.numAnchors > 0 && !nmsBlock) {
       HCK(hipMalloc(&nmsWork, (size_t)B * sizeof(NmsImage)));
       HCK(hipMemset(nmsWork, 0, (size_t)B * sizeof(NmsImage)));
     }
@@ -668,9 +674,13 @@ struct Engine {
       return;
     }
     if (g.numAnchors == 0) return;   // no detection head (single-op graphs)
-    if (g.obb)
+    const bool multi = nmsWork && !capBlock;
+    if (g.obb && multi)
+      launchNmsObbMulti(cand, nmsScratch, nmsCount, g.numAnchors, outdets, outidx, outcnt, rawcnt, params, nmsWork,
+                        Bn, st);
+    else if (g.obb)
       launchNmsObb(cand, nmsScratch, nmsCount, g.numAnchors, outdets, outidx, outcnt, rawcnt, params, Bn, st);
-    else if (nmsWork)
+    else if (multi)
       launchNmsMulti(cand, nmsScratch, nmsCount, g.numAnchors, cstride, outdets, outidx, outcnt, rawcnt, params,
                      nmsWork, Bn, st);
     else
@@ -996,6 +1006,18 @@ struct Engine {
     sg.top = (ib.H - nh) / 2;
     sg.left = (ib.W - nw) / 2;
     return sg;
+  }
+
+  // The frame graph variant for the next frame: the one-block NMS while every slot of the
+  // previous frame (the last results fetched to pinned memory; zeros before the first) had at
+  // most NMS_BLOCK_MAX candidates, else the multi-block pipeline.
+  bool sparsePrev() const {
+    for (int s = 0; s < frameB; s++)
+      if (h_rawcnt[s] > NMS_BLOCK_MAX) return false;
+    return true;
+  }
+  hipGraphExec_t frameExec() const {
+    return frameGraphBlock && sparsePrev() ? frameGraphBlock : frameGraph;
   }
 
   void run(int Bn) {
@@ -1423,8 +1445,19 @@ int yolo_frame_graph(void* h, int B, const unsigned char* const* dev_bgr, const 
       frames.push_back({dev_bgr[s], e->geom(heights[s], widths[s])});
     }
     if (e->frameGraph) HCK(hipGraphExecDestroy(e->frameGraph));
-    e->frameGraph = nullptr;
+    if (e->frameGraphBlock) HCK(hipGraphExecDestroy(e->frameGraphBlock));
+    e->frameGraph = e->frameGraphBlock = nullptr;
     e->frameGraph = e->capture(B, &frames, host_bgr, heights, widths);
+    if (e->nmsWork) {
+      e->capBlock = true;
+      try {
+        e->frameGraphBlock = e->capture(B, &frames, host_bgr, heights, widths);
+      } catch (...) {
+        e->capBlock = false;
+        throw;
+      }
+      e->capBlock = false;
+    }
     e->frameB = B;
     e->frameSrc = frames;
     e->frameH.assign(heights, heights + B);
@@ -1438,7 +1471,7 @@ int yolo_frame_run(void* h) {
   return guarded([&] {
     Engine* e = E(h);
     if (!e->frameGraph) return -1;
-    HCK(hipGraphLaunch(e->frameGraph, e->st));
+    HCK(hipGraphLaunch(e->frameExec(), e->st));
     HCK(hipStreamSynchronize(e->st));
     return 0;
   });
@@ -1448,7 +1481,7 @@ int yolo_frame_launch(void* h) {
   return guarded([&] {
     Engine* e = E(h);
     if (!e->frameGraph) return -1;
-    HCK(hipGraphLaunch(e->frameGraph, e->st));
+    HCK(hipGraphLaunch(e->frameExec(), e->st));
     return 0;
   });
 }
@@ -1458,7 +1491,7 @@ float yolo_time_graph(void* h, int which, int B, int iters) {
   guarded([&] {
     Engine* e = E(h);
     hipGraphExec_t ge = nullptr;
-    if (which == 1) ge = e->frameGraph;
+    if (which == 1) ge = e->frameGraph ? e->frameExec() : nullptr;
     else if (B >= 1 && B <= (int)e->graphs.size()) ge = e->graphs[B - 1];
     if (!ge || iters < 1) return -1;
     hipEvent_t e0, e1;
@@ -1556,10 +1589,15 @@ int yolo_profile_stages(void* h, int iters, float* ms) {
         if (k == e->lastDecode) HCK(hipEventRecord(ev[3], e->st));
       }
       HCK(hipEventRecord(ev[4], e->st));
-      if (e->g.obb)
+      // the NMS variant the frame graph would take for this frame
+      const bool multi = e->nmsWork && !(e->frameGraphBlock && e->sparsePrev());
+      if (e->g.obb && multi)
+        yolo::launchNmsObbMulti(e->cand, e->nmsScratch, e->nmsCount, e->g.numAnchors, e->outdets, e->outidx,
+                                e->outcnt, e->rawcnt, e->params, e->nmsWork, Bn, e->st);
+      else if (e->g.obb)
         yolo::launchNmsObb(e->cand, e->nmsScratch, e->nmsCount, e->g.numAnchors, e->outdets, e->outidx, e->outcnt,
                            e->rawcnt, e->params, Bn, e->st);
-      else if (e->nmsWork)
+      else if (multi)
         yolo::launchNmsMulti(e->cand, e->nmsScratch, e->nmsCount, e->g.numAnchors, e->cstride, e->outdets,
                              e->outidx, e->outcnt, e->rawcnt, e->params, e->nmsWork, Bn, e->st);
       else

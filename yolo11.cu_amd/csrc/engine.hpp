@@ -82,6 +82,7 @@ constexpr int NMS_SLACK = 256;        // selected keys beyond NMS_CAP (the bound
 constexpr int NMS_SEL = NMS_CAP + NMS_SLACK;
 constexpr int NMS_MASK_WORDS = NMS_CAP * (NMS_CAP / 64);   // bound of one image's mask columns
 constexpr int NMS_RANK_SPLIT = 4;     // parts of the selection one rank block compares against
+constexpr int NMS_BLOCK_MAX = 512;    // frame graphs: one-block NMS while frames stay this sparse
 
 // Per-image device workspace of the multi-block NMS (one array of Bn of these).
 //  sel*   the selected candidates (a superset of the NMS_CAP best keys), in arrival order:
@@ -95,14 +96,18 @@ constexpr int NMS_RANK_SPLIT = 4;     // parts of the selection one rank block c
 //         word per member i < min(members, 64(d+1)): bit j set iff member i suppresses
 //         member 64d + j (i ranked above it); column d starts 32 d (d + 1) words in
 //  kept   survivor flags by rank (cleared by the emit kernel for the next frame)
+//  Rotated boxes: box = (cx, cy, trace of the covariance or -1 where the far-pair bound does
+//  not apply, det) and aux = the covariance (A, B, C, 0).
 struct NmsImage {
   unsigned long long selKey[NMS_SEL];
   float4 selBox[NMS_SEL];
+  float4 selAux[NMS_SEL];
   int selCls[NMS_SEL];
   unsigned selRank[NMS_RANK_SPLIT][NMS_SEL];
   int rIdx[NMS_CAP];
   int cRank[NMS_CAP];
   float4 cBox[NMS_CAP];
+  float4 cAux[NMS_CAP];
   int4 cls[NMS_CLASSES];
   int4 tile[NMS_CAP];
   unsigned kept[NMS_CAP / 32];
@@ -241,6 +246,12 @@ void launchNms(const float* cand, unsigned long long* lists, int* counts, int A,
 void launchNmsMulti(const float* cand, unsigned long long* lists, int* counts, int A, int cstride,
                     float* out, int* outidx, int* outcnt, int* rawcnt, const PostParams* prm,
                     NmsImage* ws, int Bn, hipStream_t st);
+// The rotated fast-NMS (launchNmsObb's results) on the same pipeline: the suppression tiles
+// test probiou >= thr, and a candidate is dropped iff any higher-ranked member of its class
+// reaches it (an OR per chunk instead of the greedy pass).
+void launchNmsObbMulti(const float* cand, unsigned long long* lists, int* counts, int A, float* out,
+                       int* outidx, int* outcnt, int* rawcnt, const PostParams* prm, NmsImage* ws,
+                       int Bn, hipStream_t st);
 // Rotated NMS over 7-float OBB records (cx, cy, w, h, score, cls, theta); output records
 // have the same layout.
 void launchNmsObb(const float* cand, unsigned long long* lists, int* counts, int A, float* out,

@@ -818,24 +818,6 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
 }
 
 // ------------------------------------------------------------------ rotated NMS (OBB)
-// probiou of two rotated boxes as Gaussians (centre x, y; covariance [[A, C], [C, B]];
-// det = max(A*B - C*C, 0)): the ultralytics batch_probiou expression that k_nms_obb
-// evaluates (engine/engine.cu:1160-1176), eps 1e-7 in the t1/t2 denominator, in the t3
-// sqrt denominator and added to the log argument, bd clamped to [eps, 100].
-__device__ __forceinline__ float probiou(float2 p1, float4 g1, float det1, float2 p2, float4 g2,
-                                         float det2) {
-  const float eps = 1e-7f;
-  const float dx = p1.x - p2.x, dy = p1.y - p2.y;
-  const float sA = g1.x + g2.x, sB = g1.y + g2.y, sC = g1.z + g2.z;
-  const float disc = sA * sB - sC * sC;
-  const float den = disc + eps;
-  const float t1 = 0.25f * (sA * dy * dy + sB * dx * dx) / den;
-  const float t2 = 0.5f * (sC * (-dx) * dy) / den;
-  const float t3 = 0.5f * logf(disc / (4.f * sqrtf(det1 * det2) + eps) + eps);
-  const float bd = fminf(fmaxf(t1 + t2 + t3, eps), 100.f);
-  return 1.f - sqrtf(1.f - expf(-bd) + eps);
-}
-
 // One block (16 waves) per image.  ultralytics fast-NMS semantics, as k_nms_obb
 // (engine/engine.cu:1178-1252): candidate j is dropped iff some higher-ranked candidate
 // of its class, suppressed or not, has probiou >= thr with it.  There is no sequential
@@ -857,8 +839,6 @@ __device__ __forceinline__ float probiou(float2 p1, float4 g1, float det1, float
 //     LDS queue; each 64 queued pairs are evaluated exactly, one pair per lane, so the
 //     transcendental path runs on full waves;
 //  5. survivors take output slots by a block prefix count in rank order (max_det cap).
-constexpr float OBB_DET_MIN = 1.f;
-constexpr float OBB_COND = 1e-4f;            // det >= OBB_COND * trace^2: condition < ~1e4
 constexpr int OBB_QUEUE = 128;               // per-wave queue of pairs for exact evaluation
 
 __global__ __launch_bounds__(NMS_THREADS) void k_nms_obb(const float* __restrict__ cand,

@@ -124,6 +124,7 @@ __device__ __forceinline__ float boxArea(float4 b) { return (b.z - b.x) * (b.w -
 // fits: at most 6 passes.  Each thread keeps its first SEL_KPT keys in registers, so the
 // list is read from memory once; the gather places every kept key first and then has all
 // their candidate records in flight together.
+template <bool OBB>
 __global__ __launch_bounds__(BLK) void k_nms_select(const float* __restrict__ cand,
                                                     const unsigned long long* __restrict__ lists,
                                                     const int* __restrict__ counts, int A, int cstride,
@@ -210,33 +211,60 @@ __global__ __launch_bounds__(BLK) void k_nms_select(const float* __restrict__ ca
     const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
     return take && pos < NMS_SEL ? pos : -1;
   };
-  auto store = [&](int pos, unsigned long long k, float2 r01, float2 r23, float2 r45) {
+  // the record fields a candidate needs: detect x1 y1 x2 y2 . cls (6 + nm floats, 8-byte
+  // aligned); rotated cx cy w h . cls theta (7 floats)
+  struct Rec { float v[7]; };
+  auto fetch = [&](unsigned long long k) {
+    const float* rec = cand + ((size_t)img * A + keyAnchor(k)) * cstride;
+    Rec r;
+    if constexpr (OBB) {
+#pragma unroll
+      for (int q = 0; q < 7; q++) r.v[q] = rec[q];
+    } else {
+      const float2* r2 = (const float2*)rec;
+#pragma unroll
+      for (int q = 0; q < 3; q++) {
+        const float2 t = r2[q];
+        r.v[2 * q] = t.x;
+        r.v[2 * q + 1] = t.y;
+      }
+      r.v[6] = 0.f;
+    }
+    return r;
+  };
+  auto store = [&](int pos, unsigned long long k, const Rec& r) {
     w.selKey[pos] = k;
-    w.selBox[pos] = make_float4(r01.x, r01.y, r23.x, r23.y);
-    w.selCls[pos] = min(max((int)r45.y, 0), NMS_CLASSES - 1);
+    if constexpr (OBB) {
+      // covariance of the rotated box, as the one-block kernel forms it (engine/engine.cu:1199-1204)
+      const float a = r.v[2] * r.v[2] * (1.f / 12.f), b = r.v[3] * r.v[3] * (1.f / 12.f);
+      const float cs = cosf(r.v[6]), sn = sinf(r.v[6]);
+      const float Aa = a * cs * cs + b * sn * sn;
+      const float Bb = a * sn * sn + b * cs * cs;
+      const float Cc = (a - b) * cs * sn;
+      const float tr = Aa + Bb, det = fmaxf(Aa * Bb - Cc * Cc, 0.f);
+      const bool bounded = det >= OBB_DET_MIN && det >= OBB_COND * tr * tr;
+      w.selBox[pos] = make_float4(r.v[0], r.v[1], bounded ? tr : -1.f, det);
+      w.selAux[pos] = make_float4(Aa, Bb, Cc, 0.f);
+      w.selCls[pos] = (int)fminf(fmaxf(r.v[5], 0.f), (float)(NMS_CLASSES - 1));
+    } else {
+      w.selBox[pos] = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
+      w.selCls[pos] = min(max((int)r.v[5], 0), NMS_CLASSES - 1);
+    }
   };
   int pos[SEL_KPT];
 #pragma unroll
   for (int u = 0; u < SEL_KPT; u++) pos[u] = u * BLK < n ? place(kc[u], tid + u * BLK < n) : -1;
-  float2 r[SEL_KPT][3];
+  Rec r[SEL_KPT];
 #pragma unroll
   for (int u = 0; u < SEL_KPT; u++)
-    if (pos[u] >= 0) {   // records are 8-byte aligned (cstride is even)
-      const float2* rec = (const float2*)(cand + ((size_t)img * A + keyAnchor(kc[u])) * cstride);
-      r[u][0] = rec[0];
-      r[u][1] = rec[1];
-      r[u][2] = rec[2];
-    }
+    if (pos[u] >= 0) r[u] = fetch(kc[u]);
 #pragma unroll
   for (int u = 0; u < SEL_KPT; u++)
-    if (pos[u] >= 0) store(pos[u], kc[u], r[u][0], r[u][1], r[u][2]);
+    if (pos[u] >= 0) store(pos[u], kc[u], r[u]);
   for (int i0 = SEL_KPT * BLK; i0 < n; i0 += BLK) {
     const unsigned long long k = i0 + tid < n ? lst[i0 + tid] : 0ull;
     const int p = place(k, i0 + tid < n);
-    if (p >= 0) {
-      const float2* rec = (const float2*)(cand + ((size_t)img * A + keyAnchor(k)) * cstride);
-      store(p, k, rec[0], rec[1], rec[2]);
-    }
+    if (p >= 0) store(p, k, fetch(k));
   }
   __syncthreads();
   if (tid == 0) w.selN = min(sCount, NMS_SEL);
@@ -256,7 +284,7 @@ struct LayoutShared {
   unsigned long long wsum64[BLK / 64];
 };
 
-__device__ __forceinline__ void nmsLayout(NmsImage& w, int m, LayoutShared& L) {
+__device__ __forceinline__ void nmsLayout(NmsImage& w, int m, bool aux, LayoutShared& L) {
   static_assert(NMS_SEL <= 3 * BLK, "three selected keys per thread");
   const int tid = threadIdx.x;
   L.chist[tid] = 0;
@@ -319,6 +347,7 @@ __device__ __forceinline__ void nmsLayout(NmsImage& w, int m, LayoutShared& L) {
       const int pos = L.cstart[e.c] + (int)(e.v & 0xFFFFu);
       w.cRank[pos] = r;
       w.cBox[pos] = e.b;
+      if (aux) w.cAux[pos] = w.selAux[i];
     }
   };
   place(e0, 0);
@@ -399,11 +428,11 @@ __global__ __launch_bounds__(BLK) void k_nms_rank(NmsImage* __restrict__ ws) {
   }
 }
 
-__global__ __launch_bounds__(BLK) void k_nms_layout(const int* __restrict__ counts, int A,
+__global__ __launch_bounds__(BLK) void k_nms_layout(const int* __restrict__ counts, int A, int aux,
                                                     NmsImage* __restrict__ ws) {
   __shared__ LayoutShared L;
   const int img = blockIdx.x;
-  nmsLayout(ws[img], min(min(counts[img], A), NMS_CAP), L);
+  nmsLayout(ws[img], min(min(counts[img], A), NMS_CAP), aux != 0, L);
 }
 
 // ------------------------------------------------------------------ 4. masks
@@ -543,11 +572,91 @@ __global__ __launch_bounds__(256) void k_nms_greedy(NmsImage* __restrict__ ws,
   }
 }
 
+// ------------------------------------------------------------------ 4r/5r. rotated boxes
+// Suppression tiles of the rotated fast-NMS: as k_nms_masks, with probiou >= thr as the
+// test.  A pair the far-pair bound rules out is skipped; the exact expression is evaluated
+// as a wave-uniform branch for the lanes that need it.
+__global__ __launch_bounds__(256) void k_nms_masks_obb(NmsImage* __restrict__ ws,
+                                                       const PostParams* __restrict__ prm) {
+  __shared__ unsigned long long part[4][64];
+  const int img = blockIdx.y;
+  NmsImage& w = ws[img];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nT = w.nTiles;
+  const float thr = prm->iou;
+  const float bstar = (thr >= 0.05f && thr <= 0.95f) ? -logf(1.f + 1e-7f - (1.f - thr) * (1.f - thr)) : 0.f;
+  const float skipK = bstar > 0.f ? 8.f * bstar : INFINITY;
+  auto bcast = [](float v, int j) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j)); };
+  for (int it = blockIdx.x; it < nT; it += gridDim.x) {
+    const int4 e = w.tile[it];
+    const int cs = uni(e.x), g = uni(e.y), mo = uni(e.z), ab = uni(e.w);
+    const int a = ab >> 5, b = ab & 31;
+    const int row = 64 * a + lane, col = 64 * b + lane;
+    const float4 zero = make_float4(0.f, 0.f, -1.f, 0.f);
+    const float4 rb = row < g ? w.cBox[cs + row] : zero, ra = row < g ? w.cAux[cs + row] : zero;
+    const float4 cb = col < g ? w.cBox[cs + col] : zero, ca = col < g ? w.cAux[cs + col] : zero;
+    const int j0 = 16 * wave, j1 = min(j0 + 16, g - 64 * b);
+    unsigned long long word = 0ull;
+    for (int j = j0; j < j1; j++) {
+      const float4 bj = make_float4(bcast(cb.x, j), bcast(cb.y, j), bcast(cb.z, j), bcast(cb.w, j));
+      const float4 aj = make_float4(bcast(ca.x, j), bcast(ca.y, j), bcast(ca.z, j), 0.f);
+      const float dx = rb.x - bj.x, dy = rb.y - bj.y;
+      const bool far = rb.z > 0.f && bj.z > 0.f && dx * dx + dy * dy > skipK * (rb.z + bj.z);
+      const bool need = row < g && (a < b || j > lane) && !far;
+      bool s = false;
+      if (__ballot(need)) {
+        if (need) s = probiou(make_float2(rb.x, rb.y), ra, rb.w, make_float2(bj.x, bj.y), aj, bj.w) >= thr;
+      }
+      if (s) word |= 1ull << j;
+    }
+    __syncthreads();   // the previous tile's parts are read
+    part[wave][lane] = word;
+    __syncthreads();
+    if (wave == 0 && row < g)
+      w.mask[mo + 32 * b * (b + 1) + row] = part[0][lane] | part[1][lane] | part[2][lane] | part[3][lane];
+  }
+}
+
+// Fast-NMS decisions: one wave per (class, chunk d), taken from the diagonal tiles.  A member
+// of chunk d is dropped iff some higher-ranked member of its class, suppressed or not,
+// reaches it: the OR of column d's words over all its rows.  No order between chunks.
+__global__ __launch_bounds__(256) void k_nms_fast(NmsImage* __restrict__ ws) {
+  const int img = blockIdx.y;
+  NmsImage& w = ws[img];
+  const int lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
+  const int nT = uni(w.nTiles);
+  for (int it = blockIdx.x * 4 + wave; it < nT; it += gridDim.x * 4) {
+    const int4 e = w.tile[it];
+    const int ab = uni(e.w);
+    const int d = ab & 31;
+    if ((ab >> 5) != d) continue;   // wave-uniform: one diagonal tile per chunk
+    const int cs = uni(e.x), g = uni(e.y), mo = uni(e.z);
+    const unsigned long long* colp = w.mask + mo + 32 * d * (d + 1);
+    unsigned long long v[NMS_CAP / 64];
+#pragma unroll
+    for (int k = 0; k < NMS_CAP / 64; k++) {
+      const int row = 64 * k + lane;
+      v[k] = (k <= d && row < g) ? colp[row] : 0ull;
+    }
+    unsigned long long dead = 0ull;
+#pragma unroll
+    for (int k = 0; k < NMS_CAP / 64; k++) dead |= v[k];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) dead |= __shfl_xor(dead, o);
+    const int p = 64 * d + lane;
+    if (p < g && !((dead >> lane) & 1ull)) {
+      const int r = w.cRank[cs + p];
+      atomicOr(&w.kept[r >> 5], 1u << (r & 31));
+    }
+  }
+}
+
 // ------------------------------------------------------------------ 6. emit
 // Thread t owns ranks 2t, 2t+1; output slots are the prefix count of survivor flags in rank
 // order.  Clears the flags and re-arms the decode list for the next frame.
-__global__ __launch_bounds__(BLK) void k_nms_emit(int* __restrict__ counts, int A,
-                                                  NmsImage* __restrict__ ws, float* __restrict__ out,
+template <bool OBB>
+__global__ __launch_bounds__(BLK) void k_nms_emit(const float* __restrict__ cand, int* __restrict__ counts,
+                                                  int A, NmsImage* __restrict__ ws, float* __restrict__ out,
                                                   int* __restrict__ outidx, int* __restrict__ outcnt,
                                                   int* __restrict__ rawcnt,
                                                   const PostParams* __restrict__ prm) {
@@ -567,11 +676,18 @@ __global__ __launch_bounds__(BLK) void k_nms_emit(int* __restrict__ counts, int 
   auto emit = [&](int r, int slot) {
     const int i = w.rIdx[r];
     const unsigned long long k = w.selKey[i];
-    const float4 b = w.selBox[i];
-    float* d = out + ((size_t)img * MAX_OUT + slot) * 6;
-    d[0] = b.x; d[1] = b.y; d[2] = b.z; d[3] = b.w;
-    d[4] = __uint_as_float((unsigned)(k >> 32));
-    d[5] = (float)w.selCls[i];
+    if constexpr (OBB) {   // the record as decoded: cx, cy, w, h, score, cls, theta
+      const float* rec = cand + ((size_t)img * A + keyAnchor(k)) * 7;
+      float* d = out + ((size_t)img * MAX_OUT + slot) * 7;
+#pragma unroll
+      for (int q = 0; q < 7; q++) d[q] = rec[q];
+    } else {
+      const float4 b = w.selBox[i];
+      float* d = out + ((size_t)img * MAX_OUT + slot) * 6;
+      d[0] = b.x; d[1] = b.y; d[2] = b.z; d[3] = b.w;
+      d[4] = __uint_as_float((unsigned)(k >> 32));
+      d[5] = (float)w.selCls[i];
+    }
     outidx[img * MAX_OUT + slot] = keyAnchor(k);
   };
   if (f0 && ex < maxdet) emit(r0, ex);
@@ -587,12 +703,23 @@ __global__ __launch_bounds__(BLK) void k_nms_emit(int* __restrict__ counts, int 
 void launchNmsMulti(const float* cand, unsigned long long* lists, int* counts, int A, int cstride,
                     float* out, int* outidx, int* outcnt, int* rawcnt, const PostParams* prm,
                     NmsImage* ws, int Bn, hipStream_t st) {
-  k_nms_select<<<Bn, BLK, 0, st>>>(cand, lists, counts, A, cstride, prm, ws);
+  k_nms_select<false><<<Bn, BLK, 0, st>>>(cand, lists, counts, A, cstride, prm, ws);
   k_nms_rank<<<dim3(RANK_TILES * NMS_RANK_SPLIT, Bn), BLK, 0, st>>>(ws);
-  k_nms_layout<<<Bn, BLK, 0, st>>>(counts, A, ws);
+  k_nms_layout<<<Bn, BLK, 0, st>>>(counts, A, 0, ws);
   k_nms_masks<<<dim3(MASK_BLOCKS, Bn), 256, 0, st>>>(ws, prm);
   k_nms_greedy<<<dim3(GREEDY_BLOCKS, Bn), 256, 0, st>>>(ws, prm);
-  k_nms_emit<<<Bn, BLK, 0, st>>>(counts, A, ws, out, outidx, outcnt, rawcnt, prm);
+  k_nms_emit<false><<<Bn, BLK, 0, st>>>(cand, counts, A, ws, out, outidx, outcnt, rawcnt, prm);
+}
+
+void launchNmsObbMulti(const float* cand, unsigned long long* lists, int* counts, int A, float* out,
+                       int* outidx, int* outcnt, int* rawcnt, const PostParams* prm, NmsImage* ws,
+                       int Bn, hipStream_t st) {
+  k_nms_select<true><<<Bn, BLK, 0, st>>>(cand, lists, counts, A, 7, prm, ws);
+  k_nms_rank<<<dim3(RANK_TILES * NMS_RANK_SPLIT, Bn), BLK, 0, st>>>(ws);
+  k_nms_layout<<<Bn, BLK, 0, st>>>(counts, A, 1, ws);
+  k_nms_masks_obb<<<dim3(MASK_BLOCKS, Bn), 256, 0, st>>>(ws, prm);
+  k_nms_fast<<<dim3(GREEDY_BLOCKS, Bn), 256, 0, st>>>(ws);
+  k_nms_emit<true><<<Bn, BLK, 0, st>>>(cand, counts, A, ws, out, outidx, outcnt, rawcnt, prm);
 }
 
 }  // namespace yolo
