@@ -89,6 +89,24 @@ int yolo_get_mask(void* h, int slot, int det, unsigned char* out);
                               launch) instead of the multi-block pipeline (six launches
                               spread over the GPU); identical results                      */
 
+/* Batch staging and fetch for servers (one call per batch instead of one per slot; the
+ * reference server stages and reads per slot, server/serve.cpp:264-302):
+ * yolo_stage_frames copies B raw u8 HWC frames of pixel layout `format` from host memory
+ * into the handle's own device staging buffers and letterboxes them (classify handles: the
+ * resize + centre crop) into slots 0..B-1, asynchronously on the engine stream; pinned host
+ * memory (yolo_host_alloc) makes the copies asynchronous, and it must stay valid until the
+ * stream passes them (e.g. the next yolo_sync).  Both layouts give identical results; RGBX
+ * is how image decoders hold RGB in memory, so a server can stage their buffer unconverted.
+ * Returns 0, or -1 on bad arguments.
+ * yolo_get_batch / yolo_get_obb_batch write slot s's detections (as yolo_get /
+ * yolo_get_obb) to out[s * cap ...] and their number to counts[s]; return the total. */
+#define YOLO_PIXEL_BGR 0   /* B, G, R bytes per pixel (the reference's cv::Mat layout)      */
+#define YOLO_PIXEL_RGBX 1  /* R, G, B, X bytes per pixel (X ignored)                        */
+int yolo_stage_frames(void* h, int B, const unsigned char* const* host, const int* heights,
+                      const int* widths, int format);
+int yolo_get_batch(void* h, int B, YoloDet* out, int cap, int* counts);
+int yolo_get_obb_batch(void* h, int B, YoloObbDet* out, int cap, int* counts);
+
 /* Error-returning create: NULL on failure with a message in err (if non-NULL). */
 void* yolo_create_ex(const char* model_dir, int max_batch, int flags, char* err, int errlen);
 /* The reference has no destroy (the handle lives until exit); this frees everything. */

@@ -191,3 +191,46 @@ def test_frame_graph_nms_variants(models):
     for b, e in zip(bufs, engs):
         b.free()
         e.close()
+
+
+@pytest.mark.parametrize("task", ["detect", "classify"])
+def test_stage_frames_layouts(models, task):
+    """yolo_stage_frames (the server's batch staging from pinned memory) letterboxes -- or, for
+    a classify handle, resizes and crops -- every slot exactly as the oracle does, from BGR
+    and from R, G, B, X frames alike; a later call with larger frames regrows the staging."""
+    if task == "detect":
+        d, S = models("yolo11", "n"), 640
+        want_fn = lambda im: post.letterbox(im, S, S)
+    else:
+        d, S = models("yolo11", "n", "classify", imgsz=224, nc=1000), 224
+        want_fn = lambda im: post.preprocess_cls(im, S)
+    eng = yolort.Engine(d, 4, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    pinned = []
+    for sizes in ([(333, 517), (640, 640), (810, 1080), (200, 90)],
+                  [(1080, 1920), (1200, 700), (480, 640)]):
+        frames = [modelgen.synth_frame(h, w, 12, h + 3 * w) for h, w in sizes]
+        want = [want_fn(im) for im in frames]
+        for fmt in (yolort.PIXEL_BGR, yolort.PIXEL_RGBX):
+            bufs = []
+            for im in frames:
+                if fmt == yolort.PIXEL_RGBX:
+                    im = np.concatenate([im[..., ::-1], np.full(im.shape[:2] + (1,), 201, np.uint8)], axis=2)
+                b = yolort.PinnedBuffer(im.shape)
+                b.array[...] = im
+                bufs.append(b)
+            print(f"stage {task} fmt {fmt} sizes {sizes}", flush=True)
+            eng.stage_frames([b.ptr for b in bufs], [h for h, _ in sizes], [w for _, w in sizes], fmt)
+            eng.sync()
+            got = eng.read(0, len(sizes))
+            for s in range(len(sizes)):
+                np.testing.assert_array_equal(got[s], want[s])
+                if task == "detect":
+                    g2 = post.letterbox_geom(S, S, *sizes[s])
+                    scale, top, left = eng.slot_geom(s)
+                    assert (np.float32(scale), top, left) == g2[:3]
+            pinned += bufs
+    with pytest.raises(RuntimeError):
+        eng.stage_frames([pinned[0].ptr], [333], [517], 7)      # unknown layout
+    for b in pinned:
+        b.free()
+    eng.close()

@@ -1,7 +1,12 @@
 """The gRPC server with real engines on the GPU: concurrent requests over 127.0.0.1 for a detect,
-a segment and a classify model in one process; every response is checked against a direct
+a segment and a classify model in one process.  Every response is checked against a direct
 engine handle run on the same decoded pixels, to the parity bar (same kept count, classes and
-order; box IoU >= 0.99, |d score| <= 5e-3; mask IoU >= 0.99; same top-5)."""
+order; box IoU >= 0.99, |d score| <= 5e-3; mask IoU >= 0.99; same top-5), and that direct
+run is itself held to the oracle: its input tensor equals the oracle's letterbox (classify:
+resize + crop) of the decoded image bit for bit, its detections equal the oracle's decode +
+NMS on the run's own head tensors exactly, its masks match the oracle's masks on the run's
+proto (IoU >= 0.99), and its top-5 is the oracle's top-k of the run's probabilities.  (The
+network between input and heads is held to the oracle op by op in test_gpu_configs.py.)"""
 import io
 from concurrent.futures import ThreadPoolExecutor
 
@@ -13,6 +18,7 @@ from PIL import Image
 import modelgen
 import yolort
 import yoloserve
+from oracle import graphfile, post
 
 pytestmark = pytest.mark.gpu
 FLAGS = yolort.YOLO_NOTUNE
@@ -25,7 +31,17 @@ def _encode(img_bgr, fmt):
     return buf.getvalue()
 
 
-def _direct(eng, img):
+def _to_original(geom, box):
+    """Net-space boxes to original-image coordinates with yolo_get's float32 operations."""
+    scale, top, left = (np.float32(v) for v in geom)
+    b = box.astype(np.float32)
+    return np.stack([(b[:, 0] - left) / scale, (b[:, 1] - top) / scale,
+                     (b[:, 2] - left) / scale, (b[:, 3] - top) / scale], 1).astype(np.float64)
+
+
+def _direct(eng, g, img):
+    """One frame through a direct handle (upload, preprocess, run), checked against the oracle
+    on that run's own tensors; returns the direct results."""
     dev = yolort.DeviceBuffer(img.nbytes)
     eng.upload(dev, img)
     h, w = img.shape[:2]
@@ -34,12 +50,33 @@ def _direct(eng, img):
     else:
         eng.preprocess(dev.ptr, h, w, 0)
     eng.run(1)
+    S = eng.read(0, 1).shape[1]
+    want_in = post.preprocess_cls(img, S) if eng.task() == 2 else post.letterbox(img, S, S)
+    np.testing.assert_array_equal(eng.read(0, 1)[0], want_in)
     out = {"boxes": eng.get(0) if eng.task() != 2 else None}
     if eng.task() == 2:
         out["cls"] = eng.get_cls(0, 5)
+        probs = eng.read([op.out for op in g.ops if op.kind == "SOFTMAX"][0], 1)[0, 0, 0].astype(np.float32)
+        wid, wpr = post.topk(probs, 5)
+        assert out["cls"][0].tolist() == wid.tolist()
+        np.testing.assert_array_equal(out["cls"][1], wpr)
+    else:
+        heads = [(eng.read(op.a, 1)[0].astype(np.float32), eng.read(op.b, 1)[0].astype(np.float32),
+                  eng.read(op.out, 1)[0].astype(np.float32) if op.kind == "DECODESEG" else None, op.stride)
+                 for op in g.ops if op.kind in ("DECODE", "DECODESEG")]
+        want = post.detect(heads, g.nc, 0.25, 0.45)
+        got = out["boxes"]
+        assert len(got) == len(want["score"])
+        np.testing.assert_array_equal(got[:, 5].astype(int), want["cls"])
+        np.testing.assert_allclose(got[:, 4], want["score"], rtol=0, atol=2e-6)
+        np.testing.assert_allclose(got[:, :4], _to_original(eng.slot_geom(0), want["box"]), rtol=0, atol=2e-3)
     if eng.task() == 3:
         out["masks"] = [eng.get_mask(0, j) for j in range(len(out["boxes"]))]
         out["geom"] = eng.slot_geom(0)
+        proto = eng.read([op.a for op in g.ops if op.kind == "MASKS"][0], 1)[0].astype(np.float32)
+        wm = post.masks(proto, want["coef"], want["box"], S, S)
+        for j, m in enumerate(out["masks"]):
+            assert _mask_iou(m, wm[j]) >= 0.99
     dev.free()
     return out
 
@@ -64,6 +101,7 @@ def test_server_matches_direct_engine(models):
     limits = {"det": 4, "seg": 2, "cls": 3}
     served = [yoloserve.Model(n, yolort.Engine(d, limits[n], FLAGS), limits[n]) for n, d in dirs.items()]
     direct = {n: yolort.Engine(d, 1, FLAGS) for n, d in dirs.items()}
+    graphs = {n: graphfile.load(d) for n, d in dirs.items()}
     srv = yoloserve.Server(served, target_ms=20.0, log=lambda *a: None)
     gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0")
     cl = yoloserve.Client(f"127.0.0.1:{port}")
@@ -78,7 +116,7 @@ def test_server_matches_direct_engine(models):
         for i, r in enumerate(resps):
             name = route[i] or "det"
             img = yoloserve.decode_image(payload[i])          # the server's own decoder
-            want = _direct(direct[name], img)
+            want = _direct(direct[name], graphs[name], img)
             assert 1 <= r.batch <= limits[name]
             if name == "cls":
                 assert r.task == "classify"

@@ -70,7 +70,7 @@ def server():
     names = ["det", "seg", "cls", "obb"]
     engs = [FakeEngine(0), FakeEngine(3), FakeEngine(2), FakeEngine(1)]
     srv = FakeServer([yoloserve.Model(n, e, 4) for n, e in zip(names, engs)], target_ms=20.0, log=lambda *a: None)
-    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0", workers=32)
+    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0", decoders=8)
     yield f"127.0.0.1:{port}"
     gs.stop(0)
     srv.stop()

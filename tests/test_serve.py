@@ -146,6 +146,66 @@ def test_decode_image_formats():
     assert yoloserve.decode_image(b"") is None
 
 
+class _ArrayPool:
+    """The pinned pool's take/give over plain numpy buffers."""
+
+    class Buf:
+        def __init__(self, n):
+            self.array = np.full(n, 77, np.uint8)
+
+    def __init__(self):
+        self.out = 0
+
+    def take(self, n):
+        self.out += 1
+        return self.Buf(n + 13)            # larger than asked, as pooled buffers are
+
+    def give(self, b):
+        self.out -= 1
+
+
+@pytest.mark.parametrize("mode", ["RGB", "L", "RGBA", "P"])
+@pytest.mark.parametrize("zero_copy", [True, False])
+def test_decode_rgbx_into(mode, zero_copy, monkeypatch):
+    rng = np.random.default_rng(5)
+    rgb = rng.integers(0, 256, (9, 13, 3), dtype=np.uint8)
+    im = Image.fromarray(rgb)
+    im = im.convert(mode) if mode != "RGBA" else Image.fromarray(np.dstack([rgb, rgb[..., :1]]), "RGBA")
+    buf = io.BytesIO()
+    im.save(buf, format="PNG")
+    want_rgb = np.asarray(im.convert("RGB"))
+    if not zero_copy:
+        monkeypatch.setattr(yoloserve, "_rgbx_view", lambda im, n: None)
+    else:
+        assert yoloserve._rgbx_view(im.convert("RGB"), 9 * 13) is not None   # PIL exports it here
+    pool = _ArrayPool()
+    got = yoloserve.decode_rgbx_into(buf.getvalue(), pool)
+    assert got is not None and pool.out == 1
+    b, hw = got
+    assert hw == (9, 13)
+    px = b.array[:9 * 13 * 4].reshape(9, 13, 4)
+    assert np.array_equal(px[..., :3], want_rgb)
+    # the same pixels as the BGR decode, channel-reversed
+    assert np.array_equal(px[..., 2::-1], yoloserve.decode_image(buf.getvalue()))
+    assert np.all(b.array[9 * 13 * 4:] == 77)                         # nothing past the frame
+
+
+def test_decode_rgbx_into_jpeg_and_failures():
+    rng = np.random.default_rng(6)
+    rgb = rng.integers(0, 256, (40, 56, 3), dtype=np.uint8)
+    buf = io.BytesIO()
+    Image.fromarray(rgb).save(buf, format="JPEG", quality=85)
+    pool = _ArrayPool()
+    b, hw = yoloserve.decode_rgbx_into(buf.getvalue(), pool)
+    assert hw == (40, 56)
+    px = b.array[:40 * 56 * 4].reshape(40, 56, 4)
+    assert np.array_equal(px[..., 2::-1], yoloserve.decode_image(buf.getvalue()))
+    pool = _ArrayPool()
+    assert yoloserve.decode_rgbx_into(b"not an image", pool) is None
+    assert yoloserve.decode_rgbx_into(b"", pool) is None
+    assert pool.out == 0
+
+
 # ------------------------------------------------------------------ gRPC round trip, fake engine
 
 class FakeEngine:
@@ -222,7 +282,7 @@ def test_grpc_roundtrip_fake_engines():
     engs = [FakeEngine(0), FakeEngine(3), FakeEngine(2), FakeEngine(1)]
     models = [yoloserve.Model(n, e, 4) for n, e in zip(names, engs)]
     srv = FakeServer(models, target_ms=40.0, log=lambda *a: None)
-    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0", workers=48)
+    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0", decoders=8)
     cl = yoloserve.Client(f"127.0.0.1:{port}")
     try:
         colors = [(10 + i, 20 + 2 * i, 30 + 3 * i) for i in range(24)]
@@ -292,6 +352,62 @@ def test_deadline_fires_partial_batch():
         assert eng.batches == [1]
         # fired after about target - exec - decode estimate - margin (30 - 0.5 - 2 - 1 ms)
         assert 15.0 <= waited <= 2000.0
-        assert req.resp.batch == 1 and req.resp.boxes[0].x1 == 5
+        got = req.message()
+        assert got.batch == 1 and got.boxes[0].x1 == 5
+    finally:
+        srv.stop()
+
+
+def test_wire_boxes_match_protobuf():
+    """The numpy wire encoding of boxes / rotated boxes parses to the same messages as the
+    protobuf-built ones: 1- and 2-byte class varints, zeros, negatives, fp32 rounding, empty
+    lists; ids beyond two varint bytes fall back (None)."""
+    rng = np.random.default_rng(3)
+    for n in (0, 1, 7, 300):
+        d = rng.normal(0, 500, (n, 6))
+        d[:, 5] = rng.integers(0, 1024, n)
+        if n:
+            d[0, :5] = 0.0
+            d[-1, 5] = 127
+        want = pb.DetectResponse(task="detect", batch=3)
+        for x1, y1, x2, y2, s, c in d.tolist():
+            want.boxes.add(x1=x1, y1=y1, x2=x2, y2=y2, score=s, cls=int(c))
+        got = pb.DetectResponse.FromString(pb.DetectResponse(task="detect", batch=3).SerializeToString() +
+                                           yoloserve.boxes_wire(d))
+        assert got == want
+        rb = rng.normal(0, 100, (n, 7))
+        rb[:, 6] = rng.integers(0, 200, n)
+        want = pb.DetectResponse()
+        for cx, cy, w, h, a, s, c in rb.tolist():
+            want.rboxes.add(cx=cx, cy=cy, w=w, h=h, angle=a, score=s, cls=int(c))
+        got = pb.DetectResponse.FromString(yoloserve.rboxes_wire(rb))
+        assert got == want
+    assert yoloserve.boxes_wire(np.array([[0, 0, 1, 1, 0.5, 1 << 14]], float)) is None
+    assert yoloserve.boxes_wire(np.array([[0, 0, 1, 1, 0.5, -1]], float)) is None
+
+
+class _FailingEngine(FakeEngine):
+    """Raises while fetching the results of its second batch."""
+
+    def get(self, slot):
+        if len(self.batches) >= 2:
+            raise RuntimeError("device lost")
+        return super().get(slot)
+
+
+def test_engine_failure_answers_every_request():
+    """An engine failure while finishing a batch answers that batch and the one collected
+    behind it with an error (no handler waits forever), and later requests fail fast."""
+    eng = _FailingEngine(0)
+    srv = FakeServer([yoloserve.Model("det", eng, 2)], target_ms=5.0, log=lambda *a: None)
+    try:
+        reqs = [srv.submit(_png((i, i, i))) for i in range(8)]
+        for r in reqs:
+            assert r.done.wait(10.0)
+        errs = [r.error for r in reqs]
+        assert any(e and e.startswith("engine failure") for e in errs)
+        assert all(e is None or e.startswith("engine failure") or e == "server shutting down" for e in errs)
+        late = srv.submit(_png((1, 2, 3)))
+        assert late.done.wait(1.0) and late.error == "server shutting down"
     finally:
         srv.stop()

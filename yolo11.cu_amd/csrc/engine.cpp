@@ -115,6 +115,8 @@ struct Engine {
   // previous frame had at most NMS_BLOCK_MAX candidates in every slot (the one launch beats
   // the multi-block pipeline's six on sparse frames; results are identical either way).
   hipGraphExec_t frameGraphBlock = nullptr;
+  std::vector<uint8_t*> stageDev;     // yolo_stage_frames: per-slot device copies of raw frames
+  std::vector<size_t> stageCap;
   bool capBlock = false;              // capture(): post() records the one-block NMS
   int frameB = 0;
   // the frame graph's device sources and sizes (for stage timing outside the graph)
@@ -145,6 +147,10 @@ struct Engine {
     for (auto& ge : graphs)
       if (ge) (void)hipGraphExecDestroy(ge);
     graphs.clear();
+    for (uint8_t* p : stageDev)
+      if (p) (void)hipFree(p);
+    stageDev.clear();
+    stageCap.clear();
     if (frameGraph) (void)hipGraphExecDestroy(frameGraph);
     if (frameGraphBlock) (void)hipGraphExecDestroy(frameGraphBlock);
     frameGraph = frameGraphBlock = nullptr;
@@ -873,17 +879,20 @@ struct Engine {
     return gr;
   }
 
+  // Frames in pixel layout fmt (PIXEL_BGR / PIXEL_RGBX); host[s], when given, is copied to
+  // the device source first.
   void preprocessFrames(int Bn, const std::vector<std::pair<const uint8_t*, SlotGeom>>& frames,
-                        const unsigned char* const* host, const int* hs, const int* ws) {
+                        const unsigned char* const* host, const int* hs, const int* ws, int fmt = PIXEL_BGR) {
     const BufDesc& ib = g.bufs[g.tens[0].buf];
     for (int s = 0; s < Bn; s++)
       if (host && host[s])
-        HCK(hipMemcpyAsync((void*)frames[s].first, host[s], (size_t)hs[s] * ws[s] * 3, hipMemcpyHostToDevice, st));
+        HCK(hipMemcpyAsync((void*)frames[s].first, host[s], (size_t)hs[s] * ws[s] * pixelBytes(fmt),
+                           hipMemcpyHostToDevice, st));
     if (g.cls) {
       for (int s = 0; s < Bn; s++) {
         const ClsGeom cg = clsGeom(ib.H, hs[s], ws[s]);
         launchPreprocessCls(frames[s].first, hs[s], ws[s], bufp[g.tens[0].buf] + (size_t)s * ib.H * ib.W * 3,
-                            ib.H, cg.rh, cg.rw, cg.top, cg.left, st);
+                            ib.H, cg.rh, cg.rw, cg.top, cg.left, fmt, st);
       }
       return;
     }
@@ -891,7 +900,7 @@ struct Engine {
     for (int s = 0; s < Bn; s++) {
       const SlotGeom& sg = frames[s].second;
       slots[s] = LetterboxSlot{frames[s].first, hs[s], ws[s], sg.top, sg.left, (int)roundf(hs[s] * sg.scale),
-                               (int)roundf(ws[s] * sg.scale), s, sg.scale};
+                               (int)roundf(ws[s] * sg.scale), s, sg.scale, fmt};
     }
     launchPreprocessBatch(slots.data(), Bn, bufp[g.tens[0].buf], ib.H, ib.W, st);
   }
@@ -1191,6 +1200,51 @@ int yolo_get(void* h, int slot, YoloDet* out, int cap) {
   return cnt;
 }
 
+int yolo_get_batch(void* h, int B, YoloDet* out, int cap, int* counts) {
+  Engine* e = E(h);
+  if (B < 1 || B > e->B || cap < 0) return 0;
+  int total = 0;
+  for (int s = 0; s < B; s++) total += counts[s] = yolo_get(h, s, out + (size_t)s * cap, cap);
+  return total;
+}
+
+static_assert(YOLO_PIXEL_BGR == yolo::PIXEL_BGR && YOLO_PIXEL_RGBX == yolo::PIXEL_RGBX, "pixel layouts");
+
+int yolo_stage_frames(void* h, int B, const unsigned char* const* host, const int* heights, const int* widths,
+                      int format) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (B < 1 || B > e->B || !host || (format != YOLO_PIXEL_BGR && format != YOLO_PIXEL_RGBX)) return -1;
+    if (e->g.bufs[e->g.tens[0].buf].C != 3) throw Failure("letterbox needs a 3-channel input tensor");
+    if (e->g.cls && e->g.bufs[e->g.tens[0].buf].H != e->g.bufs[e->g.tens[0].buf].W)
+      throw Failure("classify preprocess needs a square input");
+    for (int s = 0; s < B; s++)
+      if (!host[s] || heights[s] <= 0 || widths[s] <= 0) return -1;
+    if ((int)e->stageDev.size() < e->B) {
+      e->stageDev.resize(e->B, nullptr);
+      e->stageCap.resize(e->B, 0);
+    }
+    std::vector<std::pair<const uint8_t*, yolo::SlotGeom>> frames;
+    for (int s = 0; s < B; s++) {
+      const size_t bytes = (size_t)heights[s] * widths[s] * yolo::pixelBytes(format);
+      if (e->stageCap[s] < bytes) {   // grow: the stream may still read the old buffer
+        HCK(hipStreamSynchronize(e->st));
+        if (e->stageDev[s]) HCK(hipFree(e->stageDev[s]));
+        e->stageDev[s] = nullptr;
+        e->stageCap[s] = 0;
+        HCK(hipMalloc(&e->stageDev[s], bytes));
+        e->stageCap[s] = bytes;
+      }
+      const yolo::SlotGeom sg = e->geom(heights[s], widths[s]);
+      if (!e->g.cls) e->slots[s] = sg;
+      frames.push_back({e->stageDev[s], sg});
+    }
+    e->preprocessFrames(B, frames, host, heights, widths, format);
+    HCK(hipGetLastError());
+    return 0;
+  });
+}
+
 void yolo_preprocess_cls(void* h, const unsigned char* dev_bgr, int height, int width, int slot) {
   Engine* e = E(h);
   try {
@@ -1200,7 +1254,7 @@ void yolo_preprocess_cls(void* h, const unsigned char* dev_bgr, int height, int 
     if (ib.H != ib.W) throw Failure("classify preprocess needs a square input");
     const yolo::ClsGeom cg = yolo::clsGeom(ib.H, height, width);
     yolo::launchPreprocessCls(dev_bgr, height, width, e->bufp[e->g.tens[0].buf] + (size_t)slot * ib.H * ib.W * 3,
-                              ib.H, cg.rh, cg.rw, cg.top, cg.left, e->st);
+                              ib.H, cg.rh, cg.rw, cg.top, cg.left, yolo::PIXEL_BGR, e->st);
     HCK(hipGetLastError());
   } catch (const std::exception& ex) {
     fatal(ex);
@@ -1252,6 +1306,14 @@ int yolo_get_obb(void* h, int slot, YoloObbDet* out, int cap) {
                         d[3] / sm.scale, d[6], d[4], (int)d[5]};
   }
   return cnt;
+}
+
+int yolo_get_obb_batch(void* h, int B, YoloObbDet* out, int cap, int* counts) {
+  Engine* e = E(h);
+  if (B < 1 || B > e->B || cap < 0) return 0;
+  int total = 0;
+  for (int s = 0; s < B; s++) total += counts[s] = yolo_get_obb(h, s, out + (size_t)s * cap, cap);
+  return total;
 }
 
 void yolo_mask_dim(void* h, int* ph, int* pw) {

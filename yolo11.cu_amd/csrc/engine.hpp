@@ -218,16 +218,22 @@ void attentionInit();
 void launchAttention(const View& qkv, const View& y, int heads, int kd, int hd, int Bn,
                      hipStream_t st);
 // frame.hip
+// Source pixel layouts of the preprocess kernels: BGR u8 (3 bytes, the reference's cv::Mat
+// layout) or R, G, B, X u8 (4 bytes, how decoders such as PIL hold RGB images in memory).
+constexpr int PIXEL_BGR = 0, PIXEL_RGBX = 1;
+inline int pixelBytes(int fmt) { return fmt == PIXEL_RGBX ? 4 : 3; }
 void launchPreprocessCls(const uint8_t* src, int sh, int sw, f16* dst, int S, int rh, int rw, int top,
-                         int left, hipStream_t st);
+                         int left, int fmt, hipStream_t st);
 // Letterbox of several frames in one launch (the frame graph's prologue): per-slot source,
-// geometry and destination image index, passed by value in chunks of LETTERBOX_BATCH.
+// pixel layout, geometry and destination image index, passed by value in chunks of
+// LETTERBOX_BATCH.
 struct LetterboxSlot {
   const uint8_t* src;
   int sh, sw, top, left, nh, nw, index;
   float scale;
+  int fmt;
 };
-constexpr int LETTERBOX_BATCH = 64;   // 64 x 40 bytes of kernel arguments
+constexpr int LETTERBOX_BATCH = 64;   // 64 x 48 bytes of kernel arguments
 struct LetterboxBatch { LetterboxSlot slot[LETTERBOX_BATCH]; };
 void launchPreprocessBatch(const LetterboxSlot* slots, int n, f16* dst, int dh, int dw, hipStream_t st);
 void launchPreprocess(const uint8_t* src, int sh, int sw, f16* dst, int dh, int dw, float scale,

@@ -9,12 +9,18 @@ namespace yolo {
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 
 // ------------------------------------------------------------------ letterbox
-// BGR u8 HWC (sh x sw) -> RGB fp16 NHWC (dh x dw), /255, pad 114, bilinear with the
-// half-pixel map src = (dst + 0.5)/scale - 0.5 and replicate-clamped edges
+// Channel c (0 blue, 1 green, 2 red) of source pixel i in layout fmt (PIXEL_BGR: B, G, R;
+// PIXEL_RGBX: R, G, B, X).  Both layouts give the same values, so results do not depend on it.
+__device__ __forceinline__ float srcChan(const uint8_t* __restrict__ src, size_t i, int fmt, int c) {
+  return fmt == PIXEL_RGBX ? (float)src[i * 4 + (2 - c)] : (float)src[i * 3 + c];
+}
+
+// BGR (or RGBX) u8 HWC (sh x sw) -> RGB fp16 NHWC (dh x dw), /255, pad 114, bilinear with
+// the half-pixel map src = (dst + 0.5)/scale - 0.5 and replicate-clamped edges
 // (k_preprocess, engine/engine.cu:966-998).  One thread per destination pixel.
 // One letterbox output pixel: bilinear sample of the scaled image, pad 114 outside it, BGR ->
 // RGB, /255.
-__device__ __forceinline__ void letterboxPixel(const uint8_t* __restrict__ src, int sh, int sw,
+__device__ __forceinline__ void letterboxPixel(const uint8_t* __restrict__ src, int sh, int sw, int fmt,
                                                f16* __restrict__ dst, int dw, float scale, int top,
                                                int left, int nh, int nw, int idx) {
   const int x = idx % dw, y = idx / dw;
@@ -29,15 +35,17 @@ __device__ __forceinline__ void letterboxPixel(const uint8_t* __restrict__ src, 
     const int y1 = min(max(y0 + 1, 0), sh - 1), x1 = min(max(x0 + 1, 0), sw - 1);
     y0 = min(max(y0, 0), sh - 1);
     x0 = min(max(x0, 0), sw - 1);
-    const uint8_t* p00 = src + ((size_t)y0 * sw + x0) * 3;
-    const uint8_t* p01 = src + ((size_t)y0 * sw + x1) * 3;
-    const uint8_t* p10 = src + ((size_t)y1 * sw + x0) * 3;
-    const uint8_t* p11 = src + ((size_t)y1 * sw + x1) * 3;
+    const size_t i00 = (size_t)y0 * sw + x0, i01 = (size_t)y0 * sw + x1;
+    const size_t i10 = (size_t)y1 * sw + x0, i11 = (size_t)y1 * sw + x1;
     const float w00 = (1.f - wy) * (1.f - wx), w01 = (1.f - wy) * wx;
     const float w10 = wy * (1.f - wx), w11 = wy * wx;
-    b = (float)p00[0] * w00 + (float)p01[0] * w01 + (float)p10[0] * w10 + (float)p11[0] * w11;
-    g = (float)p00[1] * w00 + (float)p01[1] * w01 + (float)p10[1] * w10 + (float)p11[1] * w11;
-    r = (float)p00[2] * w00 + (float)p01[2] * w01 + (float)p10[2] * w10 + (float)p11[2] * w11;
+    float v[3];
+    for (int c = 0; c < 3; c++)
+      v[c] = srcChan(src, i00, fmt, c) * w00 + srcChan(src, i01, fmt, c) * w01 +
+             srcChan(src, i10, fmt, c) * w10 + srcChan(src, i11, fmt, c) * w11;
+    b = v[0];
+    g = v[1];
+    r = v[2];
   }
   f16* o = dst + (size_t)idx * 3;
   o[0] = (f16)(r / 255.f);
@@ -50,7 +58,7 @@ __global__ __launch_bounds__(256) void k_letterbox(const uint8_t* __restrict__ s
                                                    int top, int left, int nh, int nw) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= dh * dw) return;
-  letterboxPixel(src, sh, sw, dst, dw, scale, top, left, nh, nw, idx);
+  letterboxPixel(src, sh, sw, PIXEL_BGR, dst, dw, scale, top, left, nh, nw, idx);
 }
 
 // All frames of a batch in one launch (blockIdx.y = slot within the chunk); each slot has its
@@ -60,8 +68,8 @@ __global__ __launch_bounds__(256) void k_letterbox_batch(LetterboxBatch lb, f16*
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= dh * dw) return;
   const LetterboxSlot& s = lb.slot[blockIdx.y];
-  letterboxPixel(s.src, s.sh, s.sw, dst + (size_t)s.index * dh * dw * 3, dw, s.scale, s.top, s.left, s.nh,
-                 s.nw, idx);
+  letterboxPixel(s.src, s.sh, s.sw, s.fmt, dst + (size_t)s.index * dh * dw * 3, dw, s.scale, s.top, s.left,
+                 s.nh, s.nw, idx);
 }
 
 void launchPreprocess(const uint8_t* src, int sh, int sw, f16* dst, int dh, int dw, float scale,
@@ -79,7 +87,7 @@ void launchPreprocessBatch(const LetterboxSlot* slots, int n, f16* dst, int dh, 
 }
 
 // ------------------------------------------------------------------ classify preprocess
-// BGR u8 HWC (sh x sw) -> RGB fp16 NHWC (S x S), /255: resize the shortest edge to S with
+// BGR (or RGBX) u8 HWC (sh x sw) -> RGB fp16 NHWC (S x S), /255: resize the shortest edge to S with
 // the antialiased bilinear (triangle) filter of PIL / torchvision, whose support widens by
 // the scale when downscaling, then centre-crop S x S (k_preprocess_cls,
 // engine/engine.cu:1000-1034; the host gives the resized size rh x rw and the crop offsets).
@@ -87,7 +95,7 @@ void launchPreprocessBatch(const LetterboxSlot* slots, int n, f16* dst, int dh, 
 // reference's order so the fp32 result is reproducible bit for bit.
 __global__ __launch_bounds__(256) void k_preprocess_cls(const uint8_t* __restrict__ src, int sh, int sw,
                                                         f16* __restrict__ dst, int S, int rh, int rw,
-                                                        int top, int left) {
+                                                        int top, int left, int fmt) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= S * S) return;
   const int ox = idx % S, oy = idx / S;
@@ -103,13 +111,12 @@ __global__ __launch_bounds__(256) void k_preprocess_cls(const uint8_t* __restric
   float sb = 0.f, sg = 0.f, sr = 0.f;
   for (int i = ya; i < yb; i++) {
     const float wy = tri((float)i + 0.5f - cy, ry);
-    const uint8_t* row = src + (size_t)i * sw * 3;
     for (int j = xa; j < xb; j++) {
       const float w = wy * tri((float)j + 0.5f - cx, rx);
-      const uint8_t* px = row + (size_t)j * 3;
-      sb += w * (float)px[0];
-      sg += w * (float)px[1];
-      sr += w * (float)px[2];
+      const size_t px = (size_t)i * sw + j;
+      sb += w * srcChan(src, px, fmt, 0);
+      sg += w * srcChan(src, px, fmt, 1);
+      sr += w * srcChan(src, px, fmt, 2);
     }
   }
   const float inv = 1.f / (ny * nx * 255.f);
@@ -125,8 +132,8 @@ __global__ __launch_bounds__(256) void k_preprocess_cls(const uint8_t* __restric
 }
 
 void launchPreprocessCls(const uint8_t* src, int sh, int sw, f16* dst, int S, int rh, int rw, int top,
-                         int left, hipStream_t st) {
-  k_preprocess_cls<<<(S * S + 255) / 256, 256, 0, st>>>(src, sh, sw, dst, S, rh, rw, top, left);
+                         int left, int fmt, hipStream_t st) {
+  k_preprocess_cls<<<(S * S + 255) / 256, 256, 0, st>>>(src, sh, sw, dst, S, rh, rw, top, left, fmt);
 }
 
 // ------------------------------------------------------------------ decode

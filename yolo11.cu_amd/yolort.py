@@ -19,6 +19,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "yolo.h")
 
 YOLO_NOFUSE, YOLO_NOTUNE, YOLO_NOGRAPH, YOLO_BRANCHES, YOLO_DAGGRAPH, YOLO_NOGROUP = 1, 2, 4, 8, 16, 32
 YOLO_NMS_BLOCK = 64
+PIXEL_BGR, PIXEL_RGBX = 0, 1   # frame layouts of yolo_stage_frames (B,G,R / R,G,B,X bytes)
 CFG_HALO = 1000   # op config of the LDS-halo 3x3 kernel (small-channel stride-1 convs)
 OP_KINDS = ["CONV", "ADD", "MAXPOOL5", "UPSAMPLE2", "COPYC", "ATTN", "DECODE", "GAP", "SOFTMAX",
             "DECODEOBB", "PS2", "DECODESEG", "MASKS"]
@@ -51,6 +52,10 @@ _SIGS = {
     "yolo_run_async": (None, [C.c_void_p, C.c_int]),
     "yolo_sync": (None, [C.c_void_p]),
     "yolo_get": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(YoloDet), C.c_int]),
+    "yolo_stage_frames": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_void_p), C.POINTER(C.c_int),
+                                    C.POINTER(C.c_int), C.c_int]),
+    "yolo_get_batch": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(YoloDet), C.c_int, C.POINTER(C.c_int)]),
+    "yolo_get_obb_batch": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(YoloObbDet), C.c_int, C.POINTER(C.c_int)]),
     "yolo_preprocess_cls": (None, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "yolo_get_cls": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_float), C.c_int]),
     "yolo_slot_geom": (None, [C.c_void_p, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
@@ -295,6 +300,36 @@ class Engine:
     def get(self, slot: int = 0, cap: int = MAX_OUT) -> np.ndarray:
         """Survivors as rows (x1, y1, x2, y2, score, cls) in original-image coords."""
         return self._records(self.lib.yolo_get, YoloDet, 6, slot, cap)
+
+    def _records_batch(self, fn, struct, nf: int, B: int, cap: int) -> list[np.ndarray]:
+        key = (struct, cap * B)
+        buf = self._getbuf.get(key)
+        if buf is None:
+            buf = self._getbuf[key] = np.empty((B * cap, nf), np.float32)
+        counts = np.zeros(B, np.int32)
+        fn(self.h, B, buf.ctypes.data_as(C.POINTER(struct)), cap, counts.ctypes.data_as(C.POINTER(C.c_int)))
+        allr = buf.astype(np.float64)
+        allr[:, nf - 1] = buf.view(np.int32)[:, nf - 1]
+        return [allr[s * cap:s * cap + int(counts[s])] for s in range(B)]
+
+    def get_batch(self, B: int, cap: int = MAX_OUT) -> list[np.ndarray]:
+        """`get` of slots 0..B-1 in one call."""
+        return self._records_batch(self.lib.yolo_get_batch, YoloDet, 6, B, cap)
+
+    def get_obb_batch(self, B: int, cap: int = MAX_OUT) -> list[np.ndarray]:
+        """`get_obb` of slots 0..B-1 in one call."""
+        return self._records_batch(self.lib.yolo_get_obb_batch, YoloObbDet, 7, B, cap)
+
+    def stage_frames(self, host_ptrs, heights, widths, fmt: int = PIXEL_BGR):
+        """Copies raw frames of pixel layout `fmt` (PIXEL_BGR, PIXEL_RGBX) from host memory
+        (pinned: asynchronous) into the handle's staging buffers and letterboxes them into
+        slots 0..len-1 (async on the stream)."""
+        n = len(host_ptrs)
+        p = (C.c_void_p * n)(*host_ptrs)
+        hh = (C.c_int * n)(*heights)
+        ww = (C.c_int * n)(*widths)
+        if self.lib.yolo_stage_frames(self.h, n, p, hh, ww, fmt) != 0:
+            raise RuntimeError("yolo_stage_frames failed")
 
     def get_obb(self, slot: int = 0, cap: int = MAX_OUT) -> np.ndarray:
         """OBB survivors as rows (cx, cy, w, h, theta, score, cls) in original-image coords."""

@@ -15,9 +15,13 @@ the same C ABI; gRPC C++ and protoc are not available here):
   calibrated `yolo_exec_ms(maxB)`, a decode-time EMA and a 1 ms margin; batches never mix
   models (server/serve.cpp:163-191);
 * decode overlaps the GPU (server/serve.cpp:264-302), here one step earlier: every request
-  is decoded on its own gRPC handler thread as it arrives, so the batcher collects ready
-  pixels and the worker only stages them and launches, while the next batch's images decode
-  during the current batch's GPU time.  The decoder is PIL for every format (the reference
+  is decoded on its own gRPC handler thread as it arrives and its pixels copied, in the
+  decoder's own R, G, B, X layout, into a pinned host buffer (the GPU letterbox reads that
+  layout), so the batcher collects ready pixels and the worker only stages the batch (one
+  call: asynchronous copies + one batched letterbox), launches, and fetches every slot's
+  detections in one call, while the next batch's images decode during the current batch's
+  GPU time.  Each handler thread serializes its own response (the detection lists with
+  numpy), so the worker only reads results.  The decoder is PIL for every format (the reference
   decodes JPEG with nvJPEG and PNG with stb; pixel values of a lossy JPEG can differ by
   decoder).  An undecodable image is answered at once and never takes a batch slot;
 * responses carry the task's fields -- boxes, rotated boxes, top-5 classes, or boxes plus
@@ -32,7 +36,9 @@ gRPC handler threads only enqueue and wait.
 from __future__ import annotations
 
 import argparse
+import asyncio
 import collections
+import ctypes
 import io
 import json
 import os
@@ -46,6 +52,7 @@ import numpy as np
 import yoloproto as pb
 
 TASK_NAMES = {0: "detect", 1: "obb", 2: "classify", 3: "segment"}
+PIXEL_RGBX = 1           # yolo_stage_frames layout R, G, B, X (YOLO_PIXEL_RGBX)
 MAX_MSG = 64 << 20       # request size limit (server/serve.cpp:395)
 SAFETY_MS = 1.0
 
@@ -76,24 +83,142 @@ def rle_decode(runs, n: int) -> np.ndarray:
 
 
 def decode_image(data: bytes) -> np.ndarray | None:
-    """HxWx3 BGR u8 (the engine's input layout) from encoded image bytes, None if undecodable."""
+    """HxWx3 BGR u8 (the engine's input layout) from encoded image bytes, None if undecodable.
+    PIL packs the decoded RGB image as BGR in one pass (its raw "BGR" mode)."""
     try:
         from PIL import Image
         with Image.open(io.BytesIO(data)) as im:
             if im.mode != "RGB":
                 im = im.convert("RGB")
             w, h = im.size
-            rgb = np.frombuffer(im.tobytes(), np.uint8).reshape(h, w, 3)
-        if h < 1 or w < 1:
-            return None
-        # three plane copies: numpy runs them without the GIL, unlike a reversed-stride copy
-        bgr = np.empty_like(rgb)
-        bgr[..., 0] = rgb[..., 2]
-        bgr[..., 1] = rgb[..., 1]
-        bgr[..., 2] = rgb[..., 0]
-        return bgr
+            if h < 1 or w < 1:
+                return None
+            return np.frombuffer(im.tobytes("raw", "BGR"), np.uint8).reshape(h, w, 3)
     except Exception:
         return None
+
+
+# The Apache Arrow C data interface (its published, stable C ABI).  PIL (11.2+) exports an
+# RGB image's pixel memory through it without copying, as a fixed-size list of four u8 per
+# pixel (R, G, B, X): the server copies that straight into pinned memory, GIL released,
+# instead of packing BGR under the GIL (PIL's tobytes holds it for ~0.5 ms per 640x640 image,
+# which capped the whole server near 1.2k images/s).
+class _ArrowSchema(ctypes.Structure):
+    pass
+
+
+_ArrowSchema._fields_ = [("format", ctypes.c_char_p), ("name", ctypes.c_char_p), ("metadata", ctypes.c_char_p),
+                         ("flags", ctypes.c_int64), ("n_children", ctypes.c_int64),
+                         ("children", ctypes.POINTER(ctypes.POINTER(_ArrowSchema))),
+                         ("dictionary", ctypes.c_void_p), ("release", ctypes.c_void_p),
+                         ("private_data", ctypes.c_void_p)]
+
+
+class _ArrowArray(ctypes.Structure):
+    pass
+
+
+_ArrowArray._fields_ = [("length", ctypes.c_int64), ("null_count", ctypes.c_int64), ("offset", ctypes.c_int64),
+                        ("n_buffers", ctypes.c_int64), ("n_children", ctypes.c_int64),
+                        ("buffers", ctypes.POINTER(ctypes.c_void_p)),
+                        ("children", ctypes.POINTER(ctypes.POINTER(_ArrowArray))),
+                        ("dictionary", ctypes.c_void_p), ("release", ctypes.c_void_p),
+                        ("private_data", ctypes.c_void_p)]
+
+_capsule_ptr = ctypes.pythonapi.PyCapsule_GetPointer
+_capsule_ptr.restype = ctypes.c_void_p
+_capsule_ptr.argtypes = [ctypes.py_object, ctypes.c_char_p]
+
+
+def _rgbx_view(im, npix: int):
+    """(keepalive, u8 view of npix * 4 bytes) of an RGB PIL image's pixel memory, zero-copy;
+    None when PIL does not export it (older PIL, or an image held in several blocks).  The
+    view is valid while `keepalive` (the exported capsules, which release the export when
+    collected) is referenced."""
+    try:
+        caps = im.__arrow_c_array__()
+    except Exception:
+        return None
+    sch = _ArrowSchema.from_address(_capsule_ptr(caps[0], b"arrow_schema"))
+    arr = _ArrowArray.from_address(_capsule_ptr(caps[1], b"arrow_array"))
+    if sch.format != b"+w:4" or sch.n_children != 1 or sch.children[0].contents.format != b"C":
+        return None
+    if arr.length != npix or arr.null_count != 0 or arr.n_children != 1:
+        return None
+    ch = arr.children[0].contents
+    if ch.n_buffers != 2 or ch.null_count != 0 or not ch.buffers[1] or ch.length < (arr.offset + npix) * 4:
+        return None
+    ptr = ch.buffers[1] + ch.offset + arr.offset * 4
+    return caps, np.ctypeslib.as_array((ctypes.c_uint8 * (npix * 4)).from_address(ptr))
+
+
+def decode_rgbx_into(data: bytes, pool) -> tuple | None:
+    """Decodes encoded image bytes into a buffer taken from `pool` as R, G, B, X u8 HWC;
+    (buffer, (h, w)), or None if undecodable (the buffer then goes back)."""
+    try:
+        from PIL import Image
+        with Image.open(io.BytesIO(data)) as im:
+            if im.mode != "RGB":
+                im = im.convert("RGB")
+            w, h = im.size
+            if h < 1 or w < 1:
+                return None
+            im.load()                    # the decode itself runs with the GIL released
+            n = h * w * 4
+            buf = pool.take(n)
+            try:
+                view = _rgbx_view(im, h * w)
+                if view is not None:
+                    np.copyto(buf.array[:n], view[1])
+                    del view
+                else:
+                    np.copyto(buf.array[:n], np.frombuffer(im.tobytes("raw", "RGBX"), np.uint8))
+            except BaseException:
+                pool.give(buf)
+                raise
+            return buf, (h, w)
+    except Exception:
+        return None
+
+
+# Wire encoding of the repeated Box / RBox messages (proto/yolo.proto:14-33), built with numpy
+# instead of one protobuf object per detection: each entry is the field-1 (boxes) or field-6
+# (rboxes) tag, the submessage length, every float field as tag + 4 little-endian bytes and
+# the class as tag + varint.  Fields at their default value are written out too, which proto3
+# parsers accept.  Appending these bytes to a serialized DetectResponse adds the entries.
+def _entries_wire(outer_tag: int, floats: np.ndarray, cls: np.ndarray) -> bytes | None:
+    n, nf = floats.shape
+    if n == 0:
+        return b""
+    c = cls.astype(np.int64)
+    if c.min() < 0 or c.max() >= 1 << 14:
+        return None                       # 1- and 2-byte varints only
+    two = c >= 128
+    width = 2 + 5 * nf + 3
+    rows = np.zeros((n, width), np.uint8)
+    rows[:, 0] = outer_tag
+    rows[:, 1] = np.where(two, 5 * nf + 3, 5 * nf + 2)
+    f = np.ascontiguousarray(floats, dtype="<f4").view(np.uint8).reshape(n, nf, 4)
+    for q in range(nf):
+        rows[:, 2 + 5 * q] = ((q + 1) << 3) | 5            # fixed32
+        rows[:, 3 + 5 * q:7 + 5 * q] = f[:, q]
+    rows[:, 2 + 5 * nf] = (nf + 1) << 3                     # varint
+    rows[:, 3 + 5 * nf] = np.where(two, (c & 0x7F) | 0x80, c)
+    rows[:, 4 + 5 * nf] = c >> 7
+    keep = np.ones((n, width), bool)
+    keep[~two, width - 1] = False
+    return rows[keep].tobytes()
+
+
+def boxes_wire(dets: np.ndarray) -> bytes | None:
+    """`DetectResponse.boxes` entries for rows (x1, y1, x2, y2, score, cls); None if a class
+    id needs more than two varint bytes (the caller then uses protobuf)."""
+    return _entries_wire(0x0A, dets[:, :5], dets[:, 5])
+
+
+def rboxes_wire(rb: np.ndarray) -> bytes | None:
+    """`DetectResponse.rboxes` entries for rows (cx, cy, w, h, angle, score, cls)."""
+    return _entries_wire(0x32, rb[:, :6], rb[:, 6])
 
 
 def pick_queue(queues, now: float, target_ms: float, decode_ms: float, safety_ms: float = SAFETY_MS):
@@ -128,15 +253,76 @@ def parse_dir_spec(spec: str, max_batch: int) -> tuple[str, str, int]:
 
 # ------------------------------------------------------------------ server
 
-class _Request:
-    __slots__ = ("img", "arrival", "resp", "error", "done")
+class _PinnedPool:
+    """Pinned host buffers for decoded frames: a request's pixels go straight from the
+    decoder into one (on its handler thread), the worker stages a whole batch from them
+    with one asynchronous copy per frame, and they return here once the batch is done."""
 
     def __init__(self):
+        self.free: list = []
+        self.lock = threading.Lock()
+
+    def take(self, nbytes: int):
+        with self.lock:
+            for i, b in enumerate(self.free):
+                if b.array.nbytes >= nbytes:
+                    return self.free.pop(i)
+        import yolort
+        return yolort.PinnedBuffer((max(nbytes, 1 << 20),))
+
+    def give(self, b):
+        with self.lock:
+            self.free.append(b)
+
+    def close(self):
+        with self.lock:
+            for b in self.free:
+                b.free()
+            self.free.clear()
+
+
+class _Request:
+    """`resp` holds the response's small fields; `rows` the detections (boxes, or rotated
+    boxes if `obb`) that `payload()` encodes on the caller's thread, so the engine worker
+    never does it.  `payload()` is the serialized response, `message()` the parsed one.
+    The decoded pixels are `img` (numpy) or, with a pinned pool, `host` + `hw`."""
+    __slots__ = ("img", "host", "hw", "arrival", "resp", "rows", "obb", "error", "done", "on_done")
+
+    def __init__(self, on_done=None):
+        self.on_done = on_done
         self.img = None
+        self.host = None
+        self.hw = (0, 0)
         self.arrival = time.monotonic()
         self.resp = pb.DetectResponse()
+        self.rows = None
+        self.obb = False
         self.error = None
         self.done = threading.Event()
+
+    def finish(self):
+        """Marks the response (or error) ready: sets `done`, then calls `on_done` (the event
+        loop's wake-up for an asynchronous handler) if one was given."""
+        self.done.set()
+        if self.on_done is not None:
+            self.on_done()
+
+    def payload(self) -> bytes:
+        wire = b""
+        if self.rows is not None:
+            wire = (rboxes_wire if self.obb else boxes_wire)(self.rows)
+            if wire is None:                  # class ids beyond two varint bytes
+                if self.obb:
+                    for cx, cy, w, h, a, s, c in self.rows.tolist():
+                        self.resp.rboxes.add(cx=cx, cy=cy, w=w, h=h, angle=a, score=s, cls=int(c))
+                else:
+                    for x1, y1, x2, y2, s, c in self.rows.tolist():
+                        self.resp.boxes.add(x1=x1, y1=y1, x2=x2, y2=y2, score=s, cls=int(c))
+                self.rows, wire = None, b""
+        return self.resp.SerializeToString() + wire
+
+    def message(self):
+        return pb.DetectResponse.FromString(self.payload())
 
 
 class Model:
@@ -167,6 +353,8 @@ class Server:
         self.cv = threading.Condition()
         self.buffers: dict[int, object] = {}
         self.served = 0
+        # batch staging from pinned memory when every engine offers it (test fakes do not)
+        self.pool = _PinnedPool() if all(hasattr(m.eng, "stage_frames") for m in models) else None
         self._stop = False
         self._worker = threading.Thread(target=self._work, name="yoloserve-worker", daemon=True)
         self._worker.start()
@@ -198,24 +386,34 @@ class Server:
             raise KeyError(name)
         return self.by_name[name]
 
-    def submit(self, image: bytes, model: str = "") -> _Request:
-        """Decodes on the calling thread, then queues; the returned request's `done` is set
-        when its response (or error) is ready."""
+    def submit(self, image: bytes, model: str = "", on_done=None) -> _Request:
+        """Decodes on the calling thread, then queues; the returned request's `done` is set,
+        and `on_done()` called from the thread that completes it, when its response (or
+        error) is ready."""
         mi = self.model_index(model)
-        r = _Request()
-        r.img = decode_image(image)
-        if r.img is None:
+        r = _Request(on_done)
+        if self.pool is not None:
+            got = decode_rgbx_into(image, self.pool)
+            if got is not None:
+                r.host, r.hw = got
+        else:
+            r.img = decode_image(image)
+        if r.host is None and r.img is None:
             r.error = "image decode failed"
             r.resp.task = self.models[mi].task_name
-            r.done.set()
+            r.finish()
             return r
         with self.cv:
             if self._stop:
                 r.error = "server shutting down"
-                r.done.set()
+                r.finish()
                 return r
-            self.models[mi].queue.append(r)
-            self.cv.notify_all()
+            q = self.models[mi].queue
+            q.append(r)
+            # only a queue that starts (its slack now counts) or fills can change the
+            # batcher's decision; it sleeps until the least slack runs out otherwise
+            if len(q) == 1 or len(q) >= self.models[mi].max_batch:
+                self.cv.notify_all()
         return r
 
     # -- worker side
@@ -229,13 +427,14 @@ class Server:
                 pick, fire, slack = pick_queue(qs, time.monotonic(), self.target_ms, self.stage_ema)
                 if pick >= 0 and fire:
                     break
-                self.cv.wait(None if pick < 0 else min(max(slack, 0.0) * 1e-3, 2e-4))
+                self.cv.wait(None if pick < 0 else max(slack, 0.0) * 1e-3)
             m = self.models[pick]
             batch = [m.queue.popleft() for _ in range(min(len(m.queue), m.max_batch))]
         return pick, batch
 
     def _work(self):
         prev = None
+        batch = None          # collected and not yet launched
         try:
             while True:
                 got = self._collect()
@@ -247,13 +446,18 @@ class Server:
                     prev = None
                 m = self.models[mi]
                 t0 = time.monotonic()
-                for i, r in enumerate(batch):
-                    self._stage(m, i, r.img)
-                    r.img = None
+                if self.pool is not None:   # one call: async copies + one letterbox launch
+                    m.eng.stage_frames([r.host.ptr for r in batch], [r.hw[0] for r in batch],
+                                       [r.hw[1] for r in batch], PIXEL_RGBX)
+                else:
+                    for i, r in enumerate(batch):
+                        self._stage(m, i, r.img)
+                        r.img = None
                 launch = time.monotonic()
                 self.stage_ema = 0.9 * self.stage_ema + 0.1 * (launch - t0) * 1e3
                 m.eng.run_async(len(batch))
                 prev = (mi, batch, launch)
+                batch = None
                 with self.cv:
                     idle = all(not q.queue for q in self.models)
                 if idle:                  # no traffic behind it: answer now
@@ -261,10 +465,12 @@ class Server:
                     prev = None
         except Exception as ex:        # an engine failure fails everything in flight
             self.log(f"[serve] worker stopped: {ex!r}")
-            if prev is not None:
-                for r in prev[1]:
-                    r.error = f"engine failure: {ex}"
-                    r.done.set()
+            failed = (prev[1] if prev is not None else []) + (batch or [])
+            for r in failed:
+                r.error = f"engine failure: {ex}"
+                r.finish()
+            self._release(failed)
+            batch = None
             with self.cv:
                 self._stop = True
             prev = None
@@ -275,20 +481,35 @@ class Server:
                 while m.queue:
                     r = m.queue.popleft()
                     r.error = "server shutting down"
-                    r.done.set()
+                    self._release([r])
+                    r.finish()
+
+    def _release(self, batch: list):
+        if self.pool is not None:
+            for r in batch:
+                if r.host is not None:
+                    self.pool.give(r.host)
+                    r.host = None
 
     def _finish(self, mi: int, batch: list, launch: float):
         m = self.models[mi]
         m.eng.sync()
         infer_ms = (time.monotonic() - launch) * 1e3
+        self._release(batch)              # the stream has passed the staged frames
+        rows = None                       # every slot's records in one call
+        if self.pool is not None and m.task in (0, 3):
+            rows = m.eng.get_batch(len(batch))
+        elif self.pool is not None and m.task == 1:
+            rows = m.eng.get_obb_batch(len(batch))
         for i, r in enumerate(batch):
             resp = r.resp
             resp.task = m.task_name
-            self._fill(m, i, resp)
+            r.rows = self._fill(m, i, resp, None if rows is None else rows[i])
+            r.obb = m.task == 1
             resp.queue_ms = (launch - r.arrival) * 1e3
             resp.infer_ms = infer_ms
             resp.batch = len(batch)
-            r.done.set()
+            r.finish()
         before = self.served
         self.served += len(batch)
         if self.served // 5000 != before // 5000:
@@ -296,28 +517,29 @@ class Server:
                      f"({len(batch) * 1e3 / max(infer_ms, 1e-6):.0f} img/s in-batch)")
 
     @staticmethod
-    def _fill(m: Model, slot: int, resp):
+    def _fill(m: Model, slot: int, resp, rows=None):
+        """Reads what the response needs from the engine (worker thread): sets the classes,
+        masks and letterbox geometry on `resp` and returns the detection rows (None for
+        classify).  `rows`: the slot's records when already fetched for the whole batch."""
         eng = m.eng
         if m.task == 2:
             ids, probs = eng.get_cls(slot, 5)
             for c, p in zip(ids.tolist(), probs.tolist()):
                 resp.classes.add(id=int(c), prob=float(p))
-        elif m.task == 1:
-            for cx, cy, w, h, a, s, c in eng.get_obb(slot).tolist():
-                resp.rboxes.add(cx=cx, cy=cy, w=w, h=h, angle=a, score=s, cls=int(c))
-        else:
-            dets = eng.get(slot)
-            for x1, y1, x2, y2, s, c in dets.tolist():
-                resp.boxes.add(x1=x1, y1=y1, x2=x2, y2=y2, score=s, cls=int(c))
-            if m.task == 3:
-                resp.mask_h, resp.mask_w = m.mask_hw
-                resp.lb_scale, resp.lb_top, resp.lb_left = eng.slot_geom(slot)
-                for j in range(len(dets)):
-                    mk = eng.get_mask(slot, j)
-                    if mk is None:
-                        resp.masks.add()
-                    else:
-                        resp.masks.add(rle=rle_encode(mk).tolist())
+            return None
+        if m.task == 1:
+            return np.asarray(eng.get_obb(slot) if rows is None else rows)
+        dets = np.asarray(eng.get(slot) if rows is None else rows)
+        if m.task == 3:
+            resp.mask_h, resp.mask_w = m.mask_hw
+            resp.lb_scale, resp.lb_top, resp.lb_left = eng.slot_geom(slot)
+            for j in range(len(dets)):
+                mk = eng.get_mask(slot, j)
+                if mk is None:
+                    resp.masks.add()
+                else:
+                    resp.masks.add(rle=rle_encode(mk).tolist())
+        return dets
 
     def stop(self):
         with self.cv:
@@ -327,41 +549,119 @@ class Server:
         for b in self.buffers.values():
             b.free()
         self.buffers.clear()
+        if self.pool is not None:
+            self.pool.close()
 
 
 # ------------------------------------------------------------------ gRPC glue
 
-def grpc_server(server: Server, addr: str, workers: int | None = None):
-    """A started grpc.Server exposing `server` at `addr`; returns (grpc server, bound port)."""
-    import grpc
+def _default_decoders() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 4
+    return max(4, min(n, 32))
 
-    def detect(request, context):
+
+class _AioServer:
+    """A grpc.aio server on an event-loop thread of its own.  Each RPC decodes on a thread of
+    the decode pool (PIL's decode and the pixel copy run with the GIL released), waits for
+    its batch on the loop without holding a thread, and returns the response bytes the
+    request serialized.  `stop(grace)` and `wait_for_termination()` follow grpc.Server."""
+
+    def __init__(self, server: Server, addr: str, decoders: int):
+        self.server = server
+        self.decoders = ThreadPoolExecutor(max_workers=decoders, thread_name_prefix="yoloserve-decode")
+        self.loop = asyncio.new_event_loop()
+        self.port = 0
+        self._aio = None
+        self._error = None
+        started = threading.Event()
+        self._thread = threading.Thread(target=self._run, args=(addr, started), name="yoloserve-grpc", daemon=True)
+        self._thread.start()
+        started.wait()
+        if self._error is not None:
+            self._thread.join()
+            self.decoders.shutdown(wait=False)
+            raise self._error
+
+    def _run(self, addr: str, started: threading.Event):
+        asyncio.set_event_loop(self.loop)
         try:
-            r = server.submit(request.image, request.model)
-        except KeyError:
-            context.abort(grpc.StatusCode.INVALID_ARGUMENT, f"unknown model: {request.model}")
-        r.done.wait()
-        if r.error == "image decode failed":
-            context.abort(grpc.StatusCode.INVALID_ARGUMENT, r.error)
-        elif r.error:
-            context.abort(grpc.StatusCode.UNAVAILABLE, r.error)
-        return r.resp
+            self.loop.run_until_complete(self._start(addr))
+        except BaseException as ex:
+            self._error = ex if isinstance(ex, Exception) else RuntimeError(repr(ex))
+            started.set()
+            self.loop.close()
+            return
+        started.set()
+        try:
+            self.loop.run_forever()
+        finally:
+            self.loop.close()
 
-    handler = grpc.method_handlers_generic_handler(pb.SERVICE, {
-        pb.METHOD: grpc.unary_unary_rpc_method_handler(
-            detect, request_deserializer=pb.DetectRequest.FromString,
-            response_serializer=pb.DetectResponse.SerializeToString)})
-    # every in-flight request holds a handler thread while it waits for its batch
-    nthreads = workers or max(64, 4 * sum(m.max_batch for m in server.models))
-    gs = grpc.server(ThreadPoolExecutor(max_workers=nthreads),
-                     options=[("grpc.max_receive_message_length", MAX_MSG),
-                              ("grpc.max_send_message_length", MAX_MSG)])
-    gs.add_generic_rpc_handlers((handler,))
-    port = gs.add_insecure_port(addr)
-    if port == 0:
-        raise RuntimeError(f"cannot bind {addr}")
-    gs.start()
-    return gs, port
+    async def _start(self, addr: str):
+        import grpc
+        server, decoders = self.server, self.decoders
+
+        async def detect(request, context):
+            loop = asyncio.get_running_loop()
+            ready = loop.create_future()
+
+            def wake():                   # from the thread that completes the request
+                try:
+                    loop.call_soon_threadsafe(_resolve, ready)
+                except RuntimeError:      # the loop has already closed
+                    pass
+            try:
+                r = await loop.run_in_executor(decoders, server.submit, request.image, request.model, wake)
+            except KeyError:
+                await context.abort(grpc.StatusCode.INVALID_ARGUMENT, f"unknown model: {request.model}")
+            await ready
+            if r.error == "image decode failed":
+                await context.abort(grpc.StatusCode.INVALID_ARGUMENT, r.error)
+            elif r.error:
+                await context.abort(grpc.StatusCode.UNAVAILABLE, r.error)
+            return r.payload()
+
+        # responses leave the handler already serialized (bytes pass through unchanged)
+        handler = grpc.method_handlers_generic_handler(pb.SERVICE, {
+            pb.METHOD: grpc.unary_unary_rpc_method_handler(
+                detect, request_deserializer=pb.DetectRequest.FromString, response_serializer=None)})
+        self._aio = grpc.aio.server(options=[("grpc.max_receive_message_length", MAX_MSG),
+                                             ("grpc.max_send_message_length", MAX_MSG)])
+        self._aio.add_generic_rpc_handlers((handler,))
+        self.port = self._aio.add_insecure_port(addr)
+        if self.port == 0:
+            raise RuntimeError(f"cannot bind {addr}")
+        await self._aio.start()
+
+    def stop(self, grace: float | None = None):
+        if self.loop.is_closed():
+            return
+        try:
+            asyncio.run_coroutine_threadsafe(self._aio.stop(grace), self.loop).result(timeout=(grace or 0) + 30)
+        finally:
+            self.loop.call_soon_threadsafe(self.loop.stop)
+            self._thread.join()
+            self.decoders.shutdown(wait=True)
+
+    def wait_for_termination(self, timeout: float | None = None) -> bool:
+        self._thread.join(timeout)
+        return not self._thread.is_alive()
+
+
+def _resolve(fut):
+    if not fut.done():
+        fut.set_result(None)
+
+
+def grpc_server(server: Server, addr: str, decoders: int | None = None):
+    """A started gRPC server exposing `server` at `addr` (grpc.aio on its own event-loop
+    thread, decoding on a pool of `decoders` threads); returns (server handle, bound port).
+    The handle has grpc.Server's `stop(grace)` and `wait_for_termination()`."""
+    gs = _AioServer(server, addr, decoders or _default_decoders())
+    return gs, gs.port
 
 
 def load_models(specs: list[str], max_batch: int, log=print) -> list[Model]:
@@ -393,28 +693,34 @@ class Client:
 
 
 def bench(addr: str, images: list[bytes], model: str = "", concurrency: int = 32, seconds: float = 10.0) -> dict:
-    """Closed-loop load: `concurrency` callers each send the next image as soon as the last
-    answer arrives; returns throughput and latency percentiles."""
-    cl = Client(addr)
-    lat, batches, lock = [], [], threading.Lock()
-    stop_at = time.monotonic() + seconds
+    """Closed-loop load: `concurrency` callers (coroutines on one grpc.aio channel) each send
+    the next image as soon as the last answer arrives; returns throughput and latency
+    percentiles."""
+    import grpc
 
-    def caller(k):
-        i = k
-        while time.monotonic() < stop_at:
+    async def run():
+        lat, batches = [], []
+        async with grpc.aio.insecure_channel(addr, options=[("grpc.max_send_message_length", MAX_MSG),
+                                                            ("grpc.max_receive_message_length", MAX_MSG)]) as ch:
+            call = ch.unary_unary(pb.FULL_METHOD, request_serializer=pb.DetectRequest.SerializeToString,
+                                  response_deserializer=pb.DetectResponse.FromString)
+            reqs = [pb.DetectRequest(image=im, model=model) for im in images]
+            stop_at = time.monotonic() + seconds
+
+            async def caller(k):
+                i = k
+                while time.monotonic() < stop_at:
+                    t0 = time.monotonic()
+                    r = await call(reqs[i % len(reqs)], timeout=60.0)
+                    lat.append((time.monotonic() - t0) * 1e3)
+                    batches.append(r.batch)
+                    i += concurrency
+
             t0 = time.monotonic()
-            r = cl.detect(images[i % len(images)], model)
-            dt = (time.monotonic() - t0) * 1e3
-            with lock:
-                lat.append(dt)
-                batches.append(r.batch)
-            i += concurrency
+            await asyncio.gather(*(caller(k) for k in range(concurrency)))
+            return lat, batches, time.monotonic() - t0
 
-    t0 = time.monotonic()
-    with ThreadPoolExecutor(max_workers=concurrency) as ex:
-        list(ex.map(caller, range(concurrency)))
-    wall = time.monotonic() - t0
-    cl.close()
+    lat, batches, wall = asyncio.run(run())
     a = np.array(lat)
     return dict(requests=int(a.size), img_per_s=a.size / wall, p50_ms=float(np.percentile(a, 50)),
                 p99_ms=float(np.percentile(a, 99)), mean_batch=float(np.mean(batches)), concurrency=concurrency)
