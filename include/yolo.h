@@ -103,7 +103,42 @@ int yolo_get_mask(void* h, int slot, int det, unsigned char* out);
 #define YOLO_PIXEL_BGR 0   /* B, G, R bytes per pixel (the reference's cv::Mat layout)      */
 #define YOLO_PIXEL_RGBX 1  /* R, G, B, X bytes per pixel (X ignored)                        */
 int yolo_stage_frames(void* h, int B, const unsigned char* const* host, const int* heights,
-                      const int* widths, int format);
+                      const int* widths, int format, int first_slot);
+
+/* JPEG frames decoded by the engine, as the reference server does with nvJPEG (CPU Huffman
+ * across decoder threads, the rest on the GPU; server/serve.cpp:71-131): entropy decoding on
+ * the library's decoder threads (one stream per thread, YOLO_DECODE_THREADS or the process's
+ * CPUs up to 16), then dequantisation + IDCT, chroma upsampling and YCbCr -> RGB as GPU
+ * kernels, then the letterbox (classify: resize + crop) into slots first_slot..first_slot+B-1.
+ * The pixels equal PIL's / libjpeg-turbo's decode of the same bytes exactly (integer "islow"
+ * IDCT, "fancy" upsampling, 16-bit fixed-point colour).  Baseline / extended-sequential
+ * Huffman 8-bit streams with one scan, grayscale or YCbCr, chroma subsampled by at most 2
+ * each way; status[i] says whether stream i was staged, is outside that set (decode it
+ * another way and stage it with yolo_stage_frames), or is corrupt / truncated.  Returns when
+ * the entropy decoding is done (copies and kernels are queued on the engine stream): the
+ * number of streams not staged, or -1 on bad arguments.  heights / widths (optional) receive
+ * each staged stream's size.
+ * yolo_jpeg_probe reads only the headers: 1 = yolo_stage_jpeg decodes it (size in *height /
+ * *width), 0 = a JPEG outside that set, -1 = not a JPEG or a malformed header.
+ * yolo_jpeg_coefficients (host code only, no GPU) entropy-decodes a stream into its quantised
+ * coefficients, int16 in natural order, component plane after plane, block-row-major; returns
+ * the count (out == NULL: the count needed), -1 if unsupported / cap too small, -2 if corrupt. */
+#define YOLO_JPEG_STAGED 0
+#define YOLO_JPEG_UNSUPPORTED 1
+#define YOLO_JPEG_INVALID 2
+int yolo_stage_jpeg(void* h, int B, const unsigned char* const* data, const size_t* sizes, int first_slot,
+                    int* heights, int* widths, int* status);
+/* yolo_stage_jpeg in two steps, so a pipelined caller can decode the next batch while the
+ * current one runs and still read the current one's results (their letterbox geometry is
+ * the slots' until the next letterbox): yolo_decode_jpeg decodes into the slots' staging
+ * frames only (same arguments and return value); yolo_letterbox_decoded letterboxes the
+ * frames it left in slots first_slot..first_slot+B-1 (skipping slots whose decode failed or
+ * that were restaged since) and returns how many, or -1 on bad arguments. */
+int yolo_decode_jpeg(void* h, int B, const unsigned char* const* data, const size_t* sizes, int first_slot,
+                     int* heights, int* widths, int* status);
+int yolo_letterbox_decoded(void* h, int B, int first_slot);
+int yolo_jpeg_probe(const unsigned char* data, size_t size, int* height, int* width);
+long long yolo_jpeg_coefficients(const unsigned char* data, size_t size, short* out, size_t cap);
 int yolo_get_batch(void* h, int B, YoloDet* out, int cap, int* counts);
 int yolo_get_obb_batch(void* h, int B, YoloObbDet* out, int cap, int* counts);
 

@@ -34,6 +34,8 @@ SOURCES = {
     "frame.hip": DEV_FLAGS + ["-ffp-contract=off"],
     "nms.hip": DEV_FLAGS + ["-ffp-contract=off"],
     "noalloc.hip": DEV_FLAGS,
+    "jpeg.hip": DEV_FLAGS,
+    "jpeg.cpp": ["-O3"] + HOST_FLAGS[1:],
     "graph.cpp": HOST_FLAGS,
     "engine.cpp": HOST_FLAGS,
 }

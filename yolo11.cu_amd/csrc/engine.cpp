@@ -11,6 +11,7 @@
 // ([B][A][6 + nm] fp32) plus a key array ([B][A] fp32), so decode needs no counter reset
 // and no atomics, and every graph replay starts from a clean state.
 #include "engine.hpp"
+#include "jpeg.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -115,8 +116,24 @@ struct Engine {
   // previous frame had at most NMS_BLOCK_MAX candidates in every slot (the one launch beats
   // the multi-block pipeline's six on sparse frames; results are identical either way).
   hipGraphExec_t frameGraphBlock = nullptr;
-  std::vector<uint8_t*> stageDev;     // yolo_stage_frames: per-slot device copies of raw frames
+  std::vector<uint8_t*> stageDev;     // yolo_stage_frames / _jpeg: per-slot device raw frames
   std::vector<size_t> stageCap;
+  // yolo_stage_jpeg: two pinned staging areas (coefficients + descriptors) used in turn, each
+  // rewritten only after its last copy has run; the device mirror and the IDCT sample planes
+  struct JpegStage {
+    uint8_t* host = nullptr;
+    size_t cap = 0;
+    hipEvent_t copied = nullptr;
+    bool pending = false;
+  };
+  JpegStage jpegStage[2];
+  int jpegNext = 0;
+  uint8_t* jpegDev = nullptr;
+  size_t jpegDevCap = 0;
+  uint8_t* jpegSamples = nullptr;
+  size_t jpegSamplesCap = 0;
+  std::vector<int> jpegH, jpegW;       // per slot: the frame yolo_decode_jpeg left in its
+                                       // staging buffer (0: none / failed / overwritten)
   bool capBlock = false;              // capture(): post() records the one-block NMS
   int frameB = 0;
   // the frame graph's device sources and sizes (for stage timing outside the graph)
@@ -151,6 +168,16 @@ struct Engine {
       if (p) (void)hipFree(p);
     stageDev.clear();
     stageCap.clear();
+    for (JpegStage& js : jpegStage) {
+      if (js.copied) (void)hipEventSynchronize(js.copied);
+      if (js.host) (void)hipHostFree(js.host);
+      if (js.copied) (void)hipEventDestroy(js.copied);
+      js = JpegStage{};
+    }
+    if (jpegDev) (void)hipFree(jpegDev);
+    if (jpegSamples) (void)hipFree(jpegSamples);
+    jpegDev = jpegSamples = nullptr;
+    jpegDevCap = jpegSamplesCap = 0;
     if (frameGraph) (void)hipGraphExecDestroy(frameGraph);
     if (frameGraphBlock) (void)hipGraphExecDestroy(frameGraphBlock);
     frameGraph = frameGraphBlock = nullptr;
@@ -879,30 +906,87 @@ struct Engine {
     return gr;
   }
 
-  // Frames in pixel layout fmt (PIXEL_BGR / PIXEL_RGBX); host[s], when given, is copied to
-  // the device source first.
-  void preprocessFrames(int Bn, const std::vector<std::pair<const uint8_t*, SlotGeom>>& frames,
-                        const unsigned char* const* host, const int* hs, const int* ws, int fmt = PIXEL_BGR) {
+  void checkFrameInput() const {
     const BufDesc& ib = g.bufs[g.tens[0].buf];
-    for (int s = 0; s < Bn; s++)
-      if (host && host[s])
-        HCK(hipMemcpyAsync((void*)frames[s].first, host[s], (size_t)hs[s] * ws[s] * pixelBytes(fmt),
-                           hipMemcpyHostToDevice, st));
+    if (ib.C != 3) throw Failure("letterbox needs a 3-channel input tensor");
+    if (g.cls && ib.H != ib.W) throw Failure("classify preprocess needs a square input");
+  }
+
+  // A raw frame on the device, in pixel layout fmt, for input slot `slot`.
+  struct Staged {
+    int slot;
+    const uint8_t* src;
+    int h, w;
+    SlotGeom g;
+  };
+
+  // Letterbox (classify: resize + centre crop) of device frames into their input slots: one
+  // batched launch for detect-type graphs.
+  void preprocessStaged(const std::vector<Staged>& v, int fmt) {
+    const BufDesc& ib = g.bufs[g.tens[0].buf];
     if (g.cls) {
-      for (int s = 0; s < Bn; s++) {
-        const ClsGeom cg = clsGeom(ib.H, hs[s], ws[s]);
-        launchPreprocessCls(frames[s].first, hs[s], ws[s], bufp[g.tens[0].buf] + (size_t)s * ib.H * ib.W * 3,
-                            ib.H, cg.rh, cg.rw, cg.top, cg.left, fmt, st);
+      for (const Staged& f : v) {
+        const ClsGeom cg = clsGeom(ib.H, f.h, f.w);
+        launchPreprocessCls(f.src, f.h, f.w, bufp[g.tens[0].buf] + (size_t)f.slot * ib.H * ib.W * 3, ib.H, cg.rh,
+                            cg.rw, cg.top, cg.left, fmt, st);
       }
       return;
     }
-    std::vector<LetterboxSlot> slots(Bn);
+    std::vector<LetterboxSlot> slots;
+    slots.reserve(v.size());
+    for (const Staged& f : v)
+      slots.push_back(LetterboxSlot{f.src, f.h, f.w, f.g.top, f.g.left, (int)roundf(f.h * f.g.scale),
+                                    (int)roundf(f.w * f.g.scale), f.slot, f.g.scale, fmt});
+    launchPreprocessBatch(slots.data(), (int)slots.size(), bufp[g.tens[0].buf], ib.H, ib.W, st);
+  }
+
+  // Frames of slots 0..Bn-1 in pixel layout fmt (PIXEL_BGR / PIXEL_RGBX); host[s], when
+  // given, is copied to the device source first.
+  void preprocessFrames(int Bn, const std::vector<std::pair<const uint8_t*, SlotGeom>>& frames,
+                        const unsigned char* const* host, const int* hs, const int* ws, int fmt = PIXEL_BGR,
+                        int firstSlot = 0) {
+    std::vector<Staged> v;
     for (int s = 0; s < Bn; s++) {
-      const SlotGeom& sg = frames[s].second;
-      slots[s] = LetterboxSlot{frames[s].first, hs[s], ws[s], sg.top, sg.left, (int)roundf(hs[s] * sg.scale),
-                               (int)roundf(ws[s] * sg.scale), s, sg.scale, fmt};
+      if (host && host[s])
+        HCK(hipMemcpyAsync((void*)frames[s].first, host[s], (size_t)hs[s] * ws[s] * pixelBytes(fmt),
+                           hipMemcpyHostToDevice, st));
+      v.push_back(Staged{firstSlot + s, frames[s].first, hs[s], ws[s], frames[s].second});
     }
-    launchPreprocessBatch(slots.data(), Bn, bufp[g.tens[0].buf], ib.H, ib.W, st);
+    preprocessStaged(v, fmt);
+  }
+
+  // Device staging buffer of slot s with at least `bytes` (grown after the stream has passed
+  // the old one).
+  uint8_t* stageBuffer(int s, size_t bytes) {
+    if ((int)stageDev.size() < B) {
+      stageDev.resize(B, nullptr);
+      stageCap.resize(B, 0);
+    }
+    if (stageCap[s] < bytes) {
+      HCK(hipStreamSynchronize(st));
+      if (stageDev[s]) HCK(hipFree(stageDev[s]));
+      stageDev[s] = nullptr;
+      stageCap[s] = 0;
+      HCK(hipMalloc(&stageDev[s], bytes));
+      stageCap[s] = bytes;
+    }
+    return stageDev[s];
+  }
+
+  void forgetDecoded(int slot) {
+    if (slot < (int)jpegH.size()) jpegH[slot] = jpegW[slot] = 0;
+  }
+
+  // Grows a device buffer after the stream has passed the old one.
+  void growDevice(uint8_t*& p, size_t& cap, size_t bytes) {
+    if (cap >= bytes) return;
+    const size_t want = std::max(bytes, cap + cap / 2);
+    HCK(hipStreamSynchronize(st));
+    if (p) HCK(hipFree(p));
+    p = nullptr;
+    cap = 0;
+    HCK(hipMalloc(&p, want));
+    cap = want;
   }
 
   // Batch-Bn graph: [frame prologue] + network + post, by default one single-stream
@@ -1211,38 +1295,182 @@ int yolo_get_batch(void* h, int B, YoloDet* out, int cap, int* counts) {
 static_assert(YOLO_PIXEL_BGR == yolo::PIXEL_BGR && YOLO_PIXEL_RGBX == yolo::PIXEL_RGBX, "pixel layouts");
 
 int yolo_stage_frames(void* h, int B, const unsigned char* const* host, const int* heights, const int* widths,
-                      int format) {
+                      int format, int first_slot) {
   return guarded([&] {
     Engine* e = E(h);
-    if (B < 1 || B > e->B || !host || (format != YOLO_PIXEL_BGR && format != YOLO_PIXEL_RGBX)) return -1;
-    if (e->g.bufs[e->g.tens[0].buf].C != 3) throw Failure("letterbox needs a 3-channel input tensor");
-    if (e->g.cls && e->g.bufs[e->g.tens[0].buf].H != e->g.bufs[e->g.tens[0].buf].W)
-      throw Failure("classify preprocess needs a square input");
+    if (B < 1 || first_slot < 0 || first_slot + B > e->B || !host || !heights || !widths ||
+        (format != YOLO_PIXEL_BGR && format != YOLO_PIXEL_RGBX))
+      return -1;
+    e->checkFrameInput();
     for (int s = 0; s < B; s++)
       if (!host[s] || heights[s] <= 0 || widths[s] <= 0) return -1;
-    if ((int)e->stageDev.size() < e->B) {
-      e->stageDev.resize(e->B, nullptr);
-      e->stageCap.resize(e->B, 0);
-    }
     std::vector<std::pair<const uint8_t*, yolo::SlotGeom>> frames;
     for (int s = 0; s < B; s++) {
-      const size_t bytes = (size_t)heights[s] * widths[s] * yolo::pixelBytes(format);
-      if (e->stageCap[s] < bytes) {   // grow: the stream may still read the old buffer
-        HCK(hipStreamSynchronize(e->st));
-        if (e->stageDev[s]) HCK(hipFree(e->stageDev[s]));
-        e->stageDev[s] = nullptr;
-        e->stageCap[s] = 0;
-        HCK(hipMalloc(&e->stageDev[s], bytes));
-        e->stageCap[s] = bytes;
-      }
+      e->forgetDecoded(first_slot + s);
+      uint8_t* dev = e->stageBuffer(first_slot + s, (size_t)heights[s] * widths[s] * yolo::pixelBytes(format));
       const yolo::SlotGeom sg = e->geom(heights[s], widths[s]);
-      if (!e->g.cls) e->slots[s] = sg;
-      frames.push_back({e->stageDev[s], sg});
+      if (!e->g.cls) e->slots[first_slot + s] = sg;
+      frames.push_back({dev, sg});
     }
-    e->preprocessFrames(B, frames, host, heights, widths, format);
+    e->preprocessFrames(B, frames, host, heights, widths, format, first_slot);
     HCK(hipGetLastError());
     return 0;
   });
+}
+
+int yolo_jpeg_probe(const unsigned char* data, size_t size, int* height, int* width) {
+  if (!data) return -1;
+  yolo::jpeg::Header hd;
+  const int r = yolo::jpeg::parse(data, size, hd);
+  if (r == yolo::jpeg::OK) {
+    if (height) *height = hd.H;
+    if (width) *width = hd.W;
+  }
+  return r;
+}
+
+long long yolo_jpeg_coefficients(const unsigned char* data, size_t size, short* out, size_t cap) {
+  if (!data) return -1;
+  yolo::jpeg::Header hd;
+  if (yolo::jpeg::parse(data, size, hd) != yolo::jpeg::OK) return -1;
+  const size_t n = hd.blocks() * 64;
+  if (!out) return (long long)n;
+  if (cap < n) return -1;
+  return yolo::jpeg::decode(data, size, hd, out) ? (long long)n : -2;
+}
+
+int yolo_decode_jpeg(void* h, int B, const unsigned char* const* data, const size_t* sizes, int first_slot,
+                     int* heights, int* widths, int* status) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (B < 1 || first_slot < 0 || first_slot + B > e->B || !data || !sizes || !status) return -1;
+    e->checkFrameInput();
+    namespace J = yolo::jpeg;
+    std::vector<J::Header> hd(B);
+    std::vector<size_t> block0(B, 0);
+    size_t blocks = 0;
+    for (int i = 0; i < B; i++) {
+      const int r = data[i] ? J::parse(data[i], sizes[i], hd[i]) : J::INVALID;
+      status[i] = r == J::OK ? YOLO_JPEG_STAGED : r == J::UNSUPPORTED ? YOLO_JPEG_UNSUPPORTED : YOLO_JPEG_INVALID;
+      if (heights) heights[i] = r == J::OK ? hd[i].H : 0;
+      if (widths) widths[i] = r == J::OK ? hd[i].W : 0;
+      if (r == J::OK) {
+        block0[i] = blocks;
+        blocks += hd[i].blocks();
+      }
+    }
+    // pinned staging: [coefficients][plane descriptors][frame descriptors], 256-byte aligned
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t coefBytes = blocks * 64 * sizeof(int16_t);
+    const size_t planeOff = up(coefBytes), frameOff = up(planeOff + (size_t)3 * B * sizeof(yolo::JpegPlane));
+    const size_t total = up(frameOff + (size_t)B * sizeof(yolo::JpegFrame));
+    Engine::JpegStage& S = e->jpegStage[e->jpegNext];
+    e->jpegNext ^= 1;
+    if (S.pending) HCK(hipEventSynchronize(S.copied));   // its previous copy has run
+    S.pending = false;
+    if (S.cap < total) {
+      if (S.host) HCK(hipHostFree(S.host));
+      S.host = nullptr;
+      S.cap = 0;
+      const size_t want = std::max(total, (size_t)4 << 20);
+      HCK(hipHostMalloc((void**)&S.host, want, 0));
+      S.cap = want;
+    }
+    if (!S.copied) HCK(hipEventCreateWithFlags(&S.copied, hipEventDisableTiming));
+    int16_t* coef = reinterpret_cast<int16_t*>(S.host);
+    J::parallelFor(B, [&](int i) {
+      if (status[i] == YOLO_JPEG_STAGED && !J::decode(data[i], sizes[i], hd[i], coef + block0[i] * 64))
+        status[i] = YOLO_JPEG_INVALID;
+    });
+    // descriptors of the decoded streams; sample planes 256-byte aligned
+    auto* planes = reinterpret_cast<yolo::JpegPlane*>(S.host + planeOff);
+    auto* frames = reinterpret_cast<yolo::JpegFrame*>(S.host + frameOff);
+    int np = 0, nf = 0, maxPix = 0;
+    size_t sampleBytes = 0;
+    for (int i = 0; i < B; i++) {
+      if (status[i] != YOLO_JPEG_STAGED) continue;
+      const J::Header& H = hd[i];
+      const int slot = first_slot + i;
+      yolo::JpegFrame& F = frames[nf++];
+      std::memset(&F, 0, sizeof F);
+      F.dst = e->stageBuffer(slot, (size_t)H.H * H.W * 4);
+      F.H = H.H;
+      F.W = H.W;
+      F.nc = H.nc;
+      size_t b0 = block0[i];
+      for (int c = 0; c < H.nc; c++) {
+        const J::Comp& k = H.comp[c];
+        yolo::JpegPlane& P = planes[np++];
+        P.block0 = (uint32_t)b0;
+        P.bw = (uint16_t)k.bw;
+        P.bh = (uint16_t)k.bh;
+        P.out = (uint32_t)sampleBytes;
+        P.pad = 0;
+        std::memcpy(P.q, H.q[k.tq], sizeof P.q);
+        F.plane[c] = P.out;
+        F.stride[c] = k.bw * 8;
+        F.cw[c] = k.cw;
+        F.ch[c] = k.ch;
+        F.fh[c] = k.fh;
+        F.fv[c] = k.fv;
+        b0 += (size_t)k.bw * k.bh;
+        sampleBytes = up(sampleBytes + (size_t)k.bw * k.bh * 64);
+      }
+      maxPix = std::max(maxPix, H.H * H.W);
+    }
+    if (blocks >= (size_t)1 << 31 || sampleBytes >= (size_t)1 << 32)
+      throw Failure("JPEG batch too large");
+    if ((int)e->jpegH.size() < e->B) {
+      e->jpegH.resize(e->B, 0);
+      e->jpegW.resize(e->B, 0);
+    }
+    for (int i = 0; i < B; i++) {
+      const bool ok = status[i] == YOLO_JPEG_STAGED;
+      e->jpegH[first_slot + i] = ok ? hd[i].H : 0;
+      e->jpegW[first_slot + i] = ok ? hd[i].W : 0;
+    }
+    if (nf == 0) return B;
+    e->growDevice(e->jpegDev, e->jpegDevCap, total);
+    e->growDevice(e->jpegSamples, e->jpegSamplesCap, sampleBytes);
+    HCK(hipMemcpyAsync(e->jpegDev, S.host, total, hipMemcpyHostToDevice, e->st));
+    HCK(hipEventRecord(S.copied, e->st));
+    S.pending = true;
+    const auto* dCoef = reinterpret_cast<const int16_t*>(e->jpegDev);
+    const auto* dPlanes = reinterpret_cast<const yolo::JpegPlane*>(e->jpegDev + planeOff);
+    const auto* dFrames = reinterpret_cast<const yolo::JpegFrame*>(e->jpegDev + frameOff);
+    int nblocks = 0;
+    for (int i = 0; i < B; i++)
+      if (status[i] == YOLO_JPEG_STAGED) nblocks = (int)(block0[i] + hd[i].blocks());
+    yolo::launchJpegIdct(dCoef, dPlanes, np, nblocks, e->jpegSamples, e->st);
+    yolo::launchJpegColor(e->jpegSamples, dFrames, nf, maxPix, e->st);
+    HCK(hipGetLastError());
+    return B - nf;
+  });
+}
+
+int yolo_letterbox_decoded(void* h, int B, int first_slot) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (B < 1 || first_slot < 0 || first_slot + B > e->B) return -1;
+    e->checkFrameInput();
+    std::vector<Engine::Staged> v;
+    for (int s = first_slot; s < first_slot + B; s++) {
+      if (s >= (int)e->jpegH.size() || e->jpegH[s] <= 0) continue;
+      const yolo::SlotGeom sg = e->geom(e->jpegH[s], e->jpegW[s]);
+      if (!e->g.cls) e->slots[s] = sg;
+      v.push_back(Engine::Staged{s, e->stageDev[s], e->jpegH[s], e->jpegW[s], sg});
+    }
+    if (!v.empty()) e->preprocessStaged(v, yolo::PIXEL_RGBX);
+    HCK(hipGetLastError());
+    return (int)v.size();
+  });
+}
+
+int yolo_stage_jpeg(void* h, int B, const unsigned char* const* data, const size_t* sizes, int first_slot,
+                    int* heights, int* widths, int* status) {
+  const int failed = yolo_decode_jpeg(h, B, data, sizes, first_slot, heights, widths, status);
+  if (failed < 0 || failed == B) return failed;
+  return yolo_letterbox_decoded(h, B, first_slot) < 0 ? -1 : failed;
 }
 
 void yolo_preprocess_cls(void* h, const unsigned char* dev_bgr, int height, int width, int slot) {

@@ -234,6 +234,24 @@ struct LetterboxSlot {
   int fmt;
 };
 constexpr int LETTERBOX_BATCH = 64;   // 64 x 48 bytes of kernel arguments
+// jpeg.hip: the GPU half of the JPEG decode.  One descriptor per component plane (the IDCT
+// finds a block's plane by binary search over block0) and one per image (colour kernel).
+struct JpegPlane {
+  uint32_t block0;       // first block of the plane in the batch's coefficient array
+  uint16_t bw, bh;       // block grid
+  uint32_t out;          // byte offset of the plane's samples (stride bw * 8)
+  uint32_t pad;
+  uint16_t q[64];        // dequantisation table, natural order
+};
+struct JpegFrame {
+  uint8_t* dst;          // R, G, B, X frame, W * H * 4 bytes
+  int H, W, nc, pad;
+  uint32_t plane[3];     // sample offsets of Y, Cb, Cr
+  int stride[3], cw[3], ch[3], fh[3], fv[3];
+};
+void launchJpegIdct(const int16_t* coef, const JpegPlane* planes, int nplanes, int nblocks, uint8_t* samples,
+                    hipStream_t st);
+void launchJpegColor(const uint8_t* samples, const JpegFrame* frames, int nframes, int maxPixels, hipStream_t st);
 struct LetterboxBatch { LetterboxSlot slot[LETTERBOX_BATCH]; };
 void launchPreprocessBatch(const LetterboxSlot* slots, int n, f16* dst, int dh, int dw, hipStream_t st);
 void launchPreprocess(const uint8_t* src, int sh, int sw, f16* dst, int dh, int dw, float scale,

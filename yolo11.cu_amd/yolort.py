@@ -20,6 +20,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "yolo.h")
 YOLO_NOFUSE, YOLO_NOTUNE, YOLO_NOGRAPH, YOLO_BRANCHES, YOLO_DAGGRAPH, YOLO_NOGROUP = 1, 2, 4, 8, 16, 32
 YOLO_NMS_BLOCK = 64
 PIXEL_BGR, PIXEL_RGBX = 0, 1   # frame layouts of yolo_stage_frames (B,G,R / R,G,B,X bytes)
+JPEG_STAGED, JPEG_UNSUPPORTED, JPEG_INVALID = 0, 1, 2   # yolo_stage_jpeg per-stream status
 CFG_HALO = 1000   # op config of the LDS-halo 3x3 kernel (small-channel stride-1 convs)
 OP_KINDS = ["CONV", "ADD", "MAXPOOL5", "UPSAMPLE2", "COPYC", "ATTN", "DECODE", "GAP", "SOFTMAX",
             "DECODEOBB", "PS2", "DECODESEG", "MASKS"]
@@ -53,7 +54,14 @@ _SIGS = {
     "yolo_sync": (None, [C.c_void_p]),
     "yolo_get": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(YoloDet), C.c_int]),
     "yolo_stage_frames": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_void_p), C.POINTER(C.c_int),
-                                    C.POINTER(C.c_int), C.c_int]),
+                                    C.POINTER(C.c_int), C.c_int, C.c_int]),
+    "yolo_stage_jpeg": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t), C.c_int,
+                                  C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "yolo_decode_jpeg": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t), C.c_int,
+                                   C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "yolo_letterbox_decoded": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    "yolo_jpeg_probe": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "yolo_jpeg_coefficients": (C.c_longlong, [C.c_char_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "yolo_get_batch": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(YoloDet), C.c_int, C.POINTER(C.c_int)]),
     "yolo_get_obb_batch": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(YoloObbDet), C.c_int, C.POINTER(C.c_int)]),
     "yolo_preprocess_cls": (None, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
@@ -156,6 +164,28 @@ class DeviceBuffer:
             self.free()
         except Exception:
             pass
+
+
+def jpeg_probe(data: bytes) -> tuple[int, int, int]:
+    """(1 if yolo_stage_jpeg decodes it / 0 if a JPEG outside that set / -1 if not a JPEG,
+    height, width) from the stream's headers."""
+    h, w = C.c_int(0), C.c_int(0)
+    r = load().yolo_jpeg_probe(data, len(data), C.byref(h), C.byref(w))
+    return r, h.value, w.value
+
+
+def jpeg_coefficients(data: bytes) -> np.ndarray | None:
+    """The library's entropy decode (host code): int16 quantised coefficients, natural order,
+    plane after plane; None if unsupported, raises on a corrupt stream."""
+    lib = load()
+    n = lib.yolo_jpeg_coefficients(data, len(data), None, 0)
+    if n < 0:
+        return None
+    out = np.empty(n, np.int16)
+    r = lib.yolo_jpeg_coefficients(data, len(data), out.ctypes.data, n)
+    if r == -2:
+        raise ValueError("corrupt JPEG stream")
+    return out
 
 
 class PinnedBuffer:
@@ -320,16 +350,42 @@ class Engine:
         """`get_obb` of slots 0..B-1 in one call."""
         return self._records_batch(self.lib.yolo_get_obb_batch, YoloObbDet, 7, B, cap)
 
-    def stage_frames(self, host_ptrs, heights, widths, fmt: int = PIXEL_BGR):
+    def stage_frames(self, host_ptrs, heights, widths, fmt: int = PIXEL_BGR, first_slot: int = 0):
         """Copies raw frames of pixel layout `fmt` (PIXEL_BGR, PIXEL_RGBX) from host memory
         (pinned: asynchronous) into the handle's staging buffers and letterboxes them into
-        slots 0..len-1 (async on the stream)."""
+        slots first_slot.. (async on the stream)."""
         n = len(host_ptrs)
         p = (C.c_void_p * n)(*host_ptrs)
         hh = (C.c_int * n)(*heights)
         ww = (C.c_int * n)(*widths)
-        if self.lib.yolo_stage_frames(self.h, n, p, hh, ww, fmt) != 0:
+        if self.lib.yolo_stage_frames(self.h, n, p, hh, ww, fmt, first_slot) != 0:
             raise RuntimeError("yolo_stage_frames failed")
+
+    def _jpeg(self, fn, streams, first_slot):
+        n = len(streams)
+        data = (C.c_char_p * n)(*streams)
+        sizes = (C.c_size_t * n)(*[len(b) for b in streams])
+        hh, ww, st = (C.c_int * n)(), (C.c_int * n)(), (C.c_int * n)()
+        if fn(self.h, n, data, sizes, first_slot, hh, ww, st) < 0:
+            raise RuntimeError(f"{fn.__name__} failed")
+        return [(st[i], hh[i], ww[i]) for i in range(n)]
+
+    def stage_jpeg(self, streams: list[bytes], first_slot: int = 0):
+        """Decodes JPEG streams on the engine (entropy decoding on the library's threads, the
+        rest on the GPU) and letterboxes them into slots first_slot..; returns per-stream
+        (status, height, width), status JPEG_STAGED / JPEG_UNSUPPORTED / JPEG_INVALID."""
+        return self._jpeg(self.lib.yolo_stage_jpeg, streams, first_slot)
+
+    def decode_jpeg(self, streams: list[bytes], first_slot: int = 0):
+        """The decode half of stage_jpeg: the slots' staging frames only (no letterbox, slot
+        geometry unchanged); letterbox_decoded finishes the staging."""
+        return self._jpeg(self.lib.yolo_decode_jpeg, streams, first_slot)
+
+    def letterbox_decoded(self, n: int, first_slot: int = 0) -> int:
+        r = self.lib.yolo_letterbox_decoded(self.h, n, first_slot)
+        if r < 0:
+            raise RuntimeError("yolo_letterbox_decoded failed")
+        return r
 
     def get_obb(self, slot: int = 0, cap: int = MAX_OUT) -> np.ndarray:
         """OBB survivors as rows (cx, cy, w, h, theta, score, cls) in original-image coords."""

@@ -285,12 +285,14 @@ class _Request:
     """`resp` holds the response's small fields; `rows` the detections (boxes, or rotated
     boxes if `obb`) that `payload()` encodes on the caller's thread, so the engine worker
     never does it.  `payload()` is the serialized response, `message()` the parsed one.
-    The decoded pixels are `img` (numpy) or, with a pinned pool, `host` + `hw`."""
-    __slots__ = ("img", "host", "hw", "arrival", "resp", "rows", "obb", "error", "done", "on_done")
+    The image is `jpeg` (a stream the engine decodes itself) + `hw`, or decoded pixels:
+    `img` (numpy) or, with a pinned pool, `host` + `hw`."""
+    __slots__ = ("img", "host", "jpeg", "hw", "arrival", "resp", "rows", "obb", "error", "done", "on_done")
 
     def __init__(self, on_done=None):
         self.on_done = on_done
         self.img = None
+        self.jpeg = None
         self.host = None
         self.hw = (0, 0)
         self.arrival = time.monotonic()
@@ -353,8 +355,10 @@ class Server:
         self.cv = threading.Condition()
         self.buffers: dict[int, object] = {}
         self.served = 0
-        # batch staging from pinned memory when every engine offers it (test fakes do not)
+        # batch staging from pinned memory when every engine offers it (test fakes do not),
+        # and JPEG streams decoded by the engines themselves when they all can
         self.pool = _PinnedPool() if all(hasattr(m.eng, "stage_frames") for m in models) else None
+        self.engine_jpeg = self.pool is not None and all(hasattr(m.eng, "stage_jpeg") for m in models)
         self._stop = False
         self._worker = threading.Thread(target=self._work, name="yoloserve-worker", daemon=True)
         self._worker.start()
@@ -386,19 +390,32 @@ class Server:
             raise KeyError(name)
         return self.by_name[name]
 
-    def submit(self, image: bytes, model: str = "", on_done=None) -> _Request:
-        """Decodes on the calling thread, then queues; the returned request's `done` is set,
-        and `on_done()` called from the thread that completes it, when its response (or
-        error) is ready."""
+    def engine_decodes(self, image: bytes):
+        """(height, width) if the engines decode this stream themselves (a JPEG inside their
+        decoder's set: entropy decoding on the library's threads, the rest on the GPU), else
+        None (PIL decodes it).  Reads only the headers."""
+        if not self.engine_jpeg or image[:2] != b"\xff\xd8":
+            return None
+        import yolort
+        ok, h, w = yolort.jpeg_probe(image)
+        return (h, w) if ok == 1 else None
+
+    def submit(self, image: bytes, model: str = "", on_done=None, engine_hw=None) -> _Request:
+        """Queues a request; the returned request's `done` is set, and `on_done()` called from
+        the thread that completes it, when its response (or error) is ready.  With
+        `engine_hw` (from engine_decodes) the stream goes to the engine as it is; otherwise
+        it is decoded here, on the calling thread."""
         mi = self.model_index(model)
         r = _Request(on_done)
-        if self.pool is not None:
+        if engine_hw is not None:
+            r.jpeg, r.hw = image, engine_hw
+        elif self.pool is not None:
             got = decode_rgbx_into(image, self.pool)
             if got is not None:
                 r.host, r.hw = got
         else:
             r.img = decode_image(image)
-        if r.host is None and r.img is None:
+        if r.jpeg is None and r.host is None and r.img is None:
             r.error = "image decode failed"
             r.resp.task = self.models[mi].task_name
             r.finish()
@@ -441,20 +458,41 @@ class Server:
                 if got is None:
                     break
                 mi, batch = got
+                m = self.models[mi]
+                t0 = time.monotonic()
+                jp = []
+                if self.pool is not None:
+                    # engine-decoded JPEG streams take the first slots, decoded pixels the
+                    # rest.  The JPEG entropy decoding runs now, while the previous batch is
+                    # still on the GPU; the letterbox (which sets the slots' geometry, still
+                    # the previous batch's until its results are read) waits for _finish.
+                    jp = [r for r in batch if r.jpeg is not None]
+                    px = [r for r in batch if r.jpeg is None]
+                    batch = jp + px
+                    if jp:
+                        res = m.eng.decode_jpeg([r.jpeg for r in jp], 0)
+                        for r, (st, _, _) in zip(jp, res):
+                            r.jpeg = None
+                            if st != 0:
+                                r.error = "image decode failed"
+                stage_ms = (time.monotonic() - t0) * 1e3
                 if prev is not None:
                     self._finish(*prev)
                     prev = None
-                m = self.models[mi]
-                t0 = time.monotonic()
-                if self.pool is not None:   # one call: async copies + one letterbox launch
-                    m.eng.stage_frames([r.host.ptr for r in batch], [r.hw[0] for r in batch],
-                                       [r.hw[1] for r in batch], PIXEL_RGBX)
+                t1 = time.monotonic()
+                if self.pool is not None:
+                    if jp:
+                        m.eng.letterbox_decoded(len(jp), 0)
+                    if px:                # one call: async copies + one letterbox launch
+                        m.eng.stage_frames([r.host.ptr for r in px], [r.hw[0] for r in px],
+                                           [r.hw[1] for r in px], PIXEL_RGBX, len(jp))
                 else:
                     for i, r in enumerate(batch):
                         self._stage(m, i, r.img)
                         r.img = None
                 launch = time.monotonic()
-                self.stage_ema = 0.9 * self.stage_ema + 0.1 * (launch - t0) * 1e3
+                stage_ms += (launch - t1) * 1e3
+                self.stage_ema = 0.9 * self.stage_ema + 0.1 * stage_ms
                 m.eng.run_async(len(batch))
                 prev = (mi, batch, launch)
                 batch = None
@@ -504,6 +542,9 @@ class Server:
         for i, r in enumerate(batch):
             resp = r.resp
             resp.task = m.task_name
+            if r.error:                   # its slot ran on whatever it held
+                r.finish()
+                continue
             r.rows = self._fill(m, i, resp, None if rows is None else rows[i])
             r.obb = m.task == 1
             resp.queue_ms = (launch - r.arrival) * 1e3
@@ -614,7 +655,11 @@ class _AioServer:
                 except RuntimeError:      # the loop has already closed
                     pass
             try:
-                r = await loop.run_in_executor(decoders, server.submit, request.image, request.model, wake)
+                hw = server.engine_decodes(request.image)
+                if hw is not None:        # the engine decodes it: nothing to do off the loop
+                    r = server.submit(request.image, request.model, wake, hw)
+                else:
+                    r = await loop.run_in_executor(decoders, server.submit, request.image, request.model, wake)
             except KeyError:
                 await context.abort(grpc.StatusCode.INVALID_ARGUMENT, f"unknown model: {request.model}")
             await ready
