@@ -346,7 +346,8 @@ def bench_conv(workdir, iters):
 
 def bench_serve(workdir, seconds=4.0, procs=4, callers=16):
     """The gRPC server (yoloserve) with yolo11n, max batch 16, target 50 ms (the reference
-    server's defaults, server/serve.cpp:344-346), decode on the request threads, under a closed loop of
+    server's defaults, server/serve.cpp:344-346), JPEG decoded on the engine (entropy decoding
+    on the library's decoder threads, the rest on the GPU), under a closed loop of
     `procs` client processes x `callers` threads sending 640x640 JPEG frames over 127.0.0.1.
     Throughput is the sum over the client processes; p50 is the median of their medians,
     p99 the worst of their p99s."""
@@ -392,7 +393,53 @@ def bench_serve(workdir, seconds=4.0, procs=4, callers=16):
     return dict(clients=procs * callers, client_procs=procs, img_per_s=sum(r["img_per_s"] for r in res),
                 p50_ms=float(np.median([r["p50_ms"] for r in res])), p99_ms=max(r["p99_ms"] for r in res),
                 mean_batch=float(np.mean([r["mean_batch"] for r in res])), requests=sum(r["requests"] for r in res),
-                exec_ms_b16=round(models[0].exec_ms, 4), frames="640x640 JPEG q90, decoded by PIL on the server")
+                exec_ms_b16=round(models[0].exec_ms, 4), frames="640x640 JPEG q90, decoded on the engine",
+                decoder_threads=yolort.decoder_threads())
+
+
+def bench_jpeg(workdir, batches=60, graphs=True):
+    """JPEG decode on the engine for a batch of 16 640x640 q90 frames (the server bench's
+    frames): yolo_stage_jpeg wall time per batch with the GPU drained (entropy decoding on the
+    library's decoder threads, then H2D of the coefficients, IDCT, colour and the letterbox),
+    the single-thread entropy decode of one frame, and PIL's full decode of one frame for
+    comparison (the server's decoder for everything the engine does not decode)."""
+    import io
+    import modelgen
+    import yolort
+    from PIL import Image
+    d = os.path.join(workdir, "yolo11n_jpeg")
+    modelgen.write_model(d, "yolo11", "n", cls_bias=-8.0)
+    streams = []
+    for i in range(16):
+        b = io.BytesIO()
+        Image.fromarray(modelgen.synth_frame(640, 640, 50, 500 + i)[..., ::-1].copy()).save(b, "JPEG", quality=90)
+        streams.append(b.getvalue())
+    eng = yolort.Engine(d, 16, yolort.YOLO_NOTUNE | (0 if graphs else yolort.YOLO_NOGRAPH))
+    try:
+        for _ in range(5):
+            eng.stage_jpeg(streams)
+        eng.sync()
+        t0 = time.perf_counter()
+        for _ in range(batches):
+            eng.stage_jpeg(streams)
+            eng.sync()
+        ms = (time.perf_counter() - t0) / batches * 1e3
+    finally:
+        eng.close()
+    one = streams[0]
+    yolort.jpeg_coefficients(one)
+    t0 = time.perf_counter()
+    for _ in range(50):
+        yolort.jpeg_coefficients(one)
+    entropy_ms = (time.perf_counter() - t0) / 50 * 1e3
+    t0 = time.perf_counter()
+    for _ in range(20):
+        with Image.open(io.BytesIO(one)) as im:
+            im.load()
+    pil_ms = (time.perf_counter() - t0) / 20 * 1e3
+    return dict(ms_per_batch16=round(ms, 4), img_per_s=round(16e3 / ms, 1), decoder_threads=yolort.decoder_threads(),
+                entropy_ms_one_frame_one_thread=round(entropy_ms, 4), pil_decode_ms_one_frame=round(pil_ms, 4),
+                frames="640x640 JPEG q90 4:2:0, ~69 KB")
 
 
 def cpu_baseline(budget_s=15.0):
@@ -451,7 +498,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "n", "x", "conv", "obb", "seg", "m", "sweep", "cls", "serve"],
+    ap.add_argument("--only", choices=["all", "n", "x", "conv", "obb", "seg", "m", "sweep", "cls", "serve", "jpeg"],
                     default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
@@ -500,6 +547,10 @@ def main():
             out["seg"] = bench_task(workdir, "segment", 640, 80, -8.0, modelgen.synth_polygons(640, 640, 30, 4),
                                     args.steps, args.warmup, not args.no_graph)
             log(out["seg"])
+    if args.only in ("all", "jpeg"):
+        log("JPEG decode on the engine, batch 16 ...")
+        out["jpeg"] = bench_jpeg(workdir, graphs=not args.no_graph)
+        log(out["jpeg"])
     if args.only in ("all", "serve") and not args.no_graph:
         log("gRPC server, yolo11n, 4 client processes x 16 callers ...")
         out["serve"] = bench_serve(workdir)
@@ -554,6 +605,8 @@ def main():
                                       "top1": r["top1"]}
     if out.get("sweep"):
         line["conv_sweep"] = out["sweep"]
+    if out.get("jpeg"):
+        line["jpeg_decode_b16"] = out["jpeg"]
     if out.get("serve"):
         line["grpc_server_yolo11n"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                        for k, v in out["serve"].items()}

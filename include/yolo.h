@@ -138,6 +138,8 @@ int yolo_decode_jpeg(void* h, int B, const unsigned char* const* data, const siz
                      int* heights, int* widths, int* status);
 int yolo_letterbox_decoded(void* h, int B, int first_slot);
 int yolo_jpeg_probe(const unsigned char* data, size_t size, int* height, int* width);
+/* Threads (the calling one included) the JPEG entropy decoding runs on. */
+int yolo_decoder_threads(void);
 long long yolo_jpeg_coefficients(const unsigned char* data, size_t size, short* out, size_t cap);
 int yolo_get_batch(void* h, int B, YoloDet* out, int cap, int* counts);
 int yolo_get_obb_batch(void* h, int B, YoloObbDet* out, int cap, int* counts);

@@ -1329,6 +1329,8 @@ int yolo_jpeg_probe(const unsigned char* data, size_t size, int* height, int* wi
   return r;
 }
 
+int yolo_decoder_threads(void) { return yolo::jpeg::decoderThreads(); }
+
 long long yolo_jpeg_coefficients(const unsigned char* data, size_t size, short* out, size_t cap) {
   if (!data) return -1;
   yolo::jpeg::Header hd;

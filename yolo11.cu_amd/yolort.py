@@ -60,6 +60,7 @@ _SIGS = {
     "yolo_decode_jpeg": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t), C.c_int,
                                    C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "yolo_letterbox_decoded": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    "yolo_decoder_threads": (C.c_int, []),
     "yolo_jpeg_probe": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "yolo_jpeg_coefficients": (C.c_longlong, [C.c_char_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "yolo_get_batch": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(YoloDet), C.c_int, C.POINTER(C.c_int)]),
@@ -164,6 +165,11 @@ class DeviceBuffer:
             self.free()
         except Exception:
             pass
+
+
+def decoder_threads() -> int:
+    """Threads (the caller included) the library's JPEG entropy decoding runs on."""
+    return load().yolo_decoder_threads()
 
 
 def jpeg_probe(data: bytes) -> tuple[int, int, int]:
