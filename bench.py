@@ -344,10 +344,11 @@ def bench_conv(workdir, iters):
                 copy_gbs=copy_bytes / copy_ms / 1e6)
 
 
-def bench_serve(workdir, seconds=4.0, procs=4, callers=16):
+def bench_serve(workdir, seconds=4.0, procs=4, callers=16, frontends=4):
     """The gRPC server (yoloserve) with yolo11n, max batch 16, target 50 ms (the reference
     server's defaults, server/serve.cpp:344-346), JPEG decoded on the engine (entropy decoding
-    on the library's decoder threads, the rest on the GPU), under a closed loop of
+    on the library's decoder threads, the rest on the GPU), the gRPC service in `frontends`
+    processes sharing the port (0: in this process), under a closed loop of
     `procs` client processes x `callers` threads sending 640x640 JPEG frames over 127.0.0.1.
     Throughput is the sum over the client processes; p50 is the median of their medians,
     p99 the worst of their p99s."""
@@ -366,7 +367,7 @@ def bench_serve(workdir, seconds=4.0, procs=4, callers=16):
         paths.append(p)
     models = [yoloserve.Model("yolo11n", yolort.Engine(d, 16), 16)]
     srv = yoloserve.Server(models, target_ms=50.0, log=lambda *a: None)
-    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0")
+    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0", frontends=frontends)
     script = os.path.join(ROOT, "yolo11.cu_amd", "yoloserve.py")
     imgs = sum([["--image", p] for p in paths], [])
 
@@ -394,7 +395,7 @@ def bench_serve(workdir, seconds=4.0, procs=4, callers=16):
                 p50_ms=float(np.median([r["p50_ms"] for r in res])), p99_ms=max(r["p99_ms"] for r in res),
                 mean_batch=float(np.mean([r["mean_batch"] for r in res])), requests=sum(r["requests"] for r in res),
                 exec_ms_b16=round(models[0].exec_ms, 4), frames="640x640 JPEG q90, decoded on the engine",
-                decoder_threads=yolort.decoder_threads())
+                decoder_threads=yolort.decoder_threads(), frontend_processes=frontends)
 
 
 def bench_jpeg(workdir, batches=60, graphs=True):

@@ -137,6 +137,17 @@ int yolo_stage_jpeg(void* h, int B, const unsigned char* const* data, const size
 int yolo_decode_jpeg(void* h, int B, const unsigned char* const* data, const size_t* sizes, int first_slot,
                      int* heights, int* widths, int* status);
 int yolo_letterbox_decoded(void* h, int B, int first_slot);
+/* Decoding at arrival, for servers: yolo_jpeg_submit copies a stream, reads its headers and
+ * starts its entropy decoding on the decoder threads at once (into pinned memory), returning a
+ * ticket, or NULL if the stream is not one yolo_stage_jpeg decodes (decode it another way).
+ * yolo_decode_tickets is yolo_decode_jpeg for B tickets: it waits for each one's entropy
+ * decoding (usually long done), copies the coefficients and runs the GPU half; it consumes
+ * every ticket passed (NULL entries are reported corrupt).  yolo_jpeg_release frees a ticket
+ * that will not be decoded (after its entropy decoding ends). */
+void* yolo_jpeg_submit(const unsigned char* data, size_t size);
+int yolo_decode_tickets(void* h, int B, void* const* tickets, int first_slot, int* heights, int* widths,
+                        int* status);
+void yolo_jpeg_release(void* ticket);
 int yolo_jpeg_probe(const unsigned char* data, size_t size, int* height, int* width);
 /* Threads (the calling one included) the JPEG entropy decoding runs on. */
 int yolo_decoder_threads(void);

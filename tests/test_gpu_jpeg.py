@@ -156,3 +156,33 @@ def test_decode_next_batch_keeps_results(models):
     eng.sync()
     pb.free()
     eng.close()
+
+
+def test_tickets_equal_stage_jpeg(models):
+    """Streams submitted at arrival (entropy decoding started at once on the library's threads)
+    and decoded later by yolo_decode_tickets stage exactly what yolo_stage_jpeg does; a
+    truncated stream is reported corrupt, a progressive one gets no ticket, and released
+    tickets and repeated rounds recycle the pinned buffers."""
+    d = models("yolo11", "n")
+    streams = _streams()
+    trunc = streams[0][:len(streams[0]) // 2]
+    assert yolort.jpeg_submit(_jpeg(120, 160, 5, quality=90, progressive=True)) is None
+    eng = yolort.Engine(d, len(streams) + 1, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    want = [post.letterbox(_pil_bgr(s), 640, 640) for s in streams]
+    for rnd in range(3):
+        spare = [yolort.jpeg_submit(s) for s in streams[:2]]
+        for t in spare:
+            yolort.jpeg_release(t)
+        order = streams[rnd:] + streams[:rnd]
+        wants = want[rnd:] + want[:rnd]
+        tickets = [yolort.jpeg_submit(s) for s in order] + [yolort.jpeg_submit(trunc)]
+        assert all(t is not None for t in tickets)
+        print(f"round {rnd}: decode {len(tickets)} tickets", flush=True)
+        res = eng.decode_tickets(tickets)
+        assert [r[0] for r in res] == [yolort.JPEG_STAGED] * len(order) + [yolort.JPEG_INVALID]
+        assert eng.letterbox_decoded(len(tickets)) == len(order)
+        eng.sync()
+        got = eng.read(0, len(tickets))
+        for s in range(len(order)):
+            np.testing.assert_array_equal(got[s], wants[s], err_msg=f"round {rnd} slot {s}")
+    eng.close()

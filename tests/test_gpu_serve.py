@@ -1,5 +1,6 @@
 """The gRPC server with real engines on the GPU: concurrent requests over 127.0.0.1 for a detect,
-a segment and a classify model in one process.  Every response is checked against a direct
+a segment and a classify model, served in-process and by two front-end processes sharing the
+port (half the requests JPEG, decoded on the engine).  Every response is checked against a direct
 engine handle run on the same decoded pixels, to the parity bar (same kept count, classes and
 order; box IoU >= 0.99, |d score| <= 5e-3; mask IoU >= 0.99; same top-5), and that direct
 run is itself held to the oracle: its input tensor equals the oracle's letterbox (classify:
@@ -95,7 +96,8 @@ def _iou(a, b):
     return inter / u if u > 0 else 1.0
 
 
-def test_server_matches_direct_engine(models):
+@pytest.mark.parametrize("frontends", [0, 2])
+def test_server_matches_direct_engine(models, frontends):
     dirs = {"det": models("yolo11", "n"), "seg": models("yolo11", "n", "segment"),
             "cls": models("yolo11", "n", "classify", imgsz=224, nc=1000)}
     limits = {"det": 4, "seg": 2, "cls": 3}
@@ -103,14 +105,14 @@ def test_server_matches_direct_engine(models):
     direct = {n: yolort.Engine(d, 1, FLAGS) for n, d in dirs.items()}
     graphs = {n: graphfile.load(d) for n, d in dirs.items()}
     srv = yoloserve.Server(served, target_ms=20.0, log=lambda *a: None)
-    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0")
+    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0", frontends=frontends)
     cl = yoloserve.Client(f"127.0.0.1:{port}")
     try:
         frames = [modelgen.synth_frame(480 + 40 * (i % 3), 640 + 64 * (i % 2), 20, 300 + i) for i in range(12)]
         route = [["det", "seg", "cls", ""][i % 4] for i in range(12)]
         fmt = ["JPEG" if i % 2 else "PNG" for i in range(12)]   # JPEG: decoded on the engine
         payload = [_encode(f, fm) for f, fm in zip(frames, fmt)]
-        print("server: 12 concurrent requests over det/seg/cls", flush=True)
+        print(f"server ({frontends} front-end processes): 12 concurrent requests over det/seg/cls", flush=True)
         with ThreadPoolExecutor(12) as ex:
             resps = list(ex.map(lambda i: cl.detect(payload[i], route[i], timeout=120), range(12)))
         for i, r in enumerate(resps):

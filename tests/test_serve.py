@@ -277,12 +277,15 @@ def _png(bgr):
     return buf.getvalue()
 
 
-def test_grpc_roundtrip_fake_engines():
+@pytest.mark.parametrize("frontends", [0, 2])
+def test_grpc_roundtrip_fake_engines(frontends):
+    """In-process asyncio server (frontends=0) and two front-end processes sharing the port
+    (requests and results over pipes to this process, which keeps the engines)."""
     names = ["det", "seg", "cls", "obb"]
     engs = [FakeEngine(0), FakeEngine(3), FakeEngine(2), FakeEngine(1)]
     models = [yoloserve.Model(n, e, 4) for n, e in zip(names, engs)]
     srv = FakeServer(models, target_ms=40.0, log=lambda *a: None)
-    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0", decoders=8)
+    gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0", decoders=4, frontends=frontends)
     cl = yoloserve.Client(f"127.0.0.1:{port}")
     try:
         colors = [(10 + i, 20 + 2 * i, 30 + 3 * i) for i in range(24)]

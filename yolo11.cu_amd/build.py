@@ -15,6 +15,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libyolo11_amd.so")
+# host-only JPEG header / entropy decoding, without the HIP runtime (server front-ends)
+JPEG_LIB = os.path.join(HERE, "libyolo11_jpeg.so")
+JPEG_SOURCES = ("jpeg.cpp", "jpeg_abi.cpp")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -36,6 +39,7 @@ SOURCES = {
     "noalloc.hip": DEV_FLAGS,
     "jpeg.hip": DEV_FLAGS,
     "jpeg.cpp": ["-O3"] + HOST_FLAGS[1:],
+    "jpeg_abi.cpp": HOST_FLAGS,
     "graph.cpp": HOST_FLAGS,
     "engine.cpp": HOST_FLAGS,
 }
@@ -63,8 +67,14 @@ def build(verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
     os.replace(tmp, LIB)
+    jobjs = [os.path.join(OUT, src + ".o") for src in JPEG_SOURCES]
+    tmp = JPEG_LIB + ".tmp"
+    r = subprocess.run([HOSTCXX, "-shared", "-fPIC", "-pthread", "-o", tmp, *jobjs], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link of {JPEG_LIB} failed:\n{r.stdout}{r.stderr}")
+    os.replace(tmp, JPEG_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB}, {JPEG_LIB}")
     return LIB
 
 

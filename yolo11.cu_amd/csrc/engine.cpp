@@ -20,7 +20,10 @@
 #include <cstdlib>
 #include <cstring>
 #include <deque>
+#include <condition_variable>
 #include <map>
+#include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <tuple>
@@ -134,6 +137,13 @@ struct Engine {
   size_t jpegSamplesCap = 0;
   std::vector<int> jpegH, jpegW;       // per slot: the frame yolo_decode_jpeg left in its
                                        // staging buffer (0: none / failed / overwritten)
+  // The JPEG decode's copies and kernels run on a stream of their own, beside the network of
+  // the batch in flight.  It starts after `readDone` (the last letterbox, on the engine
+  // stream, that read the staging frames); the engine stream's next reader of decoded frames
+  // waits for `decodeDone`.
+  hipStream_t decodeSt = nullptr;
+  hipEvent_t readDone = nullptr, decodeDone = nullptr;
+  bool decodePending = false;
   bool capBlock = false;              // capture(): post() records the one-block NMS
   int frameB = 0;
   // the frame graph's device sources and sizes (for stage timing outside the graph)
@@ -161,6 +171,8 @@ struct Engine {
   }
 
   void release() {
+    if (st) (void)hipStreamSynchronize(st);
+    if (decodeSt) (void)hipStreamSynchronize(decodeSt);
     for (auto& ge : graphs)
       if (ge) (void)hipGraphExecDestroy(ge);
     graphs.clear();
@@ -207,6 +219,31 @@ struct Engine {
     side.clear();
     if (st) (void)hipStreamDestroy(st);
     st = nullptr;
+    if (decodeSt) (void)hipStreamDestroy(decodeSt);
+    if (readDone) (void)hipEventDestroy(readDone);
+    if (decodeDone) (void)hipEventDestroy(decodeDone);
+    decodeSt = nullptr;
+    readDone = decodeDone = nullptr;
+    decodePending = false;
+  }
+
+  // Both streams idle (before a buffer either may use is freed).
+  void syncAll() {
+    HCK(hipStreamSynchronize(st));
+    if (decodeSt) HCK(hipStreamSynchronize(decodeSt));
+  }
+
+  void ensureDecodeStream() {
+    if (decodeSt) return;
+    HCK(hipStreamCreateWithFlags(&decodeSt, hipStreamNonBlocking));
+    HCK(hipEventCreateWithFlags(&readDone, hipEventDisableTiming));
+    HCK(hipEventCreateWithFlags(&decodeDone, hipEventDisableTiming));
+    HCK(hipEventRecord(readDone, st));   // everything already queued may read staging frames
+  }
+
+  // The engine stream's next reader or writer of staging frames orders after the decodes.
+  void waitDecoded() {
+    if (decodePending) HCK(hipStreamWaitEvent(st, decodeDone, 0));
   }
 
   // ---------------------------------------------------------------- stream plan
@@ -930,6 +967,7 @@ struct Engine {
         launchPreprocessCls(f.src, f.h, f.w, bufp[g.tens[0].buf] + (size_t)f.slot * ib.H * ib.W * 3, ib.H, cg.rh,
                             cg.rw, cg.top, cg.left, fmt, st);
       }
+      if (readDone) HCK(hipEventRecord(readDone, st));
       return;
     }
     std::vector<LetterboxSlot> slots;
@@ -938,6 +976,7 @@ struct Engine {
       slots.push_back(LetterboxSlot{f.src, f.h, f.w, f.g.top, f.g.left, (int)roundf(f.h * f.g.scale),
                                     (int)roundf(f.w * f.g.scale), f.slot, f.g.scale, fmt});
     launchPreprocessBatch(slots.data(), (int)slots.size(), bufp[g.tens[0].buf], ib.H, ib.W, st);
+    if (readDone) HCK(hipEventRecord(readDone, st));   // the staging frames are read
   }
 
   // Frames of slots 0..Bn-1 in pixel layout fmt (PIXEL_BGR / PIXEL_RGBX); host[s], when
@@ -963,7 +1002,7 @@ struct Engine {
       stageCap.resize(B, 0);
     }
     if (stageCap[s] < bytes) {
-      HCK(hipStreamSynchronize(st));
+      syncAll();
       if (stageDev[s]) HCK(hipFree(stageDev[s]));
       stageDev[s] = nullptr;
       stageCap[s] = 0;
@@ -973,6 +1012,10 @@ struct Engine {
     return stageDev[s];
   }
 
+  int convertDecoded(int Bn, int firstSlot, const std::vector<jpeg::Header>& hd,
+                     const std::vector<const int16_t*>& coef, const int* status, JpegStage& S, size_t descOff);
+  JpegStage& nextStage(size_t bytes);
+
   void forgetDecoded(int slot) {
     if (slot < (int)jpegH.size()) jpegH[slot] = jpegW[slot] = 0;
   }
@@ -981,7 +1024,7 @@ struct Engine {
   void growDevice(uint8_t*& p, size_t& cap, size_t bytes) {
     if (cap >= bytes) return;
     const size_t want = std::max(bytes, cap + cap / 2);
-    HCK(hipStreamSynchronize(st));
+    syncAll();
     if (p) HCK(hipFree(p));
     p = nullptr;
     cap = 0;
@@ -1304,6 +1347,7 @@ int yolo_stage_frames(void* h, int B, const unsigned char* const* host, const in
     e->checkFrameInput();
     for (int s = 0; s < B; s++)
       if (!host[s] || heights[s] <= 0 || widths[s] <= 0) return -1;
+    e->waitDecoded();   // a decode may still be writing these slots' staging frames
     std::vector<std::pair<const uint8_t*, yolo::SlotGeom>> frames;
     for (int s = 0; s < B; s++) {
       e->forgetDecoded(first_slot + s);
@@ -1318,27 +1362,186 @@ int yolo_stage_frames(void* h, int B, const unsigned char* const* host, const in
   });
 }
 
-int yolo_jpeg_probe(const unsigned char* data, size_t size, int* height, int* width) {
-  if (!data) return -1;
-  yolo::jpeg::Header hd;
-  const int r = yolo::jpeg::parse(data, size, hd);
-  if (r == yolo::jpeg::OK) {
-    if (height) *height = hd.H;
-    if (width) *width = hd.W;
+namespace {
+
+// Pinned buffers for the coefficients of yolo_jpeg_submit tickets, process-wide: a buffer
+// goes back to the free list once the copy that read it has run (its event has completed).
+struct CoefPool {
+  std::mutex mu;
+  std::multimap<size_t, int16_t*> free;
+  std::vector<std::pair<hipEvent_t, std::vector<std::pair<size_t, int16_t*>>>> retiring;
+
+  void reclaimLocked() {
+    for (auto it = retiring.begin(); it != retiring.end();) {
+      if (hipEventQuery(it->first) == hipSuccess) {
+        for (auto& b : it->second) free.emplace(b.first, b.second);
+        (void)hipEventDestroy(it->first);
+        it = retiring.erase(it);
+      } else {
+        ++it;
+      }
+    }
   }
-  return r;
+  std::pair<size_t, int16_t*> take(size_t bytes) {
+    {
+      std::lock_guard<std::mutex> lk(mu);
+      reclaimLocked();
+      auto it = free.lower_bound(bytes);
+      if (it != free.end() && it->first <= bytes * 2) {
+        auto b = *it;
+        free.erase(it);
+        return b;
+      }
+    }
+    const size_t cap = std::max(bytes, (size_t)1 << 20);
+    int16_t* p = nullptr;
+    HCK(hipHostMalloc((void**)&p, cap, 0));
+    return {cap, p};
+  }
+  void give(size_t cap, int16_t* p) {
+    std::lock_guard<std::mutex> lk(mu);
+    free.emplace(cap, p);
+  }
+  void retire(hipEvent_t ev, std::vector<std::pair<size_t, int16_t*>> bufs) {
+    std::lock_guard<std::mutex> lk(mu);
+    retiring.emplace_back(ev, std::move(bufs));
+  }
+};
+
+CoefPool& coefPool() {
+  static CoefPool* p = new CoefPool;   // process lifetime (pinned memory is freed at exit)
+  return *p;
 }
 
-int yolo_decoder_threads(void) { return yolo::jpeg::decoderThreads(); }
+}  // namespace
 
-long long yolo_jpeg_coefficients(const unsigned char* data, size_t size, short* out, size_t cap) {
-  if (!data) return -1;
+// A JPEG stream being entropy-decoded on a decoder thread (yolo_jpeg_submit).
+struct JpegTicket {
+  std::vector<uint8_t> data;
   yolo::jpeg::Header hd;
-  if (yolo::jpeg::parse(data, size, hd) != yolo::jpeg::OK) return -1;
-  const size_t n = hd.blocks() * 64;
-  if (!out) return (long long)n;
-  if (cap < n) return -1;
-  return yolo::jpeg::decode(data, size, hd, out) ? (long long)n : -2;
+  size_t cap = 0;
+  int16_t* coef = nullptr;   // pinned
+  std::mutex mu;
+  std::condition_variable cv;
+  bool done = false, ok = false;
+
+  void wait() {
+    std::unique_lock<std::mutex> lk(mu);
+    cv.wait(lk, [&] { return done; });
+  }
+};
+
+// The GPU half of a batch decode.  Streams i with status[i] == YOLO_JPEG_STAGED have headers
+// hd[i] and quantised coefficients at coef[i] (pinned host memory); the descriptors are written
+// at S.host + descOff.  Copies coefficients and descriptors to the device, runs the IDCT and
+// colour kernels into the slots' staging frames, records which slots hold a decoded frame and
+// records S.copied after the copies.  Returns the number of streams converted.
+int yolo::Engine::convertDecoded(int Bn, int firstSlot, const std::vector<jpeg::Header>& hd,
+                           const std::vector<const int16_t*>& coef, const int* status, JpegStage& S,
+                           size_t descOff) {
+  ensureDecodeStream();
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  std::vector<size_t> block0(Bn, 0);
+  size_t blocks = 0;
+  bool contiguous = true;
+  const int16_t* base = nullptr;
+  for (int i = 0; i < Bn; i++) {
+    if (status[i] != YOLO_JPEG_STAGED) continue;
+    if (!base) base = coef[i] - blocks * 64;
+    contiguous = contiguous && coef[i] == base + blocks * 64;
+    block0[i] = blocks;
+    blocks += hd[i].blocks();
+  }
+  const size_t coefBytes = blocks * 64 * sizeof(int16_t);
+  const size_t planeBytes = up((size_t)3 * Bn * sizeof(JpegPlane));
+  const size_t descBytes = planeBytes + (size_t)Bn * sizeof(JpegFrame);
+  auto* planes = reinterpret_cast<JpegPlane*>(S.host + descOff);
+  auto* frames = reinterpret_cast<JpegFrame*>(S.host + descOff + planeBytes);
+  int np = 0, nf = 0, maxPix = 0;
+  size_t sampleBytes = 0;
+  for (int i = 0; i < Bn; i++) {
+    if (status[i] != YOLO_JPEG_STAGED) continue;
+    const jpeg::Header& H = hd[i];
+    JpegFrame& F = frames[nf++];
+    std::memset(&F, 0, sizeof F);
+    F.dst = stageBuffer(firstSlot + i, (size_t)H.H * H.W * 4);
+    F.H = H.H;
+    F.W = H.W;
+    F.nc = H.nc;
+    size_t b0 = block0[i];
+    for (int c = 0; c < H.nc; c++) {
+      const jpeg::Comp& k = H.comp[c];
+      JpegPlane& P = planes[np++];
+      P.block0 = (uint32_t)b0;
+      P.bw = (uint16_t)k.bw;
+      P.bh = (uint16_t)k.bh;
+      P.out = (uint32_t)sampleBytes;
+      P.pad = 0;
+      std::memcpy(P.q, H.q[k.tq], sizeof P.q);
+      F.plane[c] = P.out;
+      F.stride[c] = k.bw * 8;
+      F.cw[c] = k.cw;
+      F.ch[c] = k.ch;
+      F.fh[c] = k.fh;
+      F.fv[c] = k.fv;
+      b0 += (size_t)k.bw * k.bh;
+      sampleBytes = up(sampleBytes + (size_t)k.bw * k.bh * 64);
+    }
+    maxPix = std::max(maxPix, H.H * H.W);
+  }
+  if (blocks >= (size_t)1 << 31 || sampleBytes >= (size_t)1 << 32) throw Failure("JPEG batch too large");
+  if ((int)jpegH.size() < B) {
+    jpegH.resize(B, 0);
+    jpegW.resize(B, 0);
+  }
+  for (int i = 0; i < Bn; i++) {
+    const bool ok = status[i] == YOLO_JPEG_STAGED;
+    jpegH[firstSlot + i] = ok ? hd[i].H : 0;
+    jpegW[firstSlot + i] = ok ? hd[i].W : 0;
+  }
+  if (nf == 0) return 0;
+  const size_t descDev = up(coefBytes);
+  growDevice(jpegDev, jpegDevCap, descDev + descBytes);
+  growDevice(jpegSamples, jpegSamplesCap, sampleBytes);
+  hipStream_t ds = decodeSt;
+  if (contiguous) {
+    HCK(hipMemcpyAsync(jpegDev, base, coefBytes, hipMemcpyHostToDevice, ds));
+  } else {
+    for (int i = 0; i < Bn; i++)
+      if (status[i] == YOLO_JPEG_STAGED)
+        HCK(hipMemcpyAsync(jpegDev + block0[i] * 64 * sizeof(int16_t), coef[i], hd[i].blocks() * 64 * sizeof(int16_t),
+                           hipMemcpyHostToDevice, ds));
+  }
+  HCK(hipMemcpyAsync(jpegDev + descDev, S.host + descOff, descBytes, hipMemcpyHostToDevice, ds));
+  HCK(hipEventRecord(S.copied, ds));
+  S.pending = true;
+  launchJpegIdct(reinterpret_cast<const int16_t*>(jpegDev), reinterpret_cast<const JpegPlane*>(jpegDev + descDev), np,
+                 (int)blocks, jpegSamples, ds);
+  // the colour kernel writes the staging frames: after the last letterbox read them
+  HCK(hipStreamWaitEvent(ds, readDone, 0));
+  launchJpegColor(jpegSamples, reinterpret_cast<const JpegFrame*>(jpegDev + descDev + planeBytes), nf, maxPix, ds);
+  HCK(hipEventRecord(decodeDone, ds));
+  decodePending = true;
+  HCK(hipGetLastError());
+  return nf;
+}
+
+// The next pinned staging area with at least `bytes`, once its previous copy has run.
+yolo::Engine::JpegStage& yolo::Engine::nextStage(size_t bytes) {
+  JpegStage& S = jpegStage[jpegNext];
+  jpegNext ^= 1;
+  if (S.pending) HCK(hipEventSynchronize(S.copied));
+  S.pending = false;
+  if (S.cap < bytes) {
+    if (S.host) HCK(hipHostFree(S.host));
+    S.host = nullptr;
+    S.cap = 0;
+    const size_t want = std::max(bytes, (size_t)1 << 20);
+    HCK(hipHostMalloc((void**)&S.host, want, 0));
+    S.cap = want;
+  }
+  if (!S.copied) HCK(hipEventCreateWithFlags(&S.copied, hipEventDisableTiming));
+  return S;
 }
 
 int yolo_decode_jpeg(void* h, int B, const unsigned char* const* data, const size_t* sizes, int first_slot,
@@ -1361,93 +1564,104 @@ int yolo_decode_jpeg(void* h, int B, const unsigned char* const* data, const siz
         blocks += hd[i].blocks();
       }
     }
-    // pinned staging: [coefficients][plane descriptors][frame descriptors], 256-byte aligned
-    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    const size_t coefBytes = blocks * 64 * sizeof(int16_t);
-    const size_t planeOff = up(coefBytes), frameOff = up(planeOff + (size_t)3 * B * sizeof(yolo::JpegPlane));
-    const size_t total = up(frameOff + (size_t)B * sizeof(yolo::JpegFrame));
-    Engine::JpegStage& S = e->jpegStage[e->jpegNext];
-    e->jpegNext ^= 1;
-    if (S.pending) HCK(hipEventSynchronize(S.copied));   // its previous copy has run
-    S.pending = false;
-    if (S.cap < total) {
-      if (S.host) HCK(hipHostFree(S.host));
-      S.host = nullptr;
-      S.cap = 0;
-      const size_t want = std::max(total, (size_t)4 << 20);
-      HCK(hipHostMalloc((void**)&S.host, want, 0));
-      S.cap = want;
-    }
-    if (!S.copied) HCK(hipEventCreateWithFlags(&S.copied, hipEventDisableTiming));
+    // pinned staging: [coefficients][descriptors]
+    const size_t descOff = (blocks * 64 * sizeof(int16_t) + 255) & ~(size_t)255;
+    Engine::JpegStage& S = e->nextStage(descOff + 3 * (size_t)B * sizeof(yolo::JpegPlane) + 256 +
+                                        (size_t)B * sizeof(yolo::JpegFrame));
     int16_t* coef = reinterpret_cast<int16_t*>(S.host);
     J::parallelFor(B, [&](int i) {
       if (status[i] == YOLO_JPEG_STAGED && !J::decode(data[i], sizes[i], hd[i], coef + block0[i] * 64))
         status[i] = YOLO_JPEG_INVALID;
     });
-    // descriptors of the decoded streams; sample planes 256-byte aligned
-    auto* planes = reinterpret_cast<yolo::JpegPlane*>(S.host + planeOff);
-    auto* frames = reinterpret_cast<yolo::JpegFrame*>(S.host + frameOff);
-    int np = 0, nf = 0, maxPix = 0;
-    size_t sampleBytes = 0;
+    std::vector<const int16_t*> src(B, nullptr);
+    for (int i = 0; i < B; i++) src[i] = coef + block0[i] * 64;
+    return B - e->convertDecoded(B, first_slot, hd, src, status, S, descOff);
+  });
+}
+
+void* yolo_jpeg_submit(const unsigned char* data, size_t size) {
+  if (!data) return nullptr;
+  try {
+    auto t = std::make_unique<JpegTicket>();
+    if (yolo::jpeg::parse(data, size, t->hd) != yolo::jpeg::OK) return nullptr;
+    t->data.assign(data, data + size);
+    auto buf = coefPool().take(t->hd.blocks() * 64 * sizeof(int16_t));
+    t->cap = buf.first;
+    t->coef = buf.second;
+    JpegTicket* tp = t.release();
+    yolo::jpeg::runAsync([tp] {
+      const bool ok = yolo::jpeg::decode(tp->data.data(), tp->data.size(), tp->hd, tp->coef);
+      std::lock_guard<std::mutex> lk(tp->mu);
+      tp->ok = ok;
+      tp->done = true;
+      tp->cv.notify_all();
+    });
+    return tp;
+  } catch (const std::exception& ex) {
+    std::fprintf(stderr, "[yolo] yolo_jpeg_submit: %s\n", ex.what());
+    return nullptr;
+  }
+}
+
+void yolo_jpeg_release(void* ticket) {
+  auto* t = static_cast<JpegTicket*>(ticket);
+  if (!t) return;
+  t->wait();
+  coefPool().give(t->cap, t->coef);   // never copied from
+  delete t;
+}
+
+int yolo_decode_tickets(void* h, int B, void* const* tickets, int first_slot, int* heights, int* widths,
+                        int* status) {
+  if (!tickets || B < 1) return -1;
+  std::vector<JpegTicket*> ts(B);
+  for (int i = 0; i < B; i++) ts[i] = static_cast<JpegTicket*>(tickets[i]);
+  bool copied = false;
+  hipEvent_t ev = nullptr;
+  const int r = guarded([&] {
+    Engine* e = E(h);
+    if (first_slot < 0 || first_slot + B > e->B || !status) return -1;
+    e->checkFrameInput();
+    std::vector<yolo::jpeg::Header> hd(B);
+    std::vector<const int16_t*> src(B, nullptr);
     for (int i = 0; i < B; i++) {
-      if (status[i] != YOLO_JPEG_STAGED) continue;
-      const J::Header& H = hd[i];
-      const int slot = first_slot + i;
-      yolo::JpegFrame& F = frames[nf++];
-      std::memset(&F, 0, sizeof F);
-      F.dst = e->stageBuffer(slot, (size_t)H.H * H.W * 4);
-      F.H = H.H;
-      F.W = H.W;
-      F.nc = H.nc;
-      size_t b0 = block0[i];
-      for (int c = 0; c < H.nc; c++) {
-        const J::Comp& k = H.comp[c];
-        yolo::JpegPlane& P = planes[np++];
-        P.block0 = (uint32_t)b0;
-        P.bw = (uint16_t)k.bw;
-        P.bh = (uint16_t)k.bh;
-        P.out = (uint32_t)sampleBytes;
-        P.pad = 0;
-        std::memcpy(P.q, H.q[k.tq], sizeof P.q);
-        F.plane[c] = P.out;
-        F.stride[c] = k.bw * 8;
-        F.cw[c] = k.cw;
-        F.ch[c] = k.ch;
-        F.fh[c] = k.fh;
-        F.fv[c] = k.fv;
-        b0 += (size_t)k.bw * k.bh;
-        sampleBytes = up(sampleBytes + (size_t)k.bw * k.bh * 64);
+      JpegTicket* t = ts[i];
+      if (t) t->wait();
+      status[i] = t && t->ok ? YOLO_JPEG_STAGED : YOLO_JPEG_INVALID;
+      if (t) {
+        hd[i] = t->hd;
+        src[i] = t->coef;
       }
-      maxPix = std::max(maxPix, H.H * H.W);
+      if (heights) heights[i] = status[i] == YOLO_JPEG_STAGED ? t->hd.H : 0;
+      if (widths) widths[i] = status[i] == YOLO_JPEG_STAGED ? t->hd.W : 0;
     }
-    if (blocks >= (size_t)1 << 31 || sampleBytes >= (size_t)1 << 32)
-      throw Failure("JPEG batch too large");
-    if ((int)e->jpegH.size() < e->B) {
-      e->jpegH.resize(e->B, 0);
-      e->jpegW.resize(e->B, 0);
+    Engine::JpegStage& S = e->nextStage(3 * (size_t)B * sizeof(yolo::JpegPlane) + 256 + (size_t)B * sizeof(yolo::JpegFrame));
+    const int nf = e->convertDecoded(B, first_slot, hd, src, status, S, 0);
+    if (nf > 0) {
+      HCK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+      HCK(hipEventRecord(ev, e->decodeSt));
+      copied = true;
     }
-    for (int i = 0; i < B; i++) {
-      const bool ok = status[i] == YOLO_JPEG_STAGED;
-      e->jpegH[first_slot + i] = ok ? hd[i].H : 0;
-      e->jpegW[first_slot + i] = ok ? hd[i].W : 0;
-    }
-    if (nf == 0) return B;
-    e->growDevice(e->jpegDev, e->jpegDevCap, total);
-    e->growDevice(e->jpegSamples, e->jpegSamplesCap, sampleBytes);
-    HCK(hipMemcpyAsync(e->jpegDev, S.host, total, hipMemcpyHostToDevice, e->st));
-    HCK(hipEventRecord(S.copied, e->st));
-    S.pending = true;
-    const auto* dCoef = reinterpret_cast<const int16_t*>(e->jpegDev);
-    const auto* dPlanes = reinterpret_cast<const yolo::JpegPlane*>(e->jpegDev + planeOff);
-    const auto* dFrames = reinterpret_cast<const yolo::JpegFrame*>(e->jpegDev + frameOff);
-    int nblocks = 0;
-    for (int i = 0; i < B; i++)
-      if (status[i] == YOLO_JPEG_STAGED) nblocks = (int)(block0[i] + hd[i].blocks());
-    yolo::launchJpegIdct(dCoef, dPlanes, np, nblocks, e->jpegSamples, e->st);
-    yolo::launchJpegColor(e->jpegSamples, dFrames, nf, maxPix, e->st);
-    HCK(hipGetLastError());
     return B - nf;
   });
+  // the tickets are consumed: buffers a copy read wait for its event, the others are free now
+  // (after a failure, once the stream has passed whatever was queued)
+  if (r < 0 && h) {
+    (void)hipStreamSynchronize(E(h)->st);
+    if (E(h)->decodeSt) (void)hipStreamSynchronize(E(h)->decodeSt);
+  }
+  std::vector<std::pair<size_t, int16_t*>> used;
+  for (int i = 0; i < B; i++) {
+    JpegTicket* t = ts[i];
+    if (!t) continue;
+    t->wait();
+    if (r >= 0 && copied && status[i] == YOLO_JPEG_STAGED) used.emplace_back(t->cap, t->coef);
+    else coefPool().give(t->cap, t->coef);
+    delete t;
+  }
+  if (!used.empty()) coefPool().retire(ev, std::move(used));
+  else if (ev) (void)hipEventDestroy(ev);
+  return r;
 }
 
 int yolo_letterbox_decoded(void* h, int B, int first_slot) {
@@ -1462,7 +1676,10 @@ int yolo_letterbox_decoded(void* h, int B, int first_slot) {
       if (!e->g.cls) e->slots[s] = sg;
       v.push_back(Engine::Staged{s, e->stageDev[s], e->jpegH[s], e->jpegW[s], sg});
     }
-    if (!v.empty()) e->preprocessStaged(v, yolo::PIXEL_RGBX);
+    if (!v.empty()) {
+      e->waitDecoded();
+      e->preprocessStaged(v, yolo::PIXEL_RGBX);
+    }
     HCK(hipGetLastError());
     return (int)v.size();
   });

@@ -8,6 +8,7 @@
 #include <atomic>
 #include <condition_variable>
 #include <cstdlib>
+#include <deque>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -158,6 +159,9 @@ struct Bits {
 };
 
 // ------------------------------------------------------------------ decoder threads
+// A queue of tasks served by the decoder threads.  A parallel-for posts helper tasks that pull
+// indices from a shared counter, and the caller pulls too; a helper that starts after the
+// loop is done finds the counter exhausted and never touches the loop's function.
 class Pool {
  public:
   explicit Pool(int workers) {
@@ -165,21 +169,23 @@ class Pool {
   }
   int size() const { return (int)th_.size() + 1; }
 
+  void post(std::function<void()> f) {
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      q_.push_back(std::move(f));
+    }
+    cv_.notify_one();
+  }
+
   void run(int n, const std::function<void(int)>& fn) {
-    std::lock_guard<std::mutex> serial(runMu_);
     auto job = std::make_shared<Job>();
     job->fn = &fn;
     job->n = n;
-    {
-      std::lock_guard<std::mutex> lk(mu_);
-      cur_ = job;
-      gen_++;
-    }
-    cv_.notify_all();
-    work(*job);
-    std::unique_lock<std::mutex> lk(mu_);
-    doneCv_.wait(lk, [&] { return job->done.load() == n; });
-    cur_.reset();
+    const int helpers = std::min(n - 1, (int)th_.size());
+    for (int i = 0; i < helpers; i++) post([job] { job->work(); });
+    job->work();
+    std::unique_lock<std::mutex> lk(job->mu);
+    job->cv.wait(lk, [&] { return job->done.load() == job->n; });
   }
 
  private:
@@ -187,39 +193,38 @@ class Pool {
     const std::function<void(int)>* fn = nullptr;
     int n = 0;
     std::atomic<int> next{0}, done{0};
-  };
-
-  void work(Job& j) {
-    for (;;) {
-      const int i = j.next.fetch_add(1);
-      if (i >= j.n) return;                 // a finished job's fn is never touched
-      (*j.fn)(i);
-      if (j.done.fetch_add(1) + 1 == j.n) {
-        std::lock_guard<std::mutex> lk(mu_);
-        doneCv_.notify_all();
+    std::mutex mu;
+    std::condition_variable cv;
+    void work() {
+      for (;;) {
+        const int i = next.fetch_add(1);
+        if (i >= n) return;
+        (*fn)(i);
+        if (done.fetch_add(1) + 1 == n) {
+          std::lock_guard<std::mutex> lk(mu);
+          cv.notify_all();
+        }
       }
     }
-  }
+  };
 
   void loop() {
-    uint64_t seen = 0;
     for (;;) {
-      std::shared_ptr<Job> j;
+      std::function<void()> f;
       {
         std::unique_lock<std::mutex> lk(mu_);
-        cv_.wait(lk, [&] { return gen_ != seen; });
-        seen = gen_;
-        j = cur_;
+        cv_.wait(lk, [&] { return !q_.empty(); });
+        f = std::move(q_.front());
+        q_.pop_front();
       }
-      if (j) work(*j);
+      f();
     }
   }
 
   std::vector<std::thread> th_;
-  std::mutex mu_, runMu_;
-  std::condition_variable cv_, doneCv_;
-  std::shared_ptr<Job> cur_;
-  uint64_t gen_ = 0;
+  std::mutex mu_;
+  std::condition_variable cv_;
+  std::deque<std::function<void()>> q_;
 };
 
 int threadCount() {
@@ -251,6 +256,8 @@ void parallelFor(int n, const std::function<void(int)>& fn) {
   }
   pool().run(n, fn);
 }
+
+void runAsync(std::function<void()> fn) { pool().post(std::move(fn)); }
 
 // ------------------------------------------------------------------ headers
 int parse(const uint8_t* d, size_t n, Header& hd) {

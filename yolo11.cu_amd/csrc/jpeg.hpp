@@ -59,8 +59,10 @@ int parse(const uint8_t* d, size_t n, Header& hd);
 bool decode(const uint8_t* d, size_t n, const Header& hd, int16_t* out);
 
 // Runs fn(0 .. n-1) on the process-wide decoder threads (the calling thread helps) and
-// returns when all are done.  Calls from several threads are served one after another.
+// returns when all are done.  Several threads may run loops at once.
 void parallelFor(int n, const std::function<void(int)>& fn);
+// Runs fn on a decoder thread; returns at once.
+void runAsync(std::function<void()> fn);
 int decoderThreads();
 
 }  // namespace jpeg

@@ -60,6 +60,10 @@ _SIGS = {
     "yolo_decode_jpeg": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t), C.c_int,
                                    C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "yolo_letterbox_decoded": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    "yolo_jpeg_submit": (C.c_void_p, [C.c_char_p, C.c_size_t]),
+    "yolo_decode_tickets": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_void_p), C.c_int, C.POINTER(C.c_int),
+                                      C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "yolo_jpeg_release": (None, [C.c_void_p]),
     "yolo_decoder_threads": (C.c_int, []),
     "yolo_jpeg_probe": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "yolo_jpeg_coefficients": (C.c_longlong, [C.c_char_p, C.c_size_t, C.c_void_p, C.c_size_t]),
@@ -178,6 +182,18 @@ def jpeg_probe(data: bytes) -> tuple[int, int, int]:
     h, w = C.c_int(0), C.c_int(0)
     r = load().yolo_jpeg_probe(data, len(data), C.byref(h), C.byref(w))
     return r, h.value, w.value
+
+
+def jpeg_submit(data: bytes):
+    """Starts entropy-decoding a JPEG stream on the library's decoder threads; a ticket for
+    Engine.decode_tickets, or None if the engine does not decode this stream."""
+    return load().yolo_jpeg_submit(data, len(data)) or None
+
+
+def jpeg_release(ticket) -> None:
+    """Frees a ticket that will not be decoded."""
+    if ticket:
+        load().yolo_jpeg_release(ticket)
 
 
 def jpeg_coefficients(data: bytes) -> np.ndarray | None:
@@ -386,6 +402,16 @@ class Engine:
         """The decode half of stage_jpeg: the slots' staging frames only (no letterbox, slot
         geometry unchanged); letterbox_decoded finishes the staging."""
         return self._jpeg(self.lib.yolo_decode_jpeg, streams, first_slot)
+
+    def decode_tickets(self, tickets: list, first_slot: int = 0):
+        """decode_jpeg for tickets from jpeg_submit (consumed, whatever the outcome): the
+        entropy decoding already ran at submission."""
+        n = len(tickets)
+        tk = (C.c_void_p * n)(*tickets)
+        hh, ww, st = (C.c_int * n)(), (C.c_int * n)(), (C.c_int * n)()
+        if self.lib.yolo_decode_tickets(self.h, n, tk, first_slot, hh, ww, st) < 0:
+            raise RuntimeError("yolo_decode_tickets failed")
+        return [(st[i], hh[i], ww[i]) for i in range(n)]
 
     def letterbox_decoded(self, n: int, first_slot: int = 0) -> int:
         r = self.lib.yolo_letterbox_decoded(self.h, n, first_slot)

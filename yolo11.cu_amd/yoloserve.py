@@ -40,8 +40,13 @@ import asyncio
 import collections
 import ctypes
 import io
+import itertools
 import json
 import os
+import queue
+import socket
+import struct
+import subprocess
 import sys
 import threading
 import time
@@ -253,6 +258,24 @@ def parse_dir_spec(spec: str, max_batch: int) -> tuple[str, str, int]:
 
 # ------------------------------------------------------------------ server
 
+def response_bytes(resp: bytes, rows, obb: bool) -> bytes:
+    """A serialized DetectResponse: `resp` (its other fields, serialized) plus the detection
+    rows (boxes, or rotated boxes if `obb`) appended as repeated-field entries."""
+    if rows is None or len(rows) == 0:
+        return resp
+    wire = (rboxes_wire if obb else boxes_wire)(rows)
+    if wire is not None:
+        return resp + wire
+    m = pb.DetectResponse.FromString(resp)      # class ids beyond two varint bytes
+    if obb:
+        for cx, cy, w, h, a, sc, c in np.asarray(rows, np.float64).tolist():
+            m.rboxes.add(cx=cx, cy=cy, w=w, h=h, angle=a, score=sc, cls=int(c))
+    else:
+        for x1, y1, x2, y2, sc, c in np.asarray(rows, np.float64).tolist():
+            m.boxes.add(x1=x1, y1=y1, x2=x2, y2=y2, score=sc, cls=int(c))
+    return m.SerializeToString()
+
+
 class _PinnedPool:
     """Pinned host buffers for decoded frames: a request's pixels go straight from the
     decoder into one (on its handler thread), the worker stages a whole batch from them
@@ -285,14 +308,15 @@ class _Request:
     """`resp` holds the response's small fields; `rows` the detections (boxes, or rotated
     boxes if `obb`) that `payload()` encodes on the caller's thread, so the engine worker
     never does it.  `payload()` is the serialized response, `message()` the parsed one.
-    The image is `jpeg` (a stream the engine decodes itself) + `hw`, or decoded pixels:
+    The image is `ticket` (a JPEG stream whose entropy decoding the engine library started
+    at arrival), or decoded pixels:
     `img` (numpy) or, with a pinned pool, `host` + `hw`."""
-    __slots__ = ("img", "host", "jpeg", "hw", "arrival", "resp", "rows", "obb", "error", "done", "on_done")
+    __slots__ = ("img", "host", "ticket", "hw", "arrival", "resp", "rows", "obb", "error", "done", "on_done")
 
     def __init__(self, on_done=None):
         self.on_done = on_done
         self.img = None
-        self.jpeg = None
+        self.ticket = None
         self.host = None
         self.hw = (0, 0)
         self.arrival = time.monotonic()
@@ -310,18 +334,7 @@ class _Request:
             self.on_done()
 
     def payload(self) -> bytes:
-        wire = b""
-        if self.rows is not None:
-            wire = (rboxes_wire if self.obb else boxes_wire)(self.rows)
-            if wire is None:                  # class ids beyond two varint bytes
-                if self.obb:
-                    for cx, cy, w, h, a, s, c in self.rows.tolist():
-                        self.resp.rboxes.add(cx=cx, cy=cy, w=w, h=h, angle=a, score=s, cls=int(c))
-                else:
-                    for x1, y1, x2, y2, s, c in self.rows.tolist():
-                        self.resp.boxes.add(x1=x1, y1=y1, x2=x2, y2=y2, score=s, cls=int(c))
-                self.rows, wire = None, b""
-        return self.resp.SerializeToString() + wire
+        return response_bytes(self.resp.SerializeToString(), self.rows, self.obb)
 
     def message(self):
         return pb.DetectResponse.FromString(self.payload())
@@ -358,7 +371,7 @@ class Server:
         # batch staging from pinned memory when every engine offers it (test fakes do not),
         # and JPEG streams decoded by the engines themselves when they all can
         self.pool = _PinnedPool() if all(hasattr(m.eng, "stage_frames") for m in models) else None
-        self.engine_jpeg = self.pool is not None and all(hasattr(m.eng, "stage_jpeg") for m in models)
+        self.engine_jpeg = self.pool is not None and all(hasattr(m.eng, "decode_tickets") for m in models)
         self._stop = False
         self._worker = threading.Thread(target=self._work, name="yoloserve-worker", daemon=True)
         self._worker.start()
@@ -390,39 +403,45 @@ class Server:
             raise KeyError(name)
         return self.by_name[name]
 
-    def engine_decodes(self, image: bytes):
-        """(height, width) if the engines decode this stream themselves (a JPEG inside their
-        decoder's set: entropy decoding on the library's threads, the rest on the GPU), else
-        None (PIL decodes it).  Reads only the headers."""
+    def submit_jpeg(self, image: bytes, model: str = "", on_done=None):
+        """Queues a JPEG stream the engines decode themselves, its entropy decoding started on
+        the library's decoder threads now (a few µs here); None if the engines do not decode
+        this stream (submit it instead: PIL decodes it)."""
         if not self.engine_jpeg or image[:2] != b"\xff\xd8":
             return None
+        mi = self.model_index(model)
         import yolort
-        ok, h, w = yolort.jpeg_probe(image)
-        return (h, w) if ok == 1 else None
+        ticket = yolort.jpeg_submit(image)
+        if ticket is None:
+            return None
+        r = _Request(on_done)
+        r.ticket = ticket
+        return self._queue(r, mi)
 
-    def submit(self, image: bytes, model: str = "", on_done=None, engine_hw=None) -> _Request:
-        """Queues a request; the returned request's `done` is set, and `on_done()` called from
-        the thread that completes it, when its response (or error) is ready.  With
-        `engine_hw` (from engine_decodes) the stream goes to the engine as it is; otherwise
-        it is decoded here, on the calling thread."""
+    def submit(self, image: bytes, model: str = "", on_done=None) -> _Request:
+        """Decodes on the calling thread, then queues; the returned request's `done` is set,
+        and `on_done()` called from the thread that completes it, when its response (or
+        error) is ready."""
         mi = self.model_index(model)
         r = _Request(on_done)
-        if engine_hw is not None:
-            r.jpeg, r.hw = image, engine_hw
-        elif self.pool is not None:
+        if self.pool is not None:
             got = decode_rgbx_into(image, self.pool)
             if got is not None:
                 r.host, r.hw = got
         else:
             r.img = decode_image(image)
-        if r.jpeg is None and r.host is None and r.img is None:
+        if r.ticket is None and r.host is None and r.img is None:
             r.error = "image decode failed"
             r.resp.task = self.models[mi].task_name
             r.finish()
             return r
+        return self._queue(r, mi)
+
+    def _queue(self, r: _Request, mi: int) -> _Request:
         with self.cv:
             if self._stop:
                 r.error = "server shutting down"
+                self._release([r])
                 r.finish()
                 return r
             q = self.models[mi].queue
@@ -432,6 +451,66 @@ class Server:
             if len(q) == 1 or len(q) >= self.models[mi].max_batch:
                 self.cv.notify_all()
         return r
+
+    # -- requests from front-end processes
+    def serve_frontend(self, conn):
+        """Serves one front-end process's connection (see `grpc_server(frontends=...)`): a
+        reader thread queues its requests, a sender thread encodes and returns the results.
+        Returns the two threads; both end when the connection closes."""
+        sendq = queue.SimpleQueue()
+
+        def reader():
+            try:
+                while True:
+                    hdr = conn.recv_bytes()
+                    rid, kind, mi, _, h, w = _REQ.unpack(hdr)
+                    data = conn.recv_bytes()
+                    r = _Request()
+                    r.on_done = lambda rid=rid, r=r: sendq.put((rid, r))
+                    if not 0 <= mi < len(self.models):
+                        r.error = "unknown model"
+                        r.finish()
+                        continue
+                    if kind == KIND_JPEG and self.engine_jpeg:
+                        import yolort
+                        r.ticket = yolort.jpeg_submit(data)
+                        if r.ticket is None:      # the front-end's header check said yes
+                            got = decode_rgbx_into(data, self.pool)
+                            if got is None:
+                                r.error = "image decode failed"
+                                r.finish()
+                                continue
+                            r.host, r.hw = got
+                    elif kind == KIND_RGBX and self.pool is not None:
+                        r.host, r.hw = self.pool.take(h * w * 4), (h, w)
+                        np.copyto(r.host.array[:h * w * 4], np.frombuffer(data, np.uint8))
+                    elif kind == KIND_BGR and self.pool is None:
+                        r.img = np.frombuffer(data, np.uint8).reshape(h, w, 3)
+                    else:
+                        r.error = "image decode failed"
+                        r.finish()
+                        continue
+                    self._queue(r, mi)
+            except (EOFError, OSError):
+                pass
+            sendq.put(None)
+
+        def sender():
+            while True:
+                item = sendq.get()
+                if item is None:
+                    return
+                rid, r = item
+                try:
+                    conn.send_bytes(_encode_result(rid, r))
+                except (EOFError, OSError, BrokenPipeError):
+                    return
+
+        ts = [threading.Thread(target=reader, name="yoloserve-fe-reader", daemon=True),
+              threading.Thread(target=sender, name="yoloserve-fe-sender", daemon=True)]
+        for t in ts:
+            t.start()
+        return ts
 
     # -- worker side
     def _collect(self):
@@ -463,16 +542,19 @@ class Server:
                 jp = []
                 if self.pool is not None:
                     # engine-decoded JPEG streams take the first slots, decoded pixels the
-                    # rest.  The JPEG entropy decoding runs now, while the previous batch is
-                    # still on the GPU; the letterbox (which sets the slots' geometry, still
-                    # the previous batch's until its results are read) waits for _finish.
-                    jp = [r for r in batch if r.jpeg is not None]
-                    px = [r for r in batch if r.jpeg is None]
+                    # rest.  Their entropy decoding started at arrival; the coefficient
+                    # copies and the GPU half queue now, behind the previous batch; the
+                    # letterbox (which sets the slots' geometry, still the previous batch's
+                    # until its results are read) waits for _finish.
+                    jp = [r for r in batch if r.ticket is not None]
+                    px = [r for r in batch if r.ticket is None]
                     batch = jp + px
                     if jp:
-                        res = m.eng.decode_jpeg([r.jpeg for r in jp], 0)
+                        tickets = [r.ticket for r in jp]
+                        for r in jp:
+                            r.ticket = None       # consumed by the call, whatever happens
+                        res = m.eng.decode_tickets(tickets, 0)
                         for r, (st, _, _) in zip(jp, res):
-                            r.jpeg = None
                             if st != 0:
                                 r.error = "image decode failed"
                 stage_ms = (time.monotonic() - t0) * 1e3
@@ -523,11 +605,14 @@ class Server:
                     r.finish()
 
     def _release(self, batch: list):
-        if self.pool is not None:
-            for r in batch:
-                if r.host is not None:
-                    self.pool.give(r.host)
-                    r.host = None
+        for r in batch:
+            if r.host is not None and self.pool is not None:
+                self.pool.give(r.host)
+                r.host = None
+            if r.ticket is not None:
+                import yolort
+                yolort.jpeg_release(r.ticket)
+                r.ticket = None
 
     def _finish(self, mi: int, batch: list, launch: float):
         m = self.models[mi]
@@ -596,6 +681,251 @@ class Server:
 
 # ------------------------------------------------------------------ gRPC glue
 
+# ------------------------------------------------------------------ front-end processes
+# A front-end is a process of its own (its own GIL and event loop) running the gRPC service on
+# the server's port with SO_REUSEPORT, so the kernel spreads client connections over the
+# front-ends.  It answers routing and decode errors itself, hands each image to the engine
+# process over a pipe (JPEG streams the engines decode, as they are; other formats decoded
+# here by PIL into R,G,B,X pixels), and encodes the response from the result the engine
+# process returns.  Engine calls, batching and the GPU stay in the engine process.  A
+# front-end never loads the HIP runtime: it reads JPEG headers with libyolo11_jpeg.so.
+_REQ = struct.Struct("<QBBHII")      # request id, kind, model index, 0, height, width
+_RSP = struct.Struct("<QBBHII")      # request id, code, obb, 0, rows, response-field bytes
+KIND_JPEG, KIND_RGBX, KIND_BGR = 0, 1, 2
+CODE_OK, CODE_INVALID, CODE_UNAVAILABLE = 0, 1, 2
+
+
+def _encode_result(rid: int, r: _Request) -> bytes:
+    """A finished request as the engine process returns it to a front-end: the header, the
+    detection rows (float32), then the serialized response fields (or the error text)."""
+    if r.error:
+        code = CODE_INVALID if r.error == "image decode failed" else CODE_UNAVAILABLE
+        msg = r.error.encode()
+        return _RSP.pack(rid, code, 0, 0, 0, len(msg)) + msg
+    rows, n = b"", 0
+    if r.rows is not None and len(r.rows):
+        a = np.ascontiguousarray(r.rows, np.float32)
+        rows, n = a.tobytes(), a.shape[0]
+    resp = r.resp.SerializeToString()
+    return _RSP.pack(rid, CODE_OK, 1 if r.obb else 0, 0, n, len(resp)) + rows + resp
+
+
+_JPEG_LIB = None
+
+
+def jpeg_dims(data: bytes):
+    """(height, width) if the engine decodes this JPEG stream itself, else None -- from the
+    headers, with the host-only libyolo11_jpeg.so (no HIP runtime in the calling process)."""
+    global _JPEG_LIB
+    if _JPEG_LIB is None:
+        lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "libyolo11_jpeg.so"))
+        lib.yolo_jpeg_probe.restype = ctypes.c_int
+        lib.yolo_jpeg_probe.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int),
+                                        ctypes.POINTER(ctypes.c_int)]
+        _JPEG_LIB = lib
+    h, w = ctypes.c_int(0), ctypes.c_int(0)
+    ok = _JPEG_LIB.yolo_jpeg_probe(data, len(data), ctypes.byref(h), ctypes.byref(w))
+    return (h.value, w.value) if ok == 1 else None
+
+
+def _frontend_decode(image: bytes, rgbx: bool):
+    """(kind, height, width, pixel bytes) decoded by PIL, or None if undecodable."""
+    if not rgbx:
+        img = decode_image(image)
+        return None if img is None else (KIND_BGR, img.shape[0], img.shape[1], img.tobytes())
+    try:
+        from PIL import Image
+        with Image.open(io.BytesIO(image)) as im:
+            if im.mode != "RGB":
+                im = im.convert("RGB")
+            w, h = im.size
+            if h < 1 or w < 1:
+                return None
+            im.load()
+            view = _rgbx_view(im, h * w)
+            data = view[1].tobytes() if view is not None else im.tobytes("raw", "RGBX")
+            return KIND_RGBX, h, w, data
+    except Exception:
+        return None
+
+
+def _frontend_main(addr: str, conn, names: list, engine_jpeg: bool, rgbx: bool, decoders: int):
+    asyncio.run(_frontend(addr, conn, names, engine_jpeg, rgbx, decoders))
+
+
+async def _frontend(addr: str, conn, names: list, engine_jpeg: bool, rgbx: bool, decoders: int):
+    """engine_jpeg: JPEG streams inside the engines' decoder go to the engine process as they
+    are; rgbx: other images are sent as R,G,B,X pixels (the engine process stages them from
+    pinned memory) instead of BGR."""
+    import grpc
+    loop = asyncio.get_running_loop()
+    pending: dict[int, asyncio.Future] = {}
+    ids = itertools.count()
+    outq: queue.SimpleQueue = queue.SimpleQueue()
+    pool = ThreadPoolExecutor(max_workers=decoders, thread_name_prefix="yoloserve-fe-decode")
+    stopping = asyncio.Event()
+
+    def deliver(rid, msg):
+        fut = pending.pop(rid, None)
+        if fut is not None and not fut.done():
+            fut.set_result(msg)
+
+    def engine_gone():
+        for fut in pending.values():
+            if not fut.done():
+                fut.set_result(None)
+        pending.clear()
+        stopping.set()
+
+    def reader():                         # results from the engine process
+        try:
+            while True:
+                msg = conn.recv_bytes()
+                loop.call_soon_threadsafe(deliver, _RSP.unpack_from(msg)[0], msg)
+        except (EOFError, OSError):
+            pass
+        try:
+            loop.call_soon_threadsafe(engine_gone)
+        except RuntimeError:
+            pass
+
+    def writer():                         # requests to the engine process
+        while True:
+            item = outq.get()
+            if item is None:
+                return
+            try:
+                conn.send_bytes(item[0])
+                conn.send_bytes(item[1])
+            except (EOFError, OSError):
+                return
+
+    async def detect(request, context):
+        model = request.model
+        if model and model not in names:
+            await context.abort(grpc.StatusCode.INVALID_ARGUMENT, f"unknown model: {model}")
+        mi = names.index(model) if model else 0
+        image = request.image
+        hw = jpeg_dims(image) if engine_jpeg and image[:2] == b"\xff\xd8" else None
+        if hw is not None:
+            kind, (h, w), data = KIND_JPEG, hw, image
+        else:
+            got = await loop.run_in_executor(pool, _frontend_decode, image, rgbx)
+            if got is None:
+                await context.abort(grpc.StatusCode.INVALID_ARGUMENT, "image decode failed")
+            kind, h, w, data = got
+        if stopping.is_set():
+            await context.abort(grpc.StatusCode.UNAVAILABLE, "engine process gone")
+        rid = next(ids)
+        fut = loop.create_future()
+        pending[rid] = fut
+        outq.put((_REQ.pack(rid, kind, mi, 0, h, w), data))
+        msg = await fut
+        if msg is None:
+            await context.abort(grpc.StatusCode.UNAVAILABLE, "engine process gone")
+        _, code, obb, _, n, nresp = _RSP.unpack_from(msg)
+        if code != CODE_OK:
+            err = msg[_RSP.size:_RSP.size + nresp].decode()
+            await context.abort(grpc.StatusCode.INVALID_ARGUMENT if code == CODE_INVALID
+                                else grpc.StatusCode.UNAVAILABLE, err)
+        ncol = 7 if obb else 6
+        rows = np.frombuffer(msg, np.float32, n * ncol, _RSP.size).reshape(n, ncol) if n else None
+        off = _RSP.size + n * ncol * 4
+        return response_bytes(msg[off:off + nresp], rows, bool(obb))
+
+    handler = grpc.method_handlers_generic_handler(pb.SERVICE, {
+        pb.METHOD: grpc.unary_unary_rpc_method_handler(
+            detect, request_deserializer=pb.DetectRequest.FromString, response_serializer=None)})
+    srv = grpc.aio.server(options=[("grpc.max_receive_message_length", MAX_MSG),
+                                   ("grpc.max_send_message_length", MAX_MSG), ("grpc.so_reuseport", 1)])
+    srv.add_generic_rpc_handlers((handler,))
+    try:
+        port = srv.add_insecure_port(addr)
+    except Exception as ex:
+        port, err = 0, repr(ex)
+    else:
+        err = f"cannot bind {addr}"
+    if port == 0:
+        conn.send_bytes(b"E" + err.encode())
+        return
+    await srv.start()
+    threading.Thread(target=reader, name="yoloserve-fe-results", daemon=True).start()
+    threading.Thread(target=writer, name="yoloserve-fe-requests", daemon=True).start()
+    conn.send_bytes(b"R%d" % port)
+    await stopping.wait()
+    await srv.stop(1.0)
+    outq.put(None)
+    pool.shutdown(wait=False)
+
+
+def _free_port(host: str) -> int:
+    fam = socket.AF_INET6 if ":" in host.strip("[]") else socket.AF_INET
+    with socket.socket(fam, socket.SOCK_STREAM) as sk:
+        sk.bind((host.strip("[]") if host not in ("", "0.0.0.0") else "", 0))
+        return sk.getsockname()[1]
+
+
+class _Frontends:
+    """`n` front-end processes serving `server` on one port: child programs
+    (`yoloserve.py frontend ...`) that share nothing with this process but a socket pair each;
+    grpc.Server's `stop(grace)` and `wait_for_termination()`."""
+
+    def __init__(self, server: Server, addr: str, n: int, decoders: int):
+        from multiprocessing.connection import Connection
+        host, port = addr.rsplit(":", 1)
+        if int(port) == 0:
+            port = str(_free_port(host))
+        addr = f"{host}:{port}"
+        self.procs, self.conns = [], []
+        try:
+            for _ in range(n):
+                mine, theirs = socket.socketpair()
+                cmd = [sys.executable, os.path.abspath(__file__), "frontend", "--fd", str(theirs.fileno()),
+                       "--addr", addr, "--decoders", str(decoders), "--engine-jpeg", str(int(server.engine_jpeg)),
+                       "--rgbx", str(int(server.pool is not None))]
+                for m in server.models:
+                    cmd += ["--model", m.name]
+                self.procs.append(subprocess.Popen(cmd, pass_fds=(theirs.fileno(),)))
+                theirs.close()
+                self.conns.append(Connection(mine.detach()))
+            for c, p in zip(self.conns, self.procs):
+                while not c.poll(0.5):
+                    if p.poll() is not None:
+                        raise RuntimeError(f"front-end process exited ({p.returncode}) before serving")
+                msg = c.recv_bytes()
+                if msg[:1] != b"R":
+                    raise RuntimeError(f"front-end failed: {msg[1:].decode()}")
+        except BaseException:
+            self.stop()
+            raise
+        self.port = int(port)
+        self.threads = [t for c in self.conns for t in server.serve_frontend(c)]
+
+    def stop(self, grace: float | None = None):
+        for c in self.conns:              # wakes both ends' readers: the front-ends shut down
+            try:
+                socket.socket(fileno=os.dup(c.fileno())).shutdown(socket.SHUT_RDWR)
+            except OSError:
+                pass
+        for p in self.procs:
+            try:
+                p.wait(timeout=(grace or 0) + 15)
+            except subprocess.TimeoutExpired:
+                p.kill()
+                p.wait(5)
+        for c in self.conns:
+            c.close()
+        self.conns, self.procs = [], []
+
+    def wait_for_termination(self, timeout: float | None = None) -> bool:
+        try:
+            for p in self.procs:
+                p.wait(timeout)
+        except subprocess.TimeoutExpired:
+            return False
+        return True
+
+
 def _default_decoders() -> int:
     try:
         n = len(os.sched_getaffinity(0))
@@ -655,10 +985,9 @@ class _AioServer:
                 except RuntimeError:      # the loop has already closed
                     pass
             try:
-                hw = server.engine_decodes(request.image)
-                if hw is not None:        # the engine decodes it: nothing to do off the loop
-                    r = server.submit(request.image, request.model, wake, hw)
-                else:
+                # a JPEG the engine decodes: its decoding starts on the library's threads
+                r = server.submit_jpeg(request.image, request.model, wake)
+                if r is None:
                     r = await loop.run_in_executor(decoders, server.submit, request.image, request.model, wake)
             except KeyError:
                 await context.abort(grpc.StatusCode.INVALID_ARGUMENT, f"unknown model: {request.model}")
@@ -701,10 +1030,15 @@ def _resolve(fut):
         fut.set_result(None)
 
 
-def grpc_server(server: Server, addr: str, decoders: int | None = None):
-    """A started gRPC server exposing `server` at `addr` (grpc.aio on its own event-loop
-    thread, decoding on a pool of `decoders` threads); returns (server handle, bound port).
-    The handle has grpc.Server's `stop(grace)` and `wait_for_termination()`."""
+def grpc_server(server: Server, addr: str, decoders: int | None = None, frontends: int = 0):
+    """A started gRPC server exposing `server` at `addr`; returns (server handle, bound port).
+    frontends = 0: grpc.aio on an event-loop thread of this process, decoding on a pool of
+    `decoders` threads.  frontends = n: n front-end processes on the same port (each with
+    `decoders` PIL threads, default the CPUs split between them), this process keeping the
+    engines.  The handle has grpc.Server's `stop(grace)` and `wait_for_termination()`."""
+    if frontends > 0:
+        fe = _Frontends(server, addr, frontends, decoders or max(2, _default_decoders() // frontends))
+        return fe, fe.port
     gs = _AioServer(server, addr, decoders or _default_decoders())
     return gs, gs.port
 
@@ -773,6 +1107,18 @@ def bench(addr: str, images: list[bytes], model: str = "", concurrency: int = 32
 
 def main(argv=None):
     argv = sys.argv[1:] if argv is None else argv
+    if argv and argv[0] == "frontend":    # started by grpc_server(frontends=n)
+        from multiprocessing.connection import Connection
+        ap = argparse.ArgumentParser(prog="yoloserve frontend")
+        ap.add_argument("--fd", type=int, required=True)
+        ap.add_argument("--addr", required=True)
+        ap.add_argument("--decoders", type=int, default=4)
+        ap.add_argument("--engine-jpeg", type=int, default=0)
+        ap.add_argument("--rgbx", type=int, default=0)
+        ap.add_argument("--model", action="append", default=[])
+        a = ap.parse_args(argv[1:])
+        _frontend_main(a.addr, Connection(a.fd), a.model, bool(a.engine_jpeg), bool(a.rgbx), a.decoders)
+        return 0
     if argv and argv[0] == "bench":
         ap = argparse.ArgumentParser(prog="yoloserve bench")
         ap.add_argument("--addr", default="127.0.0.1:50051")
