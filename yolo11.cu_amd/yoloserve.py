@@ -1,7 +1,7 @@
 """Detection server: the gRPC service `yolo.Yolo/Detect` over the engine's C ABI.
 
     python yolo11.cu_amd/yoloserve.py --dir models/yolo11n[:maxB] [--dir ...] \
-        [--addr 0.0.0.0:50051] [--max-batch 16] [--target-ms 50]
+        [--addr 0.0.0.0:50051] [--max-batch 16] [--target-ms 50] [--frontends N]
     python yolo11.cu_amd/yoloserve.py bench --addr 127.0.0.1:50051 --image a.jpg [--model name]
 
 Behaviour of the reference server (server/serve.cpp), on this image's stack (Python gRPC over
@@ -14,24 +14,26 @@ the same C ABI; gRPC C++ and protoc are not available here):
   request would miss `--target-ms` if the batcher waited for a full batch, given that model's
   calibrated `yolo_exec_ms(maxB)`, a decode-time EMA and a 1 ms margin; batches never mix
   models (server/serve.cpp:163-191);
-* decode overlaps the GPU (server/serve.cpp:264-302), here one step earlier: every request
-  is decoded on its own gRPC handler thread as it arrives and its pixels copied, in the
-  decoder's own R, G, B, X layout, into a pinned host buffer (the GPU letterbox reads that
-  layout), so the batcher collects ready pixels and the worker only stages the batch (one
-  call: asynchronous copies + one batched letterbox), launches, and fetches every slot's
-  detections in one call, while the next batch's images decode during the current batch's
-  GPU time.  Each handler thread serializes its own response (the detection lists with
-  numpy), so the worker only reads results.  The decoder is PIL for every format (the reference
-  decodes JPEG with nvJPEG and PNG with stb; pixel values of a lossy JPEG can differ by
-  decoder).  An undecodable image is answered at once and never takes a batch slot;
+* decoding overlaps the GPU (server/serve.cpp:71-131,264-302), here from the moment a request
+  arrives: a JPEG the engine decodes (baseline / extended Huffman, 8-bit, grayscale or YCbCr)
+  is handed to the library at once (`yolo_jpeg_submit`: entropy decoding on its decoder
+  threads), and the worker runs the GPU half for the whole batch (`yolo_decode_tickets`: copies,
+  IDCT and colour on the engine's decode stream, beside the previous batch's network), as the
+  reference does with nvJPEG; any other image is decoded by PIL on a decode pool thread
+  straight into pinned memory, in PIL's own R, G, B, X layout (the reference uses stb).  The
+  worker then reads the previous batch's results (every slot in one call), letterboxes the
+  batch in one launch and starts it.  An undecodable image is answered at once and never takes
+  a batch slot;
 * responses carry the task's fields -- boxes, rotated boxes, top-5 classes, or boxes plus
   RLE masks at proto resolution with the letterbox geometry -- and queue_ms, infer_ms and
   the batch size (server/serve.cpp:193-256); an undecodable image is INVALID_ARGUMENT
-  "image decode failed".  The slack formula's decode term is an EMA of the worker's per-batch
-  staging time (upload + preprocess).
+  "image decode failed".  Detection lists are encoded with numpy outside the worker.  The
+  slack formula's decode term is an EMA of the worker's per-batch staging time.
 
-All engine calls happen on the one worker thread (the engine handle is not thread-safe);
-gRPC handler threads only enqueue and wait.
+The gRPC layer is grpc.aio, in this process or, with `--frontends N`, in N front-end
+processes sharing the port (SO_REUSEPORT) that pass images and results to this one over
+socket pairs.  All engine calls happen on the one worker thread (the engine handle is not
+thread-safe).
 """
 from __future__ import annotations
 
@@ -1135,11 +1137,13 @@ def main(argv=None):
     ap.add_argument("--addr", default="0.0.0.0:50051")
     ap.add_argument("--max-batch", type=int, default=16)
     ap.add_argument("--target-ms", type=float, default=50.0)
+    ap.add_argument("--frontends", type=int, default=0,
+                    help="gRPC front-end processes sharing the port (0: serve in this process)")
     a = ap.parse_args(argv)
     specs = a.dir or ["build/yolo11n"]
     models = load_models(specs, a.max_batch)
     srv = Server(models, a.target_ms)
-    gs, port = grpc_server(srv, a.addr)
+    gs, port = grpc_server(srv, a.addr, frontends=a.frontends)
     print(f"yoloserve listening on {a.addr} (port {port}, {len(models)} models, target={a.target_ms:.0f} ms)",
           flush=True)
     try:
