@@ -192,3 +192,22 @@ def test_native_probe_and_failures():
             _lib_coefs(data[:hdr["offset"]] + junk + b"\xff\xd9")
         except ValueError:
             pass
+
+
+def test_host_only_jpeg_library():
+    """libyolo11_jpeg.so (what server front-end processes load) needs no HIP runtime and reads
+    every stream's headers as the engine library does."""
+    import shutil
+    import subprocess
+    import yolort
+    import yoloserve
+    path = yolort.LIB_PATH.replace("libyolo11_amd.so", "libyolo11_jpeg.so")
+    if shutil.which("readelf"):
+        needed = subprocess.run(["readelf", "-d", path], capture_output=True, text=True, check=True).stdout
+        assert "NEEDED" in needed and "amdhip" not in needed and "hsa" not in needed
+    streams = [_encode(_frame(h, w, 40 + i), **{k: v for k, v in kw.items() if k != "mode"})
+               for i, (h, w, kw) in enumerate(CORPUS[:6])]
+    streams += [_encode(_frame(24, 40, 1), quality=90, progressive=True), b"\x89PNG\r\n\x1a\n" + bytes(40), b""]
+    for s in streams:
+        r, h, w = yolort.jpeg_probe(s)
+        assert yoloserve.jpeg_dims(s) == ((h, w) if r == 1 else None)
