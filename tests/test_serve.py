@@ -414,3 +414,37 @@ def test_engine_failure_answers_every_request():
         assert late.done.wait(1.0) and late.error == "server shutting down"
     finally:
         srv.stop()
+
+
+def test_frontend_connection_malformed_message():
+    """A malformed message on a front-end connection closes that connection (the front-end
+    sees EOF and answers UNAVAILABLE) instead of stopping its reader silently; a valid request
+    on another connection is still served."""
+    import socket as _socket
+    from multiprocessing.connection import Connection
+    logs = []
+    srv = FakeServer([yoloserve.Model("det", FakeEngine(0), 4)], target_ms=5.0, log=logs.append)
+    try:
+        a, b = _socket.socketpair()
+        mine, theirs = Connection(a.detach()), Connection(b.detach())
+        srv.serve_frontend(mine)
+        theirs.send_bytes(b"\x01\x02")                     # not a request header
+        assert theirs.poll(5.0)
+        with pytest.raises(EOFError):
+            theirs.recv_bytes()
+        assert any("front-end connection closed" in l for l in logs)
+        a2, b2 = _socket.socketpair()
+        mine2, theirs2 = Connection(a2.detach()), Connection(b2.detach())
+        srv.serve_frontend(mine2)
+        img = np.full((12, 16, 3), (7, 8, 9), np.uint8)
+        theirs2.send_bytes(yoloserve._REQ.pack(5, yoloserve.KIND_BGR, 0, 0, 12, 16))
+        theirs2.send_bytes(img.tobytes())
+        assert theirs2.poll(10.0)
+        msg = theirs2.recv_bytes()
+        rid, code, obb, _, n, nresp = yoloserve._RSP.unpack_from(msg)
+        assert (rid, code, obb, n) == (5, yoloserve.CODE_OK, 0, 2)
+        rows = np.frombuffer(msg, np.float32, n * 6, yoloserve._RSP.size).reshape(n, 6)
+        assert rows[0].tolist() == [7, 8, 9, 10, 0.5, 8]
+        theirs2.close()
+    finally:
+        srv.stop()

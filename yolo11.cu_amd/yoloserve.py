@@ -495,7 +495,14 @@ class Server:
                     self._queue(r, mi)
             except (EOFError, OSError):
                 pass
-            sendq.put(None)
+            except Exception as ex:       # a malformed message: drop the connection
+                self.log(f"[serve] front-end connection closed: {ex!r}")
+                try:
+                    conn.close()
+                except OSError:
+                    pass
+            finally:
+                sendq.put(None)
 
         def sender():
             while True:
@@ -784,7 +791,7 @@ async def _frontend(addr: str, conn, names: list, engine_jpeg: bool, rgbx: bool,
             while True:
                 msg = conn.recv_bytes()
                 loop.call_soon_threadsafe(deliver, _RSP.unpack_from(msg)[0], msg)
-        except (EOFError, OSError):
+        except Exception:                 # closed, or a malformed message: stop serving
             pass
         try:
             loop.call_soon_threadsafe(engine_gone)
