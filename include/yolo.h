@@ -193,7 +193,8 @@ int yolo_run_post(void* h, int B);
 /* Tile configuration the dispatcher uses for a CONV op (autotuned or heuristic), and an
  * override (cfg < 0 restores the heuristic).  Returns -1 for non-GEMM ops.  cfg 1000 selects
  * the LDS-halo kernel for 3x3 stride-1 convs with Cin <= 64 and Cout <= 64 (Cout a multiple
- * of 16); set_op_config refuses it for other convs. */
+ * of 16), cfg 1001 the weights-resident kernel for 1x1 stride-1 convs with Cin <= 384 (a
+ * multiple of 8) and Cout a multiple of 16; set_op_config refuses them for other convs. */
 int yolo_op_config(void* h, int k);
 int yolo_set_op_config(void* h, int k, int cfg);   /* also resets the op's split-K to 1 */
 /* Split-K factor of a GEMM CONV op (autotuned at create, 1 = none) and an override: the K

@@ -394,6 +394,52 @@ def test_conv_halo_rejects(tmp_path):
         eng.close()
 
 
+@pytest.mark.parametrize("H,W,Cin,Cout,B,res,act", [
+    (80, 80, 64, 64, 2, True, modelgen.ACT_SILU),      # one chunk pair, two 16-ch fragments x 4
+    (40, 40, 384, 128, 1, False, modelgen.ACT_SILU),   # 12 chunks: two slices of 64
+    (20, 20, 256, 256, 2, True, modelgen.ACT_SILU),    # 8 chunks, two full slices of 128
+    (37, 45, 48, 96, 3, False, modelgen.ACT_SILU),     # Cin padded to 64, ragged M = 4995
+    (7, 9, 8, 16, 1, False, modelgen.ACT_NONE),        # smallest: one fragment, 63 pixels
+    (33, 17, 320, 48, 2, False, modelgen.ACT_SILU),    # Cin 320 in 12 chunks, three fragments
+    (20, 20, 192, 144, 1, False, modelgen.ACT_NONE)])  # second slice only partly live
+def test_conv_1x1_resident(tmp_path, H, W, Cin, Cout, B, res, act):
+    """The weights-resident 1x1 kernel (op config CFG_1X1): input channels from 8 to 384
+    (padded to 32-channel chunks), output slices of up to 128 channels with a partly live
+    last slice, ragged pixel counts, bias with and without SiLU and the fused residual,
+    against the oracle."""
+    d = str(tmp_path / "p1")
+    modelgen.write_single_conv(d, H, W, Cin, Cout, 1, 1, act=act, seed=Cin + Cout, residual=res)
+    g = graphfile.load(d)
+    x = np.random.default_rng(Cin).standard_normal((B, H, W, Cin), dtype=np.float32).astype(np.float16)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    ops = [graphfile.Op(**vars(o)) for o in graphfile.fuse_adds(g.ops)]
+    assert eng.num_ops == len(ops) == 1
+    eng.set_op_config(0, yolort.CFG_1X1)
+    assert eng.op_config(0) == yolort.CFG_1X1
+    eng.write(0, x)
+    eng.run_op(0, B)
+    got = eng.read(ops[0].out, B).astype(np.float32)
+    ref = interp.Interp(g, B)
+    ref.set_input(x.astype(np.float32))
+    ref.run_op(ops[0])
+    rel = post.rel_err(got, ref.view(ops[0].out))
+    print(f"1x1 {H}x{W} {Cin}->{Cout} b{B} res={res} act={act}: rel {rel:.2e}", flush=True)
+    assert rel <= TOL
+    eng.close()
+
+
+def test_conv_1x1_resident_rejects(tmp_path):
+    """The resident-1x1 config is refused where the kernel does not apply (3x3, stride 2,
+    over 384 input channels, Cout not a multiple of 16)."""
+    for i, (cin, cout, k, s) in enumerate([(32, 32, 3, 1), (32, 32, 1, 2), (512, 64, 1, 1), (32, 24, 1, 1)]):
+        d = str(tmp_path / f"r{i}")
+        modelgen.write_single_conv(d, 16, 16, cin, cout, k, s, seed=1)
+        eng = yolort.Engine(d, 1, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+        with pytest.raises(ValueError):
+            eng.set_op_config(0, yolort.CFG_1X1)
+        eng.close()
+
+
 @pytest.mark.parametrize("nmsflag", [0, yolort.YOLO_NMS_BLOCK], ids=["multi", "block"])
 @pytest.mark.parametrize("ncls", [1, 12, 20, 80])
 def test_nms_paths_crafted_heads(models, ncls, nmsflag):

@@ -1185,6 +1185,152 @@ void launchConvHalo(const View& x, const View& y, const View* res, const f16* w,
 #undef HALO_CASE
 }
 
+// ------------------------------------------------------------------ 1x1 conv, weights resident
+// Stride-1 1x1 convs with K = Cin <= 384.  Their GEMM tiles are short (a few K steps) and each
+// tile streams its weight slice into LDS again, so these memory-bound convs ran at 1.8-3.3
+// TB/s.  Here a persistent block keeps the weights of one slice of NO = 16*FN output
+// channels for the whole K in LDS, loaded once; its waves then stream groups of 16 pixels on
+// their own (no barrier after the weight load): lane (lr, lg) loads the pixel fragments
+// (input channels 32kc + 8lg .. +7 of pixel lr) straight from global memory, the next
+// group's fragments in flight while the current group computes.  MFMA 16x16x32 with the
+// weights as the A operand, so a lane ends with output channels f*16 + 4lg .. +3 of its pixel
+// (the halo kernel's epilogue).  The padded pitch (32*KC + 8) keeps the 16 lanes of a weight
+// fragment on distinct LDS banks.
+template <int KC, int FN>   // KC: 32-channel input chunks (Cin <= 32*KC); FN: 16-channel output fragments
+__global__ __launch_bounds__(256) void k_conv1x1_resident(View x, View y, View r, const f16* __restrict__ w,
+                                                          const float* __restrict__ bias, int act, int M) {
+  constexpr int CP = 32 * KC + 8;
+  constexpr int NO = 16 * FN;
+  constexpr int VPO = 4 * KC;                 // 8-channel vectors per weight row
+  __shared__ __attribute__((aligned(16))) f16 wl[NO * CP];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int Cin = x.C, Cout = y.C, o0 = blockIdx.y * NO;
+
+  // weights OHWI [Cout][Cin] of the slice -> wl[o][c], zero past Cin / Cout
+  for (int e = t; e < NO * VPO; e += 256) {
+    const int v = e % VPO, o = e / VPO, c0 = 8 * v;
+    f16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (o0 + o < Cout && c0 < Cin) val = *(const f16x8*)(w + (size_t)(o0 + o) * Cin + c0);
+    *(f16x8*)&wl[o * CP + c0] = val;
+  }
+  float bb[FN][4];
+#pragma unroll
+  for (int f = 0; f < FN; f++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int c = o0 + f * 16 + 4 * lg + e;
+      bb[f][e] = c < Cout ? bias[c] : 0.f;
+    }
+  __syncthreads();
+
+  const int groups = (M + 15) / 16;
+  const int step = gridDim.x * 4;
+  auto fetch = [&](int gi, f16x8* dst) {      // a group's pixel fragments (zeros past M / Cin)
+    const int m = gi * 16 + lr;
+    const bool live = m < M;
+    const f16* px = x.p + (size_t)(live ? m : 0) * x.s + x.o;
+#pragma unroll
+    for (int kc = 0; kc < KC; kc++) {
+      const int c0 = kc * 32 + 8 * lg;
+      f16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (live && c0 < Cin) val = *(const f16x8*)(px + c0);
+      dst[kc] = val;
+    }
+  };
+  int gi = blockIdx.x * 4 + wave;
+  f16x8 cur[KC], nxt[KC];
+  fetch(gi, cur);
+  for (; gi < groups; gi += step) {
+    fetch(gi + step, nxt);
+    f32x4 acc[FN];
+#pragma unroll
+    for (int f = 0; f < FN; f++) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < KC; kc++)
+#pragma unroll
+      for (int f = 0; f < FN; f++) {
+        const f16x8 wf = *(const f16x8*)&wl[(f * 16 + lr) * CP + kc * 32 + 8 * lg];
+        acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, cur[kc], acc[f], 0, 0, 0);
+      }
+    const int m = gi * 16 + lr;
+    if (m < M) {
+#pragma unroll
+      for (int f = 0; f < FN; f++) {
+        const int c = o0 + f * 16 + 4 * lg;
+        if (c >= Cout) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          v[e] = acc[f][e] + bb[f][e];
+          if (act == 1) v[e] = silu(v[e]);
+        }
+        if (r.p) {
+          const f16x4 rv = *(const f16x4*)(r.p + (size_t)m * r.s + r.o + c);
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[e] += (float)rv[e];
+        }
+        const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+        *(f16x4*)(y.p + (size_t)m * y.s + y.o + c) = o;
+      }
+    }
+#pragma unroll
+    for (int kc = 0; kc < KC; kc++) cur[kc] = nxt[kc];
+  }
+}
+
+// Instantiated chunk counts (Cin rounded up to 32 * KC) and fragment counts per slice.
+static int conv1x1KC(int cin) {
+  const int need = (cin + 31) / 32;
+  for (int kc : {1, 2, 3, 4, 6, 8, 12})
+    if (kc >= need) return kc;
+  return 0;
+}
+// Output channels per slice: slices of at most 128 (64 when KC = 12, whose double-buffered
+// pixel fragments leave no registers for more accumulators), evened out, rounded up to an
+// instantiated fragment count.
+static int conv1x1FN(int cout, int kc) {
+  const int most = kc >= 12 ? 64 : 128;
+  const int slices = (cout + most - 1) / most;
+  const int need = ((cout + slices - 1) / slices + 15) / 16;
+  for (int fn : {1, 2, 3, 4, 6, 8})
+    if (fn >= need && 16 * fn <= most) return fn;
+  return 0;
+}
+
+bool conv1x1Ok(const View& x, const View& y, const View* r, int k, int s, int p) {
+  return k == 1 && s == 1 && p == 0 && x.H == y.H && x.W == y.W && x.C >= 8 && x.C % 8 == 0 &&
+         conv1x1KC(x.C) > 0 && y.C >= 16 && y.C % 16 == 0 && conv1x1FN(y.C, conv1x1KC(x.C)) > 0 && x.s % 8 == 0 &&
+         x.o % 8 == 0 && y.s % 4 == 0 && y.o % 4 == 0 && (!r || (r->s % 4 == 0 && r->o % 4 == 0));
+}
+
+void launchConv1x1(const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
+                   int Bn, hipStream_t st) {
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 256;
+    return n;
+  }();
+  const View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
+  const int M = Bn * y.H * y.W, kc = conv1x1KC(x.C), fn = conv1x1FN(y.C, kc);
+  const int slices = (y.C + 16 * fn - 1) / (16 * fn);
+  const int groups = (M + 15) / 16;
+  // persistent: about four blocks per CU in all, each wave with at least one pixel group
+  int gx = std::max(1, 4 * cus / slices);
+  gx = std::min(gx, (groups + 3) / 4);
+  const dim3 grid(gx, slices);
+#define P1_CASE(KC, FN) \
+  if (kc == KC && fn == FN) { k_conv1x1_resident<KC, FN><<<grid, 256, 0, st>>>(x, y, r, w, bias, act, M); return; }
+#define P1_ROW(KC) P1_CASE(KC, 1) P1_CASE(KC, 2) P1_CASE(KC, 3) P1_CASE(KC, 4) P1_CASE(KC, 6) P1_CASE(KC, 8)
+  P1_ROW(1) P1_ROW(2) P1_ROW(3) P1_ROW(4) P1_ROW(6) P1_ROW(8)
+  P1_CASE(12, 1) P1_CASE(12, 2) P1_CASE(12, 3) P1_CASE(12, 4)
+#undef P1_ROW
+#undef P1_CASE
+}
+
 // ------------------------------------------------------------------ depthwise conv
 // One thread per (pixel, 8-channel group); weights were repacked on the host from
 // [C][k][k] to [k*k][C] so each tap is one 16-byte load (the reference does the same

@@ -187,6 +187,12 @@ constexpr int CFG_HALO = 1000;
 bool convHaloOk(const View& x, const View& y, const View* r, int k, int s, int p);
 void launchConvHalo(const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
                     int Bn, hipStream_t st);
+// 1x1 stride-1 convs with Cin <= 384 (a multiple of 8) and Cout a multiple of 16: the
+// weights-resident streaming kernel, an autotune candidate selected by the op config CFG_1X1.
+constexpr int CFG_1X1 = 1001;
+bool conv1x1Ok(const View& x, const View& y, const View* r, int k, int s, int p);
+void launchConv1x1(const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
+                   int Bn, hipStream_t st);
 void launchConvFirst(const View& x, const View& y, const f16* w, const float* bias, int s, int p,
                      int act, int Bn, hipStream_t st);
 void launchDwConv(const View& x, const View& y, const View* res, const f16* wt_kkc,

@@ -22,6 +22,7 @@ YOLO_NMS_BLOCK = 64
 PIXEL_BGR, PIXEL_RGBX = 0, 1   # frame layouts of yolo_stage_frames (B,G,R / R,G,B,X bytes)
 JPEG_STAGED, JPEG_UNSUPPORTED, JPEG_INVALID = 0, 1, 2   # yolo_stage_jpeg per-stream status
 CFG_HALO = 1000   # op config of the LDS-halo 3x3 kernel (small-channel stride-1 convs)
+CFG_1X1 = 1001    # op config of the weights-resident 1x1 kernel (stride 1, Cin <= 384)
 OP_KINDS = ["CONV", "ADD", "MAXPOOL5", "UPSAMPLE2", "COPYC", "ATTN", "DECODE", "GAP", "SOFTMAX",
             "DECODEOBB", "PS2", "DECODESEG", "MASKS"]
 MAX_OUT = 300
