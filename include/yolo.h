@@ -194,7 +194,11 @@ int yolo_run_post(void* h, int B);
  * override (cfg < 0 restores the heuristic).  Returns -1 for non-GEMM ops.  cfg 1000 selects
  * the LDS-halo kernel for 3x3 stride-1 convs with Cin <= 64 and Cout <= 64 (Cout a multiple
  * of 16), cfg 1001 the weights-resident kernel for 1x1 stride-1 convs with Cin <= 384 (a
- * multiple of 8) and Cout a multiple of 16; set_op_config refuses them for other convs. */
+ * multiple of 8) and Cout a multiple of 16, cfgs 1100 .. 1112 the tile variants of the
+ * persistent streaming conv: 1100 .. 1107 for 3x3 stride-1 convs (one LDS stage = a 32-channel
+ * block of the output tile's input halo for all 9 taps), 1108 .. 1112 for 1x1 stride-1 convs,
+ * both with Cin a multiple of 8 and Cout a multiple of 16; set_op_config refuses them for
+ * other convs. */
 int yolo_op_config(void* h, int k);
 int yolo_set_op_config(void* h, int k, int cfg);   /* also resets the op's split-K to 1 */
 /* Split-K factor of a GEMM CONV op (autotuned at create, 1 = none) and an override: the K

@@ -440,6 +440,92 @@ def test_conv_1x1_resident_rejects(tmp_path):
         eng.close()
 
 
+@pytest.mark.parametrize("v", yolort.TAP_3X3)
+@pytest.mark.parametrize("H,W,Cin,Cout,B,res", [
+    (40, 40, 192, 192, 2, True),     # six 32-channel stages, two or more channel tiles
+    (80, 80, 96, 96, 1, False),      # the yolo11x 80x80 bottleneck shape
+    (33, 45, 48, 48, 2, True),       # ragged tiles on both axes, a half-live second stage
+    (20, 20, 256, 256, 1, False),    # eight stages
+    (17, 23, 40, 112, 2, False)])    # Cin 40 (second stage 8 channels), partly live channel tile
+def test_conv_tap(tmp_path, v, H, W, Cin, Cout, B, res):
+    """The halo-staged 3x3 GEMM (op configs CFG_TAP + v, every tile variant): one LDS stage per
+    32-channel block for all 9 taps, tap groups summed through LDS, ragged tiles, channel
+    counts that leave part of a stage or a channel tile empty, bias + SiLU and the fused
+    residual, against the oracle."""
+    d = str(tmp_path / "tap")
+    modelgen.write_single_conv(d, H, W, Cin, Cout, 3, 1, seed=Cin + Cout, residual=res)
+    g = graphfile.load(d)
+    x = np.random.default_rng(Cin).standard_normal((B, H, W, Cin), dtype=np.float32).astype(np.float16)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    ops = [graphfile.Op(**vars(o)) for o in graphfile.fuse_adds(g.ops)]
+    assert eng.num_ops == len(ops) == 1
+    _check_tap(eng, g, ops, x, v, B, Cout, f"tap v{v} {H}x{W} {Cin}->{Cout} b{B} res={res}")
+
+
+def _check_tap(eng, g, ops, x, v, B, cout, label):
+    try:
+        eng.set_op_config(0, yolort.CFG_TAP + v)
+    except ValueError:
+        # refused only where the variant's channel tile is more than half empty
+        assert cout <= yolort.TAP_BN[v] // 2
+        eng.close()
+        return
+    assert eng.op_config(0) == yolort.CFG_TAP + v
+    eng.write(0, x)
+    eng.run_op(0, B)
+    got = eng.read(ops[0].out, B).astype(np.float32)
+    ref = interp.Interp(g, B)
+    ref.set_input(x.astype(np.float32))
+    ref.run_op(ops[0])
+    rel = post.rel_err(got, ref.view(ops[0].out))
+    print(f"{label}: rel {rel:.2e}", flush=True)
+    assert rel <= TOL
+    eng.close()
+
+
+@pytest.mark.parametrize("v", yolort.TAP_1X1)
+@pytest.mark.parametrize("H,W,Cin,Cout,B,res,act", [
+    (40, 40, 384, 384, 2, True, modelgen.ACT_SILU),     # 12 stages, one or more channel tiles
+    (80, 80, 192, 96, 1, False, modelgen.ACT_SILU),     # channel tile partly live (BN 128..384)
+    (33, 45, 96, 144, 2, False, modelgen.ACT_NONE),     # ragged last pixel tile, partly live channel tile
+    (20, 20, 1536, 768, 1, False, modelgen.ACT_SILU),   # 48 stages, several channel tiles
+    (17, 23, 40, 112, 2, False, modelgen.ACT_SILU)])    # Cin 40: a half-empty second stage
+def test_conv_tap_1x1(tmp_path, v, H, W, Cin, Cout, B, res, act):
+    """The streaming kernel's 1x1 variants (op configs CFG_TAP + v): the batch's pixels tiled as
+    one row, persistent blocks running the stages of all their tiles as one ring sequence, bias
+    with and without SiLU and the fused residual, against the oracle."""
+    d = str(tmp_path / "tap1")
+    modelgen.write_single_conv(d, H, W, Cin, Cout, 1, 1, act=act, seed=Cin + Cout, residual=res)
+    g = graphfile.load(d)
+    x = np.random.default_rng(Cin).standard_normal((B, H, W, Cin), dtype=np.float32).astype(np.float16)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    ops = [graphfile.Op(**vars(o)) for o in graphfile.fuse_adds(g.ops)]
+    assert eng.num_ops == len(ops) == 1
+    _check_tap(eng, g, ops, x, v, B, Cout, f"tap1x1 v{v} {H}x{W} {Cin}->{Cout} b{B} res={res}")
+
+
+def test_conv_tap_rejects(tmp_path):
+    """The streaming configs are refused where the kernel does not apply (stride 2, the
+    other kernel size, Cout not a multiple of 16) and past the last variant."""
+    cases = [(32, 32, 3, 2, yolort.TAP_3X3), (32, 32, 1, 1, yolort.TAP_3X3), (32, 24, 3, 1, yolort.TAP_3X3),
+             (256, 256, 1, 2, yolort.TAP_1X1), (256, 256, 3, 1, yolort.TAP_1X1), (256, 248, 1, 1, yolort.TAP_1X1)]
+    for i, (cin, cout, k, s, variants) in enumerate(cases):
+        d = str(tmp_path / f"r{i}")
+        modelgen.write_single_conv(d, 16, 16, cin, cout, k, s, seed=1)
+        eng = yolort.Engine(d, 1, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+        for v in variants:
+            with pytest.raises(ValueError):
+                eng.set_op_config(0, yolort.CFG_TAP + v)
+        eng.close()
+    d = str(tmp_path / "ok")
+    modelgen.write_single_conv(d, 16, 16, 64, 64, 3, 1, seed=1)
+    eng = yolort.Engine(d, 1, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    eng.set_op_config(0, yolort.CFG_TAP)
+    with pytest.raises(ValueError):
+        eng.set_op_config(0, yolort.CFG_TAP + yolort.NUM_TAP_TILES)
+    eng.close()
+
+
 @pytest.mark.parametrize("nmsflag", [0, yolort.YOLO_NMS_BLOCK], ids=["multi", "block"])
 @pytest.mark.parametrize("ncls", [1, 12, 20, 80])
 def test_nms_paths_crafted_heads(models, ncls, nmsflag):

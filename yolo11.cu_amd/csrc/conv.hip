@@ -94,6 +94,18 @@ __device__ __forceinline__ f16x8 ds_read16(unsigned addr) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
   return v;
 }
+template <int OFF>
+__device__ __forceinline__ f32x4 ds_read16f(unsigned addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds_read offset field is 16 bits");
+  f32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+template <int OFF>
+__device__ __forceinline__ void ds_write16f(unsigned addr, f32x4 v) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds_write offset field is 16 bits");
+  asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(addr), "v"(v), "i"(OFF) : "memory");
+}
 template <int N>
 __device__ __forceinline__ void lgkm_wait() {
   static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
@@ -1329,6 +1341,412 @@ void launchConv1x1(const View& x, const View& y, const View* res, const f16* w, 
   P1_CASE(12, 1) P1_CASE(12, 2) P1_CASE(12, 3) P1_CASE(12, 4)
 #undef P1_ROW
 #undef P1_CASE
+}
+
+// ------------------------------------------------------------------ streaming conv (3x3 halo-staged, 1x1)
+// 3x3 stride-1 convs with mid-size channel counts (the C3k bottleneck convs of the larger
+// models: 48-256 channels at 20-160 pixels), and 1x1 stride-1 convs (KS = 1: no halo, one tap,
+// the batch's pixels tiled as one row).  The GEMM walks K one (tap, channel block) at a
+// time, so every stage re-fetches a shifted copy of the same pixels into LDS and feeds only
+// one or two MFMA k-steps per barrier.  Here a stage is one 32-channel block of the input for
+// all 9 taps: the DMA stages the (TH+2) x (TW+2)-pixel halo of a TH x TW output tile once,
+// plus the 9 taps' weights of BN output channels, and the waves run 9 MFMA k-steps from it
+// (a tap's pixel fragment is the halo shifted by (ky, kx): a per-lane LDS address, the tap
+// offset an immediate).
+// Blocks are persistent: block b owns channel tile b % ntN (the grid is a multiple of ntN)
+// and the pixel tiles of items b, b + grid, b + 2 grid, ...; the LDS ring runs through the
+// stages of all its tiles as one sequence, so the next tile's first stages are in flight while
+// the current tile finishes and stores (these convs have only 2-8 stages per tile, and a
+// block that starts cold pays the whole DMA latency again).
+// KG tap groups of WP x WN waves split the 9 taps of every stage (group g takes taps
+// [ceil(9g/KG), ceil(9(g+1)/KG))), so each SIMD holds one wave of every group without adding
+// LDS traffic; at the end of a tile the groups' fp32 partials are summed through the ring
+// slot just consumed, in group order.
+// Halo pixels are 64-byte LDS rows (one 32-channel block), weight rows likewise, so every
+// fragment read of 16 consecutive pixels or channels is one contiguous 1 KB run.
+// Global -> LDS is the GEMM's buffer_load ... lds DMA, with the descriptor range check
+// returning zeros for halo pixels outside the image, channels past Cin and rows past Cout.
+// One 16-byte-per-lane buffer load into LDS (lane L's bytes land at dst + 16 L).  Called
+// through this function: issued directly from a kernel template's lambda, the builtin kept
+// clang's host pass from emitting that kernel's launch stub.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, lds_ptr dst, unsigned off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, off, 0, 0, 0);
+}
+
+template <int KS, int TH, int TW, int BN, int WP, int WN, int KG, int NS>
+__global__ __launch_bounds__(64 * WP * WN * KG) void k_conv_tap(View x, View y, View r, const f16* __restrict__ w,
+                                                                const float* __restrict__ bias, int act, int H,
+                                                                int W, int tilesX, int tilesY, int ntN, int items,
+                                                                int xbytes) {
+  constexpr int NWG = WP * WN, NW = NWG * KG;
+  constexpr int TAPS = KS * KS, HALO = KS / 2;
+  constexpr int HW2 = TW + KS - 1, HP = (TH + KS - 1) * HW2;
+  constexpr int FPB = TH * TW / 16;            // pixel fragments of the tile
+  constexpr int FM = FPB / WP, FN = BN / 16 / WN;
+  constexpr bool PAIR = FN % 2 == 0;
+  constexpr int HC = HP * 4, WC = TAPS * BN * 4;   // 16-byte chunks of a stage's halo and weights
+  constexpr int IH = (HC + 64 * NW - 1) / (64 * NW), IW = (WC + 64 * NW - 1) / (64 * NW);
+  constexpr int NI = IH + IW;                  // DMA instructions per wave per stage
+  constexpr int HREG = IH * NW * 64;           // chunks of the (padded) halo region
+  constexpr int SZ = HREG + IW * NW * 64;      // chunks per stage
+  static_assert(TH * TW % 16 == 0 && FPB % WP == 0 && BN % (16 * WN) == 0, "tile shape");
+  static_assert(FM + FN <= 15, "a tap's fragment reads fit the lgkm counter");
+  constexpr bool PIPE = 2 * (FM + FN) <= 15;   // two taps' reads in flight at once
+  static_assert(KS == 1 || KS == 3, "1x1 or 3x3");
+  static_assert(KG >= 1 && KG <= TAPS, "tap groups");
+  static_assert(16 * ((TAPS - 1) * BN * 4 + (FN - 1) * 64) < 65536, "weight offsets fit the ds_read offset field");
+  static_assert(NS >= 2 && (NS - 2) * NI < 64, "ring depth");
+  static_assert(KG == 1 || (KG - 1) * NWG * 64 * FM * FN <= SZ, "tap-group partials fit one ring slot");
+  static_assert(KG == 1 || 1024 * NWG * (KG - 1) * FN * FM <= 65536, "partial offsets fit the ds offset field");
+  __shared__ f16x8 ring[NS * SZ];
+
+  const int Cin = x.C, N = y.C;
+  const int nb = gridDim.x, b = blockIdx.x;
+  const int nt = b % ntN, bn = nt * BN;
+  const int mine = b < items ? (items - 1 - b) / nb + 1 : 0;   // items of this block
+  if (mine == 0) return;
+  const int perImg = tilesX * tilesY;
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int kg = wave / NWG, wq = wave - kg * NWG;
+  const int wp = wq % WP, wn = wq / WP;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int c8 = 8 * (lane & 3);   // this lane's 8 channels inside every 32-channel block
+
+  __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(x.p, (short)0, xbytes, 0x00020000);
+  __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(w), (short)0, N * TAPS * Cin * 2, 0x00020000);
+  // DMA slot (i*NW + wave)*64 + lane of a region: halo chunk = (halo pixel, lane & 3);
+  // weight chunk = ((tap, LDS row), lane & 3), LDS row r holding output channel bn + chperm(r)
+  // when fragments pair up (a lane then ends with 8 consecutive channels).  The weight
+  // addresses are the same for every tile of the block.
+  unsigned ha[IH], wa[IW];
+#pragma unroll
+  for (int i = 0; i < IW; i++) {
+    const int slot = (i * NW + wave) * 64 + lane, q = slot >> 2;
+    const int tap = q / BN, row = q - tap * BN;
+    const int n = bn + (PAIR ? chperm(row) : row);
+    const bool ok = slot < WC && n < N;
+    wa[i] = ok ? 2u * (unsigned)((n * TAPS + tap) * Cin + c8) : OOB_OFF;
+  }
+  struct Tile { int img, y0, x0; };
+  auto tileOf = [&](int k) __attribute__((always_inline)) {   // pixel tile of this block's item k
+    const int pt = (b + k * nb) / ntN;
+    const int img = pt / perImg, rem = pt - img * perImg;
+    const int ty = rem / tilesX;
+    return Tile{img, ty * TH, (rem - ty * tilesX) * TW};
+  };
+  auto haloAddrs = [&](int k) __attribute__((always_inline)) {
+    const Tile tl = tileOf(k);
+#pragma unroll
+    for (int i = 0; i < IH; i++) {
+      const int slot = (i * NW + wave) * 64 + lane, hp = slot >> 2;
+      const int hy = hp / HW2, hx = hp - hy * HW2;
+      const int iy = tl.y0 - HALO + hy, ix = tl.x0 - HALO + hx;
+      const bool ok = slot < HC && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+      ha[i] = ok ? 2u * (unsigned)(((tl.img * H + iy) * W + ix) * x.s + x.o + c8) : OOB_OFF;
+    }
+  };
+  const int nks = (Cin + 31) / 32;   // stages per tile
+  int iItem = 0, iS = 0;             // next (item, stage) the DMA fetches
+  auto issueNext = [&](f16x8* buf) __attribute__((always_inline)) {
+    if (iS == 0) haloAddrs(iItem);
+    const int k0 = iS * 32;
+    const bool kin = k0 + c8 < Cin;
+    const unsigned ku = 2u * (unsigned)k0;
+#pragma unroll
+    for (int i = 0; i < IH; i++)
+      dma16(rx, (lds_ptr)(buf + (i * NW + wave) * 64), kin ? ha[i] + ku : OOB_OFF);
+#pragma unroll
+    for (int i = 0; i < IW; i++)
+      dma16(rw, (lds_ptr)(buf + HREG + (i * NW + wave) * 64), kin ? wa[i] + ku : OOB_OFF);
+    if (++iS == nks) {
+      iS = 0;
+      iItem++;
+    }
+  };
+
+  // fragment bases: pixel fragment j of this wave (lane lr = one pixel of the tile) at tap
+  // (0, 0), and weight fragment 0 of this wave at tap 0; tap offsets are immediates
+  unsigned pb[FM];
+#pragma unroll
+  for (int j = 0; j < FM; j++) {
+    const int p = (wp * FM + j) * 16 + lr, py = p / TW, px = p - py * TW;
+    pb[j] = 16u * (unsigned)((py * HW2 + px) * 4 + lg);
+  }
+  const unsigned wb = 16u * (unsigned)(HREG + (wn * FN * 16 + lr) * 4 + lg);
+
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; i++)
+#pragma unroll
+    for (int j = 0; j < FM; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // epilogue bias of this lane's channels (the same for every tile of the block)
+  float bpre[FN][4];
+#pragma unroll
+  for (int i = 0; i < FN; i++) {
+    const int n0 = PAIR ? bn + wn * FN * 16 + 32 * (i / 2) + 8 * lg + 4 * (i % 2) : bn + wn * FN * 16 + i * 16 + 4 * lg;
+#pragma unroll
+    for (int e = 0; e < 4; e++) bpre[i][e] = n0 + e < N ? bias[n0 + e] : 0.f;
+  }
+
+  // ---- epilogue of item k: + bias, SiLU, + residual, fp16 store of this lane's pixels
+  auto epilogue = [&](int k) __attribute__((always_inline)) {
+    const Tile tl = tileOf(k);
+#pragma unroll
+    for (int q = 0; q < FM; q++) {
+      const int p = (wp * FM + q) * 16 + lr, py = p / TW, px = p - py * TW;
+      const int oy = tl.y0 + py, ox = tl.x0 + px;
+      if (oy >= H || ox >= W) continue;
+      const size_t m = (size_t)(tl.img * H + oy) * W + ox;
+      if constexpr (PAIR) {
+#pragma unroll
+        for (int p2 = 0; p2 < FN / 2; p2++) {
+          const int n0 = bn + wn * FN * 16 + 32 * p2 + 8 * lg;
+          if (n0 >= N) continue;   // N % 8 == 0: all 8 channels valid or none
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            v[e] = acc[2 * p2][q][e] + bpre[2 * p2][e];
+            v[4 + e] = acc[2 * p2 + 1][q][e] + bpre[2 * p2 + 1][e];
+          }
+          if (act == 1) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = silu(v[e]);
+          }
+          if (r.p) {
+            const f16x8 rv = *(const f16x8*)(r.p + m * r.s + r.o + n0);
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] += (float)rv[e];
+          }
+          f16x8 o;
+#pragma unroll
+          for (int e = 0; e < 8; e++) o[e] = (f16)v[e];
+          *(f16x8*)(y.p + m * y.s + y.o + n0) = o;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < FN; i++) {
+          const int n0 = bn + wn * FN * 16 + i * 16 + 4 * lg;
+          if (n0 >= N) continue;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            v[e] = acc[i][q][e] + bpre[i][e];
+            if (act == 1) v[e] = silu(v[e]);
+          }
+          if (r.p) {
+            const f16x4 rv = *(const f16x4*)(r.p + m * r.s + r.o + n0);
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] += (float)rv[e];
+          }
+          const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+          *(f16x4*)(y.p + m * y.s + y.o + n0) = o;
+        }
+      }
+    }
+  };
+
+  // Stage q of the block's sequence: wait for this wave's loads of stage q (loads and
+  // stores issued after them may stay in flight), barrier (every wave's chunks of stage q
+  // are in LDS and every wave is done with the slot the DMA refills next), refill that slot
+  // with stage q + NS - 1, then the fragment reads and MFMAs of stage q.
+  auto waitStage = [&](int ahead) __attribute__((always_inline)) {
+    static_for<NS - 1>([&](auto A) {
+      if (ahead == A) vmwait<A * NI>();
+    });
+  };
+  const int total = mine * nks;
+  static_for<NS - 1>([&](auto J) {
+    if (J < total) issueNext(ring + J * SZ);
+  });
+  int cS = 0, cItem = 0;   // (item, stage) being computed
+  for (int q0 = 0; q0 < total; q0 += NS) {
+    static_for<NS>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const int q = q0 + j;
+      if (q < total) {
+        waitStage(min(NS - 2, total - 1 - q));
+        asm volatile("s_barrier" ::: "memory");
+        const unsigned base = (unsigned)(size_t)(lds_f16x8)(ring + j * SZ);
+        unsigned ap[FM];
+#pragma unroll
+        for (int u = 0; u < FM; u++) ap[u] = base + pb[u];
+        const unsigned aw = base + wb;
+        if (q + NS - 1 < total) issueNext(ring + ((j + NS - 1) % NS) * SZ);
+        __builtin_amdgcn_sched_barrier(0);
+        // with room in the lgkm counter for two taps' reads, tap t+1's fragment reads are
+        // issued before tap t's MFMAs
+        static_for<KG>([&](auto G) {
+          constexpr int t0 = (TAPS * G + KG - 1) / KG, t1 = (TAPS * (G + 1) + KG - 1) / KG;
+          if (kg == G) {
+            f16x8 fa[2][FN], fb[2][FM];
+            auto reads = [&](auto T, auto S) __attribute__((always_inline)) {
+              constexpr int tap = decltype(T)::value, ky = tap / KS, kx = tap % KS;
+              static_for<FN>([&](auto I) { fa[S][I] = ds_read16<16 * (tap * BN * 4 + I * 64)>(aw); });
+              static_for<FM>([&](auto Q) { fb[S][Q] = ds_read16<64 * (ky * HW2 + kx)>(ap[Q]); });
+            };
+            reads(ic<t0>{}, ic<0>{});
+            static_for<t1 - t0>([&](auto U) {
+              constexpr int tap = t0 + U, cur = PIPE ? U % 2 : 0;
+              constexpr int later = PIPE && tap + 1 < t1 ? FN + FM : 0;
+              if constexpr (later > 0) reads(ic<tap + 1>{}, ic<1 - cur>{});
+              static_for<FM>([&](auto Q) {
+                lgkm_wait<later + FM - 1 - Q>();
+                if constexpr (Q == 0) {
+#pragma unroll
+                  for (int i = 0; i < FN; i++) asm volatile("" : "+v"(fa[cur][i]));
+                }
+                asm volatile("" : "+v"(fb[cur][Q]));
+#pragma unroll
+                for (int i = 0; i < FN; i++)
+                  acc[i][Q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[cur][i], fb[cur][Q], acc[i][Q], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+              });
+              if constexpr (!PIPE && tap + 1 < t1) reads(ic<tap + 1>{}, ic<0>{});
+            });
+          }
+        });
+        if (++cS == nks) {   // last stage of the tile: reduce the tap groups, store, restart
+          cS = 0;
+          if constexpr (KG > 1) {
+            // the slot just consumed is free until the DMA after the next barrier refills it;
+            // partial (g, i, u) of wave wq, lane L at 16 * ((((g-1)*FN + i)*FM + u)*NWG*64 + wq*64 + L)
+            const unsigned red = base + 16u * (unsigned)(wq * 64 + lane);
+            asm volatile("s_barrier" ::: "memory");   // every wave is done reading the slot
+            static_for<KG - 1>([&](auto G1) {
+              if (kg == G1 + 1) {
+                static_for<FN>([&](auto I) {
+                  static_for<FM>([&](auto U) {
+                    ds_write16f<1024 * NWG * ((G1 * FN + I) * FM + U)>(red, acc[I][U]);
+                  });
+                });
+              }
+            });
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (kg == 0) {
+              static_for<KG - 1>([&](auto G1) {
+                f32x4 part[FN][FM];
+                static_for<FN>([&](auto I) {
+                  static_for<FM>([&](auto U) { part[I][U] = ds_read16f<1024 * NWG * ((G1 * FN + I) * FM + U)>(red); });
+                });
+                lgkm_wait<0>();
+#pragma unroll
+                for (int i = 0; i < FN; i++)
+#pragma unroll
+                  for (int u = 0; u < FM; u++) {
+                    asm volatile("" : "+v"(part[i][u]));
+                    acc[i][u] += part[i][u];
+                  }
+              });
+            }
+          }
+          if (kg == 0) epilogue(cItem);
+#pragma unroll
+          for (int i = 0; i < FN; i++)
+#pragma unroll
+            for (int u = 0; u < FM; u++) acc[i][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+          cItem++;
+        }
+      }
+    });
+  }
+}
+
+// {kernel size, tile rows, tile columns, output channels, waves along pixels, waves along
+//  channels, tap groups, LDS stages}.  1x1 variants tile the pixels of the whole batch as one
+// row (TH = 1): a pointwise conv does not care where its pixels sit.
+#define YOLO_TAP_TILES(X)            \
+  X(0, 3, 8, 20, 64, 2, 2, 2, 2)     \
+  X(1, 3, 8, 16, 96, 2, 2, 2, 2)     \
+  X(2, 3, 4, 40, 64, 2, 2, 2, 2)     \
+  X(3, 3, 4, 16, 48, 2, 1, 2, 2)     \
+  X(4, 3, 2, 40, 64, 1, 2, 2, 2)     \
+  X(5, 3, 4, 20, 64, 1, 2, 2, 2)     \
+  X(6, 3, 8, 16, 64, 2, 2, 2, 2)     \
+  X(7, 3, 4, 16, 64, 1, 2, 2, 2)     \
+  X(8, 1, 1, 128, 384, 2, 4, 1, 3)   \
+  X(9, 1, 1, 256, 192, 4, 2, 1, 3)   \
+  X(10, 1, 1, 128, 192, 2, 2, 1, 4)  \
+  X(11, 1, 1, 256, 128, 4, 2, 1, 3)  \
+  X(12, 1, 1, 128, 256, 2, 4, 1, 3)
+
+struct TapTile { int KS, TH, TW, BN; };
+static const TapTile kTapTiles[] = {
+#define X(i, ks, th, tw, bn, wp, wn, kg, ns) {ks, th, tw, bn},
+    YOLO_TAP_TILES(X)
+#undef X
+};
+constexpr int kNumTapTiles = sizeof(kTapTiles) / sizeof(kTapTiles[0]);
+int numTapTiles() { return kNumTapTiles; }
+
+bool convTapOk(int v, const View& x, const View& y, const View* r, int k, int s, int p) {
+  if (v < 0 || v >= kNumTapTiles) return false;
+  const TapTile& tt = kTapTiles[v];
+  return k == tt.KS && s == 1 && p == tt.KS / 2 && x.H == y.H && x.W == y.W && x.C >= 8 && x.C % 8 == 0 &&
+         y.C >= 16 && y.C % 16 == 0 && tt.BN / 2 < y.C && x.s % 8 == 0 && x.o % 8 == 0 && y.s % 8 == 0 &&
+         y.o % 8 == 0 && (!r || (r->s % 8 == 0 && r->o % 8 == 0));
+}
+
+// Resident blocks of a variant on the chip (CUs x blocks per CU): the persistent grid's size.
+template <int KS, int TH, int TW, int BN, int WP, int WN, int KG, int NS>
+static int tapSlotsOf() {
+  int dev = 0, cus = 0, per = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_conv_tap<KS, TH, TW, BN, WP, WN, KG, NS>,
+                                                   64 * WP * WN * KG, 0) != hipSuccess)
+    return 0;
+  return cus * std::max(per, 1);
+}
+
+template <int KS, int TH, int TW, int BN, int WP, int WN, int KG, int NS>
+static void launchTap(const View& x, const View& y, const View& r, const f16* w, const float* bias, int act, int H,
+                      int W, int tilesX, int tilesY, int ntN, int items, int xbytes, hipStream_t st) {
+  static const int slots = tapSlotsOf<KS, TH, TW, BN, WP, WN, KG, NS>();
+  // persistent grid: the chip's resident blocks, a multiple of the channel tiles, spread so
+  // every block gets the floor or ceiling of the average item count
+  int grid = std::max(ntN, std::min(items, slots) / ntN * ntN);
+  const int per = (items + grid - 1) / grid;
+  grid = std::max(ntN, ((items + per - 1) / per + ntN - 1) / ntN * ntN);
+  k_conv_tap<KS, TH, TW, BN, WP, WN, KG, NS><<<grid, 64 * WP * WN * KG, 0, st>>>(x, y, r, w, bias, act, H, W, tilesX,
+                                                                                tilesY, ntN, items, xbytes);
+}
+
+void launchConvTap(int v, const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
+                   int Bn, hipStream_t st) {
+  if (v < 0 || v >= kNumTapTiles) return;
+  const TapTile& tt = kTapTiles[v];
+  const View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
+  // 1x1: the batch's pixels as one row of one image
+  const int H = tt.KS == 1 ? 1 : y.H, W = tt.KS == 1 ? Bn * y.H * y.W : y.W, imgs = tt.KS == 1 ? 1 : Bn;
+  const int tilesX = (W + tt.TW - 1) / tt.TW, tilesY = (H + tt.TH - 1) / tt.TH;
+  const int ntN = (y.C + tt.BN - 1) / tt.BN;
+  const int items = imgs * tilesX * tilesY * ntN;
+  const int xbytes = (int)((long)Bn * x.H * x.W * x.s * 2);
+  switch (v) {
+#define X(i, ks, th, tw, bn, wp, wn, kg, ns)                                                                       \
+    case i:                                                                                                       \
+      launchTap<ks, th, tw, bn, wp, wn, kg, ns>(x, y, r, w, bias, act, H, W, tilesX, tilesY, ntN, items, xbytes, st); \
+      break;
+    YOLO_TAP_TILES(X)
+#undef X
+    default: break;
+  }
+}
+
+bool specialConvOk(int cfg, const View& x, const View& y, const View* r, int k, int s, int p) {
+  if (cfg == CFG_HALO) return convHaloOk(x, y, r, k, s, p);
+  if (cfg == CFG_1X1) return conv1x1Ok(x, y, r, k, s, p);
+  return convTapOk(cfg - CFG_TAP, x, y, r, k, s, p);
+}
+
+void launchSpecialConv(int cfg, const View& x, const View& y, const View* res, const f16* w, const float* bias,
+                       int act, int Bn, hipStream_t st) {
+  if (cfg == CFG_HALO) launchConvHalo(x, y, res, w, bias, act, Bn, st);
+  else if (cfg == CFG_1X1) launchConv1x1(x, y, res, w, bias, act, Bn, st);
+  else launchConvTap(cfg - CFG_TAP, x, y, res, w, bias, act, Bn, st);
 }
 
 // ------------------------------------------------------------------ depthwise conv

@@ -515,10 +515,8 @@ struct Engine {
         const float* b = bias + op.boff;
         if (op.g == 1 && op.Cin == 3)
           launchConvFirst(x, y, w, b, op.s, op.p, op.act, Bn, s);
-        else if (op.g == 1 && op.cfg == CFG_HALO && convHaloOk(x, y, rp, op.k, op.s, op.p))
-          launchConvHalo(x, y, rp, w, b, op.act, Bn, s);   // (else: the GEMM's default tile)
-        else if (op.g == 1 && op.cfg == CFG_1X1 && conv1x1Ok(x, y, rp, op.k, op.s, op.p))
-          launchConv1x1(x, y, rp, w, b, op.act, Bn, s);
+        else if (op.g == 1 && specialConvCfg(op.cfg) && specialConvOk(op.cfg, x, y, rp, op.k, op.s, op.p))
+          launchSpecialConv(op.cfg, x, y, rp, w, b, op.act, Bn, s);   // (else: the GEMM's default tile)
         else if (op.g == 1)
           launchConvGemm(op.cfg, x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, op.split,
                          op.wsOff >= 0 ? splitWs + op.wsOff : nullptr,
@@ -569,7 +567,7 @@ struct Engine {
     if (op.kind == COPYC) return GK_COPY;
     if (op.kind != CONV) return GK_NONE;
     if (op.g > 1) return GK_DW;
-    if (op.Cin == 3 || op.cfg == CFG_HALO || op.cfg == CFG_1X1) return GK_NONE;
+    if (op.Cin == 3 || specialConvCfg(op.cfg)) return GK_NONE;
     return GK_GEMM;
   }
   ConvJob convJob(int k) {
@@ -815,8 +813,7 @@ struct Engine {
     size_t wsTot = 0, cntTot = 0;
     for (OpDesc& op : ops) {
       op.wsOff = op.cntOff = -1;
-      if (op.kind != CONV || op.g != 1 || op.Cin == 3 || op.split == 1 || op.split == -1 || op.cfg == CFG_HALO ||
-          op.cfg == CFG_1X1)
+      if (op.kind != CONV || op.g != 1 || op.Cin == 3 || op.split == 1 || op.split == -1 || specialConvCfg(op.cfg))
         continue;
       View y = view(op.out);
       const int M = B * y.H * y.W, cfg = op.cfg >= 0 ? op.cfg : heuristicTile(M, op.Cout, op.k * op.k * op.Cin);
@@ -845,22 +842,23 @@ struct Engine {
     std::map<std::tuple<int, int, int, int, int, int, int, int>, std::pair<int, int>> cache;
     static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
     // YOLO_TUNE_TILES="a,b,..." restricts the candidate tile configs (for A/B studies); the
-    // halo and resident-1x1 kernels take part unless YOLO_TUNE_TILES is set without their
-    // entries (1000, 1001)
+    // special kernels (halo 1000, resident 1x1 1001, halo-staged 3x3 variants 1100+) take part
+    // unless YOLO_TUNE_TILES is set without their entries
     std::vector<char> allowed(numTileConfigs(), 1);
-    bool allowHalo = true, allow1x1 = true;
+    std::vector<int> specials = {CFG_HALO, CFG_1X1};
+    for (int v = 0; v < numTapTiles(); v++) specials.push_back(CFG_TAP + v);
     if (const char* lim = getenv("YOLO_TUNE_TILES")) {
       std::fill(allowed.begin(), allowed.end(), 0);
-      allowHalo = allow1x1 = false;
+      std::vector<int> keep;
       for (const char* q = lim; *q;) {
         char* end = nullptr;
         const long v = strtol(q, &end, 10);
         if (end == q) break;
         if (v >= 0 && v < numTileConfigs()) allowed[v] = 1;
-        if (v == CFG_HALO) allowHalo = true;
-        if (v == CFG_1X1) allow1x1 = true;
+        if (specialConvCfg((int)v)) keep.push_back((int)v);
         q = *end ? end + 1 : end;
       }
+      specials = keep;
     }
     for (size_t k = 0; k < ops.size(); k++) {
       OpDesc& op = ops[k];
@@ -901,14 +899,12 @@ struct Engine {
           if (ms < bestMs) { bestMs = ms; best = cfg; bestSplit = S; }
         }
       }
-      // the LDS-halo and the resident-1x1 kernels, where they apply
+      // the special kernels, where they apply
       View hr{};
       if (op.b >= 0) hr = view(op.b);
       const View* hrp = op.b >= 0 ? &hr : nullptr;
-      for (int special : {CFG_HALO, CFG_1X1}) {
-        const bool ok = special == CFG_HALO ? allowHalo && convHaloOk(view(op.a), y, hrp, op.k, op.s, op.p)
-                                            : allow1x1 && conv1x1Ok(view(op.a), y, hrp, op.k, op.s, op.p);
-        if (!ok) continue;
+      for (int special : specials) {
+        if (!specialConvOk(special, view(op.a), y, hrp, op.k, op.s, op.p)) continue;
         op.cfg = special;
         op.split = 1;
         op.wsOff = op.cntOff = -1;
@@ -1895,13 +1891,11 @@ int yolo_set_op_config(void* h, int k, int cfg) {
   if (k < 0 || k >= (int)e->ops.size()) return -1;
   yolo::OpDesc& op = e->ops[k];
   if (op.kind != yolo::CONV || op.g != 1 || op.Cin == 3) return -1;
-  if (cfg == yolo::CFG_HALO || cfg == yolo::CFG_1X1) {
+  if (yolo::specialConvCfg(cfg)) {
     yolo::View r{};
     if (op.b >= 0) r = e->view(op.b);
     const yolo::View* rp = op.b >= 0 ? &r : nullptr;
-    const bool ok = cfg == yolo::CFG_HALO ? yolo::convHaloOk(e->view(op.a), e->view(op.out), rp, op.k, op.s, op.p)
-                                          : yolo::conv1x1Ok(e->view(op.a), e->view(op.out), rp, op.k, op.s, op.p);
-    if (!ok) return -1;
+    if (!yolo::specialConvOk(cfg, e->view(op.a), e->view(op.out), rp, op.k, op.s, op.p)) return -1;
   } else if (cfg >= yolo::numTileConfigs()) {
     return -1;
   }
@@ -1925,7 +1919,7 @@ int yolo_set_op_split(void* h, int k, int splits) {
     if (k < 0 || k >= (int)e->ops.size()) return -1;
     yolo::OpDesc& op = e->ops[k];
     if (op.kind != yolo::CONV || op.g != 1 || op.Cin == 3) return -1;
-    if (op.cfg == yolo::CFG_HALO || op.cfg == yolo::CFG_1X1) return -1;   // not GEMM tiles
+    if (yolo::specialConvCfg(op.cfg)) return -1;   // not GEMM tiles
     bool captured = e->frameGraph != nullptr;
     for (auto ge : e->graphs) captured = captured || ge != nullptr;
     if (captured) return -1;    // captured graphs hold the current workspace pointers

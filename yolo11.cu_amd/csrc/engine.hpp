@@ -193,6 +193,22 @@ constexpr int CFG_1X1 = 1001;
 bool conv1x1Ok(const View& x, const View& y, const View* r, int k, int s, int p);
 void launchConv1x1(const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
                    int Bn, hipStream_t st);
+// 3x3 stride-1 convs with Cin % 8 == 0 and Cout % 16 == 0: the halo-staged GEMM (a stage is
+// one 32-channel block of the tile's input halo for all 9 taps), tile variant v in
+// [0, numTapTiles()); autotune candidates selected by the op configs CFG_TAP + v.
+constexpr int CFG_TAP = 1100;
+int numTapTiles();
+bool convTapOk(int v, const View& x, const View& y, const View* r, int k, int s, int p);
+void launchConvTap(int v, const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
+                   int Bn, hipStream_t st);
+// Op configs that select a kernel other than a GEMM tile (no split-K, no grouped launches).
+inline bool specialConvCfg(int cfg) {
+  return cfg == CFG_HALO || cfg == CFG_1X1 || (cfg >= CFG_TAP && cfg < CFG_TAP + numTapTiles());
+}
+// Whether special config `cfg` applies to a conv, and its launch.
+bool specialConvOk(int cfg, const View& x, const View& y, const View* r, int k, int s, int p);
+void launchSpecialConv(int cfg, const View& x, const View& y, const View* res, const f16* w, const float* bias,
+                       int act, int Bn, hipStream_t st);
 void launchConvFirst(const View& x, const View& y, const f16* w, const float* bias, int s, int p,
                      int act, int Bn, hipStream_t st);
 void launchDwConv(const View& x, const View& y, const View* res, const f16* wt_kkc,
