@@ -193,9 +193,10 @@ constexpr int CFG_1X1 = 1001;
 bool conv1x1Ok(const View& x, const View& y, const View* r, int k, int s, int p);
 void launchConv1x1(const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
                    int Bn, hipStream_t st);
-// 3x3 stride-1 convs with Cin % 8 == 0 and Cout % 16 == 0: the halo-staged GEMM (a stage is
-// one 32-channel block of the tile's input halo for all 9 taps), tile variant v in
-// [0, numTapTiles()); autotune candidates selected by the op configs CFG_TAP + v.
+// The persistent streaming conv, tile variant v in [0, numTapTiles()): 3x3 stride-1 variants
+// (a stage is one 32-channel block of the tile's input halo for all 9 taps) and 1x1 stride-1
+// variants, all for Cin % 8 == 0 and Cout % 16 == 0; autotune candidates selected by the op
+// configs CFG_TAP + v.
 constexpr int CFG_TAP = 1100;
 int numTapTiles();
 bool convTapOk(int v, const View& x, const View& y, const View* r, int k, int s, int p);
