@@ -1396,8 +1396,11 @@ __global__ __launch_bounds__(64 * WP * WN * KG) void k_conv_tap(View x, View y, 
   static_assert(KG >= 1 && KG <= TAPS, "tap groups");
   static_assert(16 * ((TAPS - 1) * BN * 4 + (FN - 1) * 64) < 65536, "weight offsets fit the ds_read offset field");
   static_assert(NS >= 2 && (NS - 2) * NI < 64, "ring depth");
-  static_assert(KG == 1 || (KG - 1) * NWG * 64 * FM * FN <= SZ, "tap-group partials fit one ring slot");
-  static_assert(KG == 1 || 1024 * NWG * (KG - 1) * FN * FM <= 65536, "partial offsets fit the ds offset field");
+  // tap-group partials of RI output fragments at a time fit one ring slot and the ds offset field
+  constexpr int RI_SLOT = KG > 1 ? SZ / ((KG - 1) * NWG * 64 * FM) : FN;
+  constexpr int RI_OFF = KG > 1 ? 64 / (NWG * (KG - 1) * FM) : FN;
+  constexpr int RI = RI_SLOT < RI_OFF ? (RI_SLOT < FN ? RI_SLOT : FN) : (RI_OFF < FN ? RI_OFF : FN);
+  static_assert(KG == 1 || RI >= 1, "one output fragment's partials fit a ring slot");
   __shared__ f16x8 ring[NS * SZ];
 
   const int Cin = x.C, N = y.C;
@@ -1612,35 +1615,41 @@ __global__ __launch_bounds__(64 * WP * WN * KG) void k_conv_tap(View x, View y, 
           cS = 0;
           if constexpr (KG > 1) {
             // the slot just consumed is free until the DMA after the next barrier refills it;
-            // partial (g, i, u) of wave wq, lane L at 16 * ((((g-1)*FN + i)*FM + u)*NWG*64 + wq*64 + L)
+            // the partials go through it RI output fragments at a time: partial (g, i, u) of
+            // wave wq, lane L at 16 * ((((g-1)*RI + i % RI)*FM + u)*NWG*64 + wq*64 + L)
             const unsigned red = base + 16u * (unsigned)(wq * 64 + lane);
-            asm volatile("s_barrier" ::: "memory");   // every wave is done reading the slot
-            static_for<KG - 1>([&](auto G1) {
-              if (kg == G1 + 1) {
-                static_for<FN>([&](auto I) {
-                  static_for<FM>([&](auto U) {
-                    ds_write16f<1024 * NWG * ((G1 * FN + I) * FM + U)>(red, acc[I][U]);
+            static_for<(FN + RI - 1) / RI>([&](auto R) {
+              constexpr int i0 = R * RI, i1 = i0 + RI < FN ? i0 + RI : FN;
+              asm volatile("s_barrier" ::: "memory");   // every wave is done reading the slot
+              static_for<KG - 1>([&](auto G1) {
+                if (kg == G1 + 1) {
+                  static_for<i1 - i0>([&](auto I) {
+                    static_for<FM>([&](auto U) {
+                      ds_write16f<1024 * NWG * ((G1 * RI + I) * FM + U)>(red, acc[i0 + I][U]);
+                    });
                   });
+                }
+              });
+              asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+              if (kg == 0) {
+                static_for<KG - 1>([&](auto G1) {
+                  f32x4 part[i1 - i0][FM];
+                  static_for<i1 - i0>([&](auto I) {
+                    static_for<FM>([&](auto U) {
+                      part[I][U] = ds_read16f<1024 * NWG * ((G1 * RI + I) * FM + U)>(red);
+                    });
+                  });
+                  lgkm_wait<0>();
+#pragma unroll
+                  for (int i = 0; i < i1 - i0; i++)
+#pragma unroll
+                    for (int u = 0; u < FM; u++) {
+                      asm volatile("" : "+v"(part[i][u]));
+                      acc[i0 + i][u] += part[i][u];
+                    }
                 });
               }
             });
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            if (kg == 0) {
-              static_for<KG - 1>([&](auto G1) {
-                f32x4 part[FN][FM];
-                static_for<FN>([&](auto I) {
-                  static_for<FM>([&](auto U) { part[I][U] = ds_read16f<1024 * NWG * ((G1 * FN + I) * FM + U)>(red); });
-                });
-                lgkm_wait<0>();
-#pragma unroll
-                for (int i = 0; i < FN; i++)
-#pragma unroll
-                  for (int u = 0; u < FM; u++) {
-                    asm volatile("" : "+v"(part[i][u]));
-                    acc[i][u] += part[i][u];
-                  }
-              });
-            }
           }
           if (kg == 0) epilogue(cItem);
 #pragma unroll
@@ -1661,10 +1670,10 @@ __global__ __launch_bounds__(64 * WP * WN * KG) void k_conv_tap(View x, View y, 
   X(0, 3, 8, 20, 64, 2, 2, 2, 2)     \
   X(1, 3, 8, 16, 96, 2, 2, 2, 2)     \
   X(2, 3, 4, 40, 64, 2, 2, 2, 2)     \
-  X(3, 3, 4, 16, 48, 2, 1, 2, 2)     \
-  X(4, 3, 2, 40, 64, 1, 2, 2, 2)     \
+  X(3, 3, 8, 40, 64, 2, 2, 2, 2)     \
+  X(4, 3, 4, 40, 96, 2, 2, 2, 2)     \
   X(5, 3, 4, 20, 64, 1, 2, 2, 2)     \
-  X(6, 3, 8, 16, 64, 2, 2, 2, 2)     \
+  X(6, 3, 8, 20, 96, 2, 2, 2, 2)     \
   X(7, 3, 4, 16, 64, 1, 2, 2, 2)     \
   X(8, 1, 1, 128, 384, 2, 4, 1, 3)   \
   X(9, 1, 1, 256, 192, 4, 2, 1, 3)   \
