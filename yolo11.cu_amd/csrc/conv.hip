@@ -1494,6 +1494,28 @@ __global__ __launch_bounds__(64 * WP * WN * KG) void k_conv_tap(View x, View y, 
     for (int e = 0; e < 4; e++) bpre[i][e] = n0 + e < N ? bias[n0 + e] : 0.f;
   }
 
+  // ---- residual of item k, loaded at the start of the tile's last stage so its latency hides
+  // behind that stage's MFMAs (the epilogue would otherwise wait a memory round trip per
+  // pixel fragment)
+  constexpr int NR = PAIR ? FN / 2 : FN;   // residual vectors per pixel fragment
+  using RV = typename std::conditional<PAIR, f16x8, f16x4>::type;
+  RV rpre[FM][NR];
+  auto resLoads = [&](int k) __attribute__((always_inline)) {
+    const Tile tl = tileOf(k);
+#pragma unroll
+    for (int q = 0; q < FM; q++) {
+      const int p = (wp * FM + q) * 16 + lr, py = p / TW, px = p - py * TW;
+      const int oy = tl.y0 + py, ox = tl.x0 + px;
+      const bool live = oy < H && ox < W;
+      const size_t m = live ? (size_t)(tl.img * H + oy) * W + ox : 0;
+#pragma unroll
+      for (int p2 = 0; p2 < NR; p2++) {
+        const int n0 = PAIR ? bn + wn * FN * 16 + 32 * p2 + 8 * lg : bn + wn * FN * 16 + p2 * 16 + 4 * lg;
+        rpre[q][p2] = live && n0 < N ? *(const RV*)(r.p + m * r.s + r.o + n0) : RV{};
+      }
+    }
+  };
+
   // ---- epilogue of item k: + bias, SiLU, + residual, fp16 store of this lane's pixels
   auto epilogue = [&](int k) __attribute__((always_inline)) {
     const Tile tl = tileOf(k);
@@ -1519,9 +1541,8 @@ __global__ __launch_bounds__(64 * WP * WN * KG) void k_conv_tap(View x, View y, 
             for (int e = 0; e < 8; e++) v[e] = silu(v[e]);
           }
           if (r.p) {
-            const f16x8 rv = *(const f16x8*)(r.p + m * r.s + r.o + n0);
 #pragma unroll
-            for (int e = 0; e < 8; e++) v[e] += (float)rv[e];
+            for (int e = 0; e < 8; e++) v[e] += (float)rpre[q][p2][e];
           }
           f16x8 o;
 #pragma unroll
@@ -1540,9 +1561,8 @@ __global__ __launch_bounds__(64 * WP * WN * KG) void k_conv_tap(View x, View y, 
             if (act == 1) v[e] = silu(v[e]);
           }
           if (r.p) {
-            const f16x4 rv = *(const f16x4*)(r.p + m * r.s + r.o + n0);
 #pragma unroll
-            for (int e = 0; e < 4; e++) v[e] += (float)rv[e];
+            for (int e = 0; e < 4; e++) v[e] += (float)rpre[q][i][e];
           }
           const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
           *(f16x4*)(y.p + m * y.s + y.o + n0) = o;
@@ -1578,6 +1598,7 @@ __global__ __launch_bounds__(64 * WP * WN * KG) void k_conv_tap(View x, View y, 
         for (int u = 0; u < FM; u++) ap[u] = base + pb[u];
         const unsigned aw = base + wb;
         if (q + NS - 1 < total) issueNext(ring + ((j + NS - 1) % NS) * SZ);
+        if (r.p && cS == nks - 1 && kg == 0) resLoads(cItem);
         __builtin_amdgcn_sched_barrier(0);
         // with room in the lgkm counter for two taps' reads, tap t+1's fragment reads are
         // issued before tap t's MFMAs
@@ -1674,7 +1695,7 @@ __global__ __launch_bounds__(64 * WP * WN * KG) void k_conv_tap(View x, View y, 
   X(4, 3, 4, 40, 96, 2, 2, 2, 2)     \
   X(5, 3, 4, 20, 64, 1, 2, 2, 2)     \
   X(6, 3, 8, 20, 96, 2, 2, 2, 2)     \
-  X(7, 3, 4, 16, 64, 1, 2, 2, 2)     \
+  X(7, 3, 8, 40, 48, 4, 1, 2, 2)     \
   X(8, 1, 1, 128, 384, 2, 4, 1, 3)   \
   X(9, 1, 1, 256, 192, 4, 2, 1, 3)   \
   X(10, 1, 1, 128, 192, 2, 2, 1, 4)  \

@@ -27,7 +27,7 @@ CFG_TAP = 1100    # op configs 1100 .. 1100 + NUM_TAP_TILES - 1: streaming-conv 
 NUM_TAP_TILES = 13
 TAP_3X3 = range(0, 8)    # variants for 3x3 stride-1 convs (halo-staged)
 TAP_1X1 = range(8, 13)   # variants for 1x1 stride-1 convs
-TAP_BN = (64, 96, 64, 64, 96, 64, 96, 64, 384, 192, 192, 128, 256)   # output channels per block
+TAP_BN = (64, 96, 64, 64, 96, 64, 96, 48, 384, 192, 192, 128, 256)   # output channels per block
 OP_KINDS = ["CONV", "ADD", "MAXPOOL5", "UPSAMPLE2", "COPYC", "ATTN", "DECODE", "GAP", "SOFTMAX",
             "DECODEOBB", "PS2", "DECODESEG", "MASKS"]
 MAX_OUT = 300
