@@ -64,6 +64,17 @@ def measured_traffic(cfg):
         return None
 
 
+def conv_kernel_name(cfg):
+    """The kernel an op config selects (yolo_set_op_config's numbering)."""
+    if cfg == 1000:
+        return "k_conv3x3_halo"
+    if cfg == 1001:
+        return "k_conv1x1_resident"
+    if cfg >= 1100:
+        return f"k_conv_tap variant {cfg - 1100}"
+    return f"k_conv_gemm cfg {cfg}"
+
+
 def conv_flops(eng, k):
     info = eng.op_info(k)
     H, W, _ = eng.tensor_shape(info["out"])
@@ -619,7 +630,7 @@ def main():
         line["roofline"] = {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": 2500.0,
                             "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16, 4),
                             "traffic": measured_traffic(conv["cfg"]),
-                            "kernel": f"k_conv_gemm cfg {conv['cfg']}", "shape": conv["shape"],
+                            "kernel": conv_kernel_name(conv["cfg"]), "shape": conv["shape"],
                             "ms": round(conv["ms"], 4)}
     if cpu:
         line["cpu_baseline"] = cpu
