@@ -81,6 +81,18 @@ def conv_flops(eng, k):
     return 2.0 * H * W * info["Cout"] * info["k"] * info["k"] * info["Cin"] / max(info["g"], 1)
 
 
+def attn_flops(eng, k):
+    """QK^T and PV of one image: 2 * heads * N^2 * (kd + hd), kd = 32 (the loader's rule);
+    heads and hd follow from the qkv width heads * (2 kd + hd) and the output width heads * hd."""
+    info = eng.op_info(k)
+    H, W, cout = eng.tensor_shape(info["out"])
+    cin = eng.tensor_shape(info["a"])[2]
+    heads = (cin - cout) // 64
+    hd = cout // heads
+    n = H * W
+    return 2.0 * heads * n * n * (32 + hd)
+
+
 def bench_n(workdir, steps, warmup, graph=True):
     """yolo11n b1.  The headline step is the reference's `pipeline` loop
     (engine/engine.cu:1992-2031): one whole-frame graph holding the H2D of the raw 810x1080
@@ -308,7 +320,7 @@ def bench_x(workdir, iters, graph=True):
     # kernel time per launch unit (grouped launches as the graph runs them), each unit run
     # 5 times back to back so the per-launch gaps of a stream-ordered pass are excluded
     per_unit = eng.profile_units(B, 2, 5)
-    conv_f, conv_t, conv_t_ev, attn_t = 0.0, 0.0, 0.0, 0.0
+    conv_f, conv_t, conv_t_ev, attn_t, attn_f = 0.0, 0.0, 0.0, 0.0, 0.0
     for k in range(eng.num_ops):
         info = eng.op_info(k)
         if info["kind"] == "CONV":
@@ -317,13 +329,15 @@ def bench_x(workdir, iters, graph=True):
             conv_t_ev += per_op[k] * 1e-3
         elif info["kind"] == "ATTN":
             attn_t += per_unit[k] * 1e-3
+            attn_f += B * attn_flops(eng, k)
     for b in devs:
         b.free()
     eng.close()
     return dict(ms_per_batch=ms, img_per_s=B * 1e3 / ms, conv_tflops=conv_f / conv_t / 1e12,
                 conv_mfma_util=conv_f / conv_t / PEAK_FP16, conv_ms=conv_t * 1e3,
                 conv_mfma_util_stream_events=conv_f / conv_t_ev / PEAK_FP16, conv_ms_stream_events=conv_t_ev * 1e3,
-                attn_ms=attn_t * 1e3, stream_ops_ms=float(per_op.sum()), kept_min=min(kept),
+                attn_ms=attn_t * 1e3, attn_tflops=attn_f / attn_t / 1e12, attn_mfma_util=attn_f / attn_t / PEAK_FP16,
+                stream_ops_ms=float(per_op.sum()), kept_min=min(kept),
                 kept_max=max(kept))
 
 

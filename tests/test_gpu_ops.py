@@ -354,6 +354,31 @@ def test_dwconv(tmp_path, H, W, C, s, B, res):
     eng.close()
 
 
+@pytest.mark.parametrize("H,W,C,s,B,res", [(41, 43, 256, 1, 16, True), (80, 80, 384, 1, 16, False),
+                                            (81, 79, 128, 2, 32, False)])
+def test_dwconv_kernels_bit_identical(tmp_path, H, W, C, s, B, res):
+    """The depthwise kernels a launch size selects (four pixels per thread for large launches,
+    one pixel per thread for small ones) give the same bits: images of a large batch against
+    batch-1 runs of each image, so a frame's result does not depend on its batch."""
+    d = str(tmp_path / "dwb")
+    modelgen.write_single_conv(d, H, W, C, C, 3, s, seed=C + 7 * s, dw=True, residual=res)
+    g = graphfile.load(d)
+    x = np.random.default_rng(C + s).standard_normal((B, H, W, C), dtype=np.float32).astype(np.float16)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    out = [graphfile.Op(**vars(o)) for o in graphfile.fuse_adds(g.ops)][0].out
+    eng.write(0, x)
+    eng.run_op(0, B)
+    big = eng.read(out, B)
+    for i in (0, B // 2, B - 1):
+        eng.write(0, x[i:i + 1])
+        eng.run_op(0, 1)
+        one = eng.read(out, 1)[0]
+        diff = int(np.count_nonzero(one.view(np.uint16) != big[i].view(np.uint16)))
+        print(f"dw {H}x{W}x{C} s{s}: image {i} of {B} vs alone: {diff} differing values", flush=True)
+        assert diff == 0
+    eng.close()
+
+
 @pytest.mark.parametrize("H,W,Cin,Cout,B,res", [(160, 160, 48, 48, 2, False), (37, 45, 32, 32, 3, True),
                                                 (20, 21, 64, 64, 2, True), (8, 8, 8, 16, 1, False),
                                                 (33, 17, 24, 48, 2, False), (40, 40, 64, 16, 2, False)])
