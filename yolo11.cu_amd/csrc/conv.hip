@@ -58,6 +58,16 @@ constexpr unsigned OOB_OFF = 0x80000000u;  // past every descriptor's num_record
 template <int N>
 using ic = std::integral_constant<int, N>;
 
+// Dispatch is round-robin over the XCDs (block b of a launch runs on XCD (b + c) % 8 for a
+// launch constant c), and each XCD has its own L2.  Numbering the blocks of each XCD class with
+// a contiguous range of tile ids keeps neighbouring tiles -- the N tiles of one M tile, adjacent
+// M tiles sharing input rows -- on one L2: the j-th block of class x takes id
+// x*q + min(x, r) + j, q = n / 8, r = n % 8, which is a bijection on [0, n) for any n.
+__device__ __forceinline__ int xcdRange(int b, int n) {
+  const int x = b % NUM_XCD, j = b / NUM_XCD, q = n / NUM_XCD, r = n % NUM_XCD;
+  return x * q + min(x, r) + j;
+}
+
 // Slot permutation of the chunks of LDS row `row` (CPR chunks of 16 bytes per row).  It reads
 // only bits 0..3 of the row: fragment reads start at multiples of 16 rows, and a thread's DMA
 // rows differ by multiples of 16, so both sides can evaluate it on (row & 15).
@@ -174,7 +184,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(const GemmLaunch L) 
   int split = 0, tsl = 0, id;
   if (!tail) {
     id = bid;
-    if (dp >= 2 * NUM_XCD && dp % NUM_XCD == 0) id = (id % NUM_XCD) * (dp / NUM_XCD) + id / NUM_XCD;
+    if (dp >= 2 * NUM_XCD) id = xcdRange(id, dp);
   } else {
     const int q = bid - dp;
     split = q / rem;
