@@ -15,9 +15,10 @@ conv MFMA util %"):
     them) from hipEvents around 5 back-to-back launches; the same ratio with stream-ordered
     per-op events (launch gaps included) is reported beside it.
   * roofline: the implicit-GEMM conv kernel on the isolated-conv-sweep shape
-    3x3 s1 256->256 @80x80, batch 32, timed with hipEvents on the
-    engine stream; `traffic` = HBM bytes per launch of the tile the autotuner picked, from
-    the committed per-tile PMC passes (profiles/conv_gemm_c1_traffic.json).
+    3x3 s1 256->256 @80x80, batch 32, as the autotuner configures it
+    (tile, and the tail retile's second dispatch where it picked one), timed with hipEvents
+    on the engine stream around 5 back-to-back launches; `traffic` = HBM bytes per launch of
+    that configuration, from the committed PMC passes (profiles/conv_gemm_c1_traffic.json).
   * prepost_roofline: letterbox, decode and mask assembly against the HBM roofline, NMS time.
   * yolo11n-obb at 1024 (15 classes, 1024x1024 frame) and yolo11n-seg at 640, batch 1:
     whole-frame graph, frame in HBM (side figures; the reference quotes 1.6 ms and 1.21 ms
@@ -52,26 +53,31 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def measured_traffic(cfg):
+def measured_traffic(cfg, tail=-1):
     """HBM bytes per launch of the roofline kernel from the committed rocprofv3 PMC passes
-    (FETCH_SIZE and WRITE_SIZE per tile config, each scaled by a plain copy of known size)
-    for the tile this run's autotuner picked; None if that tile has no measurement."""
+    (FETCH_SIZE and WRITE_SIZE per tile config, or per tile + tail-retile pair summed over
+    its two dispatches, each scaled by a plain copy of known size) for the configuration this
+    run's autotuner picked; None if it has no measurement."""
     path = os.path.join(ROOT, "profiles", "conv_gemm_c1_traffic.json")
     try:
         rec = json.load(open(path))
+        if tail >= 0:
+            return int(rec["per_retile"][f"{cfg}+{tail}"]["traffic_bytes"])
         return int(rec["per_cfg"][str(cfg)]["traffic_bytes"])
     except (OSError, ValueError, KeyError):
         return None
 
 
-def conv_kernel_name(cfg):
-    """The kernel an op config selects (yolo_set_op_config's numbering)."""
+def conv_kernel_name(cfg, tail=-1):
+    """The kernel an op config selects (yolo_set_op_config's numbering), with its tail retile."""
     if cfg == 1000:
         return "k_conv3x3_halo"
     if cfg == 1001:
         return "k_conv1x1_resident"
     if cfg >= 1100:
         return f"k_conv_tap variant {cfg - 1100}"
+    if tail >= 0:
+        return f"k_conv_gemm cfg {cfg}, last-wave rows under cfg {tail} (two dispatches)"
     return f"k_conv_gemm cfg {cfg}"
 
 
@@ -282,7 +288,7 @@ def bench_sweep(workdir, iters):
             fl = 2.0 * B * Ho * Wo * cout * k * k * cin
             out[f"{k}x{k}s{s} {cin}->{cout} @{H}x{W} b{B}"] = {
                 "us": round(ms * 1e3, 2), "tflops": round(fl / ms / 1e9, 1),
-                "tile": eng.op_config(0), "split": eng.op_split(0)}
+                "tile": eng.op_config(0), "split": eng.op_split(0), "tail": eng.op_tail(0)}
             eng.close()
     return out
 
@@ -351,20 +357,23 @@ def bench_conv(workdir, iters):
     eng = yolort.Engine(d, B, yolort.YOLO_NOGRAPH)
     x = np.random.default_rng(11).standard_normal((B, H, W, cin), dtype=np.float32).astype(np.float16)
     eng.write(0, x)
-    ms = float(eng.profile_ops(B, iters)[0])
+    # kernel time per launch (both dispatches of a tail retile): 5 back-to-back launches timed
+    # with HIP events on the engine stream, averaged over `iters` rounds
+    ms = float(eng.profile_units(B, iters, 5)[0])
     flops = 2.0 * B * H * W * cout * k * k * cin
     # algorithmic HBM bytes: input + weights + output (fp16) + bias (fp32)
     nbytes = 2.0 * (B * H * W * cin + cout * k * k * cin + B * H * W * cout) + 4 * cout
     cfg = eng.op_config(0)
+    tail = eng.op_tail(0)
     eng.close()
     # a plain copy of known size on the same shape (scale reference for HBM counters)
     dc = os.path.join(workdir, "copy_c1")
     modelgen.write_copy(dc, H, W, cin)
     ec = yolort.Engine(dc, B, yolort.YOLO_NOGRAPH)
-    copy_ms = float(ec.profile_ops(B, iters)[0])
+    copy_ms = float(ec.profile_units(B, iters, 5)[0])
     ec.close()
     copy_bytes = 2.0 * 2 * B * H * W * cin
-    return dict(ms=ms, flops=flops, bytes=nbytes, tflops=flops / ms / 1e9, cfg=cfg,
+    return dict(ms=ms, flops=flops, bytes=nbytes, tflops=flops / ms / 1e9, cfg=cfg, tail=tail,
                 shape=f"3x3 s1 {cin}->{cout} @{H}x{W} b{B}", copy_ms=copy_ms,
                 copy_gbs=copy_bytes / copy_ms / 1e6)
 
@@ -643,8 +652,8 @@ def main():
         achieved = conv["flops"] / (conv["ms"] * 1e-3)
         line["roofline"] = {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": 2500.0,
                             "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16, 4),
-                            "traffic": measured_traffic(conv["cfg"]),
-                            "kernel": conv_kernel_name(conv["cfg"]), "shape": conv["shape"],
+                            "traffic": measured_traffic(conv["cfg"], conv["tail"]),
+                            "kernel": conv_kernel_name(conv["cfg"], conv["tail"]), "shape": conv["shape"],
                             "ms": round(conv["ms"], 4)}
     if cpu:
         line["cpu_baseline"] = cpu

@@ -209,6 +209,15 @@ int yolo_set_op_config(void* h, int k, int cfg);   /* also resets the op's split
  * (YOLO_NOGRAPH handles only), for non-GEMM ops and for splits that leave a block empty. */
 int yolo_op_split(void* h, int k);
 int yolo_set_op_split(void* h, int k, int splits);
+/* Tail retile of GEMM conv k (no counterpart in engine/yolo.h; a tuning and parity hook like
+ * the split override): the output tiles of the op's tile config that fill whole waves of the
+ * chip run under that config, and the pixel rows after them under the smaller tile config
+ * `tail` (same K per stage) in a second launch, so the part-empty last wave is spread over
+ * the chip.  Results are bit-identical to the op's config alone.  -1 clears it; refused (-1)
+ * for non-GEMM ops, split ops, and tails that do not apply.  yolo_op_tail returns the tail
+ * config, -1 for none, -2 for a bad op.  The autotuner sets it where it is faster. */
+int yolo_op_tail(void* h, int k);
+int yolo_set_op_tail(void* h, int k, int tail);
 /* Number of GEMM tile configurations compiled in, and the shape of one:
  * out[0..5] = BM (pixels), BN (channels), waves along M, waves along N, BK (K per stage),
  * LDS ring stages. */

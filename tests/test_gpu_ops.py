@@ -129,6 +129,68 @@ def test_conv_sweep(tmp_path, shape, B):
     eng.close()
 
 
+@pytest.mark.parametrize("shape,B,cfg", [((80, 80, 256, 256, 3, 1), 32, 31), ((80, 80, 96, 192, 3, 1), 32, 31),
+                                         ((80, 80, 512, 256, 1, 1), 32, 2), ((80, 80, 768, 768, 3, 2), 16, 5)])
+def test_conv_tail_retile(tmp_path, shape, B, cfg):
+    """Tail retile (the rows past the last whole chip wave under a smaller tile of the same
+    BK, in a second launch): for every tail config that applies, the output is bit-identical
+    to the plain tile config, which is itself within the oracle tolerance.  Covers the
+    channel-block walk (3x3 stride 1 and 2), the per-lane walk (Cin 96 with BK 64) and 1x1."""
+    H, W, cin, cout, k, s = shape
+    d = str(tmp_path / "tail")
+    modelgen.write_single_conv(d, H, W, cin, cout, k, s, seed=5)
+    g = graphfile.load(d)
+    x = np.random.default_rng(9).standard_normal((B, H, W, cin), dtype=np.float32).astype(np.float16)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    eng.write(0, x)
+    eng.set_op_config(0, cfg)
+    assert eng.op_tail(0) == -1
+    eng.run_op(0, B)
+    plain = eng.read(g.ops[0].out, B)
+    pick = [0, B - 1]
+    ref = interp.Interp(g, len(pick))
+    ref.set_input(x[pick].astype(np.float32))
+    ref.run_op(g.ops[0])
+    rel = post.rel_err(plain[pick].astype(np.float32), ref.view(g.ops[0].out))
+    assert rel <= TOL, rel
+    tried = []
+    for tail in range(len(yolort.tile_configs())):
+        try:
+            eng.set_op_tail(0, tail)
+        except ValueError:
+            continue
+        assert eng.op_tail(0) == tail
+        eng.write(g.ops[0].out, np.zeros_like(plain))
+        eng.run_op(0, B)
+        got = eng.read(g.ops[0].out, B)
+        diff = int(np.count_nonzero(got.view(np.uint16) != plain.view(np.uint16)))
+        print(f"shape {shape} B={B} cfg {cfg} tail {tail}: {diff} differing values", flush=True)
+        assert diff == 0, (tail, diff)
+        tried.append(tail)
+    assert tried, "no tail config applies"
+    eng.set_op_tail(0, -1)
+    assert eng.op_tail(0) == -1
+    eng.close()
+
+
+def test_conv_tail_rejects(tmp_path):
+    """The tail override is refused for tiles with another BK or no smaller area, for special
+    kernels, split ops and non-GEMM ops."""
+    d = str(tmp_path / "tr")
+    modelgen.write_single_conv(d, 80, 80, 256, 256, 3, 1, seed=5)
+    eng = yolort.Engine(d, 32, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    eng.set_op_config(0, 31)                      # 256x256, BK 64
+    for tail in (2, 5, 13, 31, 20, -5 + 100):     # BK 32, BK 32, BK 128, itself, same area, out of range
+        with pytest.raises(ValueError):
+            eng.set_op_tail(0, tail)
+    eng.set_op_tail(0, 6)                         # 128x128, BK 64
+    eng.set_op_split(0, 2)                        # a split clears the tail
+    assert eng.op_tail(0) == -1
+    with pytest.raises(ValueError):
+        eng.set_op_tail(0, 6)
+    eng.close()
+
+
 @pytest.mark.parametrize("res", [False, True])
 @pytest.mark.parametrize("shape", [(20, 20, 8, 16, 3, 1), (13, 17, 24, 40, 3, 2), (7, 9, 16, 8, 1, 1),
                                    (33, 31, 64, 24, 3, 1), (16, 16, 32, 32, 3, 1)])

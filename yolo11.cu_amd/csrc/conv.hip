@@ -193,7 +193,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(const GemmLaunch L) 
     id = dp + tsl;
   }
   const int mt = id / ntiles, nt = id - mt * ntiles;
-  const int bm = mt * BM, bn = nt * BN;
+  const int bm = P.m0 + mt * BM, bn = nt * BN;
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -787,27 +787,63 @@ static GemmProblem gemmProblem(int cfg, const ConvJob& j, int Bn, int blk0) {
   P.ntiles = (P.N + tc.BN - 1) / tc.BN;
   P.xbytes = (int)((long)Bn * j.x.H * j.x.W * j.x.s * 2);
   P.blk0 = blk0;
+  P.m0 = 0;
   return P;
+}
+
+int tailRow(int cfg, int km, int M, int N) {
+  if (cfg < 0 || cfg >= kNumTiles) return M;
+  const TileCfg& tc = kTiles[cfg];
+  const int ntiles = (N + tc.BN - 1) / tc.BN, mtiles = (M + tc.BM - 1) / tc.BM;
+  const int P = tileSlots(cfg, km);
+  if (P <= 0) return M;
+  const int mainMt = mtiles * ntiles / P * P / ntiles;   // whole M tiles inside whole waves
+  return mainMt >= 1 && mainMt < mtiles ? mainMt * tc.BM : M;
+}
+
+bool tailOk(int cfg, int tail, int k, int s, int p, int Cin, int M, int N) {
+  if (cfg < 0 || cfg >= kNumTiles || tail < 0 || tail >= kNumTiles || tail == cfg) return false;
+  const TileCfg &a = kTiles[cfg], &b = kTiles[tail];
+  if (a.BK != b.BK || b.BM * b.BN >= a.BM * a.BN) return false;
+  const int km = convKMode(cfg, k, s, p, Cin);
+  const int m1 = tailRow(cfg, km, M, N);
+  return m1 < M && tileOk(tail, M - m1, N, k * k * Cin);
 }
 
 void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
                     const float* bias, int k, int s, int p, int act, int Bn, int splits,
-                    float* ws, int* cnt, hipStream_t st) {
+                    float* ws, int* cnt, hipStream_t st, int tail) {
   const int M = Bn * y.H * y.W, N = y.C, Ktot = k * k * x.C;
   if (cfg < 0 || cfg >= kNumTiles) cfg = heuristicTile(M, N, Ktot);
   const int km = convKMode(cfg, k, s, p, x.C);
   if (!ws || !cnt || !splitOk(cfg, Ktot, splits)) splits = 1;
-  int dp, S;
-  splitPlan(cfg, km, numTiles(cfg, M, N), splits, &dp, &S);
+  // tail retile: rows [m1, M) go to the second launch (decided for this launch's M)
+  const int m1 = splits == 1 && tailOk(cfg, tail, k, s, p, x.C, M, N) ? tailRow(cfg, km, M, N) : M;
+  const ConvJob job{x, y, res, w, bias, k, s, p, act};
   GemmLaunch L{};
-  L.p[0] = gemmProblem(cfg, ConvJob{x, y, res, w, bias, k, s, p, act}, Bn, 0);
+  L.p[0] = gemmProblem(cfg, job, Bn, 0);
+  if (m1 < M) L.p[0].mtiles = m1 / kTiles[cfg].BM;
+  const int tiles = L.p[0].mtiles * L.p[0].ntiles;
+  int dp, S;
+  splitPlan(cfg, km, tiles, splits, &dp, &S);
   L.n = 1;
   L.dp = dp;
   L.splits = S;
   L.spl = splitStages(Ktot, kTiles[cfg].BK, S);
   L.ws = ws;
   L.cnt = cnt;
-  launchCfg(cfg, km, L, dp + (L.p[0].mtiles * L.p[0].ntiles - dp) * S, st);
+  launchCfg(cfg, km, L, dp + (tiles - dp) * S, st);
+  if (m1 < M) {
+    GemmLaunch T{};
+    T.p[0] = gemmProblem(tail, job, Bn, 0);
+    T.p[0].m0 = m1;
+    T.p[0].mtiles = (M - m1 + kTiles[tail].BM - 1) / kTiles[tail].BM;
+    T.n = 1;
+    T.dp = T.p[0].mtiles * T.p[0].ntiles;
+    T.splits = 1;
+    T.spl = splitStages(Ktot, kTiles[tail].BK, 1);
+    launchCfg(tail, km, T, T.dp, st);
+  }
 }
 
 bool convGroupOk(int cfg, const ConvJob* jobs, int n) {

@@ -20,6 +20,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <deque>
+#include <tuple>
 #include <condition_variable>
 #include <map>
 #include <memory>
@@ -520,7 +521,7 @@ struct Engine {
         else if (op.g == 1)
           launchConvGemm(op.cfg, x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, op.split,
                          op.wsOff >= 0 ? splitWs + op.wsOff : nullptr,
-                         op.cntOff >= 0 ? splitCnt + op.cntOff : nullptr, s);
+                         op.cntOff >= 0 ? splitCnt + op.cntOff : nullptr, s, op.tail);
         else
           launchDwConv(x, y, rp, w, b, op.k, op.s, op.p, op.act, Bn, s);
         break;
@@ -567,7 +568,7 @@ struct Engine {
     if (op.kind == COPYC) return GK_COPY;
     if (op.kind != CONV) return GK_NONE;
     if (op.g > 1) return GK_DW;
-    if (op.Cin == 3 || specialConvCfg(op.cfg)) return GK_NONE;
+    if (op.Cin == 3 || specialConvCfg(op.cfg) || op.tail >= 0) return GK_NONE;
     return GK_GEMM;
   }
   ConvJob convJob(int k) {
@@ -596,7 +597,8 @@ struct Engine {
     if (!s) s = st;
     bool together = u.ops.size() > 1;
     if (together && u.kind == GK_GEMM)   // (per-op overrides since planning launch one by one)
-      for (int i : u.ops) together = together && ops[i].cfg == ops[u.ops[0]].cfg && ops[i].split == 1;
+      for (int i : u.ops)
+        together = together && ops[i].cfg == ops[u.ops[0]].cfg && ops[i].split == 1 && ops[i].tail < 0;
     if (!together) {
       for (int i : u.ops)
         if (ops[i].chain >= 0) runOp(i, Bn, s);
@@ -834,12 +836,14 @@ struct Engine {
   // while the tile grid is less than one chip wave.  Tail splits are not candidates: which
   // tiles they split depends on the batch, so an image's sums would depend on the batch it
   // runs in (every choice made here keeps a batch-1 run of a frame bit-identical to its
-  // slot in a larger batch); yolo_set_op_split still selects them.
+  // slot in a larger batch); yolo_set_op_split still selects them.  Tail retiles (a smaller
+  // tile of the same BK for the rows past the last whole chip wave) are tried on the three
+  // fastest plain tiles; they do not change any result bit.
   void autotune() {
     hipEvent_t e0, e1;
     HCK(hipEventCreate(&e0));
     HCK(hipEventCreate(&e1));
-    std::map<std::tuple<int, int, int, int, int, int, int, int>, std::pair<int, int>> cache;
+    std::map<std::tuple<int, int, int, int, int, int, int, int>, std::tuple<int, int, int>> cache;
     static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
     // YOLO_TUNE_TILES="a,b,..." restricts the candidate tile configs (for A/B studies); the
     // special kernels (halo 1000, resident 1x1 1001, halo-staged 3x3 variants 1100+) take part
@@ -867,9 +871,26 @@ struct Engine {
       const int M = B * y.H * y.W, N = op.Cout, K = op.k * op.k * op.Cin;
       auto key = std::make_tuple(y.H, y.W, op.Cin, op.Cout, op.k, op.s, op.b >= 0 ? 1 : 0, op.act);
       auto it = cache.find(key);
-      if (it != cache.end()) { op.cfg = it->second.first; op.split = it->second.second; continue; }
-      int best = heuristicTile(M, N, K), bestSplit = 1;
+      if (it != cache.end()) {
+        std::tie(op.cfg, op.split, op.tail) = it->second;
+        continue;
+      }
+      int best = heuristicTile(M, N, K), bestSplit = 1, bestTail = -1;
       float bestMs = 1e30f;
+      auto timeOp = [&] {   // median of 7 timed launches after 2 warm-up ones
+        for (int r = 0; r < 2; r++) runOp((int)k, B);
+        float t[7];
+        for (int r = 0; r < 7; r++) {
+          HCK(hipEventRecord(e0, st));
+          runOp((int)k, B);
+          HCK(hipEventRecord(e1, st));
+          HCK(hipEventSynchronize(e1));
+          HCK(hipEventElapsedTime(&t[r], e0, e1));
+        }
+        std::sort(t, t + 7);
+        return t[3];   // median: robust to clock ramps and one-off stalls
+      };
+      std::vector<std::pair<float, int>> plain;   // (ms, cfg) of the unsplit tiles
       for (int cfg = 0; cfg < numTileConfigs(); cfg++) {
         if (!allowed[cfg] || !tileOk(cfg, M, N, K)) continue;
         const int km = convKMode(cfg, op.k, op.s, op.p, op.Cin);
@@ -883,22 +904,28 @@ struct Engine {
           if (S != 1 && !splitOk(cfg, K, S)) continue;
           op.cfg = cfg;
           op.split = S;
+          op.tail = -1;
           op.wsOff = op.cntOff = S != 1 ? 0 : -1;
           if (S != 1) ensureSplitScratch(splitWorkspaceBytes(cfg, km, M, N, S), (size_t)splitTiles(cfg, km, M, N, S));
-          for (int r = 0; r < 2; r++) runOp((int)k, B);
-          float t[7];
-          for (int r = 0; r < 7; r++) {
-            HCK(hipEventRecord(e0, st));
-            runOp((int)k, B);
-            HCK(hipEventRecord(e1, st));
-            HCK(hipEventSynchronize(e1));
-            HCK(hipEventElapsedTime(&t[r], e0, e1));
-          }
-          std::sort(t, t + 7);
-          const float ms = t[3];   // median: robust to clock ramps and one-off stalls
-          if (ms < bestMs) { bestMs = ms; best = cfg; bestSplit = S; }
+          const float ms = timeOp();
+          if (S == 1) plain.emplace_back(ms, cfg);
+          if (ms < bestMs) { bestMs = ms; best = cfg; bestSplit = S; bestTail = -1; }
         }
       }
+      std::sort(plain.begin(), plain.end());
+      for (size_t i = 0; i < plain.size() && i < 3; i++) {
+        const int cfg = plain[i].second;
+        for (int tail = 0; tail < numTileConfigs(); tail++) {
+          if (!allowed[tail] || !tailOk(cfg, tail, op.k, op.s, op.p, op.Cin, M, N)) continue;
+          op.cfg = cfg;
+          op.split = 1;
+          op.tail = tail;
+          op.wsOff = op.cntOff = -1;
+          const float ms = timeOp();
+          if (ms < bestMs) { bestMs = ms; best = cfg; bestSplit = 1; bestTail = tail; }
+        }
+      }
+      op.tail = -1;
       // the special kernels, where they apply
       View hr{};
       if (op.b >= 0) hr = view(op.b);
@@ -908,22 +935,14 @@ struct Engine {
         op.cfg = special;
         op.split = 1;
         op.wsOff = op.cntOff = -1;
-        for (int r = 0; r < 2; r++) runOp((int)k, B);
-        float t[7];
-        for (int r = 0; r < 7; r++) {
-          HCK(hipEventRecord(e0, st));
-          runOp((int)k, B);
-          HCK(hipEventRecord(e1, st));
-          HCK(hipEventSynchronize(e1));
-          HCK(hipEventElapsedTime(&t[r], e0, e1));
-        }
-        std::sort(t, t + 7);
-        if (t[3] < bestMs) { bestMs = t[3]; best = special; bestSplit = 1; }
+        const float ms = timeOp();
+        if (ms < bestMs) { bestMs = ms; best = special; bestSplit = 1; bestTail = -1; }
       }
       op.cfg = best;
       op.split = bestSplit;
+      op.tail = bestTail;
       op.wsOff = op.cntOff = -1;
-      cache[key] = {best, bestSplit};
+      cache[key] = std::make_tuple(best, bestSplit, bestTail);
     }
     HCK(hipGetLastError());
     (void)hipEventDestroy(e0);
@@ -1901,7 +1920,34 @@ int yolo_set_op_config(void* h, int k, int cfg) {
   }
   op.cfg = cfg < 0 ? -1 : cfg;
   op.split = 1;                 // a different tile needs a different split workspace
+  op.tail = -1;
   op.wsOff = op.cntOff = -1;
+  return 0;
+}
+
+int yolo_op_tail(void* h, int k) {
+  Engine* e = E(h);
+  if (k < 0 || k >= (int)e->ops.size()) return -2;
+  const yolo::OpDesc& op = e->ops[k];
+  if (op.kind != yolo::CONV || op.g != 1 || op.Cin == 3) return -2;
+  return op.tail;
+}
+
+int yolo_set_op_tail(void* h, int k, int tail) {
+  Engine* e = E(h);
+  if (k < 0 || k >= (int)e->ops.size()) return -1;
+  yolo::OpDesc& op = e->ops[k];
+  if (op.kind != yolo::CONV || op.g != 1 || op.Cin == 3 || yolo::specialConvCfg(op.cfg) || op.split != 1) return -1;
+  if (tail < 0) {
+    op.tail = -1;
+    return 0;
+  }
+  const yolo::View y = e->view(op.out);
+  const int M = e->B * y.H * y.W, K = op.k * op.k * op.Cin;
+  const int cfg = op.cfg >= 0 ? op.cfg : yolo::heuristicTile(M, op.Cout, K);
+  if (!yolo::tailOk(cfg, tail, op.k, op.s, op.p, op.Cin, M, op.Cout)) return -1;
+  op.cfg = cfg;
+  op.tail = tail;
   return 0;
 }
 
@@ -1930,6 +1976,7 @@ int yolo_set_op_split(void* h, int k, int splits) {
       return -1;
     op.cfg = cfg;
     op.split = splits;
+    if (splits != 1) op.tail = -1;
     e->assignSplits();
     return 0;
   });

@@ -28,6 +28,7 @@ struct OpDesc {
   int stride = 0;                     // DECODE*
   int cfg = -1;                       // GEMM tile config (-1 = heuristic)
   int split = 1;                      // GEMM split-K factor (< -1: tail split, see conv.hip)
+  int tail = -1;                      // GEMM tail retile config (-1 none; launchConvGemm)
   long wsOff = -1, cntOff = -1;       // split-K workspace / counter offsets (engine-owned)
   int chain = 0;                      // MAXPOOL5: 3 = head of a fused SPPF chain,
                                       // -1 = pooled by the chain head in forward()
@@ -148,6 +149,7 @@ struct GemmProblem {
   const f16* w;
   const float* bias;
   int ksz, cs, cp, act, M, N, Ktot, mtiles, ntiles, xbytes, blk0;
+  int m0;   // first output pixel of tile row 0 (0, or where a tail retile starts)
 };
 struct GemmLaunch {
   GemmProblem p[GEMM_GROUP];
@@ -174,9 +176,16 @@ int numTiles(int cfg, int M, int N);
 int tileSlots(int cfg, int km);
 int splitTiles(int cfg, int km, int M, int N, int splits);
 size_t splitWorkspaceBytes(int cfg, int km, int M, int N, int splits);
+// Tail retile: the output tiles of `cfg` that fill whole chip waves (CUs x resident blocks)
+// run under `cfg`, and the pixel rows after them under the smaller tile config `tail` in a
+// second launch, which spreads that remainder over the chip instead of leaving most CUs idle
+// during a part-empty last wave.  `tail` has the same BK, hence the same K walk and the same
+// MFMA sequence for every output: the result is bit-identical to `cfg` alone.
+bool tailOk(int cfg, int tail, int k, int s, int p, int Cin, int M, int N);
+int tailRow(int cfg, int km, int M, int N);   // first pixel of the tail part (M: none)
 void launchConvGemm(int cfg, const View& x, const View& y, const View* res, const f16* w,
                     const float* bias, int k, int s, int p, int act, int Bn, int splits,
-                    float* ws, int* cnt, hipStream_t st);
+                    float* ws, int* cnt, hipStream_t st, int tail = -1);
 // n independent convs in one launch under tile config `cfg` (all in the same K mode, which
 // convGroupOk checks), no split-K; each result equals a launch of that conv alone.
 bool convGroupOk(int cfg, const ConvJob* jobs, int n);

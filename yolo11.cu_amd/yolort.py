@@ -100,6 +100,8 @@ _SIGS = {
     "yolo_set_op_config": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
     "yolo_op_split": (C.c_int, [C.c_void_p, C.c_int]),
     "yolo_set_op_split": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    "yolo_op_tail": (C.c_int, [C.c_void_p, C.c_int]),
+    "yolo_set_op_tail": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
     "yolo_num_tile_configs": (C.c_int, []),
     "yolo_tile_config": (C.c_int, [C.c_int, C.POINTER(C.c_int)]),
     "yolo_frame_graph": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
@@ -324,6 +326,13 @@ class Engine:
     def set_op_split(self, k: int, splits: int):
         if self.lib.yolo_set_op_split(self.h, k, splits) != 0:
             raise ValueError((k, splits))
+
+    def op_tail(self, k: int) -> int:
+        return self.lib.yolo_op_tail(self.h, k)
+
+    def set_op_tail(self, k: int, tail: int):
+        if self.lib.yolo_set_op_tail(self.h, k, tail) != 0:
+            raise ValueError((k, tail))
 
     # -- frame API
     def set_thresholds(self, conf=0.25, iou=0.45, max_det=300):
