@@ -215,7 +215,8 @@ int yolo_set_op_split(void* h, int k, int splits);
  * `tail` (same K per stage) in a second launch, so the part-empty last wave is spread over
  * the chip.  Results are bit-identical to the op's config alone.  -1 clears it; refused (-1)
  * for non-GEMM ops, split ops, and tails that do not apply.  yolo_op_tail returns the tail
- * config, -1 for none, -2 for a bad op.  The autotuner sets it where it is faster. */
+ * config, -1 for none, -2 for a bad op.  The autotuner sets it where it is faster; graphs
+ * captured before a change keep the launches they were captured with. */
 int yolo_op_tail(void* h, int k);
 int yolo_set_op_tail(void* h, int k, int tail);
 /* Number of GEMM tile configurations compiled in, and the shape of one:
