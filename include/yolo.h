@@ -151,6 +151,14 @@ void yolo_jpeg_release(void* ticket);
 int yolo_jpeg_probe(const unsigned char* data, size_t size, int* height, int* width);
 /* Threads (the calling one included) the JPEG entropy decoding runs on. */
 int yolo_decoder_threads(void);
+/* The largest frame, in pixels (height x width), the engine decodes: larger JPEG streams are
+ * reported outside the set (yolo_jpeg_probe 0, yolo_jpeg_submit NULL, status
+ * YOLO_JPEG_UNSUPPORTED), since a header of a few bytes can declare a 65535 x 65535 frame
+ * whose coefficients the decoder would have to hold.  n > 0 sets it (process-wide); returns
+ * the value in force.  The default is PIL's Image.MAX_IMAGE_PIXELS, 89,478,485.  Streams of a
+ * batch that would push its coefficient or sample buffers past 2^31 blocks or 2^32 bytes are
+ * likewise reported YOLO_JPEG_UNSUPPORTED, and the rest of the batch is staged. */
+long long yolo_jpeg_max_pixels(long long n);
 long long yolo_jpeg_coefficients(const unsigned char* data, size_t size, short* out, size_t cap);
 int yolo_get_batch(void* h, int B, YoloDet* out, int cap, int* counts);
 int yolo_get_obb_batch(void* h, int B, YoloObbDet* out, int cap, int* counts);

@@ -211,3 +211,43 @@ def test_host_only_jpeg_library():
     for s in streams:
         r, h, w = yolort.jpeg_probe(s)
         assert yoloserve.jpeg_dims(s) == ((h, w) if r == 1 else None)
+
+
+def _declare_size(data: bytes, h: int, w: int) -> bytes:
+    """The stream with its SOF0 frame header rewritten to declare h x w pixels (the entropy
+    data is left as it is, far too short for such a frame)."""
+    i = data.index(b"\xff\xc0")
+    b = bytearray(data)
+    b[i + 5:i + 7] = h.to_bytes(2, "big")
+    b[i + 7:i + 9] = w.to_bytes(2, "big")
+    return bytes(b)
+
+
+def test_huge_declared_frame_is_refused():
+    """A few hundred bytes declaring a 16384 x 16384 4:4:4 frame (1.5 GB of coefficients if
+    accepted) is outside the engine's set: probe 0, no coefficients, no ticket, so the
+    server hands it to PIL, whose decompression-bomb check refuses it for that request only.
+    The cap is the library's maximum frame size, PIL's MAX_IMAGE_PIXELS by default."""
+    import yolort
+    data = _encode(_frame(16, 16, 2), quality=90, subsampling=0)
+    assert yolort.jpeg_probe(data) == (1, 16, 16)
+    cap = yolort.jpeg_max_pixels()
+    assert cap == Image.MAX_IMAGE_PIXELS == 89478485
+    huge = _declare_size(data, 16384, 16384)
+    assert len(huge) < 2048
+    assert yolort.jpeg_probe(huge)[0] == 0
+    assert _lib_coefs(huge) is None
+    assert yolort.jpeg_submit(huge) is None
+    # the cap is inclusive, and configurable
+    side = int(np.sqrt(cap))
+    assert yolort.jpeg_probe(_declare_size(data, side, side)) == (1, side, side)
+    assert yolort.jpeg_probe(_declare_size(data, side + 1, side + 1))[0] == 0
+    try:
+        assert yolort.jpeg_max_pixels(1 << 30) == 1 << 30
+        assert yolort.jpeg_probe(huge) == (1, 16384, 16384)
+        assert yolort.jpeg_max_pixels(255) == 255
+        assert yolort.jpeg_probe(data)[0] == 0
+        assert yolort.jpeg_max_pixels(0) == 255           # 0 reads without setting
+    finally:
+        yolort.jpeg_max_pixels(cap)
+    assert yolort.jpeg_probe(data) == (1, 16, 16)

@@ -448,3 +448,31 @@ def test_frontend_connection_malformed_message():
         theirs2.close()
     finally:
         srv.stop()
+
+
+class _TicketEngine(FakeEngine):
+    """A fake engine whose batch JPEG decode fails as a whole."""
+
+    def decode_tickets(self, tickets, first_slot=0):
+        raise RuntimeError("yolo_decode_tickets failed")
+
+
+def test_ticket_decode_failure_fails_only_its_requests():
+    """A batch decode of engine-decoded JPEG streams that fails (e.g. a batch too large to
+    stage) answers those requests with a decode error; the server keeps running and serves
+    the next request."""
+    eng = _TicketEngine(0)
+    m = yoloserve.Model("det", eng, 4)
+    srv = FakeServer([m], target_ms=5.0, log=lambda *a: None)
+    try:
+        reqs = [yoloserve._Request() for _ in range(3)]
+        for r in reqs:
+            r.ticket = object()
+        srv._decode_tickets(m, reqs)
+        assert all(r.error == "image decode failed" and r.ticket is None for r in reqs)
+        assert not srv._stop
+        r = srv.submit(_png((5, 6, 7)))
+        assert r.done.wait(10.0) and r.error is None
+        assert r.message().boxes[0].x1 == 5
+    finally:
+        srv.stop()

@@ -1037,7 +1037,7 @@ struct Engine {
   }
 
   int convertDecoded(int Bn, int firstSlot, const std::vector<jpeg::Header>& hd,
-                     const std::vector<const int16_t*>& coef, const int* status, JpegStage& S, size_t descOff);
+                     const std::vector<const int16_t*>& coef, int* status, JpegStage& S, size_t descOff);
   JpegStage& nextStage(size_t bytes);
 
   void forgetDecoded(int slot) {
@@ -1388,17 +1388,45 @@ int yolo_stage_frames(void* h, int B, const unsigned char* const* host, const in
 
 namespace {
 
+// What one batch decode can hold: the IDCT addresses blocks with 32-bit indices and the
+// sample planes with 32-bit byte offsets.  admit() adds a stream if it still fits.
+struct JpegBatchBudget {
+  size_t blocks = 0, samples = 0;
+  bool admit(const yolo::jpeg::Header& H) {
+    size_t s = samples;
+    for (int c = 0; c < H.nc; c++) s = (s + (size_t)H.comp[c].bw * H.comp[c].bh * 64 + 255) & ~(size_t)255;
+    const size_t b = blocks + H.blocks();
+    if (b >= (size_t)1 << 31 || s >= (size_t)1 << 32) return false;
+    blocks = b;
+    samples = s;
+    return true;
+  }
+};
+
 // Pinned buffers for the coefficients of yolo_jpeg_submit tickets, process-wide: a buffer
 // goes back to the free list once the copy that read it has run (its event has completed).
+// The free list keeps at most kKeepBytes in buffers of at most kKeepOne each; others are
+// freed, so a burst of large frames does not leave gigabytes pinned.
 struct CoefPool {
+  static constexpr size_t kKeepOne = (size_t)64 << 20;
+  static constexpr size_t kKeepBytes = (size_t)512 << 20;
   std::mutex mu;
   std::multimap<size_t, int16_t*> free;
+  size_t freeBytes = 0;
   std::vector<std::pair<hipEvent_t, std::vector<std::pair<size_t, int16_t*>>>> retiring;
 
+  void putLocked(size_t cap, int16_t* p) {
+    if (cap > kKeepOne || freeBytes + cap > kKeepBytes) {
+      (void)hipHostFree(p);
+      return;
+    }
+    free.emplace(cap, p);
+    freeBytes += cap;
+  }
   void reclaimLocked() {
     for (auto it = retiring.begin(); it != retiring.end();) {
       if (hipEventQuery(it->first) == hipSuccess) {
-        for (auto& b : it->second) free.emplace(b.first, b.second);
+        for (auto& b : it->second) putLocked(b.first, b.second);
         (void)hipEventDestroy(it->first);
         it = retiring.erase(it);
       } else {
@@ -1414,6 +1442,7 @@ struct CoefPool {
       if (it != free.end() && it->first <= bytes * 2) {
         auto b = *it;
         free.erase(it);
+        freeBytes -= b.first;
         return b;
       }
     }
@@ -1424,7 +1453,7 @@ struct CoefPool {
   }
   void give(size_t cap, int16_t* p) {
     std::lock_guard<std::mutex> lk(mu);
-    free.emplace(cap, p);
+    putLocked(cap, p);
   }
   void retire(hipEvent_t ev, std::vector<std::pair<size_t, int16_t*>> bufs) {
     std::lock_guard<std::mutex> lk(mu);
@@ -1457,14 +1486,20 @@ struct JpegTicket {
 
 // The GPU half of a batch decode.  Streams i with status[i] == YOLO_JPEG_STAGED have headers
 // hd[i] and quantised coefficients at coef[i] (pinned host memory); the descriptors are written
-// at S.host + descOff.  Copies coefficients and descriptors to the device, runs the IDCT and
+// at S.host + descOff.  Streams past what one batch can hold (JpegBatchBudget) are set to
+// YOLO_JPEG_UNSUPPORTED.  Copies coefficients and descriptors to the device, runs the IDCT and
 // colour kernels into the slots' staging frames, records which slots hold a decoded frame and
 // records S.copied after the copies.  Returns the number of streams converted.
 int yolo::Engine::convertDecoded(int Bn, int firstSlot, const std::vector<jpeg::Header>& hd,
-                           const std::vector<const int16_t*>& coef, const int* status, JpegStage& S,
+                           const std::vector<const int16_t*>& coef, int* status, JpegStage& S,
                            size_t descOff) {
   ensureDecodeStream();
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  {
+    JpegBatchBudget budget;
+    for (int i = 0; i < Bn; i++)
+      if (status[i] == YOLO_JPEG_STAGED && !budget.admit(hd[i])) status[i] = YOLO_JPEG_UNSUPPORTED;
+  }
   std::vector<size_t> block0(Bn, 0);
   size_t blocks = 0;
   bool contiguous = true;
@@ -1513,7 +1548,6 @@ int yolo::Engine::convertDecoded(int Bn, int firstSlot, const std::vector<jpeg::
     }
     maxPix = std::max(maxPix, H.H * H.W);
   }
-  if (blocks >= (size_t)1 << 31 || sampleBytes >= (size_t)1 << 32) throw Failure("JPEG batch too large");
   if ((int)jpegH.size() < B) {
     jpegH.resize(B, 0);
     jpegW.resize(B, 0);
@@ -1578,8 +1612,10 @@ int yolo_decode_jpeg(void* h, int B, const unsigned char* const* data, const siz
     std::vector<J::Header> hd(B);
     std::vector<size_t> block0(B, 0);
     size_t blocks = 0;
+    JpegBatchBudget budget;
     for (int i = 0; i < B; i++) {
-      const int r = data[i] ? J::parse(data[i], sizes[i], hd[i]) : J::INVALID;
+      int r = data[i] ? J::parse(data[i], sizes[i], hd[i]) : J::INVALID;
+      if (r == J::OK && !budget.admit(hd[i])) r = J::UNSUPPORTED;   // past what one batch holds
       status[i] = r == J::OK ? YOLO_JPEG_STAGED : r == J::UNSUPPORTED ? YOLO_JPEG_UNSUPPORTED : YOLO_JPEG_INVALID;
       if (heights) heights[i] = r == J::OK ? hd[i].H : 0;
       if (widths) widths[i] = r == J::OK ? hd[i].W : 0;
@@ -1656,11 +1692,13 @@ int yolo_decode_tickets(void* h, int B, void* const* tickets, int first_slot, in
         hd[i] = t->hd;
         src[i] = t->coef;
       }
-      if (heights) heights[i] = status[i] == YOLO_JPEG_STAGED ? t->hd.H : 0;
-      if (widths) widths[i] = status[i] == YOLO_JPEG_STAGED ? t->hd.W : 0;
     }
     Engine::JpegStage& S = e->nextStage(3 * (size_t)B * sizeof(yolo::JpegPlane) + 256 + (size_t)B * sizeof(yolo::JpegFrame));
     const int nf = e->convertDecoded(B, first_slot, hd, src, status, S, 0);
+    for (int i = 0; i < B; i++) {   // after convertDecoded: it may refuse streams past the batch budget
+      if (heights) heights[i] = status[i] == YOLO_JPEG_STAGED ? hd[i].H : 0;
+      if (widths) widths[i] = status[i] == YOLO_JPEG_STAGED ? hd[i].W : 0;
+    }
     if (nf > 0) {
       HCK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
       HCK(hipEventRecord(ev, e->decodeSt));

@@ -260,6 +260,13 @@ void parallelFor(int n, const std::function<void(int)>& fn) {
 void runAsync(std::function<void()> fn) { pool().post(std::move(fn)); }
 
 // ------------------------------------------------------------------ headers
+namespace {
+std::atomic<long long> g_maxPixels{kDefaultMaxPixels};
+}  // namespace
+
+long long maxPixels() { return g_maxPixels.load(std::memory_order_relaxed); }
+void setMaxPixels(long long n) { g_maxPixels.store(n, std::memory_order_relaxed); }
+
 int parse(const uint8_t* d, size_t n, Header& hd) {
   if (n < 4 || d[0] != 0xFF || d[1] != 0xD8) return INVALID;
   bool haveFrame = false, jfif = false;
@@ -352,7 +359,7 @@ int parse(const uint8_t* d, size_t n, Header& hd) {
                                     : (hd.comp[0].id == 'R' && hd.comp[1].id == 'G' && hd.comp[2].id == 'B');
         if (rgb) return UNSUPPORTED;
       }
-      if (hd.H < 1 || hd.W < 1 || (long)hd.H * hd.W > (1L << 28)) return UNSUPPORTED;
+      if (hd.H < 1 || hd.W < 1 || (long long)hd.H * hd.W > maxPixels()) return UNSUPPORTED;
       hd.hmax = hd.vmax = 1;
       for (int c = 0; c < hd.nc; c++) {
         hd.hmax = std::max(hd.hmax, hd.comp[c].h);

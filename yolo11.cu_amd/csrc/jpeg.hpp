@@ -49,9 +49,18 @@ struct Header {
 
 enum { INVALID = -1, UNSUPPORTED = 0, OK = 1 };
 
-// Reads the markers up to the scan header: OK, UNSUPPORTED (a JPEG outside the path) or
-// INVALID (not a JPEG, or a malformed header).
+// Reads the markers up to the scan header: OK, UNSUPPORTED (a JPEG outside the path, or a
+// frame of more than maxPixels() pixels) or INVALID (not a JPEG, or a malformed header).
 int parse(const uint8_t* d, size_t n, Header& hd);
+
+// The largest frame (height x width) parse() accepts.  A header of a few bytes can declare a
+// frame of up to 65535 x 65535 pixels whose coefficients (up to 6 bytes a pixel) a decoder
+// must hold, so the cap is what bounds the memory a stream can pin.  The default is PIL's
+// Image.MAX_IMAGE_PIXELS (1024^3 / 4 / 3 = 89,478,485), the size above which the server's
+// other decoder starts treating a frame as a decompression bomb.
+constexpr long long kDefaultMaxPixels = 89478485LL;
+long long maxPixels();
+void setMaxPixels(long long n);
 
 // Entropy-decodes the scan of a parsed stream into quantised coefficients, int16 in natural
 // order, component plane after plane, block-row-major within a plane (hd.blocks() * 64

@@ -17,6 +17,11 @@ int yolo_jpeg_probe(const unsigned char* data, size_t size, int* height, int* wi
 
 int yolo_decoder_threads(void) { return yolo::jpeg::decoderThreads(); }
 
+long long yolo_jpeg_max_pixels(long long n) {
+  if (n > 0) yolo::jpeg::setMaxPixels(n);
+  return yolo::jpeg::maxPixels();
+}
+
 long long yolo_jpeg_coefficients(const unsigned char* data, size_t size, short* out, size_t cap) {
   if (!data) return -1;
   yolo::jpeg::Header hd;

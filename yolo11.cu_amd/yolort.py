@@ -71,6 +71,7 @@ _SIGS = {
                                       C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "yolo_jpeg_release": (None, [C.c_void_p]),
     "yolo_decoder_threads": (C.c_int, []),
+    "yolo_jpeg_max_pixels": (C.c_longlong, [C.c_longlong]),
     "yolo_jpeg_probe": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "yolo_jpeg_coefficients": (C.c_longlong, [C.c_char_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "yolo_get_batch": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(YoloDet), C.c_int, C.POINTER(C.c_int)]),
@@ -190,6 +191,11 @@ def jpeg_probe(data: bytes) -> tuple[int, int, int]:
     h, w = C.c_int(0), C.c_int(0)
     r = load().yolo_jpeg_probe(data, len(data), C.byref(h), C.byref(w))
     return r, h.value, w.value
+
+
+def jpeg_max_pixels(n: int = 0) -> int:
+    """The largest frame (pixels) the engine decodes; n > 0 sets it (process-wide)."""
+    return load().yolo_jpeg_max_pixels(n)
 
 
 def jpeg_submit(data: bytes):

@@ -559,13 +559,7 @@ class Server:
                     px = [r for r in batch if r.ticket is None]
                     batch = jp + px
                     if jp:
-                        tickets = [r.ticket for r in jp]
-                        for r in jp:
-                            r.ticket = None       # consumed by the call, whatever happens
-                        res = m.eng.decode_tickets(tickets, 0)
-                        for r, (st, _, _) in zip(jp, res):
-                            if st != 0:
-                                r.error = "image decode failed"
+                        self._decode_tickets(m, jp)
                 stage_ms = (time.monotonic() - t0) * 1e3
                 if prev is not None:
                     self._finish(*prev)
@@ -612,6 +606,26 @@ class Server:
                     r.error = "server shutting down"
                     self._release([r])
                     r.finish()
+
+    def _decode_tickets(self, m: Model, jp: list):
+        """Queues the GPU half of the batch's engine-decoded JPEG streams (slots 0..len-1).
+        A stream the engine does not stage (corrupt, or past what one batch decode holds)
+        fails its own request; a call that fails as a whole fails these requests only, and
+        the rest of the batch goes on (their slots run on whatever they held, and their
+        results are not read).  The worker stops only for failures of the batch itself."""
+        tickets = [r.ticket for r in jp]
+        for r in jp:
+            r.ticket = None               # consumed by the call, whatever happens
+        try:
+            res = m.eng.decode_tickets(tickets, 0)
+        except Exception as ex:
+            self.log(f"[serve] JPEG batch decode failed: {ex!r}")
+            for r in jp:
+                r.error = "image decode failed"
+            return
+        for r, (st, _, _) in zip(jp, res):
+            if st != 0:
+                r.error = "image decode failed"
 
     def _release(self, batch: list):
         for r in batch:
