@@ -48,8 +48,15 @@ def conv_weights(g: Graph, op: Op) -> tuple[np.ndarray, np.ndarray]:
     return w, b
 
 
-def conv2d_nhwc(x: np.ndarray, w: np.ndarray, b: np.ndarray, s: int, p: int, groups: int) -> np.ndarray:
-    """x [B,H,W,Cin] fp32, w [O,k,k,Cin/g] -> [B,Ho,Wo,O] fp32 (im2col over (ky,kx,ci))."""
+def conv2d_nhwc(x: np.ndarray, w: np.ndarray, b: np.ndarray, s: int, p: int, groups: int,
+                acc=F32, kperm: np.random.Generator | None = None) -> np.ndarray:
+    """x [B,H,W,Cin] fp32, w [O,k,k,Cin/g] -> [B,Ho,Wo,O] fp32 (im2col over (ky,kx,ci)).
+    `acc` is the arithmetic type of the products and sums (float32, or float64 to measure
+    what fp32 accumulation alone changes); the result is float32 either way.  `kperm`
+    (dense convs): the K terms are summed in an order drawn from this generator, the same
+    sum in another valid fp32 order."""
+    if acc is not F32:
+        x, w, b = x.astype(acc), w.astype(acc), b.astype(acc)
     B, H, W, Cin = x.shape
     O, k, _, ig = w.shape
     Ho, Wo = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
@@ -60,11 +67,15 @@ def conv2d_nhwc(x: np.ndarray, w: np.ndarray, b: np.ndarray, s: int, p: int, gro
         else:
             v = sliding_window_view(xp, (k, k), axis=(1, 2))[:, ::s, ::s][:, :Ho, :Wo]
             cols = np.ascontiguousarray(v.transpose(0, 1, 2, 4, 5, 3)).reshape(B * Ho * Wo, k * k * Cin)
-        y = cols @ w.reshape(O, -1).T
+        wk = w.reshape(O, -1)
+        if kperm is not None:
+            perm = kperm.permutation(wk.shape[1])
+            cols, wk = cols[:, perm], wk[:, perm]
+        y = cols @ wk.T
         y += b
         return y.reshape(B, Ho, Wo, O).astype(F32, copy=False)
     assert groups == Cin == O and ig == 1
-    y = np.broadcast_to(b, (B, Ho, Wo, O)).astype(F32)
+    y = np.broadcast_to(b, (B, Ho, Wo, O)).astype(acc)
     for ky in range(k):
         for kx in range(k):
             y = y + xp[:, ky:ky + s * (Ho - 1) + 1:s, kx:kx + s * (Wo - 1) + 1:s, :] * w[:, ky, kx, 0]
@@ -104,14 +115,15 @@ def softmax_ch(x: np.ndarray) -> np.ndarray:
     return (e / e.sum(axis=-1, keepdims=True, dtype=F32)).astype(F32)
 
 
-def attention(qkv: np.ndarray, heads: int, kd: int, hd: int) -> np.ndarray:
-    """qkv [B,H,W,heads*(2kd+hd)] (per-head [q kd | k kd | v hd]) -> [B,H,W,heads*hd]."""
+def attention(qkv: np.ndarray, heads: int, kd: int, hd: int, acc=F32) -> np.ndarray:
+    """qkv [B,H,W,heads*(2kd+hd)] (per-head [q kd | k kd | v hd]) -> [B,H,W,heads*hd]
+    (arithmetic in `acc`, result float32)."""
     B, H, W, _ = qkv.shape
     N = H * W
     per = 2 * kd + hd
-    t = qkv.reshape(B, N, heads, per)
+    t = qkv.astype(acc).reshape(B, N, heads, per)
     out = np.empty((B, N, heads * hd), F32)
-    scale = F32(kd ** -0.5)
+    scale = acc(kd ** -0.5)
     for b in range(B):
         for h in range(heads):
             q = t[b, :, h, :kd]
@@ -126,10 +138,17 @@ def attention(qkv: np.ndarray, heads: int, kd: int, hd: int) -> np.ndarray:
 
 
 class Interp:
-    """Executes a parsed graph for a batch of B images."""
+    """Executes a parsed graph for a batch of B images.  `acc64`: conv and attention
+    arithmetic in float64 (outputs still stored as float32, and through fp16 with
+    `round_fp16`); `order_seed`: conv sums in another fp32 order.  Both measure how much a
+    whole frame depends on the rounding of its fp32 accumulations."""
 
-    def __init__(self, g: Graph, B: int = 1, round_fp16: bool = False):
+    def __init__(self, g: Graph, B: int = 1, round_fp16: bool = False, acc64: bool = False,
+                 order_seed: int | None = None):
         self.g, self.B, self.round_fp16 = g, B, round_fp16
+        self.acc = np.float64 if acc64 else F32
+        # order_seed: every dense conv sums its K terms in a seeded random order
+        self.kperm = None if order_seed is None else np.random.default_rng(order_seed)
         self.bufs = [np.zeros((B, H, W, C), F32) for (H, W, C) in g.bufs]
         self.heads_in: list = []   # DECODE / DECODESEG / DECODEOBB inputs, in op order
 
@@ -151,7 +170,7 @@ class Interp:
         g = self.g
         if op.kind == "CONV":
             w, b = conv_weights(g, op)
-            y = conv2d_nhwc(self.view(op.a), w, b, op.s, op.p, op.g)
+            y = conv2d_nhwc(self.view(op.a), w, b, op.s, op.p, op.g, self.acc, self.kperm)
             if op.act == 1:
                 y = silu(y)
             if op.b >= 0:    # fused residual: act then +res
@@ -174,7 +193,7 @@ class Interp:
             self.write(op.out, self.view(op.a).copy())
             return op.out
         if op.kind == "ATTN":
-            self.write(op.out, attention(self.view(op.a), op.heads, op.kd, op.hd))
+            self.write(op.out, attention(self.view(op.a), op.heads, op.kd, op.hd, self.acc))
             return op.out
         if op.kind == "GAP":     # export/export.py:501-502: mean over H, W
             self.write(op.out, gap(self.view(op.a)))

@@ -410,3 +410,52 @@ def rel_err(gpu: np.ndarray, ref: np.ndarray) -> float:
     """max|gpu - ref| / (max|ref| + 1e-6), the reference's per-op metric (test/compare.py:21-25)."""
     ref = ref.astype(np.float64)
     return float(np.abs(gpu.astype(np.float64) - ref).max() / (np.abs(ref).max() + 1e-6))
+
+
+def match_e2e(ref: dict, got: dict, ref_masks=None, got_masks=None, score_gate: float = 0.27):
+    """The reference's end-to-end matching (test/compare_seg.py:61-100): every reference
+    detection, in its survivor order, takes the unused same-class detection of `got` with
+    the highest box IoU (first one on ties); IoU <= 0.8 leaves it unmatched, which counts as
+    a failure when its score exceeds `score_gate`.  A matched pair fails if |dscore| > 0.02,
+    a box corner moved more than 2 px, or (with masks) their mask IoU is below 0.95.
+    `ref` / `got`: dicts with "box" [n,4], "score" [n], "cls" [n] (boxes in one coordinate
+    system).  Returns a dict of counts and the per-pair |dscore|, corner and mask-IoU lists."""
+    rb = np.asarray(ref["box"], np.float64)
+    gb = np.asarray(got["box"], np.float64)
+    rs, gs = np.asarray(ref["score"], np.float64), np.asarray(got["score"], np.float64)
+    rc, gc = np.asarray(ref["cls"]).astype(int), np.asarray(got["cls"]).astype(int)
+    used = np.zeros(len(gb), bool)
+    out = {"n_ref": len(rb), "n_got": len(gb), "unmatched": 0, "unmatched_gated": 0, "pair_fail": 0,
+           "dscore": [], "dbox": [], "mask_iou": []}
+    for i in range(len(rb)):
+        cand = np.nonzero((gc == rc[i]) & ~used)[0]
+        best, bj = 0.0, -1
+        if len(cand):
+            a, b = rb[i], gb[cand]
+            iw = np.clip(np.minimum(a[2], b[:, 2]) - np.maximum(a[0], b[:, 0]), 0, None)
+            ih = np.clip(np.minimum(a[3], b[:, 3]) - np.maximum(a[1], b[:, 1]), 0, None)
+            inter = iw * ih
+            ua = (a[2] - a[0]) * (a[3] - a[1]) + (b[:, 2] - b[:, 0]) * (b[:, 3] - b[:, 1]) - inter
+            iou = inter / np.maximum(ua, 1e-9)
+            k = int(np.argmax(iou))
+            if iou[k] > 0:
+                best, bj = float(iou[k]), int(cand[k])
+        if bj < 0 or best <= 0.8:
+            out["unmatched"] += 1
+            out["unmatched_gated"] += int(rs[i] > score_gate)
+            continue
+        used[bj] = True
+        ds = abs(rs[i] - gs[bj])
+        db = float(np.abs(rb[i] - gb[bj]).max())
+        ok = ds <= 0.02 and db <= 2.0
+        out["dscore"].append(ds)
+        out["dbox"].append(db)
+        if ref_masks is not None and got_masks is not None:
+            inter = np.logical_and(ref_masks[i], got_masks[bj]).sum()
+            union = np.logical_or(ref_masks[i], got_masks[bj]).sum()
+            miou = float(inter) / max(int(union), 1)
+            out["mask_iou"].append(miou)
+            ok = ok and miou >= 0.95
+        out["pair_fail"] += int(not ok)
+    out["fails"] = out["unmatched_gated"] + out["pair_fail"]
+    return out

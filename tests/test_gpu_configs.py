@@ -19,93 +19,10 @@ import modelgen
 import yolort
 from oracle import graphfile, interp, post
 
-TOL = 0.015
+from _frame_gate import TOL, assert_dets_equal, gate, letterbox_slots, trajectory
+import _frame_gate as fg
 
 pytestmark = pytest.mark.gpu
-
-
-def _letterbox_slots(eng, frames):
-    bufs = []
-    for s, f in enumerate(frames):
-        b = yolort.DeviceBuffer(f.nbytes)
-        eng.upload(b, f)
-        eng.preprocess(b.ptr, f.shape[0], f.shape[1], s)
-        bufs.append(b)
-    eng.sync()
-    return bufs
-
-
-def _to_original(eng, slot, dets):
-    """Oracle boxes (letterbox space) mapped to original-image coordinates with yolo_get's
-    float32 operations, so they compare with yolo_get's output directly."""
-    scale, top, left = eng.slot_geom(slot)
-    b = dets.astype(np.float32)
-    x1 = (b[:, 0] - np.float32(left)) / np.float32(scale)
-    y1 = (b[:, 1] - np.float32(top)) / np.float32(scale)
-    x2 = (b[:, 2] - np.float32(left)) / np.float32(scale)
-    y2 = (b[:, 3] - np.float32(top)) / np.float32(scale)
-    return np.stack([x1, y1, x2, y2], 1).astype(np.float64)
-
-
-def _assert_dets_equal(eng, slot, got, want):
-    """Exact decode + NMS parity: same count, classes and survivor order, scores within fp32
-    rounding of the sigmoid, boxes from the same float32 arithmetic."""
-    assert len(got) == len(want["score"]), (slot, len(got), len(want["score"]))
-    np.testing.assert_array_equal(got[:, 5].astype(int), want["cls"])
-    np.testing.assert_allclose(got[:, 4], want["score"], rtol=0, atol=2e-6)
-    np.testing.assert_allclose(got[:, :4], _to_original(eng, slot, want["box"]), rtol=0, atol=2e-3)
-
-
-def _trajectory(eng, g, B, check_slots, conf=0.25, iou=0.45):
-    """Runs the engine's (fused) op list op by op for B images; every op's output on
-    `check_slots` is compared with the oracle applied to that op's GPU inputs.  Returns the
-    worst per-op deviations and the oracle detections on the run's own head tensors."""
-    fops = graphfile.fuse_adds(g.ops)
-    assert eng.num_ops == len(fops)
-    n = len(check_slots)
-    ref = interp.Interp(g, n)
-    rels = []
-    for k, op in enumerate(fops):
-        info = eng.op_info(k)
-        assert info["kind"] == op.kind and info["a"] == op.a and info["out"] == op.out, (k, info, op)
-        ins = [t for t in ((op.a, op.b) if op.kind in ("CONV", "ADD") else (op.a,)) if t >= 0]
-        if op.kind in ("DECODESEG", "DECODEOBB"):
-            ins = [op.a, op.b, op.out]
-        elif op.kind == "DECODE":
-            ins = [op.a, op.b]
-        for t in ins:
-            for j, s in enumerate(check_slots):
-                ref.view(t)[j] = eng.read_slots(t, s)[0].astype(np.float32)
-        eng.run_op(k, B)
-        t = ref.run_op(op)
-        if t is None:
-            continue
-        got = np.concatenate([eng.read_slots(t, s) for s in check_slots]).astype(np.float32)
-        rel = post.rel_err(got, ref.view(t))
-        rels.append((k, op.kind, rel))
-        if k % 25 == 0:
-            print(f"  op {k}/{len(fops)} {op.kind} rel {rel:.2e}", flush=True)
-    eng.run_post(B)
-    wants = []
-    for j, s in enumerate(check_slots):
-        heads = []
-        for op in fops:
-            if op.kind in ("DECODE", "DECODESEG"):
-                heads.append((eng.read_slots(op.a, s)[0].astype(np.float32),
-                              eng.read_slots(op.b, s)[0].astype(np.float32),
-                              eng.read_slots(op.out, s)[0].astype(np.float32) if op.kind == "DECODESEG" else None,
-                              op.stride))
-        wants.append(post.detect(heads, g.nc, conf, iou))
-    return rels, wants
-
-
-def _gate(rels, label):
-    worst = sorted(rels, key=lambda r: -r[2])[:4]
-    print(f"{label}: {len(rels)} ops, worst " + ", ".join(f"op{k:03d} {kind} {r:.2e}" for k, kind, r in worst),
-          flush=True)
-    bad = [r for r in rels if not r[2] <= TOL]
-    assert not bad, bad
-
 
 FRAMES = {
     "C0": lambda: modelgen.synth_frame(810, 1080, 20, 1),
@@ -127,12 +44,12 @@ def test_frame_trajectory_and_graph(models, case, arch, scale, task, iou):
     print(f"{case}: {arch}{scale}-{task} frame {img.shape[:2]} iou {iou}", flush=True)
     eng = yolort.Engine(d, 1)          # fused, autotuned, graphs captured (the bench setup)
     eng.set_thresholds(0.25, iou, 300)
-    bufs = _letterbox_slots(eng, [img])
+    bufs = letterbox_slots(eng, [img])
     np.testing.assert_array_equal(eng.read(0, 1)[0], post.letterbox(img, 640, 640))
-    rels, wants = _trajectory(eng, g, 1, [0], 0.25, iou)
-    _gate(rels, case)
+    rels, wants = trajectory(eng, g, 1, [0], 0.25, iou)
+    gate(rels, case)
     traj = eng.get(0)
-    _assert_dets_equal(eng, 0, traj, wants[0])
+    assert_dets_equal(eng, 0, traj, wants[0])
     assert eng.raw_count(0) == wants[0]["n_raw"]
     print(f"{case}: kept {len(traj)} raw {eng.raw_count(0)} (exact vs oracle on the run's heads)", flush=True)
     if task == "segment":
@@ -152,6 +69,19 @@ def test_frame_trajectory_and_graph(models, case, arch, scale, task, iou):
         eng.frame_run()
         np.testing.assert_array_equal(eng.get(0), traj)
         assert eng.raw_count(0) == wants[0]["n_raw"]
+    # end to end (test/compare_seg.py:61-100): the frame's detections (= the trajectory's, in
+    # letterbox space) against the round-fp16 oracle run on the same letterboxed input, held
+    # to twice the oracle's own disagreement under fp32 rounding changes plus a small slack
+    x = post.letterbox(img, 640, 640)[None].astype(np.float32)
+    ref = fg.oracle_frame(g, x, task, iou)
+    got = dict(wants[0])
+    if task == "segment":
+        got["masks"] = np.stack([eng.get_mask(0, i) for i in range(len(traj))]) if len(traj) else None
+    d_gpu = fg.disagreement(ref, got)
+    floor = fg.noise_floor(g, x, task, iou, ref)
+    bound = fg.e2e_bound(floor)
+    print(f"{case}: end to end vs the round-fp16 oracle {d_gpu}; oracle floor {floor}; bound {bound}", flush=True)
+    assert fg.within(d_gpu, bound), (d_gpu, bound)
     bufs[0].free()
     eng.close()
 
@@ -173,7 +103,7 @@ def test_yolo11x_b16_ops_resync(models):
     frames = _x_frames()
     pick = [0, X_B - 1]
     eng = yolort.Engine(d, X_B, yolort.YOLO_NOFUSE | yolort.YOLO_NOGRAPH)
-    bufs = _letterbox_slots(eng, frames)
+    bufs = letterbox_slots(eng, frames)
     ref = interp.Interp(g, len(pick), round_fp16=True)
     ref.set_input(np.stack([post.letterbox(frames[s], 640, 640) for s in pick]).astype(np.float32))
     for j, s in enumerate(pick):
@@ -192,7 +122,7 @@ def test_yolo11x_b16_ops_resync(models):
             print(f"  op {k}/{len(g.ops)} {op.kind} rel {rels[-1][2]:.2e}", flush=True)
         for j, s in enumerate(pick):
             eng.write_slots(t, s, want[j:j + 1])
-    _gate(rels, "yolo11x b16 resync")
+    gate(rels, "yolo11x b16 resync")
     assert len(rels) == sum(1 for op in g.ops if op.kind not in ("DECODE",))
     eng.run_post(X_B)
     for j, s in enumerate(pick):
@@ -201,16 +131,16 @@ def test_yolo11x_b16_ops_resync(models):
         got = eng.get(s)
         print(f"slot {s}: kept {len(got)} raw {eng.raw_count(s)}", flush=True)
         assert eng.raw_count(s) == want["n_raw"]
-        _assert_dets_equal(eng, s, got, want)
+        assert_dets_equal(eng, s, got, want)
     for b in bufs:
         b.free()
     eng.close()
 
 
-def test_yolo11x_b16_frame_graph(models):
-    """The bench configuration: fused + autotuned yolo11x, sixteen frames in one frame graph.
-    Decode + NMS exact on the GPU's own heads for every slot; slot i equal to a batch-1 run
-    of frame i on the same handle (the reference's batch self-consistency check)."""
+@pytest.fixture(scope="module")
+def x_fused(models):
+    """The bench configuration of config 3, built once for the module: fused + autotuned
+    yolo11x at batch 16 with its graphs, and the sixteen frames uploaded to the device."""
     d = models("yolo11", "x")
     g = graphfile.load(d)
     frames = _x_frames()
@@ -220,6 +150,17 @@ def test_yolo11x_b16_frame_graph(models):
         b = yolort.DeviceBuffer(f.nbytes)
         eng.upload(b, f)
         devs.append(b)
+    yield g, frames, eng, devs
+    for b in devs:
+        b.free()
+    eng.close()
+
+
+def test_yolo11x_b16_frame_graph(x_fused):
+    """Sixteen frames in one frame graph: decode + NMS exact on the GPU's own heads for every
+    slot; slot i equal to a batch-1 run of frame i on the same handle (the reference's batch
+    self-consistency check)."""
+    g, frames, eng, devs = x_fused
     eng.frame_graph([b.ptr for b in devs], [640] * X_B, [640] * X_B)
     eng.frame_run()
     batch = [eng.get(s) for s in range(X_B)]
@@ -229,7 +170,7 @@ def test_yolo11x_b16_frame_graph(models):
                   None, op.stride) for op in dec]
         want = post.detect(heads, 80)
         assert eng.raw_count(s) == want["n_raw"]
-        _assert_dets_equal(eng, s, batch[s], want)
+        assert_dets_equal(eng, s, batch[s], want)
     print("kept per slot:", [len(b) for b in batch], flush=True)
     assert sum(len(b) for b in batch) > 0
     for i in range(X_B):
@@ -238,27 +179,20 @@ def test_yolo11x_b16_frame_graph(models):
         one = eng.get(0)
         assert len(one) == len(batch[i]), (i, len(one), len(batch[i]))
         np.testing.assert_array_equal(one, batch[i])
-    for b in devs:
-        b.free()
-    eng.close()
 
 
-def test_yolo11x_b16_trajectory(models):
-    """The fused, autotuned yolo11x batch-16 run op by op: images 0 and 15 of every op's
-    output against the oracle applied to that op's GPU inputs; decode + NMS exact."""
-    d = models("yolo11", "x")
-    g = graphfile.load(d)
-    frames = _x_frames()
-    eng = yolort.Engine(d, X_B, yolort.YOLO_NOGRAPH)
-    bufs = _letterbox_slots(eng, frames)
+def test_yolo11x_b16_trajectory(x_fused):
+    """The same fused, autotuned engine run op by op at batch 16: images 0 and 15 of every
+    op's output against the oracle applied to that op's GPU inputs; decode + NMS exact."""
+    g, frames, eng, devs = x_fused
+    for s in range(X_B):
+        eng.preprocess(devs[s].ptr, 640, 640, s)
+    eng.sync()
     pick = [0, X_B - 1]
-    rels, wants = _trajectory(eng, g, X_B, pick)
-    _gate(rels, "yolo11x b16 trajectory")
+    rels, wants = trajectory(eng, g, X_B, pick)
+    gate(rels, "yolo11x b16 trajectory")
     for j, s in enumerate(pick):
-        _assert_dets_equal(eng, s, eng.get(s), wants[j])
-    for b in bufs:
-        b.free()
-    eng.close()
+        assert_dets_equal(eng, s, eng.get(s), wants[j])
 
 
 def test_branches_eager_equals_serial(models):
@@ -270,7 +204,7 @@ def test_branches_eager_equals_serial(models):
     res = {}
     for name, flags in (("branches", yolort.YOLO_BRANCHES), ("serial", 0)):
         eng = yolort.Engine(d, 2, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH | flags)
-        bufs = _letterbox_slots(eng, [img, modelgen.synth_frame(640, 640, 50, 4)])
+        bufs = letterbox_slots(eng, [img, modelgen.synth_frame(640, 640, 50, 4)])
         outs = []
         for _ in range(3):
             eng.run(2)

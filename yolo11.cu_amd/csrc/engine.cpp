@@ -1876,15 +1876,36 @@ int yolo_tensor_shape(void* h, int t, int* hwc) {
   return 0;
 }
 
+// Tensor reads and writes for the parity harness.  A view is n*H*W pixel rows of C halves at
+// a row stride of s halves; a 2-D copy with one row per pixel costs microseconds per row on
+// this runtime (seconds for a batch-32 80x80 tensor), so the span from the first row to the
+// end of the last is moved with one 1-D copy and the rows are gathered or scattered on the
+// host (a write reads the span first, so channels outside the view are left as they are).
+namespace {
+struct TensorSpan {
+  yolo::f16* dev;   // first element of the view's first row
+  size_t rows, C, s, bytes;
+};
+TensorSpan tensorSpan(const yolo::View& v, int first, int n) {
+  const size_t img = (size_t)v.H * v.W * v.s, rows = (size_t)n * v.H * v.W;
+  return {v.p + first * img + v.o, rows, (size_t)v.C, (size_t)v.s, ((rows - 1) * v.s + v.C) * sizeof(yolo::f16)};
+}
+}  // namespace
+
 int yolo_read_tensor_slots(void* h, int t, int first, int n, void* host_f16) {
   return guarded([&] {
     Engine* e = E(h);
     if (t < 0 || t >= (int)e->g.tens.size() || first < 0 || n < 1 || first + n > e->B) return -1;
-    yolo::View v = e->view(t);
-    const size_t img = (size_t)v.H * v.W * v.s;
+    const TensorSpan sp = tensorSpan(e->view(t), first, n);
     HCK(hipStreamSynchronize(e->st));
-    HCK(hipMemcpy2D(host_f16, v.C * 2, v.p + first * img + v.o, (size_t)v.s * 2, v.C * 2,
-                    (size_t)n * v.H * v.W, hipMemcpyDeviceToHost));
+    if (sp.s == sp.C) {
+      HCK(hipMemcpy(host_f16, sp.dev, sp.bytes, hipMemcpyDeviceToHost));
+      return 0;
+    }
+    std::vector<yolo::f16> tmp(sp.bytes / sizeof(yolo::f16));
+    HCK(hipMemcpy(tmp.data(), sp.dev, sp.bytes, hipMemcpyDeviceToHost));
+    auto* out = static_cast<yolo::f16*>(host_f16);
+    for (size_t r = 0; r < sp.rows; r++) std::memcpy(out + r * sp.C, tmp.data() + r * sp.s, sp.C * sizeof(yolo::f16));
     return 0;
   });
 }
@@ -1893,11 +1914,17 @@ int yolo_write_tensor_slots(void* h, int t, int first, int n, const void* host_f
   return guarded([&] {
     Engine* e = E(h);
     if (t < 0 || t >= (int)e->g.tens.size() || first < 0 || n < 1 || first + n > e->B) return -1;
-    yolo::View v = e->view(t);
-    const size_t img = (size_t)v.H * v.W * v.s;
+    const TensorSpan sp = tensorSpan(e->view(t), first, n);
     HCK(hipStreamSynchronize(e->st));
-    HCK(hipMemcpy2D(v.p + first * img + v.o, (size_t)v.s * 2, host_f16, v.C * 2, v.C * 2,
-                    (size_t)n * v.H * v.W, hipMemcpyHostToDevice));
+    if (sp.s == sp.C) {
+      HCK(hipMemcpy(sp.dev, host_f16, sp.bytes, hipMemcpyHostToDevice));
+      return 0;
+    }
+    std::vector<yolo::f16> tmp(sp.bytes / sizeof(yolo::f16));
+    HCK(hipMemcpy(tmp.data(), sp.dev, sp.bytes, hipMemcpyDeviceToHost));
+    const auto* in = static_cast<const yolo::f16*>(host_f16);
+    for (size_t r = 0; r < sp.rows; r++) std::memcpy(tmp.data() + r * sp.s, in + r * sp.C, sp.C * sizeof(yolo::f16));
+    HCK(hipMemcpy(sp.dev, tmp.data(), sp.bytes, hipMemcpyHostToDevice));
     return 0;
   });
 }
