@@ -68,6 +68,18 @@ def measured_traffic(cfg, tail=-1):
         return None
 
 
+def measured_x_traffic(ops):
+    """HBM bytes per batch of the given yolo11x b16 conv ops (FETCH_SIZE + WRITE_SIZE of their
+    dispatches in the committed PMC passes, each scaled by a plain copy of known size), or
+    None where a pass has no figure for one of them (tile choices differ from that run's)."""
+    path = os.path.join(ROOT, "profiles", "yolo11x_b16_traffic.json")
+    try:
+        rec = json.load(open(path))["per_op"]
+        return int(sum(rec[str(k)]["traffic_bytes"] for k in ops))
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def conv_kernel_name(cfg, tail=-1):
     """The kernel an op config selects (yolo_set_op_config's numbering), with its tail retile."""
     if cfg == 1000:
@@ -85,6 +97,81 @@ def conv_flops(eng, k):
     info = eng.op_info(k)
     H, W, _ = eng.tensor_shape(info["out"])
     return 2.0 * H * W * info["Cout"] * info["k"] * info["k"] * info["Cin"] / max(info["g"], 1)
+
+
+def conv_work(eng, k, B):
+    """Algorithmic FLOPs and HBM bytes of conv op k at batch B: 2*B*Ho*Wo*Cout*k^2*Cin/g FLOPs;
+    input + weights + output (+ residual) in fp16 plus the fp32 bias."""
+    info = eng.op_info(k)
+    Ho, Wo, _ = eng.tensor_shape(info["out"])
+    Hi, Wi, _ = eng.tensor_shape(info["a"])
+    g = max(info["g"], 1)
+    kk = info["k"] * info["k"]
+    flops = 2.0 * B * Ho * Wo * info["Cout"] * kk * info["Cin"] / g
+    out_px = B * Ho * Wo * info["Cout"]
+    nbytes = 2.0 * (B * Hi * Wi * info["Cin"] + info["Cout"] * kk * info["Cin"] / g + out_px
+                    + (out_px if info["b"] >= 0 else 0)) + 4.0 * info["Cout"]
+    return flops, nbytes
+
+
+def unit_kernel(eng, k):
+    """Kernel name and shape class of the launch unit whose first op is k."""
+    info = eng.op_info(k)
+    if info["kind"] != "CONV":
+        return {"ATTN": "k_attention", "MAXPOOL5": "k_sppf_pool / k_maxpool5", "UPSAMPLE2": "k_upsample2",
+                "COPYC": "k_copyc", "ADD": "k_add", "PS2": "k_ps2", "GAP": "k_gap",
+                "SOFTMAX": "k_softmax_ch"}.get(info["kind"], info["kind"]), ""
+    if info["Cin"] == 3:
+        return "k_conv_first", "stem 3x3 s2"
+    if info["g"] > 1:
+        return "k_dwconv", "depthwise 3x3"
+    cls = "1x1" if info["k"] == 1 else f"{info['k']}x{info['k']} s{info['s']}"
+    return conv_kernel_name(eng.op_config(k), eng.op_tail(k)), cls
+
+
+def unit_table(eng, B, per_unit):
+    """Per-unit kernel time (hipEvents, units repeated back to back) grouped by kernel and
+    shape class, with the algorithmic FLOPs and bytes of the ops each unit launches."""
+    groups = {}
+    unit = [eng.op_unit(k) for k in range(eng.num_ops)]
+    first_of = {}
+    for k, u in enumerate(unit):
+        if u >= 0:
+            first_of.setdefault(u, k)
+    for k, u in enumerate(unit):
+        if u < 0:
+            continue
+        first = first_of[u]
+        name, cls = unit_kernel(eng, first)
+        g = groups.setdefault((name, cls), {"kernel": name, "class": cls, "launches": 0, "ms": 0.0,
+                                            "flops": 0.0, "bytes": 0.0, "ops": []})
+        if k == first:
+            g["launches"] += 1
+            g["ms"] += float(per_unit[k])
+        if eng.op_info(k)["kind"] == "CONV":
+            f, b = conv_work(eng, k, B)
+            g["flops"] += f
+            g["bytes"] += b
+        g["ops"].append(k)
+    return sorted(groups.values(), key=lambda g: -g["ms"])
+
+
+def group_roofline(g, traffic=None):
+    """Roofline entry of a kernel group: MFMA-bound when its arithmetic intensity is above
+    the chip's ratio (2.5 PFLOP/s / 8 TB/s = 312.5 FLOP/B), HBM-bound below."""
+    ai = g["flops"] / g["bytes"] if g["bytes"] else 0.0
+    sec = g["ms"] * 1e-3
+    if ai >= PEAK_FP16 / PEAK_HBM:
+        ach = g["flops"] / sec
+        r = {"bound": "mfma", "achieved": round(ach / 1e12, 2), "peak": 2500.0, "unit": "TFLOP/s",
+             "frac": round(ach / PEAK_FP16, 4)}
+    else:
+        ach = g["bytes"] / sec
+        r = {"bound": "hbm", "achieved": round(ach / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+             "frac": round(ach / PEAK_HBM, 4), "tflops": round(g["flops"] / sec / 1e12, 1)}
+    r.update({"traffic": traffic, "kernel": g["kernel"], "class": g["class"], "launches": g["launches"],
+              "ms": round(g["ms"], 4), "flops": g["flops"], "bytes": g["bytes"], "ai": round(ai, 1)})
+    return r
 
 
 def attn_flops(eng, k):
@@ -145,11 +232,17 @@ def bench_n(workdir, steps, warmup, graph=True):
     graph_ms = eng.time_graph(1, 1, max(steps, 50))
     kept, raw = len(dets), eng.raw_count(0)
     per_op = eng.profile_ops(1, 20)
+    # attribution of the graph's time: every launch unit timed with hipEvents around 5
+    # back-to-back launches (no host gap), grouped by kernel
+    per_unit = eng.profile_units(1, 20, 5)
+    units = unit_table(eng, 1, per_unit)
     pin.free()
     dev.free()
     eng.close()
     return dict(ms=ms, graph_ms=graph_ms, ms_hbm=ms_hbm, graph_ms_hbm=graph_ms_hbm, kept=kept, raw=raw,
-                stream_ops_ms=float(per_op.sum()), stages=stages, frame=(810, 1080), A=8400, ncpad=80)
+                stream_ops_ms=float(per_op.sum()), stages=stages, frame=(810, 1080), A=8400, ncpad=80,
+                units=units, units_ms=float(sum(g["ms"] for g in units)),
+                launches=int(sum(g["launches"] for g in units)))
 
 
 def bench_task(workdir, task, imgsz, nc, cls_bias, frame, steps, warmup, graph=True):
@@ -336,10 +429,14 @@ def bench_x(workdir, iters, graph=True):
         elif info["kind"] == "ATTN":
             attn_t += per_unit[k] * 1e-3
             attn_f += B * attn_flops(eng, k)
+    units = unit_table(eng, B, per_unit)
+    top = next(g for g in units if g["flops"] > 0)      # the conv kernel group with the most time
+    traffic = measured_x_traffic(top["ops"])
     for b in devs:
         b.free()
     eng.close()
-    return dict(ms_per_batch=ms, img_per_s=B * 1e3 / ms, conv_tflops=conv_f / conv_t / 1e12,
+    return dict(dominant=group_roofline(top, traffic), units=units[:12],
+                ms_per_batch=ms, img_per_s=B * 1e3 / ms, conv_tflops=conv_f / conv_t / 1e12,
                 conv_mfma_util=conv_f / conv_t / PEAK_FP16, conv_ms=conv_t * 1e3,
                 conv_mfma_util_stream_events=conv_f / conv_t_ev / PEAK_FP16, conv_ms_stream_events=conv_t_ev * 1e3,
                 attn_ms=attn_t * 1e3, attn_tflops=attn_f / attn_t / 1e12, attn_mfma_util=attn_f / attn_t / PEAK_FP16,
@@ -430,6 +527,65 @@ def bench_serve(workdir, seconds=4.0, procs=4, callers=16, frontends=4):
                 mean_batch=float(np.mean([r["mean_batch"] for r in res])), requests=sum(r["requests"] for r in res),
                 exec_ms_b16=round(models[0].exec_ms, 4), frames="640x640 JPEG q90, decoded on the engine",
                 decoder_threads=yolort.decoder_threads(), frontend_processes=frontends)
+
+
+def bench_feeder(workdir, seconds=4.0, feeders=48, native=True):
+    """The server's engine side alone: `feeders` threads submit 640x640 JPEG frames straight
+    to yoloserve.Server (no gRPC) in a closed loop, yolo11n with max batch 16 and target
+    50 ms; throughput and mean batch.  native=True is the library's batch worker
+    (yolo_batcher_*), False the same loop in Python."""
+    import io
+    import threading
+    import modelgen
+    import yolort
+    import yoloserve
+    from PIL import Image
+    d = os.path.join(workdir, "yolo11n_feed")
+    if not os.path.exists(os.path.join(d, "model.graph")):
+        modelgen.write_model(d, "yolo11", "n", cls_bias=-8.0)
+    streams = []
+    for i in range(16):
+        b = io.BytesIO()
+        Image.fromarray(modelgen.synth_frame(640, 640, 50, 500 + i)[..., ::-1].copy()).save(b, "JPEG", quality=90)
+        streams.append(b.getvalue())
+    eng = yolort.Engine(d, 16)
+    srv = yoloserve.Server([yoloserve.Model("yolo11n", eng, 16)], target_ms=50.0, log=lambda *a: None,
+                           native=native)
+    stop_at = [0.0]
+    counts = [0] * feeders
+    batches = [0.0] * feeders
+    errors = [0]
+
+    def feed(i):
+        k = i
+        while time.perf_counter() < stop_at[0]:
+            r = srv.submit_jpeg(streams[k % 16])
+            k += 1
+            r.done.wait()
+            if r.error:
+                errors[0] += 1
+                continue
+            counts[i] += 1
+            batches[i] += r.resp.batch
+
+    try:
+        for secs, measure in ((1.0, False), (seconds, True)):
+            counts[:] = [0] * feeders
+            batches[:] = [0.0] * feeders
+            stop_at[0] = time.perf_counter() + secs
+            t0 = time.perf_counter()
+            ts = [threading.Thread(target=feed, args=(i,)) for i in range(feeders)]
+            for t in ts:
+                t.start()
+            for t in ts:
+                t.join()
+            el = time.perf_counter() - t0
+    finally:
+        srv.stop()
+        eng.close()
+    n = sum(counts)
+    return dict(img_per_s=round(n / el, 1), feeders=feeders, mean_batch=round(sum(batches) / max(n, 1), 2),
+                errors=errors[0], worker="native (yolo_batcher)" if native else "python")
 
 
 def bench_jpeg(workdir, batches=60, graphs=True):
@@ -533,7 +689,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "n", "x", "conv", "obb", "seg", "m", "sweep", "cls", "serve", "jpeg"],
+    ap.add_argument("--only", choices=["all", "n", "x", "conv", "obb", "seg", "m", "sweep", "cls", "serve", "feed",
+                                       "jpeg"],
                     default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
@@ -586,6 +743,14 @@ def main():
         log("JPEG decode on the engine, batch 16 ...")
         out["jpeg"] = bench_jpeg(workdir, graphs=not args.no_graph)
         log(out["jpeg"])
+    if args.only in ("all", "serve", "feed") and not args.no_graph:
+        log("server engine side, 48 feeder threads, native batch worker ...")
+        out["feed"] = bench_feeder(workdir, native=True)
+        log(out["feed"])
+        if args.only == "feed":
+            log("the same with the Python batch loop ...")
+            out["feed_py"] = bench_feeder(workdir, native=False)
+            log(out["feed_py"])
     if args.only in ("all", "serve") and not args.no_graph:
         log("gRPC server, yolo11n, 4 client processes x 16 callers ...")
         out["serve"] = bench_serve(workdir)
@@ -622,9 +787,18 @@ def main():
         line["yolo11n_b1"] = {"ms_per_frame": round(n["ms"], 4), "graph_ms": round(n["graph_ms"], 4),
                               "ms_per_frame_frame_in_hbm": round(n["ms_hbm"], 4),
                               "graph_ms_frame_in_hbm": round(n["graph_ms_hbm"], 4), "kept": n["kept"],
-                              "raw_candidates": n["raw"], "stream_ops_ms": round(n["stream_ops_ms"], 4)}
+                              "raw_candidates": n["raw"], "stream_ops_ms": round(n["stream_ops_ms"], 4),
+                              "units_ms": round(n["units_ms"], 4), "launch_units": n["launches"],
+                              "units": [{"kernel": g["kernel"], "class": g["class"], "launches": g["launches"],
+                                         "us": round(g["ms"] * 1e3, 1)} for g in n["units"][:10]]}
     if x:
-        line["yolo11x_b16"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in x.items()}
+        line["yolo11x_b16"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in x.items()
+                               if k not in ("dominant", "units")}
+        line["yolo11x_b16"]["units"] = [{"kernel": g["kernel"], "class": g["class"], "launches": g["launches"],
+                                         "us": round(g["ms"] * 1e3, 1),
+                                         "tflops": round(g["flops"] / (g["ms"] * 1e-3) / 1e12, 1) if g["flops"] else 0.0}
+                                        for g in x["units"]]
+        line["roofline_yolo11x_b16"] = x["dominant"]
     for key, name in (("m", "yolo11m_b1_1080p_iou07"), ("obb", "yolo11n_obb_b1_1024"), ("seg", "yolo11n_seg_b1")):
         r = out.get(key)
         if r:
@@ -645,6 +819,10 @@ def main():
     if out.get("serve"):
         line["grpc_server_yolo11n"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                        for k, v in out["serve"].items()}
+    if out.get("feed"):
+        line["server_engine_side_yolo11n"] = out["feed"]
+        if out.get("feed_py"):
+            line["server_engine_side_yolo11n_python_loop"] = out["feed_py"]
     pp = prepost_roofline(n, out.get("seg"))
     if pp:
         line["prepost_roofline"] = pp

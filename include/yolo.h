@@ -163,6 +163,58 @@ long long yolo_jpeg_coefficients(const unsigned char* data, size_t size, short* 
 int yolo_get_batch(void* h, int B, YoloDet* out, int cap, int* counts);
 int yolo_get_obb_batch(void* h, int B, YoloObbDet* out, int cap, int* counts);
 
+/* Masks of detections first..first+n-1 of a slot (n * ph * pw bytes, one copy); 0, or -1
+ * on bad arguments.  yolo_get_mask (engine/yolo.h:44-49) for a range. */
+int yolo_get_masks(void* h, int slot, int first, int n, unsigned char* out);
+
+/* The server's batch worker (server/serve.cpp:165-191 batcher, :264-302 worker loop), native:
+ * requests are submitted from any thread; one worker thread collects a model's queue when it
+ * is full or its oldest request would otherwise miss target_ms (slack = target - age -
+ * yolo_exec_ms(max batch) - staging estimate - 1 ms), runs the GPU half of its JPEG decodes
+ * beside the previous batch, reads the previous batch's results, stages (letterboxes) and
+ * launches the batch.  Engines belong to the batcher's thread while it runs: make no other
+ * call on them.  Batches never mix models.
+ * yolo_batcher_submit_jpeg: 0 queued (the engine decodes the stream; its entropy decoding
+ * starts now), 1 not a stream the engine decodes (decode it another way and submit the
+ * pixels), -1 stopped / bad arguments.  yolo_batcher_submit_frame: R, G, B, X pixels in host
+ * memory (pinned for asynchronous copies) that must stay valid until the request's result is
+ * collected (it is returned in `host`); 0 or -1.
+ * yolo_batcher_wait: collects up to cap finished requests (waits up to timeout_ms, < 0 for
+ * ever); returns the count, 0 on timeout, -1 once stopped and every request answered.  Each
+ * result stays valid until yolo_batcher_release.  rows: n records of `stride` floats --
+ * detect / segment (x1, y1, x2, y2, score, cls) in original-image coordinates, OBB (cx, cy,
+ * w, h, angle, score, cls), classify the top-5 (cls, prob); segment also the RLE of each
+ * mask at proto resolution (alternating 0/1 runs starting with a 0-run, row-major;
+ * server/serve.cpp:193-203): rle_len[j] runs of mask j, concatenated in rle, and the
+ * letterbox geometry.  queue_ms: arrival to launch; infer_ms: launch to results.
+ * yolo_batcher_stop: no new requests; queued ones are answered with YOLO_BATCH_STOPPED. */
+#define YOLO_BATCH_OK 0
+#define YOLO_BATCH_DECODE_FAILED 1  /* corrupt stream, or past what one batch decode holds */
+#define YOLO_BATCH_STOPPED 2
+typedef struct {
+  long long tag;
+  int status, model, task, batch;
+  float queue_ms, infer_ms;
+  int n, stride;
+  const float* rows;
+  const unsigned* rle;
+  const int* rle_len;
+  int mask_h, mask_w;
+  float lb_scale;
+  int lb_top, lb_left;
+  const unsigned char* host;   /* the frame passed to yolo_batcher_submit_frame, or NULL */
+  void* owner;
+} YoloBatchResult;
+void* yolo_batcher_create(void* const* engines, const int* max_batch, int n, double target_ms);
+int yolo_batcher_submit_jpeg(void* b, int model, const unsigned char* data, size_t size, long long tag);
+int yolo_batcher_submit_frame(void* b, int model, const unsigned char* rgbx, int height, int width,
+                              long long tag);
+int yolo_batcher_wait(void* b, YoloBatchResult* out, int cap, int timeout_ms);
+void yolo_batcher_release(const YoloBatchResult* r, int n);
+double yolo_batcher_stage_ms(void* b);
+void yolo_batcher_stop(void* b);
+void yolo_batcher_destroy(void* b);
+
 /* Error-returning create: NULL on failure with a message in err (if non-NULL). */
 void* yolo_create_ex(const char* model_dir, int max_batch, int flags, char* err, int errlen);
 /* The reference has no destroy (the handle lives until exit); this frees everything. */
@@ -259,6 +311,10 @@ int yolo_profile_ops(void* h, int B, int iters, float* ms);
  * reported on the unit's first op (0 on the other members, on decode ops and on pooled ops
  * of a fused SPPF chain).  Activations are left in an unspecified state. */
 int yolo_profile_units(void* h, int B, int iters, int reps, float* ms);
+/* The launch unit op k runs in (ops of one unit share a launch; units are numbered in launch
+ * order), -1 for ops no unit launches (decode ops, pooled ops of a fused SPPF chain), -2 for
+ * a bad op index. */
+int yolo_op_unit(void* h, int k);
 /* Average ms of the frame's pre/post stages over `iters` stream-ordered passes of the frame
  * set by yolo_frame_graph (frames in device memory, no H2D): ms[0] letterbox of all slots,
  * ms[1] decode (all levels, one launch), ms[2] NMS, ms[3] mask assembly (0 without a proto).

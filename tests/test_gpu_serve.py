@@ -96,15 +96,17 @@ def _iou(a, b):
     return inter / u if u > 0 else 1.0
 
 
-@pytest.mark.parametrize("frontends", [0, 2])
-def test_server_matches_direct_engine(models, frontends):
+@pytest.mark.parametrize("frontends,native", [(0, True), (2, True), (0, False)],
+                         ids=["native", "native-frontends", "python-loop"])
+def test_server_matches_direct_engine(models, frontends, native):
     dirs = {"det": models("yolo11", "n"), "seg": models("yolo11", "n", "segment"),
             "cls": models("yolo11", "n", "classify", imgsz=224, nc=1000)}
     limits = {"det": 4, "seg": 2, "cls": 3}
     served = [yoloserve.Model(n, yolort.Engine(d, limits[n], FLAGS), limits[n]) for n, d in dirs.items()]
     direct = {n: yolort.Engine(d, 1, FLAGS) for n, d in dirs.items()}
     graphs = {n: graphfile.load(d) for n, d in dirs.items()}
-    srv = yoloserve.Server(served, target_ms=20.0, log=lambda *a: None)
+    srv = yoloserve.Server(served, target_ms=20.0, log=lambda *a: None, native=native)
+    assert (srv.batcher is not None) == native
     gs, port = yoloserve.grpc_server(srv, "127.0.0.1:0", frontends=frontends)
     cl = yoloserve.Client(f"127.0.0.1:{port}")
     try:
@@ -148,6 +150,14 @@ def test_server_matches_direct_engine(models, frontends):
         with pytest.raises(grpc.RpcError) as ei:
             cl.detect(b"\x89PNG\r\n\x1a\nbroken", "det")
         assert ei.value.details() == "image decode failed"
+        # a JPEG whose headers parse but whose entropy-coded data is cut short: the engine's
+        # decoder refuses it, and only that request fails
+        jp = payload[1]
+        with pytest.raises(grpc.RpcError) as ei:
+            cl.detect(jp[:len(jp) // 2], "det")
+        assert ei.value.details() == "image decode failed"
+        assert len(cl.detect(jp, "det").boxes) == len(_direct(direct["det"], graphs["det"],
+                                                              yoloserve.decode_image(jp))["boxes"])
         # a short closed-loop load on the detect model
         stats = yoloserve.bench(f"127.0.0.1:{port}", payload[:8:4], "det", concurrency=16, seconds=2.0)
         print(f"server bench (yolo11n, 16 callers, PNG 480-560x640-704): {stats}", flush=True)

@@ -42,6 +42,7 @@ SOURCES = {
     "jpeg_abi.cpp": HOST_FLAGS,
     "graph.cpp": HOST_FLAGS,
     "engine.cpp": HOST_FLAGS,
+    "batcher.cpp": HOST_FLAGS,
 }
 
 

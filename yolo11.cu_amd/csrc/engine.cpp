@@ -1841,6 +1841,18 @@ int yolo_get_mask(void* h, int slot, int det, unsigned char* out) {
   return hipMemcpy(out, e->masks + ((size_t)slot * yolo::MAX_OUT + det) * sz, sz, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
 }
 
+int yolo_get_masks(void* h, int slot, int first, int n, unsigned char* out) {
+  Engine* e = E(h);
+  if (e->g.protoTen < 0 || slot < 0 || slot >= e->B || first < 0 || n < 1 || first + n > e->h_cnt[slot] || !out)
+    return -1;
+  const yolo::BufDesc& b = e->g.bufs[e->g.tens[e->g.protoTen].buf];
+  const size_t sz = (size_t)b.H * b.W;
+  return hipMemcpy(out, e->masks + ((size_t)slot * yolo::MAX_OUT + first) * sz, sz * n, hipMemcpyDeviceToHost) ==
+                 hipSuccess
+             ? 0
+             : -1;
+}
+
 int yolo_set_thresholds(void* h, float conf, float iou, int max_det) {
   Engine* e = E(h);
   if (max_det < 0 || max_det > yolo::MAX_OUT || !(iou >= 0.f) || !(conf >= 0.f)) return -1;
@@ -2195,6 +2207,16 @@ int yolo_profile_units(void* h, int B, int iters, int reps, float* ms) {
     for (int k = 0; k < n; k++) ms[k] = (float)(acc[k] / iters);
     return 0;
   });
+}
+
+int yolo_op_unit(void* h, int k) {
+  Engine* e = E(h);
+  if (k < 0 || k >= (int)e->ops.size()) return -2;
+  if (yolo::isDecode(e->ops[k].kind) || e->ops[k].chain < 0) return -1;
+  for (int u = 0; u < (int)e->units.size(); u++)
+    for (int j : e->units[u].ops)
+      if (j == k) return u;
+  return -1;
 }
 
 int yolo_profile_stages(void* h, int iters, float* ms) {

@@ -49,6 +49,15 @@ class YoloHeadLevel(C.Structure):
                 ("cls_stride", C.c_int), ("cls_off", C.c_int)]
 
 
+class YoloBatchResult(C.Structure):
+    _fields_ = [("tag", C.c_longlong), ("status", C.c_int), ("model", C.c_int), ("task", C.c_int),
+                ("batch", C.c_int), ("queue_ms", C.c_float), ("infer_ms", C.c_float), ("n", C.c_int),
+                ("stride", C.c_int), ("rows", C.POINTER(C.c_float)), ("rle", C.POINTER(C.c_uint)),
+                ("rle_len", C.POINTER(C.c_int)), ("mask_h", C.c_int), ("mask_w", C.c_int),
+                ("lb_scale", C.c_float), ("lb_top", C.c_int), ("lb_left", C.c_int), ("host", C.c_void_p),
+                ("owner", C.c_void_p)]
+
+
 _SIGS = {
     "yolo_create": (C.c_void_p, [C.c_char_p, C.c_int]),
     "yolo_task": (C.c_int, [C.c_void_p]),
@@ -72,6 +81,16 @@ _SIGS = {
     "yolo_jpeg_release": (None, [C.c_void_p]),
     "yolo_decoder_threads": (C.c_int, []),
     "yolo_jpeg_max_pixels": (C.c_longlong, [C.c_longlong]),
+    "yolo_op_unit": (C.c_int, [C.c_void_p, C.c_int]),
+    "yolo_get_masks": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "yolo_batcher_create": (C.c_void_p, [C.POINTER(C.c_void_p), C.POINTER(C.c_int), C.c_int, C.c_double]),
+    "yolo_batcher_submit_jpeg": (C.c_int, [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t, C.c_longlong]),
+    "yolo_batcher_submit_frame": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_longlong]),
+    "yolo_batcher_wait": (C.c_int, [C.c_void_p, C.POINTER(YoloBatchResult), C.c_int, C.c_int]),
+    "yolo_batcher_release": (None, [C.POINTER(YoloBatchResult), C.c_int]),
+    "yolo_batcher_stage_ms": (C.c_double, [C.c_void_p]),
+    "yolo_batcher_stop": (None, [C.c_void_p]),
+    "yolo_batcher_destroy": (None, [C.c_void_p]),
     "yolo_jpeg_probe": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "yolo_jpeg_coefficients": (C.c_longlong, [C.c_char_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "yolo_get_batch": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(YoloDet), C.c_int, C.POINTER(C.c_int)]),
@@ -222,6 +241,63 @@ def jpeg_coefficients(data: bytes) -> np.ndarray | None:
     if r == -2:
         raise ValueError("corrupt JPEG stream")
     return out
+
+
+class Batcher:
+    """The native batch worker (yolo_batcher_*): a deadline-aware batcher and the per-batch
+    loop on a library thread.  The engines belong to it while it runs."""
+
+    def __init__(self, engines: list, max_batch: list[int], target_ms: float = 50.0):
+        self.lib = load()
+        n = len(engines)
+        hs = (C.c_void_p * n)(*[e.h for e in engines])
+        mb = (C.c_int * n)(*max_batch)
+        self.h = self.lib.yolo_batcher_create(hs, mb, n, float(target_ms))
+        if not self.h:
+            raise RuntimeError("yolo_batcher_create failed")
+        self._buf = (YoloBatchResult * 64)()
+
+    def submit_jpeg(self, model: int, data: bytes, tag: int) -> int:
+        """0 queued, 1 not a stream the engine decodes, -1 stopped."""
+        return self.lib.yolo_batcher_submit_jpeg(self.h, model, data, len(data), tag)
+
+    def submit_frame(self, model: int, ptr: int, height: int, width: int, tag: int) -> int:
+        return self.lib.yolo_batcher_submit_frame(self.h, model, ptr, height, width, tag)
+
+    def wait(self, timeout_ms: int = 100):
+        """Finished requests as dicts (rows copied out of the library), [] on timeout, None
+        once the batcher has stopped and answered everything.  One caller thread only."""
+        n = self.lib.yolo_batcher_wait(self.h, self._buf, len(self._buf), timeout_ms)
+        if n < 0:
+            return None
+        out = []
+        for i in range(n):
+            r = self._buf[i]
+            rows = np.ctypeslib.as_array(r.rows, (r.n * r.stride,)).reshape(r.n, r.stride).copy() \
+                if r.n > 0 else np.zeros((0, max(r.stride, 1)), np.float32)
+            rec = dict(tag=r.tag, status=r.status, model=r.model, task=r.task, batch=r.batch,
+                       queue_ms=r.queue_ms, infer_ms=r.infer_ms, rows=rows, host=r.host or 0)
+            if r.task == 3 and r.status == 0:
+                lens = np.ctypeslib.as_array(r.rle_len, (r.n,)).copy() if r.n > 0 else np.zeros(0, np.int32)
+                runs = np.ctypeslib.as_array(r.rle, (int(lens.sum()),)).copy() if r.n > 0 else np.zeros(0, np.uint32)
+                rec.update(rle_len=lens, rle=runs, mask_hw=(r.mask_h, r.mask_w),
+                           geom=(r.lb_scale, r.lb_top, r.lb_left))
+            out.append(rec)
+        if n:
+            self.lib.yolo_batcher_release(self._buf, n)
+        return out
+
+    def stage_ms(self) -> float:
+        return self.lib.yolo_batcher_stage_ms(self.h)
+
+    def stop(self):
+        if self.h:
+            self.lib.yolo_batcher_stop(self.h)
+
+    def destroy(self):
+        if self.h:
+            self.lib.yolo_batcher_destroy(self.h)
+            self.h = None
 
 
 class PinnedBuffer:
@@ -514,6 +590,10 @@ class Engine:
         if self.lib.yolo_profile_units(self.h, B, iters, reps, out) != 0:
             raise RuntimeError("yolo_profile_units failed")
         return np.array(out, np.float64)
+
+    def op_unit(self, k: int) -> int:
+        """Launch unit of op k (ops of one unit share a launch), -1 if no unit launches it."""
+        return self.lib.yolo_op_unit(self.h, k)
 
     def profile_stages(self, iters: int) -> dict:
         """ms of the frame graph's letterbox, decode, NMS and mask stages (stream-ordered)."""

@@ -357,9 +357,15 @@ class Model:
 
 
 class Server:
-    """Batcher + engine worker.  `submit` (decode + enqueue) is called from any thread."""
+    """Batcher + engine worker.  `submit` (decode + enqueue) is called from any thread.
 
-    def __init__(self, models: list[Model], target_ms: float = 50.0, log=print):
+    With real engines the batcher and the per-batch loop are the library's native batch
+    worker (yolo_batcher_*: collect, decode, fetch the previous batch, stage, launch on a
+    library thread); this object only queues requests into it and turns its finished
+    records into responses on a completion thread.  Engines without the C ABI (test fakes)
+    run the same loop in Python (`_work`)."""
+
+    def __init__(self, models: list[Model], target_ms: float = 50.0, log=print, native: bool = True):
         if not models:
             raise ValueError("no models")
         self.models = models
@@ -375,8 +381,83 @@ class Server:
         self.pool = _PinnedPool() if all(hasattr(m.eng, "stage_frames") for m in models) else None
         self.engine_jpeg = self.pool is not None and all(hasattr(m.eng, "decode_tickets") for m in models)
         self._stop = False
-        self._worker = threading.Thread(target=self._work, name="yoloserve-worker", daemon=True)
+        self.batcher = None
+        if native and self.engine_jpeg:
+            import yolort
+            self.batcher = yolort.Batcher([m.eng for m in models], [m.max_batch for m in models], self.target_ms)
+            self._tags = itertools.count(1)
+            self._pending: dict[int, tuple] = {}
+            self._plock = threading.Lock()
+            self._worker = threading.Thread(target=self._drain, name="yoloserve-completion", daemon=True)
+        else:
+            self._worker = threading.Thread(target=self._work, name="yoloserve-worker", daemon=True)
         self._worker.start()
+
+    # -- the native batch worker
+    def _native_submit(self, r: _Request, mi: int, jpeg: bytes | None = None) -> bool:
+        """Queues r on the native batcher: a JPEG stream the engine decodes (`jpeg`), or the
+        pixels in r.host.  False if the engine does not decode the stream (nothing queued)."""
+        tag = next(self._tags)
+        with self._plock:
+            self._pending[tag] = (r, mi)
+        if jpeg is not None:
+            rc = self.batcher.submit_jpeg(mi, jpeg, tag)
+        else:
+            rc = self.batcher.submit_frame(mi, r.host.ptr, r.hw[0], r.hw[1], tag)
+        if rc == 0:
+            return True
+        with self._plock:
+            self._pending.pop(tag, None)
+        if rc == 1:
+            return False
+        r.error = "server shutting down"
+        r.resp.task = self.models[mi].task_name
+        self._release([r])
+        r.finish()
+        return True
+
+    def _drain(self):
+        """Completion thread: finished records of the native batcher -> responses."""
+        while True:
+            recs = self.batcher.wait(200)
+            if recs is None:
+                break
+            for rec in recs:
+                with self._plock:
+                    r, mi = self._pending.pop(rec["tag"])
+                self._complete(r, self.models[mi], rec)
+            if recs:
+                before = self.served
+                self.served += len(recs)
+                if self.served // 5000 != before // 5000:
+                    self.log(f"[serve] {self.served} imgs, B={recs[-1]['batch']} gpu {recs[-1]['infer_ms']:.2f} ms")
+
+    def _complete(self, r: _Request, m: Model, rec: dict):
+        resp = r.resp
+        resp.task = m.task_name
+        self._release([r])                # the batch has run: its frame buffer is free
+        if rec["status"] != 0:
+            r.error = "image decode failed" if rec["status"] == 1 else "server shutting down"
+            r.finish()
+            return
+        resp.queue_ms = rec["queue_ms"]
+        resp.infer_ms = rec["infer_ms"]
+        resp.batch = rec["batch"]
+        rows = rec["rows"]
+        if m.task == 2:
+            for c, p in rows.tolist():
+                resp.classes.add(id=int(c), prob=float(p))
+        else:
+            r.rows = rows
+            r.obb = m.task == 1
+            if m.task == 3:
+                resp.mask_h, resp.mask_w = rec["mask_hw"]
+                resp.lb_scale, resp.lb_top, resp.lb_left = rec["geom"]
+                runs, at = rec["rle"], 0
+                for n in rec["rle_len"].tolist():
+                    resp.masks.add(rle=runs[at:at + n].tolist())
+                    at += n
+        r.finish()
 
     # -- engine-side steps (device staging is separate so tests can drive a fake engine)
     def _device_buffer(self, slot: int, nbytes: int):
@@ -412,6 +493,9 @@ class Server:
         if not self.engine_jpeg or image[:2] != b"\xff\xd8":
             return None
         mi = self.model_index(model)
+        if self.batcher is not None:
+            r = _Request(on_done)
+            return r if self._native_submit(r, mi, image) else None
         import yolort
         ticket = yolort.jpeg_submit(image)
         if ticket is None:
@@ -440,6 +524,9 @@ class Server:
         return self._queue(r, mi)
 
     def _queue(self, r: _Request, mi: int) -> _Request:
+        if self.batcher is not None:      # decoded pixels (r.host) into the native batcher
+            self._native_submit(r, mi)
+            return r
         with self.cv:
             if self._stop:
                 r.error = "server shutting down"
@@ -473,7 +560,16 @@ class Server:
                         r.error = "unknown model"
                         r.finish()
                         continue
-                    if kind == KIND_JPEG and self.engine_jpeg:
+                    if kind == KIND_JPEG and self.batcher is not None:
+                        if self._native_submit(r, mi, data):
+                            continue
+                        got = decode_rgbx_into(data, self.pool)    # the header check said yes
+                        if got is None:
+                            r.error = "image decode failed"
+                            r.finish()
+                            continue
+                        r.host, r.hw = got
+                    elif kind == KIND_JPEG and self.engine_jpeg:
                         import yolort
                         r.ticket = yolort.jpeg_submit(data)
                         if r.ticket is None:      # the front-end's header check said yes
@@ -694,7 +790,11 @@ class Server:
         with self.cv:
             self._stop = True
             self.cv.notify_all()
+        if self.batcher is not None:
+            self.batcher.stop()           # queued requests are answered; the drain thread ends
         self._worker.join()
+        if self.batcher is not None:
+            self.batcher.destroy()
         for b in self.buffers.values():
             b.free()
         self.buffers.clear()
