@@ -6,9 +6,12 @@
 //   qkv view [B][N][heads * (2kd + hd)], per head [q (kd) | k (kd) | v (hd)]
 //   out[b][n][h*hd + c] = sum_j softmax_j(q_n . k_j * kd^-1/2) * v_j[c]
 //
-// Design: grid (ceil(N/64), heads, B); a block of 4 waves owns 64 queries of one
-// (image, head) and walks the keys in chunks of 64, flash-style, so the N x N score matrix
-// never exists in memory.  Small N (every key fits LDS) stages all keys at once.
+// Design: one block per (image, head, 64-query group); a block of 4 waves owns 64 queries
+// and walks the keys in chunks of 64, flash-style, so the N x N score matrix never exists in
+// memory.  Small N (every key fits LDS) stages all keys at once.  Every query group of an
+// (image, head) reads the same K and V, so the blocks are numbered to put the groups of one
+// (image, head) on one XCD (dispatch is round-robin over the 8 XCDs, each with its own L2):
+// the groups after the first read K and V from that L2 instead of HBM.
 //  * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16 (kd = 32 is
 //    one MFMA K step): each lane then holds 16 scores of ONE query, so the online-softmax
 //    max needs only a 4-lane-group exchange and the running sum stays lane-local.
@@ -43,6 +46,16 @@ constexpr int ATT_WHOLE_MAX = 512;
 constexpr size_t ATT_WHOLE_LDS = 128 * 1024;   // dynamic LDS opt-in set by attentionInit()
 static bool attWholeOk = false;                 // the opt-in succeeded
 
+constexpr int NUM_XCD = 8;
+
+// Linear block b -> work item: the j-th block of XCD class x = b % 8 takes item
+// x * q + min(x, r) + j (q = n / 8, r = n % 8), a bijection on [0, n) that gives each XCD a
+// contiguous range of items.
+__device__ __forceinline__ int xcdItem(int b, int n) {
+  const int x = b % NUM_XCD, j = b / NUM_XCD, q = n / NUM_XCD, r = n % NUM_XCD;
+  return x * q + min(x, r) + j;
+}
+
 template <int HD, bool WHOLE, int KS>
 __global__ __launch_bounds__(256 * KS) void k_attention(View qkv, View y, int N, int heads, float scale_log2) {
   constexpr int KD = 32;
@@ -56,7 +69,10 @@ __global__ __launch_bounds__(256 * KS) void k_attention(View qkv, View y, int N,
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int qw = wave & 3, kp = wave >> 2;   // query group, key part
   const int lr = lane & 15, lg = lane >> 4;
-  const int h = blockIdx.y, img = blockIdx.z;
+  // items are (image, head, query group), query group fastest
+  const int nq = (N + AQ - 1) / AQ, items = (int)gridDim.x;
+  const int item = items >= 2 * NUM_XCD ? xcdItem((int)blockIdx.x, items) : (int)blockIdx.x;
+  const int qgrp = item % nq, h = (item / nq) % heads, img = item / (nq * heads);
   const int per = 2 * KD + HD;
   const int qoff = qkv.o + h * per;
   const size_t imgbase = (size_t)img * N;  // token index base of this image
@@ -84,7 +100,7 @@ __global__ __launch_bounds__(256 * KS) void k_attention(View qkv, View y, int N,
   };
 
   // Q fragment: query lr of this wave, dims 8*lg .. 8*lg+7 (MFMA B operand)
-  const int q = blockIdx.x * AQ + qw * 16 + lr;
+  const int q = qgrp * AQ + qw * 16 + lr;
   f16x8 fq = {0, 0, 0, 0, 0, 0, 0, 0};
   if (q < N) fq = *(const f16x8*)(qkv.p + (imgbase + q) * qkv.s + qoff + 8 * lg);
 
@@ -257,11 +273,12 @@ static size_t attWholeLds(int N, int KS) {
 
 template <int HD>
 static void launchAttn(const View& qkv, const View& y, int N, int heads, float sl2, int Bn, hipStream_t st) {
-  dim3 grid((N + AQ - 1) / AQ, heads, Bn);
+  const int nq = (N + AQ - 1) / AQ;
+  const dim3 grid(nq * heads * Bn);
   // key splits while one image's grid leaves most CUs idle.  Decided per image, not per
   // launch, so an image's result does not depend on the batch it runs in (the splits change
   // the softmax merge order).
-  const long blocks = (long)grid.x * grid.y;
+  const long blocks = (long)nq * heads;
   const int KS = blocks <= 128 ? 4 : blocks <= 512 ? 2 : 1;
   if (attWholeOk && N <= ATT_WHOLE_MAX && attWholeLds<HD>(N, KS) <= ATT_WHOLE_LDS) {
     const size_t lds = attWholeLds<HD>(N, KS);
