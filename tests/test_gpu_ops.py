@@ -512,6 +512,13 @@ def test_conv_1x1_resident(tmp_path, H, W, Cin, Cout, B, res, act):
     rel = post.rel_err(got, ref.view(ops[0].out))
     print(f"1x1 {H}x{W} {Cin}->{Cout} b{B} res={res} act={act}: rel {rel:.2e}", flush=True)
     assert rel <= TOL
+    # the two-groups-in-flight variant (16-byte stores for even fragment counts) runs the
+    # same MFMA chain per output: identical bits
+    eng.set_op_config(0, yolort.CFG_1X1S)
+    assert eng.op_config(0) == yolort.CFG_1X1S
+    eng.write(ops[0].out, np.zeros((B,) + eng.tensor_shape(ops[0].out), np.float16))
+    eng.run_op(0, B)
+    np.testing.assert_array_equal(eng.read(ops[0].out, B).view(np.uint16), got.astype(np.float16).view(np.uint16))
     eng.close()
 
 
@@ -522,8 +529,9 @@ def test_conv_1x1_resident_rejects(tmp_path):
         d = str(tmp_path / f"r{i}")
         modelgen.write_single_conv(d, 16, 16, cin, cout, k, s, seed=1)
         eng = yolort.Engine(d, 1, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
-        with pytest.raises(ValueError):
-            eng.set_op_config(0, yolort.CFG_1X1)
+        for cfg in (yolort.CFG_1X1, yolort.CFG_1X1S):
+            with pytest.raises(ValueError):
+                eng.set_op_config(0, cfg)
         eng.close()
 
 

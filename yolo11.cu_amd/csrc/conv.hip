@@ -617,7 +617,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv_gemm(const GemmLaunch L) 
   X(33, 64, 192, 2, 2, 32, 4)        \
   X(34, 128, 96, 2, 2, 64, 2)        \
   X(35, 256, 96, 4, 1, 64, 2)        \
-  X(36, 64, 96, 2, 2, 64, 3)
+  X(36, 64, 96, 2, 2, 64, 3)          \
+  X(37, 128, 384, 2, 4, 32, 3)       \
+  X(38, 128, 384, 2, 4, 64, 2)       \
+  X(39, 256, 192, 4, 2, 64, 2)
 
 static const TileCfg kTiles[] = {
 #define X(i, bm, bn, wm, wn, bk, ns) {bm, bn, wm, wn, bk, ns},
@@ -1389,6 +1392,163 @@ void launchConv1x1(const View& x, const View& y, const View* res, const f16* w, 
 #undef P1_CASE
 }
 
+// The same weights-resident 1x1 conv with PD groups of pixel fragments in flight per wave
+// (a memory-bound stream needs more than one group of loads outstanding per wave to cover
+// HBM latency), and, for an even fragment count, 16-byte stores: the weight rows of every
+// 32-channel slice are loaded in the order chperm() gives, so fragments (2p, 2p+1) leave a
+// lane with 8 consecutive output channels of its pixel.  Each output is the same MFMA chain
+// as the one-group kernel's (same K order), so results are identical to it.
+template <int KC, int FN, int PD>
+__global__ __launch_bounds__(256) void k_conv1x1_stream(View x, View y, View r, const f16* __restrict__ w,
+                                                        const float* __restrict__ bias, int act, int M) {
+  constexpr int CP = 32 * KC + 8;
+  constexpr int NO = 16 * FN;
+  constexpr int VPO = 4 * KC;
+  constexpr bool PAIR = FN % 2 == 0;
+  __shared__ __attribute__((aligned(16))) f16 wl[NO * CP];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int Cin = x.C, Cout = y.C, o0 = blockIdx.y * NO;
+
+  for (int e = t; e < NO * VPO; e += 256) {
+    const int v = e % VPO, o = e / VPO, c0 = 8 * v;
+    const int oc = o0 + (PAIR ? chperm(o) : o);
+    f16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (oc < Cout && c0 < Cin) val = *(const f16x8*)(w + (size_t)oc * Cin + c0);
+    *(f16x8*)&wl[o * CP + c0] = val;
+  }
+  // lane channels: pair p -> o0 + 32p + 8lg .. +7; unpaired fragment f -> o0 + 16f + 4lg .. +3
+  float bb[FN][4];
+#pragma unroll
+  for (int f = 0; f < FN; f++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int c = PAIR ? o0 + 32 * (f / 2) + 8 * lg + 4 * (f % 2) + e : o0 + f * 16 + 4 * lg + e;
+      bb[f][e] = c < Cout ? bias[c] : 0.f;
+    }
+  __syncthreads();
+
+  const int groups = (M + 15) / 16;
+  const int step = gridDim.x * 4;
+  auto fetch = [&](int gi, f16x8* dst) {
+    const int m = gi * 16 + lr;
+    const bool live = m < M;
+    const f16* px = x.p + (size_t)(live ? m : 0) * x.s + x.o;
+#pragma unroll
+    for (int kc = 0; kc < KC; kc++) {
+      const int c0 = kc * 32 + 8 * lg;
+      f16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (live && c0 < Cin) val = *(const f16x8*)(px + c0);
+      dst[kc] = val;
+    }
+  };
+  int gi = blockIdx.x * 4 + wave;
+  f16x8 buf[PD + 1][KC];
+#pragma unroll
+  for (int d = 0; d < PD; d++) fetch(gi + d * step, buf[d]);
+  for (; gi < groups; gi += (PD + 1) * step) {
+#pragma unroll
+    for (int u = 0; u <= PD; u++) {   // unrolled so every buffer index is static
+      const int g = gi + u * step;
+      if (g >= groups) break;
+      fetch(g + PD * step, buf[(u + PD) % (PD + 1)]);
+      const f16x8* cur = buf[u];
+      f32x4 acc[FN];
+#pragma unroll
+      for (int f = 0; f < FN; f++) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < KC; kc++)
+#pragma unroll
+        for (int f = 0; f < FN; f++) {
+          const f16x8 wf = *(const f16x8*)&wl[(f * 16 + lr) * CP + kc * 32 + 8 * lg];
+          acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, cur[kc], acc[f], 0, 0, 0);
+        }
+      const int m = g * 16 + lr;
+      if (m >= M) continue;
+      if constexpr (PAIR) {
+#pragma unroll
+        for (int p = 0; p < FN / 2; p++) {
+          const int c = o0 + 32 * p + 8 * lg;
+          if (c >= Cout) continue;   // Cout % 16 == 0 and slices of 32: all 8 valid or none
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            v[e] = acc[2 * p][e] + bb[2 * p][e];
+            v[4 + e] = acc[2 * p + 1][e] + bb[2 * p + 1][e];
+          }
+          if (act == 1) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = silu(v[e]);
+          }
+          if (r.p) {
+            const f16x8 rv = *(const f16x8*)(r.p + (size_t)m * r.s + r.o + c);
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] += (float)rv[e];
+          }
+          f16x8 o;
+#pragma unroll
+          for (int e = 0; e < 8; e++) o[e] = (f16)v[e];
+          *(f16x8*)(y.p + (size_t)m * y.s + y.o + c) = o;
+        }
+      } else {
+#pragma unroll
+        for (int f = 0; f < FN; f++) {
+          const int c = o0 + f * 16 + 4 * lg;
+          if (c >= Cout) continue;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            v[e] = acc[f][e] + bb[f][e];
+            if (act == 1) v[e] = silu(v[e]);
+          }
+          if (r.p) {
+            const f16x4 rv = *(const f16x4*)(r.p + (size_t)m * r.s + r.o + c);
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] += (float)rv[e];
+          }
+          const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+          *(f16x4*)(y.p + (size_t)m * y.s + y.o + c) = o;
+        }
+      }
+    }
+  }
+}
+
+// The two-groups-in-flight variant (op config CFG_1X1S): same instantiations and slices as
+// the resident kernel; 16-byte stores need the view strides and offsets 8-aligned.
+bool conv1x1StreamOk(const View& x, const View& y, const View* r, int k, int s, int p) {
+  if (!conv1x1Ok(x, y, r, k, s, p)) return false;
+  const int fn = conv1x1FN(y.C, conv1x1KC(x.C));
+  if (fn % 2 == 0 && (y.s % 8 || y.o % 8 || (r && (r->s % 8 || r->o % 8)))) return false;
+  return true;
+}
+
+void launchConv1x1Stream(const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
+                         int Bn, hipStream_t st) {
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 256;
+    return n;
+  }();
+  const View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
+  const int M = Bn * y.H * y.W, kc = conv1x1KC(x.C), fn = conv1x1FN(y.C, kc);
+  const int slices = (y.C + 16 * fn - 1) / (16 * fn);
+  const int groups = (M + 15) / 16;
+  int gx = std::max(1, 4 * cus / slices);
+  gx = std::min(gx, (groups + 3) / 4);
+  const dim3 grid(gx, slices);
+#define P2_CASE(KC, FN) \
+  if (kc == KC && fn == FN) { k_conv1x1_stream<KC, FN, 2><<<grid, 256, 0, st>>>(x, y, r, w, bias, act, M); return; }
+#define P2_ROW(KC) P2_CASE(KC, 1) P2_CASE(KC, 2) P2_CASE(KC, 3) P2_CASE(KC, 4) P2_CASE(KC, 6) P2_CASE(KC, 8)
+  P2_ROW(1) P2_ROW(2) P2_ROW(3) P2_ROW(4) P2_ROW(6) P2_ROW(8)
+  P2_CASE(12, 1) P2_CASE(12, 2) P2_CASE(12, 3) P2_CASE(12, 4)
+#undef P2_ROW
+#undef P2_CASE
+}
+
 // ------------------------------------------------------------------ streaming conv (3x3 halo-staged, 1x1)
 // 3x3 stride-1 convs with mid-size channel counts (the C3k bottleneck convs of the larger
 // models: 48-256 channels at 20-160 pixels), and 1x1 stride-1 convs (KS = 1: no halo, one tap,
@@ -1815,6 +1975,7 @@ void launchConvTap(int v, const View& x, const View& y, const View* res, const f
 bool specialConvOk(int cfg, const View& x, const View& y, const View* r, int k, int s, int p) {
   if (cfg == CFG_HALO) return convHaloOk(x, y, r, k, s, p);
   if (cfg == CFG_1X1) return conv1x1Ok(x, y, r, k, s, p);
+  if (cfg == CFG_1X1S) return conv1x1StreamOk(x, y, r, k, s, p);
   return convTapOk(cfg - CFG_TAP, x, y, r, k, s, p);
 }
 
@@ -1822,6 +1983,7 @@ void launchSpecialConv(int cfg, const View& x, const View& y, const View* res, c
                        int act, int Bn, hipStream_t st) {
   if (cfg == CFG_HALO) launchConvHalo(x, y, res, w, bias, act, Bn, st);
   else if (cfg == CFG_1X1) launchConv1x1(x, y, res, w, bias, act, Bn, st);
+  else if (cfg == CFG_1X1S) launchConv1x1Stream(x, y, res, w, bias, act, Bn, st);
   else launchConvTap(cfg - CFG_TAP, x, y, res, w, bias, act, Bn, st);
 }
 

@@ -849,7 +849,7 @@ struct Engine {
     // special kernels (halo 1000, resident 1x1 1001, halo-staged 3x3 variants 1100+) take part
     // unless YOLO_TUNE_TILES is set without their entries
     std::vector<char> allowed(numTileConfigs(), 1);
-    std::vector<int> specials = {CFG_HALO, CFG_1X1};
+    std::vector<int> specials = {CFG_HALO, CFG_1X1, CFG_1X1S};
     for (int v = 0; v < numTapTiles(); v++) specials.push_back(CFG_TAP + v);
     if (const char* lim = getenv("YOLO_TUNE_TILES")) {
       std::fill(allowed.begin(), allowed.end(), 0);

@@ -202,6 +202,12 @@ constexpr int CFG_1X1 = 1001;
 bool conv1x1Ok(const View& x, const View& y, const View* r, int k, int s, int p);
 void launchConv1x1(const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
                    int Bn, hipStream_t st);
+// The same with two pixel groups of loads in flight per wave and 16-byte stores (identical
+// results), selected by the op config CFG_1X1S.
+constexpr int CFG_1X1S = 1002;
+bool conv1x1StreamOk(const View& x, const View& y, const View* r, int k, int s, int p);
+void launchConv1x1Stream(const View& x, const View& y, const View* res, const f16* w, const float* bias,
+                         int act, int Bn, hipStream_t st);
 // The persistent streaming conv, tile variant v in [0, numTapTiles()): 3x3 stride-1 variants
 // (a stage is one 32-channel block of the tile's input halo for all 9 taps) and 1x1 stride-1
 // variants, all for Cin % 8 == 0 and Cout % 16 == 0; autotune candidates selected by the op
@@ -213,7 +219,7 @@ void launchConvTap(int v, const View& x, const View& y, const View* res, const f
                    int Bn, hipStream_t st);
 // Op configs that select a kernel other than a GEMM tile (no split-K, no grouped launches).
 inline bool specialConvCfg(int cfg) {
-  return cfg == CFG_HALO || cfg == CFG_1X1 || (cfg >= CFG_TAP && cfg < CFG_TAP + numTapTiles());
+  return cfg == CFG_HALO || cfg == CFG_1X1 || cfg == CFG_1X1S || (cfg >= CFG_TAP && cfg < CFG_TAP + numTapTiles());
 }
 // Whether special config `cfg` applies to a conv, and its launch.
 bool specialConvOk(int cfg, const View& x, const View& y, const View* r, int k, int s, int p);

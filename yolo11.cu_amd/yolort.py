@@ -23,6 +23,7 @@ PIXEL_BGR, PIXEL_RGBX = 0, 1   # frame layouts of yolo_stage_frames (B,G,R / R,G
 JPEG_STAGED, JPEG_UNSUPPORTED, JPEG_INVALID = 0, 1, 2   # yolo_stage_jpeg per-stream status
 CFG_HALO = 1000   # op config of the LDS-halo 3x3 kernel (small-channel stride-1 convs)
 CFG_1X1 = 1001    # op config of the weights-resident 1x1 kernel (stride 1, Cin <= 384)
+CFG_1X1S = 1002   # the same with two pixel groups in flight per wave and 16-byte stores
 CFG_TAP = 1100    # op configs 1100 .. 1100 + NUM_TAP_TILES - 1: streaming-conv tile variants
 NUM_TAP_TILES = 13
 TAP_3X3 = range(0, 8)    # variants for 3x3 stride-1 convs (halo-staged)
