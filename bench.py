@@ -45,6 +45,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "yolo11.cu_amd"))
 sys.path.insert(0, ROOT)
 
+from unitwork import conv_kernel_name, unit_table  # noqa: E402  (the package dir is on sys.path)
+
 PEAK_FP16 = 2.5e15        # MI355X dense fp16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12         # MI355X HBM3E, B/s
 
@@ -68,92 +70,25 @@ def measured_traffic(cfg, tail=-1):
         return None
 
 
-def measured_x_traffic(ops):
-    """HBM bytes per batch of the given yolo11x b16 conv ops (FETCH_SIZE + WRITE_SIZE of their
-    dispatches in the committed PMC passes, each scaled by a plain copy of known size), or
-    None where a pass has no figure for one of them (tile choices differ from that run's)."""
+def measured_x_traffic(firsts, kernel):
+    """HBM bytes per batch of the yolo11x b16 launch units whose first ops are `firsts`
+    (FETCH_SIZE + WRITE_SIZE of their dispatches in the committed PMC passes of traffic.py,
+    each scaled by a plain copy of known size), or None where the passes have no figure for
+    one of them with the same kernel (a tile choice that differs from that run's)."""
     path = os.path.join(ROOT, "profiles", "yolo11x_b16_traffic.json")
     try:
-        rec = json.load(open(path))["per_op"]
-        return int(sum(rec[str(k)]["traffic_bytes"] for k in ops))
+        rec = json.load(open(path))["per_unit_first_op"]
+        if any(rec[str(k)]["kernel"] != kernel for k in firsts):
+            return None
+        return int(sum(rec[str(k)]["traffic_bytes"] for k in firsts))
     except (OSError, ValueError, KeyError):
         return None
-
-
-def conv_kernel_name(cfg, tail=-1):
-    """The kernel an op config selects (yolo_set_op_config's numbering), with its tail retile."""
-    if cfg == 1000:
-        return "k_conv3x3_halo"
-    if cfg == 1001:
-        return "k_conv1x1_resident"
-    if cfg >= 1100:
-        return f"k_conv_tap variant {cfg - 1100}"
-    if tail >= 0:
-        return f"k_conv_gemm cfg {cfg}, last-wave rows under cfg {tail} (two dispatches)"
-    return f"k_conv_gemm cfg {cfg}"
 
 
 def conv_flops(eng, k):
     info = eng.op_info(k)
     H, W, _ = eng.tensor_shape(info["out"])
     return 2.0 * H * W * info["Cout"] * info["k"] * info["k"] * info["Cin"] / max(info["g"], 1)
-
-
-def conv_work(eng, k, B):
-    """Algorithmic FLOPs and HBM bytes of conv op k at batch B: 2*B*Ho*Wo*Cout*k^2*Cin/g FLOPs;
-    input + weights + output (+ residual) in fp16 plus the fp32 bias."""
-    info = eng.op_info(k)
-    Ho, Wo, _ = eng.tensor_shape(info["out"])
-    Hi, Wi, _ = eng.tensor_shape(info["a"])
-    g = max(info["g"], 1)
-    kk = info["k"] * info["k"]
-    flops = 2.0 * B * Ho * Wo * info["Cout"] * kk * info["Cin"] / g
-    out_px = B * Ho * Wo * info["Cout"]
-    nbytes = 2.0 * (B * Hi * Wi * info["Cin"] + info["Cout"] * kk * info["Cin"] / g + out_px
-                    + (out_px if info["b"] >= 0 else 0)) + 4.0 * info["Cout"]
-    return flops, nbytes
-
-
-def unit_kernel(eng, k):
-    """Kernel name and shape class of the launch unit whose first op is k."""
-    info = eng.op_info(k)
-    if info["kind"] != "CONV":
-        return {"ATTN": "k_attention", "MAXPOOL5": "k_sppf_pool / k_maxpool5", "UPSAMPLE2": "k_upsample2",
-                "COPYC": "k_copyc", "ADD": "k_add", "PS2": "k_ps2", "GAP": "k_gap",
-                "SOFTMAX": "k_softmax_ch"}.get(info["kind"], info["kind"]), ""
-    if info["Cin"] == 3:
-        return "k_conv_first", "stem 3x3 s2"
-    if info["g"] > 1:
-        return "k_dwconv", "depthwise 3x3"
-    cls = "1x1" if info["k"] == 1 else f"{info['k']}x{info['k']} s{info['s']}"
-    return conv_kernel_name(eng.op_config(k), eng.op_tail(k)), cls
-
-
-def unit_table(eng, B, per_unit):
-    """Per-unit kernel time (hipEvents, units repeated back to back) grouped by kernel and
-    shape class, with the algorithmic FLOPs and bytes of the ops each unit launches."""
-    groups = {}
-    unit = [eng.op_unit(k) for k in range(eng.num_ops)]
-    first_of = {}
-    for k, u in enumerate(unit):
-        if u >= 0:
-            first_of.setdefault(u, k)
-    for k, u in enumerate(unit):
-        if u < 0:
-            continue
-        first = first_of[u]
-        name, cls = unit_kernel(eng, first)
-        g = groups.setdefault((name, cls), {"kernel": name, "class": cls, "launches": 0, "ms": 0.0,
-                                            "flops": 0.0, "bytes": 0.0, "ops": []})
-        if k == first:
-            g["launches"] += 1
-            g["ms"] += float(per_unit[k])
-        if eng.op_info(k)["kind"] == "CONV":
-            f, b = conv_work(eng, k, B)
-            g["flops"] += f
-            g["bytes"] += b
-        g["ops"].append(k)
-    return sorted(groups.values(), key=lambda g: -g["ms"])
 
 
 def group_roofline(g, traffic=None):
@@ -430,8 +365,8 @@ def bench_x(workdir, iters, graph=True):
             attn_t += per_unit[k] * 1e-3
             attn_f += B * attn_flops(eng, k)
     units = unit_table(eng, B, per_unit)
-    top = next(g for g in units if g["flops"] > 0)      # the conv kernel group with the most time
-    traffic = measured_x_traffic(top["ops"])
+    top = next(g for g in units if g["class"])          # the conv kernel group with the most time
+    traffic = measured_x_traffic(top["firsts"], top["kernel"])
     for b in devs:
         b.free()
     eng.close()

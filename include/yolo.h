@@ -315,6 +315,13 @@ int yolo_profile_units(void* h, int B, int iters, int reps, float* ms);
  * order), -1 for ops no unit launches (decode ops, pooled ops of a fused SPPF chain), -2 for
  * a bad op index. */
 int yolo_op_unit(void* h, int k);
+/* Launch units of the handle, and one unit u at batch B on the engine stream, asynchronously
+ * (0; -1 on bad arguments; units of decode ops launch nothing).  yolo_marker queues an empty
+ * one-wave kernel (k_marker) on the engine stream: a profiler sees it as a separator, so a
+ * trace of marker, unit, marker, unit, ... attributes every dispatch to its unit. */
+int yolo_num_units(void* h);
+int yolo_run_unit(void* h, int u, int B);
+int yolo_marker(void* h);
 /* Average ms of the frame's pre/post stages over `iters` stream-ordered passes of the frame
  * set by yolo_frame_graph (frames in device memory, no H2D): ms[0] letterbox of all slots,
  * ms[1] decode (all levels, one launch), ms[2] NMS, ms[3] mask assembly (0 without a proto).

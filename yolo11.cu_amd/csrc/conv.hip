@@ -2014,6 +2014,13 @@ __device__ __forceinline__ const DwProblem& dwProblem(const DwLaunch& L) {
     if (q < L.n && (int)blockIdx.x >= L.p[q].blk0) pj = q;
   return L.p[__builtin_amdgcn_readfirstlane(pj)];
 }
+// The block's index within its problem, numbered so each XCD takes a contiguous range: the
+// blocks of neighbouring output rows, which read the same input rows (3x3 window), then share
+// one L2 instead of each XCD fetching those rows again.
+__device__ __forceinline__ int dwBlock(const DwProblem& P) {
+  const int b = (int)blockIdx.x - P.blk0, nb = (P.total + 255) / 256;
+  return nb >= 2 * NUM_XCD ? xcdRange(b, nb) : b;
+}
 
 __global__ __launch_bounds__(256) void k_dwconv(const DwLaunch L) {
   const DwProblem& P = dwProblem(L);
@@ -2021,7 +2028,7 @@ __global__ __launch_bounds__(256) void k_dwconv(const DwLaunch L) {
   const f16* __restrict__ w = P.w;
   const float* __restrict__ bias = P.bias;
   const int ksz = P.ksz, cs = P.cs, cp = P.cp, act = P.act, total = P.total;
-  const int idx = ((int)blockIdx.x - P.blk0) * blockDim.x + threadIdx.x;
+  const int idx = dwBlock(P) * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   const int cg = y.C >> 3;
   const int g = idx % cg, m = idx / cg;
@@ -2088,7 +2095,7 @@ __global__ __launch_bounds__(256) void k_dwconv3x4(const DwLaunch L) {
   const f16* __restrict__ w = P.w;
   const float* __restrict__ bias = P.bias;
   const int cp = P.cp, act = P.act, total = P.total;
-  const int idx = ((int)blockIdx.x - P.blk0) * blockDim.x + threadIdx.x;
+  const int idx = dwBlock(P) * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   const int cg = y.C >> 3, xq = (y.W + DWPX - 1) / DWPX;
   const int g = idx % cg;

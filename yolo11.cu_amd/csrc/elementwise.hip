@@ -199,6 +199,10 @@ void launchCopyCGroup(const View* xs, const View* ys, int n, int Bn, hipStream_t
   k_copyc<<<blocks, 256, 0, st>>>(L);
 }
 void launchCopyC(const View& x, const View& y, int Bn, hipStream_t st) { launchCopyCGroup(&x, &y, 1, Bn, st); }
+// An empty one-wave kernel: a dispatch that separates launch units in profiler traces.
+__global__ void k_marker() {}
+void launchMarker(hipStream_t st) { k_marker<<<1, 64, 0, st>>>(); }
+
 void launchPS2(const View& x, const View& y, int Bn, hipStream_t st) {
   int total = Bn * y.H * y.W * (y.C / 8);
   k_ps2<<<grid(total), 256, 0, st>>>(x, y, total);

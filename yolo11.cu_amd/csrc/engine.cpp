@@ -2209,6 +2209,28 @@ int yolo_profile_units(void* h, int B, int iters, int reps, float* ms) {
   });
 }
 
+int yolo_num_units(void* h) { return (int)E(h)->units.size(); }
+
+int yolo_run_unit(void* h, int u, int B) {
+  return guarded([&] {
+    Engine* e = E(h);
+    if (u < 0 || u >= (int)e->units.size() || B < 1 || B > e->B) return -1;
+    const int k0 = e->units[u].ops[0];
+    if (yolo::isDecode(e->ops[k0].kind) || e->ops[k0].chain < 0) return 0;   // launched elsewhere
+    e->runUnit(e->units[u], B);
+    HCK(hipGetLastError());
+    return 0;
+  });
+}
+
+int yolo_marker(void* h) {
+  return guarded([&] {
+    yolo::launchMarker(E(h)->st);
+    HCK(hipGetLastError());
+    return 0;
+  });
+}
+
 int yolo_op_unit(void* h, int k) {
   Engine* e = E(h);
   if (k < 0 || k >= (int)e->ops.size()) return -2;

@@ -245,6 +245,7 @@ void launchSppfPool(const View& x, const View& y1, const View& y2, const View& y
                     hipStream_t st);
 void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st);
 void launchCopyC(const View& x, const View& y, int Bn, hipStream_t st);
+void launchMarker(hipStream_t st);
 // n independent channel copies in one launch
 constexpr int COPY_GROUP = 8;
 void launchCopyCGroup(const View* xs, const View* ys, int n, int Bn, hipStream_t st);

@@ -1,0 +1,225 @@
+"""HBM traffic per launch unit of a whole frame, from rocprofv3 PMC passes.
+
+    OUT=gpurun_out/traffic_x
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/fetch -o run -- \\
+        python3 yolo11.cu_amd/traffic.py collect --scale x --batch 16 --plan $OUT/plan.json
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/write -o run -- \\
+        python3 yolo11.cu_amd/traffic.py collect --scale x --batch 16 --plan $OUT/wplan.json \\
+        --replay $OUT/plan.json
+    python3 yolo11.cu_amd/traffic.py summarize --plan $OUT/plan.json --write-plan $OUT/wplan.json \\
+        --fetch $OUT/fetch --write $OUT/write --json profiles/yolo11x_b16_traffic.json \\
+        --md profiles/yolo11x_b16_traffic.md
+
+`collect` builds the engine as the benchmark does (seeded model, autotuned tiles), stages the
+benchmark's frames, and runs every launch unit of the frame between two marker kernels
+(yolo_marker), `--passes` times, so each dispatch in the trace belongs to the unit between its
+markers; then a plain copy of known size, the scale reference: FETCH_SIZE and WRITE_SIZE are
+scaled by the known bytes of that copy over what the counters read for it.  `summarize` maps
+the dispatches to units, takes the median over the passes, pairs the two runs' units with
+the same ops and kernel, and writes the per-unit traffic beside each unit's algorithmic bytes
+(unitwork.py) as JSON and as a markdown table.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import os
+import statistics
+import sys
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+COPY_HWC = (160, 160, 384)   # the scale reference: a copy of B x 160 x 160 x 384 fp16
+
+
+def collect(args):
+    import modelgen
+    import unitwork
+    import yolort
+    B = args.batch
+    work = tempfile.mkdtemp(prefix="yolo_traffic_")
+    d = os.path.join(work, "model")
+    modelgen.write_model(d, "yolo11", args.scale, cls_bias=-8.0)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOGRAPH)
+    frames = [modelgen.synth_frame(640, 640, 50, 100 + i) for i in range(B)]
+    devs = []
+    for s, f in enumerate(frames):
+        b = yolort.DeviceBuffer(f.nbytes)
+        eng.upload(b, f)
+        eng.preprocess(b.ptr, 640, 640, s)
+        devs.append(b)
+    # a second counter's run (--replay: the first run's plan) takes the first run's kernel
+    # choices, since the autotuner times candidates and could pick differently; launch units
+    # are planned with timing too, so each run records its own and summarize pairs them
+    if args.replay:
+        prev = json.load(open(args.replay))
+        for k, (cfg, tail, split) in prev["op_configs"].items():
+            k = int(k)
+            if cfg < 0:                      # stem and depthwise convs: no choice to replay
+                continue
+            if eng.op_config(k) != cfg:
+                eng.set_op_config(k, cfg)
+            if cfg >= 1000:                  # special kernels: no split, no tail
+                continue
+            if split != eng.op_split(k):
+                eng.set_op_split(k, split)
+            if tail != eng.op_tail(k):
+                eng.set_op_tail(k, tail)
+    plan = {"model": f"yolo11{args.scale}", "batch": B, "passes": args.passes,
+            "units": unitwork.units(eng, B), "copy_bytes": 2.0 * B * COPY_HWC[0] * COPY_HWC[1] * COPY_HWC[2],
+            "op_configs": {str(k): (eng.op_config(k), eng.op_tail(k), eng.op_split(k))
+                           for k in range(eng.num_ops) if eng.op_info(k)["kind"] == "CONV"}}
+    plan["num_units"] = eng.num_units()
+    for _ in range(args.passes):
+        for u in range(plan["num_units"]):
+            eng.marker()
+            eng.run_unit(u, B)
+            eng.marker()
+    eng.sync()
+    dc = os.path.join(work, "copy")
+    modelgen.write_copy(dc, *COPY_HWC)
+    ec = yolort.Engine(dc, B, yolort.YOLO_NOGRAPH | yolort.YOLO_NOTUNE)
+    ec.marker()
+    ec.run_unit(0, B)
+    ec.marker()
+    ec.sync()
+    json.dump(plan, open(args.plan, "w"))
+    for b in devs:
+        b.free()
+    ec.close()
+    eng.close()
+    print(f"collected {args.passes} passes of {plan['num_units']} units", flush=True)
+
+
+def _segments(path: str, counter: str) -> list[list[tuple[str, float]]]:
+    """Dispatches between marker pairs, in dispatch order: [[(kernel, value), ...], ...]."""
+    f = path if path.endswith(".csv") else glob.glob(os.path.join(path, "*counter_collection.csv"))[0]
+    per = {}
+    for r in csv.DictReader(open(f)):
+        if r["Counter_Name"] != counter:
+            continue
+        k = int(r["Dispatch_Id"])
+        name, v = per.get(k, (r["Kernel_Name"], 0.0))
+        per[k] = (name, v + float(r["Counter_Value"]))
+    segs, cur = [], None
+    for k in sorted(per):
+        name, v = per[k]
+        if "k_marker" in name:
+            if cur is None:
+                cur = []
+            else:
+                segs.append(cur)
+                cur = None
+        elif cur is not None:
+            cur.append((name, v * 1024.0))     # the counters read KiB
+    return segs
+
+
+def _per_unit(plan: dict, path: str, counter: str) -> tuple[float, dict]:
+    """(scale, {op tuple: (bytes per pass (median, scaled), kernel, unit record)}) of one run."""
+    nu, passes = plan["num_units"], plan["passes"]
+    segs = _segments(path, counter)
+    if len(segs) != nu * passes + 1:
+        raise SystemExit(f"{counter}: {len(segs)} marker segments, expected {nu * passes + 1}")
+    scale = plan["copy_bytes"] / sum(v for _, v in segs[-1])   # the copy reads and writes copy_bytes
+    out = {}
+    for info in plan["units"]:
+        u = info["unit"]
+        vals = [sum(v for _, v in segs[p * nu + u]) for p in range(passes)]
+        kernels = sorted({n.split("(")[0] for p in range(passes) for n, _ in segs[p * nu + u]})
+        out[tuple(info["ops"])] = (statistics.median(vals) * scale, kernels, info)
+    return scale, out
+
+
+def summarize(args):
+    fplan, wplan = json.load(open(args.plan)), json.load(open(args.write_plan or args.plan))
+    fscale, fet = _per_unit(fplan, args.fetch, "FETCH_SIZE")
+    wscale, wri = _per_unit(wplan, args.write, "WRITE_SIZE")
+    rows, total_t, total_a, unpaired = [], 0.0, 0.0, []
+    for ops, (fb, kern, info) in fet.items():
+        if ops not in wri or wri[ops][2]["kernel"] != info["kernel"]:
+            unpaired.append(info["first"])
+            continue
+        wb = wri[ops][0]
+        t = fb + wb
+        total_t += t
+        total_a += info["bytes"]
+        rows.append({"unit": info["unit"], "first_op": info["first"], "ops": info["ops"], "kernel": info["kernel"],
+                     "class": info["class"], "dispatched": kern, "fetch_bytes": int(fb), "write_bytes": int(wb),
+                     "traffic_bytes": int(t), "algorithmic_bytes": int(info["bytes"]),
+                     "ratio": round(t / info["bytes"], 3) if info["bytes"] else None})
+    out = {"model": fplan["model"], "batch": fplan["batch"], "passes": fplan["passes"],
+           "scale": {"FETCH_SIZE": round(fscale, 4), "WRITE_SIZE": round(wscale, 4),
+                     "reference": f"copy of {int(fplan['copy_bytes'])} bytes read + written"},
+           "total_traffic_bytes": int(total_t), "total_algorithmic_bytes": int(total_a),
+           "unpaired_first_ops": unpaired,
+           "per_unit": rows, "per_unit_first_op": {str(r["first_op"]): {"traffic_bytes": r["traffic_bytes"],
+                                                                         "kernel": r["kernel"]} for r in rows}}
+    json.dump(out, open(args.json, "w"), indent=1)
+    if args.md:
+        _markdown(out, args)
+
+
+def _markdown(out, args):
+    classes = {}
+    for r in out["per_unit"]:
+        c = classes.setdefault(r["class"] or r["kernel"], [0, 0, 0])
+        c[0] += 1
+        c[1] += r["traffic_bytes"]
+        c[2] += r["algorithmic_bytes"]
+    lines = [f"# HBM traffic per launch unit: {out['model']} detect, batch {out['batch']}", "",
+             "Two `rocprofv3 --pmc` passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) over every launch",
+             "unit of the frame, each unit between two marker kernels; median over "
+             f"{out['passes']} passes.  Each counter is scaled by what it reads for a plain copy of known size",
+             f"in the same run (FETCH_SIZE x {out['scale']['FETCH_SIZE']}, WRITE_SIZE x {out['scale']['WRITE_SIZE']}).",
+             "Algorithmic bytes: input + weights + output (+ residual) per conv, inputs + outputs",
+             "elsewhere (yolo11.cu_amd/unitwork.py).", "", "```",
+             "OUT=gpurun_out/traffic_x",
+             "rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/fetch -o run -- python3 yolo11.cu_amd/traffic.py "
+             f"collect --scale {out['model'][-1]} --batch {out['batch']} --passes {out['passes']} --plan $OUT/plan.json",
+             "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/write -o run -- python3 yolo11.cu_amd/traffic.py "
+             f"collect --scale {out['model'][-1]} --batch {out['batch']} --passes {out['passes']} --plan $OUT/wplan.json "
+             "--replay $OUT/plan.json",
+             "python3 yolo11.cu_amd/traffic.py summarize --plan $OUT/plan.json --write-plan $OUT/wplan.json "
+             f"--fetch $OUT/fetch --write $OUT/write --json {args.json} --md {args.md}", "```", "",
+             f"Whole frame: {out['total_traffic_bytes'] / 1e9:.2f} GB moved against "
+             f"{out['total_algorithmic_bytes'] / 1e9:.2f} GB algorithmic "
+             f"({out['total_traffic_bytes'] / out['total_algorithmic_bytes']:.2f}x).", "",
+             "| class | units | traffic GB | algorithmic GB | ratio |", "|---|---|---|---|---|"]
+    for name, (n, t, a) in sorted(classes.items(), key=lambda kv: -kv[1][1]):
+        lines.append(f"| {name} | {n} | {t / 1e9:.3f} | {a / 1e9:.3f} | {t / a:.2f} |" if a else
+                     f"| {name} | {n} | {t / 1e9:.3f} | - | - |")
+    lines += ["", "Units moving the most bytes:", "",
+              "| unit | first op | kernel | class | traffic MB | algorithmic MB | ratio |", "|---|---|---|---|---|---|---|"]
+    for r in sorted(out["per_unit"], key=lambda r: -r["traffic_bytes"])[:30]:
+        lines.append(f"| {r['unit']} | {r['first_op']} | {r['kernel']} | {r['class']} | {r['traffic_bytes'] / 1e6:.1f} | "
+                     f"{r['algorithmic_bytes'] / 1e6:.1f} | {r['ratio']} |")
+    open(args.md, "w").write("\n".join(lines) + "\n")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    c = sub.add_parser("collect")
+    c.add_argument("--scale", default="x")
+    c.add_argument("--batch", type=int, default=16)
+    c.add_argument("--passes", type=int, default=3)
+    c.add_argument("--plan", required=True, help="where this run writes its plan")
+    c.add_argument("--replay", help="a first run's plan whose kernel choices this run takes")
+    s = sub.add_parser("summarize")
+    s.add_argument("--plan", required=True, help="the FETCH_SIZE run's plan")
+    s.add_argument("--write-plan", help="the WRITE_SIZE run's plan (default: --plan)")
+    s.add_argument("--fetch", required=True)
+    s.add_argument("--write", required=True)
+    s.add_argument("--json", required=True)
+    s.add_argument("--md")
+    args = ap.parse_args()
+    collect(args) if args.cmd == "collect" else summarize(args)
+
+
+if __name__ == "__main__":
+    main()

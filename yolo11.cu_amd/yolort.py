@@ -83,6 +83,9 @@ _SIGS = {
     "yolo_decoder_threads": (C.c_int, []),
     "yolo_jpeg_max_pixels": (C.c_longlong, [C.c_longlong]),
     "yolo_op_unit": (C.c_int, [C.c_void_p, C.c_int]),
+    "yolo_num_units": (C.c_int, [C.c_void_p]),
+    "yolo_run_unit": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    "yolo_marker": (C.c_int, [C.c_void_p]),
     "yolo_get_masks": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "yolo_batcher_create": (C.c_void_p, [C.POINTER(C.c_void_p), C.POINTER(C.c_int), C.c_int, C.c_double]),
     "yolo_batcher_submit_jpeg": (C.c_int, [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t, C.c_longlong]),
@@ -591,6 +594,17 @@ class Engine:
         if self.lib.yolo_profile_units(self.h, B, iters, reps, out) != 0:
             raise RuntimeError("yolo_profile_units failed")
         return np.array(out, np.float64)
+
+    def num_units(self) -> int:
+        return self.lib.yolo_num_units(self.h)
+
+    def run_unit(self, u: int, B: int):
+        if self.lib.yolo_run_unit(self.h, u, B) != 0:
+            raise RuntimeError(f"yolo_run_unit({u}) failed")
+
+    def marker(self):
+        if self.lib.yolo_marker(self.h) != 0:
+            raise RuntimeError("yolo_marker failed")
 
     def op_unit(self, k: int) -> int:
         """Launch unit of op k (ops of one unit share a launch), -1 if no unit launches it."""
