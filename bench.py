@@ -77,10 +77,12 @@ def measured_x_traffic(firsts, kernel):
     one of them with the same kernel (a tile choice that differs from that run's)."""
     path = os.path.join(ROOT, "profiles", "yolo11x_b16_traffic.json")
     try:
-        rec = json.load(open(path))["per_unit_first_op"]
-        if any(rec[str(k)]["kernel"] != kernel for k in firsts):
+        tab = json.load(open(path))
+        col = {c: i for i, c in enumerate(tab["columns"])}
+        rec = tab["per_unit_first_op"]
+        if any(rec[str(k)][col["kernel"]] != kernel for k in firsts):
             return None
-        return int(sum(rec[str(k)]["traffic_bytes"] for k in firsts))
+        return int(sum(rec[str(k)][col["traffic_bytes"]] for k in firsts))
     except (OSError, ValueError, KeyError):
         return None
 

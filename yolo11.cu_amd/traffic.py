@@ -156,12 +156,16 @@ def summarize(args):
            "scale": {"FETCH_SIZE": round(fscale, 4), "WRITE_SIZE": round(wscale, 4),
                      "reference": f"copy of {int(fplan['copy_bytes'])} bytes read + written"},
            "total_traffic_bytes": int(total_t), "total_algorithmic_bytes": int(total_a),
-           "unpaired_first_ops": unpaired,
-           "per_unit": rows, "per_unit_first_op": {str(r["first_op"]): {"traffic_bytes": r["traffic_bytes"],
-                                                                         "kernel": r["kernel"]} for r in rows}}
-    json.dump(out, open(args.json, "w"), indent=1)
+           "unpaired_first_ops": unpaired, "per_unit": rows}
     if args.md:
         _markdown(out, args)
+    # the committed figures: one compact row per unit, keyed by its first op
+    slim = {k: out[k] for k in ("model", "batch", "passes", "scale", "total_traffic_bytes",
+                                "total_algorithmic_bytes", "unpaired_first_ops")}
+    slim["columns"] = ["kernel", "class", "fetch_bytes", "write_bytes", "traffic_bytes", "algorithmic_bytes"]
+    slim["per_unit_first_op"] = {str(r["first_op"]): [r[c] for c in slim["columns"]] for r in rows}
+    with open(args.json, "w") as f:
+        json.dump(slim, f, separators=(",", ":"))
 
 
 def _markdown(out, args):
