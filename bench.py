@@ -71,18 +71,18 @@ def measured_traffic(cfg, tail=-1):
 
 
 def measured_x_traffic(firsts, kernel):
-    """HBM bytes per batch of the yolo11x b16 launch units whose first ops are `firsts`
-    (FETCH_SIZE + WRITE_SIZE of their dispatches in the committed PMC passes of traffic.py,
-    each scaled by a plain copy of known size), or None where the passes have no figure for
-    one of them with the same kernel (a tile choice that differs from that run's)."""
+    """(HBM bytes per batch, same kernels) of the yolo11x b16 launch units whose first ops are
+    `firsts`: FETCH_SIZE + WRITE_SIZE of their dispatches in the committed PMC passes of
+    profiling.py, each scaled by a plain copy of known size; `same kernels` says whether that
+    run's autotuner chose this run's kernel for every one of them (it times candidates, so
+    two runs can differ).  None where the passes have no figure for one of them."""
     path = os.path.join(ROOT, "profiles", "yolo11x_b16_traffic.json")
     try:
         tab = json.load(open(path))
         col = {c: i for i, c in enumerate(tab["columns"])}
         rec = tab["per_unit_first_op"]
-        if any(rec[str(k)][col["kernel"]] != kernel for k in firsts):
-            return None
-        return int(sum(rec[str(k)][col["traffic_bytes"]] for k in firsts))
+        same = all(rec[str(k)][col["kernel"]] == kernel for k in firsts)
+        return int(sum(rec[str(k)][col["traffic_bytes"]] for k in firsts)), same
     except (OSError, ValueError, KeyError):
         return None
 
@@ -368,11 +368,13 @@ def bench_x(workdir, iters, graph=True):
             attn_f += B * attn_flops(eng, k)
     units = unit_table(eng, B, per_unit)
     top = next(g for g in units if g["class"])          # the conv kernel group with the most time
-    traffic = measured_x_traffic(top["firsts"], top["kernel"])
+    mt = measured_x_traffic(top["firsts"], top["kernel"])
     for b in devs:
         b.free()
     eng.close()
-    return dict(dominant=group_roofline(top, traffic), units=units[:12],
+    dominant = group_roofline(top, mt[0] if mt else None)
+    dominant["traffic_same_kernels"] = mt[1] if mt else None
+    return dict(dominant=dominant, units=units[:12],
                 ms_per_batch=ms, img_per_s=B * 1e3 / ms, conv_tflops=conv_f / conv_t / 1e12,
                 conv_mfma_util=conv_f / conv_t / PEAK_FP16, conv_ms=conv_t * 1e3,
                 conv_mfma_util_stream_events=conv_f / conv_t_ev / PEAK_FP16, conv_ms_stream_events=conv_t_ev * 1e3,

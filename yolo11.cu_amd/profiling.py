@@ -1,12 +1,15 @@
-"""HBM traffic per launch unit of a whole frame, from rocprofv3 PMC passes.
+"""Profiling tools: HBM traffic per launch unit from rocprofv3 PMC passes, and the steady-state
+kernel time of a frame from a rocprofv3 kernel trace.
+
+HBM traffic per launch unit:
 
     OUT=gpurun_out/traffic_x
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/fetch -o run -- \\
-        python3 yolo11.cu_amd/traffic.py collect --scale x --batch 16 --plan $OUT/plan.json
+        python3 yolo11.cu_amd/profiling.py collect --scale x --batch 16 --plan $OUT/plan.json
     rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/write -o run -- \\
-        python3 yolo11.cu_amd/traffic.py collect --scale x --batch 16 --plan $OUT/wplan.json \\
+        python3 yolo11.cu_amd/profiling.py collect --scale x --batch 16 --plan $OUT/wplan.json \\
         --replay $OUT/plan.json
-    python3 yolo11.cu_amd/traffic.py summarize --plan $OUT/plan.json --write-plan $OUT/wplan.json \\
+    python3 yolo11.cu_amd/profiling.py summarize --plan $OUT/plan.json --write-plan $OUT/wplan.json \\
         --fetch $OUT/fetch --write $OUT/write --json profiles/yolo11x_b16_traffic.json \\
         --md profiles/yolo11x_b16_traffic.md
 
@@ -183,12 +186,12 @@ def _markdown(out, args):
              "Algorithmic bytes: input + weights + output (+ residual) per conv, inputs + outputs",
              "elsewhere (yolo11.cu_amd/unitwork.py).", "", "```",
              "OUT=gpurun_out/traffic_x",
-             "rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/fetch -o run -- python3 yolo11.cu_amd/traffic.py "
+             "rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/fetch -o run -- python3 yolo11.cu_amd/profiling.py "
              f"collect --scale {out['model'][-1]} --batch {out['batch']} --passes {out['passes']} --plan $OUT/plan.json",
-             "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/write -o run -- python3 yolo11.cu_amd/traffic.py "
+             "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/write -o run -- python3 yolo11.cu_amd/profiling.py "
              f"collect --scale {out['model'][-1]} --batch {out['batch']} --passes {out['passes']} --plan $OUT/wplan.json "
              "--replay $OUT/plan.json",
-             "python3 yolo11.cu_amd/traffic.py summarize --plan $OUT/plan.json --write-plan $OUT/wplan.json "
+             "python3 yolo11.cu_amd/profiling.py summarize --plan $OUT/plan.json --write-plan $OUT/wplan.json "
              f"--fetch $OUT/fetch --write $OUT/write --json {args.json} --md {args.md}", "```", "",
              f"Whole frame: {out['total_traffic_bytes'] / 1e9:.2f} GB moved against "
              f"{out['total_algorithmic_bytes'] / 1e9:.2f} GB algorithmic "
@@ -203,6 +206,47 @@ def _markdown(out, args):
         lines.append(f"| {r['unit']} | {r['first_op']} | {r['kernel']} | {r['class']} | {r['traffic_bytes'] / 1e6:.1f} | "
                      f"{r['algorithmic_bytes'] / 1e6:.1f} | {r['ratio']} |")
     open(args.md, "w").write("\n".join(lines) + "\n")
+
+
+def trace(args):
+    """Steady-state kernel time per frame from a `rocprofv3 --kernel-trace` CSV of
+    `bench.py --only <n|x> --no-graph` (stream-ordered launches of the frame's kernels): every
+    dispatch from the first letterbox on (after load and autotune), grouped by kernel; GEMM
+    and streaming-conv instantiations labelled with their op config numbers."""
+    import re
+    f = args.csv if args.csv.endswith(".csv") else glob.glob(os.path.join(args.csv, "*kernel_trace.csv"))[0]
+    rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Start_Timestamp"]))
+    src = open(os.path.join(HERE, "csrc", "conv.hip")).read()
+    tiles = {tuple(map(int, m.groups()[1:])): int(m.group(1)) for m in
+             re.finditer(r"X\((\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+)\)", src[src.index("#define YOLO_TILES"):])}
+    taps = {tuple(map(int, m.groups()[1:])): int(m.group(1)) for m in
+            re.finditer(r"X\((\d+), (\d), (\d+), (\d+), (\d+), (\d), (\d), (\d), (\d)\)",
+                        src[src.index("#define YOLO_TAP_TILES"):])}
+    km = {0: "1x1", 1: "uni", 2: "gen"}
+
+    def label(name):
+        name = name.split("(")[0]
+        m = re.search(r"k_conv_gemm<(\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d)>", name)
+        if m:
+            v = tuple(map(int, m.groups()))
+            return f"{name} [cfg {tiles.get(v[:6], '?')} {km[v[6]]}]"
+        m = re.search(r"k_conv_tap<(\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+)>", name)
+        if m:
+            return f"{name} [op config {1100 + taps.get(tuple(map(int, m.groups())), -1100)}]"
+        return name
+    start = next(i for i, r in enumerate(rows) if "letterbox" in r["Kernel_Name"])
+    rows = rows[start:]
+    agg: dict = {}
+    for r in rows:
+        agg.setdefault(label(r["Kernel_Name"]), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    tot = sum(sum(v) for v in agg.values())
+    frames = sum(1 for r in rows if "letterbox" in r["Kernel_Name"]) // args.letterboxes_per_frame
+    print(" calls   total_us    avg_us   min_us   max_us    pct  kernel")
+    for name, v in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:args.top]:
+        print(f"{len(v):6d} {sum(v):10.1f} {sum(v) / len(v):9.2f} {min(v):8.2f} {max(v):8.2f} "
+              f"{100 * sum(v) / tot:6.2f}  {name[:110]}")
+    print(f"steady-state kernel time {tot / 1e3:.3f} ms over {len(rows)} dispatches, {frames} frames: "
+          f"{tot / 1e3 / max(frames, 1):.4f} ms and {len(rows) / max(frames, 1):.0f} dispatches per frame")
 
 
 def main():
@@ -221,8 +265,12 @@ def main():
     s.add_argument("--write", required=True)
     s.add_argument("--json", required=True)
     s.add_argument("--md")
+    t = sub.add_parser("trace")
+    t.add_argument("csv", help="a rocprofv3 kernel_trace.csv, or the directory holding it")
+    t.add_argument("--letterboxes-per-frame", type=int, default=1)
+    t.add_argument("--top", type=int, default=32)
     args = ap.parse_args()
-    collect(args) if args.cmd == "collect" else summarize(args)
+    {"collect": collect, "summarize": summarize, "trace": trace}[args.cmd](args)
 
 
 if __name__ == "__main__":

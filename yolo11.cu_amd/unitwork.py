@@ -1,7 +1,7 @@
 """Algorithmic work of the ops a frame runs, and the launch units they run in.
 
 Used by the benchmark (per-unit time attribution, roofline entries) and by the HBM traffic
-tool (traffic.py), so both count work the same way:
+tool (profiling.py), so both count work the same way:
 
     conv   2*B*Ho*Wo*Cout*k^2*Cin/g FLOPs; input + weights + output (+ residual) in fp16
            plus the fp32 bias
