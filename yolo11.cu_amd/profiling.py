@@ -224,8 +224,21 @@ def trace(args):
                         src[src.index("#define YOLO_TAP_TILES"):])}
     km = {0: "1x1", 1: "uni", 2: "gen"}
 
+    def demangle(name):
+        # kernels whose trace name stays mangled: yolo::<kernel><integer/bool template args>
+        m = re.match(r"_ZN4yolo(\d+)", name)
+        if not m:
+            return name
+        n0 = m.end()
+        ident = name[n0:n0 + int(m.group(1))]
+        targs = re.match(r"I((?:L[ib]-?\d+E)+)E", name[n0 + len(ident):])
+        if not targs:
+            return f"yolo::{ident}"
+        vals = re.findall(r"L([ib])(-?\d+)E", targs.group(1))
+        return f"yolo::{ident}<{', '.join(v if t == 'i' else ('true' if v == '1' else 'false') for t, v in vals)}>"
+
     def label(name):
-        name = name.split("(")[0]
+        name = demangle(name.split("(")[0])
         m = re.search(r"k_conv_gemm<(\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d)>", name)
         if m:
             v = tuple(map(int, m.groups()))
