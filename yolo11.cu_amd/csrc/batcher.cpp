@@ -118,13 +118,14 @@ class Batcher {
     return n;
   }
 
+  // Safe from any thread and more than once: the join itself is serialised.
   void stop() {
     {
       std::lock_guard<std::mutex> lk(mu_);
-      if (stop_ && !worker_.joinable()) return;
       stop_ = true;
       cv_.notify_all();
     }
+    std::lock_guard<std::mutex> jl(joinMu_);
     if (worker_.joinable()) worker_.join();
   }
 
@@ -376,7 +377,7 @@ class Batcher {
 
   std::vector<Model> models_;
   double targetMs_, stageEma_ = 1.0;
-  std::mutex mu_;
+  std::mutex mu_, joinMu_;
   std::condition_variable cv_, doneCv_;
   std::deque<Done*> done_;
   bool stop_ = false, finished_ = false;
