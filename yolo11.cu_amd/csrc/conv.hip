@@ -1559,7 +1559,7 @@ void launchConv1x1Stream(const View& x, const View& y, const View* res, const f1
 // plus the 9 taps' weights of BN output channels, and the waves run 9 MFMA k-steps from it
 // (a tap's pixel fragment is the halo shifted by (ky, kx): a per-lane LDS address, the tap
 // offset an immediate).
-// Blocks are persistent: block b owns channel tile b % ntN (the grid is a multiple of ntN)
+// Blocks are persistent: work id b owns channel tile b % ntN (the grid is a multiple of ntN)
 // and the pixel tiles of items b, b + grid, b + 2 grid, ...; the LDS ring runs through the
 // stages of all its tiles as one sequence, so the next tile's first stages are in flight while
 // the current tile finishes and stores (these convs have only 2-8 stages per tile, and a
@@ -1610,7 +1610,10 @@ __global__ __launch_bounds__(64 * WP * WN * KG) void k_conv_tap(View x, View y, 
   __shared__ f16x8 ring[NS * SZ];
 
   const int Cin = x.C, N = y.C;
-  const int nb = gridDim.x, b = blockIdx.x;
+  // work id of this block: each XCD's blocks take one contiguous range of ids, so the ntN
+  // channel tiles of a pixel tile (which read the same halo) and neighbouring pixel tiles
+  // (which share halo rows) meet in one L2 instead of each XCD fetching them from HBM
+  const int nb = gridDim.x, b = nb >= 2 * NUM_XCD ? xcdRange((int)blockIdx.x, nb) : (int)blockIdx.x;
   const int nt = b % ntN, bn = nt * BN;
   const int mine = b < items ? (items - 1 - b) / nb + 1 : 0;   // items of this block
   if (mine == 0) return;

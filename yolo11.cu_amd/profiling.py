@@ -195,7 +195,9 @@ def _markdown(out, args):
              f"--fetch $OUT/fetch --write $OUT/write --json {args.json} --md {args.md}", "```", "",
              f"Whole frame: {out['total_traffic_bytes'] / 1e9:.2f} GB moved against "
              f"{out['total_algorithmic_bytes'] / 1e9:.2f} GB algorithmic "
-             f"({out['total_traffic_bytes'] / out['total_algorithmic_bytes']:.2f}x).", "",
+             f"({out['total_traffic_bytes'] / out['total_algorithmic_bytes']:.2f}x), over the units both passes ran "
+             "with the same ops and kernel (left out, by first op: "
+             f"{', '.join(map(str, out['unpaired_first_ops'])) or 'none'}).", "",
              "| class | units | traffic GB | algorithmic GB | ratio |", "|---|---|---|---|---|"]
     for name, (n, t, a) in sorted(classes.items(), key=lambda kv: -kv[1][1]):
         lines.append(f"| {name} | {n} | {t / 1e9:.3f} | {a / 1e9:.3f} | {t / a:.2f} |" if a else
