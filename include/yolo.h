@@ -322,6 +322,11 @@ int yolo_op_unit(void* h, int k);
 int yolo_num_units(void* h);
 int yolo_run_unit(void* h, int u, int B);
 int yolo_marker(void* h);
+/* Number of bounded waits that expired in kernels whose waves hand work to each other through
+ * LDS counters (the wave-specialised conv, op configs 1200+) on the handle's device since the
+ * process started: 0 unless such a launch went wrong, and then that launch's outputs are
+ * invalid.  No counterpart in the reference; -1 on a device error. */
+int yolo_spin_failures(void* h);
 /* Average ms of the frame's pre/post stages over `iters` stream-ordered passes of the frame
  * set by yolo_frame_graph (frames in device memory, no H2D): ms[0] letterbox of all slots,
  * ms[1] decode (all levels, one launch), ms[2] NMS, ms[3] mask assembly (0 without a proto).

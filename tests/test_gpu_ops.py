@@ -599,6 +599,73 @@ def test_conv_tap_1x1(tmp_path, v, H, W, Cin, Cout, B, res, act):
     _check_tap(eng, g, ops, x, v, B, Cout, f"tap1x1 v{v} {H}x{W} {Cin}->{Cout} b{B} res={res}")
 
 
+@pytest.mark.parametrize("v", range(yolort.NUM_TAPWS_TILES))
+@pytest.mark.parametrize("H,W,Cin,Cout,B,res", [
+    (40, 40, 192, 192, 2, True),     # six stages, several channel tiles, residual
+    (80, 80, 96, 96, 1, False),      # the yolo11x 80x80 bottleneck shape
+    (33, 45, 48, 48, 3, True),       # ragged tiles on both axes, a half-live second stage
+    (20, 20, 256, 256, 1, False),    # eight stages: every ring slot refilled several times
+    (17, 23, 40, 112, 2, False)])    # Cin 40, a partly live channel tile
+def test_conv_tapws(tmp_path, v, H, W, Cin, Cout, B, res):
+    """The wave-specialised halo-staged 3x3 conv (op configs CFG_TAPWS + v): producer waves
+    fill the LDS ring, consumer waves run the MFMAs, slots handed over through LDS counters.
+    Against the oracle; no bounded wait expired; a second launch gives the same bits; and
+    every image equals its own batch-1 run (results depend on neither timing nor batch)."""
+    d = str(tmp_path / "tapws")
+    modelgen.write_single_conv(d, H, W, Cin, Cout, 3, 1, seed=Cin + Cout, residual=res)
+    g = graphfile.load(d)
+    x = np.random.default_rng(Cin).standard_normal((B, H, W, Cin), dtype=np.float32).astype(np.float16)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    ops = [graphfile.Op(**vars(o)) for o in graphfile.fuse_adds(g.ops)]
+    try:
+        eng.set_op_config(0, yolort.CFG_TAPWS + v)
+    except ValueError:
+        assert Cout <= yolort.TAPWS_BN[v] // 2
+        eng.close()
+        return
+    before = eng.spin_failures()
+    eng.write(0, x)
+    eng.run_op(0, B)
+    got = eng.read(ops[0].out, B)
+    eng.run_op(0, B)
+    again = eng.read(ops[0].out, B)
+    one = []
+    for i in range(B):
+        eng.write(0, x[i:i + 1])
+        eng.run_op(0, 1)
+        one.append(eng.read(ops[0].out, 1)[0])
+    assert eng.spin_failures() == before == 0
+    np.testing.assert_array_equal(again.view(np.uint16), got.view(np.uint16))
+    np.testing.assert_array_equal(np.stack(one).view(np.uint16), got.view(np.uint16))
+    ref = interp.Interp(g, B)
+    ref.set_input(x.astype(np.float32))
+    ref.run_op(ops[0])
+    rel = post.rel_err(got.astype(np.float32), ref.view(ops[0].out))
+    print(f"tapws v{v} {H}x{W} {Cin}->{Cout} b{B} res={res}: rel {rel:.2e}", flush=True)
+    assert rel <= TOL
+    eng.close()
+
+
+def test_conv_tapws_rejects(tmp_path):
+    """The wave-specialised configs are refused for stride 2, 1x1 convs, Cout not a multiple
+    of 16, and past the last variant."""
+    for i, (cin, cout, k, s) in enumerate([(32, 32, 3, 2), (32, 32, 1, 1), (32, 24, 3, 1)]):
+        d = str(tmp_path / f"r{i}")
+        modelgen.write_single_conv(d, 16, 16, cin, cout, k, s, seed=1)
+        eng = yolort.Engine(d, 1, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+        for v in range(yolort.NUM_TAPWS_TILES):
+            with pytest.raises(ValueError):
+                eng.set_op_config(0, yolort.CFG_TAPWS + v)
+        eng.close()
+    d = str(tmp_path / "ok")
+    modelgen.write_single_conv(d, 16, 16, 64, 64, 3, 1, seed=1)
+    eng = yolort.Engine(d, 1, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
+    eng.set_op_config(0, yolort.CFG_TAPWS)
+    with pytest.raises(ValueError):
+        eng.set_op_config(0, yolort.CFG_TAPWS + yolort.NUM_TAPWS_TILES)
+    eng.close()
+
+
 def test_conv_tap_rejects(tmp_path):
     """The streaming configs are refused where the kernel does not apply (stride 2, the
     other kernel size, Cout not a multiple of 16) and past the last variant."""

@@ -1975,10 +1975,370 @@ void launchConvTap(int v, const View& x, const View& y, const View* res, const f
   }
 }
 
+// ------------------------------------------------------------------ streaming 3x3 conv, wave-specialised
+// The halo-staged 3x3 conv with its DMA and its MFMAs on different waves.  In k_conv_tap every
+// wave issues its share of the next stage's DMA, then runs its MFMAs, and one block barrier
+// per stage lines them up: while the waves stall in DMA issue (the memory pipeline's
+// back-pressure) or wait at the barrier, the matrix pipe idles.  Here NP producer waves only
+// move stages into the LDS ring and WP x WN consumer waves only read fragments and run MFMAs;
+// the two sides hand ring slots over through LDS counters instead of barriers:
+//   full[j]  -- each producer adds 1 once its chunks of slot j's current fill have landed
+//              (s_waitcnt vmcnt(0) before the add): fill f of slot j is ready at NP (f + 1);
+//   empty[j] -- each consumer adds 1 once its fragment reads of slot j have returned
+//              (s_waitcnt lgkmcnt(0) before the add): fill f + 1 may start at NWC (f + 1).
+// A wave's LDS operations complete in order, so a consumer that has read full[j] at its
+// target reads the landed chunks after it.  Every counter wait is a bounded spin: past
+// kSpinLimit polls the wave counts a failure in g_spinFail and the whole block stops, so no
+// mistake can leave waves spinning (that launch's outputs are then invalid; the autotuner
+// and the tests check the count).  Each output is one consumer lane's MFMA chain over the
+// stages in order with all 9 taps per stage, so results depend neither on timing nor on the
+// grid or the batch.
+__device__ int g_spinFail;
+constexpr int kSpinLimit = 1 << 20;
+
+__device__ __forceinline__ bool spinUntil(const int* c, int target, const int* stop) {
+  for (int i = 0; i < kSpinLimit; i++) {
+    const int v = __builtin_amdgcn_readfirstlane(__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    if (v >= target) {
+      asm volatile("" ::: "memory");
+      return true;
+    }
+    if (__builtin_amdgcn_readfirstlane(__hip_atomic_load(stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)))
+      return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
+template <int TH, int TW, int BN, int WP, int WN, int NP, int NS>
+__global__ __launch_bounds__(64 * (WP * WN + NP)) void k_conv_tapws(View x, View y, View r, const f16* __restrict__ w,
+                                                                    const float* __restrict__ bias, int act, int H,
+                                                                    int W, int tilesX, int tilesY, int ntN, int items,
+                                                                    int xbytes) {
+  constexpr int TAPS = 9, NWC = WP * WN;
+  constexpr int HW2 = TW + 2, HP = (TH + 2) * HW2;
+  constexpr int FPB = TH * TW / 16;
+  constexpr int FM = FPB / WP, FN = BN / 16 / WN;
+  constexpr bool PAIR = FN % 2 == 0;
+  constexpr int HC = HP * 4, WC = TAPS * BN * 4;   // 16-byte chunks of a stage's halo and weights
+  constexpr int IH = (HC + 64 * NP - 1) / (64 * NP), IW = (WC + 64 * NP - 1) / (64 * NP);
+  constexpr int HREG = IH * NP * 64;               // chunks of the (padded) halo region
+  constexpr int SZ = HREG + IW * NP * 64;          // chunks per stage
+  static_assert(TH * TW % 16 == 0 && FPB % WP == 0 && BN % (16 * WN) == 0, "tile shape");
+  static_assert(FM + FN <= 15, "a tap's fragment reads fit the lgkm counter");
+  constexpr bool PIPE = 2 * (FM + FN) <= 15;
+  static_assert(IH + IW < 64, "a producer's loads of one stage fit the vm counter");
+  static_assert(16 * ((TAPS - 1) * BN * 4 + (FN - 1) * 64) < 65536, "weight offsets fit the ds_read offset field");
+  static_assert(NS >= 2, "ring depth");
+  __shared__ f16x8 ring[NS * SZ];
+  __shared__ int full[NS], empty[NS], stop;
+
+  const int Cin = x.C, N = y.C;
+  const int nb = gridDim.x, b = nb >= 2 * NUM_XCD ? xcdRange((int)blockIdx.x, nb) : (int)blockIdx.x;
+  const int nt = b % ntN, bn = nt * BN;
+  const int mine = b < items ? (items - 1 - b) / nb + 1 : 0;
+  if (mine == 0) return;
+  const int perImg = tilesX * tilesY, nks = (Cin + 31) / 32, total = mine * nks;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  if (t < NS) {
+    full[t] = 0;
+    empty[t] = 0;
+  }
+  if (t == 0) stop = 0;
+  __syncthreads();
+
+  struct Tile { int img, y0, x0; };
+  auto tileOf = [&](int k) __attribute__((always_inline)) {
+    const int pt = (b + k * nb) / ntN;
+    const int img = pt / perImg, rem = pt - img * perImg;
+    const int ty = rem / tilesX;
+    return Tile{img, ty * TH, (rem - ty * tilesX) * TW};
+  };
+  auto failed = [&]() __attribute__((always_inline)) {
+    if (lane == 0) {
+      atomicAdd(&g_spinFail, 1);
+      __hip_atomic_store(&stop, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
+
+  if (wave >= NWC) {   // ---------------------------------------------------------------- producer
+    const int p = wave - NWC;
+    const int c8 = 8 * (lane & 3);
+    __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(x.p, (short)0, xbytes, 0x00020000);
+    __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(w), (short)0, N * TAPS * Cin * 2, 0x00020000);
+    // chunk slot (i*NP + p)*64 + lane of a region: halo chunk (halo pixel, lane & 3), weight
+    // chunk ((tap, LDS row), lane & 3) with LDS row r holding output channel bn + chperm(r)
+    // when fragments pair up -- the layout k_conv_tap uses, filled by NP waves instead of all
+    unsigned wa[IW], ha[IH];
+#pragma unroll
+    for (int i = 0; i < IW; i++) {
+      const int slot = (i * NP + p) * 64 + lane, q = slot >> 2;
+      const int tap = q / BN, row = q - tap * BN;
+      const int n = bn + (PAIR ? chperm(row) : row);
+      wa[i] = slot < WC && n < N ? 2u * (unsigned)((n * TAPS + tap) * Cin + c8) : OOB_OFF;
+    }
+    int item = 0, s = 0;
+    for (int q = 0; q < total; q++) {
+      const int j = q % NS, f = q / NS;
+      if (f > 0 && !spinUntil(&empty[j], NWC * f, &stop)) {
+        failed();
+        return;
+      }
+      if (s == 0) {
+        const Tile tl = tileOf(item);
+#pragma unroll
+        for (int i = 0; i < IH; i++) {
+          const int slot = (i * NP + p) * 64 + lane, hp = slot >> 2;
+          const int hy = hp / HW2, hx = hp - hy * HW2;
+          const int iy = tl.y0 - 1 + hy, ix = tl.x0 - 1 + hx;
+          const bool ok = slot < HC && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+          ha[i] = ok ? 2u * (unsigned)(((tl.img * H + iy) * W + ix) * x.s + x.o + c8) : OOB_OFF;
+        }
+      }
+      const int k0 = s * 32;
+      const bool kin = k0 + c8 < Cin;
+      const unsigned ku = 2u * (unsigned)k0;
+      f16x8* buf = ring + j * SZ;
+#pragma unroll
+      for (int i = 0; i < IH; i++) dma16(rx, (lds_ptr)(buf + (i * NP + p) * 64), kin ? ha[i] + ku : OOB_OFF);
+#pragma unroll
+      for (int i = 0; i < IW; i++) dma16(rw, (lds_ptr)(buf + HREG + (i * NP + p) * 64), kin ? wa[i] + ku : OOB_OFF);
+      vmwait<0>();
+      asm volatile("" ::: "memory");
+      if (lane == 0) __hip_atomic_fetch_add(&full[j], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (++s == nks) {
+        s = 0;
+        item++;
+      }
+    }
+    return;
+  }
+
+  // ------------------------------------------------------------------------------------ consumer
+  const int wp = wave % WP, wn = wave / WP;
+  const int lr = lane & 15, lg = lane >> 4;
+  unsigned pb[FM];
+#pragma unroll
+  for (int j = 0; j < FM; j++) {
+    const int p = (wp * FM + j) * 16 + lr, py = p / TW, px = p - py * TW;
+    pb[j] = 16u * (unsigned)((py * HW2 + px) * 4 + lg);
+  }
+  const unsigned wb = 16u * (unsigned)(HREG + (wn * FN * 16 + lr) * 4 + lg);
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; i++)
+#pragma unroll
+    for (int j = 0; j < FM; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float bpre[FN][4];
+#pragma unroll
+  for (int i = 0; i < FN; i++) {
+    const int n0 = PAIR ? bn + wn * FN * 16 + 32 * (i / 2) + 8 * lg + 4 * (i % 2) : bn + wn * FN * 16 + i * 16 + 4 * lg;
+#pragma unroll
+    for (int e = 0; e < 4; e++) bpre[i][e] = n0 + e < N ? bias[n0 + e] : 0.f;
+  }
+  constexpr int NR = PAIR ? FN / 2 : FN;
+  using RV = typename std::conditional<PAIR, f16x8, f16x4>::type;
+  RV rpre[FM][NR];
+  auto resLoads = [&](int k) __attribute__((always_inline)) {
+    const Tile tl = tileOf(k);
+#pragma unroll
+    for (int q = 0; q < FM; q++) {
+      const int p = (wp * FM + q) * 16 + lr, py = p / TW, px = p - py * TW;
+      const int oy = tl.y0 + py, ox = tl.x0 + px;
+      const bool live = oy < H && ox < W;
+      const size_t m = live ? (size_t)(tl.img * H + oy) * W + ox : 0;
+#pragma unroll
+      for (int p2 = 0; p2 < NR; p2++) {
+        const int n0 = PAIR ? bn + wn * FN * 16 + 32 * p2 + 8 * lg : bn + wn * FN * 16 + p2 * 16 + 4 * lg;
+        rpre[q][p2] = live && n0 < N ? *(const RV*)(r.p + m * r.s + r.o + n0) : RV{};
+      }
+    }
+  };
+  auto epilogue = [&](int k) __attribute__((always_inline)) {
+    const Tile tl = tileOf(k);
+#pragma unroll
+    for (int q = 0; q < FM; q++) {
+      const int p = (wp * FM + q) * 16 + lr, py = p / TW, px = p - py * TW;
+      const int oy = tl.y0 + py, ox = tl.x0 + px;
+      if (oy >= H || ox >= W) continue;
+      const size_t m = (size_t)(tl.img * H + oy) * W + ox;
+      if constexpr (PAIR) {
+#pragma unroll
+        for (int p2 = 0; p2 < FN / 2; p2++) {
+          const int n0 = bn + wn * FN * 16 + 32 * p2 + 8 * lg;
+          if (n0 >= N) continue;
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            v[e] = acc[2 * p2][q][e] + bpre[2 * p2][e];
+            v[4 + e] = acc[2 * p2 + 1][q][e] + bpre[2 * p2 + 1][e];
+          }
+          if (act == 1) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = silu(v[e]);
+          }
+          if (r.p) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] += (float)rpre[q][p2][e];
+          }
+          f16x8 o;
+#pragma unroll
+          for (int e = 0; e < 8; e++) o[e] = (f16)v[e];
+          *(f16x8*)(y.p + m * y.s + y.o + n0) = o;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < FN; i++) {
+          const int n0 = bn + wn * FN * 16 + i * 16 + 4 * lg;
+          if (n0 >= N) continue;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            v[e] = acc[i][q][e] + bpre[i][e];
+            if (act == 1) v[e] = silu(v[e]);
+          }
+          if (r.p) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] += (float)rpre[q][i][e];
+          }
+          const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+          *(f16x4*)(y.p + m * y.s + y.o + n0) = o;
+        }
+      }
+    }
+  };
+
+  int cS = 0, cItem = 0;
+  for (int q = 0; q < total; q++) {
+    const int j = q % NS;
+    if (!spinUntil(&full[j], NP * (q / NS + 1), &stop)) {
+      failed();
+      return;
+    }
+    if (r.p && cS == nks - 1) resLoads(cItem);
+    const unsigned base = (unsigned)(size_t)(lds_f16x8)(ring + j * SZ);
+    unsigned ap[FM];
+#pragma unroll
+    for (int u = 0; u < FM; u++) ap[u] = base + pb[u];
+    const unsigned aw = base + wb;
+    __builtin_amdgcn_sched_barrier(0);
+    f16x8 fa[2][FN], fb[2][FM];
+    auto reads = [&](auto T, auto S) __attribute__((always_inline)) {
+      constexpr int tap = decltype(T)::value, ky = tap / 3, kx = tap % 3;
+      static_for<FN>([&](auto I) { fa[S][I] = ds_read16<16 * (tap * BN * 4 + I * 64)>(aw); });
+      static_for<FM>([&](auto Q) { fb[S][Q] = ds_read16<64 * (ky * HW2 + kx)>(ap[Q]); });
+    };
+    reads(ic<0>{}, ic<0>{});
+    static_for<TAPS>([&](auto U) {
+      constexpr int tap = U, cur = PIPE ? U % 2 : 0;
+      constexpr int later = PIPE && tap + 1 < TAPS ? FN + FM : 0;
+      if constexpr (later > 0) reads(ic<tap + 1>{}, ic<1 - cur>{});
+      static_for<FM>([&](auto Q) {
+        lgkm_wait<later + FM - 1 - Q>();
+        if constexpr (Q == 0) {
+#pragma unroll
+          for (int i = 0; i < FN; i++) asm volatile("" : "+v"(fa[cur][i]));
+        }
+        asm volatile("" : "+v"(fb[cur][Q]));
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+          acc[i][Q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[cur][i], fb[cur][Q], acc[i][Q], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      if constexpr (!PIPE && tap + 1 < TAPS) reads(ic<tap + 1>{}, ic<0>{});
+    });
+    // every fragment read of the slot has returned (the last column waited lgkmcnt(0))
+    asm volatile("" ::: "memory");
+    if (lane == 0) __hip_atomic_fetch_add(&empty[j], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (++cS == nks) {
+      cS = 0;
+      epilogue(cItem);
+#pragma unroll
+      for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int u = 0; u < FM; u++) acc[i][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      cItem++;
+    }
+  }
+}
+
+// {tile rows, tile columns, output channels, consumer waves along pixels, along channels,
+//  producer waves, LDS stages}
+#define YOLO_TAPWS_TILES(X)        \
+  X(0, 8, 40, 64, 4, 2, 4, 2)      \
+  X(1, 8, 40, 48, 4, 1, 2, 2)      \
+  X(2, 4, 40, 64, 2, 2, 2, 3)      \
+  X(3, 8, 20, 96, 2, 3, 2, 2)
+
+struct TapWsTile { int BN; };
+static const TapWsTile kTapWsTiles[] = {
+#define X(i, th, tw, bn, wp, wn, np, ns) {bn},
+    YOLO_TAPWS_TILES(X)
+#undef X
+};
+constexpr int kNumTapWsTiles = sizeof(kTapWsTiles) / sizeof(kTapWsTiles[0]);
+int numTapWsTiles() { return kNumTapWsTiles; }
+
+bool convTapWsOk(int v, const View& x, const View& y, const View* r, int k, int s, int p) {
+  if (v < 0 || v >= kNumTapWsTiles) return false;
+  return k == 3 && s == 1 && p == 1 && x.H == y.H && x.W == y.W && x.C >= 8 && x.C % 8 == 0 && y.C >= 16 &&
+         y.C % 16 == 0 && kTapWsTiles[v].BN / 2 < y.C && x.s % 8 == 0 && x.o % 8 == 0 && y.s % 8 == 0 &&
+         y.o % 8 == 0 && (!r || (r->s % 8 == 0 && r->o % 8 == 0));
+}
+
+int convSpinFailures() {
+  int n = 0;
+  if (hipMemcpyFromSymbol(&n, HIP_SYMBOL(g_spinFail), sizeof n, 0, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  return n;
+}
+
+template <int TH, int TW, int BN, int WP, int WN, int NP, int NS>
+static void launchTapWs(const View& x, const View& y, const View& r, const f16* w, const float* bias, int act,
+                        int Bn, hipStream_t st) {
+  static const int slots = [] {
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_conv_tapws<TH, TW, BN, WP, WN, NP, NS>,
+                                                     64 * (WP * WN + NP), 0) != hipSuccess)
+      return 0;
+    return cus * std::max(per, 1);
+  }();
+  const int H = y.H, W = y.W;
+  const int tilesX = (W + TW - 1) / TW, tilesY = (H + TH - 1) / TH;
+  const int ntN = (y.C + BN - 1) / BN;
+  const int items = Bn * tilesX * tilesY * ntN;
+  const int xbytes = (int)((long)Bn * x.H * x.W * x.s * 2);
+  // persistent grid as in launchTap: resident blocks, a multiple of the channel tiles, every
+  // block with the floor or ceiling of the average item count
+  int grid = std::max(ntN, std::min(items, std::max(slots, 1)) / ntN * ntN);
+  const int per = (items + grid - 1) / grid;
+  grid = std::max(ntN, ((items + per - 1) / per + ntN - 1) / ntN * ntN);
+  k_conv_tapws<TH, TW, BN, WP, WN, NP, NS><<<grid, 64 * (WP * WN + NP), 0, st>>>(x, y, r, w, bias, act, H, W, tilesX,
+                                                                                  tilesY, ntN, items, xbytes);
+}
+
+void launchConvTapWs(int v, const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
+                     int Bn, hipStream_t st) {
+  const View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
+  switch (v) {
+#define X(i, th, tw, bn, wp, wn, np, ns) \
+    case i:                              \
+      launchTapWs<th, tw, bn, wp, wn, np, ns>(x, y, r, w, bias, act, Bn, st); \
+      break;
+    YOLO_TAPWS_TILES(X)
+#undef X
+    default: break;
+  }
+}
+
 bool specialConvOk(int cfg, const View& x, const View& y, const View* r, int k, int s, int p) {
   if (cfg == CFG_HALO) return convHaloOk(x, y, r, k, s, p);
   if (cfg == CFG_1X1) return conv1x1Ok(x, y, r, k, s, p);
   if (cfg == CFG_1X1S) return conv1x1StreamOk(x, y, r, k, s, p);
+  if (cfg >= CFG_TAPWS) return convTapWsOk(cfg - CFG_TAPWS, x, y, r, k, s, p);
   return convTapOk(cfg - CFG_TAP, x, y, r, k, s, p);
 }
 
@@ -1987,6 +2347,7 @@ void launchSpecialConv(int cfg, const View& x, const View& y, const View* res, c
   if (cfg == CFG_HALO) launchConvHalo(x, y, res, w, bias, act, Bn, st);
   else if (cfg == CFG_1X1) launchConv1x1(x, y, res, w, bias, act, Bn, st);
   else if (cfg == CFG_1X1S) launchConv1x1Stream(x, y, res, w, bias, act, Bn, st);
+  else if (cfg >= CFG_TAPWS) launchConvTapWs(cfg - CFG_TAPWS, x, y, res, w, bias, act, Bn, st);
   else launchConvTap(cfg - CFG_TAP, x, y, res, w, bias, act, Bn, st);
 }
 

@@ -851,6 +851,7 @@ struct Engine {
     std::vector<char> allowed(numTileConfigs(), 1);
     std::vector<int> specials = {CFG_HALO, CFG_1X1, CFG_1X1S};
     for (int v = 0; v < numTapTiles(); v++) specials.push_back(CFG_TAP + v);
+    for (int v = 0; v < numTapWsTiles(); v++) specials.push_back(CFG_TAPWS + v);
     if (const char* lim = getenv("YOLO_TUNE_TILES")) {
       std::fill(allowed.begin(), allowed.end(), 0);
       std::vector<int> keep;
@@ -935,7 +936,13 @@ struct Engine {
         op.cfg = special;
         op.split = 1;
         op.wsOff = op.cntOff = -1;
+        const bool handoff = special >= CFG_TAPWS;   // waves that wait on each other: check the waits
+        const int failsBefore = handoff ? convSpinFailures() : 0;
         const float ms = timeOp();
+        if (handoff && convSpinFailures() != failsBefore) {
+          fprintf(stderr, "yolo: op %zu: config %d had an expired wait; not used\n", k, special);
+          continue;
+        }
         if (ms < bestMs) { bestMs = ms; best = special; bestSplit = 1; bestTail = -1; }
       }
       op.cfg = best;
@@ -2228,6 +2235,14 @@ int yolo_marker(void* h) {
     yolo::launchMarker(E(h)->st);
     HCK(hipGetLastError());
     return 0;
+  });
+}
+
+int yolo_spin_failures(void* h) {
+  if (!h) return -1;
+  return guarded([&] {
+    HCK(hipStreamSynchronize(E(h)->st));
+    return yolo::convSpinFailures();
   });
 }
 

@@ -217,9 +217,21 @@ int numTapTiles();
 bool convTapOk(int v, const View& x, const View& y, const View* r, int k, int s, int p);
 void launchConvTap(int v, const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
                    int Bn, hipStream_t st);
+// The halo-staged 3x3 conv with producer waves (DMA) and consumer waves (MFMA) handing LDS
+// ring slots over through counters, tile variant v in [0, numTapWsTiles()): op configs
+// CFG_TAPWS + v.  Its waits are bounded spins; convSpinFailures() is the number of waits that
+// expired on the current device since the process started (0 unless a launch went wrong, and
+// then that launch's outputs are invalid).
+constexpr int CFG_TAPWS = 1200;
+int numTapWsTiles();
+bool convTapWsOk(int v, const View& x, const View& y, const View* r, int k, int s, int p);
+void launchConvTapWs(int v, const View& x, const View& y, const View* res, const f16* w, const float* bias, int act,
+                     int Bn, hipStream_t st);
+int convSpinFailures();
 // Op configs that select a kernel other than a GEMM tile (no split-K, no grouped launches).
 inline bool specialConvCfg(int cfg) {
-  return cfg == CFG_HALO || cfg == CFG_1X1 || cfg == CFG_1X1S || (cfg >= CFG_TAP && cfg < CFG_TAP + numTapTiles());
+  return cfg == CFG_HALO || cfg == CFG_1X1 || cfg == CFG_1X1S || (cfg >= CFG_TAP && cfg < CFG_TAP + numTapTiles()) ||
+         (cfg >= CFG_TAPWS && cfg < CFG_TAPWS + numTapWsTiles());
 }
 // Whether special config `cfg` applies to a conv, and its launch.
 bool specialConvOk(int cfg, const View& x, const View& y, const View* r, int k, int s, int p);

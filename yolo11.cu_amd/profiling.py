@@ -224,6 +224,9 @@ def trace(args):
     taps = {tuple(map(int, m.groups()[1:])): int(m.group(1)) for m in
             re.finditer(r"X\((\d+), (\d), (\d+), (\d+), (\d+), (\d), (\d), (\d), (\d)\)",
                         src[src.index("#define YOLO_TAP_TILES"):])}
+    wstaps = {tuple(map(int, m.groups()[1:])): int(m.group(1)) for m in
+              re.finditer(r"X\((\d+), (\d+), (\d+), (\d+), (\d), (\d), (\d), (\d)\)",
+                          src[src.index("#define YOLO_TAPWS_TILES"):])}
     km = {0: "1x1", 1: "uni", 2: "gen"}
 
     def demangle(name):
@@ -245,6 +248,9 @@ def trace(args):
         if m:
             v = tuple(map(int, m.groups()))
             return f"{name} [cfg {tiles.get(v[:6], '?')} {km[v[6]]}]"
+        m = re.search(r"k_conv_tapws<(\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+)>", name)
+        if m:
+            return f"{name} [op config {1200 + wstaps.get(tuple(map(int, m.groups())), -1200)}]"
         m = re.search(r"k_conv_tap<(\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+)>", name)
         if m:
             return f"{name} [op config {1100 + taps.get(tuple(map(int, m.groups())), -1100)}]"

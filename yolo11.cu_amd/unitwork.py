@@ -24,6 +24,8 @@ def conv_kernel_name(cfg: int, tail: int = -1) -> str:
         return "k_conv1x1_resident"
     if cfg == 1002:
         return "k_conv1x1_stream"
+    if cfg >= 1200:
+        return f"k_conv_tapws variant {cfg - 1200}"
     if cfg >= 1100:
         return f"k_conv_tap variant {cfg - 1100}"
     if tail >= 0:

@@ -29,6 +29,9 @@ NUM_TAP_TILES = 13
 TAP_3X3 = range(0, 8)    # variants for 3x3 stride-1 convs (halo-staged)
 TAP_1X1 = range(8, 13)   # variants for 1x1 stride-1 convs
 TAP_BN = (64, 96, 64, 64, 96, 64, 96, 48, 384, 192, 192, 128, 256)   # output channels per block
+CFG_TAPWS = 1200  # op configs 1200 .. 1200 + NUM_TAPWS_TILES - 1: wave-specialised 3x3 variants
+NUM_TAPWS_TILES = 4
+TAPWS_BN = (64, 48, 64, 96)
 OP_KINDS = ["CONV", "ADD", "MAXPOOL5", "UPSAMPLE2", "COPYC", "ATTN", "DECODE", "GAP", "SOFTMAX",
             "DECODEOBB", "PS2", "DECODESEG", "MASKS"]
 MAX_OUT = 300
@@ -136,6 +139,7 @@ _SIGS = {
     "yolo_profile_ops": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "yolo_profile_stages": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_float)]),
     "yolo_profile_units": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)]),
+    "yolo_spin_failures": (C.c_int, [C.c_void_p]),
     "yolo_dev_alloc": (C.c_void_p, [C.c_size_t]),
     "yolo_dev_free": (None, [C.c_void_p]),
     "yolo_host_alloc": (C.c_void_p, [C.c_size_t]),
@@ -601,6 +605,11 @@ class Engine:
     def run_unit(self, u: int, B: int):
         if self.lib.yolo_run_unit(self.h, u, B) != 0:
             raise RuntimeError(f"yolo_run_unit({u}) failed")
+
+    def spin_failures(self) -> int:
+        """Bounded waits that expired in wave-specialised kernels on this device (0 when every
+        launch was sound)."""
+        return self.lib.yolo_spin_failures(self.h)
 
     def marker(self):
         if self.lib.yolo_marker(self.h) != 0:
