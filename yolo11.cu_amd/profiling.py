@@ -219,14 +219,12 @@ def trace(args):
     f = args.csv if args.csv.endswith(".csv") else glob.glob(os.path.join(args.csv, "*kernel_trace.csv"))[0]
     rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Start_Timestamp"]))
     src = open(os.path.join(HERE, "csrc", "conv.hip")).read()
-    tiles = {tuple(map(int, m.groups()[1:])): int(m.group(1)) for m in
-             re.finditer(r"X\((\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+)\)", src[src.index("#define YOLO_TILES"):])}
-    taps = {tuple(map(int, m.groups()[1:])): int(m.group(1)) for m in
-            re.finditer(r"X\((\d+), (\d), (\d+), (\d+), (\d+), (\d), (\d), (\d), (\d)\)",
-                        src[src.index("#define YOLO_TAP_TILES"):])}
-    wstaps = {tuple(map(int, m.groups()[1:])): int(m.group(1)) for m in
-              re.finditer(r"X\((\d+), (\d+), (\d+), (\d+), (\d), (\d), (\d), (\d)\)",
-                          src[src.index("#define YOLO_TAPWS_TILES"):])}
+    def table(macro):   # the X(...) rows of one tile table: index -> the template arguments
+        body = src[src.index(f"#define {macro}("):]
+        body = body[:body.index("\n\n")]
+        return {tuple(map(int, m.group(1).split(", ")[1:])): int(m.group(1).split(", ")[0])
+                for m in re.finditer(r"X\(([\d, ]+)\)", body)}
+    tiles, taps, wstaps = table("YOLO_TILES"), table("YOLO_TAP_TILES"), table("YOLO_TAPWS_TILES")
     km = {0: "1x1", 1: "uni", 2: "gen"}
 
     def demangle(name):
