@@ -46,6 +46,7 @@ def test_match_rule_hand_cases():
 
 CASES = {
     "C0": ("n", "detect", lambda: modelgen.synth_frame(810, 1080, 20, 1), 0.45),
+    "C2": ("m", "detect", lambda: modelgen.synth_frame(1080, 1920, 20, 2), 0.7),
     "C4": ("n", "segment", lambda: modelgen.synth_polygons(640, 640, 30, 4), 0.45),
 }
 
