@@ -1,5 +1,5 @@
-"""Profiling tools: HBM traffic per launch unit from rocprofv3 PMC passes, and the steady-state
-kernel time of a frame from a rocprofv3 kernel trace.
+"""Profiling tools: HBM traffic per launch unit (or per tile config of one conv shape) from
+rocprofv3 PMC passes, and the steady-state kernel time of a frame from a rocprofv3 kernel trace.
 
 HBM traffic per launch unit:
 
@@ -96,6 +96,83 @@ def collect(args):
     ec.close()
     eng.close()
     print(f"collected {args.passes} passes of {plan['num_units']} units", flush=True)
+
+
+def tiles(args):
+    """One conv shape under each of the given op configs (`--passes` launches of each, every
+    launch between two markers), then the scale-reference copy."""
+    import modelgen
+    import numpy as np
+    import yolort
+    k, st, H, cin, cout = args.shape
+    B = args.batch
+    work = tempfile.mkdtemp(prefix="yolo_tiles_")
+    d = os.path.join(work, "conv")
+    modelgen.write_single_conv(d, H, H, cin, cout, k, st, seed=1)
+    eng = yolort.Engine(d, B, yolort.YOLO_NOGRAPH | yolort.YOLO_NOTUNE)
+    eng.write(0, np.random.default_rng(1).standard_normal((B, H, H, cin), dtype=np.float32).astype(np.float16))
+    done = []
+    for cfg in args.cfgs:
+        try:
+            eng.set_op_config(0, cfg)
+        except ValueError:
+            continue
+        eng.run_op(0, B)
+        for _ in range(args.passes):
+            eng.marker()
+            eng.run_op(0, B)
+            eng.marker()
+        done.append(cfg)
+    eng.sync()
+    eng.close()
+    dc = os.path.join(work, "copy")
+    modelgen.write_copy(dc, *COPY_HWC)
+    ec = yolort.Engine(dc, B, yolort.YOLO_NOGRAPH | yolort.YOLO_NOTUNE)
+    ec.marker()
+    ec.run_unit(0, B)
+    ec.marker()
+    ec.sync()
+    ec.close()
+    ho = (H + 2 * (k // 2) - k) // st + 1
+    plan = {"shape": [k, st, H, cin, cout], "batch": B, "passes": args.passes, "cfgs": done,
+            "copy_bytes": 2.0 * B * COPY_HWC[0] * COPY_HWC[1] * COPY_HWC[2],
+            "input_bytes": 2.0 * B * H * H * cin, "weight_bytes": 2.0 * cout * k * k * cin,
+            "output_bytes": 2.0 * B * ho * ho * cout, "bias_bytes": 4.0 * cout}
+    json.dump(plan, open(args.plan, "w"))
+    print(f"collected {args.passes} launches of {len(done)} configs", flush=True)
+
+
+def tiles_summary(args):
+    """Markdown rows of `tiles` runs: per config, the median scaled FETCH and WRITE bytes of a
+    launch against the algorithmic bytes."""
+    import re
+    src = open(os.path.join(HERE, "csrc", "conv.hip")).read()
+    body = src[src.index("#define YOLO_TILES("):]
+    body = body[:body.index("\n\n")]
+    shapes = {int(m.group(1).split(", ")[0]): m.group(1).split(", ")[1:] for m in re.finditer(r"X\(([\d, ]+)\)", body)}
+    print("| shape | cfg | tile (BM, BN, WM, WN, BK, NS) | N tiles | fetch MB | write MB | traffic / algorithmic | "
+          "fetch / (input + weights) |")
+    print("|---|---|---|---|---|---|---|---|")
+    for pf, fdir, wdir in zip(args.plans[0::3], args.plans[1::3], args.plans[2::3]):
+        plan = json.load(open(pf))
+        n, cfgs = plan["passes"], plan["cfgs"]
+        res = {}
+        for counter, path in (("FETCH_SIZE", fdir), ("WRITE_SIZE", wdir)):
+            segs = _segments(path, counter)
+            if len(segs) != len(cfgs) * n + 1:
+                raise SystemExit(f"{path}: {len(segs)} marker segments, expected {len(cfgs) * n + 1}")
+            scale = plan["copy_bytes"] / sum(v for _, v in segs[-1])
+            res[counter] = [statistics.median(sum(v for _, v in segs[i * n + p]) for p in range(n)) * scale
+                            for i in range(len(cfgs))]
+        k, st, H, cin, cout = plan["shape"]
+        alg = plan["input_bytes"] + plan["weight_bytes"] + plan["output_bytes"] + plan["bias_bytes"]
+        for i, c in enumerate(cfgs):
+            t = shapes.get(c, ["?"] * 6)
+            ntn = -(-cout // int(t[1])) if t[1] != "?" else "?"
+            f, w = res["FETCH_SIZE"][i], res["WRITE_SIZE"][i]
+            print(f"| {k}x{k} s{st} {cin}->{cout} @{H}, b{plan['batch']} | {c} | ({', '.join(t)}) | {ntn} | "
+                  f"{f / 1e6:.1f} | {w / 1e6:.1f} | {(f + w) / alg:.2f}x | "
+                  f"{f / (plan['input_bytes'] + plan['weight_bytes']):.2f}x |")
 
 
 def _segments(path: str, counter: str) -> list[list[tuple[str, float]]]:
@@ -284,12 +361,21 @@ def main():
     s.add_argument("--write", required=True)
     s.add_argument("--json", required=True)
     s.add_argument("--md")
+    ti = sub.add_parser("tiles")
+    ti.add_argument("--shape", type=int, nargs=5, required=True, metavar=("K", "S", "H", "CIN", "COUT"))
+    ti.add_argument("--batch", type=int, default=16)
+    ti.add_argument("--cfgs", type=int, nargs="+", required=True)
+    ti.add_argument("--passes", type=int, default=3)
+    ti.add_argument("--plan", required=True)
+    ts = sub.add_parser("tiles-summary")
+    ts.add_argument("plans", nargs="+", help="triples: plan.json, FETCH_SIZE dir, WRITE_SIZE dir")
     t = sub.add_parser("trace")
     t.add_argument("csv", help="a rocprofv3 kernel_trace.csv, or the directory holding it")
     t.add_argument("--letterboxes-per-frame", type=int, default=1)
     t.add_argument("--top", type=int, default=32)
     args = ap.parse_args()
-    {"collect": collect, "summarize": summarize, "trace": trace}[args.cmd](args)
+    {"collect": collect, "summarize": summarize, "trace": trace, "tiles": tiles,
+     "tiles-summary": tiles_summary}[args.cmd](args)
 
 
 if __name__ == "__main__":
