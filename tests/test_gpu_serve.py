@@ -96,6 +96,60 @@ def _iou(a, b):
     return inter / u if u > 0 else 1.0
 
 
+def test_batcher_queue_rules_and_stop(models):
+    """The native worker's batching rules on one detect engine (max batch 4) and a target far
+    in the future: requests below the max batch are held; the fourth fills the queue and the
+    batch fires, each result equal to a batch-1 run of the same JPEG on a handle of the same
+    max batch (so the same kernel choices); requests queued at
+    stop are answered YOLO_BATCH_STOPPED (their tickets released), and later submits refused."""
+    d = models("yolo11", "n")
+    eng = yolort.Engine(d, 4, FLAGS)
+    direct = yolort.Engine(d, 4, FLAGS)   # the same max batch: the same kernel choices
+    frames = [modelgen.synth_frame(480, 640, 20, 700 + i) for i in range(6)]
+    jpegs = [_encode(f, "JPEG") for f in frames]
+    b = yolort.Batcher([eng], [4], target_ms=60000.0)
+    try:
+        for i in range(3):
+            assert b.submit_jpeg(0, jpegs[i], i) == 0
+        assert b.wait(300) == []                        # three of four: held
+        assert b.submit_jpeg(0, jpegs[3], 3) == 0       # full: fires
+        got = []
+        while len(got) < 4:
+            out = b.wait(5000)
+            assert out, "the full batch was not answered"
+            got += out
+        for r in sorted(got, key=lambda r: r["tag"]):
+            assert r["status"] == yolort.BATCH_OK and r["batch"] == 4 and r["model"] == 0
+            img = yoloserve.decode_image(jpegs[r["tag"]])
+            dev = yolort.DeviceBuffer(img.nbytes)
+            direct.upload(dev, img)
+            direct.preprocess(dev.ptr, img.shape[0], img.shape[1], 0)
+            direct.run(1)
+            want = direct.get(0)
+            dev.free()
+            assert r["rows"].shape == (len(want), 6)
+            np.testing.assert_array_equal(r["rows"][:, :5], want[:, :5].astype(np.float32))
+            np.testing.assert_array_equal(r["rows"][:, 5].astype(int), want[:, 5].astype(int))
+        for i in (4, 5):
+            assert b.submit_jpeg(0, jpegs[i], i) == 0
+        assert b.wait(300) == []
+        b.stop()
+        left = []
+        while True:
+            out = b.wait(5000)
+            if out is None:
+                break
+            left += out
+        assert sorted(r["tag"] for r in left) == [4, 5]
+        assert all(r["status"] == yolort.BATCH_STOPPED and len(r["rows"]) == 0 for r in left)
+        assert b.submit_jpeg(0, jpegs[0], 9) == -1
+    finally:
+        b.stop()
+        b.destroy()
+        eng.close()
+        direct.close()
+
+
 @pytest.mark.parametrize("frontends,native", [(0, True), (2, True), (0, False)],
                          ids=["native", "native-frontends", "python-loop"])
 def test_server_matches_direct_engine(models, frontends, native):

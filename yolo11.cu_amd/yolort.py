@@ -251,6 +251,9 @@ def jpeg_coefficients(data: bytes) -> np.ndarray | None:
     return out
 
 
+BATCH_OK, BATCH_DECODE_FAILED, BATCH_STOPPED = 0, 1, 2   # YoloBatchResult.status
+
+
 class Batcher:
     """The native batch worker (yolo_batcher_*): a deadline-aware batcher and the per-batch
     loop on a library thread.  The engines belong to it while it runs."""
