@@ -922,28 +922,28 @@ __global__ __launch_bounds__(256) void k_conv_first(View x, View y, const f16* _
 }
 
 // MFMA form of the stem (used when Cout % 16 == 0 and stride <= 2): K = 27 taps padded to
-// one 32-wide v_mfma_f32_16x16x32_f16 step.  A block owns FIRST_RB output rows x 128 output
+// one 32-wide v_mfma_f32_16x16x32_f16 step.  A block owns RB output rows x 128 output
 // columns x up to 128 output channels (grid (column segments, row groups, images x channel
-// blocks)).  Everything it reads is staged in LDS with coalesced loads: the input window
-// ((FIRST_RB-1)*s + 3 rows x (127*s + 3) columns x 3 channels, zeros outside the image), the
+// blocks); RB = 4, or 2 where that grid would leave CUs idle).  Everything it reads is staged
+// in LDS with coalesced loads: the input window
+// ((RB-1)*s + 3 rows x (127*s + 3) columns x 3 channels, zeros outside the image), the
 // weights and the biases.  Lane (p, g) then builds its B fragment (k = 8g .. 8g+7 of pixel p)
 // from LDS at a per-lane constant offset, and its A fragments (weight rows permuted as in the
 // GEMM so fragment pairs give 8 consecutive channels per lane) once per block.  Each
 // 16-pixel group's outputs pass through a per-wave LDS buffer so global stores are
 // contiguous 16-byte-per-lane runs.
 constexpr int FIRST_TP = 128;                        // output columns per block
-constexpr int FIRST_RB = 4;                          // output rows per block
 constexpr int FIRST_COLS = (FIRST_TP - 1) * 2 + 3;   // input columns (stride <= 2)
-constexpr int FIRST_ROWS = (FIRST_RB - 1) * 2 + 3;   // input rows (stride <= 2)
 // a window row is staged as 16-byte vectors from the 8-element boundary at or below its
 // first element: up to 7 leading elements, so FIRST_NV vectors per row
 constexpr int FIRST_NV = (7 + FIRST_COLS * 3 + 7) / 8;
 constexpr int FIRST_PITCH = FIRST_NV * 8;            // LDS row pitch (elements)
 
-template <bool PAIR>
+template <bool PAIR, int RB>
 __global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f16* __restrict__ w,
                                                          const float* __restrict__ bias, int cs,
                                                          int cp, int act, int ncb) {
+  constexpr int FIRST_ROWS = (RB - 1) * 2 + 3;   // input rows (stride <= 2)
   constexpr int NF = 8;   // 16-channel fragments per block (128 channels)
   constexpr int OPITCH = 16 * NF + 8;
   __shared__ __attribute__((aligned(16))) f16 tile[FIRST_ROWS][FIRST_PITCH];
@@ -952,10 +952,10 @@ __global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f
   __shared__ __attribute__((aligned(16))) f16 ostage[4][16 * OPITCH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  const int ox0 = blockIdx.x * FIRST_TP, oy0 = blockIdx.y * FIRST_RB;
+  const int ox0 = blockIdx.x * FIRST_TP, oy0 = blockIdx.y * RB;
   const int img = blockIdx.z / ncb, cb = (blockIdx.z - img * ncb) * 16 * NF;
   const int nf = min(NF, (y.C - cb) / 16);
-  const int rows = (FIRST_RB - 1) * cs + 3;
+  const int rows = (RB - 1) * cs + 3;
   const int ix0 = ox0 * cs - cp, iy0 = oy0 * cs - cp;
 
   // ---- stage input window, weights, biases: every global load is issued before the first
@@ -1040,7 +1040,7 @@ __global__ __launch_bounds__(256) void k_conv_first_mfma(View x, View y, const f
   // lane's first (pixel, chunk) of the output exchange and the per-step advance of 64 items
   const int pxl = lane / chunks, ckl = lane - pxl * chunks;
   const int pxs = 64 / chunks, cks = 64 - pxs * chunks;
-  for (int rr = 0; rr < FIRST_RB; rr++) {
+  for (int rr = 0; rr < RB; rr++) {
     const int oy = oy0 + rr;
     if (oy >= y.H) break;                    // block-uniform
 #pragma unroll
@@ -1085,12 +1085,27 @@ void launchConvFirst(const View& x, const View& y, const f16* w, const float* bi
   // the MFMA form stages input rows as 16-byte vectors: a dense 3-channel input whose rows
   // are 16-byte multiples
   if (y.C % 16 == 0 && s >= 1 && s <= 2 && x.s == 3 && x.o == 0 && (x.W * 3) % 8 == 0) {
+    static const int cus = [] {
+      int dev = 0, n = 0;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 256;
+      return n;
+    }();
     const int ncb = (y.C + 127) / 128;
-    dim3 grid((y.W + FIRST_TP - 1) / FIRST_TP, (y.H + FIRST_RB - 1) / FIRST_RB, Bn * ncb);
-    if (y.C % 32 == 0)
-      k_conv_first_mfma<true><<<grid, 256, 0, st>>>(x, y, w, bias, s, p, act, ncb);
-    else
-      k_conv_first_mfma<false><<<grid, 256, 0, st>>>(x, y, w, bias, s, p, act, ncb);
+    const int cols = (y.W + FIRST_TP - 1) / FIRST_TP;
+    // 4 rows per block, or 2 where that would give fewer than two blocks per CU (each output
+    // is the same single MFMA step either way, so the choice never changes a value)
+    const bool small = (long)cols * ((y.H + 3) / 4) * Bn * ncb < 2L * cus;
+    const int rb = small ? 2 : 4;
+    dim3 grid(cols, (y.H + rb - 1) / rb, Bn * ncb);
+    if (y.C % 32 == 0) {
+      if (small) k_conv_first_mfma<true, 2><<<grid, 256, 0, st>>>(x, y, w, bias, s, p, act, ncb);
+      else k_conv_first_mfma<true, 4><<<grid, 256, 0, st>>>(x, y, w, bias, s, p, act, ncb);
+    } else {
+      if (small) k_conv_first_mfma<false, 2><<<grid, 256, 0, st>>>(x, y, w, bias, s, p, act, ncb);
+      else k_conv_first_mfma<false, 4><<<grid, 256, 0, st>>>(x, y, w, bias, s, p, act, ncb);
+    }
   } else {
     k_conv_first<<<(M + 255) / 256, 256, 0, st>>>(x, y, w, bias, s, p, act, M);
   }
