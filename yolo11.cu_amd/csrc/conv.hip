@@ -1458,6 +1458,15 @@ __global__ __launch_bounds__(256) void k_conv1x1_stream(View x, View y, View r, 
       dst[kc] = val;
     }
   };
+  // LDS byte address of this lane's weight row in fragment f, 32-channel chunk 0 (chunk kc at
+  // +64 kc): the weights are read one chunk at a time through inline ds_reads, the next
+  // chunk's in flight while the current one's MFMAs run, so only two chunks' fragments are
+  // live (plain loads let the compiler hoist every chunk's fragments, KC x FN of them, and
+  // spill at KC = 12)
+  unsigned wbf[FN];
+#pragma unroll
+  for (int f = 0; f < FN; f++)
+    wbf[f] = (unsigned)(size_t)(lds_f16x8)(f16x8*)wl + 2u * (unsigned)((f * 16 + lr) * CP + 8 * lg);
   int gi = blockIdx.x * 4 + wave;
   f16x8 buf[PD + 1][KC];
 #pragma unroll
@@ -1472,13 +1481,18 @@ __global__ __launch_bounds__(256) void k_conv1x1_stream(View x, View y, View r, 
       f32x4 acc[FN];
 #pragma unroll
       for (int f = 0; f < FN; f++) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kc = 0; kc < KC; kc++)
-#pragma unroll
-        for (int f = 0; f < FN; f++) {
-          const f16x8 wf = *(const f16x8*)&wl[(f * 16 + lr) * CP + kc * 32 + 8 * lg];
-          acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, cur[kc], acc[f], 0, 0, 0);
-        }
+      f16x8 wf[2][FN];
+      static_for<FN>([&](auto I) { wf[0][I] = ds_read16<0>(wbf[I]); });
+      static_for<KC>([&](auto K) {
+        constexpr int kc = decltype(K)::value, c = kc % 2;
+        if constexpr (kc + 1 < KC) static_for<FN>([&](auto I) { wf[1 - c][I] = ds_read16<64 * (kc + 1)>(wbf[I]); });
+        lgkm_wait<(kc + 1 < KC) ? FN : 0>();   // chunk kc's fragments have landed
+        static_for<FN>([&](auto I) {
+          asm volatile("" : "+v"(wf[c][I]));
+          acc[I] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[c][I], cur[kc], acc[I], 0, 0, 0);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      });
       const int m = g * 16 + lr;
       if (m >= M) continue;
       if constexpr (PAIR) {
@@ -1530,11 +1544,21 @@ __global__ __launch_bounds__(256) void k_conv1x1_stream(View x, View y, View r, 
   }
 }
 
-// The two-groups-in-flight variant (op config CFG_1X1S): same instantiations and slices as
-// the resident kernel; 16-byte stores need the view strides and offsets 8-aligned.
+// Output channels per slice of the streaming variant: up to 128 at every KC (its chunked
+// weight reads keep the registers), evened out, rounded up to an instantiated fragment count.
+static int conv1x1StreamFN(int cout) {
+  const int slices = (cout + 127) / 128;
+  const int need = ((cout + slices - 1) / slices + 15) / 16;
+  for (int fn : {1, 2, 3, 4, 6, 8})
+    if (fn >= need) return fn;
+  return 0;
+}
+
+// The streaming variant (op config CFG_1X1S); 16-byte stores need the view strides and
+// offsets 8-aligned.
 bool conv1x1StreamOk(const View& x, const View& y, const View* r, int k, int s, int p) {
   if (!conv1x1Ok(x, y, r, k, s, p)) return false;
-  const int fn = conv1x1FN(y.C, conv1x1KC(x.C));
+  const int fn = conv1x1StreamFN(y.C);
   if (fn % 2 == 0 && (y.s % 8 || y.o % 8 || (r && (r->s % 8 || r->o % 8)))) return false;
   return true;
 }
@@ -1549,17 +1573,20 @@ void launchConv1x1Stream(const View& x, const View& y, const View* res, const f1
     return n;
   }();
   const View r = res ? *res : View{nullptr, 0, 0, 0, 0, 0};
-  const int M = Bn * y.H * y.W, kc = conv1x1KC(x.C), fn = conv1x1FN(y.C, kc);
+  const int M = Bn * y.H * y.W, kc = conv1x1KC(x.C), fn = conv1x1StreamFN(y.C);
   const int slices = (y.C + 16 * fn - 1) / (16 * fn);
   const int groups = (M + 15) / 16;
-  int gx = std::max(1, 4 * cus / slices);
+  // persistent: the blocks the chip holds at once (LDS allows up to four per CU), each wave
+  // with at least one pixel group
+  const long lds = 2L * 16 * fn * (32 * kc + 8);
+  const int per = (int)std::max(1L, std::min(4L, 160L * 1024 / lds));
+  int gx = std::max(1, per * cus / slices);
   gx = std::min(gx, (groups + 3) / 4);
   const dim3 grid(gx, slices);
 #define P2_CASE(KC, FN) \
   if (kc == KC && fn == FN) { k_conv1x1_stream<KC, FN, 2><<<grid, 256, 0, st>>>(x, y, r, w, bias, act, M); return; }
 #define P2_ROW(KC) P2_CASE(KC, 1) P2_CASE(KC, 2) P2_CASE(KC, 3) P2_CASE(KC, 4) P2_CASE(KC, 6) P2_CASE(KC, 8)
-  P2_ROW(1) P2_ROW(2) P2_ROW(3) P2_ROW(4) P2_ROW(6) P2_ROW(8)
-  P2_CASE(12, 1) P2_CASE(12, 2) P2_CASE(12, 3) P2_CASE(12, 4)
+  P2_ROW(1) P2_ROW(2) P2_ROW(3) P2_ROW(4) P2_ROW(6) P2_ROW(8) P2_ROW(12)
 #undef P2_ROW
 #undef P2_CASE
 }
