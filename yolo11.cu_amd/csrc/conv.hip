@@ -1315,6 +1315,12 @@ __global__ __launch_bounds__(256) void k_conv1x1_resident(View x, View y, View r
       dst[kc] = val;
     }
   };
+  // weight fragments read one 32-channel chunk at a time (as in k_conv1x1_stream): this
+  // lane's row of fragment f at wbf[f], chunk kc at +64 kc
+  unsigned wbf[FN];
+#pragma unroll
+  for (int f = 0; f < FN; f++)
+    wbf[f] = (unsigned)(size_t)(lds_f16x8)(f16x8*)wl + 2u * (unsigned)((f * 16 + lr) * CP + 8 * lg);
   int gi = blockIdx.x * 4 + wave;
   f16x8 cur[KC], nxt[KC];
   fetch(gi, cur);
@@ -1323,13 +1329,18 @@ __global__ __launch_bounds__(256) void k_conv1x1_resident(View x, View y, View r
     f32x4 acc[FN];
 #pragma unroll
     for (int f = 0; f < FN; f++) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kc = 0; kc < KC; kc++)
-#pragma unroll
-      for (int f = 0; f < FN; f++) {
-        const f16x8 wf = *(const f16x8*)&wl[(f * 16 + lr) * CP + kc * 32 + 8 * lg];
-        acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, cur[kc], acc[f], 0, 0, 0);
-      }
+    f16x8 wf[2][FN];
+    static_for<FN>([&](auto I) { wf[0][I] = ds_read16<0>(wbf[I]); });
+    static_for<KC>([&](auto K) {
+      constexpr int kc = decltype(K)::value, c = kc % 2;
+      if constexpr (kc + 1 < KC) static_for<FN>([&](auto I) { wf[1 - c][I] = ds_read16<64 * (kc + 1)>(wbf[I]); });
+      lgkm_wait<(kc + 1 < KC) ? FN : 0>();   // chunk kc's fragments have landed
+      static_for<FN>([&](auto I) {
+        asm volatile("" : "+v"(wf[c][I]));
+        acc[I] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[c][I], cur[kc], acc[I], 0, 0, 0);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
     const int m = gi * 16 + lr;
     if (m < M) {
 #pragma unroll
