@@ -191,6 +191,7 @@ int yolo_get_masks(void* h, int slot, int first, int n, unsigned char* out);
 #define YOLO_BATCH_OK 0
 #define YOLO_BATCH_DECODE_FAILED 1  /* corrupt stream, or past what one batch decode holds */
 #define YOLO_BATCH_STOPPED 2
+#define YOLO_BATCH_FAILED 3         /* the batch could not be staged or its results built (host memory) */
 typedef struct {
   long long tag;
   int status, model, task, batch;

@@ -15,8 +15,10 @@
 //               RLE masks at proto resolution with the letterbox geometry);
 //   stage    -- letterbox the decoded JPEG frames and stage the pixel frames (one launch);
 //   launch   -- the batch graph, asynchronously.
-// A stream the engine cannot decode fails only its own request.  A device failure ends the
-// process, as everywhere in this library (engine/engine.cu:20-21).
+// A stream the engine cannot decode fails only its own request; a batch that cannot be staged
+// or whose results cannot be built (host allocation) fails only its own requests, and the
+// worker goes on.  A device failure ends the process, as everywhere in this library
+// (engine/engine.cu:20-21).
 #include <algorithm>
 #include <chrono>
 #include <condition_variable>
@@ -195,8 +197,35 @@ class Batcher {
     return d;
   }
 
-  // Reads a launched batch's results into finished requests.
+  // Reads a launched batch's results into finished requests; if that fails (host allocation),
+  // the batch's requests are answered YOLO_BATCH_FAILED.
   void finish(Batch& b) {
+    try {
+      finishResults(b);
+    } catch (...) {
+      failAll(b, YOLO_BATCH_FAILED);
+    }
+    b.reqs.clear();
+  }
+
+  // Answers every request of a batch with `status`, releasing tickets not yet consumed.
+  void failAll(Batch& b, int status) {
+    std::vector<Done*> out;
+    try {
+      for (Req& q : b.reqs) {
+        if (q.ticket) {
+          yolo_jpeg_release(q.ticket);
+          q.ticket = nullptr;
+        }
+        out.push_back(failure(q, b.model, status));
+      }
+      publish(out);
+    } catch (...) {
+      for (Done* d : out) delete d;   // nothing more can be done without memory
+    }
+  }
+
+  void finishResults(Batch& b) {
     Model& m = models_[b.model];
     yolo_sync(m.eng);
     const auto now = Clock::now();
@@ -296,13 +325,40 @@ class Batcher {
       d->r.rle_len = d->rleLen.empty() ? nullptr : d->rleLen.data();
     }
     publish(out);
-    b.reqs.clear();
   }
 
   void work() {
     Batch prev, cur;
     bool havePrev = false;
     while (collect(cur)) {
+      try {
+        step(prev, cur, havePrev);
+      } catch (...) {
+        failAll(cur, YOLO_BATCH_FAILED);   // host allocation: this batch only
+        cur.reqs.clear();
+      }
+    }
+    if (havePrev) finish(prev);
+    // stopped: whatever is still queued is answered, tickets released
+    for (int i = 0; i < (int)models_.size(); i++) {
+      Batch left;
+      left.model = i;
+      {
+        std::lock_guard<std::mutex> lk(mu_);
+        left.reqs.assign(models_[i].q.begin(), models_[i].q.end());
+        models_[i].q.clear();
+      }
+      failAll(left, YOLO_BATCH_STOPPED);
+    }
+    std::lock_guard<std::mutex> lk(mu_);
+    finished_ = true;
+    doneCv_.notify_all();
+  }
+
+  // One batch: decode its JPEG tickets (the previous batch still runs), answer the previous
+  // batch, stage and launch this one.
+  void step(Batch& prev, Batch& cur, bool& havePrev) {
+    {
       Model& m = models_[cur.model];
       const auto t0 = Clock::now();
       // engine-decoded JPEG streams take the first slots, pixel frames the rest
@@ -357,23 +413,8 @@ class Batcher {
         havePrev = false;
       }
     }
-    if (havePrev) finish(prev);
-    // stopped: whatever is still queued is answered, tickets released
-    std::vector<Done*> out;
-    {
-      std::lock_guard<std::mutex> lk(mu_);
-      for (int i = 0; i < (int)models_.size(); i++)
-        for (Req& q : models_[i].q) {
-          if (q.ticket) yolo_jpeg_release(q.ticket);
-          out.push_back(failure(q, i, YOLO_BATCH_STOPPED));
-        }
-      for (auto& m : models_) m.q.clear();
-    }
-    publish(out);
-    std::lock_guard<std::mutex> lk(mu_);
-    finished_ = true;
-    doneCv_.notify_all();
   }
+
 
   std::vector<Model> models_;
   double targetMs_, stageEma_ = 1.0;

@@ -251,7 +251,7 @@ def jpeg_coefficients(data: bytes) -> np.ndarray | None:
     return out
 
 
-BATCH_OK, BATCH_DECODE_FAILED, BATCH_STOPPED = 0, 1, 2   # YoloBatchResult.status
+BATCH_OK, BATCH_DECODE_FAILED, BATCH_STOPPED, BATCH_FAILED = 0, 1, 2, 3   # YoloBatchResult.status
 
 
 class Batcher:

@@ -437,7 +437,9 @@ class Server:
         resp.task = m.task_name
         self._release([r])                # the batch has run: its frame buffer is free
         if rec["status"] != 0:
-            r.error = "image decode failed" if rec["status"] == 1 else "server shutting down"
+            import yolort                 # loaded already: this path runs with a native batcher
+            r.error = {yolort.BATCH_DECODE_FAILED: "image decode failed",
+                       yolort.BATCH_STOPPED: "server shutting down"}.get(rec["status"], "batch failed")
             r.finish()
             return
         resp.queue_ms = rec["queue_ms"]
