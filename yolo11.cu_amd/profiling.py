@@ -1,5 +1,6 @@
-"""Profiling tools: HBM traffic per launch unit (or per tile config of one conv shape) from
-rocprofv3 PMC passes, and the steady-state kernel time of a frame from a rocprofv3 kernel trace.
+"""Profiling tools: HBM traffic per launch unit (or per tile config of one conv shape) and
+matrix-pipe occupancy per launch unit from rocprofv3 PMC passes, and the steady-state kernel
+time of a frame from a rocprofv3 kernel trace.
 
 HBM traffic per launch unit:
 
@@ -175,8 +176,9 @@ def tiles_summary(args):
                   f"{f / (plan['input_bytes'] + plan['weight_bytes']):.2f}x |")
 
 
-def _segments(path: str, counter: str) -> list[list[tuple[str, float]]]:
-    """Dispatches between marker pairs, in dispatch order: [[(kernel, value), ...], ...]."""
+def _segments(path: str, counter: str, unit: float = 1024.0) -> list[list[tuple[str, float]]]:
+    """Dispatches between marker pairs, in dispatch order: [[(kernel, value), ...], ...]; values
+    times `unit` (the byte counters read KiB)."""
     f = path if path.endswith(".csv") else glob.glob(os.path.join(path, "*counter_collection.csv"))[0]
     per = {}
     for r in csv.DictReader(open(f)):
@@ -195,7 +197,7 @@ def _segments(path: str, counter: str) -> list[list[tuple[str, float]]]:
                 segs.append(cur)
                 cur = None
         elif cur is not None:
-            cur.append((name, v * 1024.0))     # the counters read KiB
+            cur.append((name, v * unit))
     return segs
 
 
@@ -287,6 +289,74 @@ def _markdown(out, args):
     open(args.md, "w").write("\n".join(lines) + "\n")
 
 
+def mfma(args):
+    """Matrix-pipe occupancy per launch unit, from a `collect` run under
+    `rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE`.  SQ_VALU_MFMA_BUSY_CYCLES adds each
+    MFMA's pipe cycles on its SIMD: 16 for a v_mfma_f32_16x16x32_f16 (16,384 FLOPs), so busy x
+    1,024 is the FLOP count the MFMAs executed, padded rows and channels included.
+    GRBM_GUI_ACTIVE adds the dispatch's cycles over the XCDs, so GUI_ACTIVE / XCDs x SIMDs is
+    the SIMD-cycles the dispatch held; busy over that is the matrix pipe's share of them, the
+    MFMA utilisation at the clock the dispatch ran at (dispatches run one at a time under the
+    counters)."""
+    plan = json.load(open(args.plan))
+    nu, passes = plan["num_units"], plan["passes"]
+    agent = glob.glob(os.path.join(args.pmc, "*agent_info.csv"))
+    gpu = next(r for r in csv.DictReader(open(agent[0])) if r.get("Name", "").startswith("gfx"))
+    simds, xcds = int(gpu["Simd_Count"]), int(gpu["Num_Xcc"])
+    busy = _segments(args.pmc, "SQ_VALU_MFMA_BUSY_CYCLES", 1.0)
+    act = _segments(args.pmc, "GRBM_GUI_ACTIVE", 1.0)
+    for segs in (busy, act):
+        if len(segs) != nu * passes + 1:
+            raise SystemExit(f"{len(segs)} marker segments, expected {nu * passes + 1}")
+    classes, rows = {}, []
+    for info in plan["units"]:
+        if not info["flops"]:
+            continue
+        u = info["unit"]
+        b = statistics.median(sum(v for _, v in busy[p * nu + u]) for p in range(passes))
+        a = statistics.median(sum(v for _, v in act[p * nu + u]) for p in range(passes))
+        cyc = a / xcds * simds
+        name = "attention" if info["kernel"].startswith("k_attention") else info["class"]
+        c = classes.setdefault(name, [0, 0.0, 0.0, 0.0])
+        c[0] += 1
+        c[1] += info["flops"]
+        c[2] += b * 1024.0
+        c[3] += cyc
+        rows.append((info["first"], info["kernel"], info["class"], info["flops"], b * 1024.0, cyc))
+    conv = [v for k, v in classes.items() if k != "attention"]
+    tf, te, tc = (sum(v[i] for v in conv) for i in (1, 2, 3))
+    lines = [f"# Matrix-pipe occupancy per launch unit: {plan['model']} detect, batch {plan['batch']}", "",
+             "One `rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE` pass over every launch unit of",
+             f"the frame (each unit between two marker kernels, median over {passes} passes; dispatches run",
+             "one at a time under the counters).  Executed = busy cycles x 1,024 FLOPs (a",
+             "v_mfma_f32_16x16x32_f16 holds its SIMD's matrix pipe 16 cycles for 16,384 FLOPs), padding",
+             "included; algorithmic = `2*B*Ho*Wo*Cout*k^2*Cin/g` (yolo11.cu_amd/unitwork.py).  Busy share =",
+             f"busy / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} SIMDs), the MFMA utilisation at the clock the",
+             "dispatch ran at (algorithmic share: the same with algorithmic FLOPs).", "", "```",
+             f"OUT=gpurun_out/mfma_{plan['model'][-1]}",
+             "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE --output-format csv -d $OUT/pmc -o run -- "
+             f"python3 yolo11.cu_amd/profiling.py collect --scale {plan['model'][-1]} --batch {plan['batch']} "
+             f"--passes {passes} --plan $OUT/plan.json",
+             f"python3 yolo11.cu_amd/profiling.py mfma --plan $OUT/plan.json --pmc $OUT/pmc --md {args.md}", "```", "",
+             f"Conv units: {tf / 1e12:.3f} TFLOP algorithmic, {te / 1e12:.3f} TFLOP executed "
+             f"({te / tf:.3f}x); matrix pipe busy {te / 1024 / tc:.3f} of the SIMD-cycles "
+             f"(algorithmic {tf / 1024 / tc:.3f}).", "",
+             "| class | units | algorithmic GFLOP | executed GFLOP | executed / algorithmic | busy share | "
+             "algorithmic share |", "|---|---|---|---|---|---|---|"]
+    for name, (n, f, e, c) in sorted(classes.items(), key=lambda kv: -kv[1][3]):
+        lines.append(f"| {name} | {n} | {f / 1e9:.1f} | {e / 1e9:.1f} | {e / f:.3f} | {e / 1024 / c:.3f} | "
+                     f"{f / 1024 / c:.3f} |")
+    lines += ["", "Units holding the most SIMD-cycles:", "",
+              "| first op | kernel | class | algorithmic GFLOP | executed / algorithmic | busy share |",
+              "|---|---|---|---|---|---|"]
+    for first, kern, cls, f, e, c in sorted(rows, key=lambda r: -r[5])[:args.top]:
+        lines.append(f"| {first} | {kern} | {cls} | {f / 1e9:.2f} | {e / f:.3f} | {e / 1024 / c:.3f} |")
+    text = "\n".join(lines) + "\n"
+    if args.md:
+        open(args.md, "w").write(text)
+    print(text)
+
+
 def trace(args):
     """Steady-state kernel time per frame from a `rocprofv3 --kernel-trace` CSV of
     `bench.py --only <n|x> --no-graph` (stream-ordered launches of the frame's kernels): every
@@ -369,13 +439,18 @@ def main():
     ti.add_argument("--plan", required=True)
     ts = sub.add_parser("tiles-summary")
     ts.add_argument("plans", nargs="+", help="triples: plan.json, FETCH_SIZE dir, WRITE_SIZE dir")
+    mf = sub.add_parser("mfma")
+    mf.add_argument("--plan", required=True, help="the collect run's plan")
+    mf.add_argument("--pmc", required=True, help="its rocprofv3 output directory")
+    mf.add_argument("--md")
+    mf.add_argument("--top", type=int, default=20)
     t = sub.add_parser("trace")
     t.add_argument("csv", help="a rocprofv3 kernel_trace.csv, or the directory holding it")
     t.add_argument("--letterboxes-per-frame", type=int, default=1)
     t.add_argument("--top", type=int, default=32)
     args = ap.parse_args()
     {"collect": collect, "summarize": summarize, "trace": trace, "tiles": tiles,
-     "tiles-summary": tiles_summary}[args.cmd](args)
+     "tiles-summary": tiles_summary, "mfma": mfma}[args.cmd](args)
 
 
 if __name__ == "__main__":
