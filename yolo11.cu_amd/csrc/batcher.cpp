@@ -17,8 +17,8 @@
 //   launch   -- the batch graph, asynchronously.
 // A stream the engine cannot decode fails only its own request; a batch that cannot be staged
 // or whose results cannot be built (host allocation) fails only its own requests, and the
-// worker goes on.  A device failure ends the process, as everywhere in this library
-// (engine/engine.cu:20-21).
+// worker goes on; a request the queue has no memory for is refused at submission.  A device
+// failure ends the process, as everywhere in this library (engine/engine.cu:20-21).
 #include <algorithm>
 #include <chrono>
 #include <condition_variable>
@@ -98,7 +98,11 @@ class Batcher {
     std::lock_guard<std::mutex> lk(mu_);
     if (stop_) return -1;
     auto& q = models_[model].q;
-    q.push_back(r);
+    try {
+      q.push_back(r);
+    } catch (...) {
+      return -1;   // host allocation: refused like a submit after stop
+    }
     // only a queue that starts (its slack now counts) or fills changes the batcher's choice
     if (q.size() == 1 || (int)q.size() >= models_[model].maxB) cv_.notify_all();
     return 0;
@@ -179,10 +183,12 @@ class Batcher {
     }
   }
 
+  // All or nothing: a range insert of pointers at the end of a deque has no effect if it
+  // throws, so on failure every record is still the caller's to free.
   void publish(std::vector<Done*>& ds) {
     if (ds.empty()) return;
     std::lock_guard<std::mutex> lk(mu_);
-    for (Done* d : ds) done_.push_back(d);
+    done_.insert(done_.end(), ds.begin(), ds.end());
     ds.clear();
     doneCv_.notify_all();
   }
@@ -212,6 +218,7 @@ class Batcher {
   void failAll(Batch& b, int status) {
     std::vector<Done*> out;
     try {
+      out.reserve(b.reqs.size());
       for (Req& q : b.reqs) {
         if (q.ticket) {
           yolo_jpeg_release(q.ticket);
@@ -243,94 +250,111 @@ class Batcher {
     }
     std::vector<unsigned char> masks;
     std::vector<Done*> out;
-    for (int s = 0; s < B; s++) {
-      const Req& q = b.reqs[s];
-      if (q.failed) {
-        out.push_back(failure(q, b.model, YOLO_BATCH_DECODE_FAILED));
-        continue;
-      }
-      Done* d = new Done;
-      YoloBatchResult& r = d->r;
-      r.tag = q.tag;
-      r.model = b.model;
-      r.task = m.task;
-      r.batch = B;
-      r.queue_ms = (float)msSince(q.arrival, b.launch);
-      r.infer_ms = (float)inferMs;
-      r.host = q.host;
-      if (m.task == 2) {
-        int ids[kTopK];
-        float probs[kTopK];
-        const int n = yolo_get_cls(m.eng, s, ids, probs, kTopK);
-        d->rows.resize((size_t)2 * n);
-        for (int j = 0; j < n; j++) {
-          d->rows[2 * j] = (float)ids[j];
-          d->rows[2 * j + 1] = probs[j];
+    try {
+      out.reserve(B);   // the pushes below cannot throw: every record is freed on failure
+      for (int s = 0; s < B; s++) {
+        const Req& q = b.reqs[s];
+        if (q.failed) {
+          out.push_back(failure(q, b.model, YOLO_BATCH_DECODE_FAILED));
+          continue;
         }
-        r.n = n;
-        r.stride = 2;
-      } else if (m.task == 1) {
-        const int n = counts[s];
-        d->rows.resize((size_t)7 * n);
-        for (int j = 0; j < n; j++) {
-          const YoloObbDet& o = obbs[(size_t)s * kMaxDet + j];
-          const float v[7] = {o.x, o.y, o.w, o.h, o.angle, o.score, (float)o.cls};
-          std::memcpy(&d->rows[7 * j], v, sizeof v);
-        }
-        r.n = n;
-        r.stride = 7;
-      } else {
-        const int n = counts[s];
-        d->rows.resize((size_t)6 * n);
-        for (int j = 0; j < n; j++) {
-          const YoloDet& o = dets[(size_t)s * kMaxDet + j];
-          const float v[6] = {o.x1, o.y1, o.x2, o.y2, o.score, (float)o.cls};
-          std::memcpy(&d->rows[6 * j], v, sizeof v);
-        }
-        r.n = n;
-        r.stride = 6;
-        if (m.task == 3) {
-          yolo_slot_geom(m.eng, s, &r.lb_scale, &r.lb_top, &r.lb_left);
-          r.mask_h = m.mh;
-          r.mask_w = m.mw;
-          const size_t px = (size_t)m.mh * m.mw;
-          masks.resize(px * std::max(n, 1));
-          if (n > 0 && yolo_get_masks(m.eng, s, 0, n, masks.data()) != 0) std::memset(masks.data(), 0, px * n);
-          d->rleLen.resize(n);
+        Done* d = new Done;
+        out.push_back(d);
+        YoloBatchResult& r = d->r;
+        r.tag = q.tag;
+        r.model = b.model;
+        r.task = m.task;
+        r.batch = B;
+        r.queue_ms = (float)msSince(q.arrival, b.launch);
+        r.infer_ms = (float)inferMs;
+        r.host = q.host;
+        if (m.task == 2) {
+          int ids[kTopK];
+          float probs[kTopK];
+          const int n = yolo_get_cls(m.eng, s, ids, probs, kTopK);
+          d->rows.resize((size_t)2 * n);
           for (int j = 0; j < n; j++) {
-            // alternating 0/1 runs, row-major, starting with a 0-run (server/serve.cpp:193-203)
-            const unsigned char* mk = masks.data() + px * j;
-            const size_t start = d->rle.size();
-            unsigned run = 0;
-            bool cur = false;
-            for (size_t p = 0; p < px; p++) {
-              const bool v = mk[p] != 0;
-              if (v != cur) {
-                d->rle.push_back(run);
-                run = 0;
-                cur = v;
+            d->rows[2 * j] = (float)ids[j];
+            d->rows[2 * j + 1] = probs[j];
+          }
+          r.n = n;
+          r.stride = 2;
+        } else if (m.task == 1) {
+          const int n = counts[s];
+          d->rows.resize((size_t)7 * n);
+          for (int j = 0; j < n; j++) {
+            const YoloObbDet& o = obbs[(size_t)s * kMaxDet + j];
+            const float v[7] = {o.x, o.y, o.w, o.h, o.angle, o.score, (float)o.cls};
+            std::memcpy(&d->rows[7 * j], v, sizeof v);
+          }
+          r.n = n;
+          r.stride = 7;
+        } else {
+          const int n = counts[s];
+          d->rows.resize((size_t)6 * n);
+          for (int j = 0; j < n; j++) {
+            const YoloDet& o = dets[(size_t)s * kMaxDet + j];
+            const float v[6] = {o.x1, o.y1, o.x2, o.y2, o.score, (float)o.cls};
+            std::memcpy(&d->rows[6 * j], v, sizeof v);
+          }
+          r.n = n;
+          r.stride = 6;
+          if (m.task == 3) {
+            yolo_slot_geom(m.eng, s, &r.lb_scale, &r.lb_top, &r.lb_left);
+            r.mask_h = m.mh;
+            r.mask_w = m.mw;
+            const size_t px = (size_t)m.mh * m.mw;
+            masks.resize(px * std::max(n, 1));
+            if (n > 0 && yolo_get_masks(m.eng, s, 0, n, masks.data()) != 0) std::memset(masks.data(), 0, px * n);
+            d->rleLen.resize(n);
+            for (int j = 0; j < n; j++) {
+              // alternating 0/1 runs, row-major, starting with a 0-run (server/serve.cpp:193-203)
+              const unsigned char* mk = masks.data() + px * j;
+              const size_t start = d->rle.size();
+              unsigned run = 0;
+              bool cur = false;
+              for (size_t p = 0; p < px; p++) {
+                const bool v = mk[p] != 0;
+                if (v != cur) {
+                  d->rle.push_back(run);
+                  run = 0;
+                  cur = v;
+                }
+                run++;
               }
-              run++;
+              d->rle.push_back(run);
+              d->rleLen[j] = (int)(d->rle.size() - start);
             }
-            d->rle.push_back(run);
-            d->rleLen[j] = (int)(d->rle.size() - start);
           }
         }
       }
-      out.push_back(d);
+      for (Done* d : out) {   // pointers into the vectors, now that they are final
+        d->r.rows = d->rows.empty() ? nullptr : d->rows.data();
+        d->r.rle = d->rle.empty() ? nullptr : d->rle.data();
+        d->r.rle_len = d->rleLen.empty() ? nullptr : d->rleLen.data();
+      }
+      publish(out);
+    } catch (...) {   // nothing of this batch was published: the caller answers all of it
+      for (Done* d : out) delete d;
+      throw;
     }
-    for (Done* d : out) {   // pointers into the vectors, now that they are final
-      d->r.rows = d->rows.empty() ? nullptr : d->rows.data();
-      d->r.rle = d->rle.empty() ? nullptr : d->rle.data();
-      d->r.rle_len = d->rleLen.empty() ? nullptr : d->rleLen.data();
-    }
-    publish(out);
   }
 
   void work() {
     Batch prev, cur;
     bool havePrev = false;
-    while (collect(cur)) {
+    for (;;) {
+      bool got;
+      try {
+        got = collect(cur);
+      } catch (...) {
+        // host allocation while copying a batch out of its queue: the queue is unchanged
+        // (the copy comes before the erase), so its requests are taken again shortly
+        cur.reqs.clear();
+        std::this_thread::sleep_for(std::chrono::milliseconds(1));
+        continue;
+      }
+      if (!got) break;
       try {
         step(prev, cur, havePrev);
       } catch (...) {
