@@ -149,7 +149,8 @@ int yolo_decode_tickets(void* h, int B, void* const* tickets, int first_slot, in
                         int* status);
 void yolo_jpeg_release(void* ticket);
 int yolo_jpeg_probe(const unsigned char* data, size_t size, int* height, int* width);
-/* Threads (the calling one included) the JPEG entropy decoding runs on. */
+/* Threads (the calling one included) the JPEG entropy decoding runs on; -1 if they cannot be
+ * started. */
 int yolo_decoder_threads(void);
 /* The largest frame, in pixels (height x width), the engine decodes: larger JPEG streams are
  * reported outside the set (yolo_jpeg_probe 0, yolo_jpeg_submit NULL, status

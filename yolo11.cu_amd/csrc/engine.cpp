@@ -1285,13 +1285,18 @@ void yolo_destroy(void* h) {
 }
 
 int yolo_graph_check(const char* model_dir, char* err, int errlen) {
-  yolo::GraphDesc g;
-  std::string msg;
-  if (!yolo::parseGraph(model_dir, g, msg) || !yolo::validateGraph(g, msg)) {
-    setErr(err, errlen, msg.c_str());
+  try {
+    yolo::GraphDesc g;
+    std::string msg;
+    if (!yolo::parseGraph(model_dir, g, msg) || !yolo::validateGraph(g, msg)) {
+      setErr(err, errlen, msg.c_str());
+      return -1;
+    }
+    return (int)g.ops.size();
+  } catch (const std::exception& ex) {
+    setErr(err, errlen, ex.what());
     return -1;
   }
-  return (int)g.ops.size();
 }
 
 int yolo_task(void* h) { return E(h)->g.seg ? 3 : (E(h)->g.obb ? 1 : (E(h)->g.cls ? 2 : 0)); }
@@ -1427,7 +1432,12 @@ struct CoefPool {
       (void)hipHostFree(p);
       return;
     }
-    free.emplace(cap, p);
+    try {
+      free.emplace(cap, p);
+    } catch (...) {   // no memory for the list entry: give the buffer back instead
+      (void)hipHostFree(p);
+      return;
+    }
     freeBytes += cap;
   }
   void reclaimLocked() {
@@ -1655,15 +1665,20 @@ void* yolo_jpeg_submit(const unsigned char* data, size_t size) {
     auto buf = coefPool().take(t->hd.blocks() * 64 * sizeof(int16_t));
     t->cap = buf.first;
     t->coef = buf.second;
-    JpegTicket* tp = t.release();
-    yolo::jpeg::runAsync([tp] {
-      const bool ok = yolo::jpeg::decode(tp->data.data(), tp->data.size(), tp->hd, tp->coef);
-      std::lock_guard<std::mutex> lk(tp->mu);
-      tp->ok = ok;
-      tp->done = true;
-      tp->cv.notify_all();
-    });
-    return tp;
+    JpegTicket* tp = t.get();
+    try {
+      yolo::jpeg::runAsync([tp] {
+        const bool ok = yolo::jpeg::decode(tp->data.data(), tp->data.size(), tp->hd, tp->coef);
+        std::lock_guard<std::mutex> lk(tp->mu);
+        tp->ok = ok;
+        tp->done = true;
+        tp->cv.notify_all();
+      });
+    } catch (...) {   // not queued: the ticket (freed by t) never reaches the decoder
+      coefPool().give(tp->cap, tp->coef);
+      throw;
+    }
+    return t.release();
   } catch (const std::exception& ex) {
     std::fprintf(stderr, "[yolo] yolo_jpeg_submit: %s\n", ex.what());
     return nullptr;

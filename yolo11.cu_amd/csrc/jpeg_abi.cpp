@@ -4,18 +4,30 @@
 #include "../../include/yolo.h"
 #include "jpeg.hpp"
 
+// No exception leaves these functions: a host allocation (or thread creation) failure reads
+// as an error code.
 int yolo_jpeg_probe(const unsigned char* data, size_t size, int* height, int* width) {
   if (!data) return -1;
-  yolo::jpeg::Header hd;
-  const int r = yolo::jpeg::parse(data, size, hd);
-  if (r == yolo::jpeg::OK) {
-    if (height) *height = hd.H;
-    if (width) *width = hd.W;
+  try {
+    yolo::jpeg::Header hd;
+    const int r = yolo::jpeg::parse(data, size, hd);
+    if (r == yolo::jpeg::OK) {
+      if (height) *height = hd.H;
+      if (width) *width = hd.W;
+    }
+    return r;
+  } catch (...) {
+    return -1;
   }
-  return r;
 }
 
-int yolo_decoder_threads(void) { return yolo::jpeg::decoderThreads(); }
+int yolo_decoder_threads(void) {
+  try {
+    return yolo::jpeg::decoderThreads();
+  } catch (...) {
+    return -1;
+  }
+}
 
 long long yolo_jpeg_max_pixels(long long n) {
   if (n > 0) yolo::jpeg::setMaxPixels(n);
@@ -24,10 +36,14 @@ long long yolo_jpeg_max_pixels(long long n) {
 
 long long yolo_jpeg_coefficients(const unsigned char* data, size_t size, short* out, size_t cap) {
   if (!data) return -1;
-  yolo::jpeg::Header hd;
-  if (yolo::jpeg::parse(data, size, hd) != yolo::jpeg::OK) return -1;
-  const size_t n = hd.blocks() * 64;
-  if (!out) return (long long)n;
-  if (cap < n) return -1;
-  return yolo::jpeg::decode(data, size, hd, out) ? (long long)n : -2;
+  try {
+    yolo::jpeg::Header hd;
+    if (yolo::jpeg::parse(data, size, hd) != yolo::jpeg::OK) return -1;
+    const size_t n = hd.blocks() * 64;
+    if (!out) return (long long)n;
+    if (cap < n) return -1;
+    return yolo::jpeg::decode(data, size, hd, out) ? (long long)n : -2;
+  } catch (...) {
+    return -1;
+  }
 }
