@@ -568,8 +568,8 @@ struct Engine {
     if (op.kind == COPYC) return GK_COPY;
     if (op.kind != CONV) return GK_NONE;
     if (op.g > 1) return GK_DW;
-    if (op.Cin == 3 || specialConvCfg(op.cfg) || op.tail >= 0) return GK_NONE;
-    return GK_GEMM;
+    if (op.Cin == 3 || op.tail >= 0) return GK_NONE;
+    return GK_GEMM;   // a conv tuned to a special kernel too: a group must then beat that kernel
   }
   ConvJob convJob(int k) {
     const OpDesc& op = ops[k];
@@ -615,9 +615,9 @@ struct Engine {
   // the same shape class (GEMM: same kernel size, stride and output width -- the levels of a
   // detection head, the twin 1x1 convs of a C3k block); pass 2 any GEMM conv of the same K
   // mode.  Depthwise convs and copies always group; a GEMM group must find one tile config
-  // that runs it faster than its members' own tuned configs launched one after another
-  // (timed at the max batch like the autotuner; the full candidate set first, then shorter
-  // prefixes).  Without tuning GEMM ops stay single.
+  // that runs it faster than its members' own tuned configs (GEMM tiles or special kernels)
+  // launched one after another (timed at the max batch like the autotuner; the full
+  // candidate set first, then shorter prefixes).  Without tuning GEMM ops stay single.
   bool unitConflict(const Unit& a, const Unit& b) const {
     for (int i : a.ops)
       for (int j : b.ops)
