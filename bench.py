@@ -637,8 +637,8 @@ def main():
                          "crashes inside hipGraphLaunch on this image); prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (frames are independent; see DESIGN.md for how "
-              f"the path shards); --gpus {args.gpus} is not supported", file=sys.stderr)
+        print(f"bench.py measures one GPU only (frames are independent: the path shards as one engine "
+              f"per GPU with no exchange); --gpus {args.gpus} is not supported", file=sys.stderr)
         sys.exit(2)
     workdir = tempfile.mkdtemp(prefix="yolo_bench_")
     out = {}

@@ -4,7 +4,7 @@ time of a frame from a rocprofv3 kernel trace.
 
 HBM traffic per launch unit:
 
-    OUT=gpurun_out/traffic_x
+    OUT=out/traffic_x
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/fetch -o run -- \\
         python3 yolo11.cu_amd/profiling.py collect --scale x --batch 16 --plan $OUT/plan.json
     rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/write -o run -- \\
@@ -264,7 +264,7 @@ def _markdown(out, args):
              f"in the same run (FETCH_SIZE x {out['scale']['FETCH_SIZE']}, WRITE_SIZE x {out['scale']['WRITE_SIZE']}).",
              "Algorithmic bytes: input + weights + output (+ residual) per conv, inputs + outputs",
              "elsewhere (yolo11.cu_amd/unitwork.py).", "", "```",
-             "OUT=gpurun_out/traffic_x",
+             "OUT=out/traffic_x",
              "rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/fetch -o run -- python3 yolo11.cu_amd/profiling.py "
              f"collect --scale {out['model'][-1]} --batch {out['batch']} --passes {out['passes']} --plan $OUT/plan.json",
              "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/write -o run -- python3 yolo11.cu_amd/profiling.py "
@@ -333,7 +333,7 @@ def mfma(args):
              "included; algorithmic = `2*B*Ho*Wo*Cout*k^2*Cin/g` (yolo11.cu_amd/unitwork.py).  Busy share =",
              f"busy / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} SIMDs), the MFMA utilisation at the clock the",
              "dispatch ran at (algorithmic share: the same with algorithmic FLOPs).", "", "```",
-             f"OUT=gpurun_out/mfma_{plan['model'][-1]}",
+             f"OUT=out/mfma_{plan['model'][-1]}",
              "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE --output-format csv -d $OUT/pmc -o run -- "
              f"python3 yolo11.cu_amd/profiling.py collect --scale {plan['model'][-1]} --batch {plan['batch']} "
              f"--passes {passes} --plan $OUT/plan.json",
