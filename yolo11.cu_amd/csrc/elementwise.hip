@@ -63,8 +63,9 @@ __global__ __launch_bounds__(256) void k_maxpool5(View x, View y, int total) {
 // (planes r5, r9, r13 from one growing window) and one column pass, with the x plane of one
 // (image, 8-channel group) per block in LDS.  Max is exact, so this equals the chained pools.
 __device__ __forceinline__ f16x8 max8(f16x8 a, f16x8 b) { return __builtin_elementwise_max(a, b); }
+constexpr int SPPF_THREADS = 512;
 
-__global__ __launch_bounds__(256) void k_sppf_pool(View x, View y1, View y2, View y3) {
+__global__ __launch_bounds__(SPPF_THREADS) void k_sppf_pool(View x, View y1, View y2, View y3) {
   extern __shared__ f16x8 sp[];
   const int H = x.H, W = x.W, HW = H * W;
   f16x8* a = sp;
@@ -73,16 +74,17 @@ __global__ __launch_bounds__(256) void k_sppf_pool(View x, View y1, View y2, Vie
   f16x8* r13 = r9 + HW;
   const int g = blockIdx.x, img = blockIdx.y;
   const size_t pix0 = (size_t)img * HW;
-  for (int p0 = 0; p0 < HW; p0 += 4 * 256) {   // 4 loads in flight per thread
+  const int nt = blockDim.x;
+  for (int p0 = 0; p0 < HW; p0 += 4 * nt) {   // 4 loads in flight per thread
     f16x8 v[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      const int p = p0 + u * 256 + threadIdx.x;
+      const int p = p0 + u * nt + threadIdx.x;
       if (p < HW) v[u] = ld8(x, pix0 + p, g * 8);
     }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      const int p = p0 + u * 256 + threadIdx.x;
+      const int p = p0 + u * nt + threadIdx.x;
       if (p < HW) a[p] = v[u];
     }
   }
@@ -177,9 +179,12 @@ void launchMaxPool5(const View& x, const View& y, int Bn, hipStream_t st) {
   k_maxpool5<<<grid(total), 256, 0, st>>>(x, y, total);
 }
 size_t sppfPoolLds(int H, int W) { return (size_t)4 * H * W * sizeof(f16x8); }
+// one thread per pixel of the plane up to SPPF_THREADS (each pass is then one dependent
+// round of LDS reads per thread, not several)
 void launchSppfPool(const View& x, const View& y1, const View& y2, const View& y3, int Bn,
                     hipStream_t st) {
-  k_sppf_pool<<<dim3(x.C / 8, Bn), 256, sppfPoolLds(x.H, x.W), st>>>(x, y1, y2, y3);
+  const int nt = std::min(SPPF_THREADS, std::max(64, (x.H * x.W + 63) / 64 * 64));
+  k_sppf_pool<<<dim3(x.C / 8, Bn), nt, sppfPoolLds(x.H, x.W), st>>>(x, y1, y2, y3);
 }
 void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st) {
   int total = Bn * y.H * y.W * (y.C / 8);
