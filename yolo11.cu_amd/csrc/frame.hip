@@ -137,83 +137,95 @@ void launchPreprocessCls(const uint8_t* src, int sh, int sw, f16* dst, int S, in
 }
 
 // ------------------------------------------------------------------ decode
-// One thread per anchor over all levels of all images (one launch instead of one per
-// level).  Per anchor (k_decode, engine/engine.cu:844-906): first-max argmax over the nc
-// real classes (pad logits excluded), score = sigmoid(best), keep if score >= conf, DFL
-// expectation per side, xyxy = (x + 0.5 -+ d) * stride.  Every anchor owns record
-// `anchor` of the candidate array; survivors append a packed (score, anchor) key to the
-// image's list, which NMS ranks, so results do not depend on thread scheduling.
-// grid (anchor blocks of one wave, images): a wave never spans two images, so the survivors
-// of a wave are appended to the image's candidate list with one atomic (wave-aggregated).
-// The list order depends on arrival; NMS sorts by key, so results do not.  One-wave blocks
-// spread the 8,400 anchors of a 640 frame over ~130 CUs, and survivors fetch their box bins
-// before the append, so the two memory latencies overlap.
+// Four lanes per anchor over all levels of all images (one launch instead of one per level).
+// Per anchor (k_decode, engine/engine.cu:844-906): first-max argmax over the nc real classes
+// (pad logits excluded), score = sigmoid(best), keep if score >= conf, DFL expectation per
+// side, xyxy = (x + 0.5 -+ d) * stride.  Lane q of an anchor takes class chunks q, q + 4, ...
+// (8 classes each, in increasing order, first max within them) and the four lanes merge
+// (value, class) with the lower class winning ties -- the sequential first max; if kept,
+// lane q computes the DFL expectation of side q in the sequential order.  Every anchor owns
+// record `anchor` of the candidate array; survivors append a packed (score, anchor) key to
+// the image's list, which NMS ranks, so results do not depend on thread scheduling.
+// grid (blocks of 64 anchors, images): a wave never spans two images, so the survivors of a
+// wave are appended to the image's candidate list with one atomic (wave-aggregated).  The
+// list order depends on arrival; NMS sorts by key, so results do not.
 // OBB (k_decode_obb, engine/engine.cu:908-964): the angle view (channel 0 real) gives
 // theta = (sigmoid(t) - 0.25) * pi, the DFL distances are rotated by theta about the anchor
 // (dist2rbox), w = l + r, h = t + b, and the record is cx, cy, w, h, score, cls, theta.
+constexpr int DEC_ANCHORS = 64;   // anchors per block (4 lanes each)
 template <bool OBB>
-__global__ __launch_bounds__(64) void k_decode(DecodeArgs a, float* __restrict__ cand,
-                                                unsigned long long* __restrict__ lst,
-                                                int* __restrict__ count,
-                                                const PostParams* __restrict__ prm, int cstride) {
+__global__ __launch_bounds__(4 * DEC_ANCHORS) void k_decode(DecodeArgs a, float* __restrict__ cand,
+                                                             unsigned long long* __restrict__ lst,
+                                                             int* __restrict__ count,
+                                                             const PostParams* __restrict__ prm, int cstride) {
   const int img = blockIdx.y;
-  const int an = blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = threadIdx.x & 63, q = lane & 3;
+  const int an = blockIdx.x * DEC_ANCHORS + (threadIdx.x >> 2);
   const bool inside = an < a.A;
-  const int idx = img * a.A + (inside ? an : 0);
-  float best = -INFINITY;
-  int bcls = 0, lv = 0;
-  if (a.nlev > 1 && an >= a.lv[1].base) lv = 1;
-  if (a.nlev > 2 && an >= a.lv[2].base) lv = 2;
+  const int ai = inside ? an : 0;
+  const int idx = img * a.A + ai;
+  int lv = 0;
+  if (a.nlev > 1 && ai >= a.lv[1].base) lv = 1;
+  if (a.nlev > 2 && ai >= a.lv[2].base) lv = 2;
   const DecodeLevel& L = a.lv[lv];
-  const int local = an - L.base;
+  const int local = ai - L.base;
   const int yy = local / L.W, xx = local - yy * L.W;
   const size_t pix = (size_t)img * L.H * L.W + local;
 
+  float best = -INFINITY;
+  int bcls = 0;
   const f16* cp = L.cls.p + pix * L.cls.s + L.cls.o;
-  // 8 chunks (64 classes) are fetched before any is consumed, so their latencies overlap
-  for (int c0 = 0; inside && c0 < L.cls.C; c0 += 64) {
-    f16x8 v[8];
+  // this lane's chunks of up to 128 classes are fetched before any is consumed
+  for (int c00 = 0; inside && c00 < L.cls.C; c00 += 128) {
+    f16x8 v[4];
 #pragma unroll
-    for (int u = 0; u < 8; u++)
-      if (c0 + 8 * u < L.cls.C) v[u] = *(const f16x8*)(cp + c0 + 8 * u);
+    for (int u = 0; u < 4; u++) {
+      const int c0 = c00 + 8 * (q + 4 * u);
+      if (c0 < L.cls.C) v[u] = *(const f16x8*)(cp + c0);
+    }
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-      if (c0 + 8 * u >= L.cls.C) break;
+    for (int u = 0; u < 4; u++) {
+      const int c0 = c00 + 8 * (q + 4 * u);
+      if (c0 >= L.cls.C) break;
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const int cl = c0 + 8 * u + j;
+        const int cl = c0 + j;
         const float f = (float)v[u][j];
         if (cl < a.nc && f > best) { best = f; bcls = cl; }
       }
     }
   }
-  const float score = 1.f / (1.f + expf(-best));
-  const bool keep = inside && score >= prm->conf;
-  const f16* bp = L.box.p + pix * L.box.s + L.box.o;
-  f16x8 bv[8];
-  if (keep) {
 #pragma unroll
-    for (int u = 0; u < 8; u++) bv[u] = *(const f16x8*)(bp + 8 * u);
+  for (int o = 1; o < 4; o <<= 1) {
+    const float ob = __shfl_xor(best, o);
+    const int oc = __shfl_xor(bcls, o);
+    if (ob > best || (ob == best && oc < bcls)) { best = ob; bcls = oc; }
   }
-  const unsigned long long bal = __ballot(keep);
+  const float score = 1.f / (1.f + expf(-best));
+  const bool keep = inside && score >= prm->conf;   // the same in the anchor's four lanes
+  const f16* bp = L.box.p + pix * L.box.s + L.box.o + 16 * q;
+  f16x8 b0, b1;
+  if (keep) {
+    b0 = *(const f16x8*)(bp);
+    b1 = *(const f16x8*)(bp + 8);
+  }
+  const unsigned long long bal = __ballot(keep && q == 0);
   if (bal) {
     const int leader = __ffsll((long long)bal) - 1;
-    const int lane = threadIdx.x & 63;
     int base = 0;
     if (lane == leader) base = atomicAdd(&count[img], __popcll(bal));
     base = __shfl(base, leader);
     const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
-    if (keep && pos < a.A) lst[(size_t)img * a.A + pos] = packKey(score, an);
+    if (keep && q == 0 && pos < a.A) lst[(size_t)img * a.A + pos] = packKey(score, an);
   }
   if (!keep) return;
 
-  float d[4];
-#pragma unroll
-  for (int side = 0; side < 4; side++) {
-    const f16x8 v0 = bv[2 * side], v1 = bv[2 * side + 1];
+  // side q's expectation (bins 16q .. 16q+15), then every side to every lane of the anchor
+  float dq;
+  {
     float l[16];
 #pragma unroll
-    for (int j = 0; j < 8; j++) { l[j] = (float)v0[j]; l[j + 8] = (float)v1[j]; }
+    for (int j = 0; j < 8; j++) { l[j] = (float)b0[j]; l[j + 8] = (float)b1[j]; }
     float mx = l[0];
 #pragma unroll
     for (int j = 1; j < 16; j++) mx = fmaxf(mx, l[j]);
@@ -224,10 +236,21 @@ __global__ __launch_bounds__(64) void k_decode(DecodeArgs a, float* __restrict__
       sum = sum + p;
       e = e + p * (float)j;
     }
-    d[side] = e / sum;
+    dq = e / sum;
   }
-  const float cx = (float)xx + 0.5f, cy = (float)yy + 0.5f, st = (float)L.stride;
+  const int g0 = lane & ~3;
+  const float d[4] = {__shfl(dq, g0), __shfl(dq, g0 + 1), __shfl(dq, g0 + 2), __shfl(dq, g0 + 3)};
   float* o = cand + (size_t)idx * cstride;
+  if (!OBB && a.nm > 0) {   // mask coefficients: lane q copies chunks q, q + 4, ...
+    const f16* mp = L.coef.p + pix * L.coef.s + L.coef.o;
+    for (int c0 = 8 * q; c0 < a.nm; c0 += 32) {
+      const f16x8 v = *(const f16x8*)(mp + c0);
+#pragma unroll
+      for (int j = 0; j < 8; j++) o[6 + c0 + j] = (float)v[j];
+    }
+  }
+  if (q != 0) return;
+  const float cx = (float)xx + 0.5f, cy = (float)yy + 0.5f, st = (float)L.stride;
   if (OBB) {
     const float t0 = (float)L.coef.p[pix * L.coef.s + L.coef.o];
     const float th = (1.f / (1.f + expf(-t0)) - 0.25f) * 3.14159265358979f;
@@ -248,23 +271,15 @@ __global__ __launch_bounds__(64) void k_decode(DecodeArgs a, float* __restrict__
   o[3] = (cy + d[3]) * st;
   o[4] = score;
   o[5] = (float)bcls;
-  if (a.nm > 0) {
-    const f16* mp = L.coef.p + pix * L.coef.s + L.coef.o;
-    for (int c0 = 0; c0 < a.nm; c0 += 8) {
-      const f16x8 v = *(const f16x8*)(mp + c0);
-#pragma unroll
-      for (int j = 0; j < 8; j++) o[6 + c0 + j] = (float)v[j];
-    }
-  }
 }
 
 void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lst, int* count,
                   const PostParams* prm, int Bn, hipStream_t st) {
-  const dim3 grid((a.A + 63) / 64, Bn);
+  const dim3 grid((a.A + DEC_ANCHORS - 1) / DEC_ANCHORS, Bn);
   if (a.obb)
-    k_decode<true><<<grid, 64, 0, st>>>(a, cand, lst, count, prm, 7);
+    k_decode<true><<<grid, 4 * DEC_ANCHORS, 0, st>>>(a, cand, lst, count, prm, 7);
   else
-    k_decode<false><<<grid, 64, 0, st>>>(a, cand, lst, count, prm, 6 + a.nm);
+    k_decode<false><<<grid, 4 * DEC_ANCHORS, 0, st>>>(a, cand, lst, count, prm, 6 + a.nm);
 }
 
 // ------------------------------------------------------------------ NMS
