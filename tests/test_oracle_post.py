@@ -11,7 +11,7 @@ F16 = np.float16
 
 # ------------------------------------------------------------------ letterbox
 def test_letterbox_geometry_c0():
-    """810x1080 -> 640: scale 0.5926, nh 480, top 80 (the survey's C0 figures), full width."""
+    """810x1080 -> 640 (the config-0 frame): scale 0.5926, nh 480, top 80, full width."""
     scale, top, left, nh, nw = post.letterbox_geom(640, 640, 810, 1080)
     assert abs(scale - 0.5926) < 1e-4 and (nh, nw, top, left) == (480, 640, 80, 0)
     scale, top, left, nh, nw = post.letterbox_geom(640, 640, 1080, 1920)
