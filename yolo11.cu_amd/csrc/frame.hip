@@ -289,16 +289,16 @@ void launchDecode(const DecodeArgs& a, float* cand, unsigned long long* lst, int
 //  2. greedy suppression (k_nms semantics, engine/engine.cu:1091-1109: same class only,
 //     inter/union > thr with a union > 0 guard).  Suppression never crosses classes, so
 //     the greedy result is the union of independent per-class greedy passes: candidates
-//     are laid out class-major (rank order within a class), the whole block builds every
-//     class's suppression rows in chunks of 64 members (one ballot per row); a class of at
-//     most 64 members is then resolved by one wave with a bit scan, a larger one chunk by
-//     chunk with the whole block (a chunk's survivors strike the class's later members).
-//     This is exactly the sequential greedy result; survivors are flagged by rank and a
-//     block prefix sum over the flags gives their output slots;
+//     are laid out class-major (rank order within a class) and a class is decided in
+//     chunks of 64 members, one member per lane: each survivor in turn strikes the later
+//     members of its chunk that it suppresses (greedyChunk).  A class of at most 64
+//     members is one wave's work; in a larger one, a chunk's survivors then strike the
+//     class's later members before the next chunk (one wave up to NMS_WAVE_CLASS members,
+//     the whole block above).  This is exactly the sequential greedy result; survivors are
+//     flagged by rank and a block prefix sum over the flags gives their output slots;
 //  3. the list counter is re-armed (zeroed) for the next frame.
 constexpr int NMS_THREADS = 1024;
 constexpr int NMS_WAVE_CLASS = 256;          // largest class one wave resolves alone
-constexpr int NMS_THREAD_CLASS = 16;         // up to 512 candidates: per-thread rows up to this class size
 
 // Selection + ranking shared by both NMS kernels.  Leaves the m = min(n, NMS_CAP) largest
 // keys of lst[0..n) in descending order in sorted[0..m):
@@ -444,6 +444,26 @@ __device__ void selectAndRank(const unsigned long long* __restrict__ lst, int n,
   __syncthreads();
 }
 
+// Sequential greedy over one chunk of at most 64 members of a class, member j on lane j in
+// rank order: the lowest member left in `todo` is kept, and every later member of the chunk
+// that it suppresses leaves `todo` -- one ballot per survivor, the survivor's box broadcast
+// by readlane, so the serial chain is the class's survivors rather than its pairs.  `todo`
+// is wave-uniform and every lane of the wave calls this together; returns the kept members.
+__device__ __forceinline__ unsigned long long greedyChunk(float4 bx, unsigned long long todo, float thr,
+                                                          int lane) {
+  unsigned long long keep = 0ull;
+  while (todo) {
+    const int t = __builtin_ctzll(todo);
+    keep |= 1ull << t;
+    const float4 bt = make_float4(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.x), t)),
+                                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.y), t)),
+                                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.z), t)),
+                                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx.w), t)));
+    todo &= ~(__ballot(lane > t && suppresses(bt, bx, thr)) | (1ull << t));
+  }
+  return keep;
+}
+
 __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ cand,
                                                      unsigned long long* __restrict__ lists,
                                                      int* __restrict__ counts, int A, int cstride,
@@ -463,7 +483,6 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   __shared__ __attribute__((aligned(16))) short bucket[NMS_CAP];   // ranks, grouped by class
   __shared__ short perm[NMS_CAP];                  // class-major position -> rank
   __shared__ float4 cbox[NMS_CAP];                 // boxes, class-major
-  __shared__ unsigned long long rows2[NMS_CAP];    // chunk suppression rows, class-major
   __shared__ unsigned removed[NMS_CAP / 32];       // kept flags by rank
   __shared__ unsigned struck[NMS_CAP / 32];        // suppressed flags, class-major (large classes)
   __shared__ float4 stepBox[64];                   // survivors of a huge class's chunk
@@ -593,89 +612,9 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
   }
   __syncthreads();
 
-  // 3. suppression rows.  A class is decided in chunks of 64 members; rows2[p] holds the
-  //    later members of p's chunk that p suppresses.  Up to 512 candidates, classes of at
-  //    most NMS_THREAD_CLASS members take one thread per member; the larger ones are split
-  //    into work items (chunk, run of 8 positions): a wave takes items round-robin, lane j
-  //    holds member j of the chunk, and each position's row is one ballot (its box read as
-  //    an LDS broadcast); a class has ceil(g / 8) items (chunk boundaries fall on multiples
-  //    of 8).
-  //    Above that every thread is busy anyway and one thread per position tests only the
-  //    later members of its chunk (half the tests of a square ballot).
-  if (m > 512) {
-    for (int p = tid; p < m; p += NMS_THREADS) {
-      const int c = scls[perm[p]];
-      const int sc = cstart[c], a = p - sc;
-      const int q0 = sc + (a & ~63), nq = min(64, chist[c] - (a & ~63));
-      const float4 bp = cbox[p];
-      unsigned long long row = 0ull;
-      for (int j = (a & 63) + 1; j < nq; j++)
-        if (suppresses(bp, cbox[q0 + j], thr)) row |= 1ull << j;
-      rows2[p] = row;
-    }
-  } else {
-    // A class of at most NMS_THREAD_CLASS members: one thread per member tests the later
-    // members (a 64-lane ballot would leave most lanes idle); larger classes: wave items.
-    if (tid < m) {
-      const int c = scls[perm[tid]];
-      const int g = chist[c];
-      if (g <= NMS_THREAD_CLASS) {
-        const int sc = cstart[c], a = tid - sc;
-        const float4 bp = cbox[tid];
-        unsigned long long row = 0ull;
-        for (int j = a + 1; j < g; j++)
-          if (suppresses(bp, cbox[sc + j], thr)) row |= 1ull << j;
-        rows2[tid] = row;
-      }
-    }
-    {
-      // the items of class c start at cfill[c] = exclusive prefix of ceil(chist / 8) over the
-      // classes above NMS_THREAD_CLASS
-      const int h = chist[tid] > NMS_THREAD_CLASS ? (chist[tid] + 7) >> 3 : 0;
-      int incl = h;
-      for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o);
-        if (lane >= o) incl += y;
-      }
-      if (lane == 63) wsum[wave] = incl;
-      __syncthreads();
-      int off = 0;
-      for (int w = 0; w < wave; w++) off += wsum[w];
-      cfill[tid] = off + incl - h;             // cfill is free again: item start of class tid
-      if (tid == NMS_THREADS - 1) nstep = off + incl;
-      // item -> class table in `bucket` (free after the layout; at most m/8 + m <= 576 items)
-      for (int i = 0; i < h; i++) bucket[off + incl - h + i] = (short)tid;
-    }
-    __syncthreads();
-    {
-      const int nitems = uni(nstep);
-      for (int it = wave; it < nitems; it += NMS_THREADS / 64) {
-        const int c = uni(bucket[it]);
-        const int sc = uni(cstart[c]), g = uni(chist[c]);
-        const int a0 = (it - uni(cfill[c])) * 8;    // first class member of the item
-        const int q0 = a0 & ~63, nq = min(64, g - q0);
-        const float4 bq = lane < nq ? cbox[sc + q0 + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
-        const int pe = min(a0 + 8, g);
-        // the item's (up to 8) row boxes are LDS broadcasts requested together
-        float4 bp[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) bp[e] = cbox[sc + min(a0 + e, pe - 1)];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const int a = a0 + e;
-          if (a < pe) {
-            const unsigned long long row = __ballot(lane < nq && lane > (a & 63) && suppresses(bp[e], bq, thr));
-            if (lane == 0) rows2[sc + a] = row;
-          }
-        }
-      }
-    }
-  }
-  __syncthreads();
-
   // 4. per-class greedy.  `removed` holds the kept flag of every candidate by rank.
-  //  4a. a class of at most 64 members is one chunk: one wave resolves its rows by a bit
-  //      scan (waves take the classes round-robin)
+  //  4a. a class of at most 64 members is one chunk, resolved by one wave (greedyChunk;
+  //      waves take the classes round-robin)
   const int npres = uni(npresent), nlrg = uni(nlarge);
   for (int pc = wave; pc < npres; pc += NMS_THREADS / 64) {
     const int c = uni(present[pc]);
@@ -683,19 +622,12 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     if (g > 64) continue;                   // wave-uniform
     const bool valid = lane < g;
     const int mine = valid ? perm[sc + lane] : 0;
-    const unsigned long long row = valid ? rows2[sc + lane] : 0ull;
-    unsigned long long todo = g >= 64 ? ~0ull : ((1ull << g) - 1ull), keep = 0ull;
-    while (todo) {
-      const int t = __builtin_ctzll(todo);
-      keep |= 1ull << t;
-      const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, t);
-      const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), t);
-      todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << t));
-    }
+    const float4 bx = valid ? cbox[sc + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const unsigned long long keep = greedyChunk(bx, g >= 64 ? ~0ull : ((1ull << g) - 1ull), thr, lane);
     if ((keep >> lane) & 1ull) atomicOr(&removed[mine >> 5], 1u << (mine & 31));
   }
   //  4b. a class of 65 .. NMS_WAVE_CLASS members: one wave, chunk by chunk -- the chunk is
-  //      resolved by a bit scan (members struck by earlier chunks excluded), then the lanes
+  //      resolved by greedyChunk (members struck by earlier chunks excluded), then the lanes
   //      strike the class's later members that a survivor of the chunk suppresses
   //      (survivor boxes broadcast by readlane).  Waves take such classes round-robin; a
   //      class stops once it has max_det survivors (a later survivor ranks below max_det
@@ -710,17 +642,10 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
       const int p = sc + q0 + lane;
       const bool valid = lane < gq;
       const int mine = valid ? perm[p] : 0;
-      const unsigned long long row = valid ? rows2[p] : 0ull;
       const float4 bx = valid ? cbox[p] : make_float4(0.f, 0.f, 0.f, 0.f);
       const bool gone = valid && ((struck[p >> 5] >> (p & 31)) & 1u);
-      unsigned long long todo = (gq >= 64 ? ~0ull : ((1ull << gq) - 1ull)) & ~__ballot(gone), keep = 0ull;
-      while (todo) {
-        const int t = __builtin_ctzll(todo);
-        keep |= 1ull << t;
-        const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, t);
-        const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), t);
-        todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << t));
-      }
+      const unsigned long long keep =
+          greedyChunk(bx, (gq >= 64 ? ~0ull : ((1ull << gq) - 1ull)) & ~__ballot(gone), thr, lane);
       if ((keep >> lane) & 1ull) atomicOr(&removed[mine >> 5], 1u << (mine & 31));
       K += __popcll(keep);
       for (int p0 = sc + q0 + 64; p0 < sc + g; p0 += 64) {
@@ -751,7 +676,8 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
     }
   }
   __syncthreads();
-  //  4c. a larger class goes chunk by chunk with the whole block: wave 0 resolves the chunk,
+  //  4c. a larger class goes chunk by chunk with the whole block: wave 0 resolves the chunk
+  //      (greedyChunk),
   //      then every thread strikes later members of the class that a survivor of the chunk
   //      suppresses (survivor boxes read as LDS broadcasts)
   for (int li = 0; li < nlrg; li++) {
@@ -765,19 +691,13 @@ __global__ __launch_bounds__(NMS_THREADS) void k_nms(const float* __restrict__ c
         const int p = sc + q0 + lane;
         const bool valid = lane < gq;
         const int mine = valid ? perm[p] : 0;
-        const unsigned long long row = valid ? rows2[p] : 0ull;
+        const float4 bx = valid ? cbox[p] : make_float4(0.f, 0.f, 0.f, 0.f);
         const bool gone = valid && ((struck[p >> 5] >> (p & 31)) & 1u);
-        unsigned long long todo = (gq >= 64 ? ~0ull : ((1ull << gq) - 1ull)) & ~__ballot(gone), keep = 0ull;
-        while (todo) {
-          const int t = __builtin_ctzll(todo);
-          keep |= 1ull << t;
-          const unsigned lo = __builtin_amdgcn_readlane((unsigned)row, t);
-          const unsigned hi = __builtin_amdgcn_readlane((unsigned)(row >> 32), t);
-          todo &= ~((((unsigned long long)hi << 32) | lo) | (1ull << t));
-        }
+        const unsigned long long keep =
+            greedyChunk(bx, (gq >= 64 ? ~0ull : ((1ull << gq) - 1ull)) & ~__ballot(gone), thr, lane);
         if ((keep >> lane) & 1ull) {
           atomicOr(&removed[mine >> 5], 1u << (mine & 31));
-          stepBox[__popcll(keep & ((1ull << lane) - 1ull))] = cbox[p];
+          stepBox[__popcll(keep & ((1ull << lane) - 1ull))] = bx;
         }
         if (lane == 0) nstep = __popcll(keep);
       }
