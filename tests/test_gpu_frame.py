@@ -163,6 +163,40 @@ def test_dag_graph_equals_serial_graph(models, task):
     assert len(res["dag"][0][0]) > 0
 
 
+@pytest.mark.parametrize("scale,B", [("n", 2), ("x", 3)])
+def test_attention_carries_v_copies(models, scale, B):
+    """C2PSA's V-gather copies run as trailing blocks of the attention launch (one launch
+    unit with the ATTN op); every tensor and the detections equal a one-op-per-launch
+    engine's (YOLO_NOGROUP) bit for bit."""
+    d = models("yolo11", scale)
+    g = graphfile.load(d)
+    imgs = [modelgen.synth_frame(640, 640, 30, 40 + s) for s in range(B)]
+    res = {}
+    for name, flags in (("carried", 0), ("single", yolort.YOLO_NOGROUP)):
+        eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH | flags)
+        kinds = [eng.op_info(k)["kind"] for k in range(eng.num_ops)]
+        attn = [k for k, kd in enumerate(kinds) if kd == "ATTN"]
+        copies = [k for k, kd in enumerate(kinds) if kd == "COPYC"]
+        assert attn and copies
+        if name == "carried":
+            # each attention's unit holds the copies just before it
+            for a in attn:
+                mine = [k for k in copies if k < a and eng.op_unit(k) == eng.op_unit(a)]
+                assert mine, (a, [eng.op_unit(k) for k in copies], eng.op_unit(a))
+            assert all(eng.op_unit(k) in {eng.op_unit(a) for a in attn} for k in copies)
+        else:
+            assert len({eng.op_unit(k) for k in copies + attn}) == len(copies + attn)
+        bufs = [_letterbox_gpu(eng, im, s) for s, im in enumerate(imgs)]
+        eng.run(B)
+        res[name] = [eng.get(s) for s in range(B)] + [eng.read(t, B) for t in range(len(g.tens))]
+        for b in bufs:
+            b.free()
+        eng.close()
+    for x, y in zip(res["carried"], res["single"]):
+        np.testing.assert_array_equal(x, y)
+    assert sum(len(r) for r in res["carried"][:B]) > 0
+
+
 def test_frame_graph_nms_variants(models):
     """The frame graph holds both NMS variants and picks by the previous frame's candidate
     count: a sparse frame (294 candidates) and a crowded one (conf 0.05: thousands) alternate

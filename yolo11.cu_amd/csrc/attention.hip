@@ -22,6 +22,7 @@
 //  * exp is exp2 with log2(e) folded into the score scale; fp32 statistics, fp16 P and V,
 //    fp32 accumulation.
 #include "engine.hpp"
+#include "viewcopy.hpp"
 
 namespace yolo {
 
@@ -56,8 +57,10 @@ __device__ __forceinline__ int xcdItem(int b, int n) {
   return x * q + min(x, r) + j;
 }
 
+// Blocks [0, natt) are the attention's; any after them run the channel copies in `riders`.
 template <int HD, bool WHOLE, int KS>
-__global__ __launch_bounds__(256 * KS) void k_attention(View qkv, View y, int N, int heads, float scale_log2) {
+__global__ __launch_bounds__(256 * KS) void k_attention(View qkv, View y, int N, int heads, float scale_log2,
+                                                        int natt, const CopyLaunch riders) {
   constexpr int KD = 32;
   constexpr int CT = HD / 16;  // channel tiles of the output
   constexpr int NT = 256 * KS;
@@ -66,11 +69,15 @@ __global__ __launch_bounds__(256 * KS) void k_attention(View qkv, View y, int N,
   __shared__ f16x8 sKs[WHOLE ? 1 : AK * 4];
   __shared__ f16 sVts[WHOLE ? 1 : HD * VT_PITCH];
 
+  if ((int)blockIdx.x >= natt) {   // block-uniform: a carried copy, no LDS, no barrier
+    runCopyBlock(riders, (int)blockIdx.x - natt);
+    return;
+  }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int qw = wave & 3, kp = wave >> 2;   // query group, key part
   const int lr = lane & 15, lg = lane >> 4;
   // items are (image, head, query group), query group fastest
-  const int nq = (N + AQ - 1) / AQ, items = (int)gridDim.x;
+  const int nq = (N + AQ - 1) / AQ, items = natt;
   const int item = items >= 2 * NUM_XCD ? xcdItem((int)blockIdx.x, items) : (int)blockIdx.x;
   const int qgrp = item % nq, h = (item / nq) % heads, img = item / (nq * heads);
   const int per = 2 * KD + HD;
@@ -272,21 +279,27 @@ static size_t attWholeLds(int N, int KS) {
 }
 
 template <int HD>
-static void launchAttn(const View& qkv, const View& y, int N, int heads, float sl2, int Bn, hipStream_t st) {
+static void launchAttn(const View& qkv, const View& y, int N, int heads, float sl2, int Bn, hipStream_t st,
+                       const View* xs, const View* ys, int ncopy) {
   const int nq = (N + AQ - 1) / AQ;
-  const dim3 grid(nq * heads * Bn);
+  const int natt = nq * heads * Bn;
   // key splits while one image's grid leaves most CUs idle.  Decided per image, not per
   // launch, so an image's result does not depend on the batch it runs in (the splits change
   // the softmax merge order).
   const long blocks = (long)nq * heads;
   const int KS = blocks <= 128 ? 4 : blocks <= 512 ? 2 : 1;
-  if (attWholeOk && N <= ATT_WHOLE_MAX && attWholeLds<HD>(N, KS) <= ATT_WHOLE_LDS) {
+  const bool whole = attWholeOk && N <= ATT_WHOLE_MAX && attWholeLds<HD>(N, KS) <= ATT_WHOLE_LDS;
+  // carried copies go after the attention's blocks, into the CUs its last wave leaves idle
+  int ncb = 0;
+  const CopyLaunch L = copyLaunch(xs, ys, ncopy, Bn, whole ? 256 * KS : 256, &ncb);
+  const dim3 grid(natt + ncb);
+  if (whole) {
     const size_t lds = attWholeLds<HD>(N, KS);
-    if (KS == 4) k_attention<HD, true, 4><<<grid, 256 * 4, lds, st>>>(qkv, y, N, heads, sl2);
-    else if (KS == 2) k_attention<HD, true, 2><<<grid, 256 * 2, lds, st>>>(qkv, y, N, heads, sl2);
-    else k_attention<HD, true, 1><<<grid, 256, lds, st>>>(qkv, y, N, heads, sl2);
+    if (KS == 4) k_attention<HD, true, 4><<<grid, 256 * 4, lds, st>>>(qkv, y, N, heads, sl2, natt, L);
+    else if (KS == 2) k_attention<HD, true, 2><<<grid, 256 * 2, lds, st>>>(qkv, y, N, heads, sl2, natt, L);
+    else k_attention<HD, true, 1><<<grid, 256, lds, st>>>(qkv, y, N, heads, sl2, natt, L);
   } else {
-    k_attention<HD, false, 1><<<grid, 256, 0, st>>>(qkv, y, N, heads, sl2);
+    k_attention<HD, false, 1><<<grid, 256, 0, st>>>(qkv, y, N, heads, sl2, natt, L);
   }
 }
 
@@ -306,19 +319,19 @@ void attentionInit() {
 }
 
 void launchAttention(const View& qkv, const View& y, int heads, int kd, int hd, int Bn,
-                     hipStream_t st) {
+                     hipStream_t st, const View* xs, const View* ys, int ncopy) {
   (void)kd;  // the loader accepts kd == 32 only
   const int N = qkv.H * qkv.W;
   const float scale_log2 = (1.0f / sqrtf(32.0f)) * 1.4426950408889634f;
   switch (hd) {
-    case 16: launchAttn<16>(qkv, y, N, heads, scale_log2, Bn, st); break;
-    case 32: launchAttn<32>(qkv, y, N, heads, scale_log2, Bn, st); break;
-    case 48: launchAttn<48>(qkv, y, N, heads, scale_log2, Bn, st); break;
-    case 64: launchAttn<64>(qkv, y, N, heads, scale_log2, Bn, st); break;
-    case 80: launchAttn<80>(qkv, y, N, heads, scale_log2, Bn, st); break;
-    case 96: launchAttn<96>(qkv, y, N, heads, scale_log2, Bn, st); break;
-    case 112: launchAttn<112>(qkv, y, N, heads, scale_log2, Bn, st); break;
-    case 128: launchAttn<128>(qkv, y, N, heads, scale_log2, Bn, st); break;
+    case 16: launchAttn<16>(qkv, y, N, heads, scale_log2, Bn, st, xs, ys, ncopy); break;
+    case 32: launchAttn<32>(qkv, y, N, heads, scale_log2, Bn, st, xs, ys, ncopy); break;
+    case 48: launchAttn<48>(qkv, y, N, heads, scale_log2, Bn, st, xs, ys, ncopy); break;
+    case 64: launchAttn<64>(qkv, y, N, heads, scale_log2, Bn, st, xs, ys, ncopy); break;
+    case 80: launchAttn<80>(qkv, y, N, heads, scale_log2, Bn, st, xs, ys, ncopy); break;
+    case 96: launchAttn<96>(qkv, y, N, heads, scale_log2, Bn, st, xs, ys, ncopy); break;
+    case 112: launchAttn<112>(qkv, y, N, heads, scale_log2, Bn, st, xs, ys, ncopy); break;
+    case 128: launchAttn<128>(qkv, y, N, heads, scale_log2, Bn, st, xs, ys, ncopy); break;
     default: break;
   }
 }

@@ -5,6 +5,7 @@
 // are aligned 128-bit loads/stores.  Semantics follow the reference ops
 // (engine/engine.cu:663-732; torch definitions export/export.py:475-491).
 #include "engine.hpp"
+#include "viewcopy.hpp"
 
 namespace yolo {
 
@@ -137,24 +138,7 @@ __global__ __launch_bounds__(256) void k_upsample2(View x, View y, int total) {
 
 // Up to COPY_GROUP independent channel copies per launch (the per-head V gathers of an
 // attention block): copy j owns the blocks from blk0[j].
-struct CopyLaunch {
-  View x[COPY_GROUP], y[COPY_GROUP];
-  int total[COPY_GROUP], blk0[COPY_GROUP];
-  int n;
-};
-__global__ __launch_bounds__(256) void k_copyc(const CopyLaunch L) {
-  int pj = 0;
-#pragma unroll
-  for (int q = 1; q < COPY_GROUP; q++)
-    if (q < L.n && (int)blockIdx.x >= L.blk0[q]) pj = q;
-  pj = __builtin_amdgcn_readfirstlane(pj);
-  const View x = L.x[pj], y = L.y[pj];
-  int idx = ((int)blockIdx.x - L.blk0[pj]) * blockDim.x + threadIdx.x;
-  if (idx >= L.total[pj]) return;
-  int cg = y.C >> 3, g = idx % cg;
-  size_t m = idx / cg;
-  st8(y, m, g * 8, ld8(x, m, g * 8));
-}
+__global__ __launch_bounds__(256) void k_copyc(const CopyLaunch L) { runCopyBlock(L, (int)blockIdx.x); }
 
 // pixel shuffle r=2 from quadrant-major channel blocks: in(i, j, q*C + c) -> out(2i+di, 2j+dj, c)
 // with q = 2*di + dj.  After a 1x1 conv to 4C this is ConvTranspose2d(k=2, s=2) exactly.
@@ -190,17 +174,23 @@ void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st) {
   int total = Bn * y.H * y.W * (y.C / 8);
   k_upsample2<<<grid(total), 256, 0, st>>>(x, y, total);
 }
-void launchCopyCGroup(const View* xs, const View* ys, int n, int Bn, hipStream_t st) {
+CopyLaunch copyLaunch(const View* xs, const View* ys, int n, int Bn, int threads, int* blocks) {
   CopyLaunch L{};
-  int blocks = 0;
+  int nb = 0;
   for (int i = 0; i < n; i++) {
     L.x[i] = xs[i];
     L.y[i] = ys[i];
     L.total[i] = Bn * ys[i].H * ys[i].W * (ys[i].C / 8);
-    L.blk0[i] = blocks;
-    blocks += grid(L.total[i]);
+    L.blk0[i] = nb;
+    nb += (L.total[i] + threads - 1) / threads;
   }
   L.n = n;
+  *blocks = nb;
+  return L;
+}
+void launchCopyCGroup(const View* xs, const View* ys, int n, int Bn, hipStream_t st) {
+  int blocks = 0;
+  const CopyLaunch L = copyLaunch(xs, ys, n, Bn, 256, &blocks);
   k_copyc<<<blocks, 256, 0, st>>>(L);
 }
 void launchCopyC(const View& x, const View& y, int Bn, hipStream_t st) { launchCopyCGroup(&x, &y, 1, Bn, st); }

@@ -556,7 +556,7 @@ struct Engine {
   // convs, channel copies).  A group's launch computes every member exactly as a launch of
   // it alone does (grouped kernels only partition their blocks), so grouping changes launch
   // counts, never results.
-  enum { GK_NONE = 0, GK_GEMM, GK_DW, GK_COPY };
+  enum { GK_NONE = 0, GK_GEMM, GK_DW, GK_COPY, GK_ATTN };   // GK_ATTN: an attention + the copies it carries
   struct Unit {
     std::vector<int> ops;
     int kind = GK_NONE;
@@ -595,6 +595,16 @@ struct Engine {
   }
   void runUnit(const Unit& u, int Bn, hipStream_t s = nullptr) {
     if (!s) s = st;
+    if (u.kind == GK_ATTN) {
+      const OpDesc& a = ops[u.ops[0]];
+      View xs[COPY_GROUP], ys[COPY_GROUP];
+      for (size_t i = 1; i < u.ops.size(); i++) {
+        xs[i - 1] = view(ops[u.ops[i]].a);
+        ys[i - 1] = view(ops[u.ops[i]].out);
+      }
+      launchAttention(view(a.a), view(a.out), a.heads, a.kd, a.hd, Bn, s, xs, ys, (int)u.ops.size() - 1);
+      return;
+    }
     bool together = u.ops.size() > 1;
     if (together && u.kind == GK_GEMM)   // (per-op overrides since planning launch one by one)
       for (int i : u.ops)
@@ -709,6 +719,38 @@ struct Engine {
     }
     units = out;
   }
+  // A unit of channel copies (one COPYC, or a copy group) moves into the launch of a later
+  // attention op (within the next 8 units) that none of the copies conflicts with, when no
+  // unit in between conflicts with them either: the copies then run as the attention
+  // launch's trailing blocks.  C2PSA gathers each head's V slice of the qkv tensor this way
+  // for its positional conv, independent of the attention that reads the same tensor.
+  void carryCopies() {
+    std::vector<Unit> out;
+    std::vector<char> taken(units.size(), 0);
+    for (size_t a = 0; a < units.size(); a++) {
+      if (taken[a]) continue;
+      const Unit& u = units[a];
+      bool copies = !u.ops.empty() && u.ops.size() <= (size_t)COPY_GROUP;
+      for (int i : u.ops) copies = copies && groupKind(i) == GK_COPY;
+      if (copies) {
+        for (size_t b = a + 1; b < units.size() && b <= a + 8; b++) {
+          if (taken[b]) continue;
+          const Unit& v = units[b];
+          if (v.ops.size() == 1 && ops[v.ops[0]].kind == ATTN && ops[v.ops[0]].chain >= 0 && !unitConflict(u, v)) {
+            Unit m{{v.ops[0]}, GK_ATTN};
+            m.ops.insert(m.ops.end(), u.ops.begin(), u.ops.end());
+            units[b] = m;      // the copies' place becomes the attention's
+            copies = false;
+            break;
+          }
+          if (unitConflict(u, v)) break;
+        }
+        if (!copies) continue;   // carried
+      }
+      out.push_back(u);
+    }
+    units = out;
+  }
   void planUnits(bool tune) {
     computeAccesses();
     units.clear();
@@ -720,6 +762,7 @@ struct Engine {
     }
     mergePass(true, tune, e0, e1);
     mergePass(false, tune, e0, e1);
+    carryCopies();
     for (Unit& u : units)
       for (int i : u.ops) ops[i].wsOff = ops[i].cntOff = -1;
     if (e0) (void)hipEventDestroy(e0);
@@ -2222,7 +2265,7 @@ int yolo_profile_units(void* h, int B, int iters, int reps, float* ms) {
         HCK(hipEventSynchronize(e1));
         float t = 0.f;
         HCK(hipEventElapsedTime(&t, e0, e1));
-        acc[k0] += t / reps;
+        acc[*std::min_element(u.ops.begin(), u.ops.end())] += t / reps;   // the unit's first op
       }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);

@@ -261,13 +261,25 @@ void launchMarker(hipStream_t st);
 // n independent channel copies in one launch
 constexpr int COPY_GROUP = 8;
 void launchCopyCGroup(const View* xs, const View* ys, int n, int Bn, hipStream_t st);
+// Kernel arguments of up to COPY_GROUP channel copies run as blocks of a launch: copy i
+// moves total[i] 8-channel groups in the blocks from blk0[i] on, blockDim.x groups per
+// block (k_copyc, and the copies an attention launch carries after its own blocks).
+struct CopyLaunch {
+  View x[COPY_GROUP], y[COPY_GROUP];
+  int total[COPY_GROUP], blk0[COPY_GROUP];
+  int n;
+};
+// the arguments of n copies at batch Bn in blocks of `threads`; *blocks = blocks they take
+CopyLaunch copyLaunch(const View* xs, const View* ys, int n, int Bn, int threads, int* blocks);
 void launchPS2(const View& x, const View& y, int Bn, hipStream_t st);
 void launchGap(const View& x, const View& y, int Bn, hipStream_t st);
 void launchSoftmaxCh(const View& x, const View& y, int Bn, hipStream_t st);
 // attention.hip
 void attentionInit();
+// ncopy channel copies (xs[i] -> ys[i]) independent of the attention may ride in the same
+// launch as extra blocks after the attention's own
 void launchAttention(const View& qkv, const View& y, int heads, int kd, int hd, int Bn,
-                     hipStream_t st);
+                     hipStream_t st, const View* xs = nullptr, const View* ys = nullptr, int ncopy = 0);
 // frame.hip
 // Source pixel layouts of the preprocess kernels: BGR u8 (3 bytes, the reference's cv::Mat
 // layout) or R, G, B, X u8 (4 bytes, how decoders such as PIL hold RGB images in memory).

@@ -83,6 +83,8 @@ def units(eng, B: int) -> list[dict]:
         if u not in out:
             name, cls = unit_kernel(eng, k)
             out[u] = {"unit": u, "first": k, "ops": [], "kernel": name, "class": cls, "flops": 0.0, "bytes": 0.0}
+        if eng.op_info(k)["kind"] == "ATTN" and k != out[u]["first"]:
+            out[u]["kernel"] = "k_attention"   # an attention launch carrying channel copies
         f, b = op_work(eng, k, B)
         out[u]["ops"].append(k)
         out[u]["flops"] += f
