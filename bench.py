@@ -36,6 +36,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import tempfile
@@ -45,7 +46,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "yolo11.cu_amd"))
 sys.path.insert(0, ROOT)
 
-from unitwork import conv_kernel_name, unit_table  # noqa: E402  (the package dir is on sys.path)
+from unitwork import conv_kernel_name, unit_table, units as unit_list  # noqa: E402  (the package dir is on sys.path)
 
 PEAK_FP16 = 2.5e15        # MI355X dense fp16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12         # MI355X HBM3E, B/s
@@ -364,8 +365,12 @@ def bench_x(workdir, iters, graph=True):
             conv_t += per_unit[k] * 1e-3
             conv_t_ev += per_op[k] * 1e-3
         elif info["kind"] == "ATTN":
-            attn_t += per_unit[k] * 1e-3
             attn_f += B * attn_flops(eng, k)
+    # an attention launch may carry its block's V-gather copies: the unit's time (reported
+    # on its first op, a copy then) counts as attention time
+    for u in unit_list(eng, B):
+        if any(eng.op_info(k)["kind"] == "ATTN" for k in u["ops"]):
+            attn_t += per_unit[u["first"]] * 1e-3
     units = unit_table(eng, B, per_unit)
     top = next(g for g in units if g["class"])          # the conv kernel group with the most time
     mt = measured_x_traffic(top["firsts"], top["kernel"])
@@ -591,6 +596,17 @@ def cpu_baseline(budget_s=15.0):
                        f"{res['frames']} frames = {res['ms']:.1f} ms/frame ({res['threads']} torch threads)")
 
 
+def _finite(o):
+    """The JSON line in standard JSON: a figure that came out non-finite (a zero time) is null."""
+    if isinstance(o, dict):
+        return {k: _finite(v) for k, v in o.items()}
+    if isinstance(o, (list, tuple)):
+        return [_finite(v) for v in o]
+    if isinstance(o, float) and not math.isfinite(o):
+        return None
+    return o
+
+
 def prepost_roofline(n, seg):
     """Achieved HBM bandwidth of the pre/post kernels against the 8 TB/s roofline, from the
     stage times (hipEvents, stream-ordered) and their algorithmic bytes:
@@ -774,7 +790,7 @@ def main():
                             "ms": round(conv["ms"], 4)}
     if cpu:
         line["cpu_baseline"] = cpu
-    print(json.dumps(line), flush=True)
+    print(json.dumps(_finite(line)), flush=True)
 
 
 if __name__ == "__main__":
