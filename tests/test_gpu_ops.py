@@ -95,6 +95,36 @@ def test_yolo11n_seg_ops_resync(models):
     eng.close()
 
 
+@pytest.mark.parametrize("nm", [16, 32, 64])
+def test_seg_masks_nm(tmp_path, nm):
+    """Mask assembly with 16 mask coefficients (the per-lane kernel) and 32 or 64 (the MFMA
+    kernel, one or two 32-channel steps): on resynced heads, decode + NMS exactly the oracle's,
+    then every survivor's mask at IoU >= 0.99 against the oracle's masks."""
+    d = str(tmp_path / f"seg{nm}")
+    modelgen.build_model("yolo11", "n", "segment", 80, 640, 0, -8.0, nm=nm).graph.write(d, "segment", 80, 640)
+    img = modelgen.synth_polygons(640, 640, 30, 4)
+    x = post.letterbox(img, 640, 640)[None]
+    rels, eng, ref = _resync_run(d, x)
+    assert not [r for r in rels if not r[2] <= TOL]
+    eng.run_post(1)
+    want = post.detect([(b[0], c[0], m[0], s) for b, c, m, s in ref.heads_in], 80)
+    got = eng.get(0)
+    assert len(got) == len(want["score"]) and len(got) > 0
+    np.testing.assert_array_equal(got[:, 5].astype(int), want["cls"])
+    g = graphfile.load(d)
+    proto = ref.view([op.a for op in g.ops if op.kind == "MASKS"][0])[0]
+    assert proto.shape[-1] == nm
+    wm = post.masks(proto, want["coef"], want["box"], 640, 640)
+    ious = []
+    for i in range(len(got)):
+        gm = eng.get_mask(0, i)
+        union = np.logical_or(gm, wm[i]).sum()
+        ious.append(1.0 if union == 0 else np.logical_and(gm, wm[i]).sum() / union)
+    print(f"nm {nm}: {len(got)} survivors, mask IoU min {min(ious):.4f}", flush=True)
+    assert min(ious) >= 0.99
+    eng.close()
+
+
 @pytest.mark.parametrize("B", [1, 32])
 @pytest.mark.parametrize("shape", [
     (80, 80, 256, 256, 3, 1), (80, 80, 256, 512, 3, 2), (40, 40, 512, 256, 1, 1),

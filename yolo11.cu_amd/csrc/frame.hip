@@ -1066,10 +1066,102 @@ __global__ __launch_bounds__(256) void k_masks(View proto, const float* __restri
   }
 }
 
+// MFMA form (nm a multiple of 32, proto planes of whole 64-pixel tiles).  A 16-pixel x
+// 16-survivor tile of logits is one v_mfma_f32_16x16x32_f16 per 32 channels with the pixels as
+// the rows, so lane l ends up with 4 consecutive pixels (rows 4(l/16) .. +3) of survivor l % 16
+// and writes their 4 mask bytes in one store.  The fp32 coefficients enter as fp16 hi + lo parts
+// (two MFMAs; hi + lo keeps 22 of their 24 significand bits), the proto is fp16 already, and the
+// products accumulate in fp32: the logits differ from an fp32 dot product in their last bits
+// only, so only a logit within rounding of 0 can take the other mask bit.
+// Grid (64-pixel tiles, groups of MSKM_SV survivor slots, images): wave w takes pixels
+// 16w .. 16w + 15 of the tile against the group's 16-survivor tiles.  Groups past the image's
+// count exit, as in k_masks.  (256-pixel tiles, staging a group's coefficients once for four
+// times the pixels, measured no faster.)
+constexpr int MSKM_SV = 64;
+typedef float f32x4m __attribute__((ext_vector_type(4)));
+
+template <int NMK>   // 32-channel steps of the proto (nm / 32)
+__global__ __launch_bounds__(256) void k_masks_mfma(View proto, const float* __restrict__ cand, int cstride,
+                                                    int A, const int* __restrict__ outidx,
+                                                    const int* __restrict__ outcnt,
+                                                    const float* __restrict__ outdets,
+                                                    uint8_t* __restrict__ masks, float rx, float ry) {
+  constexpr int NM = 32 * NMK, CP = NM + 8;   // coefficient row pitch (halves)
+  const int img = blockIdx.z, d0 = blockIdx.y * MSKM_SV;
+  const int cnt = outcnt[img];
+  if (d0 >= cnt) return;   // block-uniform
+  const int nd = min(MSKM_SV, cnt - d0);
+  __shared__ __attribute__((aligned(16))) f16 chi[MSKM_SV * CP];
+  __shared__ __attribute__((aligned(16))) f16 clo[MSKM_SV * CP];
+  __shared__ float4 bb[MSKM_SV];
+  const int t = threadIdx.x;
+  for (int i = t; i < MSKM_SV * NM; i += 256) {
+    const int sv = i / NM, c = i - sv * NM;
+    float v = 0.f;
+    if (sv < nd) {
+      const int an = outidx[img * MAX_OUT + d0 + sv];
+      v = cand[((size_t)img * A + an) * cstride + 6 + c];
+    }
+    const f16 h = (f16)v;
+    chi[sv * CP + c] = h;
+    clo[sv * CP + c] = (f16)(v - (float)h);
+  }
+  if (t < MSKM_SV) {
+    float4 b = make_float4(0.f, 0.f, 0.f, 0.f);   // slots past the count: an empty box
+    if (t < nd) {
+      const float* det = outdets + ((size_t)img * MAX_OUT + d0 + t) * 6;
+      b = make_float4(det[0] * rx, det[1] * ry, det[2] * rx, det[3] * ry);
+    }
+    bb[t] = b;
+  }
+  const int lane = t & 63, wave = t >> 6, lr = lane & 15, lg = lane >> 4;
+  const int Pw = proto.W, HW = proto.H * Pw;
+  const int pt = blockIdx.x * 64 + wave * 16;   // the wave's 16 pixels
+  const f16* pimg = proto.p + (size_t)img * HW * proto.s + proto.o;
+  f16x8 a[NMK];
+#pragma unroll
+  for (int s = 0; s < NMK; s++) a[s] = *(const f16x8*)(pimg + (size_t)(pt + lr) * proto.s + 32 * s + 8 * lg);
+  const int q0 = pt + 4 * lg;                   // the lane's 4 output pixels
+  float fx[4], fy[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    fx[e] = (float)((q0 + e) % Pw);
+    fy[e] = (float)((q0 + e) / Pw);
+  }
+  __syncthreads();
+  for (int st = 0; 16 * st < nd; st++) {        // wave-uniform
+    const int sv = 16 * st + lr;
+    f32x4m acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NMK; s++) {
+      const f16x8 bh = *(const f16x8*)&chi[sv * CP + 32 * s + 8 * lg];
+      const f16x8 bl = *(const f16x8*)&clo[sv * CP + 32 * s + 8 * lg];
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], bh, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], bl, acc, 0, 0, 0);
+    }
+    const float4 b = bb[sv];
+    unsigned word = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const bool in = fx[e] >= b.x && fx[e] < b.z && fy[e] >= b.y && fy[e] < b.w;
+      word |= (in && acc[e] > 0.f ? 1u : 0u) << (8 * e);
+    }
+    if (sv < nd) *(unsigned*)(masks + ((size_t)img * MAX_OUT + d0 + sv) * HW + q0) = word;
+  }
+}
+
 void launchMasks(const View& proto, const float* cand, int cstride, int A, int nm,
                  const int* outidx, const int* outcnt, const float* outdets, uint8_t* masks,
                  float rx, float ry, int Bn, hipStream_t st) {
   const int HW = proto.H * proto.W;
+  if (nm % 32 == 0 && nm <= 64 && HW % 64 == 0) {
+    const dim3 g((unsigned)(HW / 64), (MAX_OUT + MSKM_SV - 1) / MSKM_SV, Bn);
+    if (nm == 32)
+      k_masks_mfma<1><<<g, 256, 0, st>>>(proto, cand, cstride, A, outidx, outcnt, outdets, masks, rx, ry);
+    else
+      k_masks_mfma<2><<<g, 256, 0, st>>>(proto, cand, cstride, A, outidx, outcnt, outdets, masks, rx, ry);
+    return;
+  }
   dim3 grid((HW + 256 * MSK_PIX - 1) / (256 * MSK_PIX), (MAX_OUT + MSK_GROUP - 1) / MSK_GROUP, Bn);
   switch (nm / 8) {
 #define MSK(n) case n: k_masks<n><<<grid, 256, 0, st>>>(proto, cand, cstride, A, outidx, outcnt, outdets, masks, rx, ry); break;
