@@ -726,15 +726,12 @@ struct Engine {
   // for its positional conv, independent of the attention that reads the same tensor.
   void carryCopies() {
     std::vector<Unit> out;
-    std::vector<char> taken(units.size(), 0);
     for (size_t a = 0; a < units.size(); a++) {
-      if (taken[a]) continue;
       const Unit& u = units[a];
       bool copies = !u.ops.empty() && u.ops.size() <= (size_t)COPY_GROUP;
       for (int i : u.ops) copies = copies && groupKind(i) == GK_COPY;
       if (copies) {
         for (size_t b = a + 1; b < units.size() && b <= a + 8; b++) {
-          if (taken[b]) continue;
           const Unit& v = units[b];
           if (v.ops.size() == 1 && ops[v.ops[0]].kind == ATTN && ops[v.ops[0]].chain >= 0 && !unitConflict(u, v)) {
             Unit m{{v.ops[0]}, GK_ATTN};
