@@ -126,14 +126,21 @@ __global__ __launch_bounds__(SPPF_THREADS) void k_sppf_pool(View x, View y1, Vie
   }
 }
 
-// nearest x2: out(oy, ox) = in(oy/2, ox/2)
+// nearest x2: out(oy, ox) = in(oy/2, ox/2).  One thread per input pixel and 8-channel group
+// loads it once and writes the 2x2 output pixels it fills (one thread per output vector read
+// every input four times and ran yolo11x b16's 384-channel 40 -> 80 upsample at ~2 TB/s).
 __global__ __launch_bounds__(256) void k_upsample2(View x, View y, int total) {
-  int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total) return;
-  int cg = y.C >> 3, g = idx % cg, m = idx / cg;
-  int HW = y.H * y.W, img = m / HW, rem = m - img * HW;
-  int oy = rem / y.W, ox = rem - oy * y.W;
-  st8(y, m, g * 8, ld8(x, (size_t)(img * x.H + (oy >> 1)) * x.W + (ox >> 1), g * 8));
+  const int cg = x.C >> 3, g = idx % cg, m = idx / cg;   // m: the input pixel
+  const int HW = x.H * x.W, img = m / HW, rem = m - img * HW;
+  const int iy = rem / x.W, ix = rem - iy * x.W;
+  const f16x8 v = ld8(x, m, g * 8);
+  const size_t o = (size_t)(img * y.H + 2 * iy) * y.W + 2 * ix;
+  st8(y, o, g * 8, v);
+  st8(y, o + 1, g * 8, v);
+  st8(y, o + y.W, g * 8, v);
+  st8(y, o + y.W + 1, g * 8, v);
 }
 
 // Up to COPY_GROUP independent channel copies per launch (the per-head V gathers of an
@@ -171,7 +178,7 @@ void launchSppfPool(const View& x, const View& y1, const View& y2, const View& y
   k_sppf_pool<<<dim3(x.C / 8, Bn), nt, sppfPoolLds(x.H, x.W), st>>>(x, y1, y2, y3);
 }
 void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st) {
-  int total = Bn * y.H * y.W * (y.C / 8);
+  const int total = Bn * x.H * x.W * (x.C / 8);
   k_upsample2<<<grid(total), 256, 0, st>>>(x, y, total);
 }
 CopyLaunch copyLaunch(const View* xs, const View* ys, int n, int Bn, int threads, int* blocks) {
