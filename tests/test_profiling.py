@@ -131,3 +131,25 @@ def test_trace_labels_follow_the_tile_tables(tmp_path, capsys):
     assert "k_conv_gemm<64, 64, 2, 2, 64, 3, 0> [cfg 12 1x1]" in out
     assert "yolo::k_conv_tap<1, 1, 256, 192, 4, 2, 1, 3> [op config 1109]" in out
     assert "4.500 ms" not in out and "1 frames: 0.0045 ms and 4 dispatches per frame" in out
+
+
+def test_conv_roofline_ceiling():
+    """The per-layer roofline tool on yolo11x b16 and yolo11n b1 (generator graph, CPU): the
+    conv count and FLOPs equal what the engine's op descriptions give (173 convs, 3.118 TFLOP:
+    the matrix-pipe profile's algorithmic total), and the summed per-layer times sit between
+    the larger of the two whole-frame bounds and their sum."""
+    x = profiling.conv_roofline("x", 16)
+    assert x["convs"] == 173 and abs(x["tflop"] - 3.118) < 5e-4
+    t_mfma, t_hbm = x["tflop"] * 1e12 / 2.5e15, x["gbytes"] * 1e9 / 6.3e12
+    assert max(t_mfma, t_hbm) * 1e3 <= x["roofline_ms"] <= (t_mfma + t_hbm) * 1e3
+    # slower MFMA-bound layers lower the reachable utilisation, by at most the factor f (no
+    # layer's time grows more than 1/f)
+    u = [x["at_frac"]["0.44"]["util"], x["at_frac"]["0.6"]["util"], x["util"]]
+    assert u[0] < u[1] < u[2] < 1.0
+    assert u[0] >= 0.44 * u[2] and u[1] >= 0.6 * u[2]
+    # batch 1 of yolo11n: every conv is bound by its bytes, so the peak fraction plays no part
+    n = profiling.conv_roofline("n", 1)
+    assert n["mfma_bound"] == 0
+    assert abs(n["roofline_ms"] - n["gbytes"] * 1e9 / 6.3e12 * 1e3) < 1e-9
+    # (at 0.44 of the peak, layers just below the ridge become MFMA-bound, never faster)
+    assert n["roofline_ms"] <= n["at_frac"]["0.44"]["ms"] <= n["roofline_ms"] / 0.44

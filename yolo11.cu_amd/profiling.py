@@ -415,6 +415,55 @@ def trace(args):
           f"{tot / 1e3 / max(frames, 1):.4f} ms and {len(rows) / max(frames, 1):.0f} dispatches per frame")
 
 
+def conv_roofline(scale: str = "x", batch: int = 16, peak: float = 2.5e15, bw: float = 6.3e12,
+                  fracs=(0.44, 0.6)) -> dict:
+    """Per-layer roofline of a model's convs at a batch size, from the generator's op graph
+    (CPU only).  Each conv takes max(FLOPs / peak, bytes / bw), its bytes counted as unitwork
+    counts them (input, weights, output, the residual a following ADD fuses in, fp32 bias);
+    bw defaults to the copy rate measured on MI355X (6.3 TB/s, read + write).  The ratio of all
+    conv FLOPs to the summed per-layer times, over the peak, is the conv MFMA utilisation a
+    frame could reach with every conv at its own roofline.  For each f in `fracs` the same
+    with MFMA-bound layers at f of the peak (0.44: the best GEMM tile's main loop streaming
+    from HBM, measured in isolation)."""
+    import modelgen
+    g = modelgen.build_model("yolo11", scale, calibrate=False).graph
+    ops = g.ops
+    flops = nbytes = t_roof = 0.0
+    t_frac = {f: 0.0 for f in fracs}
+    mfma_bound = 0
+    for i, op in enumerate(ops):
+        if op[0] != "CONV":
+            continue
+        _, x, out, k, _s, _p, grp, _act, cin, cout = op[:10]
+        H, W, _ = g.shape(x)
+        Ho, Wo, _ = g.shape(out)
+        f = 2.0 * batch * Ho * Wo * cout * k * k * cin / grp
+        out_px = batch * Ho * Wo * cout
+        b = 2.0 * (batch * H * W * cin + cout * k * k * cin / grp + out_px) + 4.0 * cout
+        nx = ops[i + 1] if i + 1 < len(ops) else None
+        if nx is not None and nx[0] == "ADD" and out in (nx[1], nx[2]):
+            b += 2.0 * out_px   # the residual read of the fused add
+        flops += f
+        nbytes += b
+        t_roof += max(f / peak, b / bw)
+        mfma_bound += f / peak >= b / bw
+        for fr in fracs:
+            t_frac[fr] += max(f / (peak * fr), b / bw)
+    return {"scale": scale, "batch": batch, "convs": sum(op[0] == "CONV" for op in ops),
+            "mfma_bound": mfma_bound, "tflop": flops / 1e12, "gbytes": nbytes / 1e9,
+            "roofline_ms": t_roof * 1e3, "util": flops / t_roof / peak,
+            "at_frac": {str(fr): {"ms": t * 1e3, "util": flops / t / peak} for fr, t in t_frac.items()}}
+
+
+def ceiling(args):
+    r = conv_roofline(args.scale, args.batch)
+    print(f"yolo11{r['scale']} b{r['batch']}: {r['convs']} convs ({r['mfma_bound']} MFMA-bound), "
+          f"{r['tflop']:.3f} TFLOP, {r['gbytes']:.2f} GB; every conv at its roofline: {r['roofline_ms']:.3f} ms, "
+          f"conv MFMA util {r['util']:.3f}")
+    for fr, v in r["at_frac"].items():
+        print(f"  MFMA-bound convs at {fr} of the peak: {v['ms']:.3f} ms, util {v['util']:.3f}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -444,13 +493,16 @@ def main():
     mf.add_argument("--pmc", required=True, help="its rocprofv3 output directory")
     mf.add_argument("--md")
     mf.add_argument("--top", type=int, default=20)
+    ce = sub.add_parser("ceiling", help="per-layer roofline of the convs (CPU only)")
+    ce.add_argument("--scale", default="x")
+    ce.add_argument("--batch", type=int, default=16)
     t = sub.add_parser("trace")
     t.add_argument("csv", help="a rocprofv3 kernel_trace.csv, or the directory holding it")
     t.add_argument("--letterboxes-per-frame", type=int, default=1)
     t.add_argument("--top", type=int, default=32)
     args = ap.parse_args()
     {"collect": collect, "summarize": summarize, "trace": trace, "tiles": tiles,
-     "tiles-summary": tiles_summary, "mfma": mfma}[args.cmd](args)
+     "tiles-summary": tiles_summary, "mfma": mfma, "ceiling": ceiling}[args.cmd](args)
 
 
 if __name__ == "__main__":
