@@ -279,12 +279,15 @@ def test_attention_op(tmp_path, H, W, heads, B):
     eng.close()
 
 
-@pytest.mark.parametrize("B", [1, 3])
-def test_sppf_pool_chain(models, B):
+@pytest.mark.parametrize("scale,B,imgsz", [("n", 1, 640), ("n", 3, 640), ("n", 32, 640), ("x", 16, 640),
+                                           ("x", 24, 320)])
+def test_sppf_pool_chain(models, scale, B, imgsz):
     """The fused SPPF pool chain (one launch for three MAXPOOL5) is bit-exact against the
     oracle's mp5, mp5(mp5), mp5(mp5(mp5)) on random activations, and the standalone
-    MAXPOOL5 of a chain follower (what the per-op harness runs) is exact too."""
-    d = models("yolo11", "n", "detect")
+    MAXPOOL5 of a chain follower (what the per-op harness runs) is exact too.  The cases
+    cover one 8-channel group per block (yolo11n b1, b3), two (yolo11n b32, yolo11x b16 at
+    20x20) and four (yolo11x b24 at 320: a 10x10 plane)."""
+    d = models("yolo11", scale, "detect", imgsz=imgsz)
     eng = yolort.Engine(d, B, yolort.YOLO_NOTUNE | yolort.YOLO_NOGRAPH)
     kinds = [eng.op_info(k) for k in range(eng.num_ops)]
     head = next(k for k in range(len(kinds) - 2)

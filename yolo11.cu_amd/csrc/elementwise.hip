@@ -66,63 +66,65 @@ __global__ __launch_bounds__(256) void k_maxpool5(View x, View y, int total) {
 __device__ __forceinline__ f16x8 max8(f16x8 a, f16x8 b) { return __builtin_elementwise_max(a, b); }
 constexpr int SPPF_THREADS = 512;
 
+template <int GPB>   // 8-channel groups per block: a pixel's GPB * 16 bytes are contiguous
 __global__ __launch_bounds__(SPPF_THREADS) void k_sppf_pool(View x, View y1, View y2, View y3) {
   extern __shared__ f16x8 sp[];
-  const int H = x.H, W = x.W, HW = H * W;
+  const int H = x.H, W = x.W, HW = H * W, n = HW * GPB;   // items (pixel, group), group fastest
   f16x8* a = sp;
-  f16x8* r5 = sp + HW;
-  f16x8* r9 = r5 + HW;
-  f16x8* r13 = r9 + HW;
-  const int g = blockIdx.x, img = blockIdx.y;
+  f16x8* r5 = sp + n;
+  f16x8* r9 = r5 + n;
+  f16x8* r13 = r9 + n;
+  const int c0 = blockIdx.x * GPB * 8, img = blockIdx.y;
   const size_t pix0 = (size_t)img * HW;
   const int nt = blockDim.x;
-  for (int p0 = 0; p0 < HW; p0 += 4 * nt) {   // 4 loads in flight per thread
+  for (int i0 = 0; i0 < n; i0 += 4 * nt) {   // 4 loads in flight per thread
     f16x8 v[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      const int p = p0 + u * nt + threadIdx.x;
-      if (p < HW) v[u] = ld8(x, pix0 + p, g * 8);
+      const int i = i0 + u * nt + threadIdx.x;
+      if (i < n) v[u] = ld8(x, pix0 + i / GPB, c0 + (i % GPB) * 8);
     }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      const int p = p0 + u * nt + threadIdx.x;
-      if (p < HW) a[p] = v[u];
+      const int i = i0 + u * nt + threadIdx.x;
+      if (i < n) a[i] = v[u];
     }
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < HW; p += blockDim.x) {
-    const int py = p / W, px = p - py * W;
-    const f16x8* row = a + py * W;
-    f16x8 m = row[px];
+  for (int i = threadIdx.x; i < n; i += nt) {
+    const int p = i / GPB, py = p / W, px = p - py * W;
+    f16x8 m = a[i];
 #pragma unroll
     for (int d = 1; d <= 6; d++) {
-      if (px >= d) m = max8(m, row[px - d]);
-      if (px + d < W) m = max8(m, row[px + d]);
-      if (d == 2) r5[p] = m;
-      if (d == 4) r9[p] = m;
+      if (px >= d) m = max8(m, a[i - d * GPB]);
+      if (px + d < W) m = max8(m, a[i + d * GPB]);
+      if (d == 2) r5[i] = m;
+      if (d == 4) r9[i] = m;
     }
-    r13[p] = m;
+    r13[i] = m;
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < HW; p += blockDim.x) {
-    const int py = p / W;
-    f16x8 m5 = r5[p], m9 = r9[p], m13 = r13[p];
+  const int rs = W * GPB;   // one image row of items
+  for (int i = threadIdx.x; i < n; i += nt) {
+    const int p = i / GPB, py = p / W;
+    f16x8 m5 = r5[i], m9 = r9[i], m13 = r13[i];
 #pragma unroll
     for (int d = 1; d <= 6; d++) {
       if (py >= d) {
-        if (d <= 2) m5 = max8(m5, r5[p - d * W]);
-        if (d <= 4) m9 = max8(m9, r9[p - d * W]);
-        m13 = max8(m13, r13[p - d * W]);
+        if (d <= 2) m5 = max8(m5, r5[i - d * rs]);
+        if (d <= 4) m9 = max8(m9, r9[i - d * rs]);
+        m13 = max8(m13, r13[i - d * rs]);
       }
       if (py + d < H) {
-        if (d <= 2) m5 = max8(m5, r5[p + d * W]);
-        if (d <= 4) m9 = max8(m9, r9[p + d * W]);
-        m13 = max8(m13, r13[p + d * W]);
+        if (d <= 2) m5 = max8(m5, r5[i + d * rs]);
+        if (d <= 4) m9 = max8(m9, r9[i + d * rs]);
+        m13 = max8(m13, r13[i + d * rs]);
       }
     }
-    st8(y1, pix0 + p, g * 8, m5);
-    st8(y2, pix0 + p, g * 8, m9);
-    st8(y3, pix0 + p, g * 8, m13);
+    const int c = c0 + (i % GPB) * 8;
+    st8(y1, pix0 + p, c, m5);
+    st8(y2, pix0 + p, c, m9);
+    st8(y3, pix0 + p, c, m13);
   }
 }
 
@@ -170,12 +172,33 @@ void launchMaxPool5(const View& x, const View& y, int Bn, hipStream_t st) {
   k_maxpool5<<<grid(total), 256, 0, st>>>(x, y, total);
 }
 size_t sppfPoolLds(int H, int W) { return (size_t)4 * H * W * sizeof(f16x8); }
-// one thread per pixel of the plane up to SPPF_THREADS (each pass is then one dependent
-// round of LDS reads per thread, not several)
+// One thread per item of the plane up to SPPF_THREADS (each pass is then one dependent round
+// of LDS reads per thread, not several).  A block takes GPB adjacent 8-channel groups so each
+// pixel access is GPB * 16 contiguous bytes (one group per block read and wrote 16 bytes per
+// 2 * C-byte pixel, 7x the algorithmic bytes on yolo11x b16); as many groups per block as
+// keep at least one block per CU, within the 64 KiB of dynamic LDS a launch gets by default.
 void launchSppfPool(const View& x, const View& y1, const View& y2, const View& y3, int Bn,
                     hipStream_t st) {
-  const int nt = std::min(SPPF_THREADS, std::max(64, (x.H * x.W + 63) / 64 * 64));
-  k_sppf_pool<<<dim3(x.C / 8, Bn), nt, sppfPoolLds(x.H, x.W), st>>>(x, y1, y2, y3);
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 256;
+    return n;
+  }();
+  const int groups = x.C / 8, HW = x.H * x.W;
+  int gpb = 1;
+  for (int c : {4, 2})
+    if (groups % c == 0 && (long)(groups / c) * Bn >= cus && sppfPoolLds(x.H, x.W) * c <= 64 * 1024) {
+      gpb = c;
+      break;
+    }
+  const int nt = std::min(SPPF_THREADS, std::max(64, (HW * gpb + 63) / 64 * 64));
+  const dim3 grid(groups / gpb, Bn);
+  const size_t lds = sppfPoolLds(x.H, x.W) * gpb;
+  if (gpb == 4) k_sppf_pool<4><<<grid, nt, lds, st>>>(x, y1, y2, y3);
+  else if (gpb == 2) k_sppf_pool<2><<<grid, nt, lds, st>>>(x, y1, y2, y3);
+  else k_sppf_pool<1><<<grid, nt, lds, st>>>(x, y1, y2, y3);
 }
 void launchUpsample2(const View& x, const View& y, int Bn, hipStream_t st) {
   const int total = Bn * x.H * x.W * (x.C / 8);
